@@ -1,0 +1,202 @@
+/*
+ * pairformer_hip.h -- C ABI of libpairformer_hip.so, the MI355X (gfx950) kernels for
+ * the Boltz-2 Pairformer pair-representation hot path.
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers (HIP global memory) unless stated otherwise.
+ *   - Dense row-major layouts.  Pair tensors are [B][N][N][C] fp32; masks are fp32 0/1.
+ *   - Weights are bf16 (raw uint16 bit patterns) in nn.Linear layout [out][in];
+ *     LayerNorm weights/biases are fp32.  Weight names in the comments are the
+ *     reference state-dict keys (tt_bio/reference.py, tt_bio/boltz2.py).
+ *   - `stream` is a hipStream_t (NULL = default stream).  Calls only enqueue work;
+ *     they do not synchronize and do not allocate device memory.  Scratch memory is
+ *     passed in as `workspace` (size from the matching *_workspace_size()).
+ *   - Return 0 on success or a negative PF_E_* code; pf_last_error() then returns a
+ *     thread-local message.  Nothing is launched when an argument is rejected.
+ *   - N (tokens) must be a positive multiple of 64: the Python boundary pads to 64
+ *     like the reference does (tt_bio/tenstorrent.py:41, 2235-2246).
+ *   - `accumulate`: 0 -> out = update, 1 -> out += update.  out may alias the input
+ *     pair tensor (in-place residual, `z = z + op(z)` in tt_bio/reference.py:877-903).
+ */
+#ifndef PAIRFORMER_HIP_H
+#define PAIRFORMER_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PF_ABI_VERSION 1
+
+enum {
+  PF_OK = 0,
+  PF_E_INVALID = -1, /* bad shape / null pointer / unsupported configuration */
+  PF_E_OOM = -2,     /* reserved: message contains "out of memory" */
+  PF_E_LAUNCH = -3   /* a kernel launch failed (message names the kernel) */
+};
+
+/* ABI version of the loaded library (PF_ABI_VERSION at build time). */
+int pf_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* pf_last_error(void);
+
+/* ------------------------------------------------------------------------------
+ * Triangle multiplication, outgoing (direction 0) and incoming (direction 1).
+ * Replaces TriangleMultiplicationOutgoing/Incoming.forward
+ * (tt_bio/reference.py:455-472, 544-561), the ttnn TriangleMultiplication.__call__
+ * (tt_bio/tenstorrent.py:409-503) and the fused-op contract
+ * kernel_triangular_mult(x, direction, mask, norm_in_weight, norm_in_bias,
+ * p_in_weight, g_in_weight, norm_out_weight, norm_out_bias, p_out_weight,
+ * g_out_weight, eps) (tt_bio/boltz2.py:820-848).
+ *   update = p_out(LN_out(x)) * sigmoid(g_out(LN_in(z))),
+ *   x[i,j] = sum_k a[i,k]*b[j,k] (outgoing) or sum_k a[k,i]*b[k,j] (incoming),
+ *   a|b = p_in(LN_in z) * sigmoid(g_in(LN_in z)) * pair_mask.
+ * -------------------------------------------------------------------------- */
+typedef struct pf_trimul_args {
+  int B, N, C;            /* C = c_z = 128 */
+  int hidden;             /* must equal C (Boltz-2: p_in is [2*C, C]) */
+  int direction;          /* 0 outgoing, 1 incoming */
+  int accumulate;
+  float eps;              /* LayerNorm eps (1e-5) */
+  const float* z_in;      /* [B][N][N][C] */
+  float* out;             /* [B][N][N][C], may alias z_in */
+  const float* pair_mask; /* [B][N][N] or NULL (all ones) */
+  const float* norm_in_w; const float* norm_in_b;    /* norm_in.{weight,bias} [C] */
+  const void* p_in_w;     /* p_in.weight  bf16 [2C][C] */
+  const void* g_in_w;     /* g_in.weight  bf16 [2C][C] */
+  const float* norm_out_w; const float* norm_out_b;  /* norm_out.{weight,bias} [C] */
+  const void* p_out_w;    /* p_out.weight bf16 [C][C] */
+  const void* g_out_w;    /* g_out.weight bf16 [C][C] */
+  void* workspace; size_t workspace_bytes;
+  void* stream;
+} pf_trimul_args;
+
+size_t pf_trimul_workspace_size(int B, int N, int C);
+int pf_trimul_fwd(const pf_trimul_args* args);
+
+/* The contraction alone: X[p][i][j] = sum_k A[p][i][k] * Bm[p][j][k] for `planes`
+ * independent N x N bf16 planes, fp32 output.  The batched matmul inside
+ * TriangleMultiplication (tt_bio/tenstorrent.py:453-460; einsum at
+ * tt_bio/reference.py:467, 556). */
+int pf_trimul_contract(const void* A, const void* Bm, float* X, int planes, int N, void* stream);
+
+/* ------------------------------------------------------------------------------
+ * Triangle attention, starting node (ending = 0) and ending node (ending = 1).
+ * Replaces TriangleAttention.forward (tt_bio/reference.py:294-365, with
+ * Attention.forward 138-194 and _attention tt_bio/boltz2.py:790-810) and the ttnn
+ * TriangleAttention.__call__ (tt_bio/tenstorrent.py:541-650).
+ *   x = LN(z) (z transposed for the ending node); per row i, head h, query j:
+ *   logits_k = (q_ij/sqrt(d)).k_ik + 1e9*(pair_mask_ik - 1) + (x_jk . w_b[h]);
+ *   softmax over k (fp32, online); o = sum_k p_k v_ik; update = linear_o(o * sigmoid(g)).
+ * -------------------------------------------------------------------------- */
+typedef struct pf_triatt_args {
+  int B, N, C;            /* C = 128 */
+  int H, D;               /* heads = 4, head dim = 32 (H*D == C) */
+  int ending;             /* 0 starting node, 1 ending node */
+  int accumulate;
+  float eps;
+  const float* z_in;      /* [B][N][N][C] */
+  float* out;             /* may alias z_in */
+  const float* pair_mask; /* [B][N][N] or NULL */
+  const float* ln_w; const float* ln_b;   /* layer_norm.{weight,bias} [C] */
+  const void* w_bias;     /* linear.weight      bf16 [H][C] */
+  const void* w_q; const void* w_k; const void* w_v; const void* w_g;  /* mha.linear_{q,k,v,g}.weight bf16 [H*D][C] */
+  const void* w_o;        /* mha.linear_o.weight bf16 [C][H*D] */
+  void* workspace; size_t workspace_bytes;
+  void* stream;
+} pf_triatt_args;
+
+size_t pf_triatt_workspace_size(int B, int N, int C, int H, int D);
+int pf_triatt_fwd(const pf_triatt_args* args);
+
+/* Attention core with the signature of the fused-op contract
+ * kernel_triangular_attn(q, k, v, tri_bias, mask, scale) (tt_bio/boltz2.py:815-817)
+ * and the semantics of the use_kernels=False path it stands in for
+ * (tt_bio/reference.py:176-190, tt_bio/boltz2.py:790-810):
+ *   o[b,i,h,j,:] = sum_k softmax_k(scale*q.k + 1e9*(mask[b,i,k]-1) + bias[b,h,j,k]) v[b,i,h,k,:]
+ * q, k, v: fp32 [B][I][H][J][D] (I = J = N); bias fp32 [B][H][N][N]; mask fp32 [B][I][N]
+ * or NULL; o fp32 [B][I][H][J][D].  D must be 32. */
+size_t pf_tri_attention_workspace_size(int B, int N, int H, int D);
+int pf_tri_attention(const float* q, const float* k, const float* v, const float* bias,
+                     const float* mask, float scale, float* o, int B, int N, int H, int D,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------
+ * Transition (SwiGLU MLP): update = fc3(silu(fc1(LN(x))) * fc2(LN(x))), no biases.
+ * Replaces Transition.forward (tt_bio/boltz2.py:1227-1258) and the ttnn Transition
+ * (tt_bio/tenstorrent.py:856-946).  rows = B*N*N for the pair track (C = 128,
+ * hidden = 512: one fused kernel, hidden never leaves the CU) or B*N for the single
+ * track (C = 384, hidden = 1536: LN + two GEMMs, hidden in workspace).
+ * -------------------------------------------------------------------------- */
+typedef struct pf_transition_args {
+  long rows; int C; int hidden;
+  int accumulate;
+  float eps;
+  const float* x_in;      /* [rows][C] */
+  float* out;             /* [rows][C], may alias x_in */
+  const float* norm_w; const float* norm_b;   /* norm.{weight,bias} [C] */
+  const void* fc1_w; const void* fc2_w;       /* bf16 [hidden][C] */
+  const void* fc3_w;                          /* bf16 [C][hidden] */
+  void* workspace; size_t workspace_bytes;
+  void* stream;
+} pf_transition_args;
+
+size_t pf_transition_workspace_size(long rows, int C, int hidden);
+int pf_transition_fwd(const pf_transition_args* args);
+
+/* ------------------------------------------------------------------------------
+ * Single-track attention with pair bias (AttentionPairBias, v2, compute_pair_bias).
+ * Replaces AttentionPairBias.forward (tt_bio/boltz2.py:343-367) as called from
+ * PairformerLayer.forward (tt_bio/reference.py:906-911) and the ttnn
+ * AttentionPairBias (tt_bio/tenstorrent.py:738-853, non-atom branch):
+ *   q = proj_q(s) + b_q, k = proj_k(k_in), v = proj_v(k_in),
+ *   bias = proj_z.1(LN_{proj_z.0}(z)) [B,H,N,N],
+ *   logits = q.k/sqrt(d) + bias - 1e6*(1 - mask_k), softmax, o = P v,
+ *   update = proj_o(sigmoid(proj_g(s)) * o).
+ * s, k_in fp32 [B][N][c_s]; z fp32 [B][N][N][C]; mask fp32 [B][N] or NULL.
+ * -------------------------------------------------------------------------- */
+typedef struct pf_apb_args {
+  int B, N, c_s, C, H;    /* c_s = 384, C = 128, H = 16 (head dim c_s/H) */
+  int accumulate;
+  float eps;              /* eps of the proj_z LayerNorm */
+  const float* s;         /* query input (pre_norm_s(s) in the Pairformer) */
+  const float* k_in;      /* key/value input */
+  const float* z;         /* pair tensor */
+  const float* mask;      /* [B][N] or NULL */
+  float* out;             /* [B][N][c_s], may alias neither s nor k_in when accumulate=0 */
+  const void* w_q; const float* b_q;          /* proj_q.{weight bf16 [c_s][c_s], bias fp32} */
+  const void* w_k; const void* w_v; const void* w_g; const void* w_o;  /* bf16 [c_s][c_s] */
+  const float* zln_w; const float* zln_b;     /* proj_z.0.{weight,bias} [C] */
+  const void* w_z;                            /* proj_z.1.weight bf16 [H][C] */
+  void* workspace; size_t workspace_bytes;
+  void* stream;
+} pf_apb_args;
+
+size_t pf_apb_workspace_size(int B, int N, int c_s, int H);
+int pf_apb_fwd(const pf_apb_args* args);
+
+/* ------------------------------------------------------------------------------
+ * Row primitives (tt_bio/boltz2.py:638-768): LayerNorm and Linear over rows.
+ * -------------------------------------------------------------------------- */
+/* out[r,:] = LN(x[r,:]) * w + b, fp32, any C <= 4096.  (nn.LayerNorm, eps) */
+int pf_layernorm_fwd(const float* x, const float* w, const float* b, float* out, long rows,
+                     int C, float eps, void* stream);
+
+/* out[r,n] = (resid ? resid[r,n] : 0) + sum_k x[r,k] * W[n,k] + (bias ? bias[n] : 0).
+ * x fp32 [rows][K], W bf16 [Nout][K], K a multiple of 16, Nout a multiple of 32.
+ * resid may alias out.  (nn.Linear) */
+int pf_linear_fwd(const float* x, const void* W, const float* bias, const float* resid,
+                  float* out, long rows, int K, int Nout, void* stream);
+
+/* Pair-track recycling step of the trunk loop (tt_bio/boltz2.py:5213-5214):
+ *   out[p,:] = base[p,:] + W . LN(x[p,:])   for every pair p, C = 128.
+ * (z = z_init + z_recycle(z_norm(z))); out may alias x but not base unless equal. */
+int pf_pair_ln_linear_fwd(const float* x, const float* base, const float* ln_w, const float* ln_b,
+                          const void* W, float* out, long rows, int C, float eps, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PAIRFORMER_HIP_H */

@@ -1,0 +1,197 @@
+"""Scalar-loop restatements of the Pairformer ops for tiny sizes (N <= 8).
+
+TEST INFRASTRUCTURE ONLY -- see ``oracle/__init__.py``.
+
+These exist to pin ``oracle.pairformer_ref`` independently of torch: every
+output element is computed by explicit Python loops in float64, indexing the
+pair grid by name (i, j, k) exactly as the reference's einsum strings and
+softmax axes state them.  A transposed operand, a wrong einsum string, a bias
+added on the wrong axis or a mask applied to the wrong index changes these
+results and fails ``tests/test_oracle.py``.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def _np(t):
+    return np.asarray(t.detach().double().numpy() if hasattr(t, "detach") else t, dtype=np.float64)
+
+
+def _sig(x):
+    return 1.0 / (1.0 + math.exp(-x))
+
+
+def _ln_vec(v, w, b, eps=1e-5):
+    n = len(v)
+    mu = sum(v) / n
+    var = sum((x - mu) ** 2 for x in v) / n
+    r = 1.0 / math.sqrt(var + eps)
+    return [((v[c] - mu) * r) * w[c] + b[c] for c in range(n)]
+
+
+def _matvec(W, v):
+    """y_o = sum_c W[o][c] v[c]  (nn.Linear convention: weight [out, in])."""
+    return [sum(W[o][c] * v[c] for c in range(len(v))) for o in range(len(W))]
+
+
+def layer_norm(x, w, b, eps=1e-5):
+    x = _np(x); w = _np(w); b = _np(b)
+    out = np.empty_like(x)
+    for idx in np.ndindex(x.shape[:-1]):
+        out[idx] = _ln_vec(list(x[idx]), w, b, eps)
+    return out
+
+
+def triangle_multiplication(z, pair_mask, W, direction):
+    """z [1,N,N,C]; returns update [1,N,N,C] in float64.
+
+    outgoing: x[i,j,d] = sum_k a[i,k,d] * b[j,k,d]
+    incoming: x[i,j,d] = sum_k a[k,i,d] * b[k,j,d]
+    """
+    z = _np(z)[0]; m = _np(pair_mask)[0]
+    W = {k: _np(v) for k, v in W.items()}
+    N, _, C = z.shape
+    H2 = W["p_in.weight"].shape[0]          # 2 * hidden
+    Hd = H2 // 2
+    xin = [[None] * N for _ in range(N)]
+    a = np.zeros((N, N, Hd)); b = np.zeros((N, N, Hd))
+    for i in range(N):
+        for j in range(N):
+            x = _ln_vec(list(z[i, j]), W["norm_in.weight"], W["norm_in.bias"])
+            xin[i][j] = x
+            p = _matvec(W["p_in.weight"], x)
+            g = _matvec(W["g_in.weight"], x)
+            y = [p[o] * _sig(g[o]) * m[i, j] for o in range(H2)]
+            a[i, j] = y[:Hd]
+            b[i, j] = y[Hd:]
+    out = np.zeros((1, N, N, W["p_out.weight"].shape[0]))
+    for i in range(N):
+        for j in range(N):
+            x = [0.0] * Hd
+            for d in range(Hd):
+                acc = 0.0
+                for k in range(N):
+                    if direction == "outgoing":
+                        acc += a[i, k, d] * b[j, k, d]
+                    else:
+                        acc += a[k, i, d] * b[k, j, d]
+                x[d] = acc
+            xn = _ln_vec(x, W["norm_out.weight"], W["norm_out.bias"])
+            po = _matvec(W["p_out.weight"], xn)
+            go = _matvec(W["g_out.weight"], xin[i][j])
+            out[0, i, j] = [po[o] * _sig(go[o]) for o in range(len(po))]
+    return out
+
+
+def triangle_attention(z, pair_mask, W, starting, n_heads, head_dim, inf=1e9):
+    """Starting node: for each row i, head h, query j:
+        logit[k] = (q[i,j]/sqrt(d)) . k[i,k] + inf*(mask[i,k]-1) + bias[h][j][k],
+        bias[h][j][k] = LN(z)[j,k] . Wb[h]   (shared by all rows i)
+    Ending node: the same on z^T / mask^T, output transposed back.
+    """
+    z = _np(z)[0]; m = _np(pair_mask)[0]
+    W = {k: _np(v) for k, v in W.items()}
+    if not starting:
+        z = z.transpose(1, 0, 2); m = m.T
+    N = z.shape[0]
+    H, D = n_heads, head_dim
+    x = [[_ln_vec(list(z[i, j]), W["layer_norm.weight"], W["layer_norm.bias"]) for j in range(N)]
+         for i in range(N)]
+    bias = [[[sum(x[j][kk][c] * W["linear.weight"][h][c] for c in range(len(x[j][kk])))
+              for kk in range(N)] for j in range(N)] for h in range(H)]
+    q = [[_matvec(W["mha.linear_q.weight"], x[i][j]) for j in range(N)] for i in range(N)]
+    k = [[_matvec(W["mha.linear_k.weight"], x[i][j]) for j in range(N)] for i in range(N)]
+    v = [[_matvec(W["mha.linear_v.weight"], x[i][j]) for j in range(N)] for i in range(N)]
+    g = [[[_sig(t) for t in _matvec(W["mha.linear_g.weight"], x[i][j])] for j in range(N)]
+         for i in range(N)]
+    out = np.zeros((1, N, N, W["mha.linear_o.weight"].shape[0]))
+    for i in range(N):
+        for j in range(N):
+            o = [0.0] * (H * D)
+            for h in range(H):
+                logits = []
+                for kk in range(N):
+                    dot = sum((q[i][j][h * D + d] / math.sqrt(D)) * k[i][kk][h * D + d]
+                              for d in range(D))
+                    # the reference adds in fp32, mask term first (boltz2.py:802-803):
+                    # at |x| ~ 1e9 the fp32 sum swallows the O(1) terms, which makes a
+                    # fully masked row uniform.  Reproduce those two roundings.
+                    f32 = np.float32
+                    lg = f32(f32(dot) + f32(inf * (m[i, kk] - 1.0)))
+                    logits.append(float(f32(lg + f32(bias[h][j][kk]))))
+                mx = max(logits)
+                e = [math.exp(t - mx) for t in logits]
+                s = sum(e)
+                for d in range(D):
+                    o[h * D + d] = sum(e[kk] / s * v[i][kk][h * D + d] for kk in range(N))
+            o = [o[c] * g[i][j][c] for c in range(H * D)]
+            out[0, i, j] = _matvec(W["mha.linear_o.weight"], o)
+    if not starting:
+        out = out.transpose(0, 2, 1, 3)
+    return out
+
+
+def transition(x, W):
+    x = _np(x)
+    W = {k: _np(v) for k, v in W.items()}
+    out = np.zeros(x.shape[:-1] + (W["fc3.weight"].shape[0],))
+    for idx in np.ndindex(x.shape[:-1]):
+        xn = _ln_vec(list(x[idx]), W["norm.weight"], W["norm.bias"])
+        h1 = _matvec(W["fc1.weight"], xn)
+        h2 = _matvec(W["fc2.weight"], xn)
+        hh = [h1[t] * _sig(h1[t]) * h2[t] for t in range(len(h1))]
+        out[idx] = _matvec(W["fc3.weight"], hh)
+    return out
+
+
+def attention_pair_bias(s, z, mask, k_in, W, num_heads, inf=1e6):
+    """out_i = proj_o( sigmoid(proj_g s_i) * concat_h sum_j p_hij v_jh ),
+    p_hij = softmax_j( q_ih . k_jh / sqrt(d) + LN(z_ij) . Wz[h] - inf*(1-mask_j) ).
+    """
+    s = _np(s)[0]; z = _np(z)[0]; mask = _np(mask)[0]; k_in = _np(k_in)[0]
+    W = {k: _np(v) for k, v in W.items()}
+    N, C = s.shape
+    H = num_heads; D = C // H
+    q = [[a + bb for a, bb in zip(_matvec(W["proj_q.weight"], s[i]), W["proj_q.bias"])]
+         for i in range(N)]
+    kk = [_matvec(W["proj_k.weight"], k_in[j]) for j in range(N)]
+    vv = [_matvec(W["proj_v.weight"], k_in[j]) for j in range(N)]
+    g = [[_sig(t) for t in _matvec(W["proj_g.weight"], s[i])] for i in range(N)]
+    zb = [[_matvec(W["proj_z.1.weight"], _ln_vec(list(z[i, j]), W["proj_z.0.weight"],
+                                                 W["proj_z.0.bias"])) for j in range(N)]
+          for i in range(N)]
+    out = np.zeros((1, N, C))
+    for i in range(N):
+        o = [0.0] * C
+        for h in range(H):
+            logits = [sum(q[i][h * D + d] * kk[j][h * D + d] for d in range(D)) / math.sqrt(D)
+                      + zb[i][j][h] + (1.0 - mask[j]) * -inf for j in range(N)]
+            mx = max(logits)
+            e = [math.exp(t - mx) for t in logits]
+            ssum = sum(e)
+            for d in range(D):
+                o[h * D + d] = sum(e[j] / ssum * vv[j][h * D + d] for j in range(N))
+        out[0, i] = _matvec(W["proj_o.weight"], [g[i][c] * o[c] for c in range(C)])
+    return out
+
+
+def pairformer_layer(s, z, mask, pair_mask, W, tri_heads, tri_dim, att_heads):
+    """Layer composed from the scalar ops above, in ``reference.py:877-912`` order."""
+    def sub(p):
+        return {k[len(p) + 1:]: v for k, v in W.items() if k.startswith(p + ".")}
+    z = _np(z)
+    z = z + triangle_multiplication(z, pair_mask, sub("tri_mul_out"), "outgoing")
+    z = z + triangle_multiplication(z, pair_mask, sub("tri_mul_in"), "incoming")
+    z = z + triangle_attention(z, pair_mask, sub("tri_att_start"), True, tri_heads, tri_dim)
+    z = z + triangle_attention(z, pair_mask, sub("tri_att_end"), False, tri_heads, tri_dim)
+    z = z + transition(z, sub("transition_z"))
+    if s is None:
+        return None, z
+    s = _np(s)
+    sn = layer_norm(s, W["pre_norm_s.weight"], W["pre_norm_s.bias"])
+    s = s + attention_pair_bias(sn, z, mask, sn, sub("attention"), att_heads)
+    s = s + transition(s, sub("transition_s"))
+    return s, z

@@ -1,0 +1,254 @@
+"""fp32 CPU restatement of the reference Boltz-2 Pairformer (test oracle).
+
+TEST INFRASTRUCTURE ONLY -- see ``oracle/__init__.py``.
+
+Every function takes plain tensors plus a flat weight mapping whose keys are the
+reference state-dict names relative to the module (e.g. ``"norm_in.weight"`` for
+a triangle multiplication, ``"tri_mul_out.norm_in.weight"`` for a layer), so a
+checkpoint slice loads unchanged.  All arithmetic is torch fp32 on the CPU, in
+the order the reference writes it.  Dropout is the identity (inference,
+``tt_bio/boltz2.py:293-304`` with ``training=False``) and ``use_kernels=False``
+(the cuequivariance branch is never taken).
+
+Reference citations are ``path:line`` inside the tt-bio (moritztng/tt-boltz)
+source tree.
+"""
+from __future__ import annotations
+
+from math import sqrt
+from typing import Mapping, Optional
+
+import torch
+import torch.nn.functional as F
+
+Tensor = torch.Tensor
+Weights = Mapping[str, Tensor]
+
+#: ``tt_bio/data/const.py:775`` -- above this N the reference chunks triangle
+#: attention rows by 128, otherwise by 512 (``tt_bio/reference.py:982-988``).
+CHUNK_SIZE_THRESHOLD = 384
+
+
+def sub(w: Weights, prefix: str) -> dict:
+    """Slice ``w`` to the keys under ``prefix.`` with the prefix removed."""
+    p = prefix + "."
+    return {k[len(p):]: v for k, v in w.items() if k.startswith(p)}
+
+
+def layer_norm(x: Tensor, weight: Tensor, bias: Tensor, eps: float = 1e-5) -> Tensor:
+    """``nn.LayerNorm`` / ``tt_bio/boltz2.py:738-768`` (fp32 branch)."""
+    return F.layer_norm(x, (x.shape[-1],), weight, bias, eps)
+
+
+def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Tensor:
+    """``nn.Linear`` / ``tt_bio/boltz2.py:720-731`` (fp32 branch)."""
+    return F.linear(x, weight, bias)
+
+
+# --------------------------------------------------------------------------------------
+# Triangle multiplication  (tt_bio/reference.py:387-472 outgoing, 476-561 incoming)
+# --------------------------------------------------------------------------------------
+def triangle_multiplication(z: Tensor, pair_mask: Tensor, w: Weights, direction: str) -> Tensor:
+    """Return the update of ``TriangleMultiplication{Outgoing,Incoming}.forward``.
+
+    ``reference.py:455-472`` (outgoing) / ``544-561`` (incoming):
+    LN_in -> p_in * sigmoid(g_in) -> * pair_mask -> split a|b (fp32) ->
+    einsum ``bikd,bjkd->bijd`` (outgoing) or ``bkid,bkjd->bijd`` (incoming) ->
+    p_out(LN_out(x)) * sigmoid(g_out(LN_in(z))).
+    """
+    if direction not in ("outgoing", "incoming"):
+        raise ValueError(f"direction must be 'outgoing' or 'incoming', got {direction!r}")
+    x = layer_norm(z, w["norm_in.weight"], w["norm_in.bias"])              # reference.py:456
+    x_in = x                                                                # :457
+    x = linear(x, w["p_in.weight"]) * torch.sigmoid(linear(x, w["g_in.weight"]))  # :458
+    x = x * pair_mask.unsqueeze(-1)                                         # :461
+    a, b = torch.chunk(x.float(), 2, dim=-1)                                # :464
+    if direction == "outgoing":
+        x = torch.einsum("bikd,bjkd->bijd", a, b)                           # :467
+    else:
+        x = torch.einsum("bkid,bkjd->bijd", a, b)                           # :556
+    x = linear(layer_norm(x, w["norm_out.weight"], w["norm_out.bias"]), w["p_out.weight"])
+    return x * torch.sigmoid(linear(x_in, w["g_out.weight"]))               # :470
+
+
+# --------------------------------------------------------------------------------------
+# Triangle attention  (tt_bio/reference.py:219-376 + Attention 33-194 + boltz2.py:790-810)
+# --------------------------------------------------------------------------------------
+def _mha_rows(x: Tensor, tri_bias: Tensor, mask_bias: Tensor, w: Weights,
+              n_heads: int, head_dim: int) -> Tensor:
+    """``Attention.forward`` with ``use_kernels=False`` on a block of rows.
+
+    x [B,I,J,C]; tri_bias [B,1,H,J,K]; mask_bias [B,I,1,1,K].
+    ``reference.py:96-121`` (_prep_qkv: q scaled by 1/sqrt(d) before QK^T),
+    ``boltz2.py:790-810`` (_attention: a = qk; a += mask_bias; a += tri_bias;
+    softmax; a @ v), ``reference.py:123-136`` (_wrap_up: sigmoid gate, flatten,
+    linear_o).
+    """
+    shp = x.shape[:-1]
+    q = linear(x, w["linear_q.weight"]).view(shp + (n_heads, head_dim)).transpose(-2, -3)
+    k = linear(x, w["linear_k.weight"]).view(shp + (n_heads, head_dim)).transpose(-2, -3)
+    v = linear(x, w["linear_v.weight"]).view(shp + (n_heads, head_dim)).transpose(-2, -3)
+    q = q / sqrt(head_dim)
+    a = torch.matmul(q, k.transpose(-1, -2))      # [B,I,H,J,K]
+    a = a + mask_bias
+    a = a + tri_bias
+    a = torch.softmax(a, dim=-1)
+    o = torch.matmul(a, v).transpose(-2, -3)      # [B,I,J,H,d]
+    g = torch.sigmoid(linear(x, w["linear_g.weight"])).view(shp + (n_heads, head_dim))
+    o = (o * g).reshape(shp + (n_heads * head_dim,))
+    return linear(o, w["linear_o.weight"])
+
+
+def triangle_attention(z: Tensor, pair_mask: Optional[Tensor], w: Weights, starting: bool = True,
+                       chunk_size: Optional[int] = None, n_heads: int = 4, head_dim: int = 32,
+                       inf: float = 1e9) -> Tensor:
+    """Return the update of ``TriangleAttention{Starting,Ending}Node.forward``.
+
+    ``reference.py:294-365``: transpose for the ending node; LN; additive
+    ``inf*(mask-1)`` per (row, key); per-head bias ``linear(x)`` shared across
+    rows; row-chunked ``mha`` (``chunk_layer``, ``boltz2.py:542-628``, which is
+    an exact partition of the row batch); transpose back.
+
+    Weight keys are those of the reference module: ``layer_norm.*``,
+    ``linear.weight`` and ``mha.linear_{q,k,v,g,o}.weight``.
+    """
+    if pair_mask is None:
+        pair_mask = z.new_ones(z.shape[:-1])
+    if not starting:
+        z = z.transpose(-2, -3)
+        pair_mask = pair_mask.transpose(-1, -2)
+    x = layer_norm(z, w["layer_norm.weight"], w["layer_norm.bias"])      # :331
+    mask = pair_mask[..., :, None, None, :]                              # :334
+    mask_bias = inf * (mask - 1)                                         # :335
+    tri_bias = linear(x, w["linear.weight"]).permute(0, 3, 1, 2).unsqueeze(-4)  # :338-341
+    mw = sub(w, "mha")
+    n_rows = x.shape[1]
+    step = n_rows if chunk_size is None else chunk_size
+    outs = []
+    for r0 in range(0, n_rows, step):
+        r1 = min(r0 + step, n_rows)
+        outs.append(_mha_rows(x[:, r0:r1], tri_bias, mask_bias[:, r0:r1], mw, n_heads, head_dim))
+    out = torch.cat(outs, dim=1)
+    if not starting:
+        out = out.transpose(-2, -3)
+    return out
+
+
+def triangle_attention_core(q: Tensor, k: Tensor, v: Tensor, tri_bias: Tensor,
+                            mask: Tensor, scale: float) -> Tensor:
+    """Masked biased attention with the signature of the fused-op contract
+    ``kernel_triangular_attn(q, k, v, tri_bias, mask, scale)`` (``boltz2.py:815-817``).
+
+    q, k, v [B,I,H,J,d]; tri_bias [B,1,H,J,K]; mask [B,I,1,1,K] (bool or 0/1).
+    Semantics are those of the ``use_kernels=False`` path it replaces
+    (``reference.py:176-190`` + ``boltz2.py:790-810``): logits =
+    (scale*q) k^T + 1e9*(mask-1) + tri_bias, fp32 softmax over keys.
+    """
+    mask_bias = 1e9 * (mask.to(torch.float32) - 1.0)
+    a = torch.matmul(q * scale, k.transpose(-1, -2))
+    a = a + mask_bias
+    a = a + tri_bias
+    return torch.matmul(torch.softmax(a, dim=-1), v)
+
+
+# --------------------------------------------------------------------------------------
+# Transition  (tt_bio/boltz2.py:1188-1258)
+# --------------------------------------------------------------------------------------
+def transition(x: Tensor, w: Weights) -> Tensor:
+    """``Transition.forward`` with ``chunk_size=None`` (``boltz2.py:1240-1245``):
+    LN -> silu(fc1) * fc2 -> fc3 (no biases)."""
+    x = layer_norm(x, w["norm.weight"], w["norm.bias"])
+    x = F.silu(linear(x, w["fc1.weight"])) * linear(x, w["fc2.weight"])
+    return linear(x, w["fc3.weight"])
+
+
+# --------------------------------------------------------------------------------------
+# Single attention with pair bias  (tt_bio/boltz2.py:307-367)
+# --------------------------------------------------------------------------------------
+def attention_pair_bias(s: Tensor, z: Tensor, mask: Tensor, k_in: Tensor, w: Weights,
+                        num_heads: int = 16, inf: float = 1e6) -> Tensor:
+    """``AttentionPairBias.forward`` (``boltz2.py:343-367``), multiplicity 1.
+
+    q = proj_q(s) (+bias), k/v from ``k_in``; bias = proj_z(z) =
+    Linear(LN(z)) -> [B,H,N,N]; logits = qk^T/sqrt(d) + bias - inf*(1-mask_key);
+    softmax; o = P v; proj_o(sigmoid(proj_g(s)) * o).
+    """
+    B, N, c_s = s.shape
+    d = c_s // num_heads
+    q = linear(s, w["proj_q.weight"], w["proj_q.bias"]).view(B, -1, num_heads, d)
+    k = linear(k_in, w["proj_k.weight"]).view(B, -1, num_heads, d)
+    v = linear(k_in, w["proj_v.weight"]).view(B, -1, num_heads, d)
+    bias = linear(layer_norm(z, w["proj_z.0.weight"], w["proj_z.0.bias"]), w["proj_z.1.weight"])
+    bias = bias.permute(0, 3, 1, 2)                                       # "b ... h -> b h ..."
+    g = torch.sigmoid(linear(s, w["proj_g.weight"]))
+    attn = torch.einsum("bihd,bjhd->bhij", q.float(), k.float())
+    attn = attn / (d ** 0.5) + bias.float()
+    attn = attn + (1 - mask[:, None, None].float()) * -inf
+    attn = attn.softmax(dim=-1)
+    o = torch.einsum("bhij,bjhd->bihd", attn, v.float()).to(v.dtype)
+    o = o.reshape(B, -1, c_s)
+    return linear(g * o, w["proj_o.weight"])
+
+
+# --------------------------------------------------------------------------------------
+# Layer / stack  (tt_bio/reference.py:822-1003, no-seq 1007-1139)
+# --------------------------------------------------------------------------------------
+def chunk_size_for(n: int) -> int:
+    """``reference.py:982-988``: eval-mode triangle-attention row chunk."""
+    return 128 if n > CHUNK_SIZE_THRESHOLD else 512
+
+
+def pairformer_layer(s: Optional[Tensor], z: Tensor, mask: Optional[Tensor], pair_mask: Tensor,
+                     w: Weights, chunk_size: Optional[int] = None,
+                     tri_att_heads: int = 4, tri_att_head_dim: int = 32, att_heads: int = 16):
+    """``PairformerLayer.forward`` (``reference.py:865-914``); ``s=None`` gives
+    ``PairformerNoSeqLayer.forward`` (``reference.py:1035-1072``).
+
+    z += TMo; z += TMi; z += TAs; z += TAe; z += Tr_z;
+    s_n = LN(s); s += APB(s_n, z, mask, k_in=s_n); s += Tr_s(s).
+    """
+    z = z + triangle_multiplication(z, pair_mask, sub(w, "tri_mul_out"), "outgoing")
+    z = z + triangle_multiplication(z, pair_mask, sub(w, "tri_mul_in"), "incoming")
+    z = z + triangle_attention(z, pair_mask, sub(w, "tri_att_start"), True, chunk_size,
+                               tri_att_heads, tri_att_head_dim)
+    z = z + triangle_attention(z, pair_mask, sub(w, "tri_att_end"), False, chunk_size,
+                               tri_att_heads, tri_att_head_dim)
+    z = z + transition(z, sub(w, "transition_z"))
+    if s is None:
+        return None, z
+    s_normed = layer_norm(s.float(), w["pre_norm_s.weight"], w["pre_norm_s.bias"])
+    s = s.float() + attention_pair_bias(s_normed, z.float(), mask.float(), s_normed,
+                                        sub(w, "attention"), att_heads)
+    s = s + transition(s, sub(w, "transition_s"))
+    return s, z
+
+
+def pairformer_stack(s: Optional[Tensor], z: Tensor, mask: Optional[Tensor], pair_mask: Tensor,
+                     w: Weights, n_blocks: int, **kw):
+    """``PairformerModule.forward`` / ``PairformerNoSeqModule.forward`` in eval
+    mode (``reference.py:958-1003``, ``1106-1139``)."""
+    chunk = chunk_size_for(z.shape[1])
+    for i in range(n_blocks):
+        s, z = pairformer_layer(s, z, mask, pair_mask, sub(w, f"layers.{i}"), chunk, **kw)
+    return s, z
+
+
+def recycle(s_init: Tensor, z_init: Tensor, mask: Tensor, w_stack: Weights, w_rec: Weights,
+            n_blocks: int, recycling_steps: int, **kw):
+    """Trunk recycling loop of ``Boltz2.forward`` (``boltz2.py:5189-5248``) with
+    the template and MSA modules absent: s, z start at zero; each of the
+    ``recycling_steps + 1`` passes does s = s_init + s_recycle(s_norm(s)),
+    z = z_init + z_recycle(z_norm(z)), then the Pairformer stack.
+
+    ``w_rec`` keys: ``s_norm.*``, ``z_norm.*``, ``s_recycle.weight``, ``z_recycle.weight``.
+    """
+    pair_mask = mask[:, :, None] * mask[:, None, :]
+    s = torch.zeros_like(s_init)
+    z = torch.zeros_like(z_init)
+    for _ in range(recycling_steps + 1):
+        s = s_init + linear(layer_norm(s, w_rec["s_norm.weight"], w_rec["s_norm.bias"]),
+                            w_rec["s_recycle.weight"])
+        z = z_init + linear(layer_norm(z, w_rec["z_norm.weight"], w_rec["z_norm.bias"]),
+                            w_rec["z_recycle.weight"])
+        s, z = pairformer_stack(s, z, mask, pair_mask, w_stack, n_blocks, **kw)
+    return s, z

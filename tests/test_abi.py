@@ -1,0 +1,76 @@
+"""C-ABI boundary checks that need no GPU: the library loads, exports every symbol
+include/pairformer_hip.h declares, reports its ABI version, and rejects bad
+arguments with a status code and a message before launching anything."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from tt_boltz_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "pairformer_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pf_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared()
+    for must in ("pf_trimul_fwd", "pf_triatt_fwd", "pf_tri_attention", "pf_transition_fwd", "pf_apb_fwd",
+                 "pf_layernorm_fwd", "pf_linear_fwd", "pf_last_error", "pf_abi_version"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert set(_declared()) == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
+
+
+def test_abi_version():
+    assert _lib.load().pf_abi_version() == _lib.ABI_VERSION == 1
+
+
+def test_struct_layouts_match_header_order():
+    # the ctypes structs mirror the C structs field by field; spot-check sizes/offsets
+    assert _lib.TrimulArgs.z_in.offset == 32 and ctypes.sizeof(_lib.TrimulArgs) == 32 + 14 * 8
+    assert _lib.TransitionArgs.x_in.offset == 24
+    assert _lib.TriattArgs.z_in.offset == 32
+
+
+def _err():
+    return _lib.load().pf_last_error().decode()
+
+
+def test_rejects_null_and_bad_shapes_without_launching():
+    lib = _lib.load()
+    assert lib.pf_trimul_fwd(None) == -1 and "null args" in _err()
+    a = _lib.TrimulArgs(B=1, N=100, C=128, hidden=128, direction=0)
+    assert lib.pf_trimul_fwd(ctypes.byref(a)) == -1 and "multiple of 64" in _err()
+    a = _lib.TrimulArgs(B=1, N=128, C=64, hidden=64, direction=0)
+    assert lib.pf_trimul_fwd(ctypes.byref(a)) == -1 and "c_z = 128" in _err()
+    t = _lib.TriattArgs(B=1, N=128, C=128, H=8, D=16)
+    assert lib.pf_triatt_fwd(ctypes.byref(t)) == -1 and "H=4" in _err()
+    assert lib.pf_layernorm_fwd(None, None, None, None, 4, 8, 1e-5, None) == -1
+    assert lib.pf_linear_fwd(1, 1, None, None, 1, 4, 15, 32, None) == -1 and "K % 16" in _err()
+
+
+def test_workspace_sizes():
+    lib = _lib.load()
+    assert lib.pf_trimul_workspace_size(1, 512, 128) == 128 * 512 * 512 * (2 + 2 + 4)
+    assert lib.pf_triatt_workspace_size(1, 64, 128, 4, 32) > 0
+    assert lib.pf_triatt_workspace_size(1, 64, 128, 8, 16) == 0
+    assert lib.pf_transition_workspace_size(4096, 128, 512) == 0          # fused, no scratch
+    assert lib.pf_transition_workspace_size(100, 384, 1536) == 100 * (384 + 1536) * 4
+
+
+def test_python_check_raises_with_message():
+    lib = _lib.load()
+    lib.pf_trimul_fwd(None)
+    with pytest.raises(RuntimeError, match="null args"):
+        _lib.check(-1, "pf_trimul_fwd")

@@ -1,0 +1,242 @@
+"""GPU parity: every HIP path against the fp32 CPU oracle on identical seeded inputs.
+
+Tolerance (bf16 compute vs fp32 reference), with
+errors normalised by the RMS of the reference output:
+    max |gpu - ref| <= 2e-2 * rms(ref)   and   mean |gpu - ref| <= 2e-3 * rms(ref).
+Masked configurations report the valid region and the full tensor separately;
+both must meet the bar.
+"""
+import pytest
+import torch
+
+from oracle import pairformer_ref as ref
+from tt_boltz_amd import ops, pairformer, synthetic
+
+pytestmark = pytest.mark.gpu
+
+MAX_TOL, MEAN_TOL = 2e-2, 2e-3
+
+
+def stats(gpu_t, ref_t):
+    g = gpu_t.detach().double().cpu()
+    r = ref_t.detach().double().cpu()
+    rms = r.pow(2).mean().sqrt().clamp_min(1e-12)
+    d = (g - r).abs()
+    return (d.max() / rms).item(), (d.mean() / rms).item()
+
+
+def check(name, gpu_t, ref_t, max_tol=MAX_TOL, mean_tol=MEAN_TOL):
+    mx, mn = stats(gpu_t, ref_t)
+    print(f"[parity] {name}: max/rms={mx:.3e} mean/rms={mn:.3e}", flush=True)
+    assert torch.isfinite(gpu_t).all(), f"{name}: non-finite output"
+    assert mx <= max_tol and mn <= mean_tol, f"{name}: max/rms={mx:.3e} mean/rms={mn:.3e}"
+
+
+def _sub_w(seed, prefix):
+    return ref.sub(synthetic.draw({f"{prefix}.{k}": v for k, v in synthetic.layer_shapes().items()
+                                   if k.startswith(prefix + ".")}, seed), prefix)
+
+
+def _dev_w(w, dev, strip=""):
+    out = {}
+    for k, v in w.items():
+        kk = k[len(strip):] if strip and k.startswith(strip) else k
+        out[kk] = ops.f32(v, dev) if v.dim() == 1 else ops.bf16(v, dev)
+    return out
+
+
+def _inputs(N, seed, pad_tail=0, rand_mask=False):
+    s, z, mask, pm = synthetic.pair_inputs(N, seed, pad_tail=pad_tail)
+    if rand_mask:
+        g = torch.Generator().manual_seed(seed + 100)
+        pm = pm * (torch.rand(pm.shape, generator=g) > 0.15).float()
+    return s, z, mask, pm
+
+
+# ------------------------------------------------------------------------------ contraction
+@pytest.mark.parametrize("N", [64, 192, 256])
+def test_contract_matches_fp32_matmul(gpu, N):
+    g = torch.Generator().manual_seed(N)
+    A = torch.randn((3, N, N), generator=g).to(torch.bfloat16)
+    Bm = torch.randn((3, N, N), generator=g).to(torch.bfloat16)
+    X = torch.empty((3, N, N), dtype=torch.float32, device=gpu)
+    ops.launch_trimul_contract(A.to(gpu), Bm.to(gpu), X)
+    want = torch.bmm(A.float(), Bm.float().transpose(1, 2))
+    mx, _ = stats(X, want)
+    print(f"[parity] contract N={N}: max/rms={mx:.3e}", flush=True)
+    assert mx < 1e-5
+
+
+# ------------------------------------------------------------------------------ triangle multiplication
+@pytest.mark.parametrize("N,direction,rand_mask", [(64, "outgoing", False), (64, "incoming", True),
+                                                   (192, "outgoing", True), (192, "incoming", False)])
+def test_trimul_small(gpu, N, direction, rand_mask):
+    prefix = "tri_mul_out" if direction == "outgoing" else "tri_mul_in"
+    w = _sub_w(7, prefix)
+    _, z, _, pm = _inputs(N, 11, pad_tail=N // 8, rand_mask=rand_mask)
+    want = ref.triangle_multiplication(z, pm, w, direction)
+    got = ops.triangle_multiplicative_update(z.to(gpu), direction, pm.to(gpu), **{
+        "norm_in_weight": w["norm_in.weight"], "norm_in_bias": w["norm_in.bias"], "p_in_weight": w["p_in.weight"],
+        "g_in_weight": w["g_in.weight"], "norm_out_weight": w["norm_out.weight"], "norm_out_bias": w["norm_out.bias"],
+        "p_out_weight": w["p_out.weight"], "g_out_weight": w["g_out.weight"]})
+    check(f"trimul {direction} N={N} rand_mask={rand_mask}", got, want)
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_config1(gpu, direction):
+    """N=512, last 51 tokens padded, seed 1."""
+    cfg = synthetic.CONFIGS[1]
+    prefix = "tri_mul_out" if direction == "outgoing" else "tri_mul_in"
+    w = _sub_w(cfg["seed"], prefix)
+    _, z, _, pm = _inputs(cfg["N"], cfg["seed"], pad_tail=cfg["pad_tail"])
+    want = ref.triangle_multiplication(z, pm, w, direction)
+    zd = z.to(gpu)
+    out = torch.empty_like(zd)
+    ws = ops.workspace(ops.trimul_workspace_bytes(1, cfg["N"]), gpu)
+    ops.launch_trimul(zd, out, pm.to(gpu).contiguous(), _dev_w(w, gpu), 0 if direction == "outgoing" else 1, ws,
+                      accumulate=False)
+    nv = cfg["N"] - cfg["pad_tail"]
+    check(f"config1 trimul {direction} valid", out[:, :nv, :nv], want[:, :nv, :nv])
+    check(f"config1 trimul {direction} full", out, want)
+
+
+def test_trimul_inplace_accumulate(gpu):
+    N = 128
+    w = _dev_w(_sub_w(5, "tri_mul_out"), gpu)
+    _, z, _, _ = _inputs(N, 12)
+    zd = z.to(gpu)
+    ws = ops.workspace(ops.trimul_workspace_bytes(1, N), gpu)
+    upd = torch.empty_like(zd)
+    ops.launch_trimul(zd, upd, None, w, 0, ws, accumulate=False)
+    zi = zd.clone()
+    ops.launch_trimul(zi, zi, None, w, 0, ws, accumulate=True)
+    assert torch.equal(zi, zd + upd)
+
+
+# ------------------------------------------------------------------------------ triangle attention
+@pytest.mark.parametrize("N,ending,rand_mask", [(64, False, False), (64, True, True), (192, False, True),
+                                                (192, True, False)])
+def test_triatt_small(gpu, N, ending, rand_mask):
+    prefix = "tri_att_end" if ending else "tri_att_start"
+    w = _sub_w(9, prefix)
+    _, z, _, pm = _inputs(N, 13, pad_tail=N // 8, rand_mask=rand_mask)
+    want = ref.triangle_attention(z, pm, w, not ending, None)
+    zd = z.to(gpu)
+    out = torch.empty_like(zd)
+    ws = ops.workspace(ops.triatt_workspace_bytes(1, N), gpu)
+    ops.launch_triatt(zd, out, pm.to(gpu).contiguous(), _dev_w(w, gpu, "mha."), ending, ws, accumulate=False)
+    check(f"triatt ending={ending} N={N} rand_mask={rand_mask}", out, want)
+
+
+@pytest.mark.parametrize("ending", [False, True])
+def test_triatt_config2(gpu, ending):
+    """N=512, last 51 tokens padded, seed 2; oracle unchunked fp32."""
+    cfg = synthetic.CONFIGS[2]
+    prefix = "tri_att_end" if ending else "tri_att_start"
+    w = _sub_w(cfg["seed"], prefix)
+    _, z, _, pm = _inputs(cfg["N"], cfg["seed"], pad_tail=cfg["pad_tail"])
+    want = ref.triangle_attention(z, pm, w, not ending, 64)
+    zd = z.to(gpu)
+    out = torch.empty_like(zd)
+    ws = ops.workspace(ops.triatt_workspace_bytes(1, cfg["N"]), gpu)
+    ops.launch_triatt(zd, out, pm.to(gpu).contiguous(), _dev_w(w, gpu, "mha."), ending, ws, accumulate=False)
+    nv = cfg["N"] - cfg["pad_tail"]
+    check(f"config2 triatt ending={ending} valid", out[:, :nv, :nv], want[:, :nv, :nv])
+    check(f"config2 triatt ending={ending} full", out, want)
+
+
+def test_tri_attention_core(gpu):
+    g = torch.Generator().manual_seed(3)
+    B, N, H, D = 1, 96, 4, 32
+    q, k, v = (torch.randn((B, N, H, N, D), generator=g) for _ in range(3))
+    bias = torch.randn((B, 1, H, N, N), generator=g)
+    mask = (torch.rand((B, N, 1, 1, N), generator=g) > 0.2).float()
+    mask[:, 5] = 0.0   # a fully masked row: uniform average of v
+    want = ref.triangle_attention_core(q, k, v, bias, mask, D ** -0.5)
+    got = ops.triangle_attention(q.to(gpu), k.to(gpu), v.to(gpu), bias.to(gpu), mask.to(gpu))
+    check("tri_attention core", got, want)
+    check("tri_attention core masked row", got[:, 5], v[:, 5].mean(dim=-2, keepdim=True).expand(B, H, N, D))
+
+
+# ------------------------------------------------------------------------------ transition / APB
+def test_transition_pair(gpu):
+    w = _sub_w(4, "transition_z")
+    _, z, _, _ = _inputs(64, 14)
+    want = ref.transition(z, w)
+    got = ops.transition(z.to(gpu), w["norm.weight"], w["norm.bias"], w["fc1.weight"], w["fc2.weight"],
+                         w["fc3.weight"])
+    check("transition z", got, want)
+
+
+def test_transition_single(gpu):
+    w = _sub_w(4, "transition_s")
+    s, _, _, _ = _inputs(100, 15)
+    want = ref.transition(s, w)
+    got = ops.transition(s.to(gpu), w["norm.weight"], w["norm.bias"], w["fc1.weight"], w["fc2.weight"],
+                         w["fc3.weight"])
+    check("transition s", got, want)
+
+
+def test_attention_pair_bias(gpu):
+    w = _sub_w(6, "attention")
+    s, z, mask, _ = _inputs(100, 16, pad_tail=7)
+    want = ref.attention_pair_bias(s, z, mask, s, w, 16)
+    got = ops.attention_pair_bias(s.to(gpu), z.to(gpu), mask.to(gpu), s.to(gpu), w, 16)
+    check("attention_pair_bias", got[:, :93], want[:, :93])
+
+
+# ------------------------------------------------------------------------------ layer / module
+def test_layer_config0(gpu):
+    """one full PairformerLayer, N=128, seed 0, masks all ones."""
+    cfg = synthetic.CONFIGS[0]
+    w = synthetic.stack_weights(1, cfg["seed"])
+    s, z, mask, pm = _inputs(cfg["N"], cfg["seed"])
+    s_ref, z_ref = ref.pairformer_stack(s, z, mask, pm, w, 1)
+    mod = pairformer.PairformerModule(1, 32, 4, 24, 16, True)
+    mod.load_state_dict(w)
+    s_got, z_got = mod(s.to(gpu), z.to(gpu), mask.to(gpu), pm.to(gpu))
+    check("config0 layer z", z_got, z_ref)
+    check("config0 layer s", s_got, s_ref)
+
+
+def test_module_dropin_padding(gpu):
+    """Drop-in on CPU tensors (like the reference's tests/test_tenstorrent.py:31-43):
+    2 blocks, N=100 (padded to 128 inside), outputs returned on the CPU."""
+    w = synthetic.stack_weights(2, 21)
+    s, z, mask, pm = _inputs(100, 22)
+    s_ref, z_ref = ref.pairformer_stack(s, z, mask, pm, w, 2)
+    mod = pairformer.PairformerModule(2, 32, 4, 24, 16, True)
+    mod.load_state_dict(w)
+    s_got, z_got = mod(s, z)
+    assert s_got.device.type == "cpu" and z_got.shape == z.shape and s_got.shape == s.shape
+    check("module N=100 z", z_got, z_ref)
+    check("module N=100 s", s_got, s_ref)
+
+
+def test_module_noseq_affinity_masks(gpu):
+    """No-seq stack with a permuted half-masked token set (cf. tests/test_tenstorrent.py:55-66)."""
+    N = 96
+    w = synthetic.stack_weights(2, 23, transform_s=False)
+    _, z, _, _ = _inputs(N, 24)
+    g = torch.Generator().manual_seed(25)
+    m = torch.ones((1, N)); m[0, : N // 2] = 0
+    m = m[:, torch.randperm(N, generator=g)]
+    pm = m[:, :, None] * m[:, None, :]
+    _, z_ref = ref.pairformer_stack(None, z, None, pm, w, 2)
+    mod = pairformer.PairformerModule(2, 32, 4, None, None, False, affinity=True)
+    mod.load_state_dict(w)
+    _, z_got = mod(None, z.to(gpu), pair_mask=pm.to(gpu))
+    check("module no-seq affinity z", z_got, z_ref)
+
+
+def test_recycler(gpu):
+    N = 64
+    w = synthetic.stack_weights(1, 26)
+    w_rec = synthetic.draw(synthetic.recycle_shapes(), 27)
+    s_init, z_init, mask, _ = _inputs(N, 28)
+    s_ref, z_ref = ref.recycle(s_init, z_init, mask, w, w_rec, 1, 1)
+    pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, w)
+    rec = pairformer.TrunkRecycler(pf, w_rec)
+    s_got, z_got = rec(s_init.to(gpu), z_init.to(gpu), mask.to(gpu), 1)
+    check("recycler z", z_got, z_ref)
+    check("recycler s", s_got, s_ref)

@@ -1,0 +1,303 @@
+"""Pin the CPU oracle (oracle/pairformer_ref.py) independently of its own formulas.
+
+Each oracle function is checked against at least one of: the scalar-loop
+restatement in oracle/brute.py (float64, explicit (i, j, k) indexing), a library
+routine (torch.nn.functional.scaled_dot_product_attention / layer_norm /
+float8_e4m3fn casts), or an invariant that a plausible mistake breaks
+(transposition identities, mask invariance, chunking invariance, closed-form
+special cases).  The reference ships no golden vectors for this path.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import brute, fp8_emu
+from oracle import pairformer_ref as ref
+from tt_boltz_amd import synthetic
+
+
+def _w(shapes, seed):
+    return synthetic.draw(shapes, seed)
+
+
+def _trimul_w(c, seed=0):
+    return _w({"norm_in.weight": (c,), "norm_in.bias": (c,), "p_in.weight": (2 * c, c), "g_in.weight": (2 * c, c),
+               "norm_out.weight": (c,), "norm_out.bias": (c,), "p_out.weight": (c, c), "g_out.weight": (c, c)}, seed)
+
+
+def _triatt_w(c, H, D, seed=0):
+    return _w({"layer_norm.weight": (c,), "layer_norm.bias": (c,), "linear.weight": (H, c),
+               "mha.linear_q.weight": (H * D, c), "mha.linear_k.weight": (H * D, c),
+               "mha.linear_v.weight": (H * D, c), "mha.linear_g.weight": (H * D, c),
+               "mha.linear_o.weight": (c, H * D)}, seed)
+
+
+def _rand_mask(N, seed, p=0.3):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.rand((1, N, N), generator=g) > p).float()
+
+
+def _close(a, b, tol=2e-5):
+    a = torch.as_tensor(np.asarray(a), dtype=torch.float64)
+    b = torch.as_tensor(np.asarray(b), dtype=torch.float64)
+    scale = b.abs().max().clamp_min(1e-6)
+    assert ((a - b).abs().max() / scale).item() < tol, ((a - b).abs().max().item(), scale.item())
+
+
+# ----------------------------------------------------------------------------- trimul
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_matches_brute(direction):
+    N, c = 5, 8
+    z = torch.randn((1, N, N, c), generator=torch.Generator().manual_seed(1))
+    m = _rand_mask(N, 2)
+    w = _trimul_w(c, 3)
+    _close(ref.triangle_multiplication(z, m, w, direction), brute.triangle_multiplication(z, m, w, direction))
+
+
+def test_trimul_transpose_identity():
+    """incoming(z^T) == outgoing(z) when the output gate is constant (g_out = 0):
+    x_ij = sum_k a_ik b_jk is the same sum in both einsum strings after transposing z."""
+    N, c = 7, 16
+    z = torch.randn((1, N, N, c), generator=torch.Generator().manual_seed(4))
+    w = _trimul_w(c, 5)
+    w["g_out.weight"] = torch.zeros_like(w["g_out.weight"])
+    ones = torch.ones((1, N, N))
+    out = ref.triangle_multiplication(z, ones, w, "outgoing")
+    inc = ref.triangle_multiplication(z.transpose(1, 2), ones, w, "incoming")
+    _close(inc, out, 1e-5)
+    # and the two directions differ for a non-symmetric z (catches a swapped einsum)
+    assert (ref.triangle_multiplication(z, ones, w, "incoming") - out).abs().max() > 1e-3
+
+
+def test_trimul_symmetric_input():
+    N, c = 6, 8
+    z = torch.randn((1, N, N, c), generator=torch.Generator().manual_seed(6))
+    z = 0.5 * (z + z.transpose(1, 2))
+    w = _trimul_w(c, 7)
+    ones = torch.ones((1, N, N))
+    _close(ref.triangle_multiplication(z, ones, w, "incoming"), ref.triangle_multiplication(z, ones, w, "outgoing"), 1e-5)
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_masked_token_invariance(direction):
+    """With pair_mask = m m^T and m_r = 0, z at pairs touching token r cannot change
+    the update at pairs (i, j) with i, j != r (both a and b are masked)."""
+    N, c, r = 6, 8, 2
+    g = torch.Generator().manual_seed(8)
+    z = torch.randn((1, N, N, c), generator=g)
+    m = torch.ones((1, N)); m[0, r] = 0
+    pm = m[:, :, None] * m[:, None, :]
+    w = _trimul_w(c, 9)
+    z2 = z.clone()
+    z2[0, r, :] += torch.randn((N, c), generator=g)
+    z2[0, :, r] += torch.randn((N, c), generator=g)
+    keep = torch.ones(N, dtype=torch.bool); keep[r] = False
+    o1 = ref.triangle_multiplication(z, pm, w, direction)[0][keep][:, keep]
+    o2 = ref.triangle_multiplication(z2, pm, w, direction)[0][keep][:, keep]
+    _close(o2, o1, 1e-6)
+
+
+# ----------------------------------------------------------------------------- triatt
+@pytest.mark.parametrize("starting", [True, False])
+def test_triatt_matches_brute(starting):
+    N, c, H, D = 4, 8, 2, 4
+    z = torch.randn((1, N, N, c), generator=torch.Generator().manual_seed(10))
+    m = _rand_mask(N, 11, 0.25)
+    w = _triatt_w(c, H, D, 12)
+    _close(ref.triangle_attention(z, m, w, starting, None, H, D),
+           brute.triangle_attention(z, m, w, starting, H, D))
+
+
+def test_triatt_chunking_invariance():
+    N, c, H, D = 9, 16, 2, 8
+    z = torch.randn((1, N, N, c), generator=torch.Generator().manual_seed(13))
+    m = _rand_mask(N, 14)
+    w = _triatt_w(c, H, D, 15)
+    full = ref.triangle_attention(z, m, w, True, None, H, D)
+    for ch in (1, 2, 4, N):
+        _close(ref.triangle_attention(z, m, w, True, ch, H, D), full, 1e-6)
+
+
+def test_triatt_ending_is_transposed_starting():
+    N, c, H, D = 6, 16, 2, 8
+    z = torch.randn((1, N, N, c), generator=torch.Generator().manual_seed(16))
+    m = _rand_mask(N, 17)
+    w = _triatt_w(c, H, D, 18)
+    end = ref.triangle_attention(z, m, w, False, None, H, D)
+    start_t = ref.triangle_attention(z.transpose(1, 2), m.transpose(1, 2), w, True, None, H, D).transpose(1, 2)
+    _close(end, start_t, 1e-6)
+
+
+def test_triatt_core_matches_sdpa():
+    """Masked biased attention vs torch's scaled_dot_product_attention (library routine)."""
+    g = torch.Generator().manual_seed(19)
+    B, I, H, J, D = 1, 5, 3, 7, 8
+    q, k, v = (torch.randn((B, I, H, J, D), generator=g) for _ in range(3))
+    bias = torch.randn((B, 1, H, J, J), generator=g)
+    mask = (torch.rand((B, I, 1, 1, J), generator=g) > 0.3).float()
+    mask[..., 0] = 1.0
+    scale = 0.3
+    o = ref.triangle_attention_core(q, k, v, bias, mask, scale)
+    o_lib = F.scaled_dot_product_attention(q, k, v, attn_mask=bias + 1e9 * (mask - 1), scale=scale)
+    _close(o, o_lib, 1e-5)
+
+
+def test_triatt_core_all_masked_row_is_uniform():
+    """A fully masked row softmaxes to the uniform average of v (fp32 -1e9 saturation,
+    tt_bio/reference.py:334-335)."""
+    g = torch.Generator().manual_seed(20)
+    B, I, H, J, D = 1, 3, 2, 6, 4
+    q, k, v = (torch.randn((B, I, H, J, D), generator=g) for _ in range(3))
+    bias = torch.randn((B, 1, H, J, J), generator=g)
+    mask = torch.ones((B, I, 1, 1, J)); mask[:, 1] = 0.0
+    o = ref.triangle_attention_core(q, k, v, bias, mask, D ** -0.5)
+    expect = v[:, 1].mean(dim=-2, keepdim=True).expand(B, H, J, D)
+    _close(o[:, 1], expect, 1e-6)
+
+
+def test_triatt_core_scalar_softmax():
+    """H = 1, D = 1: o_j = sum_k softmax_k(scale*q_j*k_k + b_jk) v_k, by explicit loops."""
+    J = 5
+    g = torch.Generator().manual_seed(21)
+    q, k, v = (torch.randn((1, 1, 1, J, 1), generator=g) for _ in range(3))
+    bias = torch.randn((1, 1, 1, J, J), generator=g)
+    o = ref.triangle_attention_core(q, k, v, bias, torch.ones((1, 1, 1, 1, J)), 0.7)
+    for j in range(J):
+        lg = [0.7 * q[0, 0, 0, j, 0].item() * k[0, 0, 0, kk, 0].item() + bias[0, 0, 0, j, kk].item() for kk in range(J)]
+        mx = max(lg)
+        e = [math.exp(x - mx) for x in lg]
+        want = sum(ei * v[0, 0, 0, kk, 0].item() for kk, ei in enumerate(e)) / sum(e)
+        assert abs(o[0, 0, 0, j, 0].item() - want) < 1e-5
+
+
+# ----------------------------------------------------------------------------- transition / APB / LN
+def test_transition_matches_brute():
+    c, hdn = 8, 16
+    x = torch.randn((1, 3, 4, c), generator=torch.Generator().manual_seed(22))
+    w = _w({"norm.weight": (c,), "norm.bias": (c,), "fc1.weight": (hdn, c), "fc2.weight": (hdn, c),
+            "fc3.weight": (c, hdn)}, 23)
+    _close(ref.transition(x, w), brute.transition(x, w))
+
+
+def test_layer_norm_matches_brute():
+    x = torch.randn((3, 5, 16), generator=torch.Generator().manual_seed(24)) * 3 + 1
+    w, b = torch.rand(16) + 0.5, torch.randn(16)
+    _close(ref.layer_norm(x, w, b), brute.layer_norm(x, w, b))
+
+
+def _apb_w(c_s, c_z, H, seed):
+    return _w({"proj_q.weight": (c_s, c_s), "proj_q.bias": (c_s,), "proj_k.weight": (c_s, c_s),
+               "proj_v.weight": (c_s, c_s), "proj_g.weight": (c_s, c_s), "proj_o.weight": (c_s, c_s),
+               "proj_z.0.weight": (c_z,), "proj_z.0.bias": (c_z,), "proj_z.1.weight": (H, c_z)}, seed)
+
+
+def test_apb_matches_brute():
+    N, c_s, c_z, H = 5, 8, 8, 2
+    g = torch.Generator().manual_seed(25)
+    s = torch.randn((1, N, c_s), generator=g)
+    z = torch.randn((1, N, N, c_z), generator=g)
+    mask = torch.ones((1, N)); mask[0, 3] = 0
+    w = _apb_w(c_s, c_z, H, 26)
+    _close(ref.attention_pair_bias(s, z, mask, s, w, H), brute.attention_pair_bias(s, z, mask, s, w, H))
+
+
+# ----------------------------------------------------------------------------- layer / stack
+def _small_layer_weights(seed):
+    return synthetic.draw(synthetic.layer_shapes(c_z=8, c_s=8, tri_heads=2, tri_dim=4, att_heads=2), seed)
+
+
+def test_layer_matches_brute_composition():
+    """The oracle layer equals the layer composed from independently written scalar ops
+    in reference.py:877-912 order (catches a wrong order, a missing residual or a
+    sub-block wired to the wrong weights)."""
+    N = 4
+    g = torch.Generator().manual_seed(27)
+    s = torch.randn((1, N, 8), generator=g)
+    z = torch.randn((1, N, N, 8), generator=g)
+    mask = torch.ones((1, N)); mask[0, 3] = 0
+    pm = mask[:, :, None] * mask[:, None, :]
+    w = _small_layer_weights(28)
+    so, zo = ref.pairformer_layer(s, z, mask, pm, w, None, 2, 4, 2)
+    sb, zb = brute.pairformer_layer(s, z, mask, pm, w, 2, 4, 2)
+    _close(zo, zb)
+    _close(so, sb)
+
+
+def test_stack_chunk_size_rule():
+    assert ref.chunk_size_for(384) == 512 and ref.chunk_size_for(385) == 128
+
+
+def test_noseq_layer_is_seq_layer_z():
+    N = 5
+    g = torch.Generator().manual_seed(29)
+    s = torch.randn((1, N, 8), generator=g)
+    z = torch.randn((1, N, N, 8), generator=g)
+    mask = torch.ones((1, N))
+    pm = mask[:, :, None] * mask[:, None, :]
+    w = _small_layer_weights(30)
+    _, z1 = ref.pairformer_layer(s, z, mask, pm, w, None, 2, 4, 2)
+    s2, z2 = ref.pairformer_layer(None, z, None, pm, w, None, 2, 4, 2)
+    assert s2 is None
+    _close(z2, z1, 1e-7)
+
+
+def test_recycle_zero_passes_is_one_stack_call():
+    """recycling_steps = 0: s = s_init + W LN(0) = s_init + W b_norm (LN of zeros is its bias)."""
+    N = 4
+    g = torch.Generator().manual_seed(31)
+    s_init = torch.randn((1, N, 8), generator=g)
+    z_init = torch.randn((1, N, N, 8), generator=g)
+    mask = torch.ones((1, N))
+    w_stack = synthetic.draw({f"layers.0.{k}": v for k, v in synthetic.layer_shapes(
+        c_z=8, c_s=8, tri_heads=2, tri_dim=4, att_heads=2).items()}, 32)
+    w_rec = synthetic.draw(synthetic.recycle_shapes(c_z=8, c_s=8), 33)
+    s_r, z_r = ref.recycle(s_init, z_init, mask, w_stack, w_rec, 1, 0, tri_att_heads=2, tri_att_head_dim=4,
+                           att_heads=2)
+    s0 = s_init + w_rec["s_norm.bias"] @ w_rec["s_recycle.weight"].T
+    z0 = z_init + w_rec["z_norm.bias"] @ w_rec["z_recycle.weight"].T
+    pm = mask[:, :, None] * mask[:, None, :]
+    s_e, z_e = ref.pairformer_layer(s0, z0, mask, pm, ref.sub(w_stack, "layers.0"), 512, 2, 4, 2)
+    _close(z_r, z_e, 1e-6)
+    _close(s_r, s_e, 1e-6)
+
+
+# ----------------------------------------------------------------------------- fp8 emulator
+def test_e4m3_rounding_matches_torch_cast():
+    g = torch.Generator().manual_seed(34)
+    x = torch.randn(20000, generator=g) * torch.exp2(torch.randint(-12, 9, (20000,), generator=g).float())
+    x = x.clamp(-448, 448)
+    ours = fp8_emu.round_e4m3(x)
+    lib = x.to(torch.float8_e4m3fn).to(torch.float32)
+    assert torch.equal(ours, lib)
+
+
+def test_e4m3_representable_roundtrip_and_saturation():
+    vals = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).to(torch.float32)
+    vals = vals[torch.isfinite(vals)]
+    assert torch.equal(fp8_emu.round_e4m3(vals), vals)
+    assert fp8_emu.round_e4m3(torch.tensor([1e6, -500.0, 449.0])).tolist() == [448.0, -448.0, 448.0]
+
+
+def test_mx8_scale_rule_and_block_independence():
+    g = torch.Generator().manual_seed(35)
+    x = torch.randn((4, 64), generator=g)
+    x[1, :32] *= 1000.0
+    q, e = fp8_emu.quantize_mx8(x)
+    amax = x.reshape(4, 2, 32).abs().amax(-1)
+    assert torch.equal(e, (torch.floor(torch.log2(amax)) - 8).to(torch.int32))
+    # blocks are quantized independently: scaling one block does not change another
+    x2 = x.clone(); x2[2, 32:] *= 64.0
+    q2, _ = fp8_emu.quantize_mx8(x2)
+    assert torch.equal(q2[2, :32], q[2, :32]) and torch.equal(q2[:2], q[:2])
+    fq = fp8_emu.fake_quant_mx8(x)
+    # RNE with 3 mantissa bits: half an ulp is <= |x| * 2^-4 in the normal range and
+    # 2^-10 * scale (half the subnormal spacing 2^-9) below it
+    scale = torch.exp2(e.float()).repeat_interleave(32, dim=-1)
+    sat = x.abs() >= 448.0 * scale          # OCP MX: values in [448, 512) * scale clamp to 448
+    assert torch.equal(fq[sat], torch.copysign(448.0 * scale[sat], x[sat]))
+    bound = torch.maximum(x.abs() * 2 ** -4, scale * 2 ** -10)
+    assert ((fq - x).abs() <= bound)[~sat].all()
+    assert torch.equal(fp8_emu.fake_quant_mx8(torch.zeros(32)), torch.zeros(32))

@@ -1,0 +1,116 @@
+"""ctypes binding of libpairformer_hip.so (the C ABI in include/pairformer_hip.h).
+
+The library is loaded from this directory.  If it is missing, every call raises:
+there is no CPU or torch fallback for any operation of this package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libpairformer_hip.so")
+ABI_VERSION = 1
+
+c_int, c_float, c_long, c_size_t, c_void_p = ctypes.c_int, ctypes.c_float, ctypes.c_long, ctypes.c_size_t, ctypes.c_void_p
+c_float_p = c_void_p   # device pointers are passed as integers
+
+
+class TrimulArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int), ("N", c_int), ("C", c_int), ("hidden", c_int), ("direction", c_int),
+        ("accumulate", c_int), ("eps", c_float),
+        ("z_in", c_void_p), ("out", c_void_p), ("pair_mask", c_void_p),
+        ("norm_in_w", c_void_p), ("norm_in_b", c_void_p), ("p_in_w", c_void_p), ("g_in_w", c_void_p),
+        ("norm_out_w", c_void_p), ("norm_out_b", c_void_p), ("p_out_w", c_void_p), ("g_out_w", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
+    ]
+
+
+class TriattArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int), ("N", c_int), ("C", c_int), ("H", c_int), ("D", c_int), ("ending", c_int),
+        ("accumulate", c_int), ("eps", c_float),
+        ("z_in", c_void_p), ("out", c_void_p), ("pair_mask", c_void_p),
+        ("ln_w", c_void_p), ("ln_b", c_void_p), ("w_bias", c_void_p),
+        ("w_q", c_void_p), ("w_k", c_void_p), ("w_v", c_void_p), ("w_g", c_void_p), ("w_o", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
+    ]
+
+
+class TransitionArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_long), ("C", c_int), ("hidden", c_int), ("accumulate", c_int), ("eps", c_float),
+        ("x_in", c_void_p), ("out", c_void_p), ("norm_w", c_void_p), ("norm_b", c_void_p),
+        ("fc1_w", c_void_p), ("fc2_w", c_void_p), ("fc3_w", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
+    ]
+
+
+class ApbArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int), ("N", c_int), ("c_s", c_int), ("C", c_int), ("H", c_int),
+        ("accumulate", c_int), ("eps", c_float),
+        ("s", c_void_p), ("k_in", c_void_p), ("z", c_void_p), ("mask", c_void_p), ("out", c_void_p),
+        ("w_q", c_void_p), ("b_q", c_void_p), ("w_k", c_void_p), ("w_v", c_void_p), ("w_g", c_void_p),
+        ("w_o", c_void_p), ("zln_w", c_void_p), ("zln_b", c_void_p), ("w_z", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
+    ]
+
+
+#: name -> (restype, argtypes); every symbol include/pairformer_hip.h declares.
+SIGNATURES = {
+    "pf_abi_version": (c_int, []),
+    "pf_last_error": (ctypes.c_char_p, []),
+    "pf_trimul_workspace_size": (c_size_t, [c_int, c_int, c_int]),
+    "pf_trimul_fwd": (c_int, [ctypes.POINTER(TrimulArgs)]),
+    "pf_trimul_contract": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "pf_triatt_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "pf_triatt_fwd": (c_int, [ctypes.POINTER(TriattArgs)]),
+    "pf_tri_attention_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "pf_tri_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p,
+                                 c_int, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]),
+    "pf_transition_workspace_size": (c_size_t, [c_long, c_int, c_int]),
+    "pf_transition_fwd": (c_int, [ctypes.POINTER(TransitionArgs)]),
+    "pf_apb_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "pf_apb_fwd": (c_int, [ctypes.POINTER(ApbArgs)]),
+    "pf_layernorm_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_float, c_void_p]),
+    "pf_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_int, c_void_p]),
+    "pf_pair_ln_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long,
+                                      c_int, c_float, c_void_p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raise if it is missing or mismatched."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python tt-boltz_amd/build.py` "
+                "(there is no fallback path)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        v = lib.pf_abi_version()
+        if v != ABI_VERSION:
+            raise RuntimeError(f"libpairformer_hip ABI {v} != expected {ABI_VERSION}; rebuild")
+        _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise RuntimeError(pf_last_error()) for a non-zero status."""
+    if rc != 0:
+        msg = load().pf_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")

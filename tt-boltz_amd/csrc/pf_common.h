@@ -1,0 +1,122 @@
+// Shared device helpers for the Pairformer CDNA4 (gfx950) kernels.
+//
+// MFMA conventions used by every kernel in this library (wave64, bf16 in, fp32 acc):
+//
+//   v_mfma_f32_32x32x16_bf16   D[32x32] += A[32x16] * B[16x32]
+//     A operand  lane l: row    m = l & 31, k = 8*(l >> 5) + t   (t = 0..7, one bf16x8)
+//     B operand  lane l: column n = l & 31, k = 8*(l >> 5) + t
+//     C/D        lane l, reg r (0..15): column n = l & 31,
+//                                      row    m = 8*(r >> 2) + 4*(l >> 5) + (r & 3)
+//
+// A GEMM only needs A and B to agree on which (lane half, slot) carries which k, so
+// a "k permutation" applied to both operands leaves the product unchanged.  Kernels
+// use this to feed an accumulator straight back in as the next MFMA's A/B operand:
+// accumulator regs 8*s .. 8*s+7 of a lane in half h hold rows
+//   16*s + 4*h + {0,1,2,3}  and  16*s + 8 + 4*h + {0,1,2,3}
+// so the partner operand is loaded with the same two 4-element runs (see
+// kperm_row()).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define PF_DEV __device__ __forceinline__
+
+PF_DEV f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+PF_DEV f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// Row of the 32x32 accumulator held by register r of a lane in half h.
+PF_DEV int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+// k index carried by slot t (0..7) of a lane in half h for k-step s when the
+// operand comes from accumulator registers 8*s .. 8*s+7 (see header comment).
+PF_DEV int kperm_row(int s, int h, int t) { return 16 * s + 4 * h + (t < 4 ? t : t + 4); }
+
+PF_DEV float sigmoidf_fast(float x) { return 1.f / (1.f + __expf(-x)); }
+
+PF_DEV float siluf(float x) { return x / (1.f + __expf(-x)); }
+
+PF_DEV float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Sum across the two 32-lane halves of a wave64.
+PF_DEV float xor32_sum(float v) { return v + __shfl_xor(v, 32); }
+PF_DEV float xor32_max(float v) { return fmaxf(v, __shfl_xor(v, 32)); }
+
+// Full wave64 reductions.
+PF_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+PF_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+PF_DEV bf16x8 ld_bf16x8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+PF_DEV bf16x4 ld_bf16x4(const bf16* p) { return *reinterpret_cast<const bf16x4*>(p); }
+
+PF_DEV bf16x8 cat44(const bf16x4& a, const bf16x4& b) {
+  bf16x8 r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+
+// Load the x-hat fragment layout: lane (m = l & 31, h = l >> 5) reads channels
+// 16*s + 8*h + t (s = 0..7, t = 0..7) of a 128-channel fp32 vector.
+PF_DEV void load_row128_frag(const float* __restrict__ p, int h, float (&x)[64]) {
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p + 16 * s + 8 * h);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 16 * s + 8 * h + 4);
+    x[8 * s + 0] = a[0]; x[8 * s + 1] = a[1]; x[8 * s + 2] = a[2]; x[8 * s + 3] = a[3];
+    x[8 * s + 4] = b[0]; x[8 * s + 5] = b[1]; x[8 * s + 6] = b[2]; x[8 * s + 7] = b[3];
+  }
+}
+
+// LayerNorm of a 128-vector split over the two halves of a wave (64 values per
+// lane, in load_row128_frag order), written as 8 bf16x8 MFMA fragments.
+// Two-pass (mean, then centred variance) in fp32, like torch's CPU kernel.
+PF_DEV void ln128_to_frag(const float (&x)[64], int h, const float* __restrict__ w,
+                          const float* __restrict__ b, float eps, bf16x8 (&f)[8]) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) s += x[i];
+  const float mean = xor32_sum(s) * (1.f / 128.f);
+  float v = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) { const float d = x[i] - mean; v += d * d; }
+  const float rstd = rsqrtf(xor32_sum(v) * (1.f / 128.f) + eps);
+#pragma unroll
+  for (int s8 = 0; s8 < 8; ++s8) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int c = 16 * s8 + 8 * h + t;
+      f[s8][t] = (bf16)((x[8 * s8 + t] - mean) * rstd * w[c] + b[c]);
+    }
+  }
+}
+
+// Workgroup-id remap so that consecutive logical ids land on one XCD.
+// Hardware dispatches workgroup w to XCD (w % 8); with total % 8 == 0 this maps
+// the ids seen by XCD x to the contiguous range [x*total/8, (x+1)*total/8).
+PF_DEV int xcd_remap(int w, int total) {
+  if (total % 8) return w;
+  return (w % 8) * (total / 8) + (w / 8);
+}

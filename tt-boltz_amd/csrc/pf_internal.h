@@ -1,0 +1,17 @@
+// Host-side helpers shared by the C-ABI entry points (error reporting).
+#pragma once
+#include <hip/hip_runtime.h>
+#include "pairformer_hip.h"
+
+// Record a thread-local error message and return `code`.
+int pf_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// After a launch: turn a launch error into PF_E_LAUNCH naming the kernel.
+#define PF_CHECK_LAUNCH(name)                                                        \
+  do {                                                                               \
+    hipError_t e_ = hipGetLastError();                                               \
+    if (e_ != hipSuccess)                                                            \
+      return pf_fail(e_ == hipErrorOutOfMemory ? PF_E_OOM : PF_E_LAUNCH,             \
+                     "%s launch failed: %s%s", name, hipGetErrorString(e_),          \
+                     e_ == hipErrorOutOfMemory ? " (out of memory)" : "");           \
+  } while (0)

@@ -1,0 +1,324 @@
+// Triangle multiplication (outgoing / incoming) for gfx950.
+//
+// Replaces TriangleMultiplication{Outgoing,Incoming}.forward
+// (tt_bio/reference.py:387-561) and the ttnn TriangleMultiplication
+// (tt_bio/tenstorrent.py:351-503).  Three launches per call:
+//
+//   tm_proj     LN_in(z) -> [p_in | g_in] projection (MFMA) -> a = p*sigmoid(g)*mask,
+//               written as channel-major operand planes opA/opB [B][128][N][N] bf16.
+//               The plane layout already folds the direction: for both directions
+//               the contraction below is  X[c][i][j] = sum_k opA[c][i][k] * opB[c][j][k].
+//                 outgoing: opA[c][i][k] = a[i,k,c],  opB[c][j][k] = b[j,k,c]
+//                 incoming: opA[c][i][k] = a[k,i,c],  opB[c][j][k] = b[k,j,c]
+//   tm_contract 128 (x B) independent N x N x N bf16 GEMMs, fp32 accumulate, 128x128
+//               tiles, LDS double buffer, XCD-aware tile order.
+//   tm_out      LN_out(X) -> p_out, LN_in(z) -> g_out (recomputed, so no gate tensor
+//               goes through HBM), update = p * sigmoid(g), residual into z.
+#include "pf_common.h"
+#include "pf_internal.h"
+
+namespace {
+
+constexpr int C = 128;        // c_z
+constexpr int LDSW = 136;     // padded LDS row stride (bf16) for [rows][128] tiles
+
+// A [32][128] bf16 block moved by 256 threads: 512 chunks of 16 B, 2 per thread.
+struct Blk32 { bf16x8 v[2]; };
+PF_DEV void blk32_load(const bf16* __restrict__ src, int tid, Blk32& r) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int c = tid + 256 * q;
+    r.v[q] = ld_bf16x8(src + (c >> 4) * C + (c & 15) * 8);
+  }
+}
+PF_DEV void blk32_store(bf16* lds, int tid, const Blk32& r) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int c = tid + 256 * q;
+    *reinterpret_cast<bf16x8*>(lds + (c >> 4) * LDSW + (c & 15) * 8) = r.v[q];
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Input projection.  One wave = 32 consecutive positions of one operand-plane row
+// (orow, ocol0 .. ocol0+31); a workgroup = 4 waves; weights streamed through LDS.
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void tm_proj_kernel(
+    const float* __restrict__ z, const float* __restrict__ mask,
+    const float* __restrict__ lnw, const float* __restrict__ lnb,
+    const bf16* __restrict__ w_p, const bf16* __restrict__ w_g,
+    bf16* __restrict__ opA, bf16* __restrict__ opB, int B, int N, int incoming, float eps) {
+  __shared__ __attribute__((aligned(16))) bf16 lds[2][2][32 * LDSW];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
+  const long NN = (long)N * N;
+  const long pos0 = ((long)blockIdx.x * 4 + wid) * 32;
+  const bool active = pos0 < (long)B * NN;
+
+  int b = 0, orow = 0, ocol0 = 0;
+  float maskv = 0.f;
+  bf16x8 xf[8];
+  if (active) {
+    b = (int)(pos0 / NN);
+    const long t0 = pos0 - (long)b * NN;
+    orow = (int)(t0 / N);
+    ocol0 = (int)(t0 - (long)orow * N);
+    const int zi = incoming ? ocol0 + m : orow;
+    const int zj = incoming ? orow : ocol0 + m;
+    const long pair = ((long)b * N + zi) * N + zj;
+    float x[64];
+    load_row128_frag(z + pair * C, h, x);
+    ln128_to_frag(x, h, lnw, lnb, eps, xf);
+    maskv = mask ? mask[pair] : 1.f;
+  }
+
+  Blk32 rp, rg;
+  blk32_load(w_p, tid, rp);
+  blk32_load(w_g, tid, rg);
+  for (int cb = 0; cb < 8; ++cb) {
+    bf16* lp = lds[cb & 1][0];
+    bf16* lg = lds[cb & 1][1];
+    blk32_store(lp, tid, rp);
+    blk32_store(lg, tid, rg);
+    __syncthreads();
+    if (cb + 1 < 8) {
+      blk32_load(w_p + (cb + 1) * 32 * C, tid, rp);
+      blk32_load(w_g + (cb + 1) * 32 * C, tid, rg);
+    }
+    if (active) {
+      f32x16 ap = zero16(), ag = zero16();
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const bf16x8 wp = ld_bf16x8(lp + m * LDSW + 16 * s + 8 * h);
+        const bf16x8 wg = ld_bf16x8(lg + m * LDSW + 16 * s + 8 * h);
+        ap = mfma32(wp, xf[s], ap);   // rows = output channel, cols = position
+        ag = mfma32(wg, xf[s], ag);
+      }
+      bf16* dst = cb < 4 ? opA : opB;
+      const int chb = 32 * (cb & 3);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int ch = chb + acc_row(r, h);
+        const float v = ap[r] * sigmoidf_fast(ag[r]) * maskv;
+        dst[(((long)b * C + ch) * N + orow) * N + ocol0 + m] = (bf16)v;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Batched contraction X[p][i][j] = sum_k A[p][i][k] * B[p][j][k] over planes p.
+// ---------------------------------------------------------------------------------
+constexpr int BM = 128, BN = 128, BK = 64, LDK = BK + 8;
+
+template <typename OutT>
+__global__ __launch_bounds__(256) void tm_contract_kernel(
+    const bf16* __restrict__ A, const bf16* __restrict__ Bop, OutT* __restrict__ X,
+    int N, int tpd, int total) {
+  __shared__ __attribute__((aligned(16))) bf16 sA[2][BM * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 sB[2][BN * LDK];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int w = xcd_remap(blockIdx.x, total);
+  const int tiles = tpd * tpd;
+  const long plane = w / tiles;
+  const int t = w - (int)plane * tiles;
+  const int i0 = (t / tpd) * BM, j0 = (t % tpd) * BN;
+  const long NN = (long)N * N;
+  const bf16* Ap = A + plane * NN;
+  const bf16* Bp = Bop + plane * NN;
+
+  // global -> register staging: rows (tid >> 3) + 32*q, 16-byte chunk (tid & 7)
+  const int lrow = tid >> 3, lcol = (tid & 7) * 8;
+  const bf16* ga[4];
+  const bf16* gb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int ra = min(i0 + lrow + 32 * q, N - 1);
+    const int rb = min(j0 + lrow + 32 * q, N - 1);
+    ga[q] = Ap + (long)ra * N + lcol;
+    gb[q] = Bp + (long)rb * N + lcol;
+  }
+  bf16x8 ra_[4], rb_[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) { ra_[q] = ld_bf16x8(ga[q]); rb_[q] = ld_bf16x8(gb[q]); }
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) acc[a][c] = zero16();
+
+  const int nk = N / BK;
+  for (int kt = 0; kt < nk; ++kt) {
+    bf16* la = sA[kt & 1];
+    bf16* lb = sB[kt & 1];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      *reinterpret_cast<bf16x8*>(la + (lrow + 32 * q) * LDK + lcol) = ra_[q];
+      *reinterpret_cast<bf16x8*>(lb + (lrow + 32 * q) * LDK + lcol) = rb_[q];
+    }
+    __syncthreads();
+    if (kt + 1 < nk) {
+      const int ko = (kt + 1) * BK;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) { ra_[q] = ld_bf16x8(ga[q] + ko); rb_[q] = ld_bf16x8(gb[q] + ko); }
+    }
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      bf16x8 fa[2], fb[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        fa[x] = ld_bf16x8(la + (wm * 64 + 32 * x + m) * LDK + 16 * s + 8 * h);
+        fb[x] = ld_bf16x8(lb + (wn * 64 + 32 * x + m) * LDK + 16 * s + 8 * h);
+      }
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[a][c] = mfma32(fa[a], fb[c], acc[a][c]);
+    }
+  }
+
+  OutT* Xp = X + plane * NN;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int j = j0 + wn * 64 + 32 * c + m;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = i0 + wm * 64 + 32 * a + acc_row(r, h);
+        if (i < N && j < N) Xp[(long)i * N + j] = (OutT)acc[a][c][r];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Output: z[i,j,:] (+)= p_out(LN_out(X[:,i,j])) * sigmoid(g_out(LN_in(z[i,j,:]))).
+// One wave = 32 consecutive pairs (i, j0..j0+31); weights resident in LDS.
+// ---------------------------------------------------------------------------------
+template <typename XT>
+__global__ __launch_bounds__(256) void tm_out_kernel(
+    const XT* __restrict__ X, const float* z_in, float* out,
+    const float* __restrict__ lni_w, const float* __restrict__ lni_b,
+    const float* __restrict__ lno_w, const float* __restrict__ lno_b,
+    const bf16* __restrict__ w_pout, const bf16* __restrict__ w_gout,
+    int B, int N, int accumulate, float eps) {
+  __shared__ __attribute__((aligned(16))) bf16 sW[2][C * LDSW];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int c = tid + 256 * q;   // 2048 chunks of 8 bf16 per matrix
+    const int row = c >> 4, col = (c & 15) * 8;
+    *reinterpret_cast<bf16x8*>(&sW[0][row * LDSW + col]) = ld_bf16x8(w_pout + row * C + col);
+    *reinterpret_cast<bf16x8*>(&sW[1][row * LDSW + col]) = ld_bf16x8(w_gout + row * C + col);
+  }
+  __syncthreads();
+
+  const long NN = (long)N * N;
+  const long pos0 = ((long)blockIdx.x * 4 + wid) * 32;
+  if (pos0 >= (long)B * NN) return;
+  const int b = (int)(pos0 / NN);
+  const long t0 = pos0 - (long)b * NN;
+  const int i = (int)(t0 / N);
+  const int j0 = (int)(t0 - (long)i * N);
+
+  float x[64];
+  bf16x8 xo[8], xi[8];
+  {
+    const XT* Xp = X + (long)b * C * NN + (long)i * N + j0 + m;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) x[8 * s + t] = (float)Xp[(long)(16 * s + 8 * h + t) * NN];
+    ln128_to_frag(x, h, lno_w, lno_b, eps, xo);
+  }
+  const long pbase = (long)b * NN + (long)i * N + j0;   // pair index of position 0
+  load_row128_frag(z_in + (pbase + m) * C, h, x);
+  ln128_to_frag(x, h, lni_w, lni_b, eps, xi);
+
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob) {
+    f32x16 ap = zero16(), ag = zero16();
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const bf16x8 wp = ld_bf16x8(&sW[0][(32 * ob + m) * LDSW + 16 * s + 8 * h]);
+      const bf16x8 wg = ld_bf16x8(&sW[1][(32 * ob + m) * LDSW + 16 * s + 8 * h]);
+      ap = mfma32(xo[s], wp, ap);   // rows = pair, cols = output channel
+      ag = mfma32(xi[s], wg, ag);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const long idx = (pbase + acc_row(r, h)) * C + 32 * ob + m;
+      const float u = ap[r] * sigmoidf_fast(ag[r]);
+      out[idx] = accumulate ? out[idx] + u : u;
+    }
+  }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------------
+extern "C" size_t pf_trimul_workspace_size(int B, int N, int C_) {
+  if (B <= 0 || N <= 0 || C_ != C) return 0;
+  const size_t planes = (size_t)B * C * N * N;
+  return planes * (2 * sizeof(bf16) + sizeof(float));
+}
+
+extern "C" int pf_trimul_fwd(const pf_trimul_args* a) {
+  if (!a) return pf_fail(PF_E_INVALID, "pf_trimul_fwd: null args");
+  if (a->C != C) return pf_fail(PF_E_INVALID, "pf_trimul_fwd: only c_z = 128 is supported (got %d)", a->C);
+  if (a->hidden != C) return pf_fail(PF_E_INVALID, "pf_trimul_fwd: hidden must equal c_z = 128 (got %d)", a->hidden);
+  if (a->B <= 0 || a->N <= 0 || a->N % 64)
+    return pf_fail(PF_E_INVALID, "pf_trimul_fwd: need B > 0 and N a positive multiple of 64 (B=%d N=%d)", a->B, a->N);
+  if (a->direction != 0 && a->direction != 1)
+    return pf_fail(PF_E_INVALID, "pf_trimul_fwd: direction must be 0 (outgoing) or 1 (incoming)");
+  if (!a->z_in || !a->out || !a->norm_in_w || !a->norm_in_b || !a->p_in_w || !a->g_in_w ||
+      !a->norm_out_w || !a->norm_out_b || !a->p_out_w || !a->g_out_w || !a->workspace)
+    return pf_fail(PF_E_INVALID, "pf_trimul_fwd: null pointer argument");
+  const size_t need = pf_trimul_workspace_size(a->B, a->N, a->C);
+  if (a->workspace_bytes < need)
+    return pf_fail(PF_E_INVALID, "pf_trimul_fwd: workspace too small (%zu < %zu bytes)", a->workspace_bytes, need);
+
+  hipStream_t st = (hipStream_t)a->stream;
+  const int B = a->B, N = a->N;
+  const size_t planes = (size_t)B * C * N * N;
+  bf16* opA = (bf16*)a->workspace;
+  bf16* opB = opA + planes;
+  float* X = (float*)(opB + planes);
+  const bf16* w_pin = (const bf16*)a->p_in_w;
+  const bf16* w_gin = (const bf16*)a->g_in_w;
+
+  const long positions = (long)B * N * N;
+  const int grid_proj = (int)((positions / 32 + 3) / 4);
+  tm_proj_kernel<<<grid_proj, 256, 0, st>>>(a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b,
+                                            w_pin, w_gin, opA, opB, B, N, a->direction, a->eps);
+  PF_CHECK_LAUNCH("tm_proj_kernel");
+
+  const int tpd = (N + BM - 1) / BM;
+  const int total = B * C * tpd * tpd;
+  tm_contract_kernel<float><<<total, 256, 0, st>>>(opA, opB, X, N, tpd, total);
+  PF_CHECK_LAUNCH("tm_contract_kernel");
+
+  tm_out_kernel<float><<<grid_proj, 256, 0, st>>>(X, a->z_in, a->out, a->norm_in_w, a->norm_in_b,
+                                                  a->norm_out_w, a->norm_out_b,
+                                                  (const bf16*)a->p_out_w, (const bf16*)a->g_out_w,
+                                                  B, N, a->accumulate, a->eps);
+  PF_CHECK_LAUNCH("tm_out_kernel");
+  return PF_OK;
+}
+
+// Standalone contraction (the MFMA hot loop alone), for measurement and tests.
+extern "C" int pf_trimul_contract(const void* opA, const void* opB, float* X, int planes, int N,
+                                  void* stream) {
+  if (!opA || !opB || !X) return pf_fail(PF_E_INVALID, "pf_trimul_contract: null pointer");
+  if (planes <= 0 || N <= 0 || N % 64)
+    return pf_fail(PF_E_INVALID, "pf_trimul_contract: need planes > 0 and N a multiple of 64");
+  const int tpd = (N + BM - 1) / BM;
+  const int total = planes * tpd * tpd;
+  tm_contract_kernel<float><<<total, 256, 0, (hipStream_t)stream>>>(
+      (const bf16*)opA, (const bf16*)opB, X, N, tpd, total);
+  PF_CHECK_LAUNCH("tm_contract_kernel");
+  return PF_OK;
+}

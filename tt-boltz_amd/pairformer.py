@@ -1,0 +1,403 @@
+"""Drop-in Pairformer modules for MI355X (PyTorch-ROCm host, HIP kernels).
+
+Mirrors the call surface of the Tenstorrent path in ``tt_bio/tenstorrent.py``:
+
+* ``PairformerModule`` (``tenstorrent.py:2194-2284``, an ``nn.Module`` built by
+  ``TorchWrapper``, ``2113-2191``): same constructor, ``load_state_dict`` (weights
+  are taken from the state dict at load time, no parameters are registered),
+  ``forward(s, z, mask=None, pair_mask=None, use_kernels=False) -> (s, z)`` and
+  ``reset_static_cache()``; pads N to a multiple of 64 and slices back; masks are
+  built on the first forward after a reset and reused.
+* ``Pairformer`` / ``PairformerLayer`` / ``TriangleMultiplication`` /
+  ``TriangleAttention`` / ``Transition`` / ``AttentionPairBias`` with the
+  reference names and weight keys (``tenstorrent.py:351-1083``), operating on
+  device-resident padded tensors.
+* ``WeightScope``, ``get_device``, ``set_fast_mode``.
+
+Numerics follow the reference CPU modules (``tt_bio/reference.py``), not the
+Tenstorrent approximations: the pair mask multiplies both trimul operands
+(``reference.py:461``), triangle attention masks per (row, key) with 1e9
+(``reference.py:334-335``), single attention masks keys with 1e6
+(``boltz2.py:362``), and the pair bias is added unscaled after q/sqrt(d)
+(``reference.py:117-118``).  The residual stream z is kept in fp32.
+"""
+from __future__ import annotations
+
+from types import MappingProxyType
+from typing import Mapping, Optional
+
+import torch
+from torch import nn
+
+from . import ops
+
+_FAST_MODE = False
+_device: Optional[torch.device] = None
+
+C_Z = 128
+
+
+def set_fast_mode(enabled: bool) -> None:
+    """``tenstorrent.py:178-181``: process-global block-fp8 switch, read at module construction."""
+    global _FAST_MODE
+    _FAST_MODE = bool(enabled)
+
+
+def get_device() -> torch.device:
+    """The process's GPU (one device per process, like ``tenstorrent.py:213-243``)."""
+    global _device
+    if _device is None:
+        if not torch.cuda.is_available():
+            raise RuntimeError("no ROCm GPU visible: the Pairformer HIP kernels have no CPU path")
+        _device = torch.device("cuda", torch.cuda.current_device())
+    return _device
+
+
+class WeightScope:
+    """Immutable scoped view over a flat state dict (``tenstorrent.py:261-293``)."""
+
+    def __init__(self, data: Mapping[str, torch.Tensor]):
+        self._data = MappingProxyType(dict(data))
+
+    @classmethod
+    def wrap(cls, data) -> "WeightScope":
+        return data if isinstance(data, cls) else cls(data)
+
+    @property
+    def data(self) -> Mapping[str, torch.Tensor]:
+        return self._data
+
+    def as_dict(self) -> dict:
+        return dict(self._data)
+
+    def __getitem__(self, key: str) -> torch.Tensor:
+        return self._data[key]
+
+    def __contains__(self, key: str) -> bool:
+        return key in self._data
+
+    def child(self, scope: str, strip_prefix: str = "") -> "WeightScope":
+        if not scope:
+            return self
+        sp = scope + "."
+        out = {}
+        for key, value in self._data.items():
+            if not key.startswith(sp):
+                continue
+            ck = key[len(sp):]
+            if strip_prefix and ck.startswith(strip_prefix):
+                ck = ck[len(strip_prefix):]
+            out[ck] = value
+        return WeightScope(out)
+
+
+class Options:
+    """Replaces ttnn's ``compute_kernel_config``: numerics knobs shared by the kernels."""
+
+    def __init__(self, eps: float = 1e-5):
+        self.eps = eps
+
+
+class Module:
+    """Base: holds a weight scope and converts weights to device tensors once."""
+
+    def __init__(self, state_dict, options: Optional[Options] = None):
+        if _FAST_MODE:
+            raise NotImplementedError("block-fp8 fast mode is not implemented in this build")
+        self.weights = WeightScope.wrap(state_dict)
+        self.options = options or Options()
+        self.device = get_device()
+
+    def scope(self, scope: str, strip_prefix: str = "") -> WeightScope:
+        return self.weights.child(scope, strip_prefix)
+
+    def mat(self, key: str) -> torch.Tensor:
+        return ops.bf16(self.weights[key], self.device)
+
+    def vec(self, key: str) -> torch.Tensor:
+        return ops.f32(self.weights[key], self.device)
+
+
+class TriangleMultiplication(Module):
+    """``tenstorrent.py:351-503``; ``ending=True`` is the incoming direction."""
+
+    def __init__(self, ending: bool, state_dict, options: Optional[Options] = None):
+        super().__init__(state_dict, options)
+        self.ending = ending
+        if self.weights["p_in.weight"].shape != (2 * C_Z, C_Z):
+            raise NotImplementedError(f"only c_z = {C_Z} is supported (p_in {tuple(self.weights['p_in.weight'].shape)})")
+        self.w = {k: self.vec(k) for k in ("norm_in.weight", "norm_in.bias", "norm_out.weight", "norm_out.bias")}
+        self.w.update({k: self.mat(k) for k in ("p_in.weight", "g_in.weight", "p_out.weight", "g_out.weight")})
+
+    def __call__(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                 accumulate: bool = False, ws: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """x [B,N,N,128] fp32 device, N % 64 == 0.  Returns the update (or ``out`` += update)."""
+        B, N = x.shape[0], x.shape[1]
+        if ws is None:
+            ws = ops.workspace(ops.trimul_workspace_bytes(B, N), x.device)
+        if out is None:
+            out = torch.empty_like(x)
+        ops.launch_trimul(x, out, mask, self.w, int(self.ending), ws, accumulate, self.options.eps)
+        return out
+
+
+class TriangleAttention(Module):
+    """``tenstorrent.py:506-650``; weight scope with the ``mha.`` prefix stripped."""
+
+    def __init__(self, head_dim: int, n_heads: int, ending: bool, state_dict, options: Optional[Options] = None,
+                 affinity: bool = False):
+        super().__init__(state_dict, options)
+        if (head_dim, n_heads) != (32, 4):
+            raise NotImplementedError(f"only 4 heads x 32 are supported (got {n_heads} x {head_dim})")
+        self.head_dim, self.n_heads, self.ending, self.affinity = head_dim, n_heads, ending, affinity
+        self.w = {k: self.vec(k) for k in ("layer_norm.weight", "layer_norm.bias")}
+        self.w.update({k: self.mat(k) for k in ("linear.weight", "linear_q.weight", "linear_k.weight",
+                                                "linear_v.weight", "linear_g.weight", "linear_o.weight")})
+
+    def __call__(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                 accumulate: bool = False, ws: Optional[torch.Tensor] = None) -> torch.Tensor:
+        B, N = x.shape[0], x.shape[1]
+        if ws is None:
+            ws = ops.workspace(ops.triatt_workspace_bytes(B, N), x.device)
+        if out is None:
+            out = torch.empty_like(x)
+        ops.launch_triatt(x, out, mask, self.w, self.ending, ws, accumulate, self.n_heads, self.head_dim,
+                          self.options.eps)
+        return out
+
+
+class Transition(Module):
+    """``tenstorrent.py:856-946`` / ``boltz2.py:1188-1258``."""
+
+    def __init__(self, state_dict, options: Optional[Options] = None):
+        super().__init__(state_dict, options)
+        self.w = {k: self.vec(k) for k in ("norm.weight", "norm.bias")}
+        self.w.update({k: self.mat(k) for k in ("fc1.weight", "fc2.weight", "fc3.weight")})
+        self.C = self.weights["fc1.weight"].shape[1]
+        self.hidden = self.weights["fc1.weight"].shape[0]
+
+    def workspace_bytes(self, rows: int) -> int:
+        return ops.transition_workspace_bytes(rows, self.C, self.hidden)
+
+    def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, accumulate: bool = False,
+                 ws: Optional[torch.Tensor] = None) -> torch.Tensor:
+        rows = x.numel() // self.C
+        if ws is None:
+            nb = self.workspace_bytes(rows)
+            ws = ops.workspace(nb, x.device) if nb else None
+        if out is None:
+            out = torch.empty_like(x)
+        ops.launch_transition(x, out, self.w, ws, accumulate, self.options.eps)
+        return out
+
+
+class AttentionPairBias(Module):
+    """``tenstorrent.py:653-853`` (non-atom branch, compute_pair_bias=True)."""
+
+    def __init__(self, head_dim: int, n_heads: int, state_dict, options: Optional[Options] = None):
+        super().__init__(state_dict, options)
+        self.head_dim, self.n_heads = head_dim, n_heads
+        self.w = {k: self.vec(k) for k in ("proj_q.bias", "proj_z.0.weight", "proj_z.0.bias")}
+        self.w.update({k: self.mat(k) for k in ("proj_q.weight", "proj_k.weight", "proj_v.weight", "proj_g.weight",
+                                                "proj_o.weight", "proj_z.1.weight")})
+        self.c_s = self.weights["proj_q.weight"].shape[0]
+
+    def workspace_bytes(self, B: int, N: int) -> int:
+        return ops.apb_workspace_bytes(B, N, self.c_s, self.n_heads)
+
+    def __call__(self, s: torch.Tensor, z: torch.Tensor, mask: Optional[torch.Tensor] = None,
+                 k_in: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None, accumulate: bool = False,
+                 ws: Optional[torch.Tensor] = None) -> torch.Tensor:
+        B, N, _ = s.shape
+        if ws is None:
+            ws = ops.workspace(self.workspace_bytes(B, N), s.device)
+        if out is None:
+            out = torch.empty_like(s)
+        ops.launch_apb(s, s if k_in is None else k_in, z, mask, out, self.w, self.n_heads, ws, accumulate,
+                       self.options.eps)
+        return out
+
+
+class PairformerLayer(Module):
+    """``tenstorrent.py:949-1046`` / ``reference.py:822-914`` (no-seq: ``1007-1072``).
+
+    ``__call__(s, z, pair_mask, mask, ws)`` updates the device tensors in place:
+    z += TMo; z += TMi; z += TAs; z += TAe; z += Tr_z; then, with ``transform_s``,
+    s += APB(LN(s), z, mask, k_in=LN(s)); s += Tr_s(s).
+    """
+
+    def __init__(self, tri_att_head_dim: int, tri_att_n_heads: int, att_head_dim: Optional[int],
+                 att_n_heads: Optional[int], transform_s: bool, state_dict, options: Optional[Options] = None,
+                 affinity: bool = False):
+        super().__init__(state_dict, options)
+        self.transform_s = transform_s
+        self.triangle_multiplication_start = TriangleMultiplication(False, self.scope("tri_mul_out"), options)
+        self.triangle_multiplication_end = TriangleMultiplication(True, self.scope("tri_mul_in"), options)
+        self.triangle_attention_start = TriangleAttention(tri_att_head_dim, tri_att_n_heads, False,
+                                                          self.scope("tri_att_start", "mha."), options, affinity)
+        self.triangle_attention_end = TriangleAttention(tri_att_head_dim, tri_att_n_heads, True,
+                                                        self.scope("tri_att_end", "mha."), options, affinity)
+        self.transition_z = Transition(self.scope("transition_z"), options)
+        if transform_s:
+            self.pre_norm_s_weight = self.vec("pre_norm_s.weight")
+            self.pre_norm_s_bias = self.vec("pre_norm_s.bias")
+            self.attention_pair_bias = AttentionPairBias(att_head_dim, att_n_heads, self.scope("attention"), options)
+            self.transition_s = Transition(self.scope("transition_s"), options)
+
+    def workspace_bytes(self, B: int, N: int) -> int:
+        n = max(ops.trimul_workspace_bytes(B, N), ops.triatt_workspace_bytes(B, N))
+        if self.transform_s:
+            c_s = self.attention_pair_bias.c_s
+            n = max(n, self.attention_pair_bias.workspace_bytes(B, N) + B * N * c_s * 4,
+                    self.transition_s.workspace_bytes(B * N))
+        return n
+
+    def __call__(self, s: Optional[torch.Tensor], z: torch.Tensor, pair_mask: Optional[torch.Tensor] = None,
+                 mask: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None):
+        B, N = z.shape[0], z.shape[1]
+        if ws is None:
+            ws = ops.workspace(self.workspace_bytes(B, N), z.device)
+        self.triangle_multiplication_start(z, pair_mask, out=z, accumulate=True, ws=ws)
+        self.triangle_multiplication_end(z, pair_mask, out=z, accumulate=True, ws=ws)
+        self.triangle_attention_start(z, pair_mask, out=z, accumulate=True, ws=ws)
+        self.triangle_attention_end(z, pair_mask, out=z, accumulate=True, ws=ws)
+        self.transition_z(z, out=z, accumulate=True, ws=ws)
+        if self.transform_s and s is not None:
+            c_s = s.shape[-1]
+            s_norm = ws[: B * N * c_s * 4].view(torch.float32).view(B, N, c_s)
+            ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps)
+            apb_ws = ws[B * N * c_s * 4:]
+            self.attention_pair_bias(s_norm, z, mask, k_in=s_norm, out=s, accumulate=True, ws=apb_ws)
+            self.transition_s(s, out=s, accumulate=True, ws=ws)
+        return s, z
+
+
+class Pairformer(Module):
+    """``tenstorrent.py:1049-1083``: the block stack on device-resident padded tensors."""
+
+    def __init__(self, n_blocks: int, tri_att_head_dim: int, tri_att_n_heads: int, att_head_dim: Optional[int],
+                 att_n_heads: Optional[int], transform_s: bool, state_dict, options: Optional[Options] = None,
+                 affinity: bool = False):
+        super().__init__(state_dict, options)
+        self.transform_s = transform_s
+        self.blocks = [
+            PairformerLayer(tri_att_head_dim, tri_att_n_heads, att_head_dim, att_n_heads, transform_s,
+                            self.scope(f"layers.{i}"), options, affinity=affinity)
+            for i in range(n_blocks)
+        ]
+
+    def workspace_bytes(self, B: int, N: int) -> int:
+        return max((b.workspace_bytes(B, N) for b in self.blocks), default=16)
+
+    def __call__(self, s: Optional[torch.Tensor], z: torch.Tensor, pair_mask: Optional[torch.Tensor] = None,
+                 mask: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None):
+        if ws is None:
+            ws = ops.workspace(self.workspace_bytes(z.shape[0], z.shape[1]), z.device)
+        for block in self.blocks:
+            s, z = block(s, z, pair_mask, mask, ws)
+        return s, z
+
+
+class PairformerModule(nn.Module):
+    """Drop-in for ``tenstorrent.PairformerModule`` (``tenstorrent.py:2194-2284``) and
+    ``reference.PairformerModule`` / ``PairformerNoSeqModule`` at the
+    ``Boltz2`` call sites (``boltz2.py:3750, 4502, 4688, 5015``)."""
+
+    def __init__(self, n_blocks: int, tri_att_head_dim: int, tri_att_n_heads: int, att_head_dim: Optional[int],
+                 att_n_heads: Optional[int], transform_s: bool, affinity: bool = False):
+        super().__init__()
+        self.n_blocks = n_blocks
+        self.tri_att_head_dim = tri_att_head_dim
+        self.tri_att_n_heads = tri_att_n_heads
+        self.att_head_dim = att_head_dim
+        self.att_n_heads = att_n_heads
+        self.transform_s = transform_s
+        self.affinity = affinity
+        self.module: Optional[Pairformer] = None
+        self.options = Options()
+        self._runtime_cache: dict = {}
+        self._first_forward_pass = True
+
+    def _load_from_state_dict(self, state_dict, prefix, _local_metadata, _strict, _missing_keys,
+                              _unexpected_keys, _error_msgs):
+        self.module = Pairformer(self.n_blocks, self.tri_att_head_dim, self.tri_att_n_heads, self.att_head_dim,
+                                 self.att_n_heads, self.transform_s,
+                                 WeightScope.wrap(state_dict).child(prefix[:-1]), self.options,
+                                 affinity=self.affinity)
+
+    def reset_static_cache(self):
+        """Drop cached masks so they are rebuilt on the next forward (``tenstorrent.py:2182-2191``)."""
+        self._runtime_cache.clear()
+        self._first_forward_pass = True
+
+    def _build_masks(self, B: int, N: int, n_pad: int, mask, pair_mask, dev) -> None:
+        if pair_mask is None and mask is not None:
+            m = mask.to(dev, torch.float32)
+            pair_mask = m[:, :, None] * m[:, None, :]
+        self._runtime_cache["pair_mask"] = ops.pad_pair_mask(pair_mask, B, N, n_pad, dev)
+        if self.transform_s:
+            tm = torch.zeros((B, n_pad), dtype=torch.float32, device=dev)
+            tm[:, :N] = 1.0 if mask is None else mask.to(dev, torch.float32)
+            self._runtime_cache["mask"] = tm
+        self._runtime_cache["shape"] = (B, n_pad)
+
+    def forward(self, s: Optional[torch.Tensor], z: torch.Tensor, mask: Optional[torch.Tensor] = None,
+                pair_mask: Optional[torch.Tensor] = None, use_kernels: bool = False):
+        """``(s [B,N,c_s] | None, z [B,N,N,c_z]) -> (s_out | None, z_out)``, fp32, on z's device.
+        ``use_kernels`` is accepted for call-site compatibility and ignored."""
+        if self.module is None:
+            raise RuntimeError("PairformerModule has no weights: call load_state_dict() first")
+        dev = get_device()
+        B, N = z.shape[0], z.shape[1]
+        n_pad = ops.padded_len(N)
+        if self._first_forward_pass or self._runtime_cache.get("shape") != (B, n_pad):
+            self._build_masks(B, N, n_pad, mask, pair_mask, dev)
+            self._first_forward_pass = False
+        z_dev = ops.pad_pair(z.to(dev, torch.float32), n_pad)
+        s_dev = None
+        if self.transform_s and s is not None:
+            s_dev = torch.zeros((B, n_pad, s.shape[-1]), dtype=torch.float32, device=dev)
+            s_dev[:, :N] = s.to(dev, torch.float32)
+        s_dev, z_dev = self.module(s_dev, z_dev, self._runtime_cache["pair_mask"], self._runtime_cache.get("mask"))
+        z_out = z_dev[:, :N, :N].to(z.device)
+        s_out = None if s_dev is None else s_dev[:, :N].to(s.device)
+        if s is not None and not self.transform_s:
+            s_out = s
+        return s_out, z_out
+
+
+class TrunkRecycler:
+    """Device-resident trunk recycling loop of ``Boltz2.forward`` (``boltz2.py:5189-5248``)
+    with the template and MSA modules absent: s, z start at zero and each of the
+    ``recycling_steps + 1`` passes computes ``s = s_init + s_recycle(s_norm(s))``,
+    ``z = z_init + z_recycle(z_norm(z))`` (``boltz2.py:5213-5214``) and runs the
+    Pairformer stack, without leaving the GPU between passes."""
+
+    def __init__(self, pairformer: Pairformer, state_dict, options: Optional[Options] = None):
+        w = WeightScope.wrap(state_dict)
+        self.pairformer = pairformer
+        self.options = options or Options()
+        dev = get_device()
+        self.s_norm_w, self.s_norm_b = ops.f32(w["s_norm.weight"], dev), ops.f32(w["s_norm.bias"], dev)
+        self.z_norm_w, self.z_norm_b = ops.f32(w["z_norm.weight"], dev), ops.f32(w["z_norm.bias"], dev)
+        self.s_rec = ops.bf16(w["s_recycle.weight"], dev)
+        self.z_rec = ops.bf16(w["z_recycle.weight"], dev)
+
+    def __call__(self, s_init: torch.Tensor, z_init: torch.Tensor, mask: Optional[torch.Tensor],
+                 recycling_steps: int, pass_hook=None):
+        """Padded device tensors in (N % 64 == 0); returns device (s, z)."""
+        B, N = z_init.shape[0], z_init.shape[1]
+        dev = z_init.device
+        pair_mask = None if mask is None else (mask[:, :, None] * mask[:, None, :]).contiguous()
+        s = torch.zeros_like(s_init)
+        z = torch.zeros_like(z_init)
+        s_tmp = torch.empty_like(s_init)
+        ws = ops.workspace(self.pairformer.workspace_bytes(B, N), dev)
+        for i in range(recycling_steps + 1):
+            ops.launch_layernorm(s, self.s_norm_w, self.s_norm_b, s_tmp, self.options.eps)
+            ops.launch_linear(s_tmp, self.s_rec, None, s_init, s)
+            ops.launch_pair_ln_linear(z, z_init, self.z_norm_w, self.z_norm_b, self.z_rec, z, self.options.eps)
+            s, z = self.pairformer(s, z, pair_mask, mask, ws)
+            if pass_hook is not None:
+                pass_hook(i)
+        return s, z
