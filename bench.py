@@ -1,0 +1,209 @@
+"""Benchmark: Pairformer layers/s at N=512 on one MI355X (BASELINE.json metric).
+
+A step is one full Boltz-2 PairformerLayer (triangle multiplication out+in,
+triangle attention start+end, pair transition, single attention with pair bias,
+single transition) applied in place to device-resident z [1,512,512,128] fp32 and
+s [1,512,384] fp32, masks all ones, random-init weights from seed 0 (the
+config-0 layer architecture), bf16 MFMA operands with fp32 accumulation.
+
+Besides the JSON line's ``value`` (layers/s), it reports per-op times and
+TFLOP/s, the roofline of the dominant kernel (timed alone with HIP events on the
+stream it is launched on) and the CPU oracle timed on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--n 512] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 (AMD published)
+HBM_PEAK_GBS = 8000.0
+
+
+def flops_layer(N: int, c: int = 128, hd: int = 128, H: int = 4, c_s: int = 384) -> dict:
+    """Algorithmic FLOP per op for one layer (matmul-like terms only)."""
+    tm_contract = 2 * N ** 3 * c
+    tm_proj = 12 * N ** 2 * c * c
+    ta_core = 4 * N ** 3 * hd
+    ta_proj = 2 * N ** 2 * c * (4 * hd + H) + 2 * N ** 2 * hd * c
+    tr = 24 * N ** 2 * c * c
+    s_track = (2 * N ** 2 * c * 16 + 2 * N * c_s * c_s * 5 + 4 * N ** 2 * c_s + 2 * N * c_s * 4 * c_s * 3)
+    return {"trimul": tm_contract + tm_proj, "trimul_contract": tm_contract, "triatt": ta_core + ta_proj,
+            "triatt_core": ta_core, "transition_z": tr, "s_track": s_track,
+            "layer": 2 * (tm_contract + tm_proj) + 2 * (ta_core + ta_proj) + tr + s_track}
+
+
+def cpu_baseline(N: int, seed: int, reps: int = 3) -> dict:
+    """Time the fp32 CPU oracle for one layer at this N on the host cores (median of reps)."""
+    import torch
+    from oracle import pairformer_ref as ref
+    from tt_boltz_amd import synthetic
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    w = synthetic.stack_weights(1, seed)
+    s, z, mask, pm = synthetic.pair_inputs(N, seed)
+    lw = ref.sub(w, "layers.0")
+    chunk = ref.chunk_size_for(N)
+    with torch.no_grad():
+        ref.pairformer_layer(s, z, mask, pm, lw, chunk)          # warm-up
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            ref.pairformer_layer(s, z, mask, pm, lw, chunk)
+            ts.append(time.perf_counter() - t0)
+    ts.sort()
+    sec = ts[len(ts) // 2]
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": 1.0 / sec, "unit": "layers/s", "cores": cores, "kind": "port",
+            "sample": f"1 PairformerLayer at N={N}, fp32 CPU oracle (oracle/pairformer_ref.py), torch "
+                      f"{torch.__version__}, {cores} threads, median of {reps} after 1 warm-up; "
+                      f"{sec:.2f} s/layer; cpu={cpu}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--n", type=int, default=512)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}): this build measures the "
+              "single-GPU Pairformer path; multi-GPU sharding is a design note only.", file=sys.stderr)
+        return 0
+
+    import torch
+    from tt_boltz_amd import ops, pairformer, synthetic
+
+    N, seed = args.n, 0
+    dev = pairformer.get_device()
+    w = synthetic.stack_weights(1, seed)
+    s_cpu, z_cpu, _, _ = synthetic.pair_inputs(N, seed)
+    pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, w)
+    layer = pf.blocks[0]
+    ws = ops.workspace(pf.workspace_bytes(1, N), dev)
+    z = z_cpu.to(dev).contiguous()
+    s = s_cpu.to(dev).contiguous()
+    stream = torch.cuda.current_stream()
+
+    def step():
+        layer(s, z, None, None, ws)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall0
+    ms_step = e0.elapsed_time(e1) / args.steps
+    if not torch.isfinite(z).all():
+        print("non-finite z after timed steps", file=sys.stderr)
+        return 1
+
+    # per-op breakdown (each op timed alone, same stream, in-place like the layer)
+    fl = flops_layer(N)
+
+    def time_op(fn, reps=10):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    ops_ms = {
+        "trimul_out": time_op(lambda: layer.triangle_multiplication_start(z, None, out=z, accumulate=True, ws=ws)),
+        "trimul_in": time_op(lambda: layer.triangle_multiplication_end(z, None, out=z, accumulate=True, ws=ws)),
+        "triatt_start": time_op(lambda: layer.triangle_attention_start(z, None, out=z, accumulate=True, ws=ws)),
+        "triatt_end": time_op(lambda: layer.triangle_attention_end(z, None, out=z, accumulate=True, ws=ws)),
+        "transition_z": time_op(lambda: layer.transition_z(z, out=z, accumulate=True, ws=ws)),
+    }
+    breakdown = {k: {"ms": round(v, 4)} for k, v in ops_ms.items()}
+    for k, key in (("trimul_out", "trimul"), ("trimul_in", "trimul"), ("triatt_start", "triatt"),
+                   ("triatt_end", "triatt"), ("transition_z", "transition_z")):
+        breakdown[k]["tflops"] = round(fl[key] / (ops_ms[k] * 1e-3) / 1e12, 1)
+
+    # dominant-kernel roofline: the trimul contraction, launched alone on its real operands
+    # (the workspace planes the last trimul call left behind), timed with HIP events on
+    # the stream it runs on.
+    nplanes = 128
+    plane_elems = nplanes * N * N
+    dt = ops.TORCH_DTYPE[layer.variant]
+    opA = ws[: plane_elems * 2].view(dt).view(nplanes, N, N)
+    opB = ws[plane_elems * 2: plane_elems * 4].view(dt).view(nplanes, N, N)
+    X = ws[plane_elems * 4: plane_elems * 6].view(dt).view(nplanes, N, N)
+    layer.triangle_multiplication_start(z, None, out=torch.empty_like(z), accumulate=False, ws=ws)
+    reps = 20
+    contract_ms = time_op(lambda: ops.launch_trimul_contract(opA, opB, X, layer.variant), reps)
+    contract_flop = fl["trimul_contract"] / 2   # one direction per launch
+    achieved = contract_flop / (contract_ms * 1e-3) / 1e12
+    roofline = {"kernel": "tm_contract_kernel", "bound": "mfma", "achieved": round(achieved, 1),
+                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                "launch_ms": round(contract_ms, 4), "flop_per_launch": contract_flop}
+
+    # the same layer with bf16 MFMA operands (libpairformer_hip_bf16.so, same kernels)
+    pf_bf16 = pairformer.Pairformer(1, 32, 4, 24, 16, True, w, pairformer.Options(operand="bf16"))
+    zb, sb = z_cpu.to(dev).contiguous(), s_cpu.to(dev).contiguous()
+    bf16_ms = time_op(lambda: pf_bf16.blocks[0](sb, zb, None, None, ws), args.steps)
+
+    out = {
+        "metric": "Pairformer layers/sec at N=512 bf16",
+        "value": round(1000.0 / ms_step, 3),
+        "unit": "layers/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "operand_variants": {"fp16_layers_per_s": round(1000.0 / ms_step, 3),
+                             "bf16_layers_per_s": round(1000.0 / bf16_ms, 3),
+                             "note": "MFMA operand type (fp32 accumulate, fp32 residual stream); fp16 is the "
+                                     "default because bf16 operands miss the 2e-3 mean-error bar"},
+        "data": "synthetic (seeded N(0,1) inputs, random-init weights, seed 0)",
+        "config": {"workload": f"one Boltz-2 PairformerLayer, N={N}, c_z=128, c_s=384, tri-att 4x32, "
+                               f"single-att 16x24, masks all ones, device-resident fp32 z/s",
+                   "N": N, "batch": 1, "layer_tflop": round(fl["layer"] / 1e12, 4),
+                   "layer_tflops_achieved": round(fl["layer"] / (ms_step * 1e-3) / 1e12, 1)},
+        "roofline": roofline,
+        "breakdown": breakdown,
+        "wall_s_timed": round(wall, 3),
+        "device": torch.cuda.get_device_name(0),
+        "host": platform.node(),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(N, seed)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

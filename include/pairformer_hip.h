@@ -5,9 +5,12 @@
  * Conventions (all entry points):
  *   - Pointers are device pointers (HIP global memory) unless stated otherwise.
  *   - Dense row-major layouts.  Pair tensors are [B][N][N][C] fp32; masks are fp32 0/1.
- *   - Weights are bf16 (raw uint16 bit patterns) in nn.Linear layout [out][in];
- *     LayerNorm weights/biases are fp32.  Weight names in the comments are the
- *     reference state-dict keys (tt_bio/reference.py, tt_bio/boltz2.py).
+ *   - Matrix weights are in the library's MFMA operand type (raw 16-bit patterns):
+ *     IEEE fp16 in libpairformer_hip.so, bf16 in libpairformer_hip_bf16.so
+ *     (pf_operand_dtype() says which), nn.Linear layout [out][in].  LayerNorm
+ *     weights/biases and linear biases are fp32.  Accumulation is fp32 everywhere.
+ *     Weight names in the comments are the reference state-dict keys
+ *     (tt_bio/reference.py, tt_bio/boltz2.py); "bf16"/"op" below means the operand type.
  *   - `stream` is a hipStream_t (NULL = default stream).  Calls only enqueue work;
  *     they do not synchronize and do not allocate device memory.  Scratch memory is
  *     passed in as `workspace` (size from the matching *_workspace_size()).
@@ -17,6 +20,10 @@
  *     like the reference does (tt_bio/tenstorrent.py:41, 2235-2246).
  *   - `accumulate`: 0 -> out = update, 1 -> out += update.  out may alias the input
  *     pair tensor (in-place residual, `z = z + op(z)` in tt_bio/reference.py:877-903).
+ *   - `n_valid` (attention entry points): tokens >= n_valid are boundary padding and
+ *     are excluded from every softmax (weight exactly 0), so a row whose valid keys are
+ *     all masked still averages over the n_valid real keys as the unpadded reference
+ *     does.  0 means N (no padding).
  */
 #ifndef PAIRFORMER_HIP_H
 #define PAIRFORMER_HIP_H
@@ -41,6 +48,9 @@ int pf_abi_version(void);
 
 /* Message for the last failing call on this thread ("" if none). */
 const char* pf_last_error(void);
+
+/* MFMA operand type of this build: 0 = IEEE fp16, 1 = bf16. */
+int pf_operand_dtype(void);
 
 /* ------------------------------------------------------------------------------
  * Triangle multiplication, outgoing (direction 0) and incoming (direction 1).
@@ -77,10 +87,11 @@ size_t pf_trimul_workspace_size(int B, int N, int C);
 int pf_trimul_fwd(const pf_trimul_args* args);
 
 /* The contraction alone: X[p][i][j] = sum_k A[p][i][k] * Bm[p][j][k] for `planes`
- * independent N x N bf16 planes, fp32 output.  The batched matmul inside
- * TriangleMultiplication (tt_bio/tenstorrent.py:453-460; einsum at
+ * independent N x N operand-type planes.  x_fp32 = 1: X is fp32; x_fp32 = 0: X is the
+ * operand type scaled by 2^-8 (the format pf_trimul_fwd uses internally).  The batched
+ * matmul inside TriangleMultiplication (tt_bio/tenstorrent.py:453-460; einsum at
  * tt_bio/reference.py:467, 556). */
-int pf_trimul_contract(const void* A, const void* Bm, float* X, int planes, int N, void* stream);
+int pf_trimul_contract(const void* A, const void* Bm, void* X, int x_fp32, int planes, int N, void* stream);
 
 /* ------------------------------------------------------------------------------
  * Triangle attention, starting node (ending = 0) and ending node (ending = 1).
@@ -96,6 +107,7 @@ typedef struct pf_triatt_args {
   int H, D;               /* heads = 4, head dim = 32 (H*D == C) */
   int ending;             /* 0 starting node, 1 ending node */
   int accumulate;
+  int n_valid;            /* keys >= n_valid excluded (boundary padding); 0 = N */
   float eps;
   const float* z_in;      /* [B][N][N][C] */
   float* out;             /* may alias z_in */
@@ -117,11 +129,11 @@ int pf_triatt_fwd(const pf_triatt_args* args);
  * (tt_bio/reference.py:176-190, tt_bio/boltz2.py:790-810):
  *   o[b,i,h,j,:] = sum_k softmax_k(scale*q.k + 1e9*(mask[b,i,k]-1) + bias[b,h,j,k]) v[b,i,h,k,:]
  * q, k, v: fp32 [B][I][H][J][D] (I = J = N); bias fp32 [B][H][N][N]; mask fp32 [B][I][N]
- * or NULL; o fp32 [B][I][H][J][D].  D must be 32. */
+ * or NULL; o fp32 [B][I][H][J][D].  D must be 32; keys >= n_valid are padding (0 = N). */
 size_t pf_tri_attention_workspace_size(int B, int N, int H, int D);
 int pf_tri_attention(const float* q, const float* k, const float* v, const float* bias,
                      const float* mask, float scale, float* o, int B, int N, int H, int D,
-                     void* workspace, size_t workspace_bytes, void* stream);
+                     int n_valid, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------
  * Transition (SwiGLU MLP): update = fc3(silu(fc1(LN(x))) * fc2(LN(x))), no biases.
@@ -160,6 +172,7 @@ int pf_transition_fwd(const pf_transition_args* args);
 typedef struct pf_apb_args {
   int B, N, c_s, C, H;    /* c_s = 384, C = 128, H = 16 (head dim c_s/H) */
   int accumulate;
+  int n_valid;            /* keys >= n_valid excluded (boundary padding); 0 = N */
   float eps;              /* eps of the proj_z LayerNorm */
   const float* s;         /* query input (pre_norm_s(s) in the Pairformer) */
   const float* k_in;      /* key/value input */

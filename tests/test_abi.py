@@ -40,7 +40,7 @@ def test_struct_layouts_match_header_order():
     # the ctypes structs mirror the C structs field by field; spot-check sizes/offsets
     assert _lib.TrimulArgs.z_in.offset == 32 and ctypes.sizeof(_lib.TrimulArgs) == 32 + 14 * 8
     assert _lib.TransitionArgs.x_in.offset == 24
-    assert _lib.TriattArgs.z_in.offset == 32
+    assert _lib.TriattArgs.z_in.offset == 40
 
 
 def _err():
@@ -60,9 +60,17 @@ def test_rejects_null_and_bad_shapes_without_launching():
     assert lib.pf_linear_fwd(1, 1, None, None, 1, 4, 15, 32, None) == -1 and "K % 16" in _err()
 
 
+def test_both_operand_variants_load():
+    for variant, code in _lib.OPERAND_CODE.items():
+        lib = _lib.load(variant)
+        assert lib.pf_operand_dtype() == code and lib.pf_abi_version() == 1
+        for name in _declared():
+            assert hasattr(lib, name), (variant, name)
+
+
 def test_workspace_sizes():
     lib = _lib.load()
-    assert lib.pf_trimul_workspace_size(1, 512, 128) == 128 * 512 * 512 * (2 + 2 + 4)
+    assert lib.pf_trimul_workspace_size(1, 512, 128) == 128 * 512 * 512 * (2 + 2 + 2)
     assert lib.pf_triatt_workspace_size(1, 64, 128, 4, 32) > 0
     assert lib.pf_triatt_workspace_size(1, 64, 128, 8, 16) == 0
     assert lib.pf_transition_workspace_size(4096, 128, 512) == 0          # fused, no scratch

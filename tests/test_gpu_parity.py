@@ -33,16 +33,12 @@ def check(name, gpu_t, ref_t, max_tol=MAX_TOL, mean_tol=MEAN_TOL):
 
 
 def _sub_w(seed, prefix):
-    return ref.sub(synthetic.draw({f"{prefix}.{k}": v for k, v in synthetic.layer_shapes().items()
+    return ref.sub(synthetic.draw({k: v for k, v in synthetic.layer_shapes().items()
                                    if k.startswith(prefix + ".")}, seed), prefix)
 
 
-def _dev_w(w, dev, strip=""):
-    out = {}
-    for k, v in w.items():
-        kk = k[len(strip):] if strip and k.startswith(strip) else k
-        out[kk] = ops.f32(v, dev) if v.dim() == 1 else ops.bf16(v, dev)
-    return out
+def _dev_w(w, dev, strip="", variant=ops.DEFAULT_VARIANT):
+    return ops.convert_weights(w, dev, variant, strip)
 
 
 def _inputs(N, seed, pad_tail=0, rand_mask=False):
@@ -54,17 +50,27 @@ def _inputs(N, seed, pad_tail=0, rand_mask=False):
 
 
 # ------------------------------------------------------------------------------ contraction
+@pytest.mark.parametrize("variant", ["fp16", "bf16"])
 @pytest.mark.parametrize("N", [64, 192, 256])
-def test_contract_matches_fp32_matmul(gpu, N):
+def test_contract_matches_fp32_matmul(gpu, N, variant):
+    """The MFMA contraction on operand-type planes equals an fp32 matmul of the same
+    (already rounded) values up to summation order; the scaled operand-type output is
+    that result rounded once."""
     g = torch.Generator().manual_seed(N)
-    A = torch.randn((3, N, N), generator=g).to(torch.bfloat16)
-    Bm = torch.randn((3, N, N), generator=g).to(torch.bfloat16)
-    X = torch.empty((3, N, N), dtype=torch.float32, device=gpu)
-    ops.launch_trimul_contract(A.to(gpu), Bm.to(gpu), X)
+    dt = ops.TORCH_DTYPE[variant]
+    A = torch.randn((3, N, N), generator=g).to(dt)
+    Bm = torch.randn((3, N, N), generator=g).to(dt)
     want = torch.bmm(A.float(), Bm.float().transpose(1, 2))
+    X = torch.empty((3, N, N), dtype=torch.float32, device=gpu)
+    ops.launch_trimul_contract(A.to(gpu), Bm.to(gpu), X, variant)
     mx, _ = stats(X, want)
-    print(f"[parity] contract N={N}: max/rms={mx:.3e}", flush=True)
+    print(f"[parity] contract {variant} N={N}: max/rms={mx:.3e}", flush=True)
     assert mx < 1e-5
+    Xh = torch.empty((3, N, N), dtype=dt, device=gpu)
+    ops.launch_trimul_contract(A.to(gpu), Bm.to(gpu), Xh, variant)
+    mx, _ = stats(Xh.float() * 256.0, want)
+    # one rounding: |err| <= 2^-11 (fp16) / 2^-8 (bf16) of |x|, and max|x| < 5 rms here
+    assert mx < (5 * 2 ** -11 if variant == "fp16" else 5 * 2 ** -8)
 
 
 # ------------------------------------------------------------------------------ triangle multiplication
@@ -197,6 +203,21 @@ def test_layer_config0(gpu):
     s_got, z_got = mod(s.to(gpu), z.to(gpu), mask.to(gpu), pm.to(gpu))
     check("config0 layer z", z_got, z_ref)
     check("config0 layer s", s_got, s_ref)
+
+
+def test_layer_config0_bf16_operands(gpu):
+    """Same layer with the bf16-operand library.  bf16 keeps 8 significant bits, so each
+    MFMA operand rounding costs ~2^-9 relative; its bar is the looser
+    max 5e-2 / mean 6e-3 of the rms (measured ~2.2e-2 / 3.0e-3)."""
+    cfg = synthetic.CONFIGS[0]
+    w = synthetic.stack_weights(1, cfg["seed"])
+    s, z, mask, pm = _inputs(cfg["N"], cfg["seed"])
+    s_ref, z_ref = ref.pairformer_stack(s, z, mask, pm, w, 1)
+    mod = pairformer.PairformerModule(1, 32, 4, 24, 16, True, options=pairformer.Options(operand="bf16"))
+    mod.load_state_dict(w)
+    s_got, z_got = mod(s.to(gpu), z.to(gpu), mask.to(gpu), pm.to(gpu))
+    check("config0 layer z (bf16 operands)", z_got, z_ref, 5e-2, 6e-3)
+    check("config0 layer s (bf16 operands)", s_got, s_ref, 5e-2, 6e-3)
 
 
 def test_module_dropin_padding(gpu):

@@ -1,7 +1,10 @@
-"""ctypes binding of libpairformer_hip.so (the C ABI in include/pairformer_hip.h).
+"""ctypes binding of libpairformer_hip (the C ABI in include/pairformer_hip.h).
 
-The library is loaded from this directory.  If it is missing, every call raises:
-there is no CPU or torch fallback for any operation of this package.
+Two builds of the same kernels live next to this file:
+``libpairformer_hip.so`` (IEEE fp16 MFMA operands, the default) and
+``libpairformer_hip_bf16.so`` (bf16 operands).  If the requested library is
+missing, loading raises: there is no CPU or torch fallback for any operation of
+this package.
 """
 from __future__ import annotations
 
@@ -10,11 +13,13 @@ import os
 import threading
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libpairformer_hip.so")
+LIBS = {"fp16": "libpairformer_hip.so", "bf16": "libpairformer_hip_bf16.so"}
+OPERAND_CODE = {"fp16": 0, "bf16": 1}
+DEFAULT_VARIANT = "fp16"
+LIB_PATH = os.path.join(HERE, LIBS[DEFAULT_VARIANT])
 ABI_VERSION = 1
 
 c_int, c_float, c_long, c_size_t, c_void_p = ctypes.c_int, ctypes.c_float, ctypes.c_long, ctypes.c_size_t, ctypes.c_void_p
-c_float_p = c_void_p   # device pointers are passed as integers
 
 
 class TrimulArgs(ctypes.Structure):
@@ -31,7 +36,7 @@ class TrimulArgs(ctypes.Structure):
 class TriattArgs(ctypes.Structure):
     _fields_ = [
         ("B", c_int), ("N", c_int), ("C", c_int), ("H", c_int), ("D", c_int), ("ending", c_int),
-        ("accumulate", c_int), ("eps", c_float),
+        ("accumulate", c_int), ("n_valid", c_int), ("eps", c_float),
         ("z_in", c_void_p), ("out", c_void_p), ("pair_mask", c_void_p),
         ("ln_w", c_void_p), ("ln_b", c_void_p), ("w_bias", c_void_p),
         ("w_q", c_void_p), ("w_k", c_void_p), ("w_v", c_void_p), ("w_g", c_void_p), ("w_o", c_void_p),
@@ -51,7 +56,7 @@ class TransitionArgs(ctypes.Structure):
 class ApbArgs(ctypes.Structure):
     _fields_ = [
         ("B", c_int), ("N", c_int), ("c_s", c_int), ("C", c_int), ("H", c_int),
-        ("accumulate", c_int), ("eps", c_float),
+        ("accumulate", c_int), ("n_valid", c_int), ("eps", c_float),
         ("s", c_void_p), ("k_in", c_void_p), ("z", c_void_p), ("mask", c_void_p), ("out", c_void_p),
         ("w_q", c_void_p), ("b_q", c_void_p), ("w_k", c_void_p), ("w_v", c_void_p), ("w_g", c_void_p),
         ("w_o", c_void_p), ("zln_w", c_void_p), ("zln_b", c_void_p), ("w_z", c_void_p),
@@ -63,14 +68,15 @@ class ApbArgs(ctypes.Structure):
 SIGNATURES = {
     "pf_abi_version": (c_int, []),
     "pf_last_error": (ctypes.c_char_p, []),
+    "pf_operand_dtype": (c_int, []),
     "pf_trimul_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "pf_trimul_fwd": (c_int, [ctypes.POINTER(TrimulArgs)]),
-    "pf_trimul_contract": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "pf_trimul_contract": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "pf_triatt_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "pf_triatt_fwd": (c_int, [ctypes.POINTER(TriattArgs)]),
     "pf_tri_attention_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "pf_tri_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p,
-                                 c_int, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]),
+                                 c_int, c_int, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]),
     "pf_transition_workspace_size": (c_size_t, [c_long, c_int, c_int]),
     "pf_transition_fwd": (c_int, [ctypes.POINTER(TransitionArgs)]),
     "pf_apb_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
@@ -82,35 +88,40 @@ SIGNATURES = {
 }
 
 _lock = threading.Lock()
-_lib = None
+_libs: dict = {}
 
 
-def load() -> ctypes.CDLL:
-    """Load (once) and return the library; raise if it is missing or mismatched."""
-    global _lib
-    if _lib is not None:
-        return _lib
+def load(variant: str = DEFAULT_VARIANT) -> ctypes.CDLL:
+    """Load (once) and return the library of ``variant`` ('fp16' or 'bf16')."""
+    lib = _libs.get(variant)
+    if lib is not None:
+        return lib
+    if variant not in LIBS:
+        raise ValueError(f"unknown operand variant {variant!r}; expected one of {sorted(LIBS)}")
     with _lock:
-        if _lib is not None:
-            return _lib
-        if not os.path.exists(LIB_PATH):
-            raise RuntimeError(
-                f"{LIB_PATH} is missing: build it with `python tt-boltz_amd/build.py` "
-                "(there is no fallback path)")
-        lib = ctypes.CDLL(LIB_PATH)
+        lib = _libs.get(variant)
+        if lib is not None:
+            return lib
+        path = os.path.join(HERE, LIBS[variant])
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: build it with `python tt-boltz_amd/build.py` "
+                               "(there is no fallback path)")
+        lib = ctypes.CDLL(path)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
         v = lib.pf_abi_version()
         if v != ABI_VERSION:
-            raise RuntimeError(f"libpairformer_hip ABI {v} != expected {ABI_VERSION}; rebuild")
-        _lib = lib
-    return _lib
+            raise RuntimeError(f"{path}: ABI {v} != expected {ABI_VERSION}; rebuild")
+        if lib.pf_operand_dtype() != OPERAND_CODE[variant]:
+            raise RuntimeError(f"{path}: operand dtype code {lib.pf_operand_dtype()} does not match {variant}")
+        _libs[variant] = lib
+    return lib
 
 
-def check(rc: int, what: str) -> None:
+def check(rc: int, what: str, variant: str = DEFAULT_VARIANT) -> None:
     """Raise RuntimeError(pf_last_error()) for a non-zero status."""
     if rc != 0:
-        msg = load().pf_last_error().decode(errors="replace")
+        msg = load(variant).pf_last_error().decode(errors="replace")
         raise RuntimeError(f"{what} failed ({rc}): {msg}")

@@ -15,7 +15,6 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
-LIB = os.path.join(HERE, "libpairformer_hip.so")
 OBJDIR = os.path.join(HERE, "_build")
 
 SOURCES = ["api.cpp", "trimul.hip", "triatt.hip", "transition.hip", "single.hip"]
@@ -29,28 +28,44 @@ CFLAGS = [
 ]
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+#: library variants: file name -> extra defines.  The default library uses IEEE fp16
+#: MFMA operands; the _bf16 variant uses bf16 operands (same kernels, same ABI).
+VARIANTS = {
+    "libpairformer_hip.so": [],
+    "libpairformer_hip_bf16.so": ["-DPF_OPERAND_BF16"],
+}
+
+
+def _compile(job) -> str:
+    src, defines, objdir = job
+    obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
+    cmd = [HIPCC, *CFLAGS, *defines, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
+        raise RuntimeError(f"hipcc failed for {src} {defines}:\n{r.stderr}")
     return obj
 
 
-def build(verbose: bool = True) -> str:
-    os.makedirs(OBJDIR, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
-    if verbose:
-        print(f"built {LIB}")
-    return LIB
+def build(verbose: bool = True) -> list:
+    jobs, outs = [], []
+    for lib, defines in VARIANTS.items():
+        objdir = os.path.join(OBJDIR, os.path.splitext(lib)[0])
+        os.makedirs(objdir, exist_ok=True)
+        jobs.append([(src, defines, objdir) for src in SOURCES])
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
+        objs = [list(ex.map(_compile, j)) for j in jobs]
+    for (lib, _), o in zip(VARIANTS.items(), objs):
+        path = os.path.join(HERE, lib)
+        tmp = path + ".tmp"
+        r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *o, "-o", tmp],
+                           capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"link failed for {lib}:\n{r.stderr}")
+        os.replace(tmp, path)
+        outs.append(path)
+        if verbose:
+            print(f"built {path}")
+    return outs
 
 
 if __name__ == "__main__":

@@ -19,3 +19,11 @@ int pf_fail(int code, const char* fmt, ...) {
 extern "C" int pf_abi_version(void) { return PF_ABI_VERSION; }
 
 extern "C" const char* pf_last_error(void) { return g_last_error; }
+
+extern "C" int pf_operand_dtype(void) {
+#ifdef PF_OPERAND_BF16
+  return 1;
+#else
+  return 0;
+#endif
+}

@@ -1,9 +1,16 @@
 // Shared device helpers for the Pairformer CDNA4 (gfx950) kernels.
 //
-// MFMA conventions used by every kernel in this library (wave64, bf16 in, fp32 acc):
+// Operand type.  MFMA operands (weights, normalized activations, attention Q/K/V/P,
+// trimul a/b planes) are `op_t`: IEEE fp16 by default, bf16 when built with
+// -DPF_OPERAND_BF16.  On gfx950 both run at the same dense MFMA rate; fp16 carries
+// 3 more mantissa bits, which is what keeps the bf16-class kernels inside the fp32
+// parity bar.  Accumulation, LayerNorm/softmax statistics and the residual stream
+// are fp32 in both builds.
 //
-//   v_mfma_f32_32x32x16_bf16   D[32x32] += A[32x16] * B[16x32]
-//     A operand  lane l: row    m = l & 31, k = 8*(l >> 5) + t   (t = 0..7, one bf16x8)
+// MFMA conventions used by every kernel in this library (wave64, fp32 acc):
+//
+//   v_mfma_f32_32x32x16_{f16,bf16}   D[32x32] += A[32x16] * B[16x32]
+//     A operand  lane l: row    m = l & 31, k = 8*(l >> 5) + t   (t = 0..7, one opx8)
 //     B operand  lane l: column n = l & 31, k = 8*(l >> 5) + t
 //     C/D        lane l, reg r (0..15): column n = l & 31,
 //                                      row    m = 8*(r >> 2) + 4*(l >> 5) + (r & 3)
@@ -13,23 +20,30 @@
 // use this to feed an accumulator straight back in as the next MFMA's A/B operand:
 // accumulator regs 8*s .. 8*s+7 of a lane in half h hold rows
 //   16*s + 4*h + {0,1,2,3}  and  16*s + 8 + 4*h + {0,1,2,3}
-// so the partner operand is loaded with the same two 4-element runs (see
-// kperm_row()).
+// so the partner operand is loaded with the same two 4-element runs (kperm_row()),
+// or the producer's rows are pre-permuted so the runs come out contiguous (perm16()).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-typedef __bf16 bf16;
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+#ifdef PF_OPERAND_BF16
+typedef __bf16 op_t;
+#else
+typedef _Float16 op_t;
+#endif
+typedef op_t opx8 __attribute__((ext_vector_type(8)));
+typedef op_t opx4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #define PF_DEV __device__ __forceinline__
 
-PF_DEV f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+PF_DEV f32x16 mfma32(const opx8& a, const opx8& b, const f32x16& c) {
+#ifdef PF_OPERAND_BF16
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+#else
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+#endif
 }
 
 PF_DEV f32x16 zero16() {
@@ -45,6 +59,11 @@ PF_DEV int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 // k index carried by slot t (0..7) of a lane in half h for k-step s when the
 // operand comes from accumulator registers 8*s .. 8*s+7 (see header comment).
 PF_DEV int kperm_row(int s, int h, int t) { return 16 * s + 4 * h + (t < 4 ? t : t + 4); }
+
+// Involution on row indices swapping bits 2 and 3.  If a producer GEMM's weight row
+// rho holds output unit perm16(rho), accumulator regs 8*s+t of half h come out as
+// units 16*s + 8*h + t: the natural k order of the next MFMA operand.
+PF_DEV int perm16(int row) { return (row & ~0xC) | ((row & 4) << 1) | ((row & 8) >> 1); }
 
 PF_DEV float sigmoidf_fast(float x) { return 1.f / (1.f + __expf(-x)); }
 
@@ -68,13 +87,22 @@ PF_DEV float wave_max(float v) {
   return v;
 }
 
-PF_DEV bf16x8 ld_bf16x8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
-PF_DEV bf16x4 ld_bf16x4(const bf16* p) { return *reinterpret_cast<const bf16x4*>(p); }
+PF_DEV opx8 ld_x8(const op_t* p) { return *reinterpret_cast<const opx8*>(p); }
+PF_DEV opx4 ld_x4(const op_t* p) { return *reinterpret_cast<const opx4*>(p); }
+PF_DEV void st_x8(op_t* p, const opx8& v) { *reinterpret_cast<opx8*>(p) = v; }
+PF_DEV void st_x4(op_t* p, const opx4& v) { *reinterpret_cast<opx4*>(p) = v; }
 
-PF_DEV bf16x8 cat44(const bf16x4& a, const bf16x4& b) {
-  bf16x8 r;
+PF_DEV opx8 cat44(const opx4& a, const opx4& b) {
+  opx8 r;
   r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
   r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+
+PF_DEV opx8 zero_x8() {
+  opx8 r;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) r[t] = (op_t)0.f;
   return r;
 }
 
@@ -91,10 +119,10 @@ PF_DEV void load_row128_frag(const float* __restrict__ p, int h, float (&x)[64])
 }
 
 // LayerNorm of a 128-vector split over the two halves of a wave (64 values per
-// lane, in load_row128_frag order), written as 8 bf16x8 MFMA fragments.
+// lane, in load_row128_frag order), written as 8 opx8 MFMA fragments.
 // Two-pass (mean, then centred variance) in fp32, like torch's CPU kernel.
 PF_DEV void ln128_to_frag(const float (&x)[64], int h, const float* __restrict__ w,
-                          const float* __restrict__ b, float eps, bf16x8 (&f)[8]) {
+                          const float* __restrict__ b, float eps, opx8 (&f)[8]) {
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 64; ++i) s += x[i];
@@ -108,7 +136,7 @@ PF_DEV void ln128_to_frag(const float (&x)[64], int h, const float* __restrict__
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const int c = 16 * s8 + 8 * h + t;
-      f[s8][t] = (bf16)((x[8 * s8 + t] - mean) * rstd * w[c] + b[c]);
+      f[s8][t] = (op_t)((x[8 * s8 + t] - mean) * rstd * w[c] + b[c]);
     }
   }
 }
@@ -120,3 +148,8 @@ PF_DEV int xcd_remap(int w, int total) {
   if (total % 8) return w;
   return (w % 8) * (total / 8) + (w / 8);
 }
+
+// Fixed power-of-two scale of the fp16 contraction planes X (trimul): X is stored
+// as X * 2^-8 so |X| up to ~1.7e7 fits fp16's range; the epilogue multiplies back.
+constexpr float X_STORE_SCALE = 1.f / 256.f;
+constexpr float X_LOAD_SCALE = 256.f;

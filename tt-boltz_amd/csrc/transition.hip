@@ -3,14 +3,14 @@
 //   tr_pair_kernel   Pair transition, C = 128: LN -> fc1|fc2 (MFMA, transposed
 //                    orientation) -> silu(a)*b in registers -> fc3 (MFMA) -> residual.
 //                    The 4C hidden activations never leave the CU.  fc1/fc2 rows are
-//                    permuted inside each 16-row group while staged in LDS (bits 2 and 3
-//                    of the row index swapped) so that the fc1/fc2 accumulator registers
-//                    come out in the natural k order fc3's A operand expects.
+//                    staged in LDS perm16-permuted so the fc1/fc2 accumulator registers
+//                    come out in the natural k order fc3's A operand expects.  A wave owns
+//                    PB*32 pairs so every weight fragment read from LDS feeds PB MFMAs.
 //                    Replaces Transition.forward (tt_bio/boltz2.py:1227-1258) and the ttnn
 //                    Transition (tt_bio/tenstorrent.py:856-946).
 //   ln_rows_kernel   LayerNorm over rows, any C (nn.LayerNorm / tt_bio/boltz2.py:738-768).
 //   linear_rows_kernel  out = resid + x W^T + bias, optional SwiGLU pairing of two weight
-//                    matrices (tt_bio/boltz2.py:638-731); fp32 in/out, bf16 MFMA inside.
+//                    matrices (tt_bio/boltz2.py:638-731); fp32 in/out, MFMA inside.
 //   pair_ln_linear_kernel  out = base + W LN(x) for C = 128 rows (trunk recycling step).
 #include "pf_common.h"
 #include "pf_internal.h"
@@ -18,37 +18,43 @@
 namespace {
 
 constexpr int C = 128, LDSW = 136, LDS3 = 40;
-
-PF_DEV int perm16(int row) { return (row & ~0xC) | ((row & 4) << 1) | ((row & 8) >> 1); }
+constexpr int PB = 2;   // 32-pair blocks per wave
 
 __global__ __launch_bounds__(256) void tr_pair_kernel(
     const float* x_in, float* out, const float* __restrict__ lnw, const float* __restrict__ lnb,
-    const bf16* __restrict__ w1, const bf16* __restrict__ w2, const bf16* __restrict__ w3,
+    const op_t* __restrict__ w1, const op_t* __restrict__ w2, const op_t* __restrict__ w3,
     long rows, int hidden, int accumulate, float eps) {
-  __shared__ __attribute__((aligned(16))) bf16 s1[2][32 * LDSW];
-  __shared__ __attribute__((aligned(16))) bf16 s2[2][32 * LDSW];
-  __shared__ __attribute__((aligned(16))) bf16 s3[2][C * LDS3];
+  __shared__ __attribute__((aligned(16))) op_t s1[2][32 * LDSW];
+  __shared__ __attribute__((aligned(16))) op_t s2[2][32 * LDSW];
+  __shared__ __attribute__((aligned(16))) op_t s3[2][C * LDS3];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
-  const long pos0 = ((long)blockIdx.x * 4 + wid) * 32;
+  const long pos0 = ((long)blockIdx.x * 4 + wid) * (32 * PB);
   const bool active = pos0 < rows;
 
-  bf16x8 xf[8];
+  opx8 xf[PB][8];
   if (active) {
-    float x[64];
-    load_row128_frag(x_in + min(pos0 + m, rows - 1) * C, h, x);
-    ln128_to_frag(x, h, lnw, lnb, eps, xf);
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) {
+      float x[64];
+      load_row128_frag(x_in + min(pos0 + 32 * pb + m, rows - 1) * C, h, x);
+      ln128_to_frag(x, h, lnw, lnb, eps, xf[pb]);
+    }
   }
-  f32x16 acc[4] = {zero16(), zero16(), zero16(), zero16()};
+  f32x16 acc[PB][4];
+#pragma unroll
+  for (int pb = 0; pb < PB; ++pb)
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob) acc[pb][ob] = zero16();
 
   // staging: fc1/fc2 block = 32 rows x 128 (2 chunks/thread each), fc3 block = 128 rows x 32 (2 chunks/thread)
-  bf16x8 r1[2], r2[2], r3[2];
+  opx8 r1[2], r2[2], r3[2];
   auto gload = [&](int hb) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int c = tid + 256 * q;
-      r1[q] = ld_bf16x8(w1 + (long)(32 * hb + (c >> 4)) * C + (c & 15) * 8);
-      r2[q] = ld_bf16x8(w2 + (long)(32 * hb + (c >> 4)) * C + (c & 15) * 8);
-      r3[q] = ld_bf16x8(w3 + (long)(c >> 2) * hidden + 32 * hb + (c & 3) * 8);
+      r1[q] = ld_x8(w1 + (long)(32 * hb + (c >> 4)) * C + (c & 15) * 8);
+      r2[q] = ld_x8(w2 + (long)(32 * hb + (c >> 4)) * C + (c & 15) * 8);
+      r3[q] = ld_x8(w3 + (long)(c >> 2) * hidden + 32 * hb + (c & 3) * 8);
     }
   };
   const int nhb = hidden / 32;
@@ -59,41 +65,55 @@ __global__ __launch_bounds__(256) void tr_pair_kernel(
     for (int q = 0; q < 2; ++q) {
       const int c = tid + 256 * q;
       const int row = perm16(c >> 4);
-      *reinterpret_cast<bf16x8*>(&s1[bufi][row * LDSW + (c & 15) * 8]) = r1[q];
-      *reinterpret_cast<bf16x8*>(&s2[bufi][row * LDSW + (c & 15) * 8]) = r2[q];
-      *reinterpret_cast<bf16x8*>(&s3[bufi][(c >> 2) * LDS3 + (c & 3) * 8]) = r3[q];
+      st_x8(&s1[bufi][row * LDSW + (c & 15) * 8], r1[q]);
+      st_x8(&s2[bufi][row * LDSW + (c & 15) * 8], r2[q]);
+      st_x8(&s3[bufi][(c >> 2) * LDS3 + (c & 3) * 8], r3[q]);
     }
     __syncthreads();
     if (hb + 1 < nhb) gload(hb + 1);
     if (!active) continue;
-    f32x16 a1 = zero16(), a2 = zero16();
+    f32x16 a1[PB], a2[PB];
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) { a1[pb] = zero16(); a2[pb] = zero16(); }
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      a1 = mfma32(ld_bf16x8(&s1[bufi][m * LDSW + 16 * s + 8 * h]), xf[s], a1);
-      a2 = mfma32(ld_bf16x8(&s2[bufi][m * LDSW + 16 * s + 8 * h]), xf[s], a2);
+      const opx8 f1 = ld_x8(&s1[bufi][m * LDSW + 16 * s + 8 * h]);
+      const opx8 f2 = ld_x8(&s2[bufi][m * LDSW + 16 * s + 8 * h]);
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) {
+        a1[pb] = mfma32(f1, xf[pb][s], a1[pb]);   // rows = hidden (perm16), cols = pairs
+        a2[pb] = mfma32(f2, xf[pb][s], a2[pb]);
+      }
     }
-    bf16x8 hf[2];
+    opx8 hf[PB][2];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int pb = 0; pb < PB; ++pb)
 #pragma unroll
-      for (int t = 0; t < 8; ++t) hf[ks][t] = (bf16)(siluf(a1[8 * ks + t]) * a2[8 * ks + t]);
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) hf[pb][ks][t] = (op_t)(siluf(a1[pb][8 * ks + t]) * a2[pb][8 * ks + t]);
 #pragma unroll
     for (int ob = 0; ob < 4; ++ob)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        acc[ob] = mfma32(hf[ks], ld_bf16x8(&s3[bufi][(32 * ob + m) * LDS3 + 16 * ks + 8 * h]), acc[ob]);
+      for (int ks = 0; ks < 2; ++ks) {
+        const opx8 f3 = ld_x8(&s3[bufi][(32 * ob + m) * LDS3 + 16 * ks + 8 * h]);
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb) acc[pb][ob] = mfma32(hf[pb][ks], f3, acc[pb][ob]);
+      }
   }
   if (!active) return;
 #pragma unroll
-  for (int ob = 0; ob < 4; ++ob)
+  for (int pb = 0; pb < PB; ++pb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const long p = pos0 + acc_row(r, h);
-      if (p < rows) {
-        const long idx = p * C + 32 * ob + m;
-        out[idx] = accumulate ? out[idx] + acc[ob][r] : acc[ob][r];
+    for (int ob = 0; ob < 4; ++ob)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const long p = pos0 + 32 * pb + acc_row(r, h);
+        if (p < rows) {
+          const long idx = p * C + 32 * ob + m;
+          out[idx] = accumulate ? out[idx] + acc[pb][ob][r] : acc[pb][ob][r];
+        }
       }
-    }
 }
 
 // One wave per row.
@@ -117,24 +137,24 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ 
 // SWIGLU: out[:, n] = silu(x W[n]) * (x W2[n]).
 template <bool SWIGLU>
 __global__ __launch_bounds__(256) void linear_rows_kernel(
-    const float* __restrict__ x, const bf16* __restrict__ W, const bf16* __restrict__ W2,
+    const float* __restrict__ x, const op_t* __restrict__ W, const op_t* __restrict__ W2,
     const float* __restrict__ bias, const float* resid, float* out, long rows, int K, int Nout) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
   const int nt = blockIdx.y * 4 + wid;   // column tile
   if (nt * 32 >= Nout) return;
   const long r0 = (long)blockIdx.x * 32;
   const float* xr = x + min(r0 + m, rows - 1) * K;
-  const bf16* wr = W + (long)(nt * 32 + m) * K;
-  const bf16* wr2 = SWIGLU ? W2 + (long)(nt * 32 + m) * K : nullptr;
+  const op_t* wr = W + (long)(nt * 32 + m) * K;
+  const op_t* wr2 = SWIGLU ? W2 + (long)(nt * 32 + m) * K : nullptr;
   f32x16 acc = zero16(), acc2 = zero16();
   for (int k0 = 0; k0 < K; k0 += 16) {
     const f32x4 a0 = *reinterpret_cast<const f32x4*>(xr + k0 + 8 * h);
     const f32x4 a1 = *reinterpret_cast<const f32x4*>(xr + k0 + 8 * h + 4);
-    bf16x8 af;
-    af[0] = (bf16)a0[0]; af[1] = (bf16)a0[1]; af[2] = (bf16)a0[2]; af[3] = (bf16)a0[3];
-    af[4] = (bf16)a1[0]; af[5] = (bf16)a1[1]; af[6] = (bf16)a1[2]; af[7] = (bf16)a1[3];
-    acc = mfma32(af, ld_bf16x8(wr + k0 + 8 * h), acc);
-    if (SWIGLU) acc2 = mfma32(af, ld_bf16x8(wr2 + k0 + 8 * h), acc2);
+    opx8 af;
+    af[0] = (op_t)a0[0]; af[1] = (op_t)a0[1]; af[2] = (op_t)a0[2]; af[3] = (op_t)a0[3];
+    af[4] = (op_t)a1[0]; af[5] = (op_t)a1[1]; af[6] = (op_t)a1[2]; af[7] = (op_t)a1[3];
+    acc = mfma32(af, ld_x8(wr + k0 + 8 * h), acc);
+    if (SWIGLU) acc2 = mfma32(af, ld_x8(wr2 + k0 + 8 * h), acc2);
   }
   const int n = nt * 32 + m;
   const float bn = bias ? bias[n] : 0.f;
@@ -153,26 +173,26 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(
 // out[p, :] = base[p, :] + W . LN(x[p, :]),  C = 128; W resident in LDS.
 __global__ __launch_bounds__(256) void pair_ln_linear_kernel(
     const float* x, const float* base, const float* __restrict__ lnw, const float* __restrict__ lnb,
-    const bf16* __restrict__ W, float* out, long rows, float eps) {
-  __shared__ __attribute__((aligned(16))) bf16 sW[C * LDSW];
+    const op_t* __restrict__ W, float* out, long rows, float eps) {
+  __shared__ __attribute__((aligned(16))) op_t sW[C * LDSW];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     const int c = tid + 256 * q;
-    *reinterpret_cast<bf16x8*>(&sW[(c >> 4) * LDSW + (c & 15) * 8]) = ld_bf16x8(W + (c >> 4) * C + (c & 15) * 8);
+    st_x8(&sW[(c >> 4) * LDSW + (c & 15) * 8], ld_x8(W + (c >> 4) * C + (c & 15) * 8));
   }
   __syncthreads();
   const long pos0 = ((long)blockIdx.x * 4 + wid) * 32;
   if (pos0 >= rows) return;
   float xv[64];
-  bf16x8 xf[8];
+  opx8 xf[8];
   load_row128_frag(x + min(pos0 + m, rows - 1) * C, h, xv);
   ln128_to_frag(xv, h, lnw, lnb, eps, xf);
 #pragma unroll
   for (int ob = 0; ob < 4; ++ob) {
     f32x16 acc = zero16();
 #pragma unroll
-    for (int s = 0; s < 8; ++s) acc = mfma32(xf[s], ld_bf16x8(&sW[(32 * ob + m) * LDSW + 16 * s + 8 * h]), acc);
+    for (int s = 0; s < 8; ++s) acc = mfma32(xf[s], ld_x8(&sW[(32 * ob + m) * LDSW + 16 * s + 8 * h]), acc);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const long p = pos0 + acc_row(r, h);
@@ -206,9 +226,9 @@ static int launch_linear(const float* x, const void* W, const void* W2, const fl
                    rows, K, Nout);
   dim3 grid((unsigned)((rows + 31) / 32), (unsigned)((Nout / 32 + 3) / 4));
   if (W2)
-    linear_rows_kernel<true><<<grid, 256, 0, st>>>(x, (const bf16*)W, (const bf16*)W2, nullptr, nullptr, out, rows, K, Nout);
+    linear_rows_kernel<true><<<grid, 256, 0, st>>>(x, (const op_t*)W, (const op_t*)W2, nullptr, nullptr, out, rows, K, Nout);
   else
-    linear_rows_kernel<false><<<grid, 256, 0, st>>>(x, (const bf16*)W, nullptr, bias, resid, out, rows, K, Nout);
+    linear_rows_kernel<false><<<grid, 256, 0, st>>>(x, (const op_t*)W, nullptr, bias, resid, out, rows, K, Nout);
   PF_CHECK_LAUNCH("linear_rows_kernel");
   return PF_OK;
 }
@@ -233,9 +253,9 @@ extern "C" int pf_transition_fwd(const pf_transition_args* a) {
     return pf_fail(PF_E_INVALID, "pf_transition_fwd: null pointer argument");
   hipStream_t st = (hipStream_t)a->stream;
   if (a->C == C) {
-    const unsigned grid = (unsigned)((a->rows + 127) / 128);
-    tr_pair_kernel<<<grid, 256, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, (const bf16*)a->fc1_w,
-                                         (const bf16*)a->fc2_w, (const bf16*)a->fc3_w, a->rows, a->hidden,
+    const unsigned grid = (unsigned)((a->rows + 128 * PB - 1) / (128 * PB));
+    tr_pair_kernel<<<grid, 256, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w,
+                                         (const op_t*)a->fc2_w, (const op_t*)a->fc3_w, a->rows, a->hidden,
                                          a->accumulate, a->eps);
     PF_CHECK_LAUNCH("tr_pair_kernel");
     return PF_OK;
@@ -258,7 +278,7 @@ extern "C" int pf_pair_ln_linear_fwd(const float* x, const float* base, const fl
   if (!x || !base || !ln_w || !ln_b || !W || !out) return pf_fail(PF_E_INVALID, "pf_pair_ln_linear_fwd: null pointer");
   if (C_ != C || rows <= 0) return pf_fail(PF_E_INVALID, "pf_pair_ln_linear_fwd: only C = 128 (got %d)", C_);
   pair_ln_linear_kernel<<<(unsigned)((rows + 127) / 128), 256, 0, (hipStream_t)stream>>>(
-      x, base, ln_w, ln_b, (const bf16*)W, out, rows, eps);
+      x, base, ln_w, ln_b, (const op_t*)W, out, rows, eps);
   PF_CHECK_LAUNCH("pair_ln_linear_kernel");
   return PF_OK;
 }

@@ -5,13 +5,14 @@
 // (tt_bio/tenstorrent.py:351-503).  Three launches per call:
 //
 //   tm_proj     LN_in(z) -> [p_in | g_in] projection (MFMA) -> a = p*sigmoid(g)*mask,
-//               written as channel-major operand planes opA/opB [B][128][N][N] bf16.
+//               written as channel-major operand planes opA/opB [B][128][N][N] (op_t).
 //               The plane layout already folds the direction: for both directions
 //               the contraction below is  X[c][i][j] = sum_k opA[c][i][k] * opB[c][j][k].
 //                 outgoing: opA[c][i][k] = a[i,k,c],  opB[c][j][k] = b[j,k,c]
 //                 incoming: opA[c][i][k] = a[k,i,c],  opB[c][j][k] = b[k,j,c]
-//   tm_contract 128 (x B) independent N x N x N bf16 GEMMs, fp32 accumulate, 128x128
-//               tiles, LDS double buffer, XCD-aware tile order.
+//   tm_contract 128 (x B) independent N x N x N GEMMs, fp32 accumulate, 128x128 tiles,
+//               LDS double buffer, XCD-aware tile order.  X is stored as op_t scaled by
+//               X_STORE_SCALE (halves the plane traffic; the scale keeps fp16 in range).
 //   tm_out      LN_out(X) -> p_out, LN_in(z) -> g_out (recomputed, so no gate tensor
 //               goes through HBM), update = p * sigmoid(g), residual into z.
 #include "pf_common.h"
@@ -20,22 +21,22 @@
 namespace {
 
 constexpr int C = 128;        // c_z
-constexpr int LDSW = 136;     // padded LDS row stride (bf16) for [rows][128] tiles
+constexpr int LDSW = 136;     // padded LDS row stride (elements) for [rows][128] tiles
 
-// A [32][128] bf16 block moved by 256 threads: 512 chunks of 16 B, 2 per thread.
-struct Blk32 { bf16x8 v[2]; };
-PF_DEV void blk32_load(const bf16* __restrict__ src, int tid, Blk32& r) {
+// A [32][128] op_t block moved by 256 threads: 512 chunks of 16 B, 2 per thread.
+struct Blk32 { opx8 v[2]; };
+PF_DEV void blk32_load(const op_t* __restrict__ src, int tid, Blk32& r) {
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int c = tid + 256 * q;
-    r.v[q] = ld_bf16x8(src + (c >> 4) * C + (c & 15) * 8);
+    r.v[q] = ld_x8(src + (c >> 4) * C + (c & 15) * 8);
   }
 }
-PF_DEV void blk32_store(bf16* lds, int tid, const Blk32& r) {
+PF_DEV void blk32_store(op_t* lds, int tid, const Blk32& r) {
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int c = tid + 256 * q;
-    *reinterpret_cast<bf16x8*>(lds + (c >> 4) * LDSW + (c & 15) * 8) = r.v[q];
+    st_x8(lds + (c >> 4) * LDSW + (c & 15) * 8, r.v[q]);
   }
 }
 
@@ -46,9 +47,9 @@ PF_DEV void blk32_store(bf16* lds, int tid, const Blk32& r) {
 __global__ __launch_bounds__(256) void tm_proj_kernel(
     const float* __restrict__ z, const float* __restrict__ mask,
     const float* __restrict__ lnw, const float* __restrict__ lnb,
-    const bf16* __restrict__ w_p, const bf16* __restrict__ w_g,
-    bf16* __restrict__ opA, bf16* __restrict__ opB, int B, int N, int incoming, float eps) {
-  __shared__ __attribute__((aligned(16))) bf16 lds[2][2][32 * LDSW];
+    const op_t* __restrict__ w_p, const op_t* __restrict__ w_g,
+    op_t* __restrict__ opA, op_t* __restrict__ opB, int B, int N, int incoming, float eps) {
+  __shared__ __attribute__((aligned(16))) op_t lds[2][2][32 * LDSW];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
   const long NN = (long)N * N;
   const long pos0 = ((long)blockIdx.x * 4 + wid) * 32;
@@ -56,7 +57,7 @@ __global__ __launch_bounds__(256) void tm_proj_kernel(
 
   int b = 0, orow = 0, ocol0 = 0;
   float maskv = 0.f;
-  bf16x8 xf[8];
+  opx8 xf[8];
   if (active) {
     b = (int)(pos0 / NN);
     const long t0 = pos0 - (long)b * NN;
@@ -75,8 +76,8 @@ __global__ __launch_bounds__(256) void tm_proj_kernel(
   blk32_load(w_p, tid, rp);
   blk32_load(w_g, tid, rg);
   for (int cb = 0; cb < 8; ++cb) {
-    bf16* lp = lds[cb & 1][0];
-    bf16* lg = lds[cb & 1][1];
+    op_t* lp = lds[cb & 1][0];
+    op_t* lg = lds[cb & 1][1];
     blk32_store(lp, tid, rp);
     blk32_store(lg, tid, rg);
     __syncthreads();
@@ -88,18 +89,18 @@ __global__ __launch_bounds__(256) void tm_proj_kernel(
       f32x16 ap = zero16(), ag = zero16();
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const bf16x8 wp = ld_bf16x8(lp + m * LDSW + 16 * s + 8 * h);
-        const bf16x8 wg = ld_bf16x8(lg + m * LDSW + 16 * s + 8 * h);
+        const opx8 wp = ld_x8(lp + m * LDSW + 16 * s + 8 * h);
+        const opx8 wg = ld_x8(lg + m * LDSW + 16 * s + 8 * h);
         ap = mfma32(wp, xf[s], ap);   // rows = output channel, cols = position
         ag = mfma32(wg, xf[s], ag);
       }
-      bf16* dst = cb < 4 ? opA : opB;
+      op_t* dst = cb < 4 ? opA : opB;
       const int chb = 32 * (cb & 3);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int ch = chb + acc_row(r, h);
         const float v = ap[r] * sigmoidf_fast(ag[r]) * maskv;
-        dst[(((long)b * C + ch) * N + orow) * N + ocol0 + m] = (bf16)v;
+        dst[(((long)b * C + ch) * N + orow) * N + ocol0 + m] = (op_t)v;
       }
     }
   }
@@ -112,10 +113,10 @@ constexpr int BM = 128, BN = 128, BK = 64, LDK = BK + 8;
 
 template <typename OutT>
 __global__ __launch_bounds__(256) void tm_contract_kernel(
-    const bf16* __restrict__ A, const bf16* __restrict__ Bop, OutT* __restrict__ X,
-    int N, int tpd, int total) {
-  __shared__ __attribute__((aligned(16))) bf16 sA[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 sB[2][BN * LDK];
+    const op_t* __restrict__ A, const op_t* __restrict__ Bop, OutT* __restrict__ X,
+    int N, int tpd, int total, float out_scale) {
+  __shared__ __attribute__((aligned(16))) op_t sA[2][BM * LDK];
+  __shared__ __attribute__((aligned(16))) op_t sB[2][BN * LDK];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
   const int wm = wid >> 1, wn = wid & 1;
   const int w = xcd_remap(blockIdx.x, total);
@@ -124,13 +125,13 @@ __global__ __launch_bounds__(256) void tm_contract_kernel(
   const int t = w - (int)plane * tiles;
   const int i0 = (t / tpd) * BM, j0 = (t % tpd) * BN;
   const long NN = (long)N * N;
-  const bf16* Ap = A + plane * NN;
-  const bf16* Bp = Bop + plane * NN;
+  const op_t* Ap = A + plane * NN;
+  const op_t* Bp = Bop + plane * NN;
 
   // global -> register staging: rows (tid >> 3) + 32*q, 16-byte chunk (tid & 7)
   const int lrow = tid >> 3, lcol = (tid & 7) * 8;
-  const bf16* ga[4];
-  const bf16* gb[4];
+  const op_t* ga[4];
+  const op_t* gb[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int ra = min(i0 + lrow + 32 * q, N - 1);
@@ -138,9 +139,9 @@ __global__ __launch_bounds__(256) void tm_contract_kernel(
     ga[q] = Ap + (long)ra * N + lcol;
     gb[q] = Bp + (long)rb * N + lcol;
   }
-  bf16x8 ra_[4], rb_[4];
+  opx8 ra_[4], rb_[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) { ra_[q] = ld_bf16x8(ga[q]); rb_[q] = ld_bf16x8(gb[q]); }
+  for (int q = 0; q < 4; ++q) { ra_[q] = ld_x8(ga[q]); rb_[q] = ld_x8(gb[q]); }
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -150,26 +151,26 @@ __global__ __launch_bounds__(256) void tm_contract_kernel(
 
   const int nk = N / BK;
   for (int kt = 0; kt < nk; ++kt) {
-    bf16* la = sA[kt & 1];
-    bf16* lb = sB[kt & 1];
+    op_t* la = sA[kt & 1];
+    op_t* lb = sB[kt & 1];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      *reinterpret_cast<bf16x8*>(la + (lrow + 32 * q) * LDK + lcol) = ra_[q];
-      *reinterpret_cast<bf16x8*>(lb + (lrow + 32 * q) * LDK + lcol) = rb_[q];
+      st_x8(la + (lrow + 32 * q) * LDK + lcol, ra_[q]);
+      st_x8(lb + (lrow + 32 * q) * LDK + lcol, rb_[q]);
     }
     __syncthreads();
     if (kt + 1 < nk) {
       const int ko = (kt + 1) * BK;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) { ra_[q] = ld_bf16x8(ga[q] + ko); rb_[q] = ld_bf16x8(gb[q] + ko); }
+      for (int q = 0; q < 4; ++q) { ra_[q] = ld_x8(ga[q] + ko); rb_[q] = ld_x8(gb[q] + ko); }
     }
 #pragma unroll
     for (int s = 0; s < BK / 16; ++s) {
-      bf16x8 fa[2], fb[2];
+      opx8 fa[2], fb[2];
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
-        fa[x] = ld_bf16x8(la + (wm * 64 + 32 * x + m) * LDK + 16 * s + 8 * h);
-        fb[x] = ld_bf16x8(lb + (wn * 64 + 32 * x + m) * LDK + 16 * s + 8 * h);
+        fa[x] = ld_x8(la + (wm * 64 + 32 * x + m) * LDK + 16 * s + 8 * h);
+        fb[x] = ld_x8(lb + (wn * 64 + 32 * x + m) * LDK + 16 * s + 8 * h);
       }
 #pragma unroll
       for (int a = 0; a < 2; ++a)
@@ -187,7 +188,7 @@ __global__ __launch_bounds__(256) void tm_contract_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int i = i0 + wm * 64 + 32 * a + acc_row(r, h);
-        if (i < N && j < N) Xp[(long)i * N + j] = (OutT)acc[a][c][r];
+        if (i < N && j < N) Xp[(long)i * N + j] = (OutT)(acc[a][c][r] * out_scale);
       }
     }
 }
@@ -198,19 +199,19 @@ __global__ __launch_bounds__(256) void tm_contract_kernel(
 // ---------------------------------------------------------------------------------
 template <typename XT>
 __global__ __launch_bounds__(256) void tm_out_kernel(
-    const XT* __restrict__ X, const float* z_in, float* out,
+    const XT* __restrict__ X, float x_scale, const float* z_in, float* out,
     const float* __restrict__ lni_w, const float* __restrict__ lni_b,
     const float* __restrict__ lno_w, const float* __restrict__ lno_b,
-    const bf16* __restrict__ w_pout, const bf16* __restrict__ w_gout,
+    const op_t* __restrict__ w_pout, const op_t* __restrict__ w_gout,
     int B, int N, int accumulate, float eps) {
-  __shared__ __attribute__((aligned(16))) bf16 sW[2][C * LDSW];
+  __shared__ __attribute__((aligned(16))) op_t sW[2][C * LDSW];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
-    const int c = tid + 256 * q;   // 2048 chunks of 8 bf16 per matrix
+    const int c = tid + 256 * q;   // 2048 chunks of 8 elements per matrix
     const int row = c >> 4, col = (c & 15) * 8;
-    *reinterpret_cast<bf16x8*>(&sW[0][row * LDSW + col]) = ld_bf16x8(w_pout + row * C + col);
-    *reinterpret_cast<bf16x8*>(&sW[1][row * LDSW + col]) = ld_bf16x8(w_gout + row * C + col);
+    st_x8(&sW[0][row * LDSW + col], ld_x8(w_pout + row * C + col));
+    st_x8(&sW[1][row * LDSW + col], ld_x8(w_gout + row * C + col));
   }
   __syncthreads();
 
@@ -223,13 +224,13 @@ __global__ __launch_bounds__(256) void tm_out_kernel(
   const int j0 = (int)(t0 - (long)i * N);
 
   float x[64];
-  bf16x8 xo[8], xi[8];
+  opx8 xo[8], xi[8];
   {
     const XT* Xp = X + (long)b * C * NN + (long)i * N + j0 + m;
 #pragma unroll
     for (int s = 0; s < 8; ++s)
 #pragma unroll
-      for (int t = 0; t < 8; ++t) x[8 * s + t] = (float)Xp[(long)(16 * s + 8 * h + t) * NN];
+      for (int t = 0; t < 8; ++t) x[8 * s + t] = (float)Xp[(long)(16 * s + 8 * h + t) * NN] * x_scale;
     ln128_to_frag(x, h, lno_w, lno_b, eps, xo);
   }
   const long pbase = (long)b * NN + (long)i * N + j0;   // pair index of position 0
@@ -241,8 +242,8 @@ __global__ __launch_bounds__(256) void tm_out_kernel(
     f32x16 ap = zero16(), ag = zero16();
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const bf16x8 wp = ld_bf16x8(&sW[0][(32 * ob + m) * LDSW + 16 * s + 8 * h]);
-      const bf16x8 wg = ld_bf16x8(&sW[1][(32 * ob + m) * LDSW + 16 * s + 8 * h]);
+      const opx8 wp = ld_x8(&sW[0][(32 * ob + m) * LDSW + 16 * s + 8 * h]);
+      const opx8 wg = ld_x8(&sW[1][(32 * ob + m) * LDSW + 16 * s + 8 * h]);
       ap = mfma32(xo[s], wp, ap);   // rows = pair, cols = output channel
       ag = mfma32(xi[s], wg, ag);
     }
@@ -263,7 +264,7 @@ __global__ __launch_bounds__(256) void tm_out_kernel(
 extern "C" size_t pf_trimul_workspace_size(int B, int N, int C_) {
   if (B <= 0 || N <= 0 || C_ != C) return 0;
   const size_t planes = (size_t)B * C * N * N;
-  return planes * (2 * sizeof(bf16) + sizeof(float));
+  return planes * 3 * sizeof(op_t);   // opA, opB, X
 }
 
 extern "C" int pf_trimul_fwd(const pf_trimul_args* a) {
@@ -284,41 +285,43 @@ extern "C" int pf_trimul_fwd(const pf_trimul_args* a) {
   hipStream_t st = (hipStream_t)a->stream;
   const int B = a->B, N = a->N;
   const size_t planes = (size_t)B * C * N * N;
-  bf16* opA = (bf16*)a->workspace;
-  bf16* opB = opA + planes;
-  float* X = (float*)(opB + planes);
-  const bf16* w_pin = (const bf16*)a->p_in_w;
-  const bf16* w_gin = (const bf16*)a->g_in_w;
+  op_t* opA = (op_t*)a->workspace;
+  op_t* opB = opA + planes;
+  op_t* X = opB + planes;
 
   const long positions = (long)B * N * N;
   const int grid_proj = (int)((positions / 32 + 3) / 4);
   tm_proj_kernel<<<grid_proj, 256, 0, st>>>(a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b,
-                                            w_pin, w_gin, opA, opB, B, N, a->direction, a->eps);
+                                            (const op_t*)a->p_in_w, (const op_t*)a->g_in_w, opA, opB, B, N,
+                                            a->direction, a->eps);
   PF_CHECK_LAUNCH("tm_proj_kernel");
 
   const int tpd = (N + BM - 1) / BM;
   const int total = B * C * tpd * tpd;
-  tm_contract_kernel<float><<<total, 256, 0, st>>>(opA, opB, X, N, tpd, total);
+  tm_contract_kernel<op_t><<<total, 256, 0, st>>>(opA, opB, X, N, tpd, total, X_STORE_SCALE);
   PF_CHECK_LAUNCH("tm_contract_kernel");
 
-  tm_out_kernel<float><<<grid_proj, 256, 0, st>>>(X, a->z_in, a->out, a->norm_in_w, a->norm_in_b,
-                                                  a->norm_out_w, a->norm_out_b,
-                                                  (const bf16*)a->p_out_w, (const bf16*)a->g_out_w,
-                                                  B, N, a->accumulate, a->eps);
+  tm_out_kernel<op_t><<<grid_proj, 256, 0, st>>>(X, X_LOAD_SCALE, a->z_in, a->out, a->norm_in_w, a->norm_in_b,
+                                                 a->norm_out_w, a->norm_out_b, (const op_t*)a->p_out_w,
+                                                 (const op_t*)a->g_out_w, B, N, a->accumulate, a->eps);
   PF_CHECK_LAUNCH("tm_out_kernel");
   return PF_OK;
 }
 
 // Standalone contraction (the MFMA hot loop alone), for measurement and tests.
-extern "C" int pf_trimul_contract(const void* opA, const void* opB, float* X, int planes, int N,
+extern "C" int pf_trimul_contract(const void* opA, const void* opB, void* X, int x_fp32, int planes, int N,
                                   void* stream) {
   if (!opA || !opB || !X) return pf_fail(PF_E_INVALID, "pf_trimul_contract: null pointer");
   if (planes <= 0 || N <= 0 || N % 64)
     return pf_fail(PF_E_INVALID, "pf_trimul_contract: need planes > 0 and N a multiple of 64");
   const int tpd = (N + BM - 1) / BM;
   const int total = planes * tpd * tpd;
-  tm_contract_kernel<float><<<total, 256, 0, (hipStream_t)stream>>>(
-      (const bf16*)opA, (const bf16*)opB, X, N, tpd, total);
+  if (x_fp32)
+    tm_contract_kernel<float><<<total, 256, 0, (hipStream_t)stream>>>(
+        (const op_t*)opA, (const op_t*)opB, (float*)X, N, tpd, total, 1.f);
+  else
+    tm_contract_kernel<op_t><<<total, 256, 0, (hipStream_t)stream>>>(
+        (const op_t*)opA, (const op_t*)opB, (op_t*)X, N, tpd, total, X_STORE_SCALE);
   PF_CHECK_LAUNCH("tm_contract_kernel");
   return PF_OK;
 }

@@ -1,14 +1,19 @@
 """Operator-level API: the Pairformer hot-path ops on PyTorch-ROCm device tensors.
 
 Each public function mirrors a reference operator (same argument names and
-meaning) and runs the HIP kernels of ``libpairformer_hip.so`` through the C ABI.
+meaning) and runs the HIP kernels of ``libpairformer_hip`` through the C ABI.
 Tensors must live on a ROCm GPU; there is no CPU path.  Token counts that are not
-a multiple of 64 are zero-padded (and masked) internally and sliced back, like the
-reference's Tenstorrent boundary does (``tt_bio/tenstorrent.py:2235-2246``).
+a multiple of 64 are zero-padded internally (padding excluded from every softmax
+and masked out of every contraction) and sliced back, like the reference's
+Tenstorrent boundary pads (``tt_bio/tenstorrent.py:2235-2246``).
+
+``variant`` selects the MFMA operand type: ``"fp16"`` (default, IEEE binary16)
+or ``"bf16"``.  Accumulation and every statistic are fp32 in both.
 
 The ``launch_*`` functions are the thin layer the modules use: they take
-already-padded contiguous device tensors and pre-converted weights (bf16 matrices,
-fp32 LayerNorm parameters) and enqueue work on the current stream.
+already-padded contiguous device tensors and pre-converted weights (operand-type
+matrices, fp32 LayerNorm parameters and biases) and enqueue work on the current
+stream.
 """
 from __future__ import annotations
 
@@ -21,6 +26,8 @@ from . import _lib
 
 PAD = 64
 C_Z = 128
+DEFAULT_VARIANT = _lib.DEFAULT_VARIANT
+TORCH_DTYPE = {"fp16": torch.float16, "bf16": torch.bfloat16}
 
 
 # --------------------------------------------------------------------------------------
@@ -51,12 +58,23 @@ def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
 
 
-def bf16(w: torch.Tensor, device: torch.device) -> torch.Tensor:
-    return w.detach().to(device=device, dtype=torch.bfloat16).contiguous()
+def opw(w: torch.Tensor, device: torch.device, variant: str = DEFAULT_VARIANT) -> torch.Tensor:
+    """A weight matrix in the MFMA operand type of ``variant``."""
+    return w.detach().to(device=device, dtype=TORCH_DTYPE[variant]).contiguous()
 
 
 def f32(t: Optional[torch.Tensor], device: torch.device) -> Optional[torch.Tensor]:
     return None if t is None else t.detach().to(device=device, dtype=torch.float32).contiguous()
+
+
+def convert_weights(w: Mapping[str, torch.Tensor], device: torch.device, variant: str = DEFAULT_VARIANT,
+                    strip: str = "") -> dict:
+    """1-D tensors (LayerNorm params, biases) -> fp32; matrices -> operand type."""
+    out = {}
+    for k, v in w.items():
+        kk = k[len(strip):] if strip and k.startswith(strip) else k
+        out[kk] = f32(v, device) if v.dim() == 1 else opw(v, device, variant)
+    return out
 
 
 def padded_len(n: int) -> int:
@@ -64,7 +82,7 @@ def padded_len(n: int) -> int:
 
 
 def pad_pair(z: torch.Tensor, n_pad: int) -> torch.Tensor:
-    """Zero-pad [B,N,N,C] to [B,n_pad,n_pad,C] (always returns a new contiguous tensor)."""
+    """Zero-pad [B,N,N,C] to [B,n_pad,n_pad,C] (always returns a new contiguous fp32 tensor)."""
     B, N, _, C = z.shape
     out = torch.zeros((B, n_pad, n_pad, C), dtype=torch.float32, device=z.device)
     out[:, :N, :N] = z
@@ -84,13 +102,13 @@ def pad_pair_mask(pair_mask: Optional[torch.Tensor], B: int, N: int, n_pad: int,
 # --------------------------------------------------------------------------------------
 # launchers (padded, contiguous, device-resident inputs; weights pre-converted)
 # --------------------------------------------------------------------------------------
-def trimul_workspace_bytes(B: int, N: int) -> int:
-    return _lib.load().pf_trimul_workspace_size(B, N, C_Z)
+def trimul_workspace_bytes(B: int, N: int, variant: str = DEFAULT_VARIANT) -> int:
+    return _lib.load(variant).pf_trimul_workspace_size(B, N, C_Z)
 
 
 def launch_trimul(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional[torch.Tensor],
                   w: Mapping[str, torch.Tensor], direction: int, ws: torch.Tensor,
-                  accumulate: bool, eps: float = 1e-5) -> None:
+                  accumulate: bool, eps: float = 1e-5, variant: str = DEFAULT_VARIANT) -> None:
     B, N, _, C = z_in.shape
     a = _lib.TrimulArgs(
         B=B, N=N, C=C, hidden=w["p_in.weight"].shape[0] // 2, direction=direction,
@@ -100,33 +118,35 @@ def launch_trimul(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional[tor
         norm_out_w=_ptr(w["norm_out.weight"]), norm_out_b=_ptr(w["norm_out.bias"]),
         p_out_w=_ptr(w["p_out.weight"]), g_out_w=_ptr(w["g_out.weight"]),
         workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
-    _lib.check(_lib.load().pf_trimul_fwd(ctypes.byref(a)), "pf_trimul_fwd")
+    _lib.check(_lib.load(variant).pf_trimul_fwd(ctypes.byref(a)), "pf_trimul_fwd", variant)
 
 
-def triatt_workspace_bytes(B: int, N: int, H: int = 4, D: int = 32) -> int:
-    return _lib.load().pf_triatt_workspace_size(B, N, C_Z, H, D)
+def triatt_workspace_bytes(B: int, N: int, H: int = 4, D: int = 32, variant: str = DEFAULT_VARIANT) -> int:
+    return _lib.load(variant).pf_triatt_workspace_size(B, N, C_Z, H, D)
 
 
 def launch_triatt(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional[torch.Tensor],
                   w: Mapping[str, torch.Tensor], ending: bool, ws: torch.Tensor, accumulate: bool,
-                  n_heads: int = 4, head_dim: int = 32, eps: float = 1e-5) -> None:
+                  n_heads: int = 4, head_dim: int = 32, eps: float = 1e-5, n_valid: int = 0,
+                  variant: str = DEFAULT_VARIANT) -> None:
     B, N, _, C = z_in.shape
     a = _lib.TriattArgs(
-        B=B, N=N, C=C, H=n_heads, D=head_dim, ending=int(ending), accumulate=int(accumulate), eps=eps,
-        z_in=_ptr(z_in), out=_ptr(out), pair_mask=_ptr(pair_mask),
+        B=B, N=N, C=C, H=n_heads, D=head_dim, ending=int(ending), accumulate=int(accumulate), n_valid=n_valid,
+        eps=eps, z_in=_ptr(z_in), out=_ptr(out), pair_mask=_ptr(pair_mask),
         ln_w=_ptr(w["layer_norm.weight"]), ln_b=_ptr(w["layer_norm.bias"]), w_bias=_ptr(w["linear.weight"]),
         w_q=_ptr(w["linear_q.weight"]), w_k=_ptr(w["linear_k.weight"]), w_v=_ptr(w["linear_v.weight"]),
         w_g=_ptr(w["linear_g.weight"]), w_o=_ptr(w["linear_o.weight"]),
         workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
-    _lib.check(_lib.load().pf_triatt_fwd(ctypes.byref(a)), "pf_triatt_fwd")
+    _lib.check(_lib.load(variant).pf_triatt_fwd(ctypes.byref(a)), "pf_triatt_fwd", variant)
 
 
-def transition_workspace_bytes(rows: int, C: int, hidden: int) -> int:
-    return _lib.load().pf_transition_workspace_size(rows, C, hidden)
+def transition_workspace_bytes(rows: int, C: int, hidden: int, variant: str = DEFAULT_VARIANT) -> int:
+    return _lib.load(variant).pf_transition_workspace_size(rows, C, hidden)
 
 
 def launch_transition(x_in: torch.Tensor, out: torch.Tensor, w: Mapping[str, torch.Tensor],
-                      ws: Optional[torch.Tensor], accumulate: bool, eps: float = 1e-5) -> None:
+                      ws: Optional[torch.Tensor], accumulate: bool, eps: float = 1e-5,
+                      variant: str = DEFAULT_VARIANT) -> None:
     C = x_in.shape[-1]
     rows = x_in.numel() // C
     a = _lib.TransitionArgs(
@@ -134,52 +154,56 @@ def launch_transition(x_in: torch.Tensor, out: torch.Tensor, w: Mapping[str, tor
         x_in=_ptr(x_in), out=_ptr(out), norm_w=_ptr(w["norm.weight"]), norm_b=_ptr(w["norm.bias"]),
         fc1_w=_ptr(w["fc1.weight"]), fc2_w=_ptr(w["fc2.weight"]), fc3_w=_ptr(w["fc3.weight"]),
         workspace=_ptr(ws), workspace_bytes=0 if ws is None else ws.numel(), stream=_stream())
-    _lib.check(_lib.load().pf_transition_fwd(ctypes.byref(a)), "pf_transition_fwd")
+    _lib.check(_lib.load(variant).pf_transition_fwd(ctypes.byref(a)), "pf_transition_fwd", variant)
 
 
-def apb_workspace_bytes(B: int, N: int, c_s: int, H: int) -> int:
-    return _lib.load().pf_apb_workspace_size(B, N, c_s, H)
+def apb_workspace_bytes(B: int, N: int, c_s: int, H: int, variant: str = DEFAULT_VARIANT) -> int:
+    return _lib.load(variant).pf_apb_workspace_size(B, N, c_s, H)
 
 
 def launch_apb(s: torch.Tensor, k_in: torch.Tensor, z: torch.Tensor, mask: Optional[torch.Tensor],
                out: torch.Tensor, w: Mapping[str, torch.Tensor], n_heads: int, ws: torch.Tensor,
-               accumulate: bool, eps: float = 1e-5) -> None:
+               accumulate: bool, eps: float = 1e-5, n_valid: int = 0, variant: str = DEFAULT_VARIANT) -> None:
     B, N, c_s = s.shape
     a = _lib.ApbArgs(
-        B=B, N=N, c_s=c_s, C=z.shape[-1], H=n_heads, accumulate=int(accumulate), eps=eps,
+        B=B, N=N, c_s=c_s, C=z.shape[-1], H=n_heads, accumulate=int(accumulate), n_valid=n_valid, eps=eps,
         s=_ptr(s), k_in=_ptr(k_in), z=_ptr(z), mask=_ptr(mask), out=_ptr(out),
         w_q=_ptr(w["proj_q.weight"]), b_q=_ptr(w["proj_q.bias"]), w_k=_ptr(w["proj_k.weight"]),
         w_v=_ptr(w["proj_v.weight"]), w_g=_ptr(w["proj_g.weight"]), w_o=_ptr(w["proj_o.weight"]),
         zln_w=_ptr(w["proj_z.0.weight"]), zln_b=_ptr(w["proj_z.0.bias"]), w_z=_ptr(w["proj_z.1.weight"]),
         workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
-    _lib.check(_lib.load().pf_apb_fwd(ctypes.byref(a)), "pf_apb_fwd")
+    _lib.check(_lib.load(variant).pf_apb_fwd(ctypes.byref(a)), "pf_apb_fwd", variant)
 
 
 def launch_layernorm(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, out: torch.Tensor,
-                     eps: float = 1e-5) -> None:
+                     eps: float = 1e-5, variant: str = DEFAULT_VARIANT) -> None:
     C = x.shape[-1]
-    _lib.check(_lib.load().pf_layernorm_fwd(_ptr(x), _ptr(w), _ptr(b), _ptr(out), x.numel() // C, C, eps,
-                                            _stream()), "pf_layernorm_fwd")
+    _lib.check(_lib.load(variant).pf_layernorm_fwd(_ptr(x), _ptr(w), _ptr(b), _ptr(out), x.numel() // C, C, eps,
+                                                   _stream()), "pf_layernorm_fwd", variant)
 
 
 def launch_linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor],
-                  resid: Optional[torch.Tensor], out: torch.Tensor) -> None:
+                  resid: Optional[torch.Tensor], out: torch.Tensor, variant: str = DEFAULT_VARIANT) -> None:
     K = x.shape[-1]
-    _lib.check(_lib.load().pf_linear_fwd(_ptr(x), _ptr(w), _ptr(bias), _ptr(resid), _ptr(out), x.numel() // K,
-                                         K, w.shape[0], _stream()), "pf_linear_fwd")
+    _lib.check(_lib.load(variant).pf_linear_fwd(_ptr(x), _ptr(w), _ptr(bias), _ptr(resid), _ptr(out),
+                                                x.numel() // K, K, w.shape[0], _stream()), "pf_linear_fwd", variant)
 
 
 def launch_pair_ln_linear(x: torch.Tensor, base: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor,
-                          w: torch.Tensor, out: torch.Tensor, eps: float = 1e-5) -> None:
+                          w: torch.Tensor, out: torch.Tensor, eps: float = 1e-5,
+                          variant: str = DEFAULT_VARIANT) -> None:
     C = x.shape[-1]
-    _lib.check(_lib.load().pf_pair_ln_linear_fwd(_ptr(x), _ptr(base), _ptr(ln_w), _ptr(ln_b), _ptr(w), _ptr(out),
-                                                 x.numel() // C, C, eps, _stream()), "pf_pair_ln_linear_fwd")
+    _lib.check(_lib.load(variant).pf_pair_ln_linear_fwd(_ptr(x), _ptr(base), _ptr(ln_w), _ptr(ln_b), _ptr(w),
+                                                        _ptr(out), x.numel() // C, C, eps, _stream()),
+               "pf_pair_ln_linear_fwd", variant)
 
 
-def launch_trimul_contract(opA: torch.Tensor, opB: torch.Tensor, X: torch.Tensor) -> None:
+def launch_trimul_contract(opA: torch.Tensor, opB: torch.Tensor, X: torch.Tensor,
+                           variant: str = DEFAULT_VARIANT) -> None:
+    """X fp32 -> unscaled fp32 output; X in the operand dtype -> 2^-8-scaled (pf_trimul_fwd's format)."""
     planes, N = opA.shape[0], opA.shape[1]
-    _lib.check(_lib.load().pf_trimul_contract(_ptr(opA), _ptr(opB), _ptr(X), planes, N, _stream()),
-               "pf_trimul_contract")
+    _lib.check(_lib.load(variant).pf_trimul_contract(_ptr(opA), _ptr(opB), _ptr(X), int(X.dtype == torch.float32),
+                                                     planes, N, _stream()), "pf_trimul_contract", variant)
 
 
 # --------------------------------------------------------------------------------------
@@ -193,7 +217,8 @@ def triangle_multiplicative_update(x: torch.Tensor, direction: str = "outgoing",
                                    mask: Optional[torch.Tensor] = None,
                                    norm_in_weight=None, norm_in_bias=None, p_in_weight=None,
                                    g_in_weight=None, norm_out_weight=None, norm_out_bias=None,
-                                   p_out_weight=None, g_out_weight=None, eps: float = 1e-5) -> torch.Tensor:
+                                   p_out_weight=None, g_out_weight=None, eps: float = 1e-5,
+                                   variant: str = DEFAULT_VARIANT) -> torch.Tensor:
     """Fused triangle multiplicative update; the contract of
     ``kernel_triangular_mult`` (``tt_bio/boltz2.py:820-848``) with the semantics of
     ``TriangleMultiplication{Outgoing,Incoming}.forward(use_kernels=False)``
@@ -206,19 +231,21 @@ def triangle_multiplicative_update(x: torch.Tensor, direction: str = "outgoing",
     n_pad = padded_len(N)
     zp = pad_pair(x.to(torch.float32), n_pad) if n_pad != N else x.to(torch.float32).contiguous()
     mp = pad_pair_mask(None if mask is None else (mask.unsqueeze(0) if mask.dim() == 2 else mask), B, N, n_pad, dev)
-    w = {"norm_in.weight": f32(norm_in_weight, dev), "norm_in.bias": f32(norm_in_bias, dev),
-         "p_in.weight": bf16(p_in_weight, dev), "g_in.weight": bf16(g_in_weight, dev),
-         "norm_out.weight": f32(norm_out_weight, dev), "norm_out.bias": f32(norm_out_bias, dev),
-         "p_out.weight": bf16(p_out_weight, dev), "g_out.weight": bf16(g_out_weight, dev)}
+    w = convert_weights({"norm_in.weight": norm_in_weight, "norm_in.bias": norm_in_bias,
+                         "p_in.weight": p_in_weight, "g_in.weight": g_in_weight,
+                         "norm_out.weight": norm_out_weight, "norm_out.bias": norm_out_bias,
+                         "p_out.weight": p_out_weight, "g_out.weight": g_out_weight}, dev, variant)
     out = torch.empty_like(zp)
-    ws = workspace(trimul_workspace_bytes(B, n_pad), dev)
-    launch_trimul(zp, out, mp, w, 0 if direction == "outgoing" else 1, ws, accumulate=False, eps=eps)
+    ws = workspace(trimul_workspace_bytes(B, n_pad, variant), dev)
+    launch_trimul(zp, out, mp, w, 0 if direction == "outgoing" else 1, ws, accumulate=False, eps=eps,
+                  variant=variant)
     out = out[:, :N, :N] if n_pad != N else out
     return out[0] if squeezed else out
 
 
 def triangle_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bias: torch.Tensor,
-                       mask: Optional[torch.Tensor] = None, scale: Optional[float] = None) -> torch.Tensor:
+                       mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+                       variant: str = DEFAULT_VARIANT) -> torch.Tensor:
     """Triangle attention core; the contract of ``kernel_triangular_attn(q, k, v,
     tri_bias, mask, scale)`` (``tt_bio/boltz2.py:815-817``) with the semantics of the
     ``use_kernels=False`` path (``tt_bio/reference.py:176-190``, ``boltz2.py:790-810``).
@@ -251,31 +278,30 @@ def triangle_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bias: 
         mp = torch.zeros((B, n_pad, n_pad), dtype=torch.float32, device=dev)
         mp[:, :N, :N] = 1.0 if mask is None else mask.reshape(B, N, N).to(torch.float32)
     o = torch.empty((B, n_pad, H, n_pad, D), dtype=torch.float32, device=dev)
-    nbytes = _lib.load().pf_tri_attention_workspace_size(B, n_pad, H, D)
-    ws = workspace(nbytes, dev)
-    _lib.check(_lib.load().pf_tri_attention(_ptr(qp), _ptr(kp), _ptr(vp), _ptr(bp), _ptr(mp), float(scale), _ptr(o),
-                                            B, n_pad, H, D, _ptr(ws), ws.numel(), _stream()), "pf_tri_attention")
+    lib = _lib.load(variant)
+    ws = workspace(lib.pf_tri_attention_workspace_size(B, n_pad, H, D), dev)
+    _lib.check(lib.pf_tri_attention(_ptr(qp), _ptr(kp), _ptr(vp), _ptr(bp), _ptr(mp), float(scale), _ptr(o),
+                                    B, n_pad, H, D, N, _ptr(ws), ws.numel(), _stream()), "pf_tri_attention", variant)
     return o[:, :N, :, :N] if n_pad != N else o
 
 
 def transition(x: torch.Tensor, norm_weight, norm_bias, fc1_weight, fc2_weight, fc3_weight,
-               eps: float = 1e-5) -> torch.Tensor:
+               eps: float = 1e-5, variant: str = DEFAULT_VARIANT) -> torch.Tensor:
     """``Transition.forward`` (``tt_bio/boltz2.py:1227-1258``): returns fc3(silu(fc1 LN x) * fc2 LN x)."""
     dev = _require_gpu(x)
     xin = x.to(torch.float32).contiguous()
-    w = {"norm.weight": f32(norm_weight, dev), "norm.bias": f32(norm_bias, dev),
-         "fc1.weight": bf16(fc1_weight, dev), "fc2.weight": bf16(fc2_weight, dev),
-         "fc3.weight": bf16(fc3_weight, dev)}
+    w = convert_weights({"norm.weight": norm_weight, "norm.bias": norm_bias, "fc1.weight": fc1_weight,
+                         "fc2.weight": fc2_weight, "fc3.weight": fc3_weight}, dev, variant)
     C = xin.shape[-1]
     out = torch.empty_like(xin)
-    nb = transition_workspace_bytes(xin.numel() // C, C, fc1_weight.shape[0])
-    launch_transition(xin, out, w, workspace(nb, dev) if nb else None, accumulate=False, eps=eps)
+    nb = transition_workspace_bytes(xin.numel() // C, C, fc1_weight.shape[0], variant)
+    launch_transition(xin, out, w, workspace(nb, dev) if nb else None, accumulate=False, eps=eps, variant=variant)
     return out
 
 
 def attention_pair_bias(s: torch.Tensor, z: torch.Tensor, mask: Optional[torch.Tensor], k_in: torch.Tensor,
                         weights: Mapping[str, torch.Tensor], num_heads: int = 16,
-                        eps: float = 1e-5) -> torch.Tensor:
+                        eps: float = 1e-5, variant: str = DEFAULT_VARIANT) -> torch.Tensor:
     """``AttentionPairBias.forward`` (``tt_bio/boltz2.py:343-367``, multiplicity 1).
     ``weights`` uses the module's state-dict keys (``proj_q.weight`` ...)."""
     dev = _require_gpu(s, z, k_in)
@@ -288,10 +314,10 @@ def attention_pair_bias(s: torch.Tensor, z: torch.Tensor, mask: Optional[torch.T
     zp = pad_pair(z.to(torch.float32), n_pad) if n_pad != N else z.to(torch.float32).contiguous()
     mp = torch.zeros((B, n_pad), dtype=torch.float32, device=dev)
     mp[:, :N] = 1.0 if mask is None else mask.to(torch.float32)
-    w = {k: (f32(v, dev) if (v.dim() == 1) else bf16(v, dev)) for k, v in weights.items()}
+    w = convert_weights(weights, dev, variant)
     out = torch.empty_like(sp)
-    ws = workspace(apb_workspace_bytes(B, n_pad, c_s, num_heads), dev)
-    launch_apb(sp, kp, zp, mp, out, w, num_heads, ws, accumulate=False, eps=eps)
+    ws = workspace(apb_workspace_bytes(B, n_pad, c_s, num_heads, variant), dev)
+    launch_apb(sp, kp, zp, mp, out, w, num_heads, ws, accumulate=False, eps=eps, n_valid=N, variant=variant)
     return out[:, :N]
 
 
@@ -303,9 +329,10 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: f
     return out
 
 
-def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+           variant: str = DEFAULT_VARIANT) -> torch.Tensor:
     dev = _require_gpu(x)
     xin = x.to(torch.float32).contiguous()
     out = torch.empty(xin.shape[:-1] + (weight.shape[0],), dtype=torch.float32, device=dev)
-    launch_linear(xin, bf16(weight, dev), f32(bias, dev), None, out)
+    launch_linear(xin, opw(weight, dev, variant), f32(bias, dev), None, out, variant)
     return out

@@ -19,7 +19,8 @@ Tenstorrent approximations: the pair mask multiplies both trimul operands
 (``reference.py:461``), triangle attention masks per (row, key) with 1e9
 (``reference.py:334-335``), single attention masks keys with 1e6
 (``boltz2.py:362``), and the pair bias is added unscaled after q/sqrt(d)
-(``reference.py:117-118``).  The residual stream z is kept in fp32.
+(``reference.py:117-118``).  The residual stream z and s are fp32; MFMA operands
+are fp16 by default (``Options(operand="bf16")`` selects bf16 operands).
 """
 from __future__ import annotations
 
@@ -92,10 +93,15 @@ class WeightScope:
 
 
 class Options:
-    """Replaces ttnn's ``compute_kernel_config``: numerics knobs shared by the kernels."""
+    """Replaces ttnn's ``compute_kernel_config``: numerics knobs shared by the kernels.
 
-    def __init__(self, eps: float = 1e-5):
+    ``operand``: MFMA operand type, ``"fp16"`` (default) or ``"bf16"``."""
+
+    def __init__(self, eps: float = 1e-5, operand: str = ops.DEFAULT_VARIANT):
+        if operand not in ops.TORCH_DTYPE:
+            raise ValueError(f"operand must be one of {sorted(ops.TORCH_DTYPE)}, got {operand!r}")
         self.eps = eps
+        self.operand = operand
 
 
 class Module:
@@ -108,11 +114,15 @@ class Module:
         self.options = options or Options()
         self.device = get_device()
 
+    @property
+    def variant(self) -> str:
+        return self.options.operand
+
     def scope(self, scope: str, strip_prefix: str = "") -> WeightScope:
         return self.weights.child(scope, strip_prefix)
 
     def mat(self, key: str) -> torch.Tensor:
-        return ops.bf16(self.weights[key], self.device)
+        return ops.opw(self.weights[key], self.device, self.variant)
 
     def vec(self, key: str) -> torch.Tensor:
         return ops.f32(self.weights[key], self.device)
@@ -129,15 +139,18 @@ class TriangleMultiplication(Module):
         self.w = {k: self.vec(k) for k in ("norm_in.weight", "norm_in.bias", "norm_out.weight", "norm_out.bias")}
         self.w.update({k: self.mat(k) for k in ("p_in.weight", "g_in.weight", "p_out.weight", "g_out.weight")})
 
+    def workspace_bytes(self, B: int, N: int) -> int:
+        return ops.trimul_workspace_bytes(B, N, self.variant)
+
     def __call__(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                  accumulate: bool = False, ws: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x [B,N,N,128] fp32 device, N % 64 == 0.  Returns the update (or ``out`` += update)."""
         B, N = x.shape[0], x.shape[1]
         if ws is None:
-            ws = ops.workspace(ops.trimul_workspace_bytes(B, N), x.device)
+            ws = ops.workspace(self.workspace_bytes(B, N), x.device)
         if out is None:
             out = torch.empty_like(x)
-        ops.launch_trimul(x, out, mask, self.w, int(self.ending), ws, accumulate, self.options.eps)
+        ops.launch_trimul(x, out, mask, self.w, int(self.ending), ws, accumulate, self.options.eps, self.variant)
         return out
 
 
@@ -154,15 +167,19 @@ class TriangleAttention(Module):
         self.w.update({k: self.mat(k) for k in ("linear.weight", "linear_q.weight", "linear_k.weight",
                                                 "linear_v.weight", "linear_g.weight", "linear_o.weight")})
 
+    def workspace_bytes(self, B: int, N: int) -> int:
+        return ops.triatt_workspace_bytes(B, N, self.n_heads, self.head_dim, self.variant)
+
     def __call__(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
-                 accumulate: bool = False, ws: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 accumulate: bool = False, ws: Optional[torch.Tensor] = None, n_valid: int = 0) -> torch.Tensor:
+        """``n_valid``: tokens at or beyond it are boundary padding (0 = none)."""
         B, N = x.shape[0], x.shape[1]
         if ws is None:
-            ws = ops.workspace(ops.triatt_workspace_bytes(B, N), x.device)
+            ws = ops.workspace(self.workspace_bytes(B, N), x.device)
         if out is None:
             out = torch.empty_like(x)
         ops.launch_triatt(x, out, mask, self.w, self.ending, ws, accumulate, self.n_heads, self.head_dim,
-                          self.options.eps)
+                          self.options.eps, n_valid, self.variant)
         return out
 
 
@@ -177,7 +194,7 @@ class Transition(Module):
         self.hidden = self.weights["fc1.weight"].shape[0]
 
     def workspace_bytes(self, rows: int) -> int:
-        return ops.transition_workspace_bytes(rows, self.C, self.hidden)
+        return ops.transition_workspace_bytes(rows, self.C, self.hidden, self.variant)
 
     def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, accumulate: bool = False,
                  ws: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -187,7 +204,7 @@ class Transition(Module):
             ws = ops.workspace(nb, x.device) if nb else None
         if out is None:
             out = torch.empty_like(x)
-        ops.launch_transition(x, out, self.w, ws, accumulate, self.options.eps)
+        ops.launch_transition(x, out, self.w, ws, accumulate, self.options.eps, self.variant)
         return out
 
 
@@ -203,27 +220,27 @@ class AttentionPairBias(Module):
         self.c_s = self.weights["proj_q.weight"].shape[0]
 
     def workspace_bytes(self, B: int, N: int) -> int:
-        return ops.apb_workspace_bytes(B, N, self.c_s, self.n_heads)
+        return ops.apb_workspace_bytes(B, N, self.c_s, self.n_heads, self.variant)
 
     def __call__(self, s: torch.Tensor, z: torch.Tensor, mask: Optional[torch.Tensor] = None,
                  k_in: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None, accumulate: bool = False,
-                 ws: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 ws: Optional[torch.Tensor] = None, n_valid: int = 0) -> torch.Tensor:
         B, N, _ = s.shape
         if ws is None:
             ws = ops.workspace(self.workspace_bytes(B, N), s.device)
         if out is None:
             out = torch.empty_like(s)
         ops.launch_apb(s, s if k_in is None else k_in, z, mask, out, self.w, self.n_heads, ws, accumulate,
-                       self.options.eps)
+                       self.options.eps, n_valid, self.variant)
         return out
 
 
 class PairformerLayer(Module):
     """``tenstorrent.py:949-1046`` / ``reference.py:822-914`` (no-seq: ``1007-1072``).
 
-    ``__call__(s, z, pair_mask, mask, ws)`` updates the device tensors in place:
-    z += TMo; z += TMi; z += TAs; z += TAe; z += Tr_z; then, with ``transform_s``,
-    s += APB(LN(s), z, mask, k_in=LN(s)); s += Tr_s(s).
+    ``__call__(s, z, pair_mask, mask, ws, n_valid)`` updates the device tensors in
+    place: z += TMo; z += TMi; z += TAs; z += TAe; z += Tr_z; then, with
+    ``transform_s``, s += APB(LN(s), z, mask, k_in=LN(s)); s += Tr_s(s).
     """
 
     def __init__(self, tri_att_head_dim: int, tri_att_n_heads: int, att_head_dim: Optional[int],
@@ -231,21 +248,23 @@ class PairformerLayer(Module):
                  affinity: bool = False):
         super().__init__(state_dict, options)
         self.transform_s = transform_s
-        self.triangle_multiplication_start = TriangleMultiplication(False, self.scope("tri_mul_out"), options)
-        self.triangle_multiplication_end = TriangleMultiplication(True, self.scope("tri_mul_in"), options)
+        self.triangle_multiplication_start = TriangleMultiplication(False, self.scope("tri_mul_out"), self.options)
+        self.triangle_multiplication_end = TriangleMultiplication(True, self.scope("tri_mul_in"), self.options)
         self.triangle_attention_start = TriangleAttention(tri_att_head_dim, tri_att_n_heads, False,
-                                                          self.scope("tri_att_start", "mha."), options, affinity)
+                                                          self.scope("tri_att_start", "mha."), self.options, affinity)
         self.triangle_attention_end = TriangleAttention(tri_att_head_dim, tri_att_n_heads, True,
-                                                        self.scope("tri_att_end", "mha."), options, affinity)
-        self.transition_z = Transition(self.scope("transition_z"), options)
+                                                        self.scope("tri_att_end", "mha."), self.options, affinity)
+        self.transition_z = Transition(self.scope("transition_z"), self.options)
         if transform_s:
             self.pre_norm_s_weight = self.vec("pre_norm_s.weight")
             self.pre_norm_s_bias = self.vec("pre_norm_s.bias")
-            self.attention_pair_bias = AttentionPairBias(att_head_dim, att_n_heads, self.scope("attention"), options)
-            self.transition_s = Transition(self.scope("transition_s"), options)
+            self.attention_pair_bias = AttentionPairBias(att_head_dim, att_n_heads, self.scope("attention"),
+                                                         self.options)
+            self.transition_s = Transition(self.scope("transition_s"), self.options)
 
     def workspace_bytes(self, B: int, N: int) -> int:
-        n = max(ops.trimul_workspace_bytes(B, N), ops.triatt_workspace_bytes(B, N))
+        n = max(self.triangle_multiplication_start.workspace_bytes(B, N),
+                self.triangle_attention_start.workspace_bytes(B, N))
         if self.transform_s:
             c_s = self.attention_pair_bias.c_s
             n = max(n, self.attention_pair_bias.workspace_bytes(B, N) + B * N * c_s * 4,
@@ -253,21 +272,23 @@ class PairformerLayer(Module):
         return n
 
     def __call__(self, s: Optional[torch.Tensor], z: torch.Tensor, pair_mask: Optional[torch.Tensor] = None,
-                 mask: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None):
+                 mask: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None, n_valid: int = 0):
         B, N = z.shape[0], z.shape[1]
         if ws is None:
             ws = ops.workspace(self.workspace_bytes(B, N), z.device)
         self.triangle_multiplication_start(z, pair_mask, out=z, accumulate=True, ws=ws)
         self.triangle_multiplication_end(z, pair_mask, out=z, accumulate=True, ws=ws)
-        self.triangle_attention_start(z, pair_mask, out=z, accumulate=True, ws=ws)
-        self.triangle_attention_end(z, pair_mask, out=z, accumulate=True, ws=ws)
+        self.triangle_attention_start(z, pair_mask, out=z, accumulate=True, ws=ws, n_valid=n_valid)
+        self.triangle_attention_end(z, pair_mask, out=z, accumulate=True, ws=ws, n_valid=n_valid)
         self.transition_z(z, out=z, accumulate=True, ws=ws)
         if self.transform_s and s is not None:
             c_s = s.shape[-1]
             s_norm = ws[: B * N * c_s * 4].view(torch.float32).view(B, N, c_s)
-            ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps)
+            ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps,
+                                 self.variant)
             apb_ws = ws[B * N * c_s * 4:]
-            self.attention_pair_bias(s_norm, z, mask, k_in=s_norm, out=s, accumulate=True, ws=apb_ws)
+            self.attention_pair_bias(s_norm, z, mask, k_in=s_norm, out=s, accumulate=True, ws=apb_ws,
+                                     n_valid=n_valid)
             self.transition_s(s, out=s, accumulate=True, ws=ws)
         return s, z
 
@@ -282,7 +303,7 @@ class Pairformer(Module):
         self.transform_s = transform_s
         self.blocks = [
             PairformerLayer(tri_att_head_dim, tri_att_n_heads, att_head_dim, att_n_heads, transform_s,
-                            self.scope(f"layers.{i}"), options, affinity=affinity)
+                            self.scope(f"layers.{i}"), self.options, affinity=affinity)
             for i in range(n_blocks)
         ]
 
@@ -290,11 +311,11 @@ class Pairformer(Module):
         return max((b.workspace_bytes(B, N) for b in self.blocks), default=16)
 
     def __call__(self, s: Optional[torch.Tensor], z: torch.Tensor, pair_mask: Optional[torch.Tensor] = None,
-                 mask: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None):
+                 mask: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None, n_valid: int = 0):
         if ws is None:
             ws = ops.workspace(self.workspace_bytes(z.shape[0], z.shape[1]), z.device)
         for block in self.blocks:
-            s, z = block(s, z, pair_mask, mask, ws)
+            s, z = block(s, z, pair_mask, mask, ws, n_valid)
         return s, z
 
 
@@ -304,7 +325,8 @@ class PairformerModule(nn.Module):
     ``Boltz2`` call sites (``boltz2.py:3750, 4502, 4688, 5015``)."""
 
     def __init__(self, n_blocks: int, tri_att_head_dim: int, tri_att_n_heads: int, att_head_dim: Optional[int],
-                 att_n_heads: Optional[int], transform_s: bool, affinity: bool = False):
+                 att_n_heads: Optional[int], transform_s: bool, affinity: bool = False,
+                 options: Optional[Options] = None):
         super().__init__()
         self.n_blocks = n_blocks
         self.tri_att_head_dim = tri_att_head_dim
@@ -314,7 +336,7 @@ class PairformerModule(nn.Module):
         self.transform_s = transform_s
         self.affinity = affinity
         self.module: Optional[Pairformer] = None
-        self.options = Options()
+        self.options = options or Options()
         self._runtime_cache: dict = {}
         self._first_forward_pass = True
 
@@ -358,7 +380,8 @@ class PairformerModule(nn.Module):
         if self.transform_s and s is not None:
             s_dev = torch.zeros((B, n_pad, s.shape[-1]), dtype=torch.float32, device=dev)
             s_dev[:, :N] = s.to(dev, torch.float32)
-        s_dev, z_dev = self.module(s_dev, z_dev, self._runtime_cache["pair_mask"], self._runtime_cache.get("mask"))
+        s_dev, z_dev = self.module(s_dev, z_dev, self._runtime_cache["pair_mask"], self._runtime_cache.get("mask"),
+                                   n_valid=N)
         z_out = z_dev[:, :N, :N].to(z.device)
         s_out = None if s_dev is None else s_dev[:, :N].to(s.device)
         if s is not None and not self.transform_s:
@@ -376,17 +399,19 @@ class TrunkRecycler:
     def __init__(self, pairformer: Pairformer, state_dict, options: Optional[Options] = None):
         w = WeightScope.wrap(state_dict)
         self.pairformer = pairformer
-        self.options = options or Options()
+        self.options = options or pairformer.options
+        v = self.options.operand
         dev = get_device()
         self.s_norm_w, self.s_norm_b = ops.f32(w["s_norm.weight"], dev), ops.f32(w["s_norm.bias"], dev)
         self.z_norm_w, self.z_norm_b = ops.f32(w["z_norm.weight"], dev), ops.f32(w["z_norm.bias"], dev)
-        self.s_rec = ops.bf16(w["s_recycle.weight"], dev)
-        self.z_rec = ops.bf16(w["z_recycle.weight"], dev)
+        self.s_rec = ops.opw(w["s_recycle.weight"], dev, v)
+        self.z_rec = ops.opw(w["z_recycle.weight"], dev, v)
 
     def __call__(self, s_init: torch.Tensor, z_init: torch.Tensor, mask: Optional[torch.Tensor],
-                 recycling_steps: int, pass_hook=None):
+                 recycling_steps: int, pass_hook=None, n_valid: int = 0):
         """Padded device tensors in (N % 64 == 0); returns device (s, z)."""
         B, N = z_init.shape[0], z_init.shape[1]
+        v = self.options.operand
         dev = z_init.device
         pair_mask = None if mask is None else (mask[:, :, None] * mask[:, None, :]).contiguous()
         s = torch.zeros_like(s_init)
@@ -394,10 +419,10 @@ class TrunkRecycler:
         s_tmp = torch.empty_like(s_init)
         ws = ops.workspace(self.pairformer.workspace_bytes(B, N), dev)
         for i in range(recycling_steps + 1):
-            ops.launch_layernorm(s, self.s_norm_w, self.s_norm_b, s_tmp, self.options.eps)
-            ops.launch_linear(s_tmp, self.s_rec, None, s_init, s)
-            ops.launch_pair_ln_linear(z, z_init, self.z_norm_w, self.z_norm_b, self.z_rec, z, self.options.eps)
-            s, z = self.pairformer(s, z, pair_mask, mask, ws)
+            ops.launch_layernorm(s, self.s_norm_w, self.s_norm_b, s_tmp, self.options.eps, v)
+            ops.launch_linear(s_tmp, self.s_rec, None, s_init, s, v)
+            ops.launch_pair_ln_linear(z, z_init, self.z_norm_w, self.z_norm_b, self.z_rec, z, self.options.eps, v)
+            s, z = self.pairformer(s, z, pair_mask, mask, ws, n_valid)
             if pass_hook is not None:
                 pass_hook(i)
         return s, z
