@@ -160,7 +160,7 @@ def main() -> int:
     layer.triangle_multiplication_start(z, None, out=torch.empty_like(z), accumulate=False, ws=ws)
     reps = 20
     contract_ms = time_op(lambda: ops.launch_trimul_contract(opA, opB, X, layer.variant), reps)
-    contract_flop = fl["trimul_contract"] / 2   # one direction per launch
+    contract_flop = fl["trimul_contract"]       # 2*N^3*128: 128 planes of 2*N^3, one direction per launch
     achieved = contract_flop / (contract_ms * 1e-3) / 1e12
     roofline = {"kernel": "tm_contract_kernel", "bound": "mfma", "achieved": round(achieved, 1),
                 "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",

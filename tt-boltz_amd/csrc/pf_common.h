@@ -65,11 +65,15 @@ PF_DEV int kperm_row(int s, int h, int t) { return 16 * s + 4 * h + (t < 4 ? t :
 // units 16*s + 8*h + t: the natural k order of the next MFMA operand.
 PF_DEV int perm16(int row) { return (row & ~0xC) | ((row & 4) << 1) | ((row & 8) >> 1); }
 
-PF_DEV float sigmoidf_fast(float x) { return 1.f / (1.f + __expf(-x)); }
+PF_DEV float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }   // v_exp_f32
 
-PF_DEV float siluf(float x) { return x / (1.f + __expf(-x)); }
+// v_rcp_f32 (1 ulp) instead of the IEEE division sequence HIP emits for '/'.
+PF_DEV float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
 
-PF_DEV float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+// sigmoid(x) = 1 / (1 + 2^(-x log2 e)): saturates cleanly to 0 / 1 for large |x|.
+PF_DEV float sigmoidf_fast(float x) { return rcp_fast(1.f + exp2_fast(-1.4426950408889634f * x)); }
+
+PF_DEV float siluf(float x) { return x * sigmoidf_fast(x); }
 
 // Sum across the two 32-lane halves of a wave64.
 PF_DEV float xor32_sum(float v) { return v + __shfl_xor(v, 32); }

@@ -18,27 +18,39 @@
 namespace {
 
 constexpr int C = 128, LDSW = 136, LDS3 = 40;
-constexpr int PB = 2;   // 32-pair blocks per wave
 
-__global__ __launch_bounds__(256) void tr_pair_kernel(
+// Launch configuration of the pair transition (pair blocks per wave, waves per WG,
+// min waves per SIMD), chosen by measurement.
+#ifndef TR_PB
+#define TR_PB 1
+#define TR_NW 4
+#define TR_MINW 2
+#endif
+
+// PB: 32-pair blocks per wave; NW: waves per workgroup; MINW: min waves per SIMD hint.
+template <int PB, int NW, int MINW>
+__global__ __launch_bounds__(64 * NW, MINW) void tr_pair_kernel(
     const float* x_in, float* out, const float* __restrict__ lnw, const float* __restrict__ lnb,
     const op_t* __restrict__ w1, const op_t* __restrict__ w2, const op_t* __restrict__ w3,
     long rows, int hidden, int accumulate, float eps) {
+  constexpr int NT = 64 * NW;            // threads
+  constexpr int CH = 512 / NT;           // 16-byte chunks per thread per 8 KB block
+  static_assert(NT <= 512 && 512 % NT == 0, "staging assumes 64..512 threads");
   __shared__ __attribute__((aligned(16))) op_t s1[2][32 * LDSW];
   __shared__ __attribute__((aligned(16))) op_t s2[2][32 * LDSW];
   __shared__ __attribute__((aligned(16))) op_t s3[2][C * LDS3];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
-  const long pos0 = ((long)blockIdx.x * 4 + wid) * (32 * PB);
-  const bool active = pos0 < rows;
+  const long pos0 = ((long)blockIdx.x * NW + wid) * (32 * PB);
 
+  // Every wave runs the whole loop (no divergent control flow around the MFMA chain,
+  // which would make the compiler shuttle accumulators between AGPRs and VGPRs);
+  // rows past the end are clamped on load and skipped on store.
   opx8 xf[PB][8];
-  if (active) {
 #pragma unroll
-    for (int pb = 0; pb < PB; ++pb) {
-      float x[64];
-      load_row128_frag(x_in + min(pos0 + 32 * pb + m, rows - 1) * C, h, x);
-      ln128_to_frag(x, h, lnw, lnb, eps, xf[pb]);
-    }
+  for (int pb = 0; pb < PB; ++pb) {
+    float x[64];
+    load_row128_frag(x_in + min(pos0 + 32 * pb + m, rows - 1) * C, h, x);
+    ln128_to_frag(x, h, lnw, lnb, eps, xf[pb]);
   }
   f32x16 acc[PB][4];
 #pragma unroll
@@ -46,12 +58,12 @@ __global__ __launch_bounds__(256) void tr_pair_kernel(
 #pragma unroll
     for (int ob = 0; ob < 4; ++ob) acc[pb][ob] = zero16();
 
-  // staging: fc1/fc2 block = 32 rows x 128 (2 chunks/thread each), fc3 block = 128 rows x 32 (2 chunks/thread)
-  opx8 r1[2], r2[2], r3[2];
+  // staging: fc1/fc2 block = 32 rows x 128, fc3 block = 128 rows x 32 (512 chunks each)
+  opx8 r1[CH], r2[CH], r3[CH];
   auto gload = [&](int hb) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int c = tid + 256 * q;
+    for (int q = 0; q < CH; ++q) {
+      const int c = tid + NT * q;
       r1[q] = ld_x8(w1 + (long)(32 * hb + (c >> 4)) * C + (c & 15) * 8);
       r2[q] = ld_x8(w2 + (long)(32 * hb + (c >> 4)) * C + (c & 15) * 8);
       r3[q] = ld_x8(w3 + (long)(c >> 2) * hidden + 32 * hb + (c & 3) * 8);
@@ -62,8 +74,8 @@ __global__ __launch_bounds__(256) void tr_pair_kernel(
   for (int hb = 0; hb < nhb; ++hb) {
     const int bufi = hb & 1;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int c = tid + 256 * q;
+    for (int q = 0; q < CH; ++q) {
+      const int c = tid + NT * q;
       const int row = perm16(c >> 4);
       st_x8(&s1[bufi][row * LDSW + (c & 15) * 8], r1[q]);
       st_x8(&s2[bufi][row * LDSW + (c & 15) * 8], r2[q]);
@@ -71,7 +83,6 @@ __global__ __launch_bounds__(256) void tr_pair_kernel(
     }
     __syncthreads();
     if (hb + 1 < nhb) gload(hb + 1);
-    if (!active) continue;
     f32x16 a1[PB], a2[PB];
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) { a1[pb] = zero16(); a2[pb] = zero16(); }
@@ -101,7 +112,6 @@ __global__ __launch_bounds__(256) void tr_pair_kernel(
         for (int pb = 0; pb < PB; ++pb) acc[pb][ob] = mfma32(hf[pb][ks], f3, acc[pb][ob]);
       }
   }
-  if (!active) return;
 #pragma unroll
   for (int pb = 0; pb < PB; ++pb)
 #pragma unroll
@@ -253,8 +263,9 @@ extern "C" int pf_transition_fwd(const pf_transition_args* a) {
     return pf_fail(PF_E_INVALID, "pf_transition_fwd: null pointer argument");
   hipStream_t st = (hipStream_t)a->stream;
   if (a->C == C) {
-    const unsigned grid = (unsigned)((a->rows + 128 * PB - 1) / (128 * PB));
-    tr_pair_kernel<<<grid, 256, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w,
+    constexpr int PB = TR_PB, NW = TR_NW;
+    const unsigned grid = (unsigned)((a->rows + 32 * PB * NW - 1) / (32 * PB * NW));
+    tr_pair_kernel<PB, NW, TR_MINW><<<grid, 64 * NW, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w,
                                          (const op_t*)a->fc2_w, (const op_t*)a->fc3_w, a->rows, a->hidden,
                                          a->accumulate, a->eps);
     PF_CHECK_LAUNCH("tr_pair_kernel");

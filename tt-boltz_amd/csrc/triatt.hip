@@ -306,7 +306,7 @@ __global__ __launch_bounds__(256, 2) void ta_attn_kernel(
     if (kbi == nKB - 1) {   // head end: normalize and store
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        const float inv = 1.f / xor32_sum(lsum[qb]);
+        const float inv = rcp_fast(xor32_sum(lsum[qb]));
         const int j = j0 + 32 * qb + m;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
