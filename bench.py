@@ -10,7 +10,16 @@ Besides the JSON line's ``value`` (layers/s), it reports per-op times and
 TFLOP/s, the roofline of the dominant kernel (timed alone with HIP events on the
 stream it is launched on) and the CPU oracle timed on this host's cores.
 
+The config-3 trunk (64 layers at N=768, recycling_steps=3 -> 4 passes, device
+resident) and the contraction alone at N=768 are reported under ``stack``.
+
+``--probe-traffic`` runs only the contraction (5 launches at N=512) and a plain
+copy kernel of known size, for ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE``
+runs; the calibrated per-launch traffic is read back from
+``profiles/tm_contract_traffic.json`` when that file exists.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--n 512] [--no-cpu-baseline]
+                       [--no-stack] [--probe-traffic]
 """
 from __future__ import annotations
 
@@ -25,8 +34,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 (AMD published)
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 / fp16 (AMD published)
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "tm_contract_traffic.json")
+COPY_BYTES = 256 << 20            # the calibration copy kernel reads and writes this many bytes
 
 
 def flops_layer(N: int, c: int = 128, hd: int = 128, H: int = 4, c_s: int = 384) -> dict:
@@ -76,6 +87,95 @@ def cpu_baseline(N: int, seed: int, reps: int = 3) -> dict:
                       f"{sec:.2f} s/layer; cpu={cpu}"}
 
 
+def probe_traffic(N: int) -> int:
+    """Contraction alone (5 launches on its real plane size) and a plain copy kernel of
+    COPY_BYTES read + COPY_BYTES written, for PMC runs (FETCH_SIZE / WRITE_SIZE)."""
+    import torch
+    from tt_boltz_amd import ops
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    A = torch.randn((128, N, N), device=dev, generator=g).half()
+    Bm = torch.randn((128, N, N), device=dev, generator=g).half()
+    X = torch.empty((128, N, N), dtype=torch.float16, device=dev)
+    src = torch.randn(COPY_BYTES // 4, device=dev, generator=g)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        ops.launch_trimul_contract(A, Bm, X)
+    for _ in range(3):
+        torch.mul(src, 2.0, out=dst)     # vectorized elementwise kernel: reads and writes COPY_BYTES
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "traffic", "N": N, "contract_launches": 5, "copy_launches": 3,
+                      "copy_bytes": COPY_BYTES}), flush=True)
+    return 0
+
+
+def load_traffic():
+    """Calibrated HBM bytes per contraction launch from the committed PMC summary (or None)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t
+    except (OSError, ValueError):
+        return None
+
+
+def time_events(fn, reps: int, stream) -> float:
+    """Average ms per call of fn, HIP events recorded on `stream` (the stream the kernels use)."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        fn()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def stack_bench(N: int = 768, n_layers: int = 64, recycling_steps: int = 3, seed: int = 3) -> dict:
+    """Config 3: the 64-layer trunk at N=768 through the device-resident recycling loop
+    (boltz2.py:5203-5248; recycling_steps=3 -> 4 passes), plus the contraction alone at N."""
+    import torch
+    from tt_boltz_amd import ops, pairformer, synthetic
+    dev = pairformer.get_device()
+    stream = torch.cuda.current_stream()
+    w = synthetic.stack_weights(n_layers, seed)
+    w_rec = synthetic.draw(synthetic.recycle_shapes(), seed + 1000)
+    s_cpu, z_cpu, mask_cpu, _ = synthetic.pair_inputs(N, seed, z_scale=0.5)
+    pf = pairformer.Pairformer(n_layers, 32, 4, 24, 16, True, w)
+    rec = pairformer.TrunkRecycler(pf, w_rec)
+    s0, z0, mask = s_cpu.to(dev), z_cpu.to(dev), mask_cpu.to(dev)
+    rec(s0, z0, mask, 0)            # warm-up pass
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    s_out, z_out = rec(s0, z0, mask, recycling_steps)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    trunk_s = e0.elapsed_time(e1) / 1e3
+    finite = bool(torch.isfinite(z_out).all() and torch.isfinite(s_out).all())
+    passes = recycling_steps + 1
+    fl = flops_layer(N)
+    # the contraction alone at this N (128 planes, one direction per launch)
+    A = torch.randn((128, N, N), device=dev).half()
+    Bm = torch.randn((128, N, N), device=dev).half()
+    X = torch.empty((128, N, N), dtype=torch.float16, device=dev)
+    c_ms = time_events(lambda: ops.launch_trimul_contract(A, Bm, X), 20, stream)
+    c_tf = fl["trimul_contract"] / (c_ms * 1e-3) / 1e12
+    del A, Bm, X
+    return {"N": N, "layers": n_layers, "recycling_steps": recycling_steps, "passes": passes,
+            "trunk_s": round(trunk_s, 4), "pass_s": round(trunk_s / passes, 4),
+            "layers_per_s": round(n_layers * passes / trunk_s, 2),
+            "layer_tflops_achieved": round(fl["layer"] * n_layers * passes / trunk_s / 1e12, 1),
+            "finite": finite,
+            "contract": {"kernel": "tm_contract_dma_kernel", "launch_ms": round(c_ms, 4),
+                         "tflops": round(c_tf, 1), "frac_of_peak": round(c_tf / MFMA_BF16_PEAK_TFLOPS, 4)},
+            "workload": "64-layer Boltz-2 Pairformer trunk, N=768, seed 3 weights, z~0.5 N(0,1), s~N(0,1), "
+                        "masks all ones, 4 recycling passes, fp32 residual stream"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -83,11 +183,16 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-stack", action="store_true")
+    ap.add_argument("--probe-traffic", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}): this build measures the "
               "single-GPU Pairformer path; multi-GPU sharding is a design note only.", file=sys.stderr)
         return 0
+
+    if args.probe_traffic:
+        return probe_traffic(args.n)
 
     import torch
     from tt_boltz_amd import ops, pairformer, synthetic
@@ -126,15 +231,7 @@ def main() -> int:
     fl = flops_layer(N)
 
     def time_op(fn, reps=10):
-        fn()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(reps):
-            fn()
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / reps
+        return time_events(fn, reps, stream)
 
     ops_ms = {
         "trimul_out": time_op(lambda: layer.triangle_multiplication_start(z, None, out=z, accumulate=True, ws=ws)),
@@ -162,10 +259,15 @@ def main() -> int:
     contract_ms = time_op(lambda: ops.launch_trimul_contract(opA, opB, X, layer.variant), reps)
     contract_flop = fl["trimul_contract"]       # 2*N^3*128: 128 planes of 2*N^3, one direction per launch
     achieved = contract_flop / (contract_ms * 1e-3) / 1e12
-    roofline = {"kernel": "tm_contract_kernel", "bound": "mfma", "achieved": round(achieved, 1),
+    kname = "tm_contract_dma_kernel" if N >= 384 else "tm_contract_kernel"
+    traffic = load_traffic()
+    roofline = {"kernel": kname, "bound": "mfma", "achieved": round(achieved, 1),
                 "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                "traffic": traffic["hbm_bytes_per_launch"] if traffic and traffic.get("N") == N else None,
                 "launch_ms": round(contract_ms, 4), "flop_per_launch": contract_flop}
+    if traffic and traffic.get("N") == N:
+        roofline["traffic_note"] = traffic.get("note")
 
     # the same layer with bf16 MFMA operands (libpairformer_hip_bf16.so, same kernels)
     pf_bf16 = pairformer.Pairformer(1, 32, 4, 24, 16, True, w, pairformer.Options(operand="bf16"))
@@ -199,6 +301,9 @@ def main() -> int:
         "device": torch.cuda.get_device_name(0),
         "host": platform.node(),
     }
+    if not args.no_stack:
+        del pf_bf16, zb, sb
+        out["stack"] = stack_bench()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(N, seed)
     print(json.dumps(out), flush=True)

@@ -193,6 +193,152 @@ __global__ __launch_bounds__(256) void tm_contract_kernel(
     }
 }
 
+// Large-N contraction: a 256x256 output tile per workgroup, 4 waves in 2x2, each wave
+// 128x128 = 4x4 MFMA 32x32 tiles (256 fp32 accumulators per lane, occupancy 1 wave per
+// SIMD).  The wave computes the transposed tile D[j][i] = sum_k B[j][k] A[i][k], so a
+// lane's accumulator registers 4g..4g+3 hold 4 consecutive j of one i and the epilogue
+// writes 8-byte (op_t) or 16-byte (fp32) runs.
+//
+// Operands move global -> LDS with global_load_lds_dwordx4 (lane l of an instruction
+// lands at LDS base + 16*l), so no VGPRs are spent on staging, through a 2-deep ring of
+// [256][64] slabs per operand: every DMA request is a whole 128-byte row segment, and
+// slab kt+1 is in flight while slab kt is consumed.
+// ---------------------------------------------------------------------------------
+constexpr int BM2 = 256;
+
+// s_waitcnt immediate (gfx9 encoding) that waits until at most v vector-memory
+// operations of this wave are outstanding and leaves expcnt / lgkmcnt unconstrained.
+constexpr int vmcnt_le(int v) { return (v & 0xF) | (((v >> 4) & 3) << 14) | 0x70 | 0xF00; }
+
+// Slab layout: chunk c (0..7, 16 bytes) of row r at position 8r + (c ^ swz8(r)) with
+// swz8(r) = ((r>>1)&7) ^ ((r&1)<<2).  A fragment read takes one chunk from each of 32
+// consecutive rows; for any 8 (or 16) consecutive aligned rows the positions fall in 8
+// (16) distinct 16-byte bank groups, so reads are conflict-free whether the LDS serves
+// 8 or 16 lanes of a 128-bit read per cycle.
+PF_DEV int slab_swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+constexpr int DK8 = 64;
+constexpr int DSLAB8 = BM2 * DK8;
+constexpr size_t TMD8_LDS_BYTES = (size_t)2 * 2 * DSLAB8 * sizeof(op_t);
+
+template <typename OutT>
+__global__ __launch_bounds__(256, 1) void tm_contract_dma_kernel(
+    const op_t* __restrict__ A, const op_t* __restrict__ Bop, OutT* __restrict__ X,
+    int N, int tpd, int total, float out_scale, long in_plane_stride) {
+  extern __shared__ __attribute__((aligned(16))) op_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wid >> 1, wn = wid & 1;
+  const int w = xcd_remap(blockIdx.x, total);
+  const int tiles = tpd * tpd;
+  const long plane = w / tiles;
+  const int t = w - (int)plane * tiles;
+  const int i0 = (t / tpd) * BM2, j0 = (t % tpd) * BM2;
+  const long NN = (long)N * N;
+
+  // DMA: instruction q (0..7) of this wave covers slab rows (8*wid + q)*8 + (lane >> 3)
+  int offA[8], offB[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int r = (8 * wid + q) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ slab_swz8(r);
+    offA[q] = min(i0 + r, N - 1) * N + 8 * c;
+    offB[q] = min(j0 + r, N - 1) * N + 8 * c;
+  }
+  const op_t* Ap = A + plane * in_plane_stride;
+  const op_t* Bp = Bop + plane * in_plane_stride;
+  auto issue = [&](int kt) {
+    op_t* sa = smem + (kt & 1) * 2 * DSLAB8;
+    op_t* sb = sa + DSLAB8;
+    const int ko = kt * DK8;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_global_load_lds(Ap + offA[q] + ko, sa + (8 * wid + q) * 512, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(Bp + offB[q] + ko, sb + (8 * wid + q) * 512, 16, 0, 0);
+    }
+  };
+  const int swz = slab_swz8(m);   // rows base + 32x + m: bits 0-3 of the row are those of m
+  const int rdA = (wm * 128 + m) * DK8, rdB = (wn * 128 + m) * DK8;
+  auto read_frags = [&](int kt, int s, opx8 (&fa)[4], opx8 (&fb)[4]) {
+    const op_t* sa = smem + (kt & 1) * 2 * DSLAB8;
+    const op_t* sb = sa + DSLAB8;
+    const int cs = 8 * ((2 * s + h) ^ swz);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      fa[x] = ld_x8(sa + rdA + 32 * x * DK8 + cs);
+      fb[x] = ld_x8(sb + rdB + 32 * x * DK8 + cs);
+    }
+  };
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int y = 0; y < 4; ++y)
+#pragma unroll
+    for (int x = 0; x < 4; ++x) acc[y][x] = zero16();
+  auto mma = [&](const opx8 (&fa)[4], const opx8 (&fb)[4]) {
+#pragma unroll
+    for (int y = 0; y < 4; ++y)
+#pragma unroll
+      for (int x = 0; x < 4; ++x) acc[y][x] = mfma32(fb[y], fa[x], acc[y][x]);
+  };
+#define PF_INTERLEAVE_8_READS()                                   \
+  _Pragma("unroll") for (int q_ = 0; q_ < 8; ++q_) {              \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            \
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);            \
+  }                                                               \
+  __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+
+  const int nk = N / DK8;
+  issue(0);
+  opx8 f0a[4], f0b[4], f1a[4], f1b[4];
+  for (int kt = 0; kt < nk; ++kt) {
+    // slab kt landed (slab kt+1 not yet issued); the barrier also tells every wave that
+    // slab kt-1's buffer is free, so slab kt+1 can go into it
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+    __builtin_amdgcn_s_barrier();
+    if (kt + 1 < nk) issue(kt + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(kt, 0, f0a, f0b);
+    read_frags(kt, 1, f1a, f1b);
+    mma(f0a, f0b);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(kt, 2, f0a, f0b);
+    mma(f1a, f1b);
+    PF_INTERLEAVE_8_READS();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(kt, 3, f1a, f1b);
+    mma(f0a, f0b);
+    PF_INTERLEAVE_8_READS();
+    __builtin_amdgcn_sched_barrier(0);
+    mma(f1a, f1b);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#undef PF_INTERLEAVE_8_READS
+  OutT* Xp = X + plane * NN;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    const int ib = i0 + wm * 128 + 32 * x;
+#pragma unroll
+    for (int y = 0; y < 4; ++y) {
+      const int jb = j0 + wn * 128 + 32 * y;
+      if (ib >= N || jb >= N) continue;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        OutT* dst = Xp + (long)(ib + m) * N + jb + 8 * g + 4 * h;
+        if constexpr (sizeof(OutT) == 4) {
+          f32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[y][x][4 * g + e] * out_scale;
+          *reinterpret_cast<f32x4*>(dst) = v;
+        } else {
+          opx4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (op_t)(acc[y][x][4 * g + e] * out_scale);
+          st_x4((op_t*)dst, v);
+        }
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------
 // Output: z[i,j,:] (+)= p_out(LN_out(X[:,i,j])) * sigmoid(g_out(LN_in(z[i,j,:]))).
 // One wave = 32 consecutive pairs (i, j0..j0+31); weights resident in LDS.
@@ -256,6 +402,32 @@ __global__ __launch_bounds__(256) void tm_out_kernel(
   }
 }
 
+// Contraction dispatch: 256x256 tiles from N = 384 up (enough tiles to fill the chip
+// and a long enough K loop), 128x128 tiles below.
+template <typename OutT>
+int launch_contract(const op_t* opA, const op_t* opB, OutT* X, int planes, int N, float scale, hipStream_t st) {
+  if (N >= 384) {
+    static bool attr_set = false;   // per process; the attribute is a property of the function
+    if (!attr_set) {
+      if (hipFuncSetAttribute((const void*)tm_contract_dma_kernel<OutT>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)TMD8_LDS_BYTES) != hipSuccess)
+        return pf_fail(PF_E_LAUNCH, "tm_contract_dma_kernel: cannot reserve %zu bytes of LDS", TMD8_LDS_BYTES);
+      attr_set = true;
+    }
+    const int tpd = (N + BM2 - 1) / BM2;
+    const int total = planes * tpd * tpd;
+    tm_contract_dma_kernel<OutT><<<total, 256, TMD8_LDS_BYTES, st>>>(opA, opB, X, N, tpd, total, scale,
+                                                                     (long)N * N);
+    PF_CHECK_LAUNCH("tm_contract_dma_kernel");
+    return PF_OK;
+  }
+  const int tpd = (N + BM - 1) / BM;
+  const int total = planes * tpd * tpd;
+  tm_contract_kernel<OutT><<<total, 256, 0, st>>>(opA, opB, X, N, tpd, total, scale);
+  PF_CHECK_LAUNCH("tm_contract_kernel");
+  return PF_OK;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------------
@@ -296,10 +468,8 @@ extern "C" int pf_trimul_fwd(const pf_trimul_args* a) {
                                             a->direction, a->eps);
   PF_CHECK_LAUNCH("tm_proj_kernel");
 
-  const int tpd = (N + BM - 1) / BM;
-  const int total = B * C * tpd * tpd;
-  tm_contract_kernel<op_t><<<total, 256, 0, st>>>(opA, opB, X, N, tpd, total, X_STORE_SCALE);
-  PF_CHECK_LAUNCH("tm_contract_kernel");
+  const int rc = launch_contract<op_t>(opA, opB, X, B * C, N, X_STORE_SCALE, st);
+  if (rc != PF_OK) return rc;
 
   tm_out_kernel<op_t><<<grid_proj, 256, 0, st>>>(X, X_LOAD_SCALE, a->z_in, a->out, a->norm_in_w, a->norm_in_b,
                                                  a->norm_out_w, a->norm_out_b, (const op_t*)a->p_out_w,
@@ -314,14 +484,9 @@ extern "C" int pf_trimul_contract(const void* opA, const void* opB, void* X, int
   if (!opA || !opB || !X) return pf_fail(PF_E_INVALID, "pf_trimul_contract: null pointer");
   if (planes <= 0 || N <= 0 || N % 64)
     return pf_fail(PF_E_INVALID, "pf_trimul_contract: need planes > 0 and N a multiple of 64");
-  const int tpd = (N + BM - 1) / BM;
-  const int total = planes * tpd * tpd;
   if (x_fp32)
-    tm_contract_kernel<float><<<total, 256, 0, (hipStream_t)stream>>>(
-        (const op_t*)opA, (const op_t*)opB, (float*)X, N, tpd, total, 1.f);
-  else
-    tm_contract_kernel<op_t><<<total, 256, 0, (hipStream_t)stream>>>(
-        (const op_t*)opA, (const op_t*)opB, (op_t*)X, N, tpd, total, X_STORE_SCALE);
-  PF_CHECK_LAUNCH("tm_contract_kernel");
-  return PF_OK;
+    return launch_contract<float>((const op_t*)opA, (const op_t*)opB, (float*)X, planes, N, 1.f,
+                                  (hipStream_t)stream);
+  return launch_contract<op_t>((const op_t*)opA, (const op_t*)opB, (op_t*)X, planes, N, X_STORE_SCALE,
+                               (hipStream_t)stream);
 }
