@@ -191,6 +191,64 @@ size_t pf_apb_workspace_size(int B, int N, int c_s, int H);
 int pf_apb_fwd(const pf_apb_args* args);
 
 /* ------------------------------------------------------------------------------
+ * Fast mode (block fp8).  Replaces the --fast path of the ttnn TriangleMultiplication
+ * and Transition (tt_bio/tenstorrent.py:60-61, 178-181, 389-407, 431-503, 879-906),
+ * which the reference selects with set_fast_mode() before building the modules
+ * (tt_bio/worker.py:151-153) and which has no CPU counterpart (tt_bio/main.py:1648-1649).
+ * Format: OCP MXFP8 -- e4m3 elements (round to nearest even, saturating at +-448) with
+ * one E8M0 scale byte per 32 consecutive elements along the contraction axis,
+ * X = 2^(floor(log2(amax)) - 8); fp32 accumulation.  Matrices are passed pre-quantized
+ * (pf_quantize_mx8): q = e4m3 bytes [rows][K], s = scale bytes [rows][K/32].
+ * -------------------------------------------------------------------------- */
+
+/* Quantize x fp32 [rows][K] (K % 32 == 0) along K: q bytes [rows][K], scales [rows][K/32].
+ * perm = 0 keeps the element order; perm = 1 stores each 32-block in accumulator order
+ * (destination 16h + 4j + e <- source 4h + 8j + e), the order pf_transition_mx8_fwd
+ * expects for fc3.weight.  Asynchronous on `stream`. */
+int pf_quantize_mx8(const float* x, long rows, int K, int perm, void* q, void* scales, void* stream);
+
+/* Triangle multiplication with MXFP8 projections and contraction operands (same
+ * semantics and argument meaning as pf_trimul_fwd; N must be a multiple of 128).
+ * Quantized: LN_in(z) and p_in/g_in (K = C); a and b along the contraction index;
+ * LN_out(x) and p_out; LN_in(z) and g_out. */
+typedef struct pf_trimul_mx8_args {
+  int B, N, C, hidden, direction, accumulate;
+  float eps;
+  const float* z_in; float* out; const float* pair_mask;
+  const float* norm_in_w; const float* norm_in_b;
+  const void* p_in_q; const void* p_in_s;     /* p_in.weight  [2C][C] e4m3, [2C][C/32] E8M0 */
+  const void* g_in_q; const void* g_in_s;     /* g_in.weight */
+  const float* norm_out_w; const float* norm_out_b;
+  const void* p_out_q; const void* p_out_s;   /* p_out.weight [C][C], [C][C/32] */
+  const void* g_out_q; const void* g_out_s;   /* g_out.weight */
+  void* workspace; size_t workspace_bytes;
+  void* stream;
+} pf_trimul_mx8_args;
+
+size_t pf_trimul_mx8_workspace_size(int B, int N, int C);
+int pf_trimul_mx8_fwd(const pf_trimul_mx8_args* args);
+
+/* The MXFP8 contraction alone (tests): X fp32 [planes][N][N] = A . B^T per plane, A/B e4m3
+ * [planes][N][N] with scales [planes][N][N/32] along the last axis; N % 128 == 0. */
+int pf_trimul_mx8_contract(const void* A8, const void* B8, const void* SA, const void* SB, float* X,
+                           int planes, int N, void* stream);
+
+/* Pair transition with MXFP8 GEMMs (C = 128, hidden % 64 == 0): LN(x) and fc1/fc2 (K = C),
+ * silu(fc1)*fc2 and fc3 (K = hidden).  fc3 must be quantized with perm = 1. */
+typedef struct pf_transition_mx8_args {
+  long rows; int C; int hidden; int accumulate;
+  float eps;
+  const float* x_in; float* out;
+  const float* norm_w; const float* norm_b;
+  const void* fc1_q; const void* fc1_s;       /* fc1.weight [hidden][C] */
+  const void* fc2_q; const void* fc2_s;       /* fc2.weight [hidden][C] */
+  const void* fc3_q; const void* fc3_s;       /* fc3.weight [C][hidden], perm = 1 */
+  void* stream;
+} pf_transition_mx8_args;
+
+int pf_transition_mx8_fwd(const pf_transition_mx8_args* args);
+
+/* ------------------------------------------------------------------------------
  * Row primitives (tt_bio/boltz2.py:638-768): LayerNorm and Linear over rows.
  * -------------------------------------------------------------------------- */
 /* out[r,:] = LN(x[r,:]) * w + b, fp32, any C <= 4096.  (nn.LayerNorm, eps) */

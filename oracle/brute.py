@@ -11,6 +11,7 @@ results and fails ``tests/test_oracle.py``.
 """
 from __future__ import annotations
 
+import bisect
 import math
 
 import numpy as np
@@ -195,3 +196,118 @@ def pairformer_layer(s, z, mask, pair_mask, W, tri_heads, tri_dim, att_heads):
     s = s + attention_pair_bias(sn, z, mask, sn, sub("attention"), att_heads)
     s = s + transition(s, sub("transition_s"))
     return s, z
+
+
+# --------------------------------------------------------------------------------------
+# MXFP8 (fast mode) by scalar loops: the quantizer below shares no code with fp8_emu.
+# Element rounding searches the e4m3 code table for the nearest value (ties to the even
+# code); the block exponent comes from math.frexp.
+# --------------------------------------------------------------------------------------
+def _e4m3_value(code):
+    s, e, m = code >> 7, (code >> 3) & 15, code & 7
+    v = m * 2.0 ** -9 if e == 0 else (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return -v if s else v
+
+
+_E4M3_POS = sorted((_e4m3_value(c), c) for c in range(0x7F))    # non-negative finite codes
+_E4M3_VALS = [v for v, _ in _E4M3_POS]
+
+
+def _e4m3_nearest(v):
+    """Nearest e4m3 value to v (|v| clamped to 448), ties to the even code: a table search
+    between the two neighbouring code values."""
+    a = min(abs(v), 448.0)
+    hi = bisect.bisect_left(_E4M3_VALS, a)
+    if hi == 0:
+        q = _E4M3_VALS[0]
+    elif hi == len(_E4M3_VALS):
+        q = _E4M3_VALS[-1]
+    else:
+        (lv, lc), (hv, hc) = _E4M3_POS[hi - 1], _E4M3_POS[hi]
+        dl, dh = a - lv, hv - a
+        q = lv if (dl < dh or (dl == dh and lc % 2 == 0)) else hv
+    return -q if v < 0 else q
+
+
+def mx8_block(vals):
+    """Quantize-dequantize one block of 32 values: X = 2^(floor(log2 amax) - 8)."""
+    amax = max(abs(v) for v in vals)
+    if amax == 0.0:
+        return [0.0] * len(vals)
+    _, ex = math.frexp(amax)            # amax = f * 2^ex, 0.5 <= f < 1  ->  floor(log2) = ex - 1
+    X = 2.0 ** (ex - 1 - 8)
+    return [_e4m3_nearest(v / X) * X for v in vals]
+
+
+def mx8_vec(v):
+    out = []
+    for b0 in range(0, len(v), 32):
+        out += mx8_block(list(v[b0:b0 + 32]))
+    return out
+
+
+def _matvec_mx8(Wq, v):
+    """Both operands quantized along the input axis (Wq rows already quantized)."""
+    vq = mx8_vec(v)
+    return [sum(Wq[o][c] * vq[c] for c in range(len(vq))) for o in range(len(Wq))]
+
+
+def triangle_multiplication_mx8(z, pair_mask, W, direction):
+    """Fast-mode triangle multiplication; quantization points as in
+    ``pairformer_ref.triangle_multiplication_mx8``."""
+    z = _np(z)[0]; m = _np(pair_mask)[0]
+    W = {k: _np(v) for k, v in W.items()}
+    Wq = {k: [mx8_vec(list(r)) for r in W[k]] for k in ("p_in.weight", "g_in.weight", "p_out.weight",
+                                                          "g_out.weight")}
+    N, _, C = z.shape
+    Hd = W["p_in.weight"].shape[0] // 2
+    xin = [[None] * N for _ in range(N)]
+    a = np.zeros((N, N, Hd)); b = np.zeros((N, N, Hd))
+    for i in range(N):
+        for j in range(N):
+            x = _ln_vec(list(z[i, j]), W["norm_in.weight"], W["norm_in.bias"])
+            xin[i][j] = x
+            p = _matvec_mx8(Wq["p_in.weight"], x)
+            g = _matvec_mx8(Wq["g_in.weight"], x)
+            y = [p[o] * _sig(g[o]) * m[i, j] for o in range(2 * Hd)]
+            a[i, j] = y[:Hd]
+            b[i, j] = y[Hd:]
+    # quantize a, b along the contraction index k
+    aq = np.zeros_like(a); bq = np.zeros_like(b)
+    for d in range(Hd):
+        for r in range(N):
+            if direction == "outgoing":      # k = second index
+                aq[r, :, d] = mx8_vec(list(a[r, :, d])); bq[r, :, d] = mx8_vec(list(b[r, :, d]))
+            else:                            # k = first index
+                aq[:, r, d] = mx8_vec(list(a[:, r, d])); bq[:, r, d] = mx8_vec(list(b[:, r, d]))
+    out = np.zeros((1, N, N, W["p_out.weight"].shape[0]))
+    for i in range(N):
+        for j in range(N):
+            x = [0.0] * Hd
+            for d in range(Hd):
+                acc = 0.0
+                for k in range(N):
+                    if direction == "outgoing":
+                        acc += aq[i, k, d] * bq[j, k, d]
+                    else:
+                        acc += aq[k, i, d] * bq[k, j, d]
+                x[d] = acc
+            xn = _ln_vec(x, W["norm_out.weight"], W["norm_out.bias"])
+            po = _matvec_mx8(Wq["p_out.weight"], xn)
+            go = _matvec_mx8(Wq["g_out.weight"], xin[i][j])
+            out[0, i, j] = [po[o] * _sig(go[o]) for o in range(len(po))]
+    return out
+
+
+def transition_mx8(x, W):
+    x = _np(x)
+    W = {k: _np(v) for k, v in W.items()}
+    Wq = {k: [mx8_vec(list(r)) for r in W[k]] for k in ("fc1.weight", "fc2.weight", "fc3.weight")}
+    out = np.zeros(x.shape[:-1] + (W["fc3.weight"].shape[0],))
+    for idx in np.ndindex(x.shape[:-1]):
+        xn = _ln_vec(list(x[idx]), W["norm.weight"], W["norm.bias"])
+        h1 = _matvec_mx8(Wq["fc1.weight"], xn)
+        h2 = _matvec_mx8(Wq["fc2.weight"], xn)
+        hh = [h1[t] * _sig(h1[t]) * h2[t] for t in range(len(h1))]
+        out[idx] = _matvec_mx8(Wq["fc3.weight"], hh)
+    return out

@@ -60,7 +60,16 @@ def quantize_mx8(x: torch.Tensor):
 
 
 def fake_quant_mx8(x: torch.Tensor) -> torch.Tensor:
-    """Quantize-dequantize along the last axis (what a scaled fp8 MFMA sees)."""
+    """Quantize-dequantize along the last axis (what a scaled fp8 MFMA sees).
+
+    A last axis that is not a multiple of 32 ends in a partial block; it is quantized
+    as if zero-padded to 32 (zeros change neither the block maximum nor the other
+    elements), which is what the GPU does on a zero-padded token grid."""
+    K = x.shape[-1]
+    if K % BLOCK:
+        pad = BLOCK - K % BLOCK
+        xp = torch.cat([x, torch.zeros(x.shape[:-1] + (pad,), dtype=x.dtype)], dim=-1)
+        return fake_quant_mx8(xp)[..., :K]
     q, e = quantize_mx8(x)
     qb = q.reshape(x.shape[:-1] + (x.shape[-1] // BLOCK, BLOCK))
     return (qb * torch.exp2(e.to(torch.float32)).unsqueeze(-1)).reshape(x.shape)

@@ -71,6 +71,34 @@ def triangle_multiplication(z: Tensor, pair_mask: Tensor, w: Weights, direction:
     return x * torch.sigmoid(linear(x_in, w["g_out.weight"]))               # :470
 
 
+def triangle_multiplication_mx8(z: Tensor, pair_mask: Tensor, w: Weights, direction: str) -> Tensor:
+    """Fast-mode (``--fast``, ``tt_bio/tenstorrent.py:60-61, 389-407, 431-503``) restatement
+    of :func:`triangle_multiplication` with this build's MXFP8 format (``fp8_emu``) at
+    the points the GPU quantizes: LN_in(z) and p_in/g_in along channels; the gated a, b
+    along the contraction index k; LN_out(x) and p_out, LN_in(z) and g_out along
+    channels.  Everything else is fp32, as in the fp32 oracle."""
+    from .fp8_emu import fake_quant_mx8 as fq, linear_mx8
+    if direction not in ("outgoing", "incoming"):
+        raise ValueError(f"direction must be 'outgoing' or 'incoming', got {direction!r}")
+    x = layer_norm(z, w["norm_in.weight"], w["norm_in.bias"])
+    x_in = x
+    x = linear_mx8(x, w["p_in.weight"]) * torch.sigmoid(linear_mx8(x, w["g_in.weight"]))
+    x = x * pair_mask.unsqueeze(-1)
+    a, b = torch.chunk(x.float(), 2, dim=-1)
+    if direction == "outgoing":
+        # x_ij = sum_k a_ik b_jk: blocks along k = dim 2 of [b, i, k, d]
+        a = fq(a.transpose(2, 3)).transpose(2, 3)
+        b = fq(b.transpose(2, 3)).transpose(2, 3)
+        x = torch.einsum("bikd,bjkd->bijd", a, b)
+    else:
+        # x_ij = sum_k a_ki b_kj: blocks along k = dim 1 of [b, k, i, d]
+        a = fq(a.permute(0, 2, 3, 1)).permute(0, 3, 1, 2)
+        b = fq(b.permute(0, 2, 3, 1)).permute(0, 3, 1, 2)
+        x = torch.einsum("bkid,bkjd->bijd", a, b)
+    x = linear_mx8(layer_norm(x, w["norm_out.weight"], w["norm_out.bias"]), w["p_out.weight"])
+    return x * torch.sigmoid(linear_mx8(x_in, w["g_out.weight"]))
+
+
 # --------------------------------------------------------------------------------------
 # Triangle attention  (tt_bio/reference.py:219-376 + Attention 33-194 + boltz2.py:790-810)
 # --------------------------------------------------------------------------------------
@@ -162,6 +190,15 @@ def transition(x: Tensor, w: Weights) -> Tensor:
     return linear(x, w["fc3.weight"])
 
 
+def transition_mx8(x: Tensor, w: Weights) -> Tensor:
+    """Fast-mode transition (``tt_bio/tenstorrent.py:879-906``) in this build's MXFP8
+    format: LN(x) and fc1/fc2 along channels, silu(fc1)*fc2 and fc3 along the hidden axis."""
+    from .fp8_emu import linear_mx8
+    x = layer_norm(x, w["norm.weight"], w["norm.bias"])
+    x = F.silu(linear_mx8(x, w["fc1.weight"])) * linear_mx8(x, w["fc2.weight"])
+    return linear_mx8(x, w["fc3.weight"])
+
+
 # --------------------------------------------------------------------------------------
 # Single attention with pair bias  (tt_bio/boltz2.py:307-367)
 # --------------------------------------------------------------------------------------
@@ -200,20 +237,23 @@ def chunk_size_for(n: int) -> int:
 
 def pairformer_layer(s: Optional[Tensor], z: Tensor, mask: Optional[Tensor], pair_mask: Tensor,
                      w: Weights, chunk_size: Optional[int] = None,
-                     tri_att_heads: int = 4, tri_att_head_dim: int = 32, att_heads: int = 16):
+                     tri_att_heads: int = 4, tri_att_head_dim: int = 32, att_heads: int = 16,
+                     fast: bool = False):
     """``PairformerLayer.forward`` (``reference.py:865-914``); ``s=None`` gives
     ``PairformerNoSeqLayer.forward`` (``reference.py:1035-1072``).
 
     z += TMo; z += TMi; z += TAs; z += TAe; z += Tr_z;
     s_n = LN(s); s += APB(s_n, z, mask, k_in=s_n); s += Tr_s(s).
+    ``fast``: the triangle multiplications and the pair transition in MXFP8.
     """
-    z = z + triangle_multiplication(z, pair_mask, sub(w, "tri_mul_out"), "outgoing")
-    z = z + triangle_multiplication(z, pair_mask, sub(w, "tri_mul_in"), "incoming")
+    tm = triangle_multiplication_mx8 if fast else triangle_multiplication
+    z = z + tm(z, pair_mask, sub(w, "tri_mul_out"), "outgoing")
+    z = z + tm(z, pair_mask, sub(w, "tri_mul_in"), "incoming")
     z = z + triangle_attention(z, pair_mask, sub(w, "tri_att_start"), True, chunk_size,
                                tri_att_heads, tri_att_head_dim)
     z = z + triangle_attention(z, pair_mask, sub(w, "tri_att_end"), False, chunk_size,
                                tri_att_heads, tri_att_head_dim)
-    z = z + transition(z, sub(w, "transition_z"))
+    z = z + (transition_mx8 if fast else transition)(z, sub(w, "transition_z"))
     if s is None:
         return None, z
     s_normed = layer_norm(s.float(), w["pre_norm_s.weight"], w["pre_norm_s.bias"])

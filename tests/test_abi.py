@@ -21,7 +21,8 @@ def _declared():
 def test_header_declares_expected_entry_points():
     names = _declared()
     for must in ("pf_trimul_fwd", "pf_triatt_fwd", "pf_tri_attention", "pf_transition_fwd", "pf_apb_fwd",
-                 "pf_layernorm_fwd", "pf_linear_fwd", "pf_last_error", "pf_abi_version"):
+                 "pf_layernorm_fwd", "pf_linear_fwd", "pf_last_error", "pf_abi_version", "pf_quantize_mx8",
+                 "pf_trimul_mx8_fwd", "pf_transition_mx8_fwd"):
         assert must in names
 
 
@@ -41,6 +42,8 @@ def test_struct_layouts_match_header_order():
     assert _lib.TrimulArgs.z_in.offset == 32 and ctypes.sizeof(_lib.TrimulArgs) == 32 + 14 * 8
     assert _lib.TransitionArgs.x_in.offset == 24
     assert _lib.TriattArgs.z_in.offset == 40
+    assert _lib.TrimulMx8Args.z_in.offset == 32 and ctypes.sizeof(_lib.TrimulMx8Args) == 32 + 18 * 8
+    assert _lib.TransitionMx8Args.x_in.offset == 24 and ctypes.sizeof(_lib.TransitionMx8Args) == 24 + 11 * 8
 
 
 def _err():
@@ -58,6 +61,12 @@ def test_rejects_null_and_bad_shapes_without_launching():
     assert lib.pf_triatt_fwd(ctypes.byref(t)) == -1 and "H=4" in _err()
     assert lib.pf_layernorm_fwd(None, None, None, None, 4, 8, 1e-5, None) == -1
     assert lib.pf_linear_fwd(1, 1, None, None, 1, 4, 15, 32, None) == -1 and "K % 16" in _err()
+    m = _lib.TrimulMx8Args(B=1, N=192, C=128, hidden=128, direction=0)
+    assert lib.pf_trimul_mx8_fwd(ctypes.byref(m)) == -1 and "multiple of 128" in _err()
+    assert lib.pf_quantize_mx8(1, 4, 48, 0, 1, 1, None) == -1 and "multiple of 32" in _err()
+    assert lib.pf_quantize_mx8(1, 4, 64, 2, 1, 1, None) == -1 and "perm" in _err()
+    tr = _lib.TransitionMx8Args(rows=16, C=384, hidden=1536)
+    assert lib.pf_transition_mx8_fwd(ctypes.byref(tr)) == -1 and "C = 128" in _err()
 
 
 def test_both_operand_variants_load():
@@ -75,6 +84,9 @@ def test_workspace_sizes():
     assert lib.pf_triatt_workspace_size(1, 64, 128, 8, 16) == 0
     assert lib.pf_transition_workspace_size(4096, 128, 512) == 0          # fused, no scratch
     assert lib.pf_transition_workspace_size(100, 384, 1536) == 100 * (384 + 1536) * 4
+    # e4m3 a/b planes + their E8M0 scales + the fp16 contraction output
+    planes = 128 * 512 * 512
+    assert lib.pf_trimul_mx8_workspace_size(1, 512, 128) == 2 * planes + 2 * planes // 32 + 2 * planes
 
 
 def test_python_check_raises_with_message():

@@ -301,3 +301,70 @@ def test_mx8_scale_rule_and_block_independence():
     bound = torch.maximum(x.abs() * 2 ** -4, scale * 2 ** -10)
     assert ((fq - x).abs() <= bound)[~sat].all()
     assert torch.equal(fp8_emu.fake_quant_mx8(torch.zeros(32)), torch.zeros(32))
+
+
+# ----------------------------------------------------------------------------- fast mode (MXFP8)
+def test_brute_e4m3_table_matches_torch_cast():
+    """The scalar table search of brute.py agrees with torch's float8_e4m3fn cast."""
+    g = torch.Generator().manual_seed(41)
+    v = torch.cat([torch.randn(4000, generator=g) * s for s in (0.01, 1.0, 40.0, 300.0)])
+    want = v.clamp(-448, 448).to(torch.float8_e4m3fn).to(torch.float32)
+    got = torch.tensor([brute._e4m3_nearest(float(x)) for x in v])
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_mx8_matches_brute(direction):
+    """Emulated-fp8 triangle multiplication vs the scalar-loop version (independent
+    quantizer), N = 32 (one MX block along k), c = 32, random mask."""
+    N, c = 32, 32
+    w = _trimul_w(c, seed=51)
+    z = torch.randn((1, N, N, c), generator=torch.Generator().manual_seed(52))
+    pm = _rand_mask(N, 53)
+    got = ref.triangle_multiplication_mx8(z, pm, w, direction)
+    want = brute.triangle_multiplication_mx8(z, pm, w, direction)
+    _close(got, want, 1e-4)
+    # and it is a genuine perturbation of the fp32 op (quantization error well above fp32 noise)
+    exact = ref.triangle_multiplication(z, pm, w, direction)
+    rel = ((got - exact).abs().mean() / exact.abs().mean()).item()
+    assert 1e-3 < rel < 0.15, rel
+
+
+def test_transition_mx8_matches_brute():
+    c = 32
+    w = _w({"norm.weight": (c,), "norm.bias": (c,), "fc1.weight": (4 * c, c), "fc2.weight": (4 * c, c),
+            "fc3.weight": (c, 4 * c)}, 54)
+    x = torch.randn((1, 3, 5, c), generator=torch.Generator().manual_seed(55))
+    got = ref.transition_mx8(x, w)
+    _close(got, brute.transition_mx8(x, w), 1e-4)
+    exact = ref.transition(x, w)
+    rel = ((got - exact).abs().mean() / exact.abs().mean()).item()
+    assert 1e-3 < rel < 0.15, rel
+
+
+def test_mx8_quantization_axis_of_trimul():
+    """The a/b quantization runs along the contraction index: scaling one k-slice of a
+    block changes only that block's scale, so outputs for (i, j) pairs whose blocks
+    are untouched stay identical (outgoing: blocks along k = z column)."""
+    N, c = 64, 32
+    w = _trimul_w(c, seed=56)
+    z = torch.randn((1, N, N, c), generator=torch.Generator().manual_seed(57))
+    pm = torch.ones((1, N, N))
+    base = ref.triangle_multiplication_mx8(z, pm, w, "outgoing")
+    # masking one column block of k for row i=3 only changes x[3, :] (a rows) and x[:, 3] (b rows)
+    pm2 = pm.clone(); pm2[0, 3, 32:] = 0.0
+    moved = ref.triangle_multiplication_mx8(z, pm2, w, "outgoing")
+    keep = torch.ones((N, N), dtype=torch.bool); keep[3, :] = False; keep[:, 3] = False
+    assert torch.equal(moved[0][keep], base[0][keep])
+
+
+def test_mx8_partial_block_equals_zero_padding():
+    """A partial last block quantizes like the zero-padded block (the GPU's padded grid)."""
+    g = torch.Generator().manual_seed(58)
+    x = torch.randn((5, 70), generator=g) * 3
+    padded = torch.cat([x, torch.zeros((5, 26))], dim=1)
+    assert torch.equal(fp8_emu.fake_quant_mx8(x), fp8_emu.fake_quant_mx8(padded)[:, :70])
+    assert torch.equal(fp8_emu.fake_quant_mx8(x)[:, :64], fp8_emu.fake_quant_mx8(x[:, :64]))
+    # and the scalar quantizer of brute.py agrees on the partial block
+    want = torch.tensor([brute.mx8_vec([float(v) for v in row]) for row in x], dtype=torch.float64)
+    assert torch.allclose(fp8_emu.fake_quant_mx8(x).double(), want, rtol=0, atol=0)

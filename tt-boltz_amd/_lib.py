@@ -64,6 +64,28 @@ class ApbArgs(ctypes.Structure):
     ]
 
 
+class TrimulMx8Args(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int), ("N", c_int), ("C", c_int), ("hidden", c_int), ("direction", c_int),
+        ("accumulate", c_int), ("eps", c_float),
+        ("z_in", c_void_p), ("out", c_void_p), ("pair_mask", c_void_p),
+        ("norm_in_w", c_void_p), ("norm_in_b", c_void_p),
+        ("p_in_q", c_void_p), ("p_in_s", c_void_p), ("g_in_q", c_void_p), ("g_in_s", c_void_p),
+        ("norm_out_w", c_void_p), ("norm_out_b", c_void_p),
+        ("p_out_q", c_void_p), ("p_out_s", c_void_p), ("g_out_q", c_void_p), ("g_out_s", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
+    ]
+
+
+class TransitionMx8Args(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_long), ("C", c_int), ("hidden", c_int), ("accumulate", c_int), ("eps", c_float),
+        ("x_in", c_void_p), ("out", c_void_p), ("norm_w", c_void_p), ("norm_b", c_void_p),
+        ("fc1_q", c_void_p), ("fc1_s", c_void_p), ("fc2_q", c_void_p), ("fc2_s", c_void_p),
+        ("fc3_q", c_void_p), ("fc3_s", c_void_p), ("stream", c_void_p),
+    ]
+
+
 #: name -> (restype, argtypes); every symbol include/pairformer_hip.h declares.
 SIGNATURES = {
     "pf_abi_version": (c_int, []),
@@ -85,6 +107,11 @@ SIGNATURES = {
     "pf_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_int, c_void_p]),
     "pf_pair_ln_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long,
                                       c_int, c_float, c_void_p]),
+    "pf_quantize_mx8": (c_int, [c_void_p, c_long, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "pf_trimul_mx8_workspace_size": (c_size_t, [c_int, c_int, c_int]),
+    "pf_trimul_mx8_fwd": (c_int, [ctypes.POINTER(TrimulMx8Args)]),
+    "pf_trimul_mx8_contract": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "pf_transition_mx8_fwd": (c_int, [ctypes.POINTER(TransitionMx8Args)]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,679 @@
+// Fast mode (block fp8) for gfx950: MXFP8 e4m3 operands with one E8M0 scale per 32
+// elements along every contraction axis, fp32 accumulation (v_mfma_scale_f32_32x32x64_f8f6f4).
+//
+// Replaces the --fast path of the ttnn TriangleMultiplication / Transition
+// (tt_bio/tenstorrent.py:60-61, 178-181, 389-407, 431-503, 879-906), which stores these
+// operands as Tenstorrent bfloat8_b; this build uses the OCP MX format instead (format and
+// rounding in pf_common.h).  Quantization points:
+//   triangle multiplication: LN_in(z) and p_in/g_in (K = 128 channels); the gated a/b
+//     values along the contraction index k (the operand planes); LN_out(x) and p_out,
+//     LN_in(z) and g_out (K = 128).  The contraction output x is stored as fp16 * 2^-8.
+//   pair transition: LN(z) and fc1/fc2 (K = 128); silu(fc1)*fc2 and fc3 (K = 512).
+// Everything else (LayerNorm statistics, gates, residual stream) is fp32.
+//
+//   mx8_quantize_kernel  rows x K fp32 -> e4m3 bytes + E8M0 scales (weights, tests)
+//   tm8_proj_kernel      LN_in -> fp8 p_in|g_in -> a = p*sigmoid(g)*mask -> MXFP8 planes
+//   tm8_contract_kernel  X[p][i][j] = sum_k A[p][i][k] B[p][j][k], MXFP8 operands
+//   tm8_out_kernel       LN_out(X), LN_in(z) -> fp8 p_out / g_out -> gate -> residual
+//   tr8_pair_kernel      LN -> fp8 fc1|fc2 -> silu*mul -> MXFP8 -> fp8 fc3 -> residual
+#include "pf_common.h"
+#include "pf_internal.h"
+
+namespace {
+
+constexpr int C = 128;
+constexpr int WROW = 144;      // LDS pitch (bytes) of a 128-byte fp8 weight row: 9 x 16 B
+
+// ---------------------------------------------------------------------------------
+// Activation fragment of one 128-channel vector: lane (position m, half h) holds the
+// channels 32j + 16h + t (j = 0..3 = channel block, t = 0..15).  As an MFMA operand
+// for K step s (channels 64s .. 64s+63) the lane supplies bytes of blocks 2s and 2s+1
+// and the scale of block 2s + h.
+// ---------------------------------------------------------------------------------
+struct X8 {
+  i32x8 q[2];
+  int sc[2];
+};
+
+PF_DEV void load_row128_x8order(const float* __restrict__ p, int h, float (&x)[4][16]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(p + 32 * j + 16 * h + 4 * v);
+      x[j][4 * v + 0] = a[0]; x[j][4 * v + 1] = a[1]; x[j][4 * v + 2] = a[2]; x[j][4 * v + 3] = a[3];
+    }
+}
+
+// Quantize one 16-value slice of an MX block (the partner lane ^ 32 holds the other 16):
+// returns the packed bytes and the block's scale byte.
+PF_DEV i32x4 quantize16(const float (&y)[16], int& byte) {
+  float a = amax16(y);
+  a = fmaxf(a, __shfl_xor(a, 32));
+  byte = mx_scale_byte(a);
+  return e4m3_pack16(y, mx_inv_scale(byte));
+}
+
+// LayerNorm (two-pass fp32, like ln128_to_frag) of a 128-vector in x8 order, quantized
+// block by block (only one block of normalized values is live at a time).
+PF_DEV void ln128_to_x8(const float (&x)[4][16], int h, const float* __restrict__ w,
+                        const float* __restrict__ b, float eps, X8& out) {
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int t = 0; t < 16; ++t) s += x[j][t];
+  const float mean = xor32_sum(s) * (1.f / 128.f);
+  float v = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int t = 0; t < 16; ++t) { const float d = x[j][t] - mean; v += d * d; }
+  const float rstd = rsqrtf(xor32_sum(v) * (1.f / 128.f) + eps);
+  i32x4 q[4];
+  int byte[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float y[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int c = 32 * j + 16 * h + t;
+      y[t] = (x[j][t] - mean) * rstd * w[c] + b[c];
+    }
+    q[j] = quantize16(y, byte[j]);
+  }
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    out.q[s2] = cat_i32x4(q[2 * s2], q[2 * s2 + 1]);
+    out.sc[s2] = h ? byte[2 * s2 + 1] : byte[2 * s2];
+  }
+}
+
+// Weight fragment (MFMA operand) of row `row` of an fp8 [rows][128] matrix staged in LDS
+// with pitch WROW, K step s, plus its scale byte (scales staged as [rows][4]).
+PF_DEV i32x8 wfrag128(const uint8_t* lds, int row, int s, int h) {
+  const uint8_t* p = lds + row * WROW + 64 * s + 16 * h;
+  return cat_i32x4(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(p + 32));
+}
+
+// Copy an fp8 [rows][128] matrix (and its [rows][4] scales) from global to LDS.
+PF_DEV void stage_w128(const uint8_t* __restrict__ q, const uint8_t* __restrict__ sc, int rows, uint8_t* lq,
+                       uint8_t* ls, int tid, int nthreads) {
+  for (int c = tid; c < rows * 8; c += nthreads)
+    *reinterpret_cast<i32x4*>(lq + (c >> 3) * WROW + (c & 7) * 16) =
+        *reinterpret_cast<const i32x4*>(q + (c >> 3) * 128 + (c & 7) * 16);
+  for (int c = tid; c < rows; c += nthreads)
+    *reinterpret_cast<int*>(ls + 4 * c) = *reinterpret_cast<const int*>(sc + 4 * c);
+}
+
+// ---------------------------------------------------------------------------------
+// Quantize rows of K fp32 values in blocks of 32 along K.  One thread per block.
+// perm = 1 stores each block in the order its values come out of a 32x32 MFMA
+// accumulator pair (element 16h + 4j + e <- 4h + 8j + e), the column order of fc3.
+// ---------------------------------------------------------------------------------
+__global__ void mx8_quantize_kernel(const float* __restrict__ x, uint8_t* __restrict__ q,
+                                    uint8_t* __restrict__ scales, long nblocks, int perm) {
+  for (long blk = (long)blockIdx.x * blockDim.x + threadIdx.x; blk < nblocks; blk += (long)gridDim.x * blockDim.x) {
+    const float* src = x + blk * 32;
+    float v[32];
+#pragma unroll
+    for (int d = 0; d < 32; ++d) {
+      const int s = perm ? 4 * (d >> 4) + 8 * ((d >> 2) & 3) + (d & 3) : d;
+      v[d] = src[s];
+    }
+    float a = 0.f;
+#pragma unroll
+    for (int d = 0; d < 32; ++d) a = fmaxf(a, fabsf(v[d]));
+    const int byte = mx_scale_byte(a);
+    const float inv = mx_inv_scale(byte);
+    int w[8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) w[d] = e4m3_pack4(v[4 * d] * inv, v[4 * d + 1] * inv, v[4 * d + 2] * inv, v[4 * d + 3] * inv);
+    i32x4* dst = reinterpret_cast<i32x4*>(q + blk * 32);
+    dst[0] = i32x4{w[0], w[1], w[2], w[3]};
+    dst[1] = i32x4{w[4], w[5], w[6], w[7]};
+    scales[blk] = (uint8_t)byte;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Triangle multiplication input projection.  One wave = 32 consecutive positions of
+// one operand-plane row; p_in / g_in ([256][128] fp8 each) resident in LDS.  The
+// projection is computed as D[position][channel], so a lane holds one channel for 16
+// of the 32 positions and the partner lane the other 16: the MX block of the
+// contraction (32 consecutive k = positions) is reduced with one exchange.
+//   A8/B8 planes [B][128][N][N] e4m3, scales SA/SB [B][128][N][N/32] E8M0.
+// ---------------------------------------------------------------------------------
+constexpr size_t TM8P_LDS = 2 * 256 * WROW + 2 * 256 * 4;
+
+__global__ __launch_bounds__(256, 2) void tm8_proj_kernel(
+    const float* __restrict__ z, const float* __restrict__ mask, const float* __restrict__ lnw,
+    const float* __restrict__ lnb, const uint8_t* __restrict__ wp_q, const uint8_t* __restrict__ wp_s,
+    const uint8_t* __restrict__ wg_q, const uint8_t* __restrict__ wg_s, uint8_t* __restrict__ A8,
+    uint8_t* __restrict__ B8, uint8_t* __restrict__ SA, uint8_t* __restrict__ SB, int B, int N, int incoming,
+    float eps) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+  uint8_t* lp = lds8;
+  uint8_t* lg = lp + 256 * WROW;
+  uint8_t* lps = lg + 256 * WROW;
+  uint8_t* lgs = lps + 256 * 4;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
+  stage_w128(wp_q, wp_s, 256, lp, lps, tid, 256);
+  stage_w128(wg_q, wg_s, 256, lg, lgs, tid, 256);
+  __syncthreads();
+
+  const long NN = (long)N * N;
+  const long ntiles = (long)B * NN / 32;
+  const int NB = N / 32;
+  for (long tile = (long)blockIdx.x * 4 + wid; tile < ntiles; tile += (long)gridDim.x * 4) {
+    // keep the LayerNorm parameters out of registers across iterations (they are re-read
+    // from cache each tile instead of pinning 128 VGPRs)
+    asm volatile("" ::: "memory");
+    const long pos0 = tile * 32;
+    const int b = (int)(pos0 / NN);
+    const long t0 = pos0 - (long)b * NN;
+    const int orow = (int)(t0 / N);
+    const int ocol0 = (int)(t0 - (long)orow * N);
+    const int zi = incoming ? ocol0 + m : orow;
+    const int zj = incoming ? orow : ocol0 + m;
+    const long pair = ((long)b * N + zi) * N + zj;
+    X8 xq;
+    {
+      float x[4][16];
+      load_row128_x8order(z + pair * C, h, x);
+      ln128_to_x8(x, h, lnw, lnb, eps, xq);
+    }
+    const float maskv = mask ? mask[pair] : 1.f;
+    float mr[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mr[r] = __shfl(maskv, acc_row(r, h));
+
+#pragma unroll 1
+    for (int cb = 0; cb < 8; ++cb) {
+      const int row = 32 * cb + m;   // weight row = output unit of this lane's column
+      f32x16 P = zero16(), G = zero16();
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        P = mfma8(xq.q[s], wfrag128(lp, row, s, h), P, xq.sc[s], lps[4 * row + 2 * s + h]);
+        G = mfma8(xq.q[s], wfrag128(lg, row, s, h), G, xq.sc[s], lgs[4 * row + 2 * s + h]);
+      }
+      float v[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = P[r] * sigmoidf_fast(G[r]) * mr[r];
+      int byte;
+      const i32x4 q = quantize16(v, byte);
+      const int ch = 32 * (cb & 3) + m;
+      uint8_t* plane = (cb < 4 ? A8 : B8) + (((long)b * C + ch) * N + orow) * N + ocol0;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *reinterpret_cast<int*>(plane + 8 * g + 4 * h) = q[g];
+      if (h == 0) (cb < 4 ? SA : SB)[(((long)b * C + ch) * N + orow) * NB + ocol0 / 32] = (uint8_t)byte;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Contraction X[p][i][j] = sum_k A[p][i][k] * B[p][j][k] on MXFP8 planes.
+// 256x256 output tile per workgroup, 4 waves of 128x128 (as the 16-bit kernel); slabs
+// of 128 k (128 bytes per row) move global -> LDS by DMA through a 2-deep ring with the
+// same XOR row swizzle; the scale dwords (4 blocks of the slab) are prefetched into
+// registers one slab ahead.
+// ---------------------------------------------------------------------------------
+constexpr int BT = 256, SK = 128;
+constexpr int SLAB8 = BT * SK;                        // bytes per operand slab
+constexpr size_t TM8C_LDS = (size_t)2 * 2 * SLAB8;
+constexpr int vmcnt_le(int v) { return (v & 0xF) | (((v >> 4) & 3) << 14) | 0x70 | 0xF00; }
+PF_DEV int slab_swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+
+template <typename OutT>
+__global__ __launch_bounds__(256, 1) void tm8_contract_kernel(
+    const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bop, const uint8_t* __restrict__ SA,
+    const uint8_t* __restrict__ SB, OutT* __restrict__ X, int N, int tpd, int total, float out_scale) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem8[];
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wid >> 1, wn = wid & 1;
+  const int w = xcd_remap(blockIdx.x, total);
+  const int tiles = tpd * tpd;
+  const long plane = w / tiles;
+  const int t = w - (int)plane * tiles;
+  const int i0 = (t / tpd) * BT, j0 = (t % tpd) * BT;
+  const long NN = (long)N * N;
+  const int NB = N / 32;
+
+  int offA[8], offB[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int r = (8 * wid + q) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ slab_swz8(r);
+    offA[q] = min(i0 + r, N - 1) * N + 16 * c;
+    offB[q] = min(j0 + r, N - 1) * N + 16 * c;
+  }
+  const uint8_t* Ap = A + plane * NN;
+  const uint8_t* Bp = Bop + plane * NN;
+  // scale rows of this lane's fragments: A rows i0 + wm*128 + 32x + m, B rows j0 + wn*128 + 32y + m
+  const uint8_t* sArow[4];
+  const uint8_t* sBrow[4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    sArow[x] = SA + (plane * N + min(i0 + wm * 128 + 32 * x + m, N - 1)) * NB;
+    sBrow[x] = SB + (plane * N + min(j0 + wn * 128 + 32 * x + m, N - 1)) * NB;
+  }
+  auto issue = [&](int kt) {
+    uint8_t* sa = smem8 + (kt & 1) * 2 * SLAB8;
+    uint8_t* sb = sa + SLAB8;
+    const int ko = kt * SK;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_global_load_lds(Ap + offA[q] + ko, sa + (8 * wid + q) * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(Bp + offB[q] + ko, sb + (8 * wid + q) * 1024, 16, 0, 0);
+    }
+  };
+  int scA[4], scB[4], nscA[4], nscB[4];
+  auto load_scales = [&](int kt, int (&a)[4], int (&b)[4]) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      a[x] = *reinterpret_cast<const int*>(sArow[x] + 4 * kt);
+      b[x] = *reinterpret_cast<const int*>(sBrow[x] + 4 * kt);
+    }
+  };
+  const int swz = slab_swz8(m);
+  const int rdA = (wm * 128 + m) * SK, rdB = (wn * 128 + m) * SK;
+  auto read_frags = [&](int kt, int s, i32x8 (&fa)[4], i32x8 (&fb)[4]) {
+    const uint8_t* sa = smem8 + (kt & 1) * 2 * SLAB8;
+    const uint8_t* sb = sa + SLAB8;
+    const int c0 = 16 * ((4 * s + h) ^ swz), c1 = 16 * ((4 * s + 2 + h) ^ swz);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      fa[x] = cat_i32x4(*reinterpret_cast<const i32x4*>(sa + rdA + 32 * x * SK + c0),
+                        *reinterpret_cast<const i32x4*>(sa + rdA + 32 * x * SK + c1));
+      fb[x] = cat_i32x4(*reinterpret_cast<const i32x4*>(sb + rdB + 32 * x * SK + c0),
+                        *reinterpret_cast<const i32x4*>(sb + rdB + 32 * x * SK + c1));
+    }
+  };
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int y = 0; y < 4; ++y)
+#pragma unroll
+    for (int x = 0; x < 4; ++x) acc[y][x] = zero16();
+
+  const int nk = N / SK;
+  issue(0);
+  load_scales(0, nscA, nscB);
+  for (int kt = 0; kt < nk; ++kt) {
+    // slab kt and its scales landed; the barrier also frees slab kt-1's buffer
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int x = 0; x < 4; ++x) { scA[x] = nscA[x]; scB[x] = nscB[x]; }
+    if (kt + 1 < nk) {
+      issue(kt + 1);
+      load_scales(kt + 1, nscA, nscB);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      i32x8 fa[4], fb[4];
+      read_frags(kt, s, fa, fb);
+      const int sh = 8 * (2 * s + h);    // this lane supplies the scale of block 2s + h
+#pragma unroll
+      for (int y = 0; y < 4; ++y)
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+          acc[y][x] = mfma8(fb[y], fa[x], acc[y][x], (scB[y] >> sh) & 0xFF, (scA[x] >> sh) & 0xFF);
+    }
+  }
+
+  OutT* Xp = X + plane * NN;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    const int ib = i0 + wm * 128 + 32 * x;
+#pragma unroll
+    for (int y = 0; y < 4; ++y) {
+      const int jb = j0 + wn * 128 + 32 * y;
+      if (ib >= N || jb >= N) continue;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        OutT* dst = Xp + (long)(ib + m) * N + jb + 8 * g + 4 * h;
+        if constexpr (sizeof(OutT) == 4) {
+          f32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[y][x][4 * g + e] * out_scale;
+          *reinterpret_cast<f32x4*>(dst) = v;
+        } else {
+          opx4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (op_t)(acc[y][x][4 * g + e] * out_scale);
+          st_x4((op_t*)dst, v);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Triangle multiplication output: z[i,j,:] (+)= p_out(q(LN_out(X))) * sigmoid(g_out(q(LN_in(z)))).
+// A workgroup takes 128 consecutive pairs (i, j0..j0+127) per step: the X slice
+// X[b][0..127][i][j0..j0+127] (32 KB, 256-byte rows) comes in with 16-byte loads and is
+// read back from LDS channel by channel; wave w owns pairs j0 + 32w .. j0 + 32w + 31.
+// p_out/g_out ([128][128] fp8) stay in LDS.
+// ---------------------------------------------------------------------------------
+constexpr int XP = 136;        // LDS pitch (halves) of one channel row of the X slice
+constexpr size_t TM8O_LDS = 2 * 128 * WROW + 2 * 128 * 4 + (size_t)C * XP * 2;
+
+template <typename XT>
+__global__ __launch_bounds__(256, 2) void tm8_out_kernel(
+    const XT* __restrict__ X, float x_scale, const float* z_in, float* out, const float* __restrict__ lni_w,
+    const float* __restrict__ lni_b, const float* __restrict__ lno_w, const float* __restrict__ lno_b,
+    const uint8_t* __restrict__ wp_q, const uint8_t* __restrict__ wp_s, const uint8_t* __restrict__ wg_q,
+    const uint8_t* __restrict__ wg_s, int B, int N, int accumulate, float eps) {
+  static_assert(sizeof(XT) == 2, "X slice staging assumes 16-bit X");
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+  uint8_t* lp = lds8;
+  uint8_t* lg = lp + 128 * WROW;
+  uint8_t* lps = lg + 128 * WROW;
+  uint8_t* lgs = lps + 128 * 4;
+  XT* lx = reinterpret_cast<XT*>(lgs + 128 * 4);
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
+  stage_w128(wp_q, wp_s, 128, lp, lps, tid, 256);
+  stage_w128(wg_q, wg_s, 128, lg, lgs, tid, 256);
+
+  const long NN = (long)N * N;
+  const long nsteps = (long)B * NN / 128;
+  for (long step = blockIdx.x; step < nsteps; step += gridDim.x) {
+    asm volatile("" ::: "memory");             // LayerNorm parameters are re-read, not pinned
+    const long pair0 = step * 128;               // first pair of the step (same b and i)
+    const int b = (int)(pair0 / NN);
+    const long t0 = pair0 - (long)b * NN;
+    const int i = (int)(t0 / N);
+    const int j0 = (int)(t0 - (long)i * N);
+    __syncthreads();                             // previous step's readers are done
+    {
+      const XT* src = X + (long)b * C * NN + (long)i * N + j0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int c = tid + 256 * q;             // 2048 chunks of 8 halves: channel c >> 4
+        const int ch = c >> 4, col = (c & 15) * 8;
+        *reinterpret_cast<opx8*>(lx + ch * XP + col) = *reinterpret_cast<const opx8*>(src + (long)ch * NN + col);
+      }
+    }
+    __syncthreads();
+    const long pos0 = pair0 + 32 * wid;          // this wave's 32 pairs
+    X8 xo, xi;
+    {
+      float x[4][16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int tt = 0; tt < 16; ++tt) x[j][tt] = (float)lx[(32 * j + 16 * h + tt) * XP + 32 * wid + m] * x_scale;
+      ln128_to_x8(x, h, lno_w, lno_b, eps, xo);
+      load_row128_x8order(z_in + (pos0 + m) * C, h, x);
+      ln128_to_x8(x, h, lni_w, lni_b, eps, xi);
+    }
+#pragma unroll 1
+    for (int ob = 0; ob < 4; ++ob) {
+      const int row = 32 * ob + m;
+      f32x16 P = zero16(), G = zero16();
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        P = mfma8(xo.q[s], wfrag128(lp, row, s, h), P, xo.sc[s], lps[4 * row + 2 * s + h]);
+        G = mfma8(xi.q[s], wfrag128(lg, row, s, h), G, xi.sc[s], lgs[4 * row + 2 * s + h]);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const long idx = (pos0 + acc_row(r, h)) * C + 32 * ob + m;
+        const float u = P[r] * sigmoidf_fast(G[r]);
+        out[idx] = accumulate ? out[idx] + u : u;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Pair transition in fp8.  One wave = 32 pairs.  Per step hp the 64 hidden units
+// 64hp .. 64hp+63 (MX blocks 2hp, 2hp+1): fc1/fc2 rows and the matching fc3 columns
+// are staged in LDS (double buffer); fc1/fc2 run as D[hidden][pair] so a lane holds 16
+// hidden units of each block for one pair, which after silu*mul and quantization is
+// directly the fc3 A operand (fc3 columns are stored in that in-block order, perm = 1
+// of mx8_quantize_kernel).
+// ---------------------------------------------------------------------------------
+constexpr int W3ROW = 80;      // LDS pitch of a 64-byte fc3 column slice: 5 x 16 B
+constexpr size_t TR8_STAGE = 2 * 64 * WROW + 128 * W3ROW + 2 * 64 * 4 + 128 * 2;
+constexpr size_t TR8_LDS = 2 * TR8_STAGE;
+
+__global__ __launch_bounds__(256) void tr8_pair_kernel(
+    const float* x_in, float* out, const float* __restrict__ lnw, const float* __restrict__ lnb,
+    const uint8_t* __restrict__ w1q, const uint8_t* __restrict__ w1s, const uint8_t* __restrict__ w2q,
+    const uint8_t* __restrict__ w2s, const uint8_t* __restrict__ w3q, const uint8_t* __restrict__ w3s,
+    long rows, int hidden, int accumulate, float eps) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
+  const long pos0 = ((long)blockIdx.x * 4 + wid) * 32;
+  const int nblk = hidden / 32;   // MX blocks along the hidden axis
+
+  X8 xq;
+  {
+    float x[4][16];
+    load_row128_x8order(x_in + min(pos0 + m, rows - 1) * C, h, x);
+    ln128_to_x8(x, h, lnw, lnb, eps, xq);
+  }
+  f32x16 acc[4];
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob) acc[ob] = zero16();
+
+  auto stage_ptrs = [&](int buf, uint8_t*& l1, uint8_t*& l2, uint8_t*& l3, uint8_t*& s1, uint8_t*& s2,
+                        uint8_t*& s3) {
+    uint8_t* base = lds8 + buf * TR8_STAGE;
+    l1 = base; l2 = l1 + 64 * WROW; l3 = l2 + 64 * WROW;
+    s1 = l3 + 128 * W3ROW; s2 = s1 + 64 * 4; s3 = s2 + 64 * 4;
+  };
+  // stage hidden units 64hp .. 64hp+63: fc1/fc2 rows (64 x 128 B), fc3 column slices (128 x 64 B)
+  auto stage = [&](int hp, int buf) {
+    uint8_t *l1, *l2, *l3, *s1, *s2, *s3;
+    stage_ptrs(buf, l1, l2, l3, s1, s2, s3);
+    for (int c = tid; c < 64 * 8; c += 256) {
+      const long src = (long)(64 * hp + (c >> 3)) * 128 + (c & 7) * 16;
+      *reinterpret_cast<i32x4*>(l1 + (c >> 3) * WROW + (c & 7) * 16) = *reinterpret_cast<const i32x4*>(w1q + src);
+      *reinterpret_cast<i32x4*>(l2 + (c >> 3) * WROW + (c & 7) * 16) = *reinterpret_cast<const i32x4*>(w2q + src);
+    }
+    for (int c = tid; c < 128 * 4; c += 256)
+      *reinterpret_cast<i32x4*>(l3 + (c >> 2) * W3ROW + (c & 3) * 16) =
+          *reinterpret_cast<const i32x4*>(w3q + (long)(c >> 2) * hidden + 64 * hp + (c & 3) * 16);
+    if (tid < 64) {
+      *reinterpret_cast<int*>(s1 + 4 * tid) = *reinterpret_cast<const int*>(w1s + (long)(64 * hp + tid) * 4);
+      *reinterpret_cast<int*>(s2 + 4 * tid) = *reinterpret_cast<const int*>(w2s + (long)(64 * hp + tid) * 4);
+    }
+    if (tid < 128)
+      *reinterpret_cast<short*>(s3 + 2 * tid) =
+          *reinterpret_cast<const short*>(w3s + (long)tid * nblk + 2 * hp);
+  };
+
+  const int nhp = hidden / 64;
+  stage(0, 0);
+  __syncthreads();
+  for (int hp = 0; hp < nhp; ++hp) {
+    if (hp + 1 < nhp) stage(hp + 1, (hp + 1) & 1);
+    uint8_t *l1, *l2, *l3, *s1, *s2, *s3;
+    stage_ptrs(hp & 1, l1, l2, l3, s1, s2, s3);
+    i32x4 hq[2];
+    int hbyte[2];
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      const int row = 32 * bb + m;   // hidden unit 64hp + row
+      f32x16 a1 = zero16(), a2 = zero16();
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        a1 = mfma8(wfrag128(l1, row, s, h), xq.q[s], a1, s1[4 * row + 2 * s + h], xq.sc[s]);
+        a2 = mfma8(wfrag128(l2, row, s, h), xq.q[s], a2, s2[4 * row + 2 * s + h], xq.sc[s]);
+      }
+      float v[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = siluf(a1[r]) * a2[r];
+      hq[bb] = quantize16(v, hbyte[bb]);
+    }
+    const i32x8 hop = cat_i32x4(hq[0], hq[1]);
+    const int hsc = h ? hbyte[1] : hbyte[0];
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob) {
+      const int orow = 32 * ob + m;
+      const uint8_t* p = l3 + orow * W3ROW + 16 * h;
+      const i32x8 wf = cat_i32x4(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(p + 32));
+      acc[ob] = mfma8(hop, wf, acc[ob], hsc, s3[2 * orow + h]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const long p = pos0 + acc_row(r, h);
+      if (p < rows) {
+        const long idx = p * C + 32 * ob + m;
+        out[idx] = accumulate ? out[idx] + acc[ob][r] : acc[ob][r];
+      }
+    }
+}
+
+// Workspace layout of the fp8 triangle multiplication.
+struct Tm8Buffers {
+  uint8_t *A8, *B8, *SA, *SB;
+  op_t* X;
+};
+size_t tm8_buffers_size(int B, int N) {
+  const size_t planes = (size_t)B * C * N * N;
+  return 2 * planes + 2 * (planes / 32) + planes * sizeof(op_t);
+}
+Tm8Buffers tm8_buffers(void* ws, int B, int N) {
+  const size_t planes = (size_t)B * C * N * N;
+  Tm8Buffers t;
+  t.A8 = (uint8_t*)ws;
+  t.B8 = t.A8 + planes;
+  t.SA = t.B8 + planes;
+  t.SB = t.SA + planes / 32;
+  t.X = (op_t*)(t.SB + planes / 32);
+  return t;
+}
+
+int set_lds(const void* fn, size_t bytes, const char* name) {
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess)
+    return pf_fail(PF_E_LAUNCH, "%s: cannot reserve %zu bytes of LDS", name, bytes);
+  return PF_OK;
+}
+
+// grid of a wave-tile loop: enough workgroups to fill the chip several times over
+int tile_grid(long ntiles) { const long g = (ntiles + 3) / 4; return (int)(g < 2048 ? g : 2048); }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------------
+extern "C" int pf_quantize_mx8(const float* x, long rows, int K, int perm, void* q, void* scales, void* stream) {
+  if (!x || !q || !scales) return pf_fail(PF_E_INVALID, "pf_quantize_mx8: null pointer");
+  if (rows <= 0 || K <= 0 || K % 32) return pf_fail(PF_E_INVALID, "pf_quantize_mx8: need rows > 0 and K a multiple of 32");
+  if (perm != 0 && perm != 1) return pf_fail(PF_E_INVALID, "pf_quantize_mx8: perm must be 0 or 1");
+  const long nblocks = rows * (K / 32);
+  const long g = (nblocks + 255) / 256;
+  const int grid = (int)(g < 4096 ? g : 4096);
+  mx8_quantize_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(x, (uint8_t*)q, (uint8_t*)scales, nblocks, perm);
+  PF_CHECK_LAUNCH("mx8_quantize_kernel");
+  return PF_OK;
+}
+
+extern "C" size_t pf_trimul_mx8_workspace_size(int B, int N, int C_) {
+  if (B <= 0 || N <= 0 || C_ != C) return 0;
+  return tm8_buffers_size(B, N);
+}
+
+extern "C" int pf_trimul_mx8_fwd(const pf_trimul_mx8_args* a) {
+  if (!a) return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: null args");
+  if (a->C != C || a->hidden != C)
+    return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: only c_z = hidden = 128 is supported (got %d, %d)", a->C, a->hidden);
+  if (a->B <= 0 || a->N <= 0 || a->N % 128)
+    return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: need B > 0 and N a positive multiple of 128 (B=%d N=%d)",
+                   a->B, a->N);
+  if (a->direction != 0 && a->direction != 1)
+    return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: direction must be 0 (outgoing) or 1 (incoming)");
+  if (!a->z_in || !a->out || !a->norm_in_w || !a->norm_in_b || !a->p_in_q || !a->p_in_s || !a->g_in_q ||
+      !a->g_in_s || !a->norm_out_w || !a->norm_out_b || !a->p_out_q || !a->p_out_s || !a->g_out_q ||
+      !a->g_out_s || !a->workspace)
+    return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: null pointer argument");
+  const size_t need = tm8_buffers_size(a->B, a->N);
+  if (a->workspace_bytes < need)
+    return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: workspace too small (%zu < %zu bytes)", a->workspace_bytes, need);
+  static bool attr = false;
+  if (!attr) {
+    int rc = set_lds((const void*)tm8_proj_kernel, TM8P_LDS, "tm8_proj_kernel");
+    if (rc == PF_OK) rc = set_lds((const void*)tm8_contract_kernel<op_t>, TM8C_LDS, "tm8_contract_kernel");
+    if (rc == PF_OK) rc = set_lds((const void*)tm8_out_kernel<op_t>, TM8O_LDS, "tm8_out_kernel");
+    if (rc != PF_OK) return rc;
+    attr = true;
+  }
+  hipStream_t st = (hipStream_t)a->stream;
+  const int B = a->B, N = a->N;
+  Tm8Buffers t = tm8_buffers(a->workspace, B, N);
+  const long ntiles = (long)B * N * N / 32;
+  const int grid = tile_grid(ntiles);
+  // the A plane (channels 0..127 of the projection) holds a, the B plane b; the
+  // 2C-row p_in / g_in matrices are [a rows ; b rows]
+  tm8_proj_kernel<<<grid, 256, TM8P_LDS, st>>>(a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b,
+                                               (const uint8_t*)a->p_in_q, (const uint8_t*)a->p_in_s,
+                                               (const uint8_t*)a->g_in_q, (const uint8_t*)a->g_in_s, t.A8, t.B8,
+                                               t.SA, t.SB, B, N, a->direction, a->eps);
+  PF_CHECK_LAUNCH("tm8_proj_kernel");
+  const int tpd = (N + BT - 1) / BT;
+  const int total = B * C * tpd * tpd;
+  tm8_contract_kernel<op_t><<<total, 256, TM8C_LDS, st>>>(t.A8, t.B8, t.SA, t.SB, t.X, N, tpd, total, X_STORE_SCALE);
+  PF_CHECK_LAUNCH("tm8_contract_kernel");
+  const long nsteps = (long)B * N * N / 128;
+  tm8_out_kernel<op_t><<<(int)(nsteps < 2048 ? nsteps : 2048), 256, TM8O_LDS, st>>>(t.X, X_LOAD_SCALE, a->z_in, a->out, a->norm_in_w,
+                                                    a->norm_in_b, a->norm_out_w, a->norm_out_b,
+                                                    (const uint8_t*)a->p_out_q, (const uint8_t*)a->p_out_s,
+                                                    (const uint8_t*)a->g_out_q, (const uint8_t*)a->g_out_s, B, N,
+                                                    a->accumulate, a->eps);
+  PF_CHECK_LAUNCH("tm8_out_kernel");
+  return PF_OK;
+}
+
+extern "C" int pf_trimul_mx8_contract(const void* A8, const void* B8, const void* SA, const void* SB, float* X,
+                                      int planes, int N, void* stream) {
+  if (!A8 || !B8 || !SA || !SB || !X) return pf_fail(PF_E_INVALID, "pf_trimul_mx8_contract: null pointer");
+  if (planes <= 0 || N <= 0 || N % 128)
+    return pf_fail(PF_E_INVALID, "pf_trimul_mx8_contract: need planes > 0 and N a multiple of 128");
+  static bool attr = false;
+  if (!attr) {
+    const int rc = set_lds((const void*)tm8_contract_kernel<float>, TM8C_LDS, "tm8_contract_kernel");
+    if (rc != PF_OK) return rc;
+    attr = true;
+  }
+  const int tpd = (N + BT - 1) / BT;
+  const int total = planes * tpd * tpd;
+  tm8_contract_kernel<float><<<total, 256, TM8C_LDS, (hipStream_t)stream>>>(
+      (const uint8_t*)A8, (const uint8_t*)B8, (const uint8_t*)SA, (const uint8_t*)SB, X, N, tpd, total, 1.f);
+  PF_CHECK_LAUNCH("tm8_contract_kernel");
+  return PF_OK;
+}
+
+extern "C" int pf_transition_mx8_fwd(const pf_transition_mx8_args* a) {
+  if (!a) return pf_fail(PF_E_INVALID, "pf_transition_mx8_fwd: null args");
+  if (a->C != C || a->hidden <= 0 || a->hidden % 64)
+    return pf_fail(PF_E_INVALID, "pf_transition_mx8_fwd: need C = 128 and hidden a multiple of 64 (got %d, %d)",
+                   a->C, a->hidden);
+  if (a->rows <= 0) return pf_fail(PF_E_INVALID, "pf_transition_mx8_fwd: rows must be positive");
+  if (!a->x_in || !a->out || !a->norm_w || !a->norm_b || !a->fc1_q || !a->fc1_s || !a->fc2_q || !a->fc2_s ||
+      !a->fc3_q || !a->fc3_s)
+    return pf_fail(PF_E_INVALID, "pf_transition_mx8_fwd: null pointer argument");
+  static bool attr = false;
+  if (!attr) {
+    const int rc = set_lds((const void*)tr8_pair_kernel, TR8_LDS, "tr8_pair_kernel");
+    if (rc != PF_OK) return rc;
+    attr = true;
+  }
+  const long waves = (a->rows + 31) / 32;
+  const int grid = (int)((waves + 3) / 4);
+  tr8_pair_kernel<<<grid, 256, TR8_LDS, (hipStream_t)a->stream>>>(
+      a->x_in, a->out, a->norm_w, a->norm_b, (const uint8_t*)a->fc1_q, (const uint8_t*)a->fc1_s,
+      (const uint8_t*)a->fc2_q, (const uint8_t*)a->fc2_s, (const uint8_t*)a->fc3_q, (const uint8_t*)a->fc3_s,
+      a->rows, a->hidden, a->accumulate, a->eps);
+  PF_CHECK_LAUNCH("tr8_pair_kernel");
+  return PF_OK;
+}

@@ -157,3 +157,68 @@ PF_DEV int xcd_remap(int w, int total) {
 // as X * 2^-8 so |X| up to ~1.7e7 fits fp16's range; the epilogue multiplies back.
 constexpr float X_STORE_SCALE = 1.f / 256.f;
 constexpr float X_LOAD_SCALE = 256.f;
+
+// ---------------------------------------------------------------------------------
+// MXFP8 (fast mode): OCP e4m3 elements with one E8M0 power-of-two scale per 32
+// consecutive elements along the contraction axis.
+//
+//   v_mfma_scale_f32_32x32x64_f8f6f4 (cbsz = blgp = 0: e4m3 x e4m3), K = 64 per MFMA.
+//   Operand lane l (row/column r = l & 31, half h = l >> 5) holds 32 bytes (8 dwords):
+//     bytes  0..15  = elements 16h + (0..15)       of K block 0 (k  0..31)
+//     bytes 16..31  = elements 16h + (0..15)       of K block 1 (k 32..63)
+//   i.e. each 32-wide K block is split 16 + 16 between lanes r and r + 32, and the
+//   block's scale byte is supplied by lane r + 32 * block (scale operand, byte 0).
+//   A and B must agree on which (lane half, byte) carries which k; any permutation
+//   inside a block applied to both operands leaves the product unchanged.
+//   Accumulator layout as for the 16-bit MFMAs.
+// Block scale (OCP MX rule): X = 2^(floor(log2(amax)) - 8), stored as the E8M0 byte
+// floor(log2(amax)) - 8 + 127 (0 for an all-zero block); elements round-to-nearest-even
+// to e4m3 after division by X, saturating at +-448.
+// ---------------------------------------------------------------------------------
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+PF_DEV f32x16 mfma8(const i32x8& a, const i32x8& b, const f32x16& c, int scale_a, int scale_b) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, scale_a, 0, scale_b);
+}
+
+// E8M0 scale byte of a block whose absolute maximum is amax (amax >= 0, finite):
+// biased exponent of amax minus 8, clamped at 0 (covers amax == 0 and tiny blocks).
+PF_DEV int mx_scale_byte(float amax) {
+  const int be = (int)((__float_as_uint(amax) >> 23) & 0xFF);
+  return max(be - 8, 0);
+}
+
+// 1 / X for a scale byte (X = 2^(byte - 127)): 2^(127 - byte), exact for byte 0..253.
+PF_DEV float mx_inv_scale(int byte) { return __uint_as_float((uint32_t)(254 - byte) << 23); }
+
+// Four floats (already divided by the block scale) -> four e4m3 bytes (value t in byte
+// t), round to nearest even, saturating at +-448.
+PF_DEV float sat448(float v) { return fminf(fmaxf(v, -448.f), 448.f); }
+PF_DEV int e4m3_pack4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), sat448(b), 0, false);
+  return __builtin_amdgcn_cvt_pk_fp8_f32(sat448(c), sat448(d), lo, true);
+}
+
+// 16 floats -> 4 dwords of e4m3 (element t in byte t), scaled by inv.
+PF_DEV i32x4 e4m3_pack16(const float (&v)[16], float inv) {
+  i32x4 r;
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    r[d] = e4m3_pack4(v[4 * d] * inv, v[4 * d + 1] * inv, v[4 * d + 2] * inv, v[4 * d + 3] * inv);
+  return r;
+}
+
+PF_DEV i32x8 cat_i32x4(const i32x4& a, const i32x4& b) {
+  i32x8 r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+
+PF_DEV float amax16(const float (&v)[16]) {
+  float a = 0.f;
+#pragma unroll
+  for (int t = 0; t < 16; ++t) a = fmaxf(a, fabsf(v[t]));
+  return a;
+}

@@ -77,8 +77,8 @@ def convert_weights(w: Mapping[str, torch.Tensor], device: torch.device, variant
     return out
 
 
-def padded_len(n: int) -> int:
-    return -(-n // PAD) * PAD
+def padded_len(n: int, pad: int = PAD) -> int:
+    return -(-n // pad) * pad
 
 
 def pad_pair(z: torch.Tensor, n_pad: int) -> torch.Tensor:
@@ -204,6 +204,81 @@ def launch_trimul_contract(opA: torch.Tensor, opB: torch.Tensor, X: torch.Tensor
     planes, N = opA.shape[0], opA.shape[1]
     _lib.check(_lib.load(variant).pf_trimul_contract(_ptr(opA), _ptr(opB), _ptr(X), int(X.dtype == torch.float32),
                                                      planes, N, _stream()), "pf_trimul_contract", variant)
+
+
+# --------------------------------------------------------------------------------------
+# fast mode (MXFP8: e4m3 elements, one E8M0 scale per 32 along the contraction axis)
+# --------------------------------------------------------------------------------------
+FAST_PAD = 128     # the fp8 triangle multiplication works on N % 128 == 0
+
+
+def quantize_mx8(x: torch.Tensor, perm: int = 0, variant: str = DEFAULT_VARIANT):
+    """fp32 [rows, K] device tensor -> (e4m3 bytes uint8 [rows, K], E8M0 scales uint8 [rows, K/32]).
+    ``perm=1`` stores each 32-block in accumulator order (the fc3.weight layout)."""
+    _require_gpu(x)
+    xf = x.detach().to(torch.float32).contiguous()
+    rows, K = xf.shape
+    q = torch.empty((rows, K), dtype=torch.uint8, device=xf.device)
+    s = torch.empty((rows, K // 32), dtype=torch.uint8, device=xf.device)
+    _lib.check(_lib.load(variant).pf_quantize_mx8(_ptr(xf), rows, K, perm, _ptr(q), _ptr(s), _stream()),
+               "pf_quantize_mx8", variant)
+    return q, s
+
+
+def mx8_weights(w: Mapping[str, torch.Tensor], device: torch.device, keys_perm: Mapping[str, int],
+                variant: str = DEFAULT_VARIANT) -> dict:
+    """Quantize the matrices named in ``keys_perm`` (key -> perm) once, on the device:
+    returns {key + ".q": bytes, key + ".s": scales}."""
+    out = {}
+    for k, perm in keys_perm.items():
+        q, s = quantize_mx8(w[k].to(device=device, dtype=torch.float32), perm, variant)
+        out[k + ".q"], out[k + ".s"] = q, s
+    return out
+
+
+def trimul_mx8_workspace_bytes(B: int, N: int, variant: str = DEFAULT_VARIANT) -> int:
+    return _lib.load(variant).pf_trimul_mx8_workspace_size(B, N, C_Z)
+
+
+def launch_trimul_mx8(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional[torch.Tensor],
+                      w: Mapping[str, torch.Tensor], direction: int, ws: torch.Tensor, accumulate: bool,
+                      eps: float = 1e-5, variant: str = DEFAULT_VARIANT) -> None:
+    """``w``: fp32 LayerNorm params plus ``p_in.weight.q`` / ``.s`` ... from mx8_weights."""
+    B, N, _, C = z_in.shape
+    a = _lib.TrimulMx8Args(
+        B=B, N=N, C=C, hidden=C, direction=direction, accumulate=int(accumulate), eps=eps,
+        z_in=_ptr(z_in), out=_ptr(out), pair_mask=_ptr(pair_mask),
+        norm_in_w=_ptr(w["norm_in.weight"]), norm_in_b=_ptr(w["norm_in.bias"]),
+        p_in_q=_ptr(w["p_in.weight.q"]), p_in_s=_ptr(w["p_in.weight.s"]),
+        g_in_q=_ptr(w["g_in.weight.q"]), g_in_s=_ptr(w["g_in.weight.s"]),
+        norm_out_w=_ptr(w["norm_out.weight"]), norm_out_b=_ptr(w["norm_out.bias"]),
+        p_out_q=_ptr(w["p_out.weight.q"]), p_out_s=_ptr(w["p_out.weight.s"]),
+        g_out_q=_ptr(w["g_out.weight.q"]), g_out_s=_ptr(w["g_out.weight.s"]),
+        workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
+    _lib.check(_lib.load(variant).pf_trimul_mx8_fwd(ctypes.byref(a)), "pf_trimul_mx8_fwd", variant)
+
+
+def launch_transition_mx8(x_in: torch.Tensor, out: torch.Tensor, w: Mapping[str, torch.Tensor],
+                          accumulate: bool, eps: float = 1e-5, variant: str = DEFAULT_VARIANT) -> None:
+    C = x_in.shape[-1]
+    a = _lib.TransitionMx8Args(
+        rows=x_in.numel() // C, C=C, hidden=w["fc1.weight.q"].shape[0], accumulate=int(accumulate), eps=eps,
+        x_in=_ptr(x_in), out=_ptr(out), norm_w=_ptr(w["norm.weight"]), norm_b=_ptr(w["norm.bias"]),
+        fc1_q=_ptr(w["fc1.weight.q"]), fc1_s=_ptr(w["fc1.weight.s"]),
+        fc2_q=_ptr(w["fc2.weight.q"]), fc2_s=_ptr(w["fc2.weight.s"]),
+        fc3_q=_ptr(w["fc3.weight.q"]), fc3_s=_ptr(w["fc3.weight.s"]), stream=_stream())
+    _lib.check(_lib.load(variant).pf_transition_mx8_fwd(ctypes.byref(a)), "pf_transition_mx8_fwd", variant)
+
+
+def launch_trimul_mx8_contract(A8: torch.Tensor, B8: torch.Tensor, SA: torch.Tensor, SB: torch.Tensor,
+                               X: torch.Tensor, variant: str = DEFAULT_VARIANT) -> None:
+    planes, N = A8.shape[0], A8.shape[1]
+    _lib.check(_lib.load(variant).pf_trimul_mx8_contract(_ptr(A8), _ptr(B8), _ptr(SA), _ptr(SB), _ptr(X), planes,
+                                                         N, _stream()), "pf_trimul_mx8_contract", variant)
+
+
+TRIMUL_MX8_KEYS = {"p_in.weight": 0, "g_in.weight": 0, "p_out.weight": 0, "g_out.weight": 0}
+TRANSITION_MX8_KEYS = {"fc1.weight": 0, "fc2.weight": 0, "fc3.weight": 1}
 
 
 # --------------------------------------------------------------------------------------

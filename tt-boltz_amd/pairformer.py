@@ -105,14 +105,18 @@ class Options:
 
 
 class Module:
-    """Base: holds a weight scope and converts weights to device tensors once."""
+    """Base: holds a weight scope and converts weights to device tensors once.
+
+    ``fast`` is the process-global fast mode at construction time (the reference reads
+    it when it builds the modules, ``tenstorrent.py:537-539``): the triangle
+    multiplications and the pair transition then keep MXFP8 weights and run the fp8
+    kernels."""
 
     def __init__(self, state_dict, options: Optional[Options] = None):
-        if _FAST_MODE:
-            raise NotImplementedError("block-fp8 fast mode is not implemented in this build")
         self.weights = WeightScope.wrap(state_dict)
         self.options = options or Options()
         self.device = get_device()
+        self.fast = _FAST_MODE
 
     @property
     def variant(self) -> str:
@@ -137,20 +141,30 @@ class TriangleMultiplication(Module):
         if self.weights["p_in.weight"].shape != (2 * C_Z, C_Z):
             raise NotImplementedError(f"only c_z = {C_Z} is supported (p_in {tuple(self.weights['p_in.weight'].shape)})")
         self.w = {k: self.vec(k) for k in ("norm_in.weight", "norm_in.bias", "norm_out.weight", "norm_out.bias")}
-        self.w.update({k: self.mat(k) for k in ("p_in.weight", "g_in.weight", "p_out.weight", "g_out.weight")})
+        if self.fast:
+            self.w.update(ops.mx8_weights(self.weights, self.device, ops.TRIMUL_MX8_KEYS, self.variant))
+        else:
+            self.w.update({k: self.mat(k) for k in ("p_in.weight", "g_in.weight", "p_out.weight", "g_out.weight")})
 
     def workspace_bytes(self, B: int, N: int) -> int:
+        if self.fast:
+            return ops.trimul_mx8_workspace_bytes(B, N, self.variant)
         return ops.trimul_workspace_bytes(B, N, self.variant)
 
     def __call__(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                  accumulate: bool = False, ws: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """x [B,N,N,128] fp32 device, N % 64 == 0.  Returns the update (or ``out`` += update)."""
+        """x [B,N,N,128] fp32 device, N % 64 == 0 (N % 128 == 0 in fast mode).
+        Returns the update (or ``out`` += update)."""
         B, N = x.shape[0], x.shape[1]
         if ws is None:
             ws = ops.workspace(self.workspace_bytes(B, N), x.device)
         if out is None:
             out = torch.empty_like(x)
-        ops.launch_trimul(x, out, mask, self.w, int(self.ending), ws, accumulate, self.options.eps, self.variant)
+        if self.fast:
+            ops.launch_trimul_mx8(x, out, mask, self.w, int(self.ending), ws, accumulate, self.options.eps,
+                                  self.variant)
+        else:
+            ops.launch_trimul(x, out, mask, self.w, int(self.ending), ws, accumulate, self.options.eps, self.variant)
         return out
 
 
@@ -189,21 +203,31 @@ class Transition(Module):
     def __init__(self, state_dict, options: Optional[Options] = None):
         super().__init__(state_dict, options)
         self.w = {k: self.vec(k) for k in ("norm.weight", "norm.bias")}
-        self.w.update({k: self.mat(k) for k in ("fc1.weight", "fc2.weight", "fc3.weight")})
         self.C = self.weights["fc1.weight"].shape[1]
         self.hidden = self.weights["fc1.weight"].shape[0]
+        # fast mode covers the pair transition (c_z = 128); the single-track one stays 16-bit
+        self.fast = self.fast and self.C == C_Z
+        if self.fast:
+            self.w.update(ops.mx8_weights(self.weights, self.device, ops.TRANSITION_MX8_KEYS, self.variant))
+        else:
+            self.w.update({k: self.mat(k) for k in ("fc1.weight", "fc2.weight", "fc3.weight")})
 
     def workspace_bytes(self, rows: int) -> int:
+        if self.fast:
+            return 0
         return ops.transition_workspace_bytes(rows, self.C, self.hidden, self.variant)
 
     def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, accumulate: bool = False,
                  ws: Optional[torch.Tensor] = None) -> torch.Tensor:
         rows = x.numel() // self.C
+        if out is None:
+            out = torch.empty_like(x)
+        if self.fast:
+            ops.launch_transition_mx8(x, out, self.w, accumulate, self.options.eps, self.variant)
+            return out
         if ws is None:
             nb = self.workspace_bytes(rows)
             ws = ops.workspace(nb, x.device) if nb else None
-        if out is None:
-            out = torch.empty_like(x)
         ops.launch_transition(x, out, self.w, ws, accumulate, self.options.eps, self.variant)
         return out
 
@@ -371,7 +395,7 @@ class PairformerModule(nn.Module):
             raise RuntimeError("PairformerModule has no weights: call load_state_dict() first")
         dev = get_device()
         B, N = z.shape[0], z.shape[1]
-        n_pad = ops.padded_len(N)
+        n_pad = ops.padded_len(N, ops.FAST_PAD if self.module.fast else ops.PAD)
         if self._first_forward_pass or self._runtime_cache.get("shape") != (B, n_pad):
             self._build_masks(B, N, n_pad, mask, pair_mask, dev)
             self._first_forward_pass = False
