@@ -111,6 +111,9 @@ def test_trimul_config1(gpu, direction):
 
 
 def test_trimul_inplace_accumulate(gpu):
+    """In place (out aliases z_in) and into a separate buffer, accumulate=True equals the
+    plain update added to z: up to the single rounding of a fused multiply-add (the kernel
+    may form z + p*sigmoid(g) with one rounding), i.e. within a few ulps of |z| + |update|."""
     N = 128
     w = _dev_w(_sub_w(5, "tri_mul_out"), gpu)
     _, z, _, _ = _inputs(N, 12)
@@ -118,9 +121,15 @@ def test_trimul_inplace_accumulate(gpu):
     ws = ops.workspace(ops.trimul_workspace_bytes(1, N), gpu)
     upd = torch.empty_like(zd)
     ops.launch_trimul(zd, upd, None, w, 0, ws, accumulate=False)
+    want = zd + upd
+    ulp = 2.0 ** -23 * (zd.abs() + upd.abs())
     zi = zd.clone()
-    ops.launch_trimul(zi, zi, None, w, 0, ws, accumulate=True)
-    assert torch.equal(zi, zd + upd)
+    ops.launch_trimul(zi, zi, None, w, 0, ws, accumulate=True)            # in place
+    assert bool(((zi - want).abs() <= 4 * ulp).all())
+    zo = zd.clone()
+    zsrc = zd.clone()
+    ops.launch_trimul(zsrc, zo, None, w, 0, ws, accumulate=True)          # out != z_in: out += update
+    assert bool(((zo - want).abs() <= 4 * ulp).all())
 
 
 # ------------------------------------------------------------------------------ triangle attention

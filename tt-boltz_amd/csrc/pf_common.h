@@ -222,3 +222,49 @@ PF_DEV float amax16(const float (&v)[16]) {
   for (int t = 0; t < 16; ++t) a = fmaxf(a, fabsf(v[t]));
   return a;
 }
+
+// ---------------------------------------------------------------------------------
+// "Output-aligned" layout of a 128-channel row for lane (position n, half h): the lane
+// holds channels 32*(q>>2) + 8*(q&3) + 4h + e in x[4q + e] (chunk q = 0..15, e = 0..3),
+// which are exactly the rows a 32x32 accumulator D[channel][position] (A = weight
+// rows, B = activations) gives this lane for output block ob = q >> 2 in registers
+// 4*(q&3) + e.  A residual update therefore adds x[16*ob + r] to accumulator register r
+// of block ob, with no data exchange.  As an MFMA B operand, K step s (0..7) carries
+// chunks 2s and 2s+1: slot t <-> channel 16s + 8*(t>>2) + 4h + (t&3); the weight
+// (A operand) fragment of row m uses the same k order (wfrag_oa).
+// ---------------------------------------------------------------------------------
+PF_DEV int oa_channel(int q, int h) { return 32 * (q >> 2) + 8 * (q & 3) + 4 * h; }
+
+PF_DEV void load_row128_oa(const float* __restrict__ p, int h, float (&x)[64]) {
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p + oa_channel(q, h));
+    x[4 * q + 0] = a[0]; x[4 * q + 1] = a[1]; x[4 * q + 2] = a[2]; x[4 * q + 3] = a[3];
+  }
+}
+
+// LayerNorm (two-pass fp32) of a row held in output-aligned order, as 8 MFMA B fragments.
+PF_DEV void ln128_oa_to_frag(const float (&x)[64], int h, const float* __restrict__ w,
+                             const float* __restrict__ b, float eps, opx8 (&f)[8]) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) s += x[i];
+  const float mean = xor32_sum(s) * (1.f / 128.f);
+  float v = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) { const float d = x[i] - mean; v += d * d; }
+  const float rstd = rsqrtf(xor32_sum(v) * (1.f / 128.f) + eps);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int c = oa_channel(q, h);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      f[q >> 1][4 * (q & 1) + e] = (op_t)((x[4 * q + e] - mean) * rstd * w[c + e] + b[c + e]);
+  }
+}
+
+// Weight fragment (A operand) of weight row `wrow` (128 op_t, contiguous) for K step s in
+// the output-aligned k order.
+PF_DEV opx8 wfrag_oa(const op_t* wrow, int s, int h) {
+  return cat44(ld_x4(wrow + 16 * s + 4 * h), ld_x4(wrow + 16 * s + 8 + 4 * h));
+}

@@ -15,3 +15,6 @@ int pf_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3))
                      "%s launch failed: %s%s", name, hipGetErrorString(e_),          \
                      e_ == hipErrorOutOfMemory ? " (out of memory)" : "");           \
   } while (0)
+
+// Compute units of the current device (cached per device; 0 if the query fails).
+int device_cus();

@@ -41,66 +41,92 @@ PF_DEV void blk32_store(op_t* lds, int tid, const Blk32& r) {
 }
 
 // ---------------------------------------------------------------------------------
-// Input projection.  One wave = 32 consecutive positions of one operand-plane row
-// (orow, ocol0 .. ocol0+31); a workgroup = 4 waves; weights streamed through LDS.
+// Input projection.  Persistent: one workgroup (8 waves, two per SIMD, so one wave's
+// loads, LayerNorm and sigmoid work overlap the other's MFMAs) per CU keeps p_in and
+// g_in ([256][128] each) resident in LDS, and every wave walks tiles of 32 consecutive
+// positions of one operand-plane row (orow, ocol0 .. ocol0+31).  The projection is formed
+// as D[position][channel]; each 32x32 output block goes through a per-wave LDS stage
+// so that it leaves as 16-byte stores, four lanes per 64-byte plane-row segment.  The projection is formed as
+// D[position][channel], so a lane holds one channel for 16 positions and writes them
+// as 8-byte runs of 4 consecutive positions.
 // ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void tm_proj_kernel(
+constexpr int TMP_WAVES = 8;
+constexpr int SPITCH = 40;     // output staging pitch (elements): one 32-position row + 16 B
+constexpr size_t TMP_LDS = (size_t)2 * 256 * LDSW * sizeof(op_t) + (size_t)TMP_WAVES * 32 * SPITCH * sizeof(op_t);
+
+__global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
     const float* __restrict__ z, const float* __restrict__ mask,
     const float* __restrict__ lnw, const float* __restrict__ lnb,
     const op_t* __restrict__ w_p, const op_t* __restrict__ w_g,
     op_t* __restrict__ opA, op_t* __restrict__ opB, int B, int N, int incoming, float eps) {
-  __shared__ __attribute__((aligned(16))) op_t lds[2][2][32 * LDSW];
+  extern __shared__ __attribute__((aligned(16))) op_t wlds[];
+  op_t* lp = wlds;
+  op_t* lg = wlds + 256 * LDSW;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
-  const long NN = (long)N * N;
-  const long pos0 = ((long)blockIdx.x * 4 + wid) * 32;
-  const bool active = pos0 < (long)B * NN;
+  op_t* stg = wlds + 2 * 256 * LDSW + wid * 32 * SPITCH;   // this wave's output stage
+#pragma unroll 4
+  for (int c = tid; c < 256 * 16; c += 64 * TMP_WAVES) {
+    const int row = c >> 4, col = (c & 15) * 8;
+    st_x8(lp + row * LDSW + col, ld_x8(w_p + row * C + col));
+    st_x8(lg + row * LDSW + col, ld_x8(w_g + row * C + col));
+  }
+  __syncthreads();
 
-  int b = 0, orow = 0, ocol0 = 0;
-  float maskv = 0.f;
-  opx8 xf[8];
-  if (active) {
+  const long NN = (long)N * N;
+  const long ntiles = (long)B * NN / 32;
+  const long stride = (long)gridDim.x * TMP_WAVES;
+  auto tile_pair = [&](long t, int& b, int& orow, int& ocol0) -> long {
+    const long pos0 = t * 32;
     b = (int)(pos0 / NN);
     const long t0 = pos0 - (long)b * NN;
     orow = (int)(t0 / N);
     ocol0 = (int)(t0 - (long)orow * N);
     const int zi = incoming ? ocol0 + m : orow;
     const int zj = incoming ? orow : ocol0 + m;
-    const long pair = ((long)b * N + zi) * N + zj;
-    float x[64];
-    load_row128_frag(z + pair * C, h, x);
-    ln128_to_frag(x, h, lnw, lnb, eps, xf);
-    maskv = mask ? mask[pair] : 1.f;
-  }
+    return ((long)b * N + zi) * N + zj;
+  };
 
-  Blk32 rp, rg;
-  blk32_load(w_p, tid, rp);
-  blk32_load(w_g, tid, rg);
-  for (int cb = 0; cb < 8; ++cb) {
-    op_t* lp = lds[cb & 1][0];
-    op_t* lg = lds[cb & 1][1];
-    blk32_store(lp, tid, rp);
-    blk32_store(lg, tid, rg);
-    __syncthreads();
-    if (cb + 1 < 8) {
-      blk32_load(w_p + (cb + 1) * 32 * C, tid, rp);
-      blk32_load(w_g + (cb + 1) * 32 * C, tid, rg);
+  for (long t = (long)blockIdx.x * TMP_WAVES + wid; t < ntiles; t += stride) {
+    asm volatile("" ::: "memory");   // LayerNorm parameters are re-read each tile, not pinned in VGPRs
+    int cb_b, cb_orow, cb_ocol0;
+    const long pair = tile_pair(t, cb_b, cb_orow, cb_ocol0);
+    opx8 xf[8];
+    float maskv = 1.f;
+    {
+      float x[64];
+      load_row128_frag(z + pair * C, h, x);
+      if (mask) maskv = mask[pair];
+      ln128_to_frag(x, h, lnw, lnb, eps, xf);
     }
-    if (active) {
+    float mr[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mr[r] = __shfl(maskv, acc_row(r, h));
+#pragma unroll 1
+    for (int cb = 0; cb < 8; ++cb) {
+      const op_t* wp = lp + (32 * cb + m) * LDSW + 8 * h;
+      const op_t* wg = lg + (32 * cb + m) * LDSW + 8 * h;
       f32x16 ap = zero16(), ag = zero16();
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const opx8 wp = ld_x8(lp + m * LDSW + 16 * s + 8 * h);
-        const opx8 wg = ld_x8(lg + m * LDSW + 16 * s + 8 * h);
-        ap = mfma32(wp, xf[s], ap);   // rows = output channel, cols = position
-        ag = mfma32(wg, xf[s], ag);
+        ap = mfma32(xf[s], ld_x8(wp + 16 * s), ap);   // rows = position, cols = output channel
+        ag = mfma32(xf[s], ld_x8(wg + 16 * s), ag);
       }
-      op_t* dst = cb < 4 ? opA : opB;
-      const int chb = 32 * (cb & 3);
+      // lane (channel m, half h) holds positions 8g + 4h + e: stage [channel][position]
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ch = chb + acc_row(r, h);
-        const float v = ap[r] * sigmoidf_fast(ag[r]) * maskv;
-        dst[(((long)b * C + ch) * N + orow) * N + ocol0 + m] = (op_t)v;
+      for (int g = 0; g < 4; ++g) {
+        opx4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          v[e] = (op_t)(ap[r] * sigmoidf_fast(ag[r]) * mr[r]);
+        }
+        st_x4(stg + m * SPITCH + 8 * g + 4 * h, v);
+      }
+      op_t* dst = (cb < 4 ? opA : opB) + (((long)cb_b * C + 32 * (cb & 3)) * N + cb_orow) * N + cb_ocol0;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int row = 16 * q + (lane >> 2), chunk = lane & 3;
+        st_x8(dst + (long)row * N * N + 8 * chunk, ld_x8(stg + row * SPITCH + 8 * chunk));
       }
     }
   }
@@ -341,63 +367,87 @@ __global__ __launch_bounds__(256, 1) void tm_contract_dma_kernel(
 
 // ---------------------------------------------------------------------------------
 // Output: z[i,j,:] (+)= p_out(LN_out(X[:,i,j])) * sigmoid(g_out(LN_in(z[i,j,:]))).
-// One wave = 32 consecutive pairs (i, j0..j0+31); weights resident in LDS.
+// Persistent: one workgroup (8 waves) per CU keeps p_out / g_out in LDS; each wave walks
+// tiles of 32 consecutive pairs.  The tile's X slice (128 channels x 32 pairs, 64-byte
+// rows of the planes) comes in with 16-byte loads into a per-wave LDS stage and is read
+// back per channel.  Both products are formed as D[channel][pair] in the output-aligned
+// layout, so the residual z values the wave loaded for LN_in are the ones it adds to (no
+// second read of z).
 // ---------------------------------------------------------------------------------
+constexpr int TMO_WAVES = 8, XSP = 40;   // per-wave X stage: [128 channels][32 pairs + 8]
+constexpr size_t TMO_LDS = (size_t)2 * C * LDSW * sizeof(op_t) + (size_t)TMO_WAVES * C * XSP * sizeof(op_t);
+
+// resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
 template <typename XT>
-__global__ __launch_bounds__(256) void tm_out_kernel(
+__global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
     const XT* __restrict__ X, float x_scale, const float* z_in, float* out,
     const float* __restrict__ lni_w, const float* __restrict__ lni_b,
     const float* __restrict__ lno_w, const float* __restrict__ lno_b,
     const op_t* __restrict__ w_pout, const op_t* __restrict__ w_gout,
-    int B, int N, int accumulate, float eps) {
-  __shared__ __attribute__((aligned(16))) op_t sW[2][C * LDSW];
+    int B, int N, int resid, float eps) {
+  extern __shared__ __attribute__((aligned(16))) op_t olds[];
+  op_t* sWp = olds;
+  op_t* sWg = olds + C * LDSW;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int c = tid + 256 * q;   // 2048 chunks of 8 elements per matrix
+  XT* xs = reinterpret_cast<XT*>(olds + 2 * C * LDSW) + wid * C * XSP;   // this wave's X stage
+  for (int c = tid; c < C * 16; c += 64 * TMO_WAVES) {
     const int row = c >> 4, col = (c & 15) * 8;
-    st_x8(&sW[0][row * LDSW + col], ld_x8(w_pout + row * C + col));
-    st_x8(&sW[1][row * LDSW + col], ld_x8(w_gout + row * C + col));
+    st_x8(&sWp[row * LDSW + col], ld_x8(w_pout + row * C + col));
+    st_x8(&sWg[row * LDSW + col], ld_x8(w_gout + row * C + col));
   }
   __syncthreads();
-
   const long NN = (long)N * N;
-  const long pos0 = ((long)blockIdx.x * 4 + wid) * 32;
-  if (pos0 >= (long)B * NN) return;
-  const int b = (int)(pos0 / NN);
-  const long t0 = pos0 - (long)b * NN;
-  const int i = (int)(t0 / N);
-  const int j0 = (int)(t0 - (long)i * N);
-
-  float x[64];
-  opx8 xo[8], xi[8];
-  {
-    const XT* Xp = X + (long)b * C * NN + (long)i * N + j0 + m;
+  const long ntiles = (long)B * NN / 32;
+  for (long t = (long)blockIdx.x * TMO_WAVES + wid; t < ntiles; t += (long)gridDim.x * TMO_WAVES) {
+    asm volatile("" ::: "memory");   // LayerNorm parameters are re-read, not pinned in VGPRs
+    const long p0 = t * 32;                        // first pair (global index b*NN + i*N + j)
+    const int b = (int)(p0 / NN);
+    {
+      // X[b][ch][q0 .. q0+31]: 16-byte chunk c -> channel c >> 2, pairs 8*(c & 3) ..
+      const XT* src = X + (long)b * C * NN + (p0 - (long)b * NN);
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-#pragma unroll
-      for (int t = 0; t < 8; ++t) x[8 * s + t] = (float)Xp[(long)(16 * s + 8 * h + t) * NN] * x_scale;
-    ln128_to_frag(x, h, lno_w, lno_b, eps, xo);
-  }
-  const long pbase = (long)b * NN + (long)i * N + j0;   // pair index of position 0
-  load_row128_frag(z_in + (pbase + m) * C, h, x);
-  ln128_to_frag(x, h, lni_w, lni_b, eps, xi);
-
-#pragma unroll
-  for (int ob = 0; ob < 4; ++ob) {
-    f32x16 ap = zero16(), ag = zero16();
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const opx8 wp = ld_x8(&sW[0][(32 * ob + m) * LDSW + 16 * s + 8 * h]);
-      const opx8 wg = ld_x8(&sW[1][(32 * ob + m) * LDSW + 16 * s + 8 * h]);
-      ap = mfma32(xo[s], wp, ap);   // rows = pair, cols = output channel
-      ag = mfma32(xi[s], wg, ag);
+      for (int k = 0; k < 8; ++k) {
+        const int c = lane + 64 * k, ch = c >> 2, col = (c & 3) * 8;
+        *reinterpret_cast<opx8*>(xs + ch * XSP + col) = *reinterpret_cast<const opx8*>(src + (long)ch * NN + col);
+      }
     }
+    const long pair = p0 + m;
+    opx8 xo[8], xi[8];
+    float zr[64];
+    {
+      float xv[64];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const long idx = (pbase + acc_row(r, h)) * C + 32 * ob + m;
-      const float u = ap[r] * sigmoidf_fast(ag[r]);
-      out[idx] = accumulate ? out[idx] + u : u;
+      for (int q = 0; q < 16; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[4 * q + e] = (float)xs[(oa_channel(q, h) + e) * XSP + m] * x_scale;
+      ln128_oa_to_frag(xv, h, lno_w, lno_b, eps, xo);
+    }
+    load_row128_oa(z_in + pair * C, h, zr);
+    ln128_oa_to_frag(zr, h, lni_w, lni_b, eps, xi);
+#pragma unroll   // fully unrolled: zr[] must be indexed with constants to stay in VGPRs
+    for (int ob = 0; ob < 4; ++ob) {
+      const op_t* wp = &sWp[(32 * ob + m) * LDSW];
+      const op_t* wg = &sWg[(32 * ob + m) * LDSW];
+      f32x16 P = zero16(), G = zero16();
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        P = mfma32(wfrag_oa(wp, s, h), xo[s], P);   // rows = output channel, cols = pair
+        G = mfma32(wfrag_oa(wg, s, h), xi[s], G);
+      }
+      float* orow = out + pair * C;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int q = 4 * ob + g;
+        float* dst = orow + oa_channel(q, h);
+        f32x4 v;
+        if (resid == 2) v = *reinterpret_cast<const f32x4*>(dst);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float u = P[4 * g + e] * sigmoidf_fast(G[4 * g + e]);
+          v[e] = resid == 1 ? zr[4 * q + e] + u : resid == 2 ? v[e] + u : u;
+        }
+        *reinterpret_cast<f32x4*>(dst) = v;
+      }
     }
   }
 }
@@ -462,18 +512,41 @@ extern "C" int pf_trimul_fwd(const pf_trimul_args* a) {
   op_t* X = opB + planes;
 
   const long positions = (long)B * N * N;
-  const int grid_proj = (int)((positions / 32 + 3) / 4);
-  tm_proj_kernel<<<grid_proj, 256, 0, st>>>(a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b,
-                                            (const op_t*)a->p_in_w, (const op_t*)a->g_in_w, opA, opB, B, N,
-                                            a->direction, a->eps);
-  PF_CHECK_LAUNCH("tm_proj_kernel");
+  {
+    static bool attr = false;
+    if (!attr) {
+      if (hipFuncSetAttribute((const void*)tm_proj_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)TMP_LDS) != hipSuccess)
+        return pf_fail(PF_E_LAUNCH, "tm_proj_kernel: cannot reserve %zu bytes of LDS", TMP_LDS);
+      attr = true;
+    }
+    const int cus = device_cus();
+    if (cus <= 0) return pf_fail(PF_E_LAUNCH, "tm_proj_kernel: cannot query the device");
+    const int grid = (int)min((long)cus, (positions / 32 + TMP_WAVES - 1) / TMP_WAVES);
+    tm_proj_kernel<<<grid, 64 * TMP_WAVES, TMP_LDS, st>>>(a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b,
+                                               (const op_t*)a->p_in_w, (const op_t*)a->g_in_w, opA, opB, B, N,
+                                               a->direction, a->eps);
+    PF_CHECK_LAUNCH("tm_proj_kernel");
+  }
 
   const int rc = launch_contract<op_t>(opA, opB, X, B * C, N, X_STORE_SCALE, st);
   if (rc != PF_OK) return rc;
 
-  tm_out_kernel<op_t><<<grid_proj, 256, 0, st>>>(X, X_LOAD_SCALE, a->z_in, a->out, a->norm_in_w, a->norm_in_b,
-                                                 a->norm_out_w, a->norm_out_b, (const op_t*)a->p_out_w,
-                                                 (const op_t*)a->g_out_w, B, N, a->accumulate, a->eps);
+  {
+    static bool attr = false;
+    if (!attr) {
+      if (hipFuncSetAttribute((const void*)tm_out_kernel<op_t>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)TMO_LDS) != hipSuccess)
+        return pf_fail(PF_E_LAUNCH, "tm_out_kernel: cannot reserve %zu bytes of LDS", TMO_LDS);
+      attr = true;
+    }
+    const int grid = (int)min((long)device_cus(), (positions / 32 + TMO_WAVES - 1) / TMO_WAVES);
+    const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);
+    tm_out_kernel<op_t><<<grid, 64 * TMO_WAVES, TMO_LDS, st>>>(X, X_LOAD_SCALE, a->z_in, a->out, a->norm_in_w,
+                                                               a->norm_in_b, a->norm_out_w, a->norm_out_b,
+                                                               (const op_t*)a->p_out_w, (const op_t*)a->g_out_w, B, N,
+                                                               resid, a->eps);
+  }
   PF_CHECK_LAUNCH("tm_out_kernel");
   return PF_OK;
 }
