@@ -25,8 +25,9 @@
 //            come from v_dot2 over the rounded P that the MFMA consumes.  K/V and the
 //            next bias tile are prefetched one step ahead.  Output O (normalized,
 //            ungated) op_t [B][N(i)][N(j)][H*D].
-//   ta_out   o-proj epilogue: gate recomputed from LN(z) (MFMA), o*sigmoid(g) built in
-//            registers as the next MFMA's A operand, linear_o, residual into z.
+//   ta_out   o-proj epilogue (persistent, W_g / W_o in LDS, output-aligned layout): gate
+//            recomputed from LN(z) (MFMA), o*sigmoid(g) built in registers as linear_o's B
+//            operand, residual added to the z values the lane loaded for the LayerNorm.
 #include "pf_common.h"
 #include "pf_internal.h"
 
@@ -329,63 +330,81 @@ __global__ __launch_bounds__(256, 2) void ta_attn_kernel(
 
 // ---------------------------------------------------------------------------------
 // Output projection: z[pair(i, j)] (+)= linear_o(O[i, j] * sigmoid(linear_g(LN(z[pair])))).
-// One wave = 32 frame positions (ip, j0 .. j0+31); W_g, W_o resident in LDS, W_g rows
-// stored perm16-permuted so the gate accumulator is already in O's k order.
+// Persistent: one workgroup (8 waves) per CU keeps W_g and W_o in LDS; each wave walks
+// tiles of 32 frame positions (ip, j0 .. j0+31).  Everything is in the output-aligned
+// layout (pf_common.h): the gate comes out of D[channel][position] = W_g . LN(z) in the
+// same channel order as the O values the lane loads, o * sigmoid(g) is directly the B
+// operand of D[out][position] = W_o . (o * g), and the residual is the z the lane loaded.
 // ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void ta_out_kernel(
+constexpr int TAO_WAVES = 8;
+constexpr size_t TAO_LDS = (size_t)2 * C * LDSW * sizeof(op_t);
+
+// resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
+__global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
     const op_t* __restrict__ O, const float* z_in, float* out, const float* __restrict__ lnw,
     const float* __restrict__ lnb, const op_t* __restrict__ wg, const op_t* __restrict__ wo,
-    int B, int N, int ending, int accumulate, float eps) {
-  __shared__ __attribute__((aligned(16))) op_t sW[2][C * LDSW];
+    int B, int N, int ending, int resid, float eps) {
+  extern __shared__ __attribute__((aligned(16))) op_t tlds[];
+  op_t* sWg = tlds;
+  op_t* sWo = tlds + C * LDSW;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int c = tid + 256 * q;
+  for (int c = tid; c < C * 16; c += 64 * TAO_WAVES) {
     const int row = c >> 4, col = (c & 15) * 8;
-    st_x8(&sW[0][perm16(row) * LDSW + col], ld_x8(wg + row * C + col));
-    st_x8(&sW[1][row * LDSW + col], ld_x8(wo + row * C + col));
+    st_x8(&sWg[row * LDSW + col], ld_x8(wg + row * C + col));
+    st_x8(&sWo[row * LDSW + col], ld_x8(wo + row * C + col));
   }
   __syncthreads();
   const long NN = (long)N * N;
-  const long pos0 = ((long)blockIdx.x * 4 + wid) * 32;
-  if (pos0 >= (long)B * NN) return;
-  const int b = (int)(pos0 / NN);
-  const long t0 = pos0 - (long)b * NN;
-  const int ip = (int)(t0 / N);
-  const int j0 = (int)(t0 - (long)ip * N);
-  auto zpair = [&](int j) -> long {
-    return ending ? ((long)b * N + j) * N + ip : ((long)b * N + ip) * N + j;
-  };
-
-  opx8 xf[8], og[8];
-  {
-    float x[64];
-    load_row128_frag(z_in + zpair(j0 + m) * C, h, x);
-    ln128_to_frag(x, h, lnw, lnb, eps, xf);
-  }
-  const op_t* Op = O + (((long)b * N + ip) * N + j0 + m) * C;
+  const long ntiles = (long)B * NN / 32;
+  for (long t = (long)blockIdx.x * TAO_WAVES + wid; t < ntiles; t += (long)gridDim.x * TAO_WAVES) {
+    asm volatile("" ::: "memory");   // LayerNorm parameters are re-read, not pinned in VGPRs
+    const long pos0 = t * 32;
+    const int b = (int)(pos0 / NN);
+    const long t0 = pos0 - (long)b * NN;
+    const int ip = (int)(t0 / N);
+    const int j = (int)(t0 - (long)ip * N) + m;
+    const long zp = ending ? ((long)b * N + j) * N + ip : ((long)b * N + ip) * N + j;
+    float zr[64];
+    opx8 xf[8];
+    load_row128_oa(z_in + zp * C, h, zr);
+    ln128_oa_to_frag(zr, h, lnw, lnb, eps, xf);
+    // o * sigmoid(g) as the B operand of the output projection (k order = output-aligned)
+    opx8 og[8];
+    const op_t* orow = O + (pos0 + m) * C;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) og[s] = ld_x8(Op + 16 * s + 8 * h);
+    for (int cb = 0; cb < 4; ++cb) {
+      const op_t* wrow = &sWg[(32 * cb + m) * LDSW];
+      f32x16 g = zero16();
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
-    f32x16 g = zero16();
+      for (int s = 0; s < 8; ++s) g = mfma32(wfrag_oa(wrow, s, h), xf[s], g);   // D[channel][position]
 #pragma unroll
-    for (int s = 0; s < 8; ++s) g = mfma32(ld_x8(&sW[0][(32 * cb + m) * LDSW + 16 * s + 8 * h]), xf[s], g);
+      for (int gg = 0; gg < 4; ++gg) {
+        const int q = 4 * cb + gg;            // chunk: channels oa_channel(q, h) + 0..3
+        const opx4 ov = ld_x4(orow + oa_channel(q, h));
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
+        for (int e = 0; e < 4; ++e)
+          og[q >> 1][4 * (q & 1) + e] = (op_t)((float)ov[e] * sigmoidf_fast(g[4 * gg + e]));
+      }
+    }
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
-        og[2 * cb + s2][t] = (op_t)((float)og[2 * cb + s2][t] * sigmoidf_fast(g[8 * s2 + t]));
-  }
+    for (int ob = 0; ob < 4; ++ob) {
+      const op_t* wrow = &sWo[(32 * ob + m) * LDSW];
+      f32x16 acc = zero16();
 #pragma unroll
-  for (int ob = 0; ob < 4; ++ob) {
-    f32x16 acc = zero16();
+      for (int s = 0; s < 8; ++s) acc = mfma32(wfrag_oa(wrow, s, h), og[s], acc);   // D[out][position]
 #pragma unroll
-    for (int s = 0; s < 8; ++s) acc = mfma32(og[s], ld_x8(&sW[1][(32 * ob + m) * LDSW + 16 * s + 8 * h]), acc);
+      for (int gg = 0; gg < 4; ++gg) {
+        const int q = 4 * ob + gg;
+        float* dst = out + zp * C + oa_channel(q, h);
+        f32x4 v;
+        if (resid == 2) v = *reinterpret_cast<const f32x4*>(dst);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const long idx = zpair(j0 + acc_row(r, h)) * C + 32 * ob + m;
-      out[idx] = accumulate ? out[idx] + acc[r] : acc[r];
+        for (int e = 0; e < 4; ++e) {
+          const float u = acc[4 * gg + e];
+          v[e] = resid == 1 ? zr[4 * q + e] + u : resid == 2 ? v[e] + u : u;
+        }
+        *reinterpret_cast<f32x4*>(dst) = v;
+      }
     }
   }
 }
@@ -480,8 +499,20 @@ extern "C" int pf_triatt_fwd(const pf_triatt_args* a) {
   const int total = B * (N / 4) * (N / 64);
   ta_attn_kernel<false><<<total, 256, 0, st>>>(t.Q, t.K, t.Vt, t.bias2, t.M2, t.O, nullptr, N, total);
   PF_CHECK_LAUNCH("ta_attn_kernel");
-  ta_out_kernel<<<grid_pos, 256, 0, st>>>(t.O, a->z_in, a->out, a->ln_w, a->ln_b, (const op_t*)a->w_g,
-                                          (const op_t*)a->w_o, B, N, a->ending, a->accumulate, a->eps);
+  {
+    static bool attr = false;
+    if (!attr) {
+      if (hipFuncSetAttribute((const void*)ta_out_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)TAO_LDS) != hipSuccess)
+        return pf_fail(PF_E_LAUNCH, "ta_out_kernel: cannot reserve %zu bytes of LDS", TAO_LDS);
+      attr = true;
+    }
+    const int grid = (int)min((long)device_cus(), (positions / 32 + TAO_WAVES - 1) / TAO_WAVES);
+    const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);
+    ta_out_kernel<<<grid, 64 * TAO_WAVES, TAO_LDS, st>>>(t.O, a->z_in, a->out, a->ln_w, a->ln_b,
+                                                         (const op_t*)a->w_g, (const op_t*)a->w_o, B, N, a->ending,
+                                                         resid, a->eps);
+  }
   PF_CHECK_LAUNCH("ta_out_kernel");
   return PF_OK;
 }
