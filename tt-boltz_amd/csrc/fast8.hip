@@ -221,7 +221,6 @@ __global__ __launch_bounds__(256, 2) void tm8_proj_kernel(
 constexpr int BT = 256, SK = 128;
 constexpr int SLAB8 = BT * SK;                        // bytes per operand slab
 constexpr size_t TM8C_LDS = (size_t)2 * 2 * SLAB8;
-constexpr int vmcnt_le(int v) { return (v & 0xF) | (((v >> 4) & 3) << 14) | 0x70 | 0xF00; }
 PF_DEV int slab_swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 
 template <typename OutT>

@@ -145,6 +145,10 @@ PF_DEV void ln128_to_frag(const float (&x)[64], int h, const float* __restrict__
   }
 }
 
+// s_waitcnt immediate (gfx9 encoding) that waits until at most v vector-memory
+// operations of this wave are outstanding and leaves expcnt / lgkmcnt unconstrained.
+constexpr int vmcnt_le(int v) { return (v & 0xF) | (((v >> 4) & 3) << 14) | 0x70 | 0xF00; }
+
 // Workgroup-id remap so that consecutive logical ids land on one XCD.
 // Hardware dispatches workgroup w to XCD (w % 8); with total % 8 == 0 this maps
 // the ids seen by XCD x to the contiguous range [x*total/8, (x+1)*total/8).

@@ -10,24 +10,19 @@
 //
 //   ta_proj  LN(z) -> q (pre-scaled by log2(e)/sqrt(d)), k, v^T, per-head bias
 //            (x log2(e)) and the per-(row, key) additive mask term, one pass over z.
-//              Q, K  op_t [B][N(row i)][H][N(j)][D]
-//              Vt    op_t [B][N(row i)][H][D][N(k)]
-//              bias2 fp32 [B][H][N(j)][N(k)]   (shared by all rows i)
-//              M2    fp32 [B][N(i)][N(k)]      1e9*(mask-1)*log2(e), -inf for padding
-//   ta_attn  flash attention.  A workgroup = 4 waves = 4 frame rows sharing one block of
-//            64 queries, so every bias tile [64 q][64 k] is fetched once into LDS and
-//            used by 4 rows; each wave loops over the 4 heads.  Scores are kept in the
-//            transposed layout S^T[key][query]: each lane owns one query, the bias tile
-//            is loaded straight into the MFMA accumulator, softmax statistics are per
-//            lane (plus one cross-half exchange), and P feeds the P.V MFMA from
-//            registers via the k-permutation of pf_common.h.  Online softmax with lazy
-//            rescaling (the reference max only moves when it grows by > 2^8); row sums
-//            come from v_dot2 over the rounded P that the MFMA consumes.  K/V and the
-//            next bias tile are prefetched one step ahead.  Output O (normalized,
-//            ungated) op_t [B][N(i)][N(j)][H*D].
+//              Q, K    op_t [B][N(row i)][H][N(j)][D]
+//              Vt      op_t [B][N(row i)][H][D][N(k)], keys stored at perm16(k) (bits 2
+//                      and 3 swapped) so a P.V operand fragment is one 16-byte run
+//              bias16  op_t [B][H][N(j)][N(k)]   (shared by all rows i)
+//              mask16  op_t [B][N(i)][N(k)]      0, or -inf for masked / padding keys
+//   ta_attn  flash attention (see the kernel's comment): 8-wave workgroups of 4 frame rows
+//            x 128 queries, LDS-DMA ring, bias / mask / reference max folded into MFMAs,
+//            lazy-max softmax.  Output O (normalized, ungated) op_t [B][N(i)][N(j)][H*D].
 //   ta_out   o-proj epilogue (persistent, W_g / W_o in LDS, output-aligned layout): gate
 //            recomputed from LN(z) (MFMA), o*sigmoid(g) built in registers as linear_o's B
 //            operand, residual added to the z values the lane loaded for the LayerNorm.
+#include <type_traits>
+
 #include "pf_common.h"
 #include "pf_internal.h"
 
@@ -47,6 +42,13 @@ PF_DEV float dot2_ones(const opx2& p, float acc) {
   const opx2 one = {(op_t)1.f, (op_t)1.f};
   return __builtin_amdgcn_fdot2(p, one, acc, false);
 #endif
+}
+
+// Additive mask term of one (row, key), log2 units: -inf for padding keys and for the
+// reference's 1e9*(mask-1) whenever that is beyond op_t's range (a masked key).
+PF_DEV op_t mask_term(bool pad, float mv) {
+  const float t = 1e9f * (mv - 1.f) * LOG2E;
+  return (op_t)(pad || t < -65504.f ? -INFINITY : t);
 }
 
 struct Blk32 { opx8 v[2]; };
@@ -76,7 +78,7 @@ __global__ __launch_bounds__(256) void ta_proj_kernel(
     const float* __restrict__ lnw, const float* __restrict__ lnb,
     const op_t* __restrict__ wq, const op_t* __restrict__ wk, const op_t* __restrict__ wv,
     const op_t* __restrict__ wb, op_t* __restrict__ Q, op_t* __restrict__ K,
-    op_t* __restrict__ Vt, float* __restrict__ bias2, float* __restrict__ M2,
+    op_t* __restrict__ Vt, op_t* __restrict__ bias16, op_t* __restrict__ mask16,
     int B, int N, int n_valid, int ending, float qscale, float eps) {
   __shared__ __attribute__((aligned(16))) op_t lds[2][32 * LDSW];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
@@ -100,7 +102,7 @@ __global__ __launch_bounds__(256) void ta_proj_kernel(
     if (h == 0) {
       // frame key j0+m of row ip: padding -> excluded; otherwise inf*(mask-1) (log2 units)
       const float mv = pair_mask ? pair_mask[pair] : 1.f;
-      M2[((long)b * N + ip) * N + j0 + m] = j0 + m >= n_valid ? -INFINITY : 1e9f * (mv - 1.f) * LOG2E;
+      mask16[((long)b * N + ip) * N + j0 + m] = mask_term(j0 + m >= n_valid, mv);
     }
   }
 
@@ -131,12 +133,12 @@ __global__ __launch_bounds__(256) void ta_proj_kernel(
 #pragma unroll
       for (int s = 0; s < 8; ++s) acc = mfma32(ld_x8(lw + m * LDSW + 16 * s + 8 * h), xf[s], acc);
       if (bk < 12) {
-        const long base = (((long)b * N + ip) * H + (bk - 8)) * D * (long)N + j0 + m;
+        const long base = (((long)b * N + ip) * H + (bk - 8)) * D * (long)N + j0 + perm16(m);
 #pragma unroll
         for (int r = 0; r < 16; ++r) Vt[base + (long)acc_row(r, h) * N] = (op_t)acc[r];
       } else if (h == 0) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) bias2[(((long)b * H + r) * N + ip) * N + j0 + m] = acc[r] * LOG2E;
+        for (int r = 0; r < 4; ++r) bias16[(((long)b * H + r) * N + ip) * N + j0 + m] = (op_t)(acc[r] * LOG2E);
       }
     }
   }
@@ -145,187 +147,315 @@ __global__ __launch_bounds__(256) void ta_proj_kernel(
 // ---------------------------------------------------------------------------------
 // Flash attention.  OUT_F32 = false: O op_t [B][N][N][H*D] (frame pair layout);
 // OUT_F32 = true: O fp32 [B][N][H][N][D] (the standalone attention-core API).
+//
+// A workgroup is 8 waves: 4 frame rows (ip0 .. ip0+3) x 2 blocks of 64 queries; it walks
+// 4 heads x N/64 key tiles.  Per step the workgroup's bias tile [128 q][64 k], the four
+// rows' K [64 k][32 d] and V^T [32 d][64 k] tiles and their mask entries move
+// global -> LDS by DMA (global_load_lds, no VGPR staging) through a 3-deep ring, one
+// barrier per step.  Scores S'^T[key][query] come out of five MFMAs per 32x32 tile:
+//     K.Q^T (2)  +  I.bias^T (2: identity A operand, op_t bias as the B operand)
+//                +  [1, mask[key]] . [-m[q], 1]^T (1: two used k-slots)
+// so the bias, the key mask and the reference max cost no VALU; the softmax is exp2,
+// an fp16 pair pack and v_dot2 row sums.  The reference max m[q] is kept as an op_t
+// value (exact as an MFMA operand) and moves lazily: at a head's first tile, while a
+// query has seen no unmasked key, or when a tile's row sum exceeds 2^14 (some P above
+// 2^9).  A P that would overflow op_t fails the same test before it reaches the P.V
+// MFMA, and the tile is then redone from S' with the new reference.
+// Waves w and w+4 share a SIMD.  Waves 4..7 run each step rotated by half a step
+// (softmax + P.V of step t-1, then the score MFMAs of step t), so while one wave of the
+// pair issues score MFMAs the other issues its softmax VALU work.
+// Rows whose valid keys are all masked: the fp32 reference adds -1e9 to every logit,
+// which rounds them all to -1e9 (|logit| < 32), i.e. a uniform average over the keys.
+// Such a row zeroes Q and the identity operand and feeds mask 0 for its valid keys.
 // ---------------------------------------------------------------------------------
-constexpr int BP = 68;   // bias LDS pitch (floats): conflict-free b128 column reads
+constexpr int TA_WAVES = 8;
+constexpr int TS_BIAS = 0, TS_K = 16384, TS_V = 32768, TS_MASK = 49152, TS_STAGE = 50176;   // bytes
+constexpr size_t TA_LDS = 3 * (size_t)TS_STAGE;
+constexpr float LSTEP_MAX = 16384.f;   // per-lane row sum of one tile that forces a rescale
+
+// 16-byte chunk swizzles: rows of 8 chunks (bias, V^T) and of 4 chunks (K).  A fragment
+// read takes one chunk from each of 32 consecutive rows; any 16 consecutive rows land in
+// 16 distinct 16-byte bank groups.
+PF_DEV int swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+PF_DEV int swz4(int r) { return (r >> 2) & 3; }
+#define PF_INLINE __attribute__((always_inline))
+PF_DEV opx8 lds_x8(const char* p) { return *reinterpret_cast<const opx8*>(p); }
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+PF_DEV uint32_t half_bits(op_t v) { return __builtin_bit_cast(uint16_t, v); }
+PF_DEV opx8 as_x8(const u32x4& v) { return __builtin_bit_cast(opx8, v); }
+// operand whose slots 0 and 1 are (lo, hi) in lanes 0..31 and zero elsewhere
+PF_DEV opx8 slots01(int h, uint32_t lo_hi) {
+  const u32x4 v = {h ? 0u : lo_hi, 0u, 0u, 0u};
+  return as_x8(v);
+}
 
 template <bool OUT_F32>
-__global__ __launch_bounds__(256, 2) void ta_attn_kernel(
+__global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
     const op_t* __restrict__ Q, const op_t* __restrict__ K, const op_t* __restrict__ Vt,
-    const float* __restrict__ bias2, const float* __restrict__ M2, op_t* __restrict__ O16,
-    float* __restrict__ O32, int N, int total) {
-  __shared__ __attribute__((aligned(16))) float sBias[2][64 * BP];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
-  const int nJB = N / 64, nIB = N / 4, nKB = N / 64;
+    const op_t* __restrict__ bias16, const op_t* __restrict__ mask16, op_t* __restrict__ O16,
+    float* __restrict__ O32, int N, int n_valid, int total) {
+  extern __shared__ __attribute__((aligned(16))) char alds[];
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row = wid & 3, qw = wid >> 2;
+  const bool odd = qw == 1;
+  const int nQP = (N + 127) >> 7, nKB = N >> 6, T = H * nKB;
   const int w = xcd_remap(blockIdx.x, total);
-  const int b = w / (nIB * nJB);
-  const int rem = w - b * nIB * nJB;
-  const int ib = rem / nJB;
-  const int j0 = (rem - ib * nJB) * 64;
-  const int ip = ib * 4 + wid;          // this wave's frame row
+  const int per_b = (N >> 2) * nQP;
+  const int b = w / per_b;
+  const int rem = w - b * per_b;
+  const int rg = rem / nQP;
+  const int jw0 = (rem - rg * nQP) * 128;
+  const int ip0 = 4 * rg, ip = ip0 + row;
+  const int jq0 = jw0 + 64 * qw;
+  const bool qvalid = jq0 < N;            // the second block of a trailing half pair idles
   const long NN = (long)N * N;
-  const float* Mr = M2 + ((long)b * N + ip) * N;
+  const int seqD = N * D;                 // elements of one (row, head) Q / K / V^T block
 
-  // does any key of this row carry a mask/padding term?  (wave-uniform)
-  bool masked = false;
-  for (int k = lane; k < N; k += 64) masked |= (Mr[k] != 0.f);
-  masked = __ballot(masked) != 0;
-
-  const long rowbase = ((long)b * N + ip) * H;   // + head
-  const int steps = H * nKB;
-
-  // ---- prefetch state: bias tile (4 x float4 per thread), K and V fragments ----
-  f32x4 breg[4];
-  opx8 kreg[2][2], vreg[2][2];
-  auto bias_load = [&](int t) {
+  // ---- DMA sources: chunk e = tid + 512 i of each 16 KB tile ----
+  const op_t* bias_b = bias16 + (long)b * H * NN;
+  const op_t* k_b = K + ((long)b * N + ip0) * H * seqD;
+  const op_t* v_b = Vt + ((long)b * N + ip0) * H * seqD;
+  const op_t* mask_b = mask16 + ((long)b * N + ip0) * N;
+  // byte offsets from wave-uniform bases (32-bit: one VGPR each, the base stays scalar)
+  uint32_t offB[2], offK[2], offV[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int e = tid + 512 * i;
+    const int q = e >> 3;
+    offB[i] = 2u * (min(jw0 + q, N - 1) * N + 8 * ((e & 7) ^ swz8(q)));
+    const int rk = e >> 8, key = (e >> 2) & 63;
+    offK[i] = 2u * (rk * H * seqD + key * D + 8 * ((e & 3) ^ swz4(key)));
+    const int d = (e >> 3) & 31;
+    offV[i] = 2u * (rk * H * seqD + d * N + 8 * ((e & 7) ^ swz8(d)));
+  }
+  const uint32_t offM = 2u * (((lane >> 3) & 3) * N + 8 * (lane & 7));
+  auto issue = [&](int t) PF_INLINE {
     const int hd = t / nKB, kb0 = (t - hd * nKB) * 64;
-    const float* src = bias2 + ((long)b * H + hd) * NN + (long)j0 * N + kb0;
+    char* st = alds + (t % 3) * TS_STAGE;
+    const char* bs = (const char*)(bias_b + (long)hd * NN + kb0);
+    const char* ks = (const char*)(k_b + hd * seqD + kb0 * D);
+    const char* vs = (const char*)(v_b + hd * seqD + kb0);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int c = tid + 256 * q;
-      breg[q] = *reinterpret_cast<const f32x4*>(src + (long)(c >> 4) * N + (c & 15) * 4);
+    for (int i = 0; i < 2; ++i) {
+      __builtin_amdgcn_global_load_lds(bs + offB[i], st + TS_BIAS + 1024 * wid + 8192 * i, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(ks + offK[i], st + TS_K + 1024 * wid + 8192 * i, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vs + offV[i], st + TS_V + 1024 * wid + 8192 * i, 16, 0, 0);
     }
+    if (wid == 0)
+      __builtin_amdgcn_global_load_lds((const char*)(mask_b + kb0) + offM, st + TS_MASK, 16, 0, 0);
   };
-  auto kv_load = [&](int t) {
-    const int hd = t / nKB, kb0 = (t - hd * nKB) * 64;
-    const op_t* Kh = K + (rowbase + hd) * N * D;
-    const op_t* Vh = Vt + (rowbase + hd) * D * N;
+
+  // ---- per-lane LDS read addresses (bytes from a stage base) ----
+  const int sw = swz8(m), ksw = swz4(m);
+  int aB[4], aK[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+  for (int u = 0; u < 4; ++u)            // u = 2*kb + s: chunk 2u + h of a 64-key row
+    aB[u] = TS_BIAS + 128 * (64 * qw + m) + 16 * ((2 * u + h) ^ sw);
+  const int dV = TS_V - TS_BIAS + 4096 * row - 8192 * qw;   // V^T chunk (m, c) sits at aB + dV
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        kreg[kb][s] = ld_x8(Kh + (long)(kb0 + 32 * kb + m) * D + 16 * s + 8 * h);
-        const op_t* vp = Vh + (long)m * N + kb0 + 32 * kb + 16 * s + 4 * h;
-        vreg[kb][s] = cat44(ld_x4(vp), ld_x4(vp + 8));
-      }
+  for (int s = 0; s < 2; ++s) aK[s] = TS_K + 4096 * row + 64 * m + 16 * ((2 * s + h) ^ ksw);
+  const int aM = TS_MASK + 128 * row + 2 * m;
+
+  // rows whose valid keys are all masked (wave-uniform)
+  bool live_l = false;
+  {
+    const op_t* mr = mask16 + ((long)b * N + ip) * N;
+    for (int k = lane; k < n_valid; k += 64) live_l |= (float)mr[k] != -INFINITY;
+  }
+  const bool live = __ballot(live_l) != 0;
+
+  // identity A operand of k-step s: lane (row m, half h) slot t is 1 iff m == 16s + 8h + t
+  const uint32_t ONE = half_bits((op_t)1.f);
+  opx8 iden[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int t = m - 16 * s - 8 * h;   // the slot holding the 1, if in 0..7
+    u32x4 v;
+#pragma unroll
+    for (int wd = 0; wd < 4; ++wd)
+      v[wd] = !live || (t >> 1) != wd ? 0u : (t & 1) ? ONE << 16 : ONE;
+    iden[s] = as_x8(v);
+  }
+  auto fold_b = [&](float mv) PF_INLINE { return slots01(h, half_bits((op_t)(-mv)) | ONE << 16); };
+
+  const int jq = min(jq0, N - 64);
+  opx8 qf[2][2], qn[2][2], fb[2];
+  u32x4 pf[2][2][2];
+  f32x16 sc[2][2], o[2];
+  float mh[2], lsum[2];
+  bool mset[2];
+  auto q_load = [&](int hd) PF_INLINE {
+    const op_t* qp = Q + ((((long)b * N + ip) * H + hd) * N + jq) * D;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) qn[qb][s] = ld_x8(qp + (32 * qb + m) * D + 16 * s + 8 * h);
   };
-  bias_load(0);
-  kv_load(0);
-
-  opx8 qf[2][2];
-  f32x16 o[2];
-  float mref[2], lsum[2];
-
-  for (int t = 0; t < steps; ++t) {
-    const int hd = t / nKB, kbi = t - hd * nKB, kb0 = kbi * 64;
-    float* bt = sBias[t & 1];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int c = tid + 256 * q;
-      *reinterpret_cast<f32x4*>(&bt[(c >> 4) * BP + (c & 15) * 4]) = breg[q];
-    }
-    opx8 kc[2][2], vc[2][2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) { kc[kb][s] = kreg[kb][s]; vc[kb][s] = vreg[kb][s]; }
-    __syncthreads();
-    if (t + 1 < steps) { bias_load(t + 1); kv_load(t + 1); }
-
-    if (kbi == 0) {   // head start
-      const op_t* Qh = Q + (rowbase + hd) * N * D;
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) qf[qb][s] = ld_x8(Qh + (long)(j0 + 32 * qb + m) * D + 16 * s + 8 * h);
-        o[qb] = zero16();
-        mref[qb] = -INFINITY;
-        lsum[qb] = 0.f;
-      }
-    }
-
-    // S^T = bias + K Q^T   (rows = keys, cols = queries)
-    f32x16 sc[2][2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 bv = *reinterpret_cast<const f32x4*>(&bt[(32 * qb + m) * BP + 32 * kb + 8 * g + 4 * h]);
-          sc[kb][qb][4 * g + 0] = bv[0]; sc[kb][qb][4 * g + 1] = bv[1];
-          sc[kb][qb][4 * g + 2] = bv[2]; sc[kb][qb][4 * g + 3] = bv[3];
-        }
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) sc[kb][qb] = mfma32(kc[kb][s], qf[qb][s], sc[kb][qb]);
-    if (masked) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 mv = *reinterpret_cast<const f32x4*>(Mr + kb0 + 32 * kb + 8 * g + 4 * h);
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sc[kb][qb][4 * g + e] += mv[e];
-        }
-    }
-
-    opx8 pf[2][2][2];   // [qb][kb][ks]
+  auto head_start = [&]() PF_INLINE {
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      float mx = sc[0][qb][0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[0][qb][r]);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[1][qb][r]);
-      mx = xor32_max(mx);
-      if (__ballot(mx > mref[qb] + RESCALE_SLACK) != 0) {
-        const float mnew = fmaxf(mref[qb], mx);
-        const float alpha = exp2_fast(mref[qb] - mnew);
-        mref[qb] = mnew;
-        lsum[qb] *= alpha;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[qb][r] *= alpha;
-      }
-      const float mr = mref[qb];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-          for (int t2 = 0; t2 < 8; t2 += 2) {
-            opx2 pk;
-            pk[0] = (op_t)exp2_fast(sc[kb][qb][8 * ks + t2] - mr);
-            pk[1] = (op_t)exp2_fast(sc[kb][qb][8 * ks + t2 + 1] - mr);
-            lsum[qb] = dot2_ones(pk, lsum[qb]);
-            pf[qb][kb][ks][t2] = pk[0];
-            pf[qb][kb][ks][t2 + 1] = pk[1];
-          }
+      o[qb] = zero16();
+      lsum[qb] = 0.f;
+      mh[qb] = 0.f;
+      mset[qb] = false;
+      fb[qb] = fold_b(0.f);
     }
-    // O^T[d][q] += V^T[d][keys] * P^T[keys][q]  (keys in the accumulator's k-permutation)
+  };
+  auto qk = [&](int t) PF_INLINE {
+    const int kb0 = (t % nKB) * 64;
+    const char* st = alds + (t % 3) * TS_STAGE;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const opx8 k0 = lds_x8(st + aK[0] + 2048 * kb), k1 = lds_x8(st + aK[1] + 2048 * kb);
+      uint32_t mk;
+      if (live) mk = *reinterpret_cast<const uint16_t*>(st + aM + 64 * kb);
+      else mk = half_bits((op_t)(kb0 + 32 * kb + m < n_valid ? 0.f : -INFINITY));
+      const opx8 fa = slots01(h, ONE | mk << 16);
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const opx8 b0 = lds_x8(st + aB[2 * kb] + 4096 * qb), b1 = lds_x8(st + aB[2 * kb + 1] + 4096 * qb);
+        f32x16 a = mfma32(k0, qf[qb][0], zero16());
+        a = mfma32(k1, qf[qb][1], a);
+        a = mfma32(iden[0], b0, a);
+        a = mfma32(iden[1], b1, a);
+        sc[kb][qb] = mfma32(fa, fb[qb], a);
+      }
+    }
+  };
+  // P = exp2(S') for one query block: pack into the P.V operands, return the row sum
+  auto exp_pack = [&](int qb) PF_INLINE {
+    float ls = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) o[qb] = mfma32(vc[kb][ks], pf[qb][kb][ks], o[qb]);
-
-    if (kbi == nKB - 1) {   // head end: normalize and store
+        for (int t2 = 0; t2 < 8; t2 += 2) {
+          opx2 pk;
+          pk[0] = (op_t)exp2_fast(sc[kb][qb][8 * ks + t2]);
+          pk[1] = (op_t)exp2_fast(sc[kb][qb][8 * ks + t2 + 1]);
+          ls = dot2_ones(pk, ls);
+          pf[qb][kb][ks][t2 >> 1] = __builtin_bit_cast(uint32_t, pk);
+        }
+    return ls;
+  };
+  // Softmax of the scores sc into pf.  Pass 1 packs P against the current reference;
+  // if a query has no reference yet or a row sum exceeds LSTEP_MAX, pass 2 moves the
+  // reference (rescaling o and lsum, shifting sc) and packs again.  After a reference
+  // move P <= 2^RESCALE_SLACK, so pass 2 always passes the row-sum test.
+  auto softmax = [&]() PF_INLINE {
+    bool rare = __ballot(!(mset[0] && mset[1])) != 0;
+    float l[2];
+#pragma nounroll
+    for (int pass = 0; pass < 2; ++pass) {
+      if (rare) {
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const float inv = rcp_fast(xor32_sum(lsum[qb]));
-        const int j = j0 + 32 * qb + m;
+        for (int qb = 0; qb < 2; ++qb) {
+          float mx = sc[0][qb][0];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          if (OUT_F32) {
-            f32x4 v;
+          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[0][qb][r]);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = o[qb][4 * g + e] * inv;
-            *reinterpret_cast<f32x4*>(O32 + ((rowbase + hd) * N + j) * D + 8 * g + 4 * h) = v;
-          } else {
-            opx4 v;
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[1][qb][r]);
+          mx = xor32_max(mx);
+          const float d = mset[qb] ? (mx > RESCALE_SLACK ? mx : 0.f) : (mx == -INFINITY ? 0.f : mx);
+          const float mnew = (float)(op_t)(mh[qb] + d);
+          const float dsub = mnew - mh[qb];
+          const float alpha = mset[qb] ? exp2_fast(-dsub) : 1.f;
+          lsum[qb] *= alpha;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = (op_t)(o[qb][4 * g + e] * inv);
-            st_x4(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd + 8 * g + 4 * h, v);
+          for (int r = 0; r < 16; ++r) {
+            o[qb][r] *= alpha;
+            sc[0][qb][r] -= dsub;
+            sc[1][qb][r] -= dsub;
           }
+          mset[qb] = mset[qb] || mx != -INFINITY;
+          mh[qb] = mnew;
+          fb[qb] = fold_b(mnew);
+        }
+      }
+      l[0] = exp_pack(0);
+      l[1] = exp_pack(1);
+      if (rare) break;
+      rare = __ballot(l[0] > LSTEP_MAX || l[1] > LSTEP_MAX) != 0;
+      if (!rare) break;
+    }
+    lsum[0] += l[0];
+    lsum[1] += l[1];
+  };
+  auto pv = [&](int t) PF_INLINE {
+    const char* st = alds + (t % 3) * TS_STAGE;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const opx8 vf = lds_x8(st + dV + aB[u]);
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) o[qb] = mfma32(vf, as_x8(pf[qb][u >> 1][u & 1]), o[qb]);
+    }
+  };
+  auto finalize = [&](int hd) PF_INLINE {
+    const long rowbase = ((long)b * N + ip) * H;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const float inv = rcp_fast(xor32_sum(lsum[qb]));
+      const int j = jq0 + 32 * qb + m;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        if (OUT_F32) {
+          f32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = o[qb][4 * g + e] * inv;
+          *reinterpret_cast<f32x4*>(O32 + ((rowbase + hd) * N + j) * D + 8 * g + 4 * h) = v;
+        } else {
+          opx4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (op_t)(o[qb][4 * g + e] * inv);
+          st_x4(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd + 8 * g + 4 * h, v);
         }
       }
     }
-  }
+  };
+
+  // Step loop, instantiated once per wave group so each copy is straight-line code.
+  // ODD = false: scores, softmax and P.V of step it; ODD = true: softmax and P.V of step
+  // it-1, then the scores of step it.  Both run T+1 iterations (same barrier count).
+  auto run = [&](auto odd_tag) PF_INLINE {
+    constexpr bool ODD = decltype(odd_tag)::value;
+    q_load(0);
+    issue(0);
+    for (int it = 0; it <= T; ++it) {
+      // stage it landed and every wave is done with stage it-2's buffer
+      __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (it < T && it % nKB == 0) {   // take this head's Q before qn is reused
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int s = 0; s < 2; ++s) qf[qb][s] = live ? qn[qb][s] : zero_x8();
+      }
+      if (it + 1 < T) {
+        issue(it + 1);
+        if ((it + 1) % nKB == 0) q_load((it + 1) / nKB);
+      }
+      if (!qvalid) continue;
+      if (ODD && it >= 1) {
+        softmax();
+        pv(it - 1);
+        if ((it - 1) % nKB == nKB - 1) finalize((it - 1) / nKB);
+      }
+      if (it < T) {
+        if (it % nKB == 0) head_start();
+        qk(it);
+        if (!ODD) {
+          softmax();
+          pv(it);
+          if (it % nKB == nKB - 1) finalize(it / nKB);
+        }
+      }
+    }
+  };
+  if (odd) run(std::true_type{});
+  else run(std::false_type{});
 }
 
 // ---------------------------------------------------------------------------------
@@ -421,30 +551,26 @@ __global__ void ta_prep_qkv_kernel(const float* __restrict__ q, const float* __r
     const int j = jd / D, d = jd - j * D;
     Q[e] = (op_t)(q[e] * qs);
     K[e] = (op_t)k[e];
-    Vt[r * N * D + (long)d * N + j] = (op_t)v[e];
+    Vt[r * N * D + (long)d * N + perm16(j)] = (op_t)v[e];
   }
 }
 
 __global__ void ta_prep_bias_kernel(const float* __restrict__ bias, const float* __restrict__ mask,
-                                    float* __restrict__ bias2, float* __restrict__ M2,
+                                    op_t* __restrict__ bias16, op_t* __restrict__ mask16,
                                     long nbias, long nmask, int N, int n_valid) {
   for (long e = (long)blockIdx.x * blockDim.x + threadIdx.x; e < nbias; e += (long)gridDim.x * blockDim.x) {
-    bias2[e] = bias[e] * LOG2E;
-    if (e < nmask) {
-      const int key = (int)(e % N);
-      M2[e] = key >= n_valid ? -INFINITY : mask ? 1e9f * (mask[e] - 1.f) * LOG2E : 0.f;
-    }
+    bias16[e] = (op_t)(bias[e] * LOG2E);
+    if (e < nmask) mask16[e] = mask_term((int)(e % N) >= n_valid, mask ? mask[e] : 1.f);
   }
 }
 
 struct TaBuffers {
-  op_t *Q, *K, *Vt, *O;
-  float *bias2, *M2;
+  op_t *Q, *K, *Vt, *O, *bias16, *mask16;
 };
 
 size_t ta_buffers_size(int B, int N) {
   const size_t e = (size_t)B * N * H * N * D;
-  return 4 * e * sizeof(op_t) + ((size_t)B * H * N * N + (size_t)B * N * N) * sizeof(float);
+  return (4 * e + (size_t)B * H * N * N + (size_t)B * N * N) * sizeof(op_t);
 }
 
 TaBuffers ta_buffers(void* ws, int B, int N) {
@@ -454,9 +580,25 @@ TaBuffers ta_buffers(void* ws, int B, int N) {
   t.K = t.Q + e;
   t.Vt = t.K + e;
   t.O = t.Vt + e;
-  t.bias2 = (float*)(t.O + e);
-  t.M2 = t.bias2 + (size_t)B * H * N * N;
+  t.bias16 = t.O + e;
+  t.mask16 = t.bias16 + (size_t)B * H * N * N;
   return t;
+}
+
+template <bool OUT_F32>
+int launch_attn(const TaBuffers& t, float* o32, int B, int N, int n_valid, hipStream_t st) {
+  static bool attr = false;
+  if (!attr) {
+    if (hipFuncSetAttribute((const void*)ta_attn_kernel<OUT_F32>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)TA_LDS) != hipSuccess)
+      return pf_fail(PF_E_LAUNCH, "ta_attn_kernel: cannot reserve %zu bytes of LDS", TA_LDS);
+    attr = true;
+  }
+  const int total = B * (N / 4) * ((N + 127) / 128);
+  ta_attn_kernel<OUT_F32><<<total, 64 * TA_WAVES, TA_LDS, st>>>(t.Q, t.K, t.Vt, t.bias16, t.mask16, t.O, o32, N,
+                                                               n_valid, total);
+  PF_CHECK_LAUNCH("ta_attn_kernel");
+  return PF_OK;
 }
 
 }  // namespace
@@ -493,12 +635,11 @@ extern "C" int pf_triatt_fwd(const pf_triatt_args* a) {
   const int grid_pos = (int)((positions / 32 + 3) / 4);
   ta_proj_kernel<<<grid_pos, 256, 0, st>>>(a->z_in, a->pair_mask, a->ln_w, a->ln_b,
                                            (const op_t*)a->w_q, (const op_t*)a->w_k, (const op_t*)a->w_v,
-                                           (const op_t*)a->w_bias, t.Q, t.K, t.Vt, t.bias2, t.M2, B, N,
+                                           (const op_t*)a->w_bias, t.Q, t.K, t.Vt, t.bias16, t.mask16, B, N,
                                            n_valid, a->ending, qscale, a->eps);
   PF_CHECK_LAUNCH("ta_proj_kernel");
-  const int total = B * (N / 4) * (N / 64);
-  ta_attn_kernel<false><<<total, 256, 0, st>>>(t.Q, t.K, t.Vt, t.bias2, t.M2, t.O, nullptr, N, total);
-  PF_CHECK_LAUNCH("ta_attn_kernel");
+  int rc = launch_attn<false>(t, nullptr, B, N, n_valid, st);
+  if (rc) return rc;
   {
     static bool attr = false;
     if (!attr) {
@@ -542,11 +683,8 @@ extern "C" int pf_tri_attention(const float* q, const float* k, const float* v, 
   const long rows = (long)B * N * H;
   ta_prep_qkv_kernel<<<2048, 256, 0, st>>>(q, k, v, scale * LOG2E, t.Q, t.K, t.Vt, rows, N);
   PF_CHECK_LAUNCH("ta_prep_qkv_kernel");
-  ta_prep_bias_kernel<<<1024, 256, 0, st>>>(bias, mask, t.bias2, t.M2, (long)B * H * N * N, (long)B * N * N, N,
-                                            n_valid);
+  ta_prep_bias_kernel<<<1024, 256, 0, st>>>(bias, mask, t.bias16, t.mask16, (long)B * H * N * N, (long)B * N * N,
+                                            N, n_valid);
   PF_CHECK_LAUNCH("ta_prep_bias_kernel");
-  const int total = B * (N / 4) * (N / 64);
-  ta_attn_kernel<true><<<total, 256, 0, st>>>(t.Q, t.K, t.Vt, t.bias2, t.M2, nullptr, o, N, total);
-  PF_CHECK_LAUNCH("ta_attn_kernel");
-  return PF_OK;
+  return launch_attn<true>(t, o, B, N, n_valid, st);
 }

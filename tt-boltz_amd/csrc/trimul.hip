@@ -232,9 +232,6 @@ __global__ __launch_bounds__(256) void tm_contract_kernel(
 // ---------------------------------------------------------------------------------
 constexpr int BM2 = 256;
 
-// s_waitcnt immediate (gfx9 encoding) that waits until at most v vector-memory
-// operations of this wave are outstanding and leaves expcnt / lgkmcnt unconstrained.
-constexpr int vmcnt_le(int v) { return (v & 0xF) | (((v >> 4) & 3) << 14) | 0x70 | 0xF00; }
 
 // Slab layout: chunk c (0..7, 16 bytes) of row r at position 8r + (c ^ swz8(r)) with
 // swz8(r) = ((r>>1)&7) ^ ((r&1)<<2).  A fragment read takes one chunk from each of 32
