@@ -15,7 +15,7 @@
 //                      and 3 swapped) so a P.V operand fragment is one 16-byte run
 //              bias16  op_t [B][H][N(j)][N(k)]   (shared by all rows i)
 //              mask16  op_t [B][N(i)][N(k)]      0, or -inf for masked / padding keys
-//   ta_attn  flash attention (see the kernel's comment): 8-wave workgroups of 4 frame rows
+//   ta_attn  flash attention (see the kernel's comment): 16-wave workgroups of 4 frame rows
 //            x 128 queries, LDS-DMA ring, bias / mask / reference max folded into MFMAs,
 //            lazy-max softmax.  Output O (normalized, ungated) op_t [B][N(i)][N(j)][H*D].
 //   ta_out   o-proj epilogue (persistent, W_g / W_o in LDS, output-aligned layout): gate
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void ta_proj_kernel(
 // Flash attention.  OUT_F32 = false: O op_t [B][N][N][H*D] (frame pair layout);
 // OUT_F32 = true: O fp32 [B][N][H][N][D] (the standalone attention-core API).
 //
-// A workgroup is 8 waves: 4 frame rows (ip0 .. ip0+3) x 2 blocks of 64 queries; it walks
+// A workgroup is 16 waves: 4 frame rows (ip0 .. ip0+3) x 4 blocks of 32 queries; it walks
 // 4 heads x N/64 key tiles.  Per step the workgroup's bias tile [128 q][64 k], the four
 // rows' K [64 k][32 d] and V^T [32 d][64 k] tiles and their mask entries move
 // global -> LDS by DMA (global_load_lds, no VGPR staging) through a 3-deep ring, one
@@ -160,15 +160,15 @@ __global__ __launch_bounds__(256) void ta_proj_kernel(
 // value (exact as an MFMA operand) and moves lazily: at a head's first tile, while a
 // query has seen no unmasked key, or when a tile's row sum exceeds 2^14 (some P above
 // 2^9).  A P that would overflow op_t fails the same test before it reaches the P.V
-// MFMA, and the tile is then redone from S' with the new reference.
-// Waves w and w+4 share a SIMD.  Waves 4..7 run each step rotated by half a step
-// (softmax + P.V of step t-1, then the score MFMAs of step t), so while one wave of the
-// pair issues score MFMAs the other issues its softmax VALU work.
+// MFMA, and the tile is then repacked from S' with the new reference.
+// Each wave takes its two 32-key halves in turn (128 VGPRs: four waves per SIMD).  On
+// gfx950 the step is bound by the SIMD's MFMA + v_exp_f32 time (the two largely
+// serialize), not by latency: 2, 4 or 8 waves per SIMD all measure alike.
 // Rows whose valid keys are all masked: the fp32 reference adds -1e9 to every logit,
 // which rounds them all to -1e9 (|logit| < 32), i.e. a uniform average over the keys.
 // Such a row zeroes Q and the identity operand and feeds mask 0 for its valid keys.
 // ---------------------------------------------------------------------------------
-constexpr int TA_WAVES = 8;
+constexpr int TA_WAVES = 16;
 constexpr int TS_BIAS = 0, TS_K = 16384, TS_V = 32768, TS_MASK = 49152, TS_STAGE = 50176;   // bytes
 constexpr size_t TA_LDS = 3 * (size_t)TS_STAGE;
 constexpr float LSTEP_MAX = 16384.f;   // per-lane row sum of one tile that forces a rescale
@@ -197,8 +197,7 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   extern __shared__ __attribute__((aligned(16))) char alds[];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int row = wid & 3, qw = wid >> 2;
-  const bool odd = qw == 1;
+  const int row = wid & 3, qw = wid >> 2;   // frame row, block of 32 queries
   const int nQP = (N + 127) >> 7, nKB = N >> 6, T = H * nKB;
   const int w = xcd_remap(blockIdx.x, total);
   const int per_b = (N >> 2) * nQP;
@@ -207,43 +206,28 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   const int rg = rem / nQP;
   const int jw0 = (rem - rg * nQP) * 128;
   const int ip0 = 4 * rg, ip = ip0 + row;
-  const int jq0 = jw0 + 64 * qw;
-  const bool qvalid = jq0 < N;            // the second block of a trailing half pair idles
+  const int jq0 = jw0 + 32 * qw;
+  const bool qvalid = jq0 < N;            // query blocks past N (trailing part tile) idle
   const long NN = (long)N * N;
   const int seqD = N * D;                 // elements of one (row, head) Q / K / V^T block
 
-  // ---- DMA sources: chunk e = tid + 512 i of each 16 KB tile ----
+  // ---- DMA: chunk tid of each 16 KB tile; byte offsets from wave-uniform bases ----
   const op_t* bias_b = bias16 + (long)b * H * NN;
   const op_t* k_b = K + ((long)b * N + ip0) * H * seqD;
   const op_t* v_b = Vt + ((long)b * N + ip0) * H * seqD;
   const op_t* mask_b = mask16 + ((long)b * N + ip0) * N;
-  // byte offsets from wave-uniform bases (32-bit: one VGPR each, the base stays scalar)
-  uint32_t offB[2], offK[2], offV[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int e = tid + 512 * i;
-    const int q = e >> 3;
-    offB[i] = 2u * (min(jw0 + q, N - 1) * N + 8 * ((e & 7) ^ swz8(q)));
-    const int rk = e >> 8, key = (e >> 2) & 63;
-    offK[i] = 2u * (rk * H * seqD + key * D + 8 * ((e & 3) ^ swz4(key)));
-    const int d = (e >> 3) & 31;
-    offV[i] = 2u * (rk * H * seqD + d * N + 8 * ((e & 7) ^ swz8(d)));
-  }
+  const uint32_t offB = 2u * (min(jw0 + (tid >> 3), N - 1) * N + 8 * ((tid & 7) ^ swz8(tid >> 3)));
+  const int rk = tid >> 8, kk = (tid >> 2) & 63, dd = (tid >> 3) & 31;
+  const uint32_t offK = 2u * (rk * H * seqD + kk * D + 8 * ((tid & 3) ^ swz4(kk)));
+  const uint32_t offV = 2u * (rk * H * seqD + dd * N + 8 * ((tid & 7) ^ swz8(dd)));
   const uint32_t offM = 2u * (((lane >> 3) & 3) * N + 8 * (lane & 7));
-  auto issue = [&](int t) PF_INLINE {
-    const int hd = t / nKB, kb0 = (t - hd * nKB) * 64;
-    char* st = alds + (t % 3) * TS_STAGE;
-    const char* bs = (const char*)(bias_b + (long)hd * NN + kb0);
-    const char* ks = (const char*)(k_b + hd * seqD + kb0 * D);
-    const char* vs = (const char*)(v_b + hd * seqD + kb0);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      __builtin_amdgcn_global_load_lds(bs + offB[i], st + TS_BIAS + 1024 * wid + 8192 * i, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(ks + offK[i], st + TS_K + 1024 * wid + 8192 * i, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vs + offV[i], st + TS_V + 1024 * wid + 8192 * i, 16, 0, 0);
-    }
+  auto issue = [&](int st_off, int hd, int kb0) PF_INLINE {
+    char* st = alds + st_off + 1024 * wid;
+    __builtin_amdgcn_global_load_lds((const char*)(bias_b + (long)hd * NN + kb0) + offB, st + TS_BIAS, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const char*)(k_b + hd * seqD + kb0 * D) + offK, st + TS_K, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const char*)(v_b + hd * seqD + kb0) + offV, st + TS_V, 16, 0, 0);
     if (wid == 0)
-      __builtin_amdgcn_global_load_lds((const char*)(mask_b + kb0) + offM, st + TS_MASK, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const char*)(mask_b + kb0) + offM, alds + st_off + TS_MASK, 16, 0, 0);
   };
 
   // ---- per-lane LDS read addresses (bytes from a stage base) ----
@@ -251,10 +235,10 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   int aB[4], aK[2];
 #pragma unroll
   for (int u = 0; u < 4; ++u)            // u = 2*kb + s: chunk 2u + h of a 64-key row
-    aB[u] = TS_BIAS + 128 * (64 * qw + m) + 16 * ((2 * u + h) ^ sw);
-  const int dV = TS_V - TS_BIAS + 4096 * row - 8192 * qw;   // V^T chunk (m, c) sits at aB + dV
+    aB[u] = TS_BIAS + 128 * (32 * qw + m) + 16 * ((2 * u + h) ^ sw);
 #pragma unroll
   for (int s = 0; s < 2; ++s) aK[s] = TS_K + 4096 * row + 64 * m + 16 * ((2 * s + h) ^ ksw);
+  const int dV = TS_V - TS_BIAS + 4096 * row - 4096 * qw;   // V^T chunk (m, c) sits at aB + dV
   const int aM = TS_MASK + 128 * row + 2 * m;
 
   // rows whose valid keys are all masked (wave-uniform)
@@ -279,183 +263,136 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   }
   auto fold_b = [&](float mv) PF_INLINE { return slots01(h, half_bits((op_t)(-mv)) | ONE << 16); };
 
-  const int jq = min(jq0, N - 64);
-  opx8 qf[2][2], qn[2][2], fb[2];
-  u32x4 pf[2][2][2];
-  f32x16 sc[2][2], o[2];
-  float mh[2], lsum[2];
-  bool mset[2];
+  const int jq = min(jq0, N - 32);
+  opx8 qf[2], qn[2], fb;
+  f32x16 o;
+  float mh, lsum;
+  bool mset;
   auto q_load = [&](int hd) PF_INLINE {
-    const op_t* qp = Q + ((((long)b * N + ip) * H + hd) * N + jq) * D;
+    const op_t* qp = Q + ((((long)b * N + ip) * H + hd) * N + jq + m) * D + 8 * h;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) qn[qb][s] = ld_x8(qp + (32 * qb + m) * D + 16 * s + 8 * h);
+    for (int s = 0; s < 2; ++s) qn[s] = ld_x8(qp + 16 * s);
   };
   auto head_start = [&]() PF_INLINE {
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      o[qb] = zero16();
-      lsum[qb] = 0.f;
-      mh[qb] = 0.f;
-      mset[qb] = false;
-      fb[qb] = fold_b(0.f);
-    }
+    o = zero16();
+    lsum = 0.f;
+    mh = 0.f;
+    mset = false;
+    fb = fold_b(0.f);
   };
-  auto qk = [&](int t) PF_INLINE {
-    const int kb0 = (t % nKB) * 64;
-    const char* st = alds + (t % 3) * TS_STAGE;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const opx8 k0 = lds_x8(st + aK[0] + 2048 * kb), k1 = lds_x8(st + aK[1] + 2048 * kb);
-      uint32_t mk;
-      if (live) mk = *reinterpret_cast<const uint16_t*>(st + aM + 64 * kb);
-      else mk = half_bits((op_t)(kb0 + 32 * kb + m < n_valid ? 0.f : -INFINITY));
-      const opx8 fa = slots01(h, ONE | mk << 16);
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const opx8 b0 = lds_x8(st + aB[2 * kb] + 4096 * qb), b1 = lds_x8(st + aB[2 * kb + 1] + 4096 * qb);
-        f32x16 a = mfma32(k0, qf[qb][0], zero16());
-        a = mfma32(k1, qf[qb][1], a);
-        a = mfma32(iden[0], b0, a);
-        a = mfma32(iden[1], b1, a);
-        sc[kb][qb] = mfma32(fa, fb[qb], a);
-      }
-    }
-  };
-  // P = exp2(S') for one query block: pack into the P.V operands, return the row sum
-  auto exp_pack = [&](int qb) PF_INLINE {
+  // P = exp2(S') packed into the two P.V operands; returns the lane's row sum
+  auto exp_pack = [&](const f32x16& sc, u32x4 (&pf)[2]) PF_INLINE {
     float ls = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int t2 = 0; t2 < 8; t2 += 2) {
-          opx2 pk;
-          pk[0] = (op_t)exp2_fast(sc[kb][qb][8 * ks + t2]);
-          pk[1] = (op_t)exp2_fast(sc[kb][qb][8 * ks + t2 + 1]);
-          ls = dot2_ones(pk, ls);
-          pf[qb][kb][ks][t2 >> 1] = __builtin_bit_cast(uint32_t, pk);
-        }
+      for (int t2 = 0; t2 < 8; t2 += 2) {
+        opx2 pk;
+        pk[0] = (op_t)exp2_fast(sc[8 * ks + t2]);
+        pk[1] = (op_t)exp2_fast(sc[8 * ks + t2 + 1]);
+        ls = dot2_ones(pk, ls);
+        pf[ks][t2 >> 1] = __builtin_bit_cast(uint32_t, pk);
+      }
     return ls;
   };
-  // Softmax of the scores sc into pf.  Pass 1 packs P against the current reference;
-  // if a query has no reference yet or a row sum exceeds LSTEP_MAX, pass 2 moves the
-  // reference (rescaling o and lsum, shifting sc) and packs again.  After a reference
-  // move P <= 2^RESCALE_SLACK, so pass 2 always passes the row-sum test.
-  auto softmax = [&]() PF_INLINE {
-    bool rare = __ballot(!(mset[0] && mset[1])) != 0;
-    float l[2];
-#pragma nounroll
-    for (int pass = 0; pass < 2; ++pass) {
-      if (rare) {
+  // One 32-key half of a step: scores S'^T = K.Q^T + I.bias^T + [1, mask].[-m, 1]^T, the
+  // softmax (P against the current reference; if a query has no reference yet or the
+  // row sum exceeds LSTEP_MAX the reference moves, o and lsum are rescaled and P is packed
+  // again -- after a move P <= 2^RESCALE_SLACK, so once is enough), then P.V.
+  auto half = [&](const char* st, int kb0, auto kbt) PF_INLINE {
+    constexpr int kb = decltype(kbt)::value;
+    const opx8 k0 = lds_x8(st + aK[0] + 2048 * kb), k1 = lds_x8(st + aK[1] + 2048 * kb);
+    const opx8 b0 = lds_x8(st + aB[2 * kb]), b1 = lds_x8(st + aB[2 * kb + 1]);
+    uint32_t mk;
+    if (live) mk = *reinterpret_cast<const uint16_t*>(st + aM + 64 * kb);
+    else mk = half_bits((op_t)(kb0 + 32 * kb + m < n_valid ? 0.f : -INFINITY));
+    f32x16 sc = mfma32(k0, qf[0], zero16());
+    sc = mfma32(k1, qf[1], sc);
+    sc = mfma32(iden[0], b0, sc);
+    sc = mfma32(iden[1], b1, sc);
+    sc = mfma32(slots01(h, ONE | mk << 16), fb, sc);
+    const opx8 v0 = lds_x8(st + dV + aB[2 * kb]), v1 = lds_x8(st + dV + aB[2 * kb + 1]);
+    u32x4 pf[2];
+    float l = exp_pack(sc, pf);
+    if (__ballot(!mset || l > LSTEP_MAX) != 0) {
+      float mx = sc[0];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          float mx = sc[0][qb][0];
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[r]);
+      mx = xor32_max(mx);
+      const float d = mset ? (mx > RESCALE_SLACK ? mx : 0.f) : (mx == -INFINITY ? 0.f : mx);
+      const float mnew = (float)(op_t)(mh + d);
+      const float dsub = mnew - mh;
+      const float alpha = mset ? exp2_fast(-dsub) : 1.f;
+      lsum *= alpha;
 #pragma unroll
-          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[0][qb][r]);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[1][qb][r]);
-          mx = xor32_max(mx);
-          const float d = mset[qb] ? (mx > RESCALE_SLACK ? mx : 0.f) : (mx == -INFINITY ? 0.f : mx);
-          const float mnew = (float)(op_t)(mh[qb] + d);
-          const float dsub = mnew - mh[qb];
-          const float alpha = mset[qb] ? exp2_fast(-dsub) : 1.f;
-          lsum[qb] *= alpha;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            o[qb][r] *= alpha;
-            sc[0][qb][r] -= dsub;
-            sc[1][qb][r] -= dsub;
-          }
-          mset[qb] = mset[qb] || mx != -INFINITY;
-          mh[qb] = mnew;
-          fb[qb] = fold_b(mnew);
-        }
+      for (int r = 0; r < 16; ++r) {
+        o[r] *= alpha;
+        sc[r] -= dsub;
       }
-      l[0] = exp_pack(0);
-      l[1] = exp_pack(1);
-      if (rare) break;
-      rare = __ballot(l[0] > LSTEP_MAX || l[1] > LSTEP_MAX) != 0;
-      if (!rare) break;
+      mset = mset || mx != -INFINITY;
+      mh = mnew;
+      fb = fold_b(mnew);
+      l = exp_pack(sc, pf);
     }
-    lsum[0] += l[0];
-    lsum[1] += l[1];
-  };
-  auto pv = [&](int t) PF_INLINE {
-    const char* st = alds + (t % 3) * TS_STAGE;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const opx8 vf = lds_x8(st + dV + aB[u]);
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) o[qb] = mfma32(vf, as_x8(pf[qb][u >> 1][u & 1]), o[qb]);
-    }
+    lsum += l;
+    o = mfma32(v0, as_x8(pf[0]), o);
+    o = mfma32(v1, as_x8(pf[1]), o);
   };
   auto finalize = [&](int hd) PF_INLINE {
+    const float inv = rcp_fast(xor32_sum(lsum));
+    const int j = jq0 + m;
     const long rowbase = ((long)b * N + ip) * H;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      const float inv = rcp_fast(xor32_sum(lsum[qb]));
-      const int j = jq0 + 32 * qb + m;
+    for (int g = 0; g < 4; ++g) {
+      if (OUT_F32) {
+        f32x4 v;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        if (OUT_F32) {
-          f32x4 v;
+        for (int e = 0; e < 4; ++e) v[e] = o[4 * g + e] * inv;
+        *reinterpret_cast<f32x4*>(O32 + ((rowbase + hd) * N + j) * D + 8 * g + 4 * h) = v;
+      } else {
+        opx4 v;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = o[qb][4 * g + e] * inv;
-          *reinterpret_cast<f32x4*>(O32 + ((rowbase + hd) * N + j) * D + 8 * g + 4 * h) = v;
-        } else {
-          opx4 v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (op_t)(o[qb][4 * g + e] * inv);
-          st_x4(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd + 8 * g + 4 * h, v);
-        }
+        for (int e = 0; e < 4; ++e) v[e] = (op_t)(o[4 * g + e] * inv);
+        st_x4(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd + 8 * g + 4 * h, v);
       }
     }
   };
 
-  // Step loop, instantiated once per wave group so each copy is straight-line code.
-  // ODD = false: scores, softmax and P.V of step it; ODD = true: softmax and P.V of step
-  // it-1, then the scores of step it.  Both run T+1 iterations (same barrier count).
-  auto run = [&](auto odd_tag) PF_INLINE {
-    constexpr bool ODD = decltype(odd_tag)::value;
-    q_load(0);
-    issue(0);
-    for (int it = 0; it <= T; ++it) {
-      // stage it landed and every wave is done with stage it-2's buffer
-      __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      if (it < T && it % nKB == 0) {   // take this head's Q before qn is reused
+  // Step loop: T steps, one barrier each (the loop-top wait + barrier), the DMA of the
+  // next stage and, at a head's last tile, the next head's Q prefetch; then the two halves.
+  using K0 = std::integral_constant<int, 0>;
+  using K1 = std::integral_constant<int, 1>;
+  int cur = 0;          // stage byte offset of step it
+  int kbi = 0, hd = 0;  // step it = hd * nKB + kbi
+  q_load(0);
+  issue(0, 0, 0);
+  for (int it = 0; it < T; ++it) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));   // stage it landed ...
+    __builtin_amdgcn_s_barrier();              // ... for every wave; stage it-2 is free
+    asm volatile("" ::: "memory");
+    if (kbi == 0) {   // take this head's Q before qn is reused
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-          for (int s = 0; s < 2; ++s) qf[qb][s] = live ? qn[qb][s] : zero_x8();
-      }
-      if (it + 1 < T) {
-        issue(it + 1);
-        if ((it + 1) % nKB == 0) q_load((it + 1) / nKB);
-      }
-      if (!qvalid) continue;
-      if (ODD && it >= 1) {
-        softmax();
-        pv(it - 1);
-        if ((it - 1) % nKB == nKB - 1) finalize((it - 1) / nKB);
-      }
-      if (it < T) {
-        if (it % nKB == 0) head_start();
-        qk(it);
-        if (!ODD) {
-          softmax();
-          pv(it);
-          if (it % nKB == nKB - 1) finalize(it / nKB);
-        }
-      }
+      for (int s = 0; s < 2; ++s) qf[s] = live ? qn[s] : zero_x8();
     }
-  };
-  if (odd) run(std::true_type{});
-  else run(std::false_type{});
+    const int nst = cur == 2 * TS_STAGE ? 0 : cur + TS_STAGE;
+    if (it + 1 < T) {
+      const bool wrap = kbi + 1 == nKB;
+      issue(nst, wrap ? hd + 1 : hd, wrap ? 0 : 64 * (kbi + 1));
+      if (wrap) q_load(hd + 1);
+    }
+    if (qvalid) {
+      if (kbi == 0) head_start();
+      const char* st = alds + cur;
+      half(st, 64 * kbi, K0{});
+      half(st, 64 * kbi, K1{});
+      if (kbi == nKB - 1) finalize(hd);
+    }
+    cur = nst;
+    if (++kbi == nKB) {
+      kbi = 0;
+      ++hd;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------
