@@ -417,12 +417,13 @@ __global__ __launch_bounds__(256, 2) void tm8_out_kernel(
         P = mfma8(xo.q[s], wfrag128(lp, row, s, h), P, xo.sc[s], lps[4 * row + 2 * s + h]);
         G = mfma8(xi.q[s], wfrag128(lg, row, s, h), G, xi.sc[s], lgs[4 * row + 2 * s + h]);
       }
+      // residuals first (all loads ahead of the stores, so they overlap)
+      float res[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const long idx = (pos0 + acc_row(r, h)) * C + 32 * ob + m;
-        const float u = P[r] * sigmoidf_fast(G[r]);
-        out[idx] = accumulate ? out[idx] + u : u;
-      }
+      for (int r = 0; r < 16; ++r) res[r] = accumulate ? out[(pos0 + acc_row(r, h)) * C + 32 * ob + m] : 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        out[(pos0 + acc_row(r, h)) * C + 32 * ob + m] = P[r] * sigmoidf_fast(G[r]) + res[r];
     }
   }
 }
@@ -520,15 +521,20 @@ __global__ __launch_bounds__(256) void tr8_pair_kernel(
     }
     __syncthreads();
   }
+  // residuals first (all loads ahead of the stores, so they overlap); rows past the end
+  // are clamped on load and skipped on store
+  float res[4][16];
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      res[ob][r] = accumulate ? out[min(pos0 + acc_row(r, h), rows - 1) * C + 32 * ob + m] : 0.f;
 #pragma unroll
   for (int ob = 0; ob < 4; ++ob)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const long p = pos0 + acc_row(r, h);
-      if (p < rows) {
-        const long idx = p * C + 32 * ob + m;
-        out[idx] = accumulate ? out[idx] + acc[ob][r] : acc[ob][r];
-      }
+      if (p < rows) out[p * C + 32 * ob + m] = acc[ob][r] + res[ob][r];
     }
 }
 

@@ -4,8 +4,11 @@
 //                    orientation) -> silu(a)*b in registers -> fc3 (MFMA) -> residual.
 //                    The 4C hidden activations never leave the CU.  fc1/fc2 rows are
 //                    staged in LDS perm16-permuted so the fc1/fc2 accumulator registers
-//                    come out in the natural k order fc3's A operand expects.  A wave owns
-//                    PB*32 pairs so every weight fragment read from LDS feeds PB MFMAs.
+//                    come out in the natural k order of fc3's B operand.  Everything is in
+//                    the output-aligned layout (pf_common.h): fc3 yields D[channel][pair],
+//                    so a lane owns one pair and writes 16-byte runs, and the residual is
+//                    fetched with 16-byte loads, all issued before the first store.  A wave
+//                    owns PB*32 pairs so every weight fragment read from LDS feeds PB MFMAs.
 //                    Replaces Transition.forward (tt_bio/boltz2.py:1227-1258) and the ttnn
 //                    Transition (tt_bio/tenstorrent.py:856-946).
 //   ln_rows_kernel   LayerNorm over rows, any C (nn.LayerNorm / tt_bio/boltz2.py:738-768).
@@ -49,8 +52,8 @@ __global__ __launch_bounds__(64 * NW, MINW) void tr_pair_kernel(
 #pragma unroll
   for (int pb = 0; pb < PB; ++pb) {
     float x[64];
-    load_row128_frag(x_in + min(pos0 + 32 * pb + m, rows - 1) * C, h, x);
-    ln128_to_frag(x, h, lnw, lnb, eps, xf[pb]);
+    load_row128_oa(x_in + min(pos0 + 32 * pb + m, rows - 1) * C, h, x);
+    ln128_oa_to_frag(x, h, lnw, lnb, eps, xf[pb]);
   }
   f32x16 acc[PB][4];
 #pragma unroll
@@ -88,8 +91,8 @@ __global__ __launch_bounds__(64 * NW, MINW) void tr_pair_kernel(
     for (int pb = 0; pb < PB; ++pb) { a1[pb] = zero16(); a2[pb] = zero16(); }
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const opx8 f1 = ld_x8(&s1[bufi][m * LDSW + 16 * s + 8 * h]);
-      const opx8 f2 = ld_x8(&s2[bufi][m * LDSW + 16 * s + 8 * h]);
+      const opx8 f1 = wfrag_oa(&s1[bufi][m * LDSW], s, h);
+      const opx8 f2 = wfrag_oa(&s2[bufi][m * LDSW], s, h);
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb) {
         a1[pb] = mfma32(f1, xf[pb][s], a1[pb]);   // rows = hidden (perm16), cols = pairs
@@ -109,21 +112,28 @@ __global__ __launch_bounds__(64 * NW, MINW) void tr_pair_kernel(
       for (int ks = 0; ks < 2; ++ks) {
         const opx8 f3 = ld_x8(&s3[bufi][(32 * ob + m) * LDS3 + 16 * ks + 8 * h]);
 #pragma unroll
-        for (int pb = 0; pb < PB; ++pb) acc[pb][ob] = mfma32(hf[pb][ks], f3, acc[pb][ob]);
+        for (int pb = 0; pb < PB; ++pb) acc[pb][ob] = mfma32(f3, hf[pb][ks], acc[pb][ob]);   // D[ch][pair]
       }
   }
+  // lane (m, h) owns pair pos0 + 32 pb + m; acc[pb][ob][4g + e] is channel 32 ob + 8 g + 4 h + e
 #pragma unroll
-  for (int pb = 0; pb < PB; ++pb)
+  for (int pb = 0; pb < PB; ++pb) {
+    const long p = pos0 + 32 * pb + m;
+    if (p < rows) {
+      float* dst = out + p * C;
+      f32x4 res[16];
 #pragma unroll
-    for (int ob = 0; ob < 4; ++ob)
+      for (int q = 0; q < 16; ++q)
+        res[q] = accumulate ? *reinterpret_cast<const f32x4*>(dst + oa_channel(q, h)) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const long p = pos0 + 32 * pb + acc_row(r, h);
-        if (p < rows) {
-          const long idx = p * C + 32 * ob + m;
-          out[idx] = accumulate ? out[idx] + acc[pb][ob][r] : acc[pb][ob][r];
-        }
+      for (int q = 0; q < 16; ++q) {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[pb][q >> 2][4 * (q & 3) + e] + res[q][e];
+        *reinterpret_cast<f32x4*>(dst + oa_channel(q, h)) = v;
       }
+    }
+  }
 }
 
 // One wave per row.
@@ -168,15 +178,16 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(
   }
   const int n = nt * 32 + m;
   const float bn = bias ? bias[n] : 0.f;
+  // residuals first (resid may alias out: all loads ahead of the stores, so they overlap)
+  float res[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    res[r] = !SWIGLU && resid ? resid[min(r0 + acc_row(r, h), rows - 1) * Nout + n] : 0.f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const long row = r0 + acc_row(r, h);
     if (row >= rows) continue;
-    const long idx = row * Nout + n;
-    float v;
-    if (SWIGLU) v = siluf(acc[r]) * acc2[r];
-    else v = acc[r] + bn + (resid ? resid[idx] : 0.f);
-    out[idx] = v;
+    out[row * Nout + n] = SWIGLU ? siluf(acc[r]) * acc2[r] : acc[r] + bn + res[r];
   }
 }
 
@@ -203,13 +214,14 @@ __global__ __launch_bounds__(256) void pair_ln_linear_kernel(
     f32x16 acc = zero16();
 #pragma unroll
     for (int s = 0; s < 8; ++s) acc = mfma32(xf[s], ld_x8(&sW[(32 * ob + m) * LDSW + 16 * s + 8 * h]), acc);
+    // base may alias out: all loads ahead of the stores, so they overlap
+    float res[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) res[r] = base[min(pos0 + acc_row(r, h), rows - 1) * C + 32 * ob + m];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const long p = pos0 + acc_row(r, h);
-      if (p < rows) {
-        const long idx = p * C + 32 * ob + m;
-        out[idx] = base[idx] + acc[r];
-      }
+      if (p < rows) out[p * C + 32 * ob + m] = res[r] + acc[r];
     }
   }
 }
