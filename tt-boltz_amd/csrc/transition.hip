@@ -7,8 +7,8 @@
 //                    come out in the natural k order of fc3's B operand.  Everything is in
 //                    the output-aligned layout (pf_common.h): fc3 yields D[channel][pair],
 //                    so a lane owns one pair and writes 16-byte runs, and the residual is
-//                    fetched with 16-byte loads, all issued before the first store.  A wave
-//                    owns PB*32 pairs so every weight fragment read from LDS feeds PB MFMAs.
+//                    fetched with 16-byte loads, all issued before the first store.  Weight
+//                    blocks arrive by LDS DMA (layout at the kernel).
 //                    Replaces Transition.forward (tt_bio/boltz2.py:1227-1258) and the ttnn
 //                    Transition (tt_bio/tenstorrent.py:856-946).
 //   ln_rows_kernel   LayerNorm over rows, any C (nn.LayerNorm / tt_bio/boltz2.py:738-768).
@@ -21,117 +21,107 @@
 namespace {
 
 constexpr int C = 128, LDSW = 136, LDS3 = 40;
+PF_DEV opx8 lds_x8(const char* p) { return *reinterpret_cast<const opx8*>(p); }
 
-// Launch configuration of the pair transition (pair blocks per wave, waves per WG,
-// min waves per SIMD), chosen by measurement.
-#ifndef TR_PB
-#define TR_PB 1
-#define TR_NW 4
-#define TR_MINW 2
-#endif
+// Pair transition: a workgroup is TRW waves x 32 pairs; three workgroups share a CU.
+// Weight blocks of 32 hidden units move global -> LDS by DMA (global_load_lds) into a
+// 2-stage ring, one barrier per block:
+//   W1 / W2 block: LDS row R (0..31) holds hidden unit 32 hb + perm16(R) (so the fc1/fc2
+//                  accumulator rows come out in fc3's k order); 16 chunks of 8 channels,
+//                  chunk c at slot c ^ (R & 15)
+//   W3 block:      row R (output channel 0..127) holds hidden 32 hb .. 32 hb + 31; 4
+//                  chunks, chunk c at slot c ^ swz4(R)
+// so every fragment read (one 16-byte chunk from each of 32 consecutive rows) is free of
+// bank conflicts.
+constexpr int TRW = 4;
+constexpr int TR_BLK = 8192;                 // bytes of one fp16 weight block
+constexpr int TR_STAGE = 3 * TR_BLK;
+PF_DEV int tr_swz4(int r) { return (r >> 2) & 3; }
 
-// PB: 32-pair blocks per wave; NW: waves per workgroup; MINW: min waves per SIMD hint.
-template <int PB, int NW, int MINW>
-__global__ __launch_bounds__(64 * NW, MINW) void tr_pair_kernel(
+__global__ __launch_bounds__(64 * TRW, 3) void tr_pair_kernel(
     const float* x_in, float* out, const float* __restrict__ lnw, const float* __restrict__ lnb,
     const op_t* __restrict__ w1, const op_t* __restrict__ w2, const op_t* __restrict__ w3,
     long rows, int hidden, int accumulate, float eps) {
-  constexpr int NT = 64 * NW;            // threads
-  constexpr int CH = 512 / NT;           // 16-byte chunks per thread per 8 KB block
-  static_assert(NT <= 512 && 512 % NT == 0, "staging assumes 64..512 threads");
-  __shared__ __attribute__((aligned(16))) op_t s1[2][32 * LDSW];
-  __shared__ __attribute__((aligned(16))) op_t s2[2][32 * LDSW];
-  __shared__ __attribute__((aligned(16))) op_t s3[2][C * LDS3];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
-  const long pos0 = ((long)blockIdx.x * NW + wid) * (32 * PB);
+  __shared__ __attribute__((aligned(16))) char tl[2 * TR_STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const long pos0 = ((long)blockIdx.x * TRW + wid) * 32;
 
-  // Every wave runs the whole loop (no divergent control flow around the MFMA chain,
-  // which would make the compiler shuttle accumulators between AGPRs and VGPRs);
-  // rows past the end are clamped on load and skipped on store.
-  opx8 xf[PB][8];
-#pragma unroll
-  for (int pb = 0; pb < PB; ++pb) {
+  // rows past the end are clamped on load and skipped on store
+  opx8 xf[8];
+  {
     float x[64];
-    load_row128_oa(x_in + min(pos0 + 32 * pb + m, rows - 1) * C, h, x);
-    ln128_oa_to_frag(x, h, lnw, lnb, eps, xf[pb]);
+    load_row128_frag(x_in + min(pos0 + m, rows - 1) * C, h, x);
+    ln128_to_frag(x, h, lnw, lnb, eps, xf);
   }
-  f32x16 acc[PB][4];
+  f32x16 acc[4];
 #pragma unroll
-  for (int pb = 0; pb < PB; ++pb)
-#pragma unroll
-    for (int ob = 0; ob < 4; ++ob) acc[pb][ob] = zero16();
+  for (int ob = 0; ob < 4; ++ob) acc[ob] = zero16();
 
-  // staging: fc1/fc2 block = 32 rows x 128, fc3 block = 128 rows x 32 (512 chunks each)
-  opx8 r1[CH], r2[CH], r3[CH];
-  auto gload = [&](int hb) {
+  // DMA: chunk e = tid + 256 i (i = 0, 1) of each block; chunk tid + 256 is row R + 16
+  // (W1 / W2: same slot, perm16(R + 16) = perm16(R) + 16) or R + 64 (W3: same slot)
+  const int R = tid >> 4, R3 = tid >> 2;
+  const uint32_t o12 = 2u * (perm16(R) * C + 8 * ((tid & 15) ^ (R & 15)));
+  const uint32_t o3 = 2u * (R3 * hidden + 8 * ((tid & 3) ^ tr_swz4(R3)));
+  const uint32_t o3b = 2u * 64 * hidden;
+  auto issue = [&](int hb, int buf) {
+    char* st = tl + buf * TR_STAGE + 1024 * wid;
+    const char* b1 = (const char*)(w1 + (long)32 * hb * C);
+    const char* b2 = (const char*)(w2 + (long)32 * hb * C);
+    const char* b3 = (const char*)(w3 + 32 * hb);
 #pragma unroll
-    for (int q = 0; q < CH; ++q) {
-      const int c = tid + NT * q;
-      r1[q] = ld_x8(w1 + (long)(32 * hb + (c >> 4)) * C + (c & 15) * 8);
-      r2[q] = ld_x8(w2 + (long)(32 * hb + (c >> 4)) * C + (c & 15) * 8);
-      r3[q] = ld_x8(w3 + (long)(c >> 2) * hidden + 32 * hb + (c & 3) * 8);
+    for (int i = 0; i < 2; ++i) {
+      __builtin_amdgcn_global_load_lds(b1 + o12 + 4096 * i, st + 4096 * i, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(b2 + o12 + 4096 * i, st + TR_BLK + 4096 * i, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(b3 + o3 + o3b * i, st + 2 * TR_BLK + 4096 * i, 16, 0, 0);
     }
   };
+  // fragment read addresses: fc1 / fc2 k-step s of row m; fc3 k-step ks of row 32 ob + m
+  int a12[8], a3[2];
+#pragma unroll
+  for (int s2 = 0; s2 < 8; ++s2) a12[s2] = 256 * m + 16 * ((2 * s2 + h) ^ (m & 15));
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) a3[ks] = 2 * TR_BLK + 64 * m + 16 * ((2 * ks + h) ^ tr_swz4(m));
+
   const int nhb = hidden / 32;
-  gload(0);
+  issue(0, 0);
   for (int hb = 0; hb < nhb; ++hb) {
-    const int bufi = hb & 1;
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));   // block hb landed ...
+    __builtin_amdgcn_s_barrier();              // ... for every wave; the other stage is free
+    asm volatile("" ::: "memory");
+    if (hb + 1 < nhb) issue(hb + 1, (hb + 1) & 1);
+    const char* st = tl + (hb & 1) * TR_STAGE;
+    f32x16 a1 = zero16(), a2 = zero16();
 #pragma unroll
-    for (int q = 0; q < CH; ++q) {
-      const int c = tid + NT * q;
-      const int row = perm16(c >> 4);
-      st_x8(&s1[bufi][row * LDSW + (c & 15) * 8], r1[q]);
-      st_x8(&s2[bufi][row * LDSW + (c & 15) * 8], r2[q]);
-      st_x8(&s3[bufi][(c >> 2) * LDS3 + (c & 3) * 8], r3[q]);
+    for (int s2 = 0; s2 < 8; ++s2) {
+      a1 = mfma32(lds_x8(st + a12[s2]), xf[s2], a1);            // rows = hidden (perm16), cols = pairs
+      a2 = mfma32(lds_x8(st + TR_BLK + a12[s2]), xf[s2], a2);
     }
-    __syncthreads();
-    if (hb + 1 < nhb) gload(hb + 1);
-    f32x16 a1[PB], a2[PB];
+    opx8 hf[2];
 #pragma unroll
-    for (int pb = 0; pb < PB; ++pb) { a1[pb] = zero16(); a2[pb] = zero16(); }
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const opx8 f1 = wfrag_oa(&s1[bufi][m * LDSW], s, h);
-      const opx8 f2 = wfrag_oa(&s2[bufi][m * LDSW], s, h);
-#pragma unroll
-      for (int pb = 0; pb < PB; ++pb) {
-        a1[pb] = mfma32(f1, xf[pb][s], a1[pb]);   // rows = hidden (perm16), cols = pairs
-        a2[pb] = mfma32(f2, xf[pb][s], a2[pb]);
-      }
-    }
-    opx8 hf[PB][2];
-#pragma unroll
-    for (int pb = 0; pb < PB; ++pb)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) hf[pb][ks][t] = (op_t)(siluf(a1[pb][8 * ks + t]) * a2[pb][8 * ks + t]);
+      for (int t = 0; t < 8; ++t) hf[ks][t] = (op_t)(siluf(a1[8 * ks + t]) * a2[8 * ks + t]);
 #pragma unroll
     for (int ob = 0; ob < 4; ++ob)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const opx8 f3 = ld_x8(&s3[bufi][(32 * ob + m) * LDS3 + 16 * ks + 8 * h]);
-#pragma unroll
-        for (int pb = 0; pb < PB; ++pb) acc[pb][ob] = mfma32(f3, hf[pb][ks], acc[pb][ob]);   // D[ch][pair]
-      }
+      for (int ks = 0; ks < 2; ++ks) acc[ob] = mfma32(lds_x8(st + a3[ks] + 2048 * ob), hf[ks], acc[ob]);
   }
-  // lane (m, h) owns pair pos0 + 32 pb + m; acc[pb][ob][4g + e] is channel 32 ob + 8 g + 4 h + e
+  // lane (m, h) owns pair pos0 + m; acc[ob][4g + e] is channel 32 ob + 8 g + 4 h + e.  The
+  // residual (x_in may alias out) is loaded in 16-byte runs, all before the first store.
+  const long p = pos0 + m;
+  if (p < rows) {
+    float* dst = out + p * C;
+    f32x4 res[16];
 #pragma unroll
-  for (int pb = 0; pb < PB; ++pb) {
-    const long p = pos0 + 32 * pb + m;
-    if (p < rows) {
-      float* dst = out + p * C;
-      f32x4 res[16];
+    for (int q = 0; q < 16; ++q)
+      res[q] = accumulate ? *reinterpret_cast<const f32x4*>(dst + oa_channel(q, h)) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int q = 0; q < 16; ++q)
-        res[q] = accumulate ? *reinterpret_cast<const f32x4*>(dst + oa_channel(q, h)) : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < 16; ++q) {
+      f32x4 v;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        f32x4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[pb][q >> 2][4 * (q & 3) + e] + res[q][e];
-        *reinterpret_cast<f32x4*>(dst + oa_channel(q, h)) = v;
-      }
+      for (int e = 0; e < 4; ++e) v[e] = acc[q >> 2][4 * (q & 3) + e] + res[q][e];
+      *reinterpret_cast<f32x4*>(dst + oa_channel(q, h)) = v;
     }
   }
 }
@@ -275,11 +265,10 @@ extern "C" int pf_transition_fwd(const pf_transition_args* a) {
     return pf_fail(PF_E_INVALID, "pf_transition_fwd: null pointer argument");
   hipStream_t st = (hipStream_t)a->stream;
   if (a->C == C) {
-    constexpr int PB = TR_PB, NW = TR_NW;
-    const unsigned grid = (unsigned)((a->rows + 32 * PB * NW - 1) / (32 * PB * NW));
-    tr_pair_kernel<PB, NW, TR_MINW><<<grid, 64 * NW, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w,
-                                         (const op_t*)a->fc2_w, (const op_t*)a->fc3_w, a->rows, a->hidden,
-                                         a->accumulate, a->eps);
+    const unsigned grid = (unsigned)((a->rows + 32 * TRW - 1) / (32 * TRW));
+    tr_pair_kernel<<<grid, 64 * TRW, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w,
+                                              (const op_t*)a->fc2_w, (const op_t*)a->fc3_w, a->rows, a->hidden,
+                                              a->accumulate, a->eps);
     PF_CHECK_LAUNCH("tr_pair_kernel");
     return PF_OK;
   }
