@@ -122,6 +122,23 @@ PF_DEV void load_row128_frag(const float* __restrict__ p, int h, float (&x)[64])
   }
 }
 
+// (x - mean) * rstd of a 128-vector (load_row128_frag order) as 8 MFMA fragments: the
+// LayerNorm without its affine part, for callers that fold gamma / beta into the weights.
+PF_DEV void ln128_norm_to_frag(const float (&x)[64], float eps, opx8 (&f)[8]) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) s += x[i];
+  const float mean = xor32_sum(s) * (1.f / 128.f);
+  float v = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) { const float d = x[i] - mean; v += d * d; }
+  const float rstd = rsqrtf(xor32_sum(v) * (1.f / 128.f) + eps);
+#pragma unroll
+  for (int s8 = 0; s8 < 8; ++s8)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) f[s8][t] = (op_t)((x[8 * s8 + t] - mean) * rstd);
+}
+
 // LayerNorm of a 128-vector split over the two halves of a wave (64 values per
 // lane, in load_row128_frag order), written as 8 opx8 MFMA fragments.
 // Two-pass (mean, then centred variance) in fp32, like torch's CPU kernel.
@@ -148,6 +165,39 @@ PF_DEV void ln128_to_frag(const float (&x)[64], int h, const float* __restrict__
 // s_waitcnt immediate (gfx9 encoding) that waits until at most v vector-memory
 // operations of this wave are outstanding and leaves expcnt / lgkmcnt unconstrained.
 constexpr int vmcnt_le(int v) { return (v & 0xF) | (((v >> 4) & 3) << 14) | 0x70 | 0xF00; }
+
+// 16-byte stores from the [d][pos] accumulator layout.  Lane (m, h) holds, for run g,
+// the 4 values of elements 8g + 4h .. 8g + 4h + 3 (acc registers 4g .. 4g + 3).  One
+// v_permlane32_swap per dword gives lane (m, 0) elements 8(2p+1) .. +7 and lane (m, 1)
+// elements 16p .. 16p + 7 of run pair p, so each lane then writes 8 consecutive
+// elements (16 bytes of op_t): half-row pieces of 16 bytes are half as fast to write.
+// Writes elements [16p + 8(1-h), +8) of row `dst` (op_t, element 0 at dst) for p = 0, 1.
+PF_DEV void store_runs16(op_t* dst, const f32x16& acc, float scale, int h) {
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    uint32_t u[2][2];   // [run 2p / 2p+1][dword]
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int dw = 0; dw < 2; ++dw) {
+        typedef op_t pair_t __attribute__((ext_vector_type(2)));
+        pair_t v;
+        v[0] = (op_t)(acc[4 * (2 * p + k) + 2 * dw] * scale);
+        v[1] = (op_t)(acc[4 * (2 * p + k) + 2 * dw + 1] * scale);
+        u[k][dw] = __builtin_bit_cast(uint32_t, v);
+      }
+    uint32_t x[2], y[2];
+#pragma unroll
+    for (int dw = 0; dw < 2; ++dw) {
+      const auto r = __builtin_amdgcn_permlane32_swap(u[1][dw], u[0][dw], false, false);
+      x[dw] = r[0];   // lanes 0-31: own run 2p+1; lanes 32-63: run 2p of the lane 32 below
+      y[dw] = r[1];   // lanes 0-31: run 2p+1 of the lane 32 above; lanes 32-63: own run 2p
+    }
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const u32x4_t v = {x[0], x[1], y[0], y[1]};
+    *reinterpret_cast<u32x4_t*>(dst + 16 * p + 8 * (1 - h)) = v;
+  }
+}
 
 // Workgroup-id remap so that consecutive logical ids land on one XCD.
 // Hardware dispatches workgroup w to XCD (w % 8); with total % 8 == 0 this maps

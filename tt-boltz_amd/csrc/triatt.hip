@@ -51,94 +51,148 @@ PF_DEV op_t mask_term(bool pad, float mv) {
   return (op_t)(pad || t < -65504.f ? -INFINITY : t);
 }
 
-struct Blk32 { opx8 v[2]; };
-// Load rows [0, nrows) of a [*][128] op_t block (rows >= nrows read as zero).
-PF_DEV void blk32_load(const op_t* __restrict__ src, int nrows, int tid, Blk32& r) {
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int c = tid + 256 * q;
-    const int row = c >> 4;
-    r.v[q] = row < nrows ? ld_x8(src + row * C + (c & 15) * 8) : zero_x8();
-  }
-}
-PF_DEV void blk32_store(op_t* lds, int tid, const Blk32& r) {
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int c = tid + 256 * q;
-    st_x8(lds + (c >> 4) * LDSW + (c & 15) * 8, r.v[q]);
-  }
-}
+// ---------------------------------------------------------------------------------
+// Projection (persistent): one workgroup of 8 waves per CU keeps W_q, W_k, W_v and the
+// bias rows in LDS with the LayerNorm affine folded in (W' = W diag(gamma) in op_t,
+// c = W beta in fp32 as the accumulator start), so a tile only normalizes.  Each wave
+// walks tiles of 32 frame positions (ip, j0 .. j0+31) and loads the next tile's z rows
+// while it computes the current one.  The MFMA orientation is chosen per output so that
+// the stores are 16-byte runs (8-byte runs write at ~2/3 of the bandwidth):
+//   Q, K  [j][d]:  D[d][pos]   runs of 4 d, paired across lane halves (store_runs16)
+//   V^T   [d][k]:  D[pos][d]   a lane's key runs g = 2p, 2p+1 are 8 adjacent slots
+//   bias  [hd][j]: D[hd][pos]  a lane holds the 4 heads of its position
+// ---------------------------------------------------------------------------------
+constexpr int TAP_WAVES = 8;
+constexpr int TAP_ROWS = 3 * C + 32;   // q, k, v rows, then 32 bias rows (H used, rest zero)
+constexpr size_t TAP_LDS = (size_t)TAP_ROWS * LDSW * sizeof(op_t) + TAP_ROWS * sizeof(float);
 
-// ---------------------------------------------------------------------------------
-// Projection: one wave = 32 frame positions (ip, j0 .. j0+31).
-// Weight blocks (32 rows each): 0-3 q heads, 4-7 k heads, 8-11 v heads, 12 bias.
-// ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void ta_proj_kernel(
+__global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
     const float* __restrict__ z, const float* __restrict__ pair_mask,
     const float* __restrict__ lnw, const float* __restrict__ lnb,
     const op_t* __restrict__ wq, const op_t* __restrict__ wk, const op_t* __restrict__ wv,
     const op_t* __restrict__ wb, op_t* __restrict__ Q, op_t* __restrict__ K,
     op_t* __restrict__ Vt, op_t* __restrict__ bias16, op_t* __restrict__ mask16,
     int B, int N, int n_valid, int ending, float qscale, float eps) {
-  __shared__ __attribute__((aligned(16))) op_t lds[2][32 * LDSW];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
-  const long NN = (long)N * N;
-  const long pos0 = ((long)blockIdx.x * 4 + wid) * 32;
-  const bool active = pos0 < (long)B * NN;
+  extern __shared__ __attribute__((aligned(16))) op_t plds[];
+  float* cb = reinterpret_cast<float*>(plds + TAP_ROWS * LDSW);
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  auto wrow = [&](int row) -> const op_t* {
+    return row < C ? wq + row * C : row < 2 * C ? wk + (row - C) * C
+         : row < 3 * C ? wv + (row - 2 * C) * C : wb + (row - 3 * C) * C;
+  };
+  for (int c = tid; c < TAP_ROWS * 16; c += 64 * TAP_WAVES) {
+    const int row = c >> 4, col = (c & 15) * 8;
+    opx8 v = zero_x8();
+    if (row < 3 * C + H) {
+      const opx8 w = ld_x8(wrow(row) + col);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (op_t)((float)w[e] * lnw[col + e]);
+    }
+    st_x8(plds + row * LDSW + col, v);
+  }
+  for (int row = tid; row < TAP_ROWS; row += 64 * TAP_WAVES) {
+    float acc = 0.f;
+    if (row < 3 * C + H) {
+      const op_t* w = wrow(row);
+      for (int c = 0; c < C; ++c) acc += (float)w[c] * lnb[c];
+    }
+    cb[row] = acc;
+  }
+  __syncthreads();
 
-  int b = 0, ip = 0, j0 = 0;
-  opx8 xf[8];
-  if (active) {
+  const long NN = (long)N * N;
+  const long tiles = (long)B * NN / 32;
+  const long stride = (long)gridDim.x * TAP_WAVES;
+  // frame tile t -> (b, ip, j0) and the z pair this lane's row comes from
+  auto decode = [&](long t, int& b, int& ip, int& j0) {
+    const long pos0 = 32 * t;
     b = (int)(pos0 / NN);
     const long t0 = pos0 - (long)b * NN;
     ip = (int)(t0 / N);
     j0 = (int)(t0 - (long)ip * N);
-    const int zi = ending ? j0 + m : ip;
-    const int zj = ending ? ip : j0 + m;
-    const long pair = ((long)b * N + zi) * N + zj;
-    float x[64];
-    load_row128_frag(z + pair * C, h, x);
-    ln128_to_frag(x, h, lnw, lnb, eps, xf);
+  };
+  auto zpair = [&](int b, int ip, int j0) -> long {
+    return ((long)b * N + (ending ? j0 + m : ip)) * N + (ending ? ip : j0 + m);
+  };
+  float xn[64];
+  long t = (long)blockIdx.x * TAP_WAVES + wid;
+  if (t < tiles) {
+    int b, ip, j0;
+    decode(t, b, ip, j0);
+    load_row128_frag(z + zpair(b, ip, j0) * C, h, xn);
+  }
+  for (; t < tiles; t += stride) {
+    int b, ip, j0;
+    decode(t, b, ip, j0);
+    const long pair = zpair(b, ip, j0);
+    opx8 xf[8];
+    {
+      float x[64];
+#pragma unroll
+      for (int i = 0; i < 64; ++i) x[i] = xn[i];
+      if (t + stride < tiles) {   // next tile's rows, in flight during this tile
+        int b2, ip2, j02;
+        decode(t + stride, b2, ip2, j02);
+        load_row128_frag(z + zpair(b2, ip2, j02) * C, h, xn);
+      }
+      ln128_norm_to_frag(x, eps, xf);
+    }
     if (h == 0) {
       // frame key j0+m of row ip: padding -> excluded; otherwise inf*(mask-1) (log2 units)
       const float mv = pair_mask ? pair_mask[pair] : 1.f;
       mask16[((long)b * N + ip) * N + j0 + m] = mask_term(j0 + m >= n_valid, mv);
     }
-  }
-
-  auto src = [&](int bk) -> const op_t* {
-    return bk < 4 ? wq + bk * 32 * C : bk < 8 ? wk + (bk - 4) * 32 * C
-         : bk < 12 ? wv + (bk - 8) * 32 * C : wb;
-  };
-  Blk32 rw;
-  blk32_load(src(0), 32, tid, rw);
-  for (int bk = 0; bk < 13; ++bk) {
-    op_t* lw = lds[bk & 1];
-    blk32_store(lw, tid, rw);
-    __syncthreads();
-    if (bk + 1 < 13) blk32_load(src(bk + 1), bk + 1 < 12 ? 32 : H, tid, rw);
-    if (!active) continue;
-    f32x16 acc = zero16();
-    if (bk < 8) {
-      // normal orientation: rows = positions, cols = head dim
+    const long rowh = ((long)b * N + ip) * H;   // (b, ip) head-block index base
+    // Q, K: D[d][pos]; lane (pos m, h) holds d = 8g + 4h + e in acc[4g + e]
+#pragma unroll 1
+    for (int blk = 0; blk < 8; ++blk) {
+      f32x16 acc;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) acc = mfma32(xf[s], ld_x8(lw + m * LDSW + 16 * s + 8 * h), acc);
-      op_t* dst = bk < 4 ? Q : K;
-      const float sc = bk < 4 ? qscale : 1.f;
-      const long base = ((((long)b * N + ip) * H + (bk & 3)) * N + j0) * D;
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 c4 = *reinterpret_cast<const f32x4*>(cb + 32 * blk + 8 * g + 4 * h);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dst[base + acc_row(r, h) * D + m] = (op_t)(acc[r] * sc);
-    } else {
-      // transposed orientation: rows = head dim (or head for the bias), cols = positions
+        for (int e = 0; e < 4; ++e) acc[4 * g + e] = c4[e];
+      }
 #pragma unroll
-      for (int s = 0; s < 8; ++s) acc = mfma32(ld_x8(lw + m * LDSW + 16 * s + 8 * h), xf[s], acc);
-      if (bk < 12) {
-        const long base = (((long)b * N + ip) * H + (bk - 8)) * D * (long)N + j0 + perm16(m);
+      for (int s2 = 0; s2 < 8; ++s2) acc = mfma32(ld_x8(plds + (32 * blk + m) * LDSW + 16 * s2 + 8 * h), xf[s2], acc);
+      op_t* dst = blk < 4 ? Q : K;
+      store_runs16(dst + ((rowh + (blk & 3)) * N + j0 + m) * D, acc, blk < 4 ? qscale : 1.f, h);
+    }
+    // V^T: D[pos][d]; lane (d m, h) holds keys j0 + 8g + 4h + e in acc[4g + e]
+#pragma unroll 1
+    for (int hd = 0; hd < H; ++hd) {
+      const float c0 = cb[2 * C + 32 * hd + m];
+      f32x16 acc;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) Vt[base + (long)acc_row(r, h) * N] = (op_t)acc[r];
-      } else if (h == 0) {
+      for (int r = 0; r < 16; ++r) acc[r] = c0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) bias16[(((long)b * H + r) * N + ip) * N + j0 + m] = (op_t)(acc[r] * LOG2E);
+      for (int s2 = 0; s2 < 8; ++s2)
+        acc = mfma32(xf[s2], ld_x8(plds + (2 * C + 32 * hd + m) * LDSW + 16 * s2 + 8 * h), acc);
+      // keys 8g + 4h + e of runs g = 2p, 2p+1 sit at storage 16p + 8h .. +7 (perm16)
+      op_t* row = Vt + ((rowh + hd) * D + m) * (long)N + j0;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        opx8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (op_t)acc[8 * p + e];
+        st_x8(row + 16 * p + 8 * h, v);
+      }
+    }
+    // bias: D[hd][pos]; rows 0..H-1 are acc[0..3] of the h = 0 lanes
+    {
+      f32x16 acc;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 c4 = *reinterpret_cast<const f32x4*>(cb + 3 * C + 8 * g + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[4 * g + e] = c4[e];
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < 8; ++s2) acc = mfma32(ld_x8(plds + (3 * C + m) * LDSW + 16 * s2 + 8 * h), xf[s2], acc);
+      if (h == 0) {
+#pragma unroll
+        for (int r = 0; r < H; ++r) bias16[(((long)b * H + r) * N + ip) * N + j0 + m] = (op_t)(acc[r] * LOG2E);
       }
     }
   }
@@ -569,11 +623,21 @@ extern "C" int pf_triatt_fwd(const pf_triatt_args* a) {
   TaBuffers t = ta_buffers(a->workspace, B, N);
   const float qscale = LOG2E / sqrtf((float)D);
   const long positions = (long)B * N * N;
-  const int grid_pos = (int)((positions / 32 + 3) / 4);
-  ta_proj_kernel<<<grid_pos, 256, 0, st>>>(a->z_in, a->pair_mask, a->ln_w, a->ln_b,
-                                           (const op_t*)a->w_q, (const op_t*)a->w_k, (const op_t*)a->w_v,
-                                           (const op_t*)a->w_bias, t.Q, t.K, t.Vt, t.bias16, t.mask16, B, N,
-                                           n_valid, a->ending, qscale, a->eps);
+  {
+    static bool attr = false;
+    if (!attr) {
+      if (hipFuncSetAttribute((const void*)ta_proj_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)TAP_LDS) != hipSuccess)
+        return pf_fail(PF_E_LAUNCH, "ta_proj_kernel: cannot reserve %zu bytes of LDS", TAP_LDS);
+      attr = true;
+    }
+    const int grid = (int)min((long)device_cus(), (positions / 32 + TAP_WAVES - 1) / TAP_WAVES);
+    ta_proj_kernel<<<grid, 64 * TAP_WAVES, TAP_LDS, st>>>(a->z_in, a->pair_mask, a->ln_w, a->ln_b,
+                                                           (const op_t*)a->w_q, (const op_t*)a->w_k,
+                                                           (const op_t*)a->w_v, (const op_t*)a->w_bias, t.Q, t.K,
+                                                           t.Vt, t.bias16, t.mask16, B, N, n_valid, a->ending,
+                                                           qscale, a->eps);
+  }
   PF_CHECK_LAUNCH("ta_proj_kernel");
   int rc = launch_attn<false>(t, nullptr, B, N, n_valid, st);
   if (rc) return rc;
