@@ -396,19 +396,16 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
     const float inv = rcp_fast(xor32_sum(lsum));
     const int j = jq0 + m;
     const long rowbase = ((long)b * N + ip) * H;
+    if (OUT_F32) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      if (OUT_F32) {
+      for (int g = 0; g < 4; ++g) {
         f32x4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = o[4 * g + e] * inv;
         *reinterpret_cast<f32x4*>(O32 + ((rowbase + hd) * N + j) * D + 8 * g + 4 * h) = v;
-      } else {
-        opx4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (op_t)(o[4 * g + e] * inv);
-        st_x4(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd + 8 * g + 4 * h, v);
       }
+    } else {
+      store_runs16(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd, o, inv, h);   // 16-byte runs
     }
   };
 

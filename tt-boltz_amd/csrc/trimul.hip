@@ -343,20 +343,16 @@ __global__ __launch_bounds__(256, 1) void tm_contract_dma_kernel(
     for (int y = 0; y < 4; ++y) {
       const int jb = j0 + wn * 128 + 32 * y;
       if (ib >= N || jb >= N) continue;
+      if constexpr (sizeof(OutT) == 4) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        OutT* dst = Xp + (long)(ib + m) * N + jb + 8 * g + 4 * h;
-        if constexpr (sizeof(OutT) == 4) {
+        for (int g = 0; g < 4; ++g) {
           f32x4 v;
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = acc[y][x][4 * g + e] * out_scale;
-          *reinterpret_cast<f32x4*>(dst) = v;
-        } else {
-          opx4 v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (op_t)(acc[y][x][4 * g + e] * out_scale);
-          st_x4((op_t*)dst, v);
+          *reinterpret_cast<f32x4*>(Xp + (long)(ib + m) * N + jb + 8 * g + 4 * h) = v;
         }
+      } else {
+        store_runs16((op_t*)(Xp + (long)(ib + m) * N + jb), acc[y][x], out_scale, h);   // 16-byte runs
       }
     }
   }
