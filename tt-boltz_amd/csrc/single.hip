@@ -4,10 +4,11 @@
 // PairformerLayer (tt_bio/reference.py:906-911) and the ttnn AttentionPairBias
 // non-atom branch (tt_bio/tenstorrent.py:738-787, 838-853).
 //
-//   apb_zbias_kernel  bias[b][h][i][j] = LN(z[b,i,j]) . W_z[h]  (MFMA, one pass over z)
-//   apb_attn_kernel   one wave per (b, query i, head): fp32 logits
-//                     q.k/sqrt(d) + bias - 1e6*(1-mask_k), softmax, o = P v,
-//                     o * sigmoid(g) written for the output projection.
+//   apb_zbias_kernel  bias[b][h][i][j] = log2(e) * LN(z[b,i,j]) . W_z[h]  (MFMA, one pass
+//                     over z; log2 units for the exp2 softmax)
+//   apb_attn_kernel   one wave per (b, head, 32 queries), keys in tiles of 32: MFMA
+//                     scores q.k/sqrt(d) + bias - 1e6*(1-mask_k), fp32 online softmax,
+//                     o = P v (MFMA), o * sigmoid(g) written for the output projection.
 //   q/k/v/g and the output projection use linear_rows_kernel (transition.hip).
 #include "pf_common.h"
 #include "pf_internal.h"
@@ -44,59 +45,141 @@ __global__ __launch_bounds__(256) void apb_zbias_kernel(
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int hd = acc_row(r, h);
-    if (hd < H) bias[((long)b * H + hd) * NN + t0 + m] = acc[r];
+    if (hd < H) bias[((long)b * H + hd) * NN + t0 + m] = acc[r] * 1.4426950408889634f;
   }
 }
 
-// One wave per (b, i, head).  Logits staged in LDS (N <= 4096).  DH = head dim.
+// Attention core: one workgroup of APB_SPLIT waves per (b, head, 32 queries i0 .. i0+31);
+// wave w takes key tiles w, w + APB_SPLIT, ... (tiles of 32 keys) and the partial
+// results (running max, row sum, unnormalized O) meet in LDS at the end.
+// Scores are formed transposed, S^T[key][query] = bias^T + K.Q^T (MFMA, head dim DH
+// zero-padded to 32), in log2 units (Q pre-scaled by log2(e)/sqrt(DH), the bias stored
+// in log2 units); fp32 online softmax per query (a lane owns one query; its two halves
+// hold 16 keys each and meet in one exchange); O^T += V^T P^T (MFMA, P rounded to op_t);
+// the merged output is normalized and gated by sigmoid(g).  V^T
+// fragments are gathered straight from the fp32 rows: the 32 lanes of a half read 32
+// consecutive floats of one key row.
+constexpr int APB_SPLIT = 8;
 template <int DH>
-__global__ __launch_bounds__(256) void apb_attn_kernel(
+__global__ __launch_bounds__(64 * APB_SPLIT) void apb_attn_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ bias, const float* __restrict__ mask,
     float* __restrict__ og, int B, int N, int n_valid, int c_s, int H, float inf) {
-  extern __shared__ float slog[];   // [4][N]
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const long task = (long)blockIdx.x * 4 + wid;
-  if (task >= (long)B * N * H) return;
-  const int hd = (int)(task % H);
-  const long bi = task / H;          // b*N + i
-  const int b = (int)(bi / N), i = (int)(bi - (long)b * N);
-  constexpr int dh = DH;
-  float* lg = slog + wid * N;
-  const float scale = rsqrtf((float)dh);
-  const float* qp = q + bi * c_s + hd * dh;
-  const float* bp = bias + (((long)b * H + hd) * N + i) * N;
-  float mx = -INFINITY;
-  for (int j = lane; j < n_valid; j += 64) {   // keys >= n_valid are boundary padding
-    const float* kp = k + ((long)b * N + j) * c_s + hd * dh;
-    float dot = 0.f;
+  constexpr float LOG2E_ = 1.4426950408889634f;
+  __shared__ float so[APB_SPLIT][32][33];   // [wave][query][d] partial O (padded)
+  __shared__ float sm[APB_SPLIT][32], sl[APB_SPLIT][32];
+  const int lane = threadIdx.x & 63, h = lane >> 5, m = lane & 31;
+  const int wid = threadIdx.x >> 6;
+  const int nqb = N / 32;
+  const long task = blockIdx.x;
+  const int qb = (int)(task % nqb);
+  const long bh = task / nqb;
+  const int hd = (int)(bh % H), b = (int)(bh / H);
+  const int i0 = 32 * qb;
+  const float qs = LOG2E_ * rsqrtf((float)DH);
+  const long rowb = (long)b * N;
+  // Q (B operand): lane (query m, half h), k-step s holds d = 16 s + 8 h + t
+  opx8 qf[2];
+  {
+    const float* qr = q + (rowb + i0 + m) * c_s + hd * DH;
 #pragma unroll
-    for (int d = 0; d < dh; ++d) dot += qp[d] * kp[d];
-    float l = dot * scale + bp[j];
-    if (mask) l += (1.f - mask[(long)b * N + j]) * -inf;
-    lg[j] = l;
-    mx = fmaxf(mx, l);
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int d = 16 * s2 + 8 * h + t;
+        qf[s2][t] = (op_t)(d < DH ? qr[min(d, DH - 1)] * qs : 0.f);
+      }
   }
-  mx = wave_max(mx);
-  float sum = 0.f;
-  float acc[DH];
+  const float* br = bias + (((long)b * H + hd) * N + i0 + m) * N;   // bias row of query i0 + m
+  const float mterm = -inf * LOG2E_;
+  f32x16 o = zero16();
+  float mref = -INFINITY, lsum = 0.f;
+  for (int j0 = 32 * wid; j0 < n_valid; j0 += 32 * APB_SPLIT) {
+    // S^T init: bias[q][key] + key mask; register 4g + e is key j0 + 8g + 4h + e
+    f32x16 sc;
 #pragma unroll
-  for (int d = 0; d < dh; ++d) acc[d] = 0.f;
-  for (int j = lane; j < n_valid; j += 64) {
-    const float p = __expf(lg[j] - mx);
-    sum += p;
-    const float* vp = v + ((long)b * N + j) * c_s + hd * dh;
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(br + j0 + 8 * g4 + 4 * h);
 #pragma unroll
-    for (int d = 0; d < dh; ++d) acc[d] += p * vp[d];
-  }
-  const float inv = 1.f / wave_sum(sum);
-#pragma unroll
-  for (int d = 0; d < dh; ++d) {
-    const float od = wave_sum(acc[d]) * inv;
-    if (lane == 0) {
-      const long idx = bi * c_s + hd * dh + d;
-      og[idx] = od * sigmoidf_fast(g[idx]);
+      for (int e = 0; e < 4; ++e) {
+        const int key = j0 + 8 * g4 + 4 * h + e;
+        float t = bv[e];
+        if (key >= n_valid) t = -INFINITY;
+        else if (mask) t += (1.f - mask[rowb + key]) * mterm;
+        sc[4 * g4 + e] = t;
+      }
     }
+    // K (A operand): lane (key j0 + m, half h), k-step s holds d = 16 s + 8 h + t
+    {
+      const float* kr = k + (rowb + j0 + m) * c_s + hd * DH;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        opx8 kf;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int d = 16 * s2 + 8 * h + t;
+          kf[t] = (op_t)(d < DH ? kr[min(d, DH - 1)] : 0.f);
+        }
+        sc = mfma32(kf, qf[s2], sc);
+      }
+    }
+    // online softmax of the tile (fp32); a fully masked prefix keeps mref = -inf, P = 0
+    float mx = sc[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[r]);
+    mx = xor32_max(mx);
+    const float mnew = fmaxf(mref, mx);
+    const float msub = mnew == -INFINITY ? 0.f : mnew;
+    const float alpha = exp2_fast(mref - msub);
+    mref = mnew;
+    float ps = 0.f;
+    opx8 pf[2];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float pr = exp2_fast(sc[r] - msub);
+      ps += pr;
+      pf[r >> 3][r & 7] = (op_t)pr;
+    }
+    lsum = lsum * alpha + ps;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[r] *= alpha;
+    // V^T (A operand): lane (d = m, half h), k-step ks holds key j0 + 16 ks + 8 (t >> 2) + 4 h + (t & 3)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      opx8 vf;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int key = j0 + 16 * ks + 8 * (t >> 2) + 4 * h + (t & 3);
+        vf[t] = (op_t)(m < DH ? v[(rowb + key) * c_s + hd * DH + min(m, DH - 1)] : 0.f);
+      }
+      o = mfma32(vf, pf[ks], o);
+    }
+  }
+  // partials to LDS: lane (query m, half h) holds o[4 g4 + e] = d 8 g4 + 4 h + e
+  const float lw = xor32_sum(lsum);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) so[wid][m][acc_row(r, h)] = o[r];
+  if (h == 0) {
+    sm[wid][m] = mref;
+    sl[wid][m] = lw;
+  }
+  __syncthreads();
+  // merge: thread t < 32 * DH handles (query t / DH, d t % DH)
+  for (int t = threadIdx.x; t < 32 * DH; t += 64 * APB_SPLIT) {
+    const int qq = t / DH, d = t - qq * DH;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w2 = 0; w2 < APB_SPLIT; ++w2) M = fmaxf(M, sm[w2][qq]);
+    const float Ms = M == -INFINITY ? 0.f : M;
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < APB_SPLIT; ++w2) {
+      const float f = exp2_fast(sm[w2][qq] - Ms);
+      L += sl[w2][qq] * f;
+      O += so[w2][qq][d] * f;
+    }
+    const long idx = (rowb + i0 + qq) * c_s + hd * DH + d;
+    og[idx] = O / L * sigmoidf_fast(g[idx]);
   }
 }
 
@@ -145,13 +228,13 @@ extern "C" int pf_apb_fwd(const pf_apb_args* a) {
   apb_zbias_kernel<<<(unsigned)((pairs / 32 + 3) / 4), 256, 0, st>>>(a->z, a->zln_w, a->zln_b, (const op_t*)a->w_z,
                                                                     bias, a->B, a->N, a->H, a->eps);
   PF_CHECK_LAUNCH("apb_zbias_kernel");
-  const long tasks = rows * a->H;
-  const unsigned grid = (unsigned)((tasks + 3) / 4);
-  const size_t lds = 4 * a->N * sizeof(float);
+  const unsigned grid = (unsigned)((long)a->B * a->H * (a->N / 32));
   if (cs / a->H == 24)
-    apb_attn_kernel<24><<<grid, 256, lds, st>>>(q, k, v, g, bias, a->mask, og, a->B, a->N, n_valid, cs, a->H, 1e6f);
+    apb_attn_kernel<24><<<grid, 64 * APB_SPLIT, 0, st>>>(q, k, v, g, bias, a->mask, og, a->B, a->N, n_valid, cs,
+                                                        a->H, 1e6f);
   else
-    apb_attn_kernel<32><<<grid, 256, lds, st>>>(q, k, v, g, bias, a->mask, og, a->B, a->N, n_valid, cs, a->H, 1e6f);
+    apb_attn_kernel<32><<<grid, 64 * APB_SPLIT, 0, st>>>(q, k, v, g, bias, a->mask, og, a->B, a->N, n_valid, cs,
+                                                        a->H, 1e6f);
   PF_CHECK_LAUNCH("apb_attn_kernel");
   return pf_linear_fwd(og, a->w_o, nullptr, a->accumulate ? a->out : nullptr, a->out, rows, cs, cs, a->stream);
 }
