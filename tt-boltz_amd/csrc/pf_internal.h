@@ -18,3 +18,17 @@ int pf_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3))
 
 // Compute units of the current device (cached per device; 0 if the query fails).
 int device_cus();
+
+// One row-major projection out = resid + x W^T + bias (fp32 x/out, op_t W [Nout][K]);
+// W2 != nullptr selects SwiGLU: out = silu(x W^T) * (x W2^T).  Up to PF_LIN_MAX_JOBS
+// projections of one shape (rows, K, Nout) run in a single launch (transition.hip).
+constexpr int PF_LIN_MAX_JOBS = 4;
+struct pf_lin_job {
+  const float* x;
+  const void* W;
+  const void* W2;
+  const float* bias;
+  const float* resid;
+  float* out;
+};
+int pf_linear_batch(const pf_lin_job* jobs, int njobs, long rows, int K, int Nout, hipStream_t st);

@@ -6,10 +6,13 @@
 //
 //   apb_zbias_kernel  bias[b][h][i][j] = log2(e) * LN(z[b,i,j]) . W_z[h]  (MFMA, one pass
 //                     over z; log2 units for the exp2 softmax)
-//   apb_attn_kernel   one wave per (b, head, 32 queries), keys in tiles of 32: MFMA
-//                     scores q.k/sqrt(d) + bias - 1e6*(1-mask_k), fp32 online softmax,
-//                     o = P v (MFMA), o * sigmoid(g) written for the output projection.
-//   q/k/v/g and the output projection use linear_rows_kernel (transition.hip).
+//   apb_attn_kernel   one workgroup of 8 waves per (b, head, 32 queries); wave w takes
+//                     key tiles w, w + 8, ... (32 keys each): MFMA scores
+//                     q.k/sqrt(d) + bias - 1e6*(1-mask_k), fp32 online softmax, o = P v
+//                     (MFMA); the 8 partial (o, max, sum) merge in LDS and
+//                     o * sigmoid(g) is written for the output projection.
+//   q/k/v/g (one launch, four jobs) and the output projection use linear_rows_kernel
+//   (transition.hip).
 #include "pf_common.h"
 #include "pf_internal.h"
 
@@ -220,10 +223,12 @@ extern "C" int pf_apb_fwd(const pf_apb_args* a) {
   float* og = g + rows * cs;
   float* bias = og + rows * cs;
   int rc;
-  if ((rc = pf_linear_fwd(a->s, a->w_q, a->b_q, nullptr, q, rows, cs, cs, a->stream))) return rc;
-  if ((rc = pf_linear_fwd(a->k_in, a->w_k, nullptr, nullptr, k, rows, cs, cs, a->stream))) return rc;
-  if ((rc = pf_linear_fwd(a->k_in, a->w_v, nullptr, nullptr, v, rows, cs, cs, a->stream))) return rc;
-  if ((rc = pf_linear_fwd(a->s, a->w_g, nullptr, nullptr, g, rows, cs, cs, a->stream))) return rc;
+  // q/k/v/g share (rows, c_s, c_s): one launch
+  const pf_lin_job proj[4] = {{a->s, a->w_q, nullptr, a->b_q, nullptr, q},
+                              {a->k_in, a->w_k, nullptr, nullptr, nullptr, k},
+                              {a->k_in, a->w_v, nullptr, nullptr, nullptr, v},
+                              {a->s, a->w_g, nullptr, nullptr, nullptr, g}};
+  if ((rc = pf_linear_batch(proj, 4, rows, cs, cs, st))) return rc;
   const long pairs = (long)a->B * a->N * a->N;
   apb_zbias_kernel<<<(unsigned)((pairs / 32 + 3) / 4), 256, 0, st>>>(a->z, a->zln_w, a->zln_b, (const op_t*)a->w_z,
                                                                     bias, a->B, a->N, a->H, a->eps);

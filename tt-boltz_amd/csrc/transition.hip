@@ -143,41 +143,82 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ 
   for (int c = lane; c < C_; c += 64) out[row * C_ + c] = (xr[c] - mean) * rstd * w[c] + b[c];
 }
 
-// One wave = 32 rows x 32 output columns; a workgroup = 4 waves along the columns.
-// SWIGLU: out[:, n] = silu(x W[n]) * (x W2[n]).
+// A workgroup = one 32-row x 32-column output tile of one job; its 4 waves split the K
+// steps (contiguous quarters), each wave issuing up to 8 steps of loads before their
+// MFMAs, so a tile pays about one memory round trip per 8 steps of its quarter.  The
+// partial accumulators meet in LDS and all 256 threads run the epilogue (4 outputs each,
+// 32 consecutive columns per row).  blockIdx.z selects the job (several projections of
+// the same shape in one launch).  SWIGLU: out[:, n] = silu(x W[n]) * (x W2[n]).
+constexpr int LIN_SPLIT = 4;
+struct LinJobs { pf_lin_job j[PF_LIN_MAX_JOBS]; };
+
 template <bool SWIGLU>
-__global__ __launch_bounds__(256) void linear_rows_kernel(
-    const float* __restrict__ x, const op_t* __restrict__ W, const op_t* __restrict__ W2,
-    const float* __restrict__ bias, const float* resid, float* out, long rows, int K, int Nout) {
+__global__ __launch_bounds__(256) void linear_rows_kernel(LinJobs jobs, long rows, int K, int Nout) {
+  __shared__ float red[LIN_SPLIT][SWIGLU ? 2 : 1][16][64];
+  const pf_lin_job& jb = jobs.j[blockIdx.z];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
-  const int nt = blockIdx.y * 4 + wid;   // column tile
-  if (nt * 32 >= Nout) return;
+  const int n0 = blockIdx.y * 32;
   const long r0 = (long)blockIdx.x * 32;
-  const float* xr = x + min(r0 + m, rows - 1) * K;
-  const op_t* wr = W + (long)(nt * 32 + m) * K;
-  const op_t* wr2 = SWIGLU ? W2 + (long)(nt * 32 + m) * K : nullptr;
+  const float* xr = jb.x + min(r0 + m, rows - 1) * K;
+  const op_t* wr = (const op_t*)jb.W + (long)(n0 + m) * K;
+  const op_t* wr2 = SWIGLU ? (const op_t*)jb.W2 + (long)(n0 + m) * K : nullptr;
+  const int nsteps = K >> 4, per = (nsteps + LIN_SPLIT - 1) / LIN_SPLIT;
+  const int s0 = min(nsteps, wid * per), s1 = min(nsteps, s0 + per);
   f32x16 acc = zero16(), acc2 = zero16();
-  for (int k0 = 0; k0 < K; k0 += 16) {
-    const f32x4 a0 = *reinterpret_cast<const f32x4*>(xr + k0 + 8 * h);
-    const f32x4 a1 = *reinterpret_cast<const f32x4*>(xr + k0 + 8 * h + 4);
-    opx8 af;
-    af[0] = (op_t)a0[0]; af[1] = (op_t)a0[1]; af[2] = (op_t)a0[2]; af[3] = (op_t)a0[3];
-    af[4] = (op_t)a1[0]; af[5] = (op_t)a1[1]; af[6] = (op_t)a1[2]; af[7] = (op_t)a1[3];
-    acc = mfma32(af, ld_x8(wr + k0 + 8 * h), acc);
-    if (SWIGLU) acc2 = mfma32(af, ld_x8(wr2 + k0 + 8 * h), acc2);
-  }
-  const int n = nt * 32 + m;
-  const float bn = bias ? bias[n] : 0.f;
-  // residuals first (resid may alias out: all loads ahead of the stores, so they overlap)
-  float res[16];
+  for (int sg = s0; sg < s1; sg += 8) {
+    opx8 af[8], wf[8], wf2[8];
 #pragma unroll
-  for (int r = 0; r < 16; ++r)
-    res[r] = !SWIGLU && resid ? resid[min(r0 + acc_row(r, h), rows - 1) * Nout + n] : 0.f;
+    for (int u = 0; u < 8; ++u) {
+      const int kk = 16 * (sg + u);
+      if (sg + u < s1) {
+        const f32x4 a0 = *reinterpret_cast<const f32x4*>(xr + kk + 8 * h);
+        const f32x4 a1 = *reinterpret_cast<const f32x4*>(xr + kk + 8 * h + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          af[u][e] = (op_t)a0[e];
+          af[u][4 + e] = (op_t)a1[e];
+        }
+        wf[u] = ld_x8(wr + kk + 8 * h);
+        if (SWIGLU) wf2[u] = ld_x8(wr2 + kk + 8 * h);
+      } else {
+        af[u] = zero_x8();
+        wf[u] = zero_x8();
+        if (SWIGLU) wf2[u] = zero_x8();
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      acc = mfma32(af[u], wf[u], acc);
+      if (SWIGLU) acc2 = mfma32(af[u], wf2[u], acc2);
+    }
+  }
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const long row = r0 + acc_row(r, h);
-    if (row >= rows) continue;
-    out[row * Nout + n] = SWIGLU ? siluf(acc[r]) * acc2[r] : acc[r] + bn + res[r];
+    red[wid][0][r][lane] = acc[r];
+    if (SWIGLU) red[wid][1][r][lane] = acc2[r];
+  }
+  __syncthreads();
+  // thread (wid, lane) finishes accumulator registers 4 wid .. 4 wid + 3 of lane
+  const int n = n0 + m;
+  const float bn = jb.bias ? jb.bias[n] : 0.f;
+  float v[4], res[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * wid + i;
+    float a = 0.f, a2 = 0.f;
+#pragma unroll
+    for (int w = 0; w < LIN_SPLIT; ++w) {
+      a += red[w][0][r][lane];
+      if (SWIGLU) a2 += red[w][1][r][lane];
+    }
+    v[i] = SWIGLU ? siluf(a) * a2 : a + bn;
+    // resid may alias out: all loads ahead of the stores, so they overlap
+    res[i] = !SWIGLU && jb.resid ? jb.resid[min(r0 + acc_row(r, h), rows - 1) * Nout + n] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const long row = r0 + acc_row(4 * wid + i, h);
+    if (row < rows) jb.out[row * Nout + n] = v[i] + res[i];
   }
 }
 
@@ -230,19 +271,31 @@ extern "C" int pf_layernorm_fwd(const float* x, const float* w, const float* b, 
   return PF_OK;
 }
 
-static int launch_linear(const float* x, const void* W, const void* W2, const float* bias, const float* resid,
-                         float* out, long rows, int K, int Nout, hipStream_t st) {
-  if (!x || !W || !out) return pf_fail(PF_E_INVALID, "pf_linear_fwd: null pointer");
+int pf_linear_batch(const pf_lin_job* jobs, int njobs, long rows, int K, int Nout, hipStream_t st) {
+  if (njobs < 1 || njobs > PF_LIN_MAX_JOBS) return pf_fail(PF_E_INVALID, "pf_linear_fwd: %d jobs", njobs);
   if (rows <= 0 || K <= 0 || K % 16 || Nout <= 0 || Nout % 32)
     return pf_fail(PF_E_INVALID, "pf_linear_fwd: need rows > 0, K %% 16 == 0, Nout %% 32 == 0 (rows=%ld K=%d Nout=%d)",
                    rows, K, Nout);
-  dim3 grid((unsigned)((rows + 31) / 32), (unsigned)((Nout / 32 + 3) / 4));
-  if (W2)
-    linear_rows_kernel<true><<<grid, 256, 0, st>>>(x, (const op_t*)W, (const op_t*)W2, nullptr, nullptr, out, rows, K, Nout);
+  LinJobs J{};
+  const bool swiglu = jobs[0].W2 != nullptr;
+  for (int i = 0; i < njobs; ++i) {
+    if (!jobs[i].x || !jobs[i].W || !jobs[i].out) return pf_fail(PF_E_INVALID, "pf_linear_fwd: null pointer");
+    if ((jobs[i].W2 != nullptr) != swiglu) return pf_fail(PF_E_INVALID, "pf_linear_fwd: mixed SwiGLU jobs");
+    J.j[i] = jobs[i];
+  }
+  dim3 grid((unsigned)((rows + 31) / 32), (unsigned)(Nout / 32), (unsigned)njobs);
+  if (swiglu)
+    linear_rows_kernel<true><<<grid, 256, 0, st>>>(J, rows, K, Nout);
   else
-    linear_rows_kernel<false><<<grid, 256, 0, st>>>(x, (const op_t*)W, nullptr, bias, resid, out, rows, K, Nout);
+    linear_rows_kernel<false><<<grid, 256, 0, st>>>(J, rows, K, Nout);
   PF_CHECK_LAUNCH("linear_rows_kernel");
   return PF_OK;
+}
+
+static int launch_linear(const float* x, const void* W, const void* W2, const float* bias, const float* resid,
+                         float* out, long rows, int K, int Nout, hipStream_t st) {
+  const pf_lin_job job{x, W, W2, bias, resid, out};
+  return pf_linear_batch(&job, 1, rows, K, Nout, st);
 }
 
 extern "C" int pf_linear_fwd(const float* x, const void* W, const float* bias, const float* resid, float* out,
