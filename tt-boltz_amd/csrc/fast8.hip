@@ -157,23 +157,21 @@ __global__ __launch_bounds__(256, 2) void tm8_proj_kernel(
   uint8_t* lg = lp + 256 * WROW;
   uint8_t* lps = lg + 256 * WROW;
   uint8_t* lgs = lps + 256 * 4;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   stage_w128(wp_q, wp_s, 256, lp, lps, tid, 256);
   stage_w128(wg_q, wg_s, 256, lg, lgs, tid, 256);
   __syncthreads();
 
   const long NN = (long)N * N;
-  const long ntiles = (long)B * NN / 32;
+  const uint32_t ntiles = (uint32_t)B * N * N / 32;
   const int NB = N / 32;
-  for (long tile = (long)blockIdx.x * 4 + wid; tile < ntiles; tile += (long)gridDim.x * 4) {
+  for (uint32_t tile = blockIdx.x * 4 + wid; tile < ntiles; tile += gridDim.x * 4) {
     // keep the LayerNorm parameters out of registers across iterations (they are re-read
     // from cache each tile instead of pinning 128 VGPRs)
     asm volatile("" ::: "memory");
-    const long pos0 = tile * 32;
-    const int b = (int)(pos0 / NN);
-    const long t0 = pos0 - (long)b * NN;
-    const int orow = (int)(t0 / N);
-    const int ocol0 = (int)(t0 - (long)orow * N);
+    const PosTile pt = pos_tile(tile, N);
+    const int b = pt.b, orow = pt.r, ocol0 = pt.c0;
     const int zi = incoming ? ocol0 + m : orow;
     const int zj = incoming ? orow : ocol0 + m;
     const long pair = ((long)b * N + zi) * N + zj;
@@ -596,6 +594,8 @@ extern "C" int pf_trimul_mx8_fwd(const pf_trimul_mx8_args* a) {
   if (a->B <= 0 || a->N <= 0 || a->N % 128)
     return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: need B > 0 and N a positive multiple of 128 (B=%d N=%d)",
                    a->B, a->N);
+  if ((unsigned long long)a->B * a->N * a->N >= (1ull << 32))
+    return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: B * N * N must be below 2^32 (B=%d N=%d)", a->B, a->N);
   if (a->direction != 0 && a->direction != 1)
     return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: direction must be 0 (outgoing) or 1 (incoming)");
   if (!a->z_in || !a->out || !a->norm_in_w || !a->norm_in_b || !a->p_in_q || !a->p_in_s || !a->g_in_q ||

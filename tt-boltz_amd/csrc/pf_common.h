@@ -37,6 +37,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #define PF_DEV __device__ __forceinline__
+// Device lambdas: always inlined (an outlined lambda moves captured state through memory).
+#define PF_INLINE __attribute__((always_inline))
 
 PF_DEV f32x16 mfma32(const opx8& a, const opx8& b, const f32x16& c) {
 #ifdef PF_OPERAND_BF16
@@ -197,6 +199,16 @@ PF_DEV void store_runs16(op_t* dst, const f32x16& acc, float scale, int h) {
     const u32x4_t v = {x[0], x[1], y[0], y[1]};
     *reinterpret_cast<u32x4_t*>(dst + 16 * p + 8 * (1 - h)) = v;
   }
+}
+
+// Decode of a wave-uniform tile index t (32 consecutive positions) of a [B][N][N] grid of
+// positions, N % 32 == 0 and B * N * N < 2^32 (callers check on the host): batch b, row r,
+// first column c0.  32-bit and uniform, so it is a short scalar sequence.
+struct PosTile { int b, r, c0; };
+PF_DEV PosTile pos_tile(uint32_t t, uint32_t N) {
+  const uint32_t NN = N * N, pos0 = 32u * t;
+  const uint32_t b = pos0 / NN, t0 = pos0 - b * NN, r = t0 / N;
+  return {(int)b, (int)r, (int)(t0 - r * N)};
 }
 
 // Workgroup-id remap so that consecutive logical ids land on one XCD.

@@ -101,22 +101,20 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
   }
   __syncthreads();
 
-  const long NN = (long)N * N;
-  const long tiles = (long)B * NN / 32;
-  const long stride = (long)gridDim.x * TAP_WAVES;
+  const uint32_t tiles = (uint32_t)B * N * N / 32;
+  const uint32_t stride = gridDim.x * TAP_WAVES;
   // frame tile t -> (b, ip, j0) and the z pair this lane's row comes from
-  auto decode = [&](long t, int& b, int& ip, int& j0) {
-    const long pos0 = 32 * t;
-    b = (int)(pos0 / NN);
-    const long t0 = pos0 - (long)b * NN;
-    ip = (int)(t0 / N);
-    j0 = (int)(t0 - (long)ip * N);
+  auto decode = [&](uint32_t t, int& b, int& ip, int& j0) PF_INLINE {
+    const PosTile pt = pos_tile(t, N);
+    b = pt.b;
+    ip = pt.r;
+    j0 = pt.c0;
   };
   auto zpair = [&](int b, int ip, int j0) -> long {
     return ((long)b * N + (ending ? j0 + m : ip)) * N + (ending ? ip : j0 + m);
   };
   float xn[64];
-  long t = (long)blockIdx.x * TAP_WAVES + wid;
+  uint32_t t = blockIdx.x * TAP_WAVES + wid;
   if (t < tiles) {
     int b, ip, j0;
     decode(t, b, ip, j0);
@@ -232,7 +230,6 @@ constexpr float LSTEP_MAX = 16384.f;   // per-lane row sum of one tile that forc
 // 16 distinct 16-byte bank groups.
 PF_DEV int swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 PF_DEV int swz4(int r) { return (r >> 2) & 3; }
-#define PF_INLINE __attribute__((always_inline))
 PF_DEV opx8 lds_x8(const char* p) { return *reinterpret_cast<const opx8*>(p); }
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 PF_DEV uint32_t half_bits(op_t v) { return __builtin_bit_cast(uint16_t, v); }
@@ -465,22 +462,20 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
   extern __shared__ __attribute__((aligned(16))) op_t tlds[];
   op_t* sWg = tlds;
   op_t* sWo = tlds + C * LDSW;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   for (int c = tid; c < C * 16; c += 64 * TAO_WAVES) {
     const int row = c >> 4, col = (c & 15) * 8;
     st_x8(&sWg[row * LDSW + col], ld_x8(wg + row * C + col));
     st_x8(&sWo[row * LDSW + col], ld_x8(wo + row * C + col));
   }
   __syncthreads();
-  const long NN = (long)N * N;
-  const long ntiles = (long)B * NN / 32;
-  for (long t = (long)blockIdx.x * TAO_WAVES + wid; t < ntiles; t += (long)gridDim.x * TAO_WAVES) {
+  const uint32_t ntiles = (uint32_t)B * N * N / 32;
+  for (uint32_t t = blockIdx.x * TAO_WAVES + wid; t < ntiles; t += gridDim.x * TAO_WAVES) {
     asm volatile("" ::: "memory");   // LayerNorm parameters are re-read, not pinned in VGPRs
-    const long pos0 = t * 32;
-    const int b = (int)(pos0 / NN);
-    const long t0 = pos0 - (long)b * NN;
-    const int ip = (int)(t0 / N);
-    const int j = (int)(t0 - (long)ip * N) + m;
+    const long pos0 = 32l * t;
+    const PosTile pt = pos_tile(t, N);
+    const int b = pt.b, ip = pt.r, j = pt.c0 + m;
     const long zp = ending ? ((long)b * N + j) * N + ip : ((long)b * N + ip) * N + j;
     float zr[64];
     opx8 xf[8];
@@ -606,6 +601,8 @@ extern "C" int pf_triatt_fwd(const pf_triatt_args* a) {
                    a->C, a->H, a->D);
   if (a->B <= 0 || a->N <= 0 || a->N % 64)
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: need B > 0 and N a positive multiple of 64 (B=%d N=%d)", a->B, a->N);
+  if ((unsigned long long)a->B * a->N * a->N >= (1ull << 32))
+    return pf_fail(PF_E_INVALID, "pf_triatt_fwd: B * N * N must be below 2^32 (B=%d N=%d)", a->B, a->N);
   if (!a->z_in || !a->out || !a->ln_w || !a->ln_b || !a->w_bias || !a->w_q || !a->w_k ||
       !a->w_v || !a->w_g || !a->w_o || !a->workspace)
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: null pointer argument");

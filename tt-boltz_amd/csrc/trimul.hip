@@ -62,7 +62,8 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
   extern __shared__ __attribute__((aligned(16))) op_t wlds[];
   op_t* lp = wlds;
   op_t* lg = wlds + 256 * LDSW;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   op_t* stg = wlds + 2 * 256 * LDSW + wid * 32 * SPITCH;   // this wave's output stage
 #pragma unroll 4
   for (int c = tid; c < 256 * 16; c += 64 * TMP_WAVES) {
@@ -72,21 +73,19 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
   }
   __syncthreads();
 
-  const long NN = (long)N * N;
-  const long ntiles = (long)B * NN / 32;
-  const long stride = (long)gridDim.x * TMP_WAVES;
-  auto tile_pair = [&](long t, int& b, int& orow, int& ocol0) -> long {
-    const long pos0 = t * 32;
-    b = (int)(pos0 / NN);
-    const long t0 = pos0 - (long)b * NN;
-    orow = (int)(t0 / N);
-    ocol0 = (int)(t0 - (long)orow * N);
+  const uint32_t ntiles = (uint32_t)B * N * N / 32;
+  const uint32_t stride = gridDim.x * TMP_WAVES;
+  auto tile_pair = [&](uint32_t t, int& b, int& orow, int& ocol0) PF_INLINE -> long {
+    const PosTile pt = pos_tile(t, N);
+    b = pt.b;
+    orow = pt.r;
+    ocol0 = pt.c0;
     const int zi = incoming ? ocol0 + m : orow;
     const int zj = incoming ? orow : ocol0 + m;
     return ((long)b * N + zi) * N + zj;
   };
 
-  for (long t = (long)blockIdx.x * TMP_WAVES + wid; t < ntiles; t += stride) {
+  for (uint32_t t = blockIdx.x * TMP_WAVES + wid; t < ntiles; t += stride) {
     asm volatile("" ::: "memory");   // LayerNorm parameters are re-read each tile, not pinned in VGPRs
     int cb_b, cb_orow, cb_ocol0;
     const long pair = tile_pair(t, cb_b, cb_orow, cb_ocol0);
@@ -381,7 +380,8 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
   extern __shared__ __attribute__((aligned(16))) op_t olds[];
   op_t* sWp = olds;
   op_t* sWg = olds + C * LDSW;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   XT* xs = reinterpret_cast<XT*>(olds + 2 * C * LDSW) + wid * C * XSP;   // this wave's X stage
   for (int c = tid; c < C * 16; c += 64 * TMO_WAVES) {
     const int row = c >> 4, col = (c & 15) * 8;
@@ -390,11 +390,11 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
   }
   __syncthreads();
   const long NN = (long)N * N;
-  const long ntiles = (long)B * NN / 32;
-  for (long t = (long)blockIdx.x * TMO_WAVES + wid; t < ntiles; t += (long)gridDim.x * TMO_WAVES) {
+  const uint32_t ntiles = (uint32_t)B * N * N / 32;
+  for (uint32_t t = blockIdx.x * TMO_WAVES + wid; t < ntiles; t += gridDim.x * TMO_WAVES) {
     asm volatile("" ::: "memory");   // LayerNorm parameters are re-read, not pinned in VGPRs
-    const long p0 = t * 32;                        // first pair (global index b*NN + i*N + j)
-    const int b = (int)(p0 / NN);
+    const long p0 = 32l * t;                       // first pair (global index b*NN + i*N + j)
+    const int b = pos_tile(t, N).b;
     {
       // X[b][ch][q0 .. q0+31]: 16-byte chunk c -> channel c >> 2, pairs 8*(c & 3) ..
       const XT* src = X + (long)b * C * NN + (p0 - (long)b * NN);
@@ -488,6 +488,8 @@ extern "C" int pf_trimul_fwd(const pf_trimul_args* a) {
   if (a->hidden != C) return pf_fail(PF_E_INVALID, "pf_trimul_fwd: hidden must equal c_z = 128 (got %d)", a->hidden);
   if (a->B <= 0 || a->N <= 0 || a->N % 64)
     return pf_fail(PF_E_INVALID, "pf_trimul_fwd: need B > 0 and N a positive multiple of 64 (B=%d N=%d)", a->B, a->N);
+  if ((unsigned long long)a->B * a->N * a->N >= (1ull << 32))
+    return pf_fail(PF_E_INVALID, "pf_trimul_fwd: B * N * N must be below 2^32 (B=%d N=%d)", a->B, a->N);
   if (a->direction != 0 && a->direction != 1)
     return pf_fail(PF_E_INVALID, "pf_trimul_fwd: direction must be 0 (outgoing) or 1 (incoming)");
   if (!a->z_in || !a->out || !a->norm_in_w || !a->norm_in_b || !a->p_in_w || !a->g_in_w ||
