@@ -190,6 +190,17 @@ typedef struct pf_apb_args {
 size_t pf_apb_workspace_size(int B, int N, int c_s, int H);
 int pf_apb_fwd(const pf_apb_args* args);
 
+/* pf_apb_fwd in two halves, for callers that overlap the single track with the next
+ * layer's pair operations on a second stream: pf_apb_pair_bias computes the z-dependent
+ * part (bias = proj_z.1(LN(z)), tt_bio/boltz2.py:353-356) into the workspace, and
+ * pf_apb_attend runs the rest (boltz2.py:343-352, 357-367) with that bias, on its own
+ * stream (args->stream of each call).  Same arguments for both (pf_apb_pair_bias reads
+ * only the shape, z, zln_w, zln_b, w_z, eps, workspace and stream); the caller orders
+ * pf_apb_attend after pf_apb_pair_bias and the next pf_apb_pair_bias after the previous
+ * pf_apb_attend on one workspace.  pf_apb_fwd(a) == pf_apb_pair_bias(a); pf_apb_attend(a). */
+int pf_apb_pair_bias(const pf_apb_args* args);
+int pf_apb_attend(const pf_apb_args* args);
+
 /* ------------------------------------------------------------------------------
  * Fast mode (block fp8).  Replaces the --fast path of the ttnn TriangleMultiplication
  * and Transition (tt_bio/tenstorrent.py:60-61, 178-181, 389-407, 431-503, 879-906),

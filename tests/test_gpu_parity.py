@@ -274,3 +274,23 @@ def test_recycler(gpu):
     s_got, z_got = rec(s_init.to(gpu), z_init.to(gpu), mask.to(gpu), 1)
     check("recycler z", z_got, z_ref)
     check("recycler s", s_got, s_ref)
+
+
+def test_single_track_overlap_identical(gpu):
+    """The single track on a second stream (overlapped with the next layer's pair
+    operations) gives bit-identical s and z to the same stack run in reference order on
+    one stream: same kernels, same inputs, only the schedule differs."""
+    N, n_blocks = 128, 3
+    w = synthetic.stack_weights(n_blocks, 31)
+    s, z, mask, pm = _inputs(N, 32)
+    out = {}
+    for overlap in (False, True):
+        pf = pairformer.Pairformer(n_blocks, 32, 4, 24, 16, True, w,
+                                   options=pairformer.Options(overlap_single=overlap))
+        s_d, z_d = s.to(gpu).contiguous(), z.to(gpu).contiguous()
+        out[overlap] = pf(s_d, z_d, pm.to(gpu), mask.to(gpu))
+        torch.cuda.synchronize()
+    assert torch.equal(out[True][0], out[False][0]) and torch.equal(out[True][1], out[False][1])
+    s_ref, z_ref = ref.pairformer_stack(s, z, mask, pm, w, n_blocks)
+    check("overlapped 3-layer stack z", out[True][1], z_ref)
+    check("overlapped 3-layer stack s", out[True][0], s_ref)

@@ -103,6 +103,8 @@ SIGNATURES = {
     "pf_transition_fwd": (c_int, [ctypes.POINTER(TransitionArgs)]),
     "pf_apb_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "pf_apb_fwd": (c_int, [ctypes.POINTER(ApbArgs)]),
+    "pf_apb_pair_bias": (c_int, [ctypes.POINTER(ApbArgs)]),
+    "pf_apb_attend": (c_int, [ctypes.POINTER(ApbArgs)]),
     "pf_layernorm_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_float, c_void_p]),
     "pf_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_int, c_void_p]),
     "pf_pair_ln_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long,

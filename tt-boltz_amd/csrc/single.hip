@@ -198,21 +198,45 @@ extern "C" size_t pf_apb_workspace_size(int B, int N, int c_s, int H) {
   return (5 * rows * c_s + (size_t)B * H * N * N) * sizeof(float);
 }
 
-extern "C" int pf_apb_fwd(const pf_apb_args* a) {
-  if (!a) return pf_fail(PF_E_INVALID, "pf_apb_fwd: null args");
+// Shape / pointer / workspace checks shared by the three entry points.
+static int apb_check(const pf_apb_args* a, const char* fn, bool bias_only) {
+  if (!a) return pf_fail(PF_E_INVALID, "%s: null args", fn);
   if (a->B <= 0 || a->N <= 0 || a->C != C || a->H <= 0 || a->H > 32 || a->c_s % a->H ||
       (a->c_s / a->H != 24 && a->c_s / a->H != 32) || a->c_s % 32 || a->N > 4096 || (a->N % 32))
-    return pf_fail(PF_E_INVALID, "pf_apb_fwd: unsupported shape B=%d N=%d c_s=%d C=%d H=%d", a->B, a->N, a->c_s,
-                   a->C, a->H);
-  if (!a->s || !a->k_in || !a->z || !a->out || !a->w_q || !a->b_q || !a->w_k || !a->w_v || !a->w_g ||
-      !a->w_o || !a->zln_w || !a->zln_b || !a->w_z || !a->workspace)
-    return pf_fail(PF_E_INVALID, "pf_apb_fwd: null pointer argument");
+    return pf_fail(PF_E_INVALID, "%s: unsupported shape B=%d N=%d c_s=%d C=%d H=%d", fn, a->B, a->N, a->c_s, a->C,
+                   a->H);
+  if (!a->z || !a->zln_w || !a->zln_b || !a->w_z || !a->workspace)
+    return pf_fail(PF_E_INVALID, "%s: null pointer argument", fn);
+  if (!bias_only && (!a->s || !a->k_in || !a->out || !a->w_q || !a->b_q || !a->w_k || !a->w_v || !a->w_g ||
+                     !a->w_o))
+    return pf_fail(PF_E_INVALID, "%s: null pointer argument", fn);
   if (a->n_valid < 0 || a->n_valid > a->N)
-    return pf_fail(PF_E_INVALID, "pf_apb_fwd: n_valid %d outside [0, N=%d]", a->n_valid, a->N);
-  const int n_valid = a->n_valid ? a->n_valid : a->N;
+    return pf_fail(PF_E_INVALID, "%s: n_valid %d outside [0, N=%d]", fn, a->n_valid, a->N);
   const size_t need = pf_apb_workspace_size(a->B, a->N, a->c_s, a->H);
   if (a->workspace_bytes < need)
-    return pf_fail(PF_E_INVALID, "pf_apb_fwd: workspace too small (%zu < %zu bytes)", a->workspace_bytes, need);
+    return pf_fail(PF_E_INVALID, "%s: workspace too small (%zu < %zu bytes)", fn, a->workspace_bytes, need);
+  return PF_OK;
+}
+
+// Workspace: q, k, v, g, o*sigmoid(g) [rows][c_s] fp32 each, then the pair bias [B][H][N][N].
+static float* apb_bias_buf(const pf_apb_args* a) {
+  return (float*)a->workspace + 5 * (size_t)a->B * a->N * a->c_s;
+}
+
+extern "C" int pf_apb_pair_bias(const pf_apb_args* a) {
+  int rc = apb_check(a, "pf_apb_pair_bias", true);
+  if (rc) return rc;
+  const long pairs = (long)a->B * a->N * a->N;
+  apb_zbias_kernel<<<(unsigned)((pairs / 32 + 3) / 4), 256, 0, (hipStream_t)a->stream>>>(
+      a->z, a->zln_w, a->zln_b, (const op_t*)a->w_z, apb_bias_buf(a), a->B, a->N, a->H, a->eps);
+  PF_CHECK_LAUNCH("apb_zbias_kernel");
+  return PF_OK;
+}
+
+extern "C" int pf_apb_attend(const pf_apb_args* a) {
+  int rc = apb_check(a, "pf_apb_attend", false);
+  if (rc) return rc;
+  const int n_valid = a->n_valid ? a->n_valid : a->N;
   hipStream_t st = (hipStream_t)a->stream;
   const long rows = (long)a->B * a->N;
   const int cs = a->c_s;
@@ -221,18 +245,13 @@ extern "C" int pf_apb_fwd(const pf_apb_args* a) {
   float* v = k + rows * cs;
   float* g = v + rows * cs;
   float* og = g + rows * cs;
-  float* bias = og + rows * cs;
-  int rc;
+  float* bias = apb_bias_buf(a);
   // q/k/v/g share (rows, c_s, c_s): one launch
   const pf_lin_job proj[4] = {{a->s, a->w_q, nullptr, a->b_q, nullptr, q},
                               {a->k_in, a->w_k, nullptr, nullptr, nullptr, k},
                               {a->k_in, a->w_v, nullptr, nullptr, nullptr, v},
                               {a->s, a->w_g, nullptr, nullptr, nullptr, g}};
   if ((rc = pf_linear_batch(proj, 4, rows, cs, cs, st))) return rc;
-  const long pairs = (long)a->B * a->N * a->N;
-  apb_zbias_kernel<<<(unsigned)((pairs / 32 + 3) / 4), 256, 0, st>>>(a->z, a->zln_w, a->zln_b, (const op_t*)a->w_z,
-                                                                    bias, a->B, a->N, a->H, a->eps);
-  PF_CHECK_LAUNCH("apb_zbias_kernel");
   const unsigned grid = (unsigned)((long)a->B * a->H * (a->N / 32));
   if (cs / a->H == 24)
     apb_attn_kernel<24><<<grid, 64 * APB_SPLIT, 0, st>>>(q, k, v, g, bias, a->mask, og, a->B, a->N, n_valid, cs,
@@ -242,4 +261,11 @@ extern "C" int pf_apb_fwd(const pf_apb_args* a) {
                                                         a->H, 1e6f);
   PF_CHECK_LAUNCH("apb_attn_kernel");
   return pf_linear_fwd(og, a->w_o, nullptr, a->accumulate ? a->out : nullptr, a->out, rows, cs, cs, a->stream);
+}
+
+extern "C" int pf_apb_fwd(const pf_apb_args* a) {
+  int rc = apb_check(a, "pf_apb_fwd", false);
+  if (rc) return rc;
+  if ((rc = pf_apb_pair_bias(a))) return rc;
+  return pf_apb_attend(a);
 }

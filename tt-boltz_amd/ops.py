@@ -161,18 +161,29 @@ def apb_workspace_bytes(B: int, N: int, c_s: int, H: int, variant: str = DEFAULT
     return _lib.load(variant).pf_apb_workspace_size(B, N, c_s, H)
 
 
-def launch_apb(s: torch.Tensor, k_in: torch.Tensor, z: torch.Tensor, mask: Optional[torch.Tensor],
-               out: torch.Tensor, w: Mapping[str, torch.Tensor], n_heads: int, ws: torch.Tensor,
-               accumulate: bool, eps: float = 1e-5, n_valid: int = 0, variant: str = DEFAULT_VARIANT) -> None:
+def _apb_args(s: torch.Tensor, k_in: torch.Tensor, z: torch.Tensor, mask: Optional[torch.Tensor],
+              out: torch.Tensor, w: Mapping[str, torch.Tensor], n_heads: int, ws: torch.Tensor,
+              accumulate: bool, eps: float, n_valid: int):
     B, N, c_s = s.shape
-    a = _lib.ApbArgs(
+    return _lib.ApbArgs(
         B=B, N=N, c_s=c_s, C=z.shape[-1], H=n_heads, accumulate=int(accumulate), n_valid=n_valid, eps=eps,
         s=_ptr(s), k_in=_ptr(k_in), z=_ptr(z), mask=_ptr(mask), out=_ptr(out),
         w_q=_ptr(w["proj_q.weight"]), b_q=_ptr(w["proj_q.bias"]), w_k=_ptr(w["proj_k.weight"]),
         w_v=_ptr(w["proj_v.weight"]), w_g=_ptr(w["proj_g.weight"]), w_o=_ptr(w["proj_o.weight"]),
         zln_w=_ptr(w["proj_z.0.weight"]), zln_b=_ptr(w["proj_z.0.bias"]), w_z=_ptr(w["proj_z.1.weight"]),
         workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
-    _lib.check(_lib.load(variant).pf_apb_fwd(ctypes.byref(a)), "pf_apb_fwd", variant)
+
+
+def launch_apb(s: torch.Tensor, k_in: torch.Tensor, z: torch.Tensor, mask: Optional[torch.Tensor],
+               out: torch.Tensor, w: Mapping[str, torch.Tensor], n_heads: int, ws: torch.Tensor,
+               accumulate: bool, eps: float = 1e-5, n_valid: int = 0, variant: str = DEFAULT_VARIANT,
+               part: str = "all") -> None:
+    """AttentionPairBias on the current stream.  ``part``: "all" (pf_apb_fwd), "bias" (only
+    the z-dependent pair bias into ``ws``, pf_apb_pair_bias) or "attend" (the rest, reading
+    the bias a previous "bias" call left in ``ws``, pf_apb_attend)."""
+    a = _apb_args(s, k_in, z, mask, out, w, n_heads, ws, accumulate, eps, n_valid)
+    fn = {"all": "pf_apb_fwd", "bias": "pf_apb_pair_bias", "attend": "pf_apb_attend"}[part]
+    _lib.check(getattr(_lib.load(variant), fn)(ctypes.byref(a)), fn, variant)
 
 
 def launch_layernorm(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, out: torch.Tensor,

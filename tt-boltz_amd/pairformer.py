@@ -95,13 +95,16 @@ class WeightScope:
 class Options:
     """Replaces ttnn's ``compute_kernel_config``: numerics knobs shared by the kernels.
 
-    ``operand``: MFMA operand type, ``"fp16"`` (default) or ``"bf16"``."""
+    ``operand``: MFMA operand type, ``"fp16"`` (default) or ``"bf16"``.
+    ``overlap_single``: run each layer's single-track update on a second stream, overlapped
+    with the next layer's pair operations (results are identical; default on)."""
 
-    def __init__(self, eps: float = 1e-5, operand: str = ops.DEFAULT_VARIANT):
+    def __init__(self, eps: float = 1e-5, operand: str = ops.DEFAULT_VARIANT, overlap_single: bool = True):
         if operand not in ops.TORCH_DTYPE:
             raise ValueError(f"operand must be one of {sorted(ops.TORCH_DTYPE)}, got {operand!r}")
         self.eps = eps
         self.operand = operand
+        self.overlap_single = overlap_single
 
 
 class Module:
@@ -248,15 +251,46 @@ class AttentionPairBias(Module):
 
     def __call__(self, s: torch.Tensor, z: torch.Tensor, mask: Optional[torch.Tensor] = None,
                  k_in: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None, accumulate: bool = False,
-                 ws: Optional[torch.Tensor] = None, n_valid: int = 0) -> torch.Tensor:
+                 ws: Optional[torch.Tensor] = None, n_valid: int = 0, part: str = "all") -> torch.Tensor:
+        """``part="bias"`` computes only the pair bias from z into ``ws``; ``part="attend"``
+        runs the rest with the bias a previous "bias" call left in the same ``ws`` (the two
+        halves may run on different streams, ordered by the caller)."""
         B, N, _ = s.shape
         if ws is None:
+            if part != "all":
+                raise ValueError("AttentionPairBias: part='bias'/'attend' need the caller's workspace")
             ws = ops.workspace(self.workspace_bytes(B, N), s.device)
         if out is None:
             out = torch.empty_like(s)
         ops.launch_apb(s, s if k_in is None else k_in, z, mask, out, self.w, self.n_heads, ws, accumulate,
-                       self.options.eps, n_valid, self.variant)
+                       self.options.eps, n_valid, self.variant, part)
         return out
+
+
+class SingleTrackStream:
+    """A second HIP stream (default priority) for the single-track half of each layer.
+
+    The single track of layer L (pre_norm_s, attention with pair bias, transition_s) reads
+    z only through the pair bias, which is computed on the caller's stream right after the
+    layer's pair operations; the rest runs here, overlapped with layer L+1's pair
+    operations, which never touch s.  ``ws`` is the single track's own workspace.  The
+    next layer's pair bias (which overwrites the bias in ``ws``) and ``join()`` wait for
+    the previous single track on the caller's stream.
+    """
+
+    def __init__(self, nbytes: int, device: torch.device):
+        self.stream = torch.cuda.Stream(device=device)
+        self.ws = ops.workspace(nbytes, device)
+        self.done: Optional[torch.cuda.Event] = None
+
+    def wait_previous(self) -> None:
+        if self.done is not None:
+            torch.cuda.current_stream().wait_event(self.done)
+
+    def join(self) -> None:
+        """Make the caller's stream wait for every single-track update issued so far."""
+        self.wait_previous()
+        self.done = None
 
 
 class PairformerLayer(Module):
@@ -286,17 +320,25 @@ class PairformerLayer(Module):
                                                          self.options)
             self.transition_s = Transition(self.scope("transition_s"), self.options)
 
+    def single_workspace_bytes(self, B: int, N: int) -> int:
+        """Workspace of the single-track half (pre_norm_s output, then the attention's)."""
+        if not self.transform_s:
+            return 0
+        c_s = self.attention_pair_bias.c_s
+        return max(self.attention_pair_bias.workspace_bytes(B, N) + B * N * c_s * 4,
+                   self.transition_s.workspace_bytes(B * N))
+
     def workspace_bytes(self, B: int, N: int) -> int:
         n = max(self.triangle_multiplication_start.workspace_bytes(B, N),
                 self.triangle_attention_start.workspace_bytes(B, N))
-        if self.transform_s:
-            c_s = self.attention_pair_bias.c_s
-            n = max(n, self.attention_pair_bias.workspace_bytes(B, N) + B * N * c_s * 4,
-                    self.transition_s.workspace_bytes(B * N))
-        return n
+        return max(n, self.single_workspace_bytes(B, N))
 
     def __call__(self, s: Optional[torch.Tensor], z: torch.Tensor, pair_mask: Optional[torch.Tensor] = None,
-                 mask: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None, n_valid: int = 0):
+                 mask: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None, n_valid: int = 0,
+                 single: Optional[SingleTrackStream] = None):
+        """With ``single``, the single-track update is left running on ``single.stream``
+        (call ``single.join()`` before reading s); otherwise everything is on the current
+        stream in reference order."""
         B, N = z.shape[0], z.shape[1]
         if ws is None:
             ws = ops.workspace(self.workspace_bytes(B, N), z.device)
@@ -307,13 +349,34 @@ class PairformerLayer(Module):
         self.transition_z(z, out=z, accumulate=True, ws=ws)
         if self.transform_s and s is not None:
             c_s = s.shape[-1]
-            s_norm = ws[: B * N * c_s * 4].view(torch.float32).view(B, N, c_s)
-            ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps,
-                                 self.variant)
-            apb_ws = ws[B * N * c_s * 4:]
-            self.attention_pair_bias(s_norm, z, mask, k_in=s_norm, out=s, accumulate=True, ws=apb_ws,
-                                     n_valid=n_valid)
-            self.transition_s(s, out=s, accumulate=True, ws=ws)
+            sws = ws if single is None else single.ws
+            s_norm = sws[: B * N * c_s * 4].view(torch.float32).view(B, N, c_s)
+            apb_ws = sws[B * N * c_s * 4:]
+            if single is None:
+                ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps,
+                                     self.variant)
+                self.attention_pair_bias(s_norm, z, mask, k_in=s_norm, out=s, accumulate=True, ws=apb_ws,
+                                         n_valid=n_valid)
+                self.transition_s(s, out=s, accumulate=True, ws=sws)
+                return s, z
+            # the previous single track must be done with the workspace (and s) first
+            single.wait_previous()
+            self.attention_pair_bias(s, z, mask, out=s, ws=apb_ws, n_valid=n_valid, part="bias")
+            ready = torch.cuda.Event()
+            ready.record(torch.cuda.current_stream())
+            with torch.cuda.stream(single.stream):
+                single.stream.wait_event(ready)
+                ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps,
+                                     self.variant)
+                self.attention_pair_bias(s_norm, z, mask, k_in=s_norm, out=s, accumulate=True, ws=apb_ws,
+                                         n_valid=n_valid, part="attend")
+                self.transition_s(s, out=s, accumulate=True, ws=sws)
+                done = torch.cuda.Event()
+                done.record(single.stream)
+            for t in (s, mask, sws):
+                if t is not None:
+                    t.record_stream(single.stream)
+            single.done = done
         return s, z
 
 
@@ -334,12 +397,26 @@ class Pairformer(Module):
     def workspace_bytes(self, B: int, N: int) -> int:
         return max((b.workspace_bytes(B, N) for b in self.blocks), default=16)
 
+    def single_track(self, B: int, N: int, device: torch.device) -> Optional[SingleTrackStream]:
+        """The (cached) second stream and workspace for overlapping the single track."""
+        if not self.transform_s or not self.options.overlap_single:
+            return None
+        nb = max((b.single_workspace_bytes(B, N) for b in self.blocks), default=16)
+        key = (B, N, str(device))
+        if getattr(self, "_single_key", None) != key:
+            self._single = SingleTrackStream(nb, device)
+            self._single_key = key
+        return self._single
+
     def __call__(self, s: Optional[torch.Tensor], z: torch.Tensor, pair_mask: Optional[torch.Tensor] = None,
                  mask: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None, n_valid: int = 0):
         if ws is None:
             ws = ops.workspace(self.workspace_bytes(z.shape[0], z.shape[1]), z.device)
+        single = self.single_track(z.shape[0], z.shape[1], z.device) if s is not None else None
         for block in self.blocks:
-            s, z = block(s, z, pair_mask, mask, ws, n_valid)
+            s, z = block(s, z, pair_mask, mask, ws, n_valid, single)
+        if single is not None:
+            single.join()
         return s, z
 
 
