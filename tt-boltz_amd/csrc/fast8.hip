@@ -202,8 +202,18 @@ __global__ __launch_bounds__(256, 2) void tm8_proj_kernel(
       const i32x4 q = quantize16(v, byte);
       const int ch = 32 * (cb & 3) + m;
       uint8_t* plane = (cb < 4 ? A8 : B8) + (((long)b * C + ch) * N + orow) * N + ocol0;
+      // dword g of lane half h holds positions 8g + 4h .. +3; one v_permlane32_swap per
+      // dword pair gives half 0 positions 0..15 and half 1 positions 16..31, so the
+      // 32-byte plane-row segment leaves as two 16-byte stores instead of eight 4-byte ones
+      i32x4 o;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) *reinterpret_cast<int*>(plane + 8 * g + 4 * h) = q[g];
+      for (int k = 0; k < 2; ++k) {
+        // r[1] on half 0 = half 1's q[k]; r[0] on half 1 = half 0's q[2+k]
+        const auto r = __builtin_amdgcn_permlane32_swap(q[k], q[2 + k], false, false);
+        o[2 * k] = h ? (int)r[0] : q[k];
+        o[2 * k + 1] = h ? q[2 + k] : (int)r[1];
+      }
+      *reinterpret_cast<i32x4*>(plane + 16 * h) = o;
       if (h == 0) (cb < 4 ? SA : SB)[(((long)b * C + ch) * N + orow) * NB + ocol0 / 32] = (uint8_t)byte;
     }
   }
