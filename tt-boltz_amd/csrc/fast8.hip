@@ -437,26 +437,32 @@ __global__ __launch_bounds__(256, 2) void tm8_out_kernel(
 }
 
 // ---------------------------------------------------------------------------------
-// Pair transition in fp8.  One wave = 32 pairs.  Per step hp the 64 hidden units
-// 64hp .. 64hp+63 (MX blocks 2hp, 2hp+1): fc1/fc2 rows and the matching fc3 columns
-// are staged in LDS (double buffer); fc1/fc2 run as D[hidden][pair] so a lane holds 16
-// hidden units of each block for one pair, which after silu*mul and quantization is
-// directly the fc3 A operand (fc3 columns are stored in that in-block order, perm = 1
-// of mx8_quantize_kernel).
+// Pair transition, MXFP8.  A workgroup is 4 waves x 32 pairs; three workgroups share a CU
+// (<= 168 VGPRs).  Per block of 64 hidden units the fp8 fc1 / fc2 rows ([64][128] bytes),
+// the fc3 column slice ([128][64] bytes) and their scale bytes move global -> LDS by DMA
+// (global_load_lds, no VGPR staging) into a 2-stage ring, one barrier per block.  Rows
+// are unpadded with XOR-swizzled 16-byte chunks (fc1 / fc2: chunk c of row R at slot
+// c ^ swz8(R); fc3: c ^ swz4(R)) so fragment reads are conflict-free.  fc1 / fc2 run as
+// D[hidden][pair]; silu(a)*b is quantized per 32 hidden units (one lane-half exchange)
+// and is directly fc3's B operand (fc3.weight is stored in accumulator order, perm = 1);
+// fc3 runs as D[channel][pair], so a lane owns one pair and the residual update is
+// 16-byte loads and stores in the output-aligned layout.
 // ---------------------------------------------------------------------------------
-constexpr int W3ROW = 80;      // LDS pitch of a 64-byte fc3 column slice: 5 x 16 B
-constexpr size_t TR8_STAGE = 2 * 64 * WROW + 128 * W3ROW + 2 * 64 * 4 + 128 * 2;
-constexpr size_t TR8_LDS = 2 * TR8_STAGE;
+constexpr int TR8_W1 = 0, TR8_W2 = 8192, TR8_W3 = 16384, TR8_S1 = 24576, TR8_S2 = 24832, TR8_S3 = 25088;
+constexpr int TR8_STAGE = 25600;   // bytes of one ring stage
+PF_DEV int tr8_swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+PF_DEV int tr8_swz4(int r) { return (r >> 2) & 3; }
 
-__global__ __launch_bounds__(256) void tr8_pair_kernel(
+__global__ __launch_bounds__(256, 3) void tr8_pair_kernel(
     const float* x_in, float* out, const float* __restrict__ lnw, const float* __restrict__ lnb,
     const uint8_t* __restrict__ w1q, const uint8_t* __restrict__ w1s, const uint8_t* __restrict__ w2q,
     const uint8_t* __restrict__ w2s, const uint8_t* __restrict__ w3q, const uint8_t* __restrict__ w3s,
     long rows, int hidden, int accumulate, float eps) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
+  __shared__ __attribute__((aligned(16))) uint8_t tl[2 * TR8_STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const long pos0 = ((long)blockIdx.x * 4 + wid) * 32;
-  const int nblk = hidden / 32;   // MX blocks along the hidden axis
+  const int nblk = hidden / 32;   // MX blocks along the hidden axis (a multiple of 4)
 
   X8 xq;
   {
@@ -468,82 +474,95 @@ __global__ __launch_bounds__(256) void tr8_pair_kernel(
 #pragma unroll
   for (int ob = 0; ob < 4; ++ob) acc[ob] = zero16();
 
-  auto stage_ptrs = [&](int buf, uint8_t*& l1, uint8_t*& l2, uint8_t*& l3, uint8_t*& s1, uint8_t*& s2,
-                        uint8_t*& s3) {
-    uint8_t* base = lds8 + buf * TR8_STAGE;
-    l1 = base; l2 = l1 + 64 * WROW; l3 = l2 + 64 * WROW;
-    s1 = l3 + 128 * W3ROW; s2 = s1 + 64 * 4; s3 = s2 + 64 * 4;
-  };
-  // stage hidden units 64hp .. 64hp+63: fc1/fc2 rows (64 x 128 B), fc3 column slices (128 x 64 B)
-  auto stage = [&](int hp, int buf) {
-    uint8_t *l1, *l2, *l3, *s1, *s2, *s3;
-    stage_ptrs(buf, l1, l2, l3, s1, s2, s3);
-    for (int c = tid; c < 64 * 8; c += 256) {
-      const long src = (long)(64 * hp + (c >> 3)) * 128 + (c & 7) * 16;
-      *reinterpret_cast<i32x4*>(l1 + (c >> 3) * WROW + (c & 7) * 16) = *reinterpret_cast<const i32x4*>(w1q + src);
-      *reinterpret_cast<i32x4*>(l2 + (c >> 3) * WROW + (c & 7) * 16) = *reinterpret_cast<const i32x4*>(w2q + src);
+  // DMA: wave w moves 1 KB pieces 2w and 2w+1 of each 8 KB matrix block, plus one piece
+  // of scales (w = 0: fc1, 1: fc2, 2 / 3: fc3 rows 0-63 / 64-127, one dword per row)
+  uint32_t o12[2], o3[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int R = 8 * (2 * wid + i) + (lane >> 3);
+    o12[i] = (uint32_t)(R * C + 16 * ((lane & 7) ^ tr8_swz8(R)));
+    const int R3 = 16 * (2 * wid + i) + (lane >> 2);
+    o3[i] = (uint32_t)(R3 * hidden + 16 * ((lane & 3) ^ tr8_swz4(R3)));
+  }
+  auto issue = [&](int hp, int buf) PF_INLINE {
+    uint8_t* st = tl + buf * TR8_STAGE;
+    const uint8_t* b1 = w1q + (long)64 * hp * C;
+    const uint8_t* b2 = w2q + (long)64 * hp * C;
+    const uint8_t* b3 = w3q + 64 * hp;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int piece = 1024 * (2 * wid + i);
+      __builtin_amdgcn_global_load_lds(b1 + o12[i], st + TR8_W1 + piece, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(b2 + o12[i], st + TR8_W2 + piece, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(b3 + o3[i], st + TR8_W3 + piece, 16, 0, 0);
     }
-    for (int c = tid; c < 128 * 4; c += 256)
-      *reinterpret_cast<i32x4*>(l3 + (c >> 2) * W3ROW + (c & 3) * 16) =
-          *reinterpret_cast<const i32x4*>(w3q + (long)(c >> 2) * hidden + 64 * hp + (c & 3) * 16);
-    if (tid < 64) {
-      *reinterpret_cast<int*>(s1 + 4 * tid) = *reinterpret_cast<const int*>(w1s + (long)(64 * hp + tid) * 4);
-      *reinterpret_cast<int*>(s2 + 4 * tid) = *reinterpret_cast<const int*>(w2s + (long)(64 * hp + tid) * 4);
-    }
-    if (tid < 128)
-      *reinterpret_cast<short*>(s3 + 2 * tid) =
-          *reinterpret_cast<const short*>(w3s + (long)tid * nblk + 2 * hp);
+    if (wid == 0) __builtin_amdgcn_global_load_lds(w1s + 256 * hp + 4 * lane, st + TR8_S1, 4, 0, 0);
+    else if (wid == 1) __builtin_amdgcn_global_load_lds(w2s + 256 * hp + 4 * lane, st + TR8_S2, 4, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds(w3s + (long)(64 * (wid - 2) + lane) * nblk + 4 * (hp >> 1),
+                                       st + TR8_S3 + 256 * (wid - 2), 4, 0, 0);
   };
+  const int sw8 = tr8_swz8(m), sw4 = tr8_swz4(m);   // rows 32x + m share the low 4 bits of m
 
   const int nhp = hidden / 64;
-  stage(0, 0);
-  __syncthreads();
+  issue(0, 0);
   for (int hp = 0; hp < nhp; ++hp) {
-    if (hp + 1 < nhp) stage(hp + 1, (hp + 1) & 1);
-    uint8_t *l1, *l2, *l3, *s1, *s2, *s3;
-    stage_ptrs(hp & 1, l1, l2, l3, s1, s2, s3);
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));   // block hp landed ...
+    __builtin_amdgcn_s_barrier();              // ... for every wave; the other stage is free
+    asm volatile("" ::: "memory");
+    if (hp + 1 < nhp) issue(hp + 1, (hp + 1) & 1);
+    const uint8_t* st = tl + (hp & 1) * TR8_STAGE;
     i32x4 hq[2];
     int hbyte[2];
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb) {
-      const int row = 32 * bb + m;   // hidden unit 64hp + row
+      const int row = 32 * bb + m;   // hidden unit 64 hp + row
       f32x16 a1 = zero16(), a2 = zero16();
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        a1 = mfma8(wfrag128(l1, row, s, h), xq.q[s], a1, s1[4 * row + 2 * s + h], xq.sc[s]);
-        a2 = mfma8(wfrag128(l2, row, s, h), xq.q[s], a2, s2[4 * row + 2 * s + h], xq.sc[s]);
+        const int c0 = ((4 * s + h) ^ sw8) * 16, c1 = ((4 * s + h + 2) ^ sw8) * 16;
+        const uint8_t* r1 = st + TR8_W1 + row * C;
+        const uint8_t* r2 = st + TR8_W2 + row * C;
+        const i32x8 f1 = cat_i32x4(*reinterpret_cast<const i32x4*>(r1 + c0), *reinterpret_cast<const i32x4*>(r1 + c1));
+        const i32x8 f2 = cat_i32x4(*reinterpret_cast<const i32x4*>(r2 + c0), *reinterpret_cast<const i32x4*>(r2 + c1));
+        a1 = mfma8(f1, xq.q[s], a1, st[TR8_S1 + 4 * row + 2 * s + h], xq.sc[s]);
+        a2 = mfma8(f2, xq.q[s], a2, st[TR8_S2 + 4 * row + 2 * s + h], xq.sc[s]);
       }
       float v[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) v[r] = siluf(a1[r]) * a2[r];
       hq[bb] = quantize16(v, hbyte[bb]);
+      __builtin_amdgcn_sched_barrier(0);   // keep the next half's fragment reads after this one (registers)
     }
     const i32x8 hop = cat_i32x4(hq[0], hq[1]);
     const int hsc = h ? hbyte[1] : hbyte[0];
+    const int sb = 2 * (hp & 1) + h;   // scale byte of K block h within the fc3 row dword
 #pragma unroll
     for (int ob = 0; ob < 4; ++ob) {
       const int orow = 32 * ob + m;
-      const uint8_t* p = l3 + orow * W3ROW + 16 * h;
-      const i32x8 wf = cat_i32x4(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(p + 32));
-      acc[ob] = mfma8(hop, wf, acc[ob], hsc, s3[2 * orow + h]);
+      const uint8_t* p = st + TR8_W3 + orow * 64;
+      const i32x8 wf = cat_i32x4(*reinterpret_cast<const i32x4*>(p + 16 * (h ^ sw4)),
+                                 *reinterpret_cast<const i32x4*>(p + 16 * ((h + 2) ^ sw4)));
+      acc[ob] = mfma8(wf, hop, acc[ob], st[TR8_S3 + 4 * orow + sb], hsc);   // rows = channel, cols = pair
     }
-    __syncthreads();
   }
-  // residuals first (all loads ahead of the stores, so they overlap); rows past the end
-  // are clamped on load and skipped on store
-  float res[4][16];
+  // lane (m, h) owns pair pos0 + m; acc[ob][4g + e] is channel 32 ob + 8 g + 4 h + e.  The
+  // residual (x_in may alias out) is loaded in 16-byte runs, all before the first store.
+  const long p = pos0 + m;
+  if (p < rows) {
+    float* dst = out + p * C;
+    f32x4 res[16];
 #pragma unroll
-  for (int ob = 0; ob < 4; ++ob)
+    for (int q = 0; q < 16; ++q)
+      res[q] = accumulate ? *reinterpret_cast<const f32x4*>(dst + oa_channel(q, h)) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      res[ob][r] = accumulate ? out[min(pos0 + acc_row(r, h), rows - 1) * C + 32 * ob + m] : 0.f;
+    for (int q = 0; q < 16; ++q) {
+      f32x4 v;
 #pragma unroll
-  for (int ob = 0; ob < 4; ++ob)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const long p = pos0 + acc_row(r, h);
-      if (p < rows) out[p * C + 32 * ob + m] = acc[ob][r] + res[ob][r];
+      for (int e = 0; e < 4; ++e) v[e] = acc[q >> 2][4 * (q & 3) + e] + res[q][e];
+      *reinterpret_cast<f32x4*>(dst + oa_channel(q, h)) = v;
     }
+  }
 }
 
 // Workspace layout of the fp8 triangle multiplication.
@@ -670,22 +689,16 @@ extern "C" int pf_trimul_mx8_contract(const void* A8, const void* B8, const void
 
 extern "C" int pf_transition_mx8_fwd(const pf_transition_mx8_args* a) {
   if (!a) return pf_fail(PF_E_INVALID, "pf_transition_mx8_fwd: null args");
-  if (a->C != C || a->hidden <= 0 || a->hidden % 64)
-    return pf_fail(PF_E_INVALID, "pf_transition_mx8_fwd: need C = 128 and hidden a multiple of 64 (got %d, %d)",
+  if (a->C != C || a->hidden <= 0 || a->hidden % 128)
+    return pf_fail(PF_E_INVALID, "pf_transition_mx8_fwd: need C = 128 and hidden a multiple of 128 (got %d, %d)",
                    a->C, a->hidden);
   if (a->rows <= 0) return pf_fail(PF_E_INVALID, "pf_transition_mx8_fwd: rows must be positive");
   if (!a->x_in || !a->out || !a->norm_w || !a->norm_b || !a->fc1_q || !a->fc1_s || !a->fc2_q || !a->fc2_s ||
       !a->fc3_q || !a->fc3_s)
     return pf_fail(PF_E_INVALID, "pf_transition_mx8_fwd: null pointer argument");
-  static bool attr = false;
-  if (!attr) {
-    const int rc = set_lds((const void*)tr8_pair_kernel, TR8_LDS, "tr8_pair_kernel");
-    if (rc != PF_OK) return rc;
-    attr = true;
-  }
   const long waves = (a->rows + 31) / 32;
   const int grid = (int)((waves + 3) / 4);
-  tr8_pair_kernel<<<grid, 256, TR8_LDS, (hipStream_t)a->stream>>>(
+  tr8_pair_kernel<<<grid, 256, 0, (hipStream_t)a->stream>>>(
       a->x_in, a->out, a->norm_w, a->norm_b, (const uint8_t*)a->fc1_q, (const uint8_t*)a->fc1_s,
       (const uint8_t*)a->fc2_q, (const uint8_t*)a->fc2_s, (const uint8_t*)a->fc3_q, (const uint8_t*)a->fc3_s,
       a->rows, a->hidden, a->accumulate, a->eps);
