@@ -201,6 +201,15 @@ int pf_apb_fwd(const pf_apb_args* args);
 int pf_apb_pair_bias(const pf_apb_args* args);
 int pf_apb_attend(const pf_apb_args* args);
 
+/* The pair transition (pf_transition_fwd, C = 128 only) with pf_apb_pair_bias of its
+ * result fused into the same kernel: after writing out = [x_in +] Transition(x_in) for a
+ * pair, the kernel also writes that pair's single-track bias log2(e)*proj_z(LN(out)) into
+ * apb's workspace, as pf_apb_pair_bias(apb) on `out` would (tt_bio/boltz2.py:353-356), so
+ * the layer's last pair operation and the single track's only z read are one pass.
+ * apb: shape, zln_w, zln_b, w_z, eps, workspace (the other fields are not read; apb->z is
+ * ignored: the bias is computed from t->out).  t->rows must equal apb->B * apb->N^2. */
+int pf_transition_pair_bias_fwd(const pf_transition_args* t, const pf_apb_args* apb);
+
 /* ------------------------------------------------------------------------------
  * Fast mode (block fp8).  Replaces the --fast path of the ttnn TriangleMultiplication
  * and Transition (tt_bio/tenstorrent.py:60-61, 178-181, 389-407, 431-503, 879-906),

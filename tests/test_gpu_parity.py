@@ -6,6 +6,8 @@ errors normalised by the RMS of the reference output:
 Masked configurations report the valid region and the full tensor separately;
 both must meet the bar.
 """
+import math
+
 import pytest
 import torch
 
@@ -294,3 +296,32 @@ def test_single_track_overlap_identical(gpu):
     s_ref, z_ref = ref.pairformer_stack(s, z, mask, pm, w, n_blocks)
     check("overlapped 3-layer stack z", out[True][1], z_ref)
     check("overlapped 3-layer stack s", out[True][0], s_ref)
+
+
+def test_transition_fused_pair_bias(gpu):
+    """pf_transition_pair_bias_fwd: z is bit-identical to pf_transition_fwd, and the pair
+    bias it writes matches pf_apb_pair_bias on that z (same formula, different summation
+    order and LayerNorm lane layout) and the fp32 oracle's proj_z."""
+    N, c_s, H = 96, 384, 16
+    w_tr = _sub_w(41, "transition_z")
+    w_apb = _sub_w(42, "attention")
+    s, z, mask, _ = _inputs(N, 43)
+    tr = pairformer.Transition(w_tr)
+    apb = pairformer.AttentionPairBias(24, H, w_apb)
+    z1, z2 = z.to(gpu).contiguous(), z.to(gpu).contiguous()
+    s_d = s.to(gpu).contiguous()
+    nb = apb.workspace_bytes(1, N)
+    ws1, ws2 = ops.workspace(nb, gpu), ops.workspace(nb, gpu)
+    tr(z1, out=z1, accumulate=True)
+    apb(s_d, z1, None, out=s_d.clone(), ws=ws1, part="bias")
+    tr(z2, out=z2, accumulate=True, pair_bias=(apb, s_d, ws2))
+    torch.cuda.synchronize()
+    assert torch.equal(z1, z2)
+    off = 5 * N * c_s * 4
+    b1 = ws1[off: off + H * N * N * 4].view(torch.float32).view(H, N, N)
+    b2 = ws2[off: off + H * N * N * 4].view(torch.float32).view(H, N, N)
+    check("fused pair bias vs pf_apb_pair_bias", b2, b1, 1e-2, 1e-3)
+    zn = torch.nn.functional.layer_norm(z2.cpu().double()[0], (128,), w_apb["proj_z.0.weight"].double(),
+                                        w_apb["proj_z.0.bias"].double(), 1e-5)
+    want = torch.einsum("ijc,hc->hij", zn, w_apb["proj_z.1.weight"].double()) * math.log2(math.e)
+    check("fused pair bias vs fp64 proj_z", b2, want)

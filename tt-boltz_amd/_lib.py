@@ -105,6 +105,7 @@ SIGNATURES = {
     "pf_apb_fwd": (c_int, [ctypes.POINTER(ApbArgs)]),
     "pf_apb_pair_bias": (c_int, [ctypes.POINTER(ApbArgs)]),
     "pf_apb_attend": (c_int, [ctypes.POINTER(ApbArgs)]),
+    "pf_transition_pair_bias_fwd": (c_int, [ctypes.POINTER(TransitionArgs), ctypes.POINTER(ApbArgs)]),
     "pf_layernorm_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_float, c_void_p]),
     "pf_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_int, c_void_p]),
     "pf_pair_ln_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long,

@@ -32,3 +32,9 @@ struct pf_lin_job {
   float* out;
 };
 int pf_linear_batch(const pf_lin_job* jobs, int njobs, long rows, int K, int Nout, hipStream_t st);
+
+// Single-track attention workspace helpers (single.hip): argument checks shared by the
+// entry points (bias_only: only what the pair bias reads), and the address of the pair
+// bias [B][H][N][N] inside the workspace.
+int pf_apb_check(const pf_apb_args* a, const char* fn, bool bias_only);
+float* pf_apb_bias_ptr(const pf_apb_args* a);

@@ -198,8 +198,8 @@ extern "C" size_t pf_apb_workspace_size(int B, int N, int c_s, int H) {
   return (5 * rows * c_s + (size_t)B * H * N * N) * sizeof(float);
 }
 
-// Shape / pointer / workspace checks shared by the three entry points.
-static int apb_check(const pf_apb_args* a, const char* fn, bool bias_only) {
+// Shape / pointer / workspace checks shared by the entry points.
+int pf_apb_check(const pf_apb_args* a, const char* fn, bool bias_only) {
   if (!a) return pf_fail(PF_E_INVALID, "%s: null args", fn);
   if (a->B <= 0 || a->N <= 0 || a->C != C || a->H <= 0 || a->H > 32 || a->c_s % a->H ||
       (a->c_s / a->H != 24 && a->c_s / a->H != 32) || a->c_s % 32 || a->N > 4096 || (a->N % 32))
@@ -219,22 +219,22 @@ static int apb_check(const pf_apb_args* a, const char* fn, bool bias_only) {
 }
 
 // Workspace: q, k, v, g, o*sigmoid(g) [rows][c_s] fp32 each, then the pair bias [B][H][N][N].
-static float* apb_bias_buf(const pf_apb_args* a) {
+float* pf_apb_bias_ptr(const pf_apb_args* a) {
   return (float*)a->workspace + 5 * (size_t)a->B * a->N * a->c_s;
 }
 
 extern "C" int pf_apb_pair_bias(const pf_apb_args* a) {
-  int rc = apb_check(a, "pf_apb_pair_bias", true);
+  int rc = pf_apb_check(a, "pf_apb_pair_bias", true);
   if (rc) return rc;
   const long pairs = (long)a->B * a->N * a->N;
   apb_zbias_kernel<<<(unsigned)((pairs / 32 + 3) / 4), 256, 0, (hipStream_t)a->stream>>>(
-      a->z, a->zln_w, a->zln_b, (const op_t*)a->w_z, apb_bias_buf(a), a->B, a->N, a->H, a->eps);
+      a->z, a->zln_w, a->zln_b, (const op_t*)a->w_z, pf_apb_bias_ptr(a), a->B, a->N, a->H, a->eps);
   PF_CHECK_LAUNCH("apb_zbias_kernel");
   return PF_OK;
 }
 
 extern "C" int pf_apb_attend(const pf_apb_args* a) {
-  int rc = apb_check(a, "pf_apb_attend", false);
+  int rc = pf_apb_check(a, "pf_apb_attend", false);
   if (rc) return rc;
   const int n_valid = a->n_valid ? a->n_valid : a->N;
   hipStream_t st = (hipStream_t)a->stream;
@@ -245,7 +245,7 @@ extern "C" int pf_apb_attend(const pf_apb_args* a) {
   float* v = k + rows * cs;
   float* g = v + rows * cs;
   float* og = g + rows * cs;
-  float* bias = apb_bias_buf(a);
+  float* bias = pf_apb_bias_ptr(a);
   // q/k/v/g share (rows, c_s, c_s): one launch
   const pf_lin_job proj[4] = {{a->s, a->w_q, nullptr, a->b_q, nullptr, q},
                               {a->k_in, a->w_k, nullptr, nullptr, nullptr, k},
@@ -264,7 +264,7 @@ extern "C" int pf_apb_attend(const pf_apb_args* a) {
 }
 
 extern "C" int pf_apb_fwd(const pf_apb_args* a) {
-  int rc = apb_check(a, "pf_apb_fwd", false);
+  int rc = pf_apb_check(a, "pf_apb_fwd", false);
   if (rc) return rc;
   if ((rc = pf_apb_pair_bias(a))) return rc;
   return pf_apb_attend(a);

@@ -38,10 +38,19 @@ constexpr int TR_BLK = 8192;                 // bytes of one fp16 weight block
 constexpr int TR_STAGE = 3 * TR_BLK;
 PF_DEV int tr_swz4(int r) { return (r >> 2) & 3; }
 
+// Optional epilogue (ZBIAS): the single-track pair bias of the updated pair row,
+// bias[b][hd][i][j] = log2(e) * LN_zb(out[b,i,j,:]) . W_z[hd], from the values the lane
+// has just written (no second pass over z).
+struct ZBiasArgs {
+  const float* lnw; const float* lnb; const op_t* wz; float* bias;
+  long NN; int H; float eps;
+};
+
+template <bool ZBIAS>
 __global__ __launch_bounds__(64 * TRW, 3) void tr_pair_kernel(
     const float* x_in, float* out, const float* __restrict__ lnw, const float* __restrict__ lnb,
     const op_t* __restrict__ w1, const op_t* __restrict__ w2, const op_t* __restrict__ w3,
-    long rows, int hidden, int accumulate, float eps) {
+    long rows, int hidden, int accumulate, float eps, ZBiasArgs zb) {
   __shared__ __attribute__((aligned(16))) char tl[2 * TR_STAGE];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -110,19 +119,82 @@ __global__ __launch_bounds__(64 * TRW, 3) void tr_pair_kernel(
   // lane (m, h) owns pair pos0 + m; acc[ob][4g + e] is channel 32 ob + 8 g + 4 h + e.  The
   // residual (x_in may alias out) is loaded in 16-byte runs, all before the first store.
   const long p = pos0 + m;
-  if (p < rows) {
-    float* dst = out + p * C;
-    f32x4 res[16];
+  if (!ZBIAS) {
+    if (p < rows) {
+      float* dst = out + p * C;
+      f32x4 res[16];
 #pragma unroll
-    for (int q = 0; q < 16; ++q)
-      res[q] = accumulate ? *reinterpret_cast<const f32x4*>(dst + oa_channel(q, h)) : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int q = 0; q < 16; ++q)
+        res[q] = accumulate ? *reinterpret_cast<const f32x4*>(dst + oa_channel(q, h)) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      f32x4 v;
+      for (int q = 0; q < 16; ++q) {
+        f32x4 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = acc[q >> 2][4 * (q & 3) + e] + res[q][e];
-      *reinterpret_cast<f32x4*>(dst + oa_channel(q, h)) = v;
+        for (int e = 0; e < 4; ++e) v[e] = acc[q >> 2][4 * (q & 3) + e] + res[q][e];
+        *reinterpret_cast<f32x4*>(dst + oa_channel(q, h)) = v;
+      }
     }
+    return;
+  }
+  // ZBIAS: whole tiles only (rows is a multiple of 32, checked on the host)
+  float* dst = out + p * C;
+  __builtin_amdgcn_sched_barrier(0);
+  float zv[64];   // residual, then the updated row, in output-aligned order (in place)
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const f32x4 r = accumulate ? *reinterpret_cast<const f32x4*>(dst + oa_channel(q, h)) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) zv[4 * q + e] = r[e];
+  }
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      zv[4 * q + e] += acc[q >> 2][4 * (q & 3) + e];
+      v[e] = zv[4 * q + e];
+    }
+    *reinterpret_cast<f32x4*>(dst + oa_channel(q, h)) = v;
+  }
+  opx8 zf[8];
+  {
+    float sm = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) sm += zv[i];
+    const float mean = xor32_sum(sm) * (1.f / 128.f);
+    float var = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) { const float d = zv[i] - mean; var += d * d; }
+    const float rstd = rsqrtf(xor32_sum(var) * (1.f / 128.f) + zb.eps);
+    // the affine parameters are read 8 channels at a time (the scheduling barrier keeps
+    // their loads from being hoisted together, which would need 128 more registers)
+#pragma unroll
+    for (int q2 = 0; q2 < 8; ++q2) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int q = 2 * q2 + u, c0 = oa_channel(q, h);
+        const f32x4 g4 = *reinterpret_cast<const f32x4*>(zb.lnw + c0);
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(zb.lnb + c0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) zf[q2][4 * u + e] = (op_t)((zv[4 * q + e] - mean) * rstd * g4[e] + b4[e]);
+      }
+    }
+  }
+  // D[head][pair]: weight row m from global memory (4 KB, cache-resident); lanes m >= H
+  // repeat row H - 1 and their output rows (heads >= H) are not stored
+  __builtin_amdgcn_sched_barrier(0);
+  f32x16 hb = zero16();
+  const op_t* wrow = zb.wz + min(m, zb.H - 1) * C;
+#pragma unroll
+  for (int s2 = 0; s2 < 8; ++s2) hb = mfma32(wfrag_oa(wrow, s2, h), zf[s2], hb);
+  // lane (pair m, h) holds heads acc_row(r, h); the tile's 32 pairs are consecutive (i, j)
+  const long b = pos0 / zb.NN;
+  float* brow = zb.bias + b * zb.H * zb.NN + (pos0 - b * zb.NN) + m;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int hd = acc_row(r, h);
+    if (hd < zb.H) brow[hd * zb.NN] = hb[r] * 1.4426950408889634f;
   }
 }
 
@@ -319,9 +391,9 @@ extern "C" int pf_transition_fwd(const pf_transition_args* a) {
   hipStream_t st = (hipStream_t)a->stream;
   if (a->C == C) {
     const unsigned grid = (unsigned)((a->rows + 32 * TRW - 1) / (32 * TRW));
-    tr_pair_kernel<<<grid, 64 * TRW, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w,
-                                              (const op_t*)a->fc2_w, (const op_t*)a->fc3_w, a->rows, a->hidden,
-                                              a->accumulate, a->eps);
+    tr_pair_kernel<false><<<grid, 64 * TRW, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w,
+                                                     (const op_t*)a->fc2_w, (const op_t*)a->fc3_w, a->rows,
+                                                     a->hidden, a->accumulate, a->eps, ZBiasArgs{});
     PF_CHECK_LAUNCH("tr_pair_kernel");
     return PF_OK;
   }
@@ -345,5 +417,28 @@ extern "C" int pf_pair_ln_linear_fwd(const float* x, const float* base, const fl
   pair_ln_linear_kernel<<<(unsigned)((rows + 127) / 128), 256, 0, (hipStream_t)stream>>>(
       x, base, ln_w, ln_b, (const op_t*)W, out, rows, eps);
   PF_CHECK_LAUNCH("pair_ln_linear_kernel");
+  return PF_OK;
+}
+
+extern "C" int pf_transition_pair_bias_fwd(const pf_transition_args* a, const pf_apb_args* apb) {
+  if (!a || !apb) return pf_fail(PF_E_INVALID, "pf_transition_pair_bias_fwd: null args");
+  if (a->C != C || a->hidden <= 0 || a->hidden % 32)
+    return pf_fail(PF_E_INVALID, "pf_transition_pair_bias_fwd: need C = 128 and hidden a multiple of 32 (C=%d hidden=%d)",
+                   a->C, a->hidden);
+  if (!a->x_in || !a->out || !a->norm_w || !a->norm_b || !a->fc1_w || !a->fc2_w || !a->fc3_w)
+    return pf_fail(PF_E_INVALID, "pf_transition_pair_bias_fwd: null pointer argument");
+  pf_apb_args chk = *apb;
+  chk.z = a->out;   // the bias is computed from the transition's output
+  int rc = pf_apb_check(&chk, "pf_transition_pair_bias_fwd", true);
+  if (rc) return rc;
+  const long NN = (long)apb->N * apb->N;
+  if (a->rows != (long)apb->B * NN)
+    return pf_fail(PF_E_INVALID, "pf_transition_pair_bias_fwd: rows %ld != B*N*N = %ld", a->rows, (long)apb->B * NN);
+  const ZBiasArgs zb{apb->zln_w, apb->zln_b, (const op_t*)apb->w_z, pf_apb_bias_ptr(apb), NN, apb->H, apb->eps};
+  const unsigned grid = (unsigned)(a->rows / (32 * TRW));   // N % 32 == 0: whole workgroups
+  tr_pair_kernel<true><<<grid, 64 * TRW, 0, (hipStream_t)a->stream>>>(
+      a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w, (const op_t*)a->fc2_w, (const op_t*)a->fc3_w,
+      a->rows, a->hidden, a->accumulate, a->eps, zb);
+  PF_CHECK_LAUNCH("tr_pair_kernel");
   return PF_OK;
 }

@@ -146,7 +146,9 @@ def transition_workspace_bytes(rows: int, C: int, hidden: int, variant: str = DE
 
 def launch_transition(x_in: torch.Tensor, out: torch.Tensor, w: Mapping[str, torch.Tensor],
                       ws: Optional[torch.Tensor], accumulate: bool, eps: float = 1e-5,
-                      variant: str = DEFAULT_VARIANT) -> None:
+                      variant: str = DEFAULT_VARIANT, pair_bias: Optional[tuple] = None) -> None:
+    """``pair_bias = (s, w_apb, n_heads, apb_ws, eps_apb)``: also write the single-track pair
+    bias of ``out`` into ``apb_ws`` in the same kernel (pf_transition_pair_bias_fwd; c_z = 128)."""
     C = x_in.shape[-1]
     rows = x_in.numel() // C
     a = _lib.TransitionArgs(
@@ -154,7 +156,13 @@ def launch_transition(x_in: torch.Tensor, out: torch.Tensor, w: Mapping[str, tor
         x_in=_ptr(x_in), out=_ptr(out), norm_w=_ptr(w["norm.weight"]), norm_b=_ptr(w["norm.bias"]),
         fc1_w=_ptr(w["fc1.weight"]), fc2_w=_ptr(w["fc2.weight"]), fc3_w=_ptr(w["fc3.weight"]),
         workspace=_ptr(ws), workspace_bytes=0 if ws is None else ws.numel(), stream=_stream())
-    _lib.check(_lib.load(variant).pf_transition_fwd(ctypes.byref(a)), "pf_transition_fwd", variant)
+    if pair_bias is None:
+        _lib.check(_lib.load(variant).pf_transition_fwd(ctypes.byref(a)), "pf_transition_fwd", variant)
+        return
+    s, w_apb, n_heads, apb_ws, eps_apb = pair_bias
+    b = _apb_args(s, s, out, None, s, w_apb, n_heads, apb_ws, False, eps_apb, 0)
+    _lib.check(_lib.load(variant).pf_transition_pair_bias_fwd(ctypes.byref(a), ctypes.byref(b)),
+               "pf_transition_pair_bias_fwd", variant)
 
 
 def apb_workspace_bytes(B: int, N: int, c_s: int, H: int, variant: str = DEFAULT_VARIANT) -> int:

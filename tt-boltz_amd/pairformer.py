@@ -220,18 +220,31 @@ class Transition(Module):
             return 0
         return ops.transition_workspace_bytes(rows, self.C, self.hidden, self.variant)
 
+    def fuses_pair_bias(self) -> bool:
+        """Whether ``__call__`` can also produce the single-track pair bias of its output."""
+        return not self.fast and self.C == C_Z
+
     def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, accumulate: bool = False,
-                 ws: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 ws: Optional[torch.Tensor] = None, pair_bias: Optional[tuple] = None) -> torch.Tensor:
+        """``pair_bias = (attention_pair_bias, s, apb_ws)`` (only if ``fuses_pair_bias()``): the
+        same kernel also writes the attention's pair bias of the updated ``out`` into
+        ``apb_ws``, as ``attention_pair_bias(s, out, ..., part="bias")`` would."""
         rows = x.numel() // self.C
         if out is None:
             out = torch.empty_like(x)
         if self.fast:
+            if pair_bias is not None:
+                raise ValueError("Transition: the fp8 transition does not fuse the pair bias")
             ops.launch_transition_mx8(x, out, self.w, accumulate, self.options.eps, self.variant)
             return out
         if ws is None:
             nb = self.workspace_bytes(rows)
             ws = ops.workspace(nb, x.device) if nb else None
-        ops.launch_transition(x, out, self.w, ws, accumulate, self.options.eps, self.variant)
+        pb = None
+        if pair_bias is not None:
+            apb, s, apb_ws = pair_bias
+            pb = (s, apb.w, apb.n_heads, apb_ws, apb.options.eps)
+        ops.launch_transition(x, out, self.w, ws, accumulate, self.options.eps, self.variant, pb)
         return out
 
 
@@ -346,37 +359,46 @@ class PairformerLayer(Module):
         self.triangle_multiplication_end(z, pair_mask, out=z, accumulate=True, ws=ws)
         self.triangle_attention_start(z, pair_mask, out=z, accumulate=True, ws=ws, n_valid=n_valid)
         self.triangle_attention_end(z, pair_mask, out=z, accumulate=True, ws=ws, n_valid=n_valid)
-        self.transition_z(z, out=z, accumulate=True, ws=ws)
-        if self.transform_s and s is not None:
-            c_s = s.shape[-1]
-            sws = ws if single is None else single.ws
-            s_norm = sws[: B * N * c_s * 4].view(torch.float32).view(B, N, c_s)
-            apb_ws = sws[B * N * c_s * 4:]
-            if single is None:
-                ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps,
-                                     self.variant)
-                self.attention_pair_bias(s_norm, z, mask, k_in=s_norm, out=s, accumulate=True, ws=apb_ws,
-                                         n_valid=n_valid)
-                self.transition_s(s, out=s, accumulate=True, ws=sws)
-                return s, z
+        if not (self.transform_s and s is not None):
+            self.transition_z(z, out=z, accumulate=True, ws=ws)
+            return s, z
+        c_s = s.shape[-1]
+        sws = ws if single is None else single.ws
+        s_norm = sws[: B * N * c_s * 4].view(torch.float32).view(B, N, c_s)
+        apb_ws = sws[B * N * c_s * 4:]
+        if single is not None:
             # the previous single track must be done with the workspace (and s) first
             single.wait_previous()
+        # the single track reads z only through the pair bias of the final z: with the 16-bit
+        # pair transition it comes out of the same kernel
+        if self.transition_z.fuses_pair_bias():
+            self.transition_z(z, out=z, accumulate=True, ws=ws,
+                              pair_bias=(self.attention_pair_bias, s, apb_ws))
+        else:
+            self.transition_z(z, out=z, accumulate=True, ws=ws)
             self.attention_pair_bias(s, z, mask, out=s, ws=apb_ws, n_valid=n_valid, part="bias")
-            ready = torch.cuda.Event()
-            ready.record(torch.cuda.current_stream())
-            with torch.cuda.stream(single.stream):
-                single.stream.wait_event(ready)
-                ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps,
-                                     self.variant)
-                self.attention_pair_bias(s_norm, z, mask, k_in=s_norm, out=s, accumulate=True, ws=apb_ws,
-                                         n_valid=n_valid, part="attend")
-                self.transition_s(s, out=s, accumulate=True, ws=sws)
-                done = torch.cuda.Event()
-                done.record(single.stream)
-            for t in (s, mask, sws):
-                if t is not None:
-                    t.record_stream(single.stream)
-            single.done = done
+        if single is None:
+            ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps,
+                                 self.variant)
+            self.attention_pair_bias(s_norm, z, mask, k_in=s_norm, out=s, accumulate=True, ws=apb_ws,
+                                     n_valid=n_valid, part="attend")
+            self.transition_s(s, out=s, accumulate=True, ws=sws)
+            return s, z
+        ready = torch.cuda.Event()
+        ready.record(torch.cuda.current_stream())
+        with torch.cuda.stream(single.stream):
+            single.stream.wait_event(ready)
+            ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps,
+                                 self.variant)
+            self.attention_pair_bias(s_norm, z, mask, k_in=s_norm, out=s, accumulate=True, ws=apb_ws,
+                                     n_valid=n_valid, part="attend")
+            self.transition_s(s, out=s, accumulate=True, ws=sws)
+            done = torch.cuda.Event()
+            done.record(single.stream)
+        for t in (s, mask, sws):
+            if t is not None:
+                t.record_stream(single.stream)
+        single.done = done
         return s, z
 
 
