@@ -325,3 +325,23 @@ def test_transition_fused_pair_bias(gpu):
                                         w_apb["proj_z.0.bias"].double(), 1e-5)
     want = torch.einsum("ijc,hc->hij", zn, w_apb["proj_z.1.weight"].double()) * math.log2(math.e)
     check("fused pair bias vs fp64 proj_z", b2, want)
+
+
+def test_layer_batch2_matches_single(gpu):
+    """B = 2 through the whole layer (every kernel's batch indexing: trimul planes,
+    attention rows/bias, transitions, the single track) equals the two proteins run one at
+    a time, bit for bit, and the fp32 oracle on the batch."""
+    N = 64
+    w = synthetic.stack_weights(1, 51)
+    s0, z0, m0, pm0 = _inputs(N, 52)
+    s1, z1, m1, pm1 = _inputs(N, 53, pad_tail=9)
+    S, Z, M, PM = (torch.cat(t, 0) for t in ((s0, s1), (z0, z1), (m0, m1), (pm0, pm1)))
+    pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, w)
+    s_b, z_b = pf(S.to(gpu).contiguous(), Z.to(gpu).contiguous(), PM.to(gpu).contiguous(), M.to(gpu).contiguous())
+    for i, (s, z, m, pm) in enumerate(((s0, z0, m0, pm0), (s1, z1, m1, pm1))):
+        s_1, z_1 = pf(s.to(gpu).contiguous(), z.to(gpu).contiguous(), pm.to(gpu).contiguous(),
+                      m.to(gpu).contiguous())
+        assert torch.equal(s_b[i:i + 1], s_1) and torch.equal(z_b[i:i + 1], z_1), f"batch element {i} differs"
+    s_ref, z_ref = ref.pairformer_stack(S, Z, M, PM, w, 1)
+    check("batch-2 layer z", z_b, z_ref)
+    check("batch-2 layer s", s_b, s_ref)
