@@ -313,11 +313,24 @@ def main() -> int:
     achieved = contract_flop / (contract_ms * 1e-3) / 1e12
     kname = "tm_contract_dma_kernel" if N >= 384 else "tm_contract_kernel"
     traffic = load_traffic()
-    roofline = {"kernel": kname, "bound": "mfma", "achieved": round(achieved, 1),
-                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-                "traffic": traffic["hbm_bytes_per_launch"] if traffic and traffic.get("N") == N else None,
-                "launch_ms": round(contract_ms, 4), "flop_per_launch": contract_flop}
+    # The binding roof: algorithmic bytes (a and b planes read once, x written once, 16-bit)
+    # over the published HBM peak vs FLOP over the MFMA peak.  Below the ridge point
+    # (2.5 PF / 8 TB/s = 312 FLOP/B) HBM binds: at N = 512 the intensity is 171 FLOP/B.
+    alg_bytes = 3 * 128 * N * N * 2
+    t_hbm = alg_bytes / (HBM_PEAK_GBS * 1e9)
+    t_mfma = contract_flop / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+    mfma_part = {"achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                 "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4)}
+    gbs = alg_bytes / (contract_ms * 1e-3) / 1e9
+    if t_hbm >= t_mfma:
+        roofline = {"kernel": kname, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    else:
+        roofline = {"kernel": kname, "bound": "mfma", **mfma_part}
+    roofline.update({"traffic": traffic["hbm_bytes_per_launch"] if traffic and traffic.get("N") == N else None,
+                     "algorithmic_bytes": alg_bytes, "flop_per_launch": contract_flop,
+                     "intensity_flop_per_byte": round(contract_flop / alg_bytes, 1),
+                     "launch_ms": round(contract_ms, 4), "mfma": mfma_part})
     if traffic and traffic.get("N") == N:
         roofline["traffic_note"] = traffic.get("note")
 
