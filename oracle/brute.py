@@ -311,3 +311,65 @@ def transition_mx8(x, W):
         hh = [h1[t] * _sig(h1[t]) * h2[t] for t in range(len(h1))]
         out[idx] = _matvec_mx8(Wq["fc3.weight"], hh)
     return out
+
+
+# ----------------------------------------------------------------------------- MSA module
+def outer_product_mean(m, msa_mask, W):
+    """z[b,i,j,o] = sum_k Wo[o][k] f[k] + bo[o], f[c*H + d] = sum_s a[s,i,c] b[s,j,d] / n_ij,
+    n_ij = max(1, sum_s mask[s,i] mask[s,j]); a, b = proj(LN(m[s,i])) * mask[s,i]."""
+    m, msk = _np(m), _np(msa_mask)
+    W = {k: _np(v) for k, v in W.items()}
+    B, S, N, _ = m.shape
+    Hh = W["proj_a.weight"].shape[0]
+    a = np.zeros((B, S, N, Hh))
+    b = np.zeros((B, S, N, Hh))
+    for bb in range(B):
+        for s in range(S):
+            for i in range(N):
+                xn = _ln_vec(list(m[bb, s, i]), W["norm.weight"], W["norm.bias"])
+                a[bb, s, i] = np.array(_matvec(W["proj_a.weight"], xn)) * msk[bb, s, i]
+                b[bb, s, i] = np.array(_matvec(W["proj_b.weight"], xn)) * msk[bb, s, i]
+    out = np.zeros((B, N, N, W["proj_o.weight"].shape[0]))
+    for bb in range(B):
+        for i in range(N):
+            for j in range(N):
+                n = max(1.0, sum(msk[bb, s, i] * msk[bb, s, j] for s in range(S)))
+                f = [sum(a[bb, s, i, c] * b[bb, s, j, d] for s in range(S)) / n
+                     for c in range(Hh) for d in range(Hh)]
+                out[bb, i, j] = np.array(_matvec(W["proj_o.weight"], f)) + W["proj_o.bias"]
+    return out
+
+
+def pair_weighted_averaging(m, z, pair_mask, W, num_heads, c_h, inf=1e6):
+    """o[s,i,h*c_h+d] = sigmoid(g[s,i,h,d]) * sum_j w[h,i,j] v[s,j,h,d], w = softmax over j
+    of (LN(z[i,j]) . Wz[h]) - inf*(1 - mask[i,j]); out = proj_o(o)."""
+    m, z, pm = _np(m), _np(z), _np(pair_mask)
+    W = {k: _np(v) for k, v in W.items()}
+    B, S, N, _ = m.shape
+    out = np.zeros((B, S, N, W["proj_o.weight"].shape[0]))
+    for bb in range(B):
+        mn = {(s, i): _ln_vec(list(m[bb, s, i]), W["norm_m.weight"], W["norm_m.bias"])
+              for s in range(S) for i in range(N)}
+        v = {k: _matvec(W["proj_m.weight"], x) for k, x in mn.items()}
+        g = {k: [_sig(t) for t in _matvec(W["proj_g.weight"], x)] for k, x in mn.items()}
+        logit = {}
+        for i in range(N):
+            for j in range(N):
+                zn = _ln_vec(list(z[bb, i, j]), W["norm_z.weight"], W["norm_z.bias"])
+                lg = _matvec(W["proj_z.weight"], zn)
+                for h in range(num_heads):
+                    logit[h, i, j] = lg[h] - inf * (1.0 - pm[bb, i, j])
+        wts = {}
+        for h in range(num_heads):
+            for i in range(N):
+                mx = max(logit[h, i, j] for j in range(N))
+                e = [math.exp(logit[h, i, j] - mx) for j in range(N)]
+                den = sum(e)
+                for j in range(N):
+                    wts[h, i, j] = e[j] / den
+        for s in range(S):
+            for i in range(N):
+                o = [g[s, i][h * c_h + d] * sum(wts[h, i, j] * v[s, j][h * c_h + d] for j in range(N))
+                     for h in range(num_heads) for d in range(c_h)]
+                out[bb, s, i] = _matvec(W["proj_o.weight"], o)
+    return out

@@ -368,3 +368,88 @@ def test_mx8_partial_block_equals_zero_padding():
     # and the scalar quantizer of brute.py agrees on the partial block
     want = torch.tensor([brute.mx8_vec([float(v) for v in row]) for row in x], dtype=torch.float64)
     assert torch.allclose(fp8_emu.fake_quant_mx8(x).double(), want, rtol=0, atol=0)
+
+
+# ----------------------------------------------------------------------------- MSA module
+from oracle import msa_ref  # noqa: E402
+
+
+def _opm_w(c_m, hh, c_z, seed):
+    return _w({"norm.weight": (c_m,), "norm.bias": (c_m,), "proj_a.weight": (hh, c_m),
+               "proj_b.weight": (hh, c_m), "proj_o.weight": (c_z, hh * hh), "proj_o.bias": (c_z,)}, seed)
+
+
+def _pwa_w(c_m, c_z, H, ch, seed):
+    return _w({"norm_m.weight": (c_m,), "norm_m.bias": (c_m,), "norm_z.weight": (c_z,), "norm_z.bias": (c_z,),
+               "proj_m.weight": (H * ch, c_m), "proj_g.weight": (H * ch, c_m), "proj_z.weight": (H, c_z),
+               "proj_o.weight": (c_m, H * ch)}, seed)
+
+
+def test_opm_matches_brute():
+    """Outer product mean: pairwise mask counts (with a fully masked sequence and a token
+    masked in some sequences), channel order c*H + d, bias."""
+    B, S, N, c_m, hh, c_z = 1, 4, 5, 8, 3, 6
+    g = torch.Generator().manual_seed(61)
+    m = torch.randn((B, S, N, c_m), generator=g)
+    mask = (torch.rand((B, S, N), generator=g) > 0.3).float()
+    mask[:, 1] = 0.0
+    w = _opm_w(c_m, hh, c_z, 62)
+    _close(msa_ref.outer_product_mean(m, mask, w), brute.outer_product_mean(m, mask, w))
+
+
+def test_opm_single_sequence_closed_form():
+    """S = 1, all ones: z[i,j] = Wo vec(a_i outer b_j) + bo (mean over one sequence)."""
+    c_m, hh, c_z, N = 8, 4, 5, 3
+    g = torch.Generator().manual_seed(63)
+    m = torch.randn((1, 1, N, c_m), generator=g)
+    w = _opm_w(c_m, hh, c_z, 64)
+    mn = F.layer_norm(m, (c_m,), w["norm.weight"], w["norm.bias"])
+    a, b = mn @ w["proj_a.weight"].T, mn @ w["proj_b.weight"].T
+    want = torch.einsum("ic,jd->ijcd", a[0, 0], b[0, 0]).reshape(N, N, -1) @ w["proj_o.weight"].T + w["proj_o.bias"]
+    _close(msa_ref.outer_product_mean(m, torch.ones((1, 1, N)), w)[0], want)
+
+
+def test_pwa_matches_brute():
+    """Pair weighted averaging: softmax over j (not s), per-head slices, masked pairs."""
+    B, S, N, c_m, c_z, H, ch = 1, 3, 5, 8, 6, 2, 3
+    g = torch.Generator().manual_seed(65)
+    m = torch.randn((B, S, N, c_m), generator=g)
+    z = torch.randn((B, N, N, c_z), generator=g)
+    tok = torch.ones((B, N)); tok[:, -1] = 0
+    pm = tok[:, :, None] * tok[:, None, :]
+    w = _pwa_w(c_m, c_z, H, ch, 66)
+    got = msa_ref.pair_weighted_averaging(m, z, pm, w, H, ch)
+    want = brute.pair_weighted_averaging(m, z, pm, w, H, ch)
+    # the fully masked row (i = N-1) is fp32 rounding of logit - 1e6 in the reference
+    # (ulp 0.0625), which the float64 loops do not reproduce: compared separately, loosely
+    _close(got[:, :, :-1], want[:, :, :-1])
+    _close(got[:, :, -1:], want[:, :, -1:], tol=5e-2)
+
+
+def test_pwa_uniform_bias_is_mean():
+    """proj_z = 0 and no mask: every weight is 1/N, so o = sigmoid(g) * mean_j v."""
+    B, S, N, c_m, c_z, H, ch = 1, 2, 4, 8, 6, 2, 3
+    g = torch.Generator().manual_seed(67)
+    m = torch.randn((B, S, N, c_m), generator=g)
+    z = torch.randn((B, N, N, c_z), generator=g)
+    w = _pwa_w(c_m, c_z, H, ch, 68)
+    w["proj_z.weight"] = torch.zeros_like(w["proj_z.weight"])
+    mn = F.layer_norm(m, (c_m,), w["norm_m.weight"], w["norm_m.bias"])
+    v, gg = mn @ w["proj_m.weight"].T, torch.sigmoid(mn @ w["proj_g.weight"].T)
+    want = (gg * v.mean(dim=2, keepdim=True)) @ w["proj_o.weight"].T
+    _close(msa_ref.pair_weighted_averaging(m, z, torch.ones((B, N, N)), w, H, ch), want)
+
+
+def test_msa_input_is_column_gather():
+    """One-hot projection = the weight column of the token, plus the three feature columns
+    and the s projection broadcast over sequences."""
+    S, N, c_m, c_s = 3, 4, 6, 5
+    g = torch.Generator().manual_seed(69)
+    msa = torch.randint(0, msa_ref.NUM_TOKENS, (1, S, N), generator=g)
+    hd, dv, pr = (torch.rand((1, S, N), generator=g) for _ in range(3))
+    emb = torch.randn((1, N, c_s), generator=g)
+    w = _w({"msa_proj.weight": (c_m, msa_ref.NUM_TOKENS + 3), "s_proj.weight": (c_m, c_s)}, 70)
+    W = w["msa_proj.weight"]
+    want = (W[:, msa[0]].permute(1, 2, 0) + hd[0, ..., None] * W[:, 33] + dv[0, ..., None] * W[:, 34]
+            + pr[0, ..., None] * W[:, 35] + (emb[0] @ w["s_proj.weight"].T)[None])
+    _close(msa_ref.msa_input(msa, hd, dv, pr, emb, w)[0], want)
