@@ -269,6 +269,42 @@ typedef struct pf_transition_mx8_args {
 int pf_transition_mx8_fwd(const pf_transition_mx8_args* args);
 
 /* ------------------------------------------------------------------------------
+ * MSA module (widening beyond the Pairformer: tt_bio/reference.py:1150-1398, the ttnn
+ * MSA / MSALayer in tt_bio/tenstorrent.py:1723-1855).
+ * -------------------------------------------------------------------------- */
+/* Outer product mean (OuterProductMean.forward, tt_bio/reference.py:596-664; ttnn
+ * tt_bio/tenstorrent.py:1632-1720, which divides by the sequence count instead of the
+ * per-pair mask count -- this follows the CPU reference):
+ *   z[b,i,j,:] (+)= W_o vec_{c,d}(sum_s a[s,i,c] b[s,j,d]) / max(1, sum_s mask[s,i] mask[s,j]) + b_o,
+ *   a = W_a LN(m) * mask, b = W_b LN(m) * mask.
+ * m fp32 [B][S][N][c_m], msa_mask fp32 [B][S][N] or NULL (all ones), z fp32 [B][N][N][C]
+ * updated in place (accumulate = 1) or overwritten.  c_m = 64, c_hidden = 32, C = 128,
+ * N a multiple of 32, any S. */
+typedef struct pf_opm_args {
+  int B, S, N, c_m, c_hidden, C;
+  int accumulate;
+  float eps;
+  const float* m; const float* msa_mask; float* z;
+  const float* norm_w; const float* norm_b;   /* norm.{weight,bias} [c_m] */
+  const void* w_a; const void* w_b;           /* proj_{a,b}.weight [c_hidden][c_m] */
+  const void* w_o; const float* b_o;          /* proj_o.weight [C][c_hidden^2], bias [C] fp32 */
+  void* workspace; size_t workspace_bytes;
+  void* stream;
+} pf_opm_args;
+
+size_t pf_opm_workspace_size(int B, int S, int N);
+int pf_opm_fwd(const pf_opm_args* args);
+
+/* Batched NT product X[p][i][j] = scale * sum_k A[p][i][k] * B[p][j][k] on the MFMA
+ * contraction kernel: A [planes][M][K], B [planes][Nc][K] in the operand type, X
+ * [planes][M][Nc] fp32 (x_fp32 = 1) or operand type; M, Nc multiples of 32, K a multiple of
+ * 64.  No single reference counterpart: it is the building block of the MSA module's
+ * einsums "bsic,bsjd->bijcd" (tt_bio/reference.py:656) and "bhij,bhsjd->bhsid" (:786),
+ * exported for tests and measurement.  Asynchronous on `stream`. */
+int pf_batched_nt_gemm(const void* A, const void* B, void* X, int x_fp32, int planes, int M, int Nc, int K,
+                       float scale, void* stream);
+
+/* ------------------------------------------------------------------------------
  * Row primitives (tt_bio/boltz2.py:638-768): LayerNorm and Linear over rows.
  * -------------------------------------------------------------------------- */
 /* out[r,:] = LN(x[r,:]) * w + b, fp32, any C <= 4096.  (nn.LayerNorm, eps) */

@@ -345,3 +345,49 @@ def test_layer_batch2_matches_single(gpu):
     s_ref, z_ref = ref.pairformer_stack(S, Z, M, PM, w, 1)
     check("batch-2 layer z", z_b, z_ref)
     check("batch-2 layer s", s_b, s_ref)
+
+
+@pytest.mark.parametrize("P,M,Nc,K", [(3, 96, 320, 192), (2, 512, 256, 1024), (1, 288, 800, 64)])
+def test_batched_nt_gemm(gpu, P, M, Nc, K):
+    """Rectangular form of the contraction kernel (partial 256-tiles in both dimensions):
+    fp32 output equals an fp32 product of the same rounded operands up to summation order;
+    the operand-type output is that result (times scale) rounded once."""
+    g = torch.Generator().manual_seed(M + Nc + K)
+    A = torch.randn((P, M, K), generator=g).half()
+    Bm = torch.randn((P, Nc, K), generator=g).half()
+    want = torch.bmm(A.float(), Bm.float().transpose(1, 2).contiguous())
+    X = torch.empty((P, M, Nc), dtype=torch.float32, device=gpu)
+    ops.launch_batched_nt_gemm(A.to(gpu), Bm.to(gpu), X)
+    mx, _ = stats(X, want)
+    assert mx < 1e-5, mx
+    Xh = torch.empty((P, M, Nc), dtype=torch.float16, device=gpu)
+    ops.launch_batched_nt_gemm(A.to(gpu), Bm.to(gpu), Xh, 0.25)
+    err = (Xh.float().cpu() - 0.25 * want).abs()
+    assert (err <= 2 ** -10 * (0.25 * want).abs() + 1e-3).all()
+
+
+# ------------------------------------------------------------------------------ MSA module
+from oracle import msa_ref  # noqa: E402
+
+
+def _msa_sub(seed, prefix, c_m=64, c_z=128):
+    shapes = synthetic.msa_layer_shapes(c_m, c_z)
+    return ref.sub(synthetic.draw({k: v for k, v in shapes.items() if k.startswith(prefix + ".")}, seed), prefix)
+
+
+@pytest.mark.parametrize("S,N", [(40, 64), (130, 96)])
+def test_outer_product_mean(gpu, S, N):
+    """pf_opm_fwd vs the fp32 oracle: S padded to 64 inside, random sequence mask (with a
+    fully masked sequence and tokens missing from some sequences), z += update."""
+    w = _msa_sub(71, "outer_product_mean")
+    g = torch.Generator().manual_seed(S + N)
+    m = torch.randn((1, S, N, 64), generator=g)
+    mask = (torch.rand((1, S, N), generator=g) > 0.2).float()
+    mask[:, 3] = 0.0
+    z = torch.randn((1, N, N, 128), generator=g)
+    want = z + msa_ref.outer_product_mean(m, mask, w)
+    zd = z.to(gpu).contiguous()
+    wd = _dev_w(w, gpu)
+    ws = ops.workspace(ops.opm_workspace_bytes(1, S, N), gpu)
+    ops.launch_opm(m.to(gpu).contiguous(), mask.to(gpu).contiguous(), zd, wd, ws)
+    check(f"outer product mean S={S} N={N}", zd, want)

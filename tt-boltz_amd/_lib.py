@@ -64,6 +64,16 @@ class ApbArgs(ctypes.Structure):
     ]
 
 
+class OpmArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int), ("S", c_int), ("N", c_int), ("c_m", c_int), ("c_hidden", c_int), ("C", c_int),
+        ("accumulate", c_int), ("eps", c_float),
+        ("m", c_void_p), ("msa_mask", c_void_p), ("z", c_void_p), ("norm_w", c_void_p), ("norm_b", c_void_p),
+        ("w_a", c_void_p), ("w_b", c_void_p), ("w_o", c_void_p), ("b_o", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
+    ]
+
+
 class TrimulMx8Args(ctypes.Structure):
     _fields_ = [
         ("B", c_int), ("N", c_int), ("C", c_int), ("hidden", c_int), ("direction", c_int),
@@ -106,6 +116,10 @@ SIGNATURES = {
     "pf_apb_pair_bias": (c_int, [ctypes.POINTER(ApbArgs)]),
     "pf_apb_attend": (c_int, [ctypes.POINTER(ApbArgs)]),
     "pf_transition_pair_bias_fwd": (c_int, [ctypes.POINTER(TransitionArgs), ctypes.POINTER(ApbArgs)]),
+    "pf_opm_workspace_size": (c_size_t, [c_int, c_int, c_int]),
+    "pf_opm_fwd": (c_int, [ctypes.POINTER(OpmArgs)]),
+    "pf_batched_nt_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_float,
+                                   c_void_p]),
     "pf_layernorm_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_float, c_void_p]),
     "pf_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_int, c_void_p]),
     "pf_pair_ln_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long,

@@ -38,3 +38,8 @@ int pf_linear_batch(const pf_lin_job* jobs, int njobs, long rows, int K, int Nou
 // bias [B][H][N][N] inside the workspace.
 int pf_apb_check(const pf_apb_args* a, const char* fn, bool bias_only);
 float* pf_apb_bias_ptr(const pf_apb_args* a);
+
+// Batched X[p][i][j] = scale * sum_k A[p][i][k] * B[p][j][k] (trimul.hip): A [P][M][K],
+// B [P][Nc][K] op_t, X [P][M][Nc] fp32 (x_fp32) or op_t; M, Nc % 32 == 0, K % 64 == 0.
+int pf_contract_rect(const void* A, const void* B, void* X, int x_fp32, int planes, int M, int Nc, int K,
+                     float scale, hipStream_t st);

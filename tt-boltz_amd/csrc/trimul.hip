@@ -245,17 +245,16 @@ constexpr size_t TMD8_LDS_BYTES = (size_t)2 * 2 * DSLAB8 * sizeof(op_t);
 template <typename OutT>
 __global__ __launch_bounds__(256, 1) void tm_contract_dma_kernel(
     const op_t* __restrict__ A, const op_t* __restrict__ Bop, OutT* __restrict__ X,
-    int N, int tpd, int total, float out_scale, long in_plane_stride) {
+    int M, int Nc, int K, int tn, int total, float out_scale) {
   extern __shared__ __attribute__((aligned(16))) op_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wid >> 1, wn = wid & 1;
   const int w = xcd_remap(blockIdx.x, total);
-  const int tiles = tpd * tpd;
+  const int tiles = ((M + BM2 - 1) / BM2) * tn;
   const long plane = w / tiles;
   const int t = w - (int)plane * tiles;
-  const int i0 = (t / tpd) * BM2, j0 = (t % tpd) * BM2;
-  const long NN = (long)N * N;
+  const int i0 = (t / tn) * BM2, j0 = (t % tn) * BM2;
 
   // DMA: instruction q (0..7) of this wave covers slab rows (8*wid + q)*8 + (lane >> 3)
   int offA[8], offB[8];
@@ -263,11 +262,11 @@ __global__ __launch_bounds__(256, 1) void tm_contract_dma_kernel(
   for (int q = 0; q < 8; ++q) {
     const int r = (8 * wid + q) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ slab_swz8(r);
-    offA[q] = min(i0 + r, N - 1) * N + 8 * c;
-    offB[q] = min(j0 + r, N - 1) * N + 8 * c;
+    offA[q] = min(i0 + r, M - 1) * K + 8 * c;
+    offB[q] = min(j0 + r, Nc - 1) * K + 8 * c;
   }
-  const op_t* Ap = A + plane * in_plane_stride;
-  const op_t* Bp = Bop + plane * in_plane_stride;
+  const op_t* Ap = A + plane * M * K;
+  const op_t* Bp = Bop + plane * Nc * K;
   auto issue = [&](int kt) {
     op_t* sa = smem + (kt & 1) * 2 * DSLAB8;
     op_t* sb = sa + DSLAB8;
@@ -308,7 +307,7 @@ __global__ __launch_bounds__(256, 1) void tm_contract_dma_kernel(
   }                                                               \
   __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
 
-  const int nk = N / DK8;
+  const int nk = K / DK8;
   issue(0);
   opx8 f0a[4], f0b[4], f1a[4], f1b[4];
   for (int kt = 0; kt < nk; ++kt) {
@@ -334,24 +333,24 @@ __global__ __launch_bounds__(256, 1) void tm_contract_dma_kernel(
     __builtin_amdgcn_sched_barrier(0);
   }
 #undef PF_INTERLEAVE_8_READS
-  OutT* Xp = X + plane * NN;
+  OutT* Xp = X + plane * M * Nc;
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
     const int ib = i0 + wm * 128 + 32 * x;
 #pragma unroll
     for (int y = 0; y < 4; ++y) {
       const int jb = j0 + wn * 128 + 32 * y;
-      if (ib >= N || jb >= N) continue;
+      if (ib >= M || jb >= Nc) continue;
       if constexpr (sizeof(OutT) == 4) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           f32x4 v;
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = acc[y][x][4 * g + e] * out_scale;
-          *reinterpret_cast<f32x4*>(Xp + (long)(ib + m) * N + jb + 8 * g + 4 * h) = v;
+          *reinterpret_cast<f32x4*>(Xp + (long)(ib + m) * Nc + jb + 8 * g + 4 * h) = v;
         }
       } else {
-        store_runs16((op_t*)(Xp + (long)(ib + m) * N + jb), acc[y][x], out_scale, h);   // 16-byte runs
+        store_runs16((op_t*)(Xp + (long)(ib + m) * Nc + jb), acc[y][x], out_scale, h);   // 16-byte runs
       }
     }
   }
@@ -447,23 +446,30 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
 
 // Contraction dispatch: 256x256 tiles from N = 384 up (enough tiles to fill the chip
 // and a long enough K loop), 128x128 tiles below.
+// Rectangular form (256x256 tiles, any M, Nc multiple of 32, K multiple of 64):
+// X[p][i][j] = sum_k A[p][i][k] * B[p][j][k], A [P][M][K], B [P][Nc][K], X [P][M][Nc].
+template <typename OutT>
+int launch_contract_rect(const op_t* A, const op_t* B, OutT* X, int planes, int M, int Nc, int K, float scale,
+                         hipStream_t st) {
+  static bool attr_set = false;   // per process; the attribute is a property of the function
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)tm_contract_dma_kernel<OutT>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)TMD8_LDS_BYTES) != hipSuccess)
+      return pf_fail(PF_E_LAUNCH, "tm_contract_dma_kernel: cannot reserve %zu bytes of LDS", TMD8_LDS_BYTES);
+    attr_set = true;
+  }
+  const int tn = (Nc + BM2 - 1) / BM2;
+  const long total = (long)planes * ((M + BM2 - 1) / BM2) * tn;
+  if (total > 0x7fffffff) return pf_fail(PF_E_INVALID, "contraction: too many tiles (%ld)", total);
+  tm_contract_dma_kernel<OutT><<<(unsigned)total, 256, TMD8_LDS_BYTES, st>>>(A, B, X, M, Nc, K, tn, (int)total,
+                                                                             scale);
+  PF_CHECK_LAUNCH("tm_contract_dma_kernel");
+  return PF_OK;
+}
+
 template <typename OutT>
 int launch_contract(const op_t* opA, const op_t* opB, OutT* X, int planes, int N, float scale, hipStream_t st) {
-  if (N >= 384) {
-    static bool attr_set = false;   // per process; the attribute is a property of the function
-    if (!attr_set) {
-      if (hipFuncSetAttribute((const void*)tm_contract_dma_kernel<OutT>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)TMD8_LDS_BYTES) != hipSuccess)
-        return pf_fail(PF_E_LAUNCH, "tm_contract_dma_kernel: cannot reserve %zu bytes of LDS", TMD8_LDS_BYTES);
-      attr_set = true;
-    }
-    const int tpd = (N + BM2 - 1) / BM2;
-    const int total = planes * tpd * tpd;
-    tm_contract_dma_kernel<OutT><<<total, 256, TMD8_LDS_BYTES, st>>>(opA, opB, X, N, tpd, total, scale,
-                                                                     (long)N * N);
-    PF_CHECK_LAUNCH("tm_contract_dma_kernel");
-    return PF_OK;
-  }
+  if (N >= 384) return launch_contract_rect<OutT>(opA, opB, X, planes, N, N, N, scale, st);
   const int tpd = (N + BM - 1) / BM;
   const int total = planes * tpd * tpd;
   tm_contract_kernel<OutT><<<total, 256, 0, st>>>(opA, opB, X, N, tpd, total, scale);
@@ -544,6 +550,23 @@ extern "C" int pf_trimul_fwd(const pf_trimul_args* a) {
   }
   PF_CHECK_LAUNCH("tm_out_kernel");
   return PF_OK;
+}
+
+int pf_contract_rect(const void* A, const void* B, void* X, int x_fp32, int planes, int M, int Nc, int K,
+                     float scale, hipStream_t st) {
+  if (!A || !B || !X) return pf_fail(PF_E_INVALID, "pf_batched_nt_gemm: null pointer");
+  if (planes <= 0 || M <= 0 || Nc <= 0 || K <= 0 || M % 32 || Nc % 32 || K % 64)
+    return pf_fail(PF_E_INVALID, "pf_batched_nt_gemm: need M, Nc multiples of 32 and K a multiple of 64 "
+                                 "(planes=%d M=%d Nc=%d K=%d)", planes, M, Nc, K);
+  if ((long)M * K >= (1l << 31) || (long)Nc * K >= (1l << 31))
+    return pf_fail(PF_E_INVALID, "pf_batched_nt_gemm: a plane of A or B exceeds 2^31 elements");
+  if (x_fp32) return launch_contract_rect<float>((const op_t*)A, (const op_t*)B, (float*)X, planes, M, Nc, K, scale, st);
+  return launch_contract_rect<op_t>((const op_t*)A, (const op_t*)B, (op_t*)X, planes, M, Nc, K, scale, st);
+}
+
+extern "C" int pf_batched_nt_gemm(const void* A, const void* B, void* X, int x_fp32, int planes, int M, int Nc,
+                                  int K, float scale, void* stream) {
+  return pf_contract_rect(A, B, X, x_fp32, planes, M, Nc, K, scale, (hipStream_t)stream);
 }
 
 // Standalone contraction (the MFMA hot loop alone), for measurement and tests.

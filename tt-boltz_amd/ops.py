@@ -217,6 +217,16 @@ def launch_pair_ln_linear(x: torch.Tensor, base: torch.Tensor, ln_w: torch.Tenso
                "pf_pair_ln_linear_fwd", variant)
 
 
+def launch_batched_nt_gemm(A: torch.Tensor, B: torch.Tensor, X: torch.Tensor, scale: float = 1.0,
+                           variant: str = DEFAULT_VARIANT) -> None:
+    """X[p] = scale * A[p] @ B[p]^T (pf_batched_nt_gemm): A [P,M,K], B [P,Nc,K] operand type,
+    X [P,M,Nc] fp32 or operand type."""
+    P, M, K = A.shape
+    Nc = B.shape[1]
+    _lib.check(_lib.load(variant).pf_batched_nt_gemm(_ptr(A), _ptr(B), _ptr(X), int(X.dtype == torch.float32), P, M,
+                                                     Nc, K, float(scale), _stream()), "pf_batched_nt_gemm", variant)
+
+
 def launch_trimul_contract(opA: torch.Tensor, opB: torch.Tensor, X: torch.Tensor,
                            variant: str = DEFAULT_VARIANT) -> None:
     """X fp32 -> unscaled fp32 output; X in the operand dtype -> 2^-8-scaled (pf_trimul_fwd's format)."""
@@ -430,3 +440,23 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
     out = torch.empty(xin.shape[:-1] + (weight.shape[0],), dtype=torch.float32, device=dev)
     launch_linear(xin, opw(weight, dev, variant), f32(bias, dev), None, out, variant)
     return out
+
+
+# --------------------------------------------------------------------------------------
+# MSA module
+# --------------------------------------------------------------------------------------
+def opm_workspace_bytes(B: int, S: int, N: int, variant: str = DEFAULT_VARIANT) -> int:
+    return _lib.load(variant).pf_opm_workspace_size(B, S, N)
+
+
+def launch_opm(m: torch.Tensor, msa_mask: Optional[torch.Tensor], z: torch.Tensor, w: Mapping[str, torch.Tensor],
+               ws: torch.Tensor, accumulate: bool = True, eps: float = 1e-5, variant: str = DEFAULT_VARIANT) -> None:
+    """z (+)= OuterProductMean(m, msa_mask) (pf_opm_fwd); m [B,S,N,64], z [B,N,N,128]."""
+    B, S, N, c_m = m.shape
+    a = _lib.OpmArgs(
+        B=B, S=S, N=N, c_m=c_m, c_hidden=w["proj_a.weight"].shape[0], C=z.shape[-1], accumulate=int(accumulate),
+        eps=eps, m=_ptr(m), msa_mask=_ptr(msa_mask), z=_ptr(z), norm_w=_ptr(w["norm.weight"]),
+        norm_b=_ptr(w["norm.bias"]), w_a=_ptr(w["proj_a.weight"]), w_b=_ptr(w["proj_b.weight"]),
+        w_o=_ptr(w["proj_o.weight"]), b_o=_ptr(w["proj_o.bias"]),
+        workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
+    _lib.check(_lib.load(variant).pf_opm_fwd(ctypes.byref(a)), "pf_opm_fwd", variant)

@@ -54,6 +54,37 @@ def layer_shapes(c_z: int = 128, c_s: int = 384, tri_heads: int = 4, tri_dim: in
     return sh
 
 
+def msa_layer_shapes(c_m: int = 64, c_z: int = 128, avg_heads: int = 8, avg_dim: int = 32, opm_hidden: int = 32,
+                     tri_heads: int = 4, tri_dim: int = 32) -> Dict[str, tuple]:
+    """State-dict keys and shapes of one MSALayer (reference.py:1311-1351): pair weighted
+    averaging, msa transition, outer product mean and a no-seq PairformerLayer."""
+    hd = avg_heads * avg_dim
+    sh = {"pair_weighted_averaging.norm_m.weight": (c_m,), "pair_weighted_averaging.norm_m.bias": (c_m,),
+          "pair_weighted_averaging.norm_z.weight": (c_z,), "pair_weighted_averaging.norm_z.bias": (c_z,),
+          "pair_weighted_averaging.proj_m.weight": (hd, c_m), "pair_weighted_averaging.proj_g.weight": (hd, c_m),
+          "pair_weighted_averaging.proj_z.weight": (avg_heads, c_z),
+          "pair_weighted_averaging.proj_o.weight": (c_m, hd),
+          "msa_transition.norm.weight": (c_m,), "msa_transition.norm.bias": (c_m,),
+          "msa_transition.fc1.weight": (4 * c_m, c_m), "msa_transition.fc2.weight": (4 * c_m, c_m),
+          "msa_transition.fc3.weight": (c_m, 4 * c_m),
+          "outer_product_mean.norm.weight": (c_m,), "outer_product_mean.norm.bias": (c_m,),
+          "outer_product_mean.proj_a.weight": (opm_hidden, c_m), "outer_product_mean.proj_b.weight": (opm_hidden, c_m),
+          "outer_product_mean.proj_o.weight": (c_z, opm_hidden * opm_hidden),
+          "outer_product_mean.proj_o.bias": (c_z,)}
+    sh.update({f"pairformer_layer.{k}": v for k, v in layer_shapes(c_z, tri_heads=tri_heads, tri_dim=tri_dim,
+                                                                    transform_s=False).items()})
+    return sh
+
+
+def msa_module_shapes(n_blocks: int, c_m: int = 64, c_z: int = 128, c_s: int = 384, n_feat: int = 36) -> Dict[str, tuple]:
+    """MSAModule (reference.py:1150-1203): s_proj, msa_proj and ``layers.{i}.*``."""
+    sh = {"s_proj.weight": (c_m, c_s), "msa_proj.weight": (c_m, n_feat)}
+    one = msa_layer_shapes(c_m, c_z)
+    for i in range(n_blocks):
+        sh.update({f"layers.{i}.{k}": v for k, v in one.items()})
+    return sh
+
+
 def recycle_shapes(c_z: int = 128, c_s: int = 384) -> Dict[str, tuple]:
     """Boltz2 recycling parameters (boltz2.py:4961-4968)."""
     return {"s_norm.weight": (c_s,), "s_norm.bias": (c_s,), "z_norm.weight": (c_z,), "z_norm.bias": (c_z,),
