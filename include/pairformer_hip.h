@@ -295,6 +295,30 @@ typedef struct pf_opm_args {
 size_t pf_opm_workspace_size(int B, int S, int N);
 int pf_opm_fwd(const pf_opm_args* args);
 
+/* Pair weighted averaging (PairWeightedAveraging.forward, tt_bio/reference.py:715-790;
+ * ttnn tt_bio/tenstorrent.py:1757-1796 callers):
+ *   w[h,i,j] = softmax_j(LN_z(z[i,j]) . W_z[h] - 1e6 (1 - pair_mask[i,j])),
+ *   o[s,i,h,:] = sigmoid(W_g LN_m(m[s,i]))_h * sum_j w[h,i,j] (W_m LN_m(m[s,j]))_h,
+ *   out[s,i,:] = (accumulate ? m[s,i,:] : 0) + W_o o[s,i,:]   (out may alias m).
+ * m fp32 [B][S][N][c_m], z fp32 [B][N][N][C], pair_mask fp32 [B][N][N] or NULL.
+ * c_m = 64, C = 128, H = 8 heads of c_h = 32, N a multiple of 64, any S. */
+typedef struct pf_pwa_args {
+  int B, S, N, c_m, C, H, c_h;
+  int accumulate;
+  float eps;
+  const float* m; float* out; const float* z; const float* pair_mask;
+  const float* norm_m_w; const float* norm_m_b;   /* norm_m.{weight,bias} [c_m] */
+  const float* norm_z_w; const float* norm_z_b;   /* norm_z.{weight,bias} [C] */
+  const void* w_m; const void* w_g;               /* proj_{m,g}.weight [H*c_h][c_m] */
+  const void* w_z;                                /* proj_z.weight [H][C] */
+  const void* w_o;                                /* proj_o.weight [c_m][H*c_h] */
+  void* workspace; size_t workspace_bytes;
+  void* stream;
+} pf_pwa_args;
+
+size_t pf_pwa_workspace_size(int B, int S, int N);
+int pf_pwa_fwd(const pf_pwa_args* args);
+
 /* Batched NT product X[p][i][j] = scale * sum_k A[p][i][k] * B[p][j][k] on the MFMA
  * contraction kernel: A [planes][M][K], B [planes][Nc][K] in the operand type, X
  * [planes][M][Nc] fp32 (x_fp32 = 1) or operand type; M, Nc multiples of 32, K a multiple of

@@ -391,3 +391,22 @@ def test_outer_product_mean(gpu, S, N):
     ws = ops.workspace(ops.opm_workspace_bytes(1, S, N), gpu)
     ops.launch_opm(m.to(gpu).contiguous(), mask.to(gpu).contiguous(), zd, wd, ws)
     check(f"outer product mean S={S} N={N}", zd, want)
+
+
+@pytest.mark.parametrize("S,N", [(40, 64), (33, 128)])
+def test_pair_weighted_averaging(gpu, S, N):
+    """pf_pwa_fwd vs the fp32 oracle, m += update in place, a padded token tail (its row of
+    weights is fully masked: compared on the valid tokens, where the reference's fp32
+    rounding of logit - 1e6 does not enter)."""
+    w = _msa_sub(72, "pair_weighted_averaging")
+    g = torch.Generator().manual_seed(S * N)
+    m = torch.randn((1, S, N, 64), generator=g)
+    z = torch.randn((1, N, N, 128), generator=g)
+    tok = torch.ones((1, N)); tok[:, N - 7:] = 0
+    pm = tok[:, :, None] * tok[:, None, :]
+    want = m + msa_ref.pair_weighted_averaging(m, z, pm, w)
+    md = m.to(gpu).contiguous()
+    wd = _dev_w(w, gpu)
+    ws = ops.workspace(ops.pwa_workspace_bytes(1, S, N), gpu)
+    ops.launch_pwa(md, z.to(gpu).contiguous(), pm.to(gpu).contiguous(), md, wd, ws)
+    check(f"pair weighted averaging S={S} N={N} (valid tokens)", md[:, :, : N - 7], want[:, :, : N - 7])

@@ -74,6 +74,17 @@ class OpmArgs(ctypes.Structure):
     ]
 
 
+class PwaArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int), ("S", c_int), ("N", c_int), ("c_m", c_int), ("C", c_int), ("H", c_int), ("c_h", c_int),
+        ("accumulate", c_int), ("eps", c_float),
+        ("m", c_void_p), ("out", c_void_p), ("z", c_void_p), ("pair_mask", c_void_p),
+        ("norm_m_w", c_void_p), ("norm_m_b", c_void_p), ("norm_z_w", c_void_p), ("norm_z_b", c_void_p),
+        ("w_m", c_void_p), ("w_g", c_void_p), ("w_z", c_void_p), ("w_o", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
+    ]
+
+
 class TrimulMx8Args(ctypes.Structure):
     _fields_ = [
         ("B", c_int), ("N", c_int), ("C", c_int), ("hidden", c_int), ("direction", c_int),
@@ -118,6 +129,8 @@ SIGNATURES = {
     "pf_transition_pair_bias_fwd": (c_int, [ctypes.POINTER(TransitionArgs), ctypes.POINTER(ApbArgs)]),
     "pf_opm_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "pf_opm_fwd": (c_int, [ctypes.POINTER(OpmArgs)]),
+    "pf_pwa_workspace_size": (c_size_t, [c_int, c_int, c_int]),
+    "pf_pwa_fwd": (c_int, [ctypes.POINTER(PwaArgs)]),
     "pf_batched_nt_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_float,
                                    c_void_p]),
     "pf_layernorm_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_float, c_void_p]),

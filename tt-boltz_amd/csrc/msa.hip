@@ -177,6 +177,183 @@ __global__ __launch_bounds__(256, 2) void opm_out_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Pair weighted averaging (PairWeightedAveraging.forward, tt_bio/reference.py:715-790):
+//   logits   log2(e) * LN_z(z) . W_z[h] by the single track's pair-bias kernel
+//   softmax  pwa_softmax_kernel: over j, with -1e6 * (1 - mask[i,j]), to fp16 weights
+//            Wt [B*H][N (i)][N (j)]
+//   v        pwa_proj_kernel: W_m LN_m(m) written k-major, v_t [B*H][S*32 (s, d)][N (j)]
+//   average  O[b*H+h][i][(s, d)] = sum_j Wt[.][i][j] v_t[.][(s, d)][j] on the batched NT
+//            kernel ("bhij,bhsjd->bhsid")
+//   output   pwa_out_kernel: gate sigmoid(W_g LN_m(m)) recomputed in registers, times O,
+//            W_o (64 x 256), residual into m
+// ---------------------------------------------------------------------------------
+constexpr int PH = 8, PD = 32, PHD = PH * PD;   // heads, head width, 256
+
+// One wave per row (b, h, i): three passes over the row (max, sum, write).
+__global__ __launch_bounds__(256) void pwa_softmax_kernel(const float* __restrict__ logits,
+                                                          const float* __restrict__ pair_mask, op_t* __restrict__ Wt,
+                                                          int B, int N) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (long)B * PH * N) return;
+  const int i = (int)(row % N);
+  const int b = (int)(row / ((long)PH * N));
+  const float* x = logits + row * N;
+  const float* pm = pair_mask ? pair_mask + ((long)b * N + i) * N : nullptr;
+  constexpr float MASKED = -1e6f * 1.4426950408889634f;   // reference -inf = 1e6, log2 units
+  auto val = [&](int j) PF_INLINE { return x[j] + (pm ? (1.f - pm[j]) * MASKED : 0.f); };
+  float mx = -INFINITY;
+  for (int j = lane; j < N; j += 64) mx = fmaxf(mx, val(j));
+  mx = wave_max(mx);
+  float sm = 0.f;
+  for (int j = lane; j < N; j += 64) sm += exp2_fast(val(j) - mx);
+  const float inv = 1.f / wave_sum(sm);
+  op_t* w = Wt + row * N;
+  for (int j = lane; j < N; j += 64) w[j] = (op_t)(exp2_fast(val(j) - mx) * inv);
+}
+
+// LN over the 64 channels of a row held as channels 16 st + 8 h + t (st = 0..3) by lane
+// half h, as 4 MFMA fragments.
+PF_DEV void ln64_to_frag(const float* __restrict__ row, int h, const float* __restrict__ w,
+                         const float* __restrict__ b, float eps, opx8 (&f)[4]) {
+  float x[32];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const f32x4 u = *reinterpret_cast<const f32x4*>(row + 16 * st + 8 * h);
+    const f32x4 v = *reinterpret_cast<const f32x4*>(row + 16 * st + 8 * h + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[8 * st + e] = u[e];
+      x[8 * st + 4 + e] = v[e];
+    }
+  }
+  float sm = 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) sm += x[k];
+  const float mean = xor32_sum(sm) * (1.f / CM);
+  float var = 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) { const float d = x[k] - mean; var += d * d; }
+  const float rstd = rsqrtf(xor32_sum(var) * (1.f / CM) + eps);
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int c = 16 * st + 8 * h + t;
+      f[st][t] = (op_t)((x[8 * st + t] - mean) * rstd * w[c] + b[c]);
+    }
+}
+
+// v projection: a wave takes 32 consecutive tokens j of one (b, s); W_m [256][64] sits in
+// LDS (128-byte rows, 16-byte chunk c of row R at slot c ^ swz8r(R)).  D[(h, d)][j]: lane
+// (j, half) writes v_t rows ((b*H + h)*S + s)*32 + d at column j (64 contiguous bytes per
+// row and register).
+__global__ __launch_bounds__(512) void pwa_proj_kernel(
+    const float* __restrict__ m, const float* __restrict__ lnw, const float* __restrict__ lnb,
+    const op_t* __restrict__ wm, op_t* __restrict__ vt, int B, int S, int N, float eps) {
+  __shared__ __attribute__((aligned(16))) op_t sw[PHD * CM];
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, mm = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int c = tid; c < PHD * 8; c += 512) {
+    const int R = c >> 3, k = c & 7;
+    st_x8(sw + R * CM + 8 * (k ^ swz8r(R)), ld_x8(wm + R * CM + 8 * k));
+  }
+  __syncthreads();
+  const int nj = N / 32;
+  const long wv = (long)blockIdx.x * 8 + wid;
+  if (wv >= (long)B * S * nj) return;
+  const int j0 = 32 * (int)(wv % nj);
+  const long bs = wv / nj;   // b * S + s
+  const int s = (int)(bs % S), b = (int)(bs / S);
+  opx8 xf[4];
+  ln64_to_frag(m + (bs * N + j0 + mm) * CM, h, lnw, lnb, eps, xf);
+  const int sw8 = swz8r(mm);
+#pragma unroll 1
+  for (int blk = 0; blk < PH; ++blk) {
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+      acc = mfma32(ld_x8(sw + (32 * blk + mm) * CM + 8 * ((2 * st + h) ^ sw8)), xf[st], acc);   // rows = (h, d)
+    op_t* dst = vt + (((long)b * PH + blk) * S + s) * PD * (long)N + j0 + mm;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dst[(long)acc_row(r, h) * N] = (op_t)acc[r];
+  }
+}
+
+// Output: a wave takes 32 consecutive sequences s of one (b, i).  W_g [256][64] and
+// W_o [64][256] sit in LDS.  The gate is formed as D[k][s] with W_g rows loaded in perm16
+// order, so its accumulator registers 8 s' + t of half h hold k = 16 s' + 8 h + t of the
+// block -- the B-operand order of the W_o product; each such fragment is multiplied by
+// the matching 16 bytes of O and fed to D[o][s] += W_o . og.  Residual into m in the
+// output-aligned layout (16-byte loads / stores).
+__global__ __launch_bounds__(512) void pwa_out_kernel(
+    const float* m_in, float* m_out, const float* __restrict__ lnw, const float* __restrict__ lnb,
+    const op_t* __restrict__ wg, const op_t* __restrict__ wo, const op_t* __restrict__ O, int B, int S, int N,
+    int accumulate, float eps) {
+  __shared__ __attribute__((aligned(16))) op_t sg[PHD * CM];
+  __shared__ __attribute__((aligned(16))) op_t so[CM * PHD];
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, mm = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int c = tid; c < PHD * 8; c += 512) {   // W_g: 256 rows of 8 chunks
+    const int R = c >> 3, k = c & 7;
+    st_x8(sg + R * CM + 8 * (k ^ swz8r(R)), ld_x8(wg + R * CM + 8 * k));
+  }
+  for (int c = tid; c < CM * 32; c += 512) {   // W_o: 64 rows of 32 chunks
+    const int R = c >> 5, k = c & 31;
+    st_x8(so + R * PHD + 8 * (k ^ (R & 15)), ld_x8(wo + R * PHD + 8 * k));
+  }
+  __syncthreads();
+  const int ns = (S + 31) / 32;
+  const long wv = (long)blockIdx.x * 8 + wid;
+  if (wv >= (long)B * N * ns) return;
+  const int s0 = 32 * (int)(wv % ns);
+  const long bi = wv / ns;   // b * N + i
+  const int i = (int)(bi % N), b = (int)(bi / N);
+  const int s = min(s0 + mm, S - 1);   // rows past S are computed on a clamped row and not stored
+  const long mrow = (((long)b * S + s) * N + i) * CM;
+  opx8 xf[4];
+  ln64_to_frag(m_in + mrow, h, lnw, lnb, eps, xf);
+  const int gr = perm16(mm), sg8 = swz8r(gr);
+  f32x16 acc[2] = {zero16(), zero16()};
+#pragma unroll 1
+  for (int blk = 0; blk < PH; ++blk) {
+    f32x16 g = zero16();
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+      g = mfma32(ld_x8(sg + (32 * blk + gr) * CM + 8 * ((2 * st + h) ^ sg8)), xf[st], g);   // rows = k (perm16)
+    const op_t* orow = O + ((long)(b * PH + blk) * N + i) * ((long)S * PD) + (long)s * PD + 8 * h;
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp) {
+      const opx8 ov = ld_x8(orow + 16 * sp);
+      opx8 og;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) og[t] = (op_t)((float)ov[t] * sigmoidf_fast(g[8 * sp + t]));
+      const int kc = 2 * (2 * blk + sp) + h;   // 16-byte chunk of the W_o row: k = 32 blk + 16 sp + 8 h
+#pragma unroll
+      for (int ob = 0; ob < 2; ++ob) {
+        const int R = 32 * ob + mm;
+        acc[ob] = mfma32(ld_x8(so + R * PHD + 8 * (kc ^ (R & 15))), og, acc[ob]);   // rows = output channel
+      }
+    }
+  }
+  if (s0 + mm >= S) return;
+  // lane (s, h): acc[ob][4 g + e] is channel 32 ob + 8 g + 4 h + e
+  const float* src = m_in + mrow;
+  float* dst = m_out + mrow;
+  f32x4 res[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    res[q] = accumulate ? *reinterpret_cast<const f32x4*>(src + oa_channel(q, h)) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = acc[q >> 2][4 * (q & 3) + e] + res[q][e];
+    *reinterpret_cast<f32x4*>(dst + oa_channel(q, h)) = v;
+  }
+}
+
 }  // namespace
 
 // Workspace of pf_opm_fwd: At, Bt [B][32N][S'], mask [B][N][S'], Z [B][32N][32N] (op_t),
@@ -223,5 +400,54 @@ extern "C" int pf_opm_fwd(const pf_opm_args* a) {
   opm_out_kernel<<<(unsigned)((pairs / 32 + 3) / 4), 256, 0, st>>>(Z, cnt, (const op_t*)a->w_o, a->b_o, a->z, B, N,
                                                                   X_LOAD_SCALE, a->accumulate);
   PF_CHECK_LAUNCH("opm_out_kernel");
+  return PF_OK;
+}
+
+// Workspace of pf_pwa_fwd: logits [B*H][N][N] fp32, weights [B*H][N][N], v_t [B*H][32S][N],
+// O [B*H][N][32S] (op_t).
+extern "C" size_t pf_pwa_workspace_size(int B, int S, int N) {
+  if (B <= 0 || S <= 0 || N <= 0) return 0;
+  const size_t bh = (size_t)B * PH, nn = (size_t)N * N, sn = (size_t)S * PD * N;
+  return bh * nn * sizeof(float) + (bh * nn + 2 * bh * sn) * sizeof(op_t);
+}
+
+extern "C" int pf_pwa_fwd(const pf_pwa_args* a) {
+  if (!a) return pf_fail(PF_E_INVALID, "pf_pwa_fwd: null args");
+  if (a->c_m != CM || a->C != CZ || a->H != PH || a->c_h != PD)
+    return pf_fail(PF_E_INVALID, "pf_pwa_fwd: need c_m = 64, C = 128, 8 heads of 32 (got %d, %d, %d, %d)", a->c_m,
+                   a->C, a->H, a->c_h);
+  if (a->B <= 0 || a->S <= 0 || a->N <= 0 || a->N % 64)
+    return pf_fail(PF_E_INVALID, "pf_pwa_fwd: need B, S > 0 and N a positive multiple of 64 (B=%d S=%d N=%d)", a->B,
+                   a->S, a->N);
+  if ((long)a->S * PD * a->N >= (1l << 31) || (long)a->B * a->N * a->N >= (1l << 31))
+    return pf_fail(PF_E_INVALID, "pf_pwa_fwd: shape too large (B=%d S=%d N=%d)", a->B, a->S, a->N);
+  if (!a->m || !a->out || !a->z || !a->norm_m_w || !a->norm_m_b || !a->norm_z_w || !a->norm_z_b || !a->w_m ||
+      !a->w_g || !a->w_z || !a->w_o || !a->workspace)
+    return pf_fail(PF_E_INVALID, "pf_pwa_fwd: null pointer argument");
+  const size_t need = pf_pwa_workspace_size(a->B, a->S, a->N);
+  if (a->workspace_bytes < need)
+    return pf_fail(PF_E_INVALID, "pf_pwa_fwd: workspace too small (%zu < %zu bytes)", a->workspace_bytes, need);
+  hipStream_t st = (hipStream_t)a->stream;
+  const int B = a->B, S = a->S, N = a->N;
+  const size_t bh = (size_t)B * PH, nn = (size_t)N * N, sn = (size_t)S * PD * N;
+  float* logits = (float*)a->workspace;
+  op_t* Wt = (op_t*)(logits + bh * nn);
+  op_t* vt = Wt + bh * nn;
+  op_t* O = vt + bh * sn;
+  int rc = pf_pair_logits(a->z, a->norm_z_w, a->norm_z_b, a->w_z, logits, B, N, PH, a->eps, st);
+  if (rc) return rc;
+  pwa_softmax_kernel<<<(unsigned)((bh * N + 3) / 4), 256, 0, st>>>(logits, a->pair_mask, Wt, B, N);
+  PF_CHECK_LAUNCH("pwa_softmax_kernel");
+  const long vw = (long)B * S * (N / 32);
+  pwa_proj_kernel<<<(unsigned)((vw + 7) / 8), 512, 0, st>>>(a->m, a->norm_m_w, a->norm_m_b, (const op_t*)a->w_m, vt,
+                                                           B, S, N, a->eps);
+  PF_CHECK_LAUNCH("pwa_proj_kernel");
+  // rows (s, d) of v_t are the Nc dimension; S*32 is a multiple of 32
+  if ((rc = pf_contract_rect(Wt, vt, O, 0, (int)bh, N, S * PD, N, 1.f, st))) return rc;
+  const long ow = (long)B * N * ((S + 31) / 32);
+  pwa_out_kernel<<<(unsigned)((ow + 7) / 8), 512, 0, st>>>(a->m, a->out, a->norm_m_w, a->norm_m_b,
+                                                          (const op_t*)a->w_g, (const op_t*)a->w_o, O, B, S, N,
+                                                          a->accumulate, a->eps);
+  PF_CHECK_LAUNCH("pwa_out_kernel");
   return PF_OK;
 }

@@ -43,3 +43,8 @@ float* pf_apb_bias_ptr(const pf_apb_args* a);
 // B [P][Nc][K] op_t, X [P][M][Nc] fp32 (x_fp32) or op_t; M, Nc % 32 == 0, K % 64 == 0.
 int pf_contract_rect(const void* A, const void* B, void* X, int x_fp32, int planes, int M, int Nc, int K,
                      float scale, hipStream_t st);
+
+// out[b][h][i][j] = log2(e) * LN(z[b,i,j,:]) . W_z[h] for H <= 32 heads, C = 128, B*N*N a
+// multiple of 32 (single.hip: the single-track pair-bias kernel).
+int pf_pair_logits(const float* z, const float* lnw, const float* lnb, const void* wz, float* out, int B, int N,
+                   int H, float eps, hipStream_t st);

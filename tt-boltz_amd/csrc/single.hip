@@ -223,6 +223,14 @@ float* pf_apb_bias_ptr(const pf_apb_args* a) {
   return (float*)a->workspace + 5 * (size_t)a->B * a->N * a->c_s;
 }
 
+int pf_pair_logits(const float* z, const float* lnw, const float* lnb, const void* wz, float* out, int B, int N,
+                   int H, float eps, hipStream_t st) {
+  const long pairs = (long)B * N * N;
+  apb_zbias_kernel<<<(unsigned)((pairs / 32 + 3) / 4), 256, 0, st>>>(z, lnw, lnb, (const op_t*)wz, out, B, N, H, eps);
+  PF_CHECK_LAUNCH("apb_zbias_kernel");
+  return PF_OK;
+}
+
 extern "C" int pf_apb_pair_bias(const pf_apb_args* a) {
   int rc = pf_apb_check(a, "pf_apb_pair_bias", true);
   if (rc) return rc;

@@ -460,3 +460,23 @@ def launch_opm(m: torch.Tensor, msa_mask: Optional[torch.Tensor], z: torch.Tenso
         w_o=_ptr(w["proj_o.weight"]), b_o=_ptr(w["proj_o.bias"]),
         workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
     _lib.check(_lib.load(variant).pf_opm_fwd(ctypes.byref(a)), "pf_opm_fwd", variant)
+
+
+def pwa_workspace_bytes(B: int, S: int, N: int, variant: str = DEFAULT_VARIANT) -> int:
+    return _lib.load(variant).pf_pwa_workspace_size(B, S, N)
+
+
+def launch_pwa(m: torch.Tensor, z: torch.Tensor, pair_mask: Optional[torch.Tensor], out: torch.Tensor,
+               w: Mapping[str, torch.Tensor], ws: torch.Tensor, accumulate: bool = True, eps: float = 1e-5,
+               variant: str = DEFAULT_VARIANT) -> None:
+    """out = (m if accumulate) + PairWeightedAveraging(m, z, pair_mask) (pf_pwa_fwd)."""
+    B, S, N, c_m = m.shape
+    H = w["proj_z.weight"].shape[0]
+    a = _lib.PwaArgs(
+        B=B, S=S, N=N, c_m=c_m, C=z.shape[-1], H=H, c_h=w["proj_m.weight"].shape[0] // H,
+        accumulate=int(accumulate), eps=eps, m=_ptr(m), out=_ptr(out), z=_ptr(z), pair_mask=_ptr(pair_mask),
+        norm_m_w=_ptr(w["norm_m.weight"]), norm_m_b=_ptr(w["norm_m.bias"]), norm_z_w=_ptr(w["norm_z.weight"]),
+        norm_z_b=_ptr(w["norm_z.bias"]), w_m=_ptr(w["proj_m.weight"]), w_g=_ptr(w["proj_g.weight"]),
+        w_z=_ptr(w["proj_z.weight"]), w_o=_ptr(w["proj_o.weight"]),
+        workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
+    _lib.check(_lib.load(variant).pf_pwa_fwd(ctypes.byref(a)), "pf_pwa_fwd", variant)
