@@ -319,6 +319,16 @@ typedef struct pf_pwa_args {
 size_t pf_pwa_workspace_size(int B, int S, int N);
 int pf_pwa_fwd(const pf_pwa_args* args);
 
+/* MSA input embedding (MSAModule.forward, tt_bio/reference.py:1253-1276, with
+ * use_paired_feature): m[b,s,i,:] = msa_proj([one_hot(msa), has_deletion, deletion_value,
+ * is_paired]) + s_emb[b,i,:], as a column gather.  msa int32 [B][S][N] token ids
+ * (clamped to [0, n_tok)); the three features fp32 [B][S][N] or NULL (zero); s_emb fp32
+ * [B][N][c_m] (= s_proj(emb), e.g. by pf_linear_fwd); w_t fp32 [n_tok + 3][c_m] = msa_proj.weight
+ * transposed; m fp32 [B][S][N][c_m].  c_m = 64. */
+int pf_msa_embed(const int* msa, const float* has_deletion, const float* deletion_value, const float* msa_paired,
+                 const float* s_emb, const float* w_t, float* m, int B, int S, int N, int c_m, int n_tok,
+                 void* stream);
+
 /* Batched NT product X[p][i][j] = scale * sum_k A[p][i][k] * B[p][j][k] on the MFMA
  * contraction kernel: A [planes][M][K], B [planes][Nc][K] in the operand type, X
  * [planes][M][Nc] fp32 (x_fp32 = 1) or operand type; M, Nc multiples of 32, K a multiple of

@@ -410,3 +410,35 @@ def test_pair_weighted_averaging(gpu, S, N):
     ws = ops.workspace(ops.pwa_workspace_bytes(1, S, N), gpu)
     ops.launch_pwa(md, z.to(gpu).contiguous(), pm.to(gpu).contiguous(), md, wd, ws)
     check(f"pair weighted averaging S={S} N={N} (valid tokens)", md[:, :, : N - 7], want[:, :, : N - 7])
+
+
+def _msa_feats(S, N, seed, pad_tail=0):
+    g = torch.Generator().manual_seed(seed)
+    tok = torch.ones((1, N))
+    if pad_tail:
+        tok[:, N - pad_tail:] = 0
+    return {"msa": torch.randint(0, msa_ref.NUM_TOKENS, (1, S, N), generator=g),
+            "has_deletion": (torch.rand((1, S, N), generator=g) > 0.8).float(),
+            "deletion_value": torch.rand((1, S, N), generator=g),
+            "msa_paired": (torch.rand((1, S, N), generator=g) > 0.5).float(),
+            "msa_mask": (torch.rand((1, S, N), generator=g) > 0.1).float() * tok[:, None, :],
+            "token_pad_mask": tok}
+
+
+def test_msa_module_dropin(gpu):
+    """MSAModule drop-in (2 blocks) on CPU tensors: N = 50 padded to 64 inside, 20 MSA rows,
+    a masked token tail and random sequence masks, vs the fp32 oracle (valid tokens)."""
+    from tt_boltz_amd import msa as msa_mod
+    N, S, nb = 50, 20, 2
+    w = synthetic.draw(synthetic.msa_module_shapes(nb), 81)
+    g = torch.Generator().manual_seed(82)
+    z = torch.randn((1, N, N, 128), generator=g)
+    emb = torch.randn((1, N, 384), generator=g)
+    feats = _msa_feats(S, N, 83, pad_tail=6)
+    want = msa_ref.msa_module(z, emb, feats, w, nb)
+    mod = msa_mod.MSAModule(nb, 32, 8, 32, 4)
+    mod.load_state_dict(w)
+    got = mod(z, emb, feats)
+    assert got.device.type == "cpu" and got.shape == z.shape
+    v = N - 6
+    check("MSA module 2 blocks (valid tokens)", got[:, :v, :v], want[:, :v, :v])

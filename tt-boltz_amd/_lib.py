@@ -131,6 +131,8 @@ SIGNATURES = {
     "pf_opm_fwd": (c_int, [ctypes.POINTER(OpmArgs)]),
     "pf_pwa_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "pf_pwa_fwd": (c_int, [ctypes.POINTER(PwaArgs)]),
+    "pf_msa_embed": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                             c_int, c_int, c_int, c_void_p]),
     "pf_batched_nt_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_float,
                                    c_void_p]),
     "pf_layernorm_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_float, c_void_p]),

@@ -354,6 +354,36 @@ __global__ __launch_bounds__(512) void pwa_out_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------------
+// MSA input embedding (MSAModule.forward, tt_bio/reference.py:1253-1276):
+//   m[b,s,i,:] = W[:, msa[b,s,i]] + has_del W[:,T] + del_val W[:,T+1] + paired W[:,T+2]
+//                + s_emb[b,i,:]
+// the one-hot product as a column gather; one thread per 4 channels.
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void msa_embed_kernel(
+    const int* __restrict__ msa, const float* __restrict__ has_del, const float* __restrict__ del_val,
+    const float* __restrict__ paired, const float* __restrict__ s_emb, const float* __restrict__ wt,
+    float* __restrict__ m, long rows, int S, int N, int n_tok) {
+  const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= rows * (CM / 4)) return;
+  const long r = t / (CM / 4);
+  const int c0 = 4 * (int)(t - r * (CM / 4));
+  const int i = (int)(r % N);
+  const long b = r / ((long)S * N);
+  const int tok = min(max(msa[r], 0), n_tok - 1);
+  const float f0 = has_del ? has_del[r] : 0.f, f1 = del_val ? del_val[r] : 0.f, f2 = paired ? paired[r] : 0.f;
+  // wt is the transposed projection [n_tok + 3][CM]: one row per input feature
+  const f32x4 e = *reinterpret_cast<const f32x4*>(s_emb + (b * N + i) * CM + c0);
+  const f32x4 w0 = *reinterpret_cast<const f32x4*>(wt + (long)tok * CM + c0);
+  const f32x4 w1 = *reinterpret_cast<const f32x4*>(wt + (long)n_tok * CM + c0);
+  const f32x4 w2 = *reinterpret_cast<const f32x4*>(wt + (long)(n_tok + 1) * CM + c0);
+  const f32x4 w3 = *reinterpret_cast<const f32x4*>(wt + (long)(n_tok + 2) * CM + c0);
+  f32x4 v;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = w0[k] + f0 * w1[k] + f1 * w2[k] + f2 * w3[k] + e[k];
+  *reinterpret_cast<f32x4*>(m + r * CM + c0) = v;
+}
+
 }  // namespace
 
 // Workspace of pf_opm_fwd: At, Bt [B][32N][S'], mask [B][N][S'], Z [B][32N][32N] (op_t),
@@ -449,5 +479,20 @@ extern "C" int pf_pwa_fwd(const pf_pwa_args* a) {
                                                           (const op_t*)a->w_g, (const op_t*)a->w_o, O, B, S, N,
                                                           a->accumulate, a->eps);
   PF_CHECK_LAUNCH("pwa_out_kernel");
+  return PF_OK;
+}
+
+extern "C" int pf_msa_embed(const int* msa, const float* has_deletion, const float* deletion_value,
+                            const float* msa_paired, const float* s_emb, const float* w_t, float* m, int B, int S,
+                            int N, int c_m, int n_tok, void* stream) {
+  if (!msa || !s_emb || !w_t || !m) return pf_fail(PF_E_INVALID, "pf_msa_embed: null pointer");
+  if (c_m != CM || B <= 0 || S <= 0 || N <= 0 || n_tok <= 0)
+    return pf_fail(PF_E_INVALID, "pf_msa_embed: need c_m = 64 and positive B, S, N, n_tok (got %d %d %d %d %d)", c_m,
+                   B, S, N, n_tok);
+  const long rows = (long)B * S * N;
+  const long threads = rows * (CM / 4);
+  msa_embed_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      msa, has_deletion, deletion_value, msa_paired, s_emb, w_t, m, rows, S, N, n_tok);
+  PF_CHECK_LAUNCH("msa_embed_kernel");
   return PF_OK;
 }

@@ -480,3 +480,13 @@ def launch_pwa(m: torch.Tensor, z: torch.Tensor, pair_mask: Optional[torch.Tenso
         w_z=_ptr(w["proj_z.weight"]), w_o=_ptr(w["proj_o.weight"]),
         workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
     _lib.check(_lib.load(variant).pf_pwa_fwd(ctypes.byref(a)), "pf_pwa_fwd", variant)
+
+
+def launch_msa_embed(msa: torch.Tensor, has_deletion: Optional[torch.Tensor], deletion_value: Optional[torch.Tensor],
+                     msa_paired: Optional[torch.Tensor], s_emb: torch.Tensor, w_t: torch.Tensor, m: torch.Tensor,
+                     variant: str = DEFAULT_VARIANT) -> None:
+    """m = msa_proj(one_hot features) + s_emb (pf_msa_embed); msa int32 [B,S,N]."""
+    B, S, N = msa.shape
+    _lib.check(_lib.load(variant).pf_msa_embed(_ptr(msa), _ptr(has_deletion), _ptr(deletion_value), _ptr(msa_paired),
+                                               _ptr(s_emb), _ptr(w_t), _ptr(m), B, S, N, m.shape[-1],
+                                               w_t.shape[0] - 3, _stream()), "pf_msa_embed", variant)
