@@ -176,6 +176,39 @@ def stack_bench(N: int = 768, n_layers: int = 64, recycling_steps: int = 3, seed
                         "masks all ones, 4 recycling passes, fp32 residual stream"}
 
 
+def msa_bench(N: int = 512, S: int = 1024, seed: int = 5, steps: int = 3) -> dict:
+    """One MSA layer of the Boltz-2 MSA module (the next row after the Pairformer): pair
+    weighted averaging, MSA transition, outer product mean and the no-seq PairformerLayer,
+    at N tokens and S MSA rows, masks all ones; each op timed alone and the layer."""
+    import torch
+    from tt_boltz_amd import msa as msa_mod, ops, pairformer, synthetic
+    dev = pairformer.get_device()
+    stream = torch.cuda.current_stream()
+    w = synthetic.draw(synthetic.msa_layer_shapes(), seed)
+    layer = msa_mod.MSALayer(32, 8, 32, 4, w)
+    g = torch.Generator().manual_seed(seed)
+    z = torch.randn((1, N, N, 128), generator=g).to(dev).contiguous()
+    m = torch.randn((1, S, N, 64), generator=g).to(dev).contiguous()
+    ws = ops.workspace(layer.workspace_bytes(1, S, N), dev)
+    ms = {
+        "pair_weighted_averaging": time_events(lambda: layer.pair_weighted_averaging(m, z, None, ws), steps, stream),
+        "msa_transition": time_events(lambda: layer.msa_transition(m, out=m, accumulate=True, ws=ws), steps, stream),
+        "outer_product_mean": time_events(lambda: layer.outer_product_mean(m, None, z, ws), steps, stream),
+        "pairformer_noseq_layer": time_events(lambda: layer.pairformer_layer(None, z, None, None, ws), steps, stream),
+        "layer": time_events(lambda: layer(z, m, None, None, ws), steps, stream),
+    }
+    opm_fl = 2 * (32 * N) ** 2 * S + 2 * N * N * 1024 * 128
+    pwa_fl = 2 * N * N * S * 256
+    return {"N": N, "S": S, "seed": seed, "layer_ms": round(ms["layer"], 3),
+            "layers_per_s": round(1000.0 / ms["layer"], 2),
+            "ops_ms": {k: round(v, 3) for k, v in ms.items() if k != "layer"},
+            "outer_product_mean_tflops": round(opm_fl / (ms["outer_product_mean"] * 1e-3) / 1e12, 1),
+            "pair_weighted_averaging_tflops": round(pwa_fl / (ms["pair_weighted_averaging"] * 1e-3) / 1e12, 1),
+            "finite": bool(torch.isfinite(z).all() and torch.isfinite(m).all()),
+            "workload": f"one Boltz-2 MSALayer, N={N} tokens, S={S} MSA rows, c_m=64, PWA 8x32, OPM hidden 32, "
+                        "masks all ones, seed 5 weights"}
+
+
 def fast_bench(N: int = 1024, seed: int = 4, steps: int = 5) -> dict:
     """Config 4: one layer in fast mode (MXFP8 triangle multiplications and pair
     transition) at N=1024 next to the same layer in 16-bit, plus the fp8 contraction alone."""
@@ -380,6 +413,8 @@ def main() -> int:
         out["stack"] = stack_bench()
         torch.cuda.empty_cache()
         out["fast"] = fast_bench()
+        torch.cuda.empty_cache()
+        out["msa"] = msa_bench()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(N, seed)
     print(json.dumps(out), flush=True)

@@ -375,6 +375,23 @@ def _msa_sub(seed, prefix, c_m=64, c_z=128):
     return ref.sub(synthetic.draw({k: v for k, v in shapes.items() if k.startswith(prefix + ".")}, seed), prefix)
 
 
+def test_transition_msa(gpu):
+    """C = 64 / hidden = 256 (the MSA transition's persistent fused kernel): a row count that
+    is not a multiple of the 32-row tile, then in place with accumulate (m += Tr(m))."""
+    w = _msa_sub(72, "msa_transition")
+    g = torch.Generator().manual_seed(72)
+    m = torch.randn((3, 37, 41, 64), generator=g)
+    want = ref.transition(m, w)
+    got = ops.transition(m.to(gpu), w["norm.weight"], w["norm.bias"], w["fc1.weight"], w["fc2.weight"],
+                         w["fc3.weight"])
+    check("transition msa", got, want)
+    wd = ops.convert_weights(w, gpu)
+    x = m.to(gpu).contiguous()
+    assert ops.transition_workspace_bytes(x.numel() // 64, 64, 256) == 0
+    ops.launch_transition(x, x, wd, None, accumulate=True)
+    check("transition msa in place", x, m + want)
+
+
 @pytest.mark.parametrize("S,N", [(40, 64), (130, 96)])
 def test_outer_product_mean(gpu, S, N):
     """pf_opm_fwd vs the fp32 oracle: S padded to 64 inside, random sequence mask (with a

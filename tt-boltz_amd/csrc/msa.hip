@@ -95,7 +95,6 @@ __global__ __launch_bounds__(256) void opm_proj_kernel(
 // output-aligned 16-byte residual update of the pair transition.
 // ---------------------------------------------------------------------------------
 constexpr int OPM_CHUNK_BYTES = CZ * 64 * 2;   // 16 KB
-PF_DEV int swz8r(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 
 __global__ __launch_bounds__(256, 2) void opm_out_kernel(
     const op_t* __restrict__ Z, const float* __restrict__ cnt, const op_t* __restrict__ wo,
@@ -211,38 +210,6 @@ __global__ __launch_bounds__(256) void pwa_softmax_kernel(const float* __restric
   const float inv = 1.f / wave_sum(sm);
   op_t* w = Wt + row * N;
   for (int j = lane; j < N; j += 64) w[j] = (op_t)(exp2_fast(val(j) - mx) * inv);
-}
-
-// LN over the 64 channels of a row held as channels 16 st + 8 h + t (st = 0..3) by lane
-// half h, as 4 MFMA fragments.
-PF_DEV void ln64_to_frag(const float* __restrict__ row, int h, const float* __restrict__ w,
-                         const float* __restrict__ b, float eps, opx8 (&f)[4]) {
-  float x[32];
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    const f32x4 u = *reinterpret_cast<const f32x4*>(row + 16 * st + 8 * h);
-    const f32x4 v = *reinterpret_cast<const f32x4*>(row + 16 * st + 8 * h + 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      x[8 * st + e] = u[e];
-      x[8 * st + 4 + e] = v[e];
-    }
-  }
-  float sm = 0.f;
-#pragma unroll
-  for (int k = 0; k < 32; ++k) sm += x[k];
-  const float mean = xor32_sum(sm) * (1.f / CM);
-  float var = 0.f;
-#pragma unroll
-  for (int k = 0; k < 32; ++k) { const float d = x[k] - mean; var += d * d; }
-  const float rstd = rsqrtf(xor32_sum(var) * (1.f / CM) + eps);
-#pragma unroll
-  for (int st = 0; st < 4; ++st)
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int c = 16 * st + 8 * h + t;
-      f[st][t] = (op_t)((x[8 * st + t] - mean) * rstd * w[c] + b[c]);
-    }
 }
 
 // v projection: a wave takes 32 consecutive tokens j of one (b, s); W_m [256][64] sits in

@@ -164,6 +164,42 @@ PF_DEV void ln128_to_frag(const float (&x)[64], int h, const float* __restrict__
   }
 }
 
+// 16-byte-chunk XOR swizzle for LDS rows of 64 op_t (128 bytes): the 32 rows one
+// MFMA operand read touches at one chunk index land on distinct bank groups.
+PF_DEV int swz8r(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+
+// LN over the 64 channels of a row held as channels 16 st + 8 h + t (st = 0..3) by lane
+// half h, as 4 MFMA fragments.
+PF_DEV void ln64_to_frag(const float* __restrict__ row, int h, const float* __restrict__ w,
+                         const float* __restrict__ b, float eps, opx8 (&f)[4]) {
+  float x[32];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const f32x4 u = *reinterpret_cast<const f32x4*>(row + 16 * st + 8 * h);
+    const f32x4 v = *reinterpret_cast<const f32x4*>(row + 16 * st + 8 * h + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[8 * st + e] = u[e];
+      x[8 * st + 4 + e] = v[e];
+    }
+  }
+  float sm = 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) sm += x[k];
+  const float mean = xor32_sum(sm) * (1.f / 64.f);
+  float var = 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) { const float d = x[k] - mean; var += d * d; }
+  const float rstd = rsqrtf(xor32_sum(var) * (1.f / 64.f) + eps);
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int c = 16 * st + 8 * h + t;
+      f[st][t] = (op_t)((x[8 * st + t] - mean) * rstd * w[c] + b[c]);
+    }
+}
+
 // s_waitcnt immediate (gfx9 encoding) that waits until at most v vector-memory
 // operations of this wave are outstanding and leaves expcnt / lgkmcnt unconstrained.
 constexpr int vmcnt_le(int v) { return (v & 0xF) | (((v >> 4) & 3) << 14) | 0x70 | 0xF00; }

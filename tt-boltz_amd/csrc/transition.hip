@@ -198,6 +198,84 @@ __global__ __launch_bounds__(64 * TRW, 3) void tr_pair_kernel(
   }
 }
 
+// Transition with C = 64, hidden = 256 (the MSA transition, tt_bio/reference.py:1333,
+// boltz2.py:1188-1258), fused like the pair transition.  Persistent: one workgroup of
+// 8 waves per CU keeps fc1, fc2 ([256][64]) and fc3 ([64][256]) in LDS (96 KB); a wave
+// walks tiles of 32 rows: LN -> fc1|fc2 as D[hidden][row] (rows of fc1/fc2 in perm16
+// order within each 32-block, so the accumulators come out in fc3's k order) ->
+// silu(a)*b -> fc3 as D[channel][row] -> residual in the output-aligned layout.
+// LDS rows are unpadded with XOR-swizzled 16-byte chunks (conflict-free fragment reads).
+constexpr int T64_WAVES = 8;
+
+__global__ __launch_bounds__(64 * T64_WAVES, 1) void tr64_kernel(
+    const float* x_in, float* out, const float* __restrict__ lnw, const float* __restrict__ lnb,
+    const op_t* __restrict__ w1, const op_t* __restrict__ w2, const op_t* __restrict__ w3, long rows,
+    int accumulate, float eps) {
+  __shared__ __attribute__((aligned(16))) op_t s1[256 * 64];
+  __shared__ __attribute__((aligned(16))) op_t s2[256 * 64];
+  __shared__ __attribute__((aligned(16))) op_t s3[64 * 256];
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int c = tid; c < 256 * 8; c += 64 * T64_WAVES) {   // fc1 / fc2: 256 rows of 8 chunks
+    const int R = c >> 3, k = c & 7;
+    const int src = (32 * (R >> 5) + perm16(R & 31)) * 64 + 8 * k;
+    const int dst = R * 64 + 8 * (k ^ swz8r(R));
+    st_x8(s1 + dst, ld_x8(w1 + src));
+    st_x8(s2 + dst, ld_x8(w2 + src));
+  }
+  for (int c = tid; c < 64 * 32; c += 64 * T64_WAVES) {   // fc3: 64 rows of 32 chunks
+    const int R = c >> 5, k = c & 31;
+    st_x8(s3 + R * 256 + 8 * (k ^ (R & 15)), ld_x8(w3 + R * 256 + 8 * k));
+  }
+  __syncthreads();
+  const int sw = swz8r(m);
+  const long ntiles = (rows + 31) / 32;
+  for (long t = (long)blockIdx.x * T64_WAVES + wid; t < ntiles; t += (long)gridDim.x * T64_WAVES) {
+    const long r0 = 32 * t;
+    const long row = min(r0 + m, rows - 1);
+    opx8 xf[4];
+    ln64_to_frag(x_in + row * 64, h, lnw, lnb, eps, xf);
+    f32x16 acc[2] = {zero16(), zero16()};
+#pragma unroll 1
+    for (int blk = 0; blk < 8; ++blk) {
+      f32x16 a1 = zero16(), a2 = zero16();
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int off = (32 * blk + m) * 64 + 8 * ((2 * st + h) ^ sw);
+        a1 = mfma32(ld_x8(s1 + off), xf[st], a1);   // rows = hidden (perm16), cols = row
+        a2 = mfma32(ld_x8(s2 + off), xf[st], a2);
+      }
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp) {
+        opx8 hf;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) hf[u] = (op_t)(siluf(a1[8 * sp + u]) * a2[8 * sp + u]);
+        const int kc = 2 * (2 * blk + sp) + h;   // fc3 row chunk: hidden 32 blk + 16 sp + 8 h
+#pragma unroll
+        for (int ob = 0; ob < 2; ++ob) {
+          const int R = 32 * ob + m;
+          acc[ob] = mfma32(ld_x8(s3 + R * 256 + 8 * (kc ^ (R & 15))), hf, acc[ob]);   // rows = channel
+        }
+      }
+    }
+    if (r0 + m >= rows) continue;
+    // lane (row m, h): acc[ob][4 g + e] is channel 32 ob + 8 g + 4 h + e; x_in may alias out
+    const float* src = x_in + (r0 + m) * 64;
+    float* dst = out + (r0 + m) * 64;
+    f32x4 res[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      res[q] = accumulate ? *reinterpret_cast<const f32x4*>(src + oa_channel(q, h)) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      f32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = acc[q >> 2][4 * (q & 3) + e] + res[q][e];
+      *reinterpret_cast<f32x4*>(dst + oa_channel(q, h)) = v;
+    }
+  }
+}
+
 // One wave per row.
 __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                       const float* __restrict__ b, float* __restrict__ out,
@@ -378,6 +456,7 @@ extern "C" int pf_linear_fwd(const float* x, const void* W, const float* bias, c
 extern "C" size_t pf_transition_workspace_size(long rows, int C_, int hidden) {
   if (rows <= 0 || C_ <= 0 || hidden <= 0) return 0;
   if (C_ == C && hidden % 32 == 0) return 0;   // fused pair kernel: no scratch
+  if (C_ == 64 && hidden == 256) return 0;      // fused C = 64 kernel: no scratch
   return (size_t)rows * (C_ + hidden) * sizeof(float);
 }
 
@@ -395,6 +474,17 @@ extern "C" int pf_transition_fwd(const pf_transition_args* a) {
                                                      (const op_t*)a->fc2_w, (const op_t*)a->fc3_w, a->rows,
                                                      a->hidden, a->accumulate, a->eps, ZBiasArgs{});
     PF_CHECK_LAUNCH("tr_pair_kernel");
+    return PF_OK;
+  }
+  if (a->C == 64 && a->hidden == 256) {
+    const int cus = device_cus();
+    if (cus <= 0) return pf_fail(PF_E_LAUNCH, "tr64_kernel: cannot query the device");
+    const long tiles = (a->rows + 31) / 32;
+    const int grid = (int)min((long)cus, (tiles + T64_WAVES - 1) / T64_WAVES);
+    tr64_kernel<<<grid, 64 * T64_WAVES, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w,
+                                                 (const op_t*)a->fc2_w, (const op_t*)a->fc3_w, a->rows,
+                                                 a->accumulate, a->eps);
+    PF_CHECK_LAUNCH("tr64_kernel");
     return PF_OK;
   }
   const size_t need = pf_transition_workspace_size(a->rows, a->C, a->hidden);
