@@ -357,6 +357,11 @@ int pf_linear_fwd(const float* x, const void* W, const float* bias, const float*
 int pf_pair_ln_linear_fwd(const float* x, const float* base, const float* ln_w, const float* ln_b,
                           const void* W, float* out, long rows, int C, float eps, void* stream);
 
+/* Residual hand-off of the trunk loop (tt_bio/boltz2.py:5221, 5230:
+ *   z = z + template_module(z, ...), z = z + msa_module(z, ...)):
+ *   out[i] = a[i] + b[i], fp32, 16-byte aligned pointers; out may alias a or b. */
+int pf_add_fwd(const float* a, const float* b, float* out, long n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -274,11 +274,12 @@ def pairformer_stack(s: Optional[Tensor], z: Tensor, mask: Optional[Tensor], pai
 
 
 def recycle(s_init: Tensor, z_init: Tensor, mask: Tensor, w_stack: Weights, w_rec: Weights,
-            n_blocks: int, recycling_steps: int, **kw):
-    """Trunk recycling loop of ``Boltz2.forward`` (``boltz2.py:5189-5248``) with
-    the template and MSA modules absent: s, z start at zero; each of the
-    ``recycling_steps + 1`` passes does s = s_init + s_recycle(s_norm(s)),
-    z = z_init + z_recycle(z_norm(z)), then the Pairformer stack.
+            n_blocks: int, recycling_steps: int, msa=None, **kw):
+    """Trunk recycling loop of ``Boltz2.forward`` (``boltz2.py:5189-5248``) without the
+    template module: s, z start at zero; each of the ``recycling_steps + 1`` passes does
+    s = s_init + s_recycle(s_norm(s)), z = z_init + z_recycle(z_norm(z)) (5213-5214), with
+    ``msa = (w_msa, emb, feats, msa_blocks)`` z = z + msa_module(z, emb, feats) (5230), then
+    the Pairformer stack (5239-5245).
 
     ``w_rec`` keys: ``s_norm.*``, ``z_norm.*``, ``s_recycle.weight``, ``z_recycle.weight``.
     """
@@ -290,5 +291,9 @@ def recycle(s_init: Tensor, z_init: Tensor, mask: Tensor, w_stack: Weights, w_re
                             w_rec["s_recycle.weight"])
         z = z_init + linear(layer_norm(z, w_rec["z_norm.weight"], w_rec["z_norm.bias"]),
                             w_rec["z_recycle.weight"])
+        if msa is not None:
+            from .msa_ref import msa_module
+            w_msa, emb, feats, msa_blocks = msa
+            z = z + msa_module(z, emb, feats, w_msa, msa_blocks)
         s, z = pairformer_stack(s, z, mask, pair_mask, w_stack, n_blocks, **kw)
     return s, z

@@ -278,6 +278,29 @@ def test_recycler(gpu):
     check("recycler s", s_got, s_ref)
 
 
+def test_recycler_msa(gpu):
+    """Recycling loop with the MSA hand-off on the device (z = z + MSA(z) before the stack,
+    boltz2.py:5203-5245): 2 passes, 1 MSA block, 1 Pairformer block, N = 64, 24 MSA rows."""
+    from tt_boltz_amd import msa as msa_mod
+    N, S = 64, 24
+    w = synthetic.stack_weights(1, 29)
+    w_rec = synthetic.draw(synthetic.recycle_shapes(), 30)
+    w_msa = synthetic.draw(synthetic.msa_module_shapes(1), 31)
+    s_init, z_init, mask, _ = _inputs(N, 32)
+    emb = torch.randn((1, N, 384), generator=torch.Generator().manual_seed(33))
+    feats = _msa_feats(S, N, 34)
+    feats["token_pad_mask"] = mask
+    feats["msa_mask"] = feats["msa_mask"] * mask[:, None, :]
+    s_ref, z_ref = ref.recycle(s_init, z_init, mask, w, w_rec, 1, 1, msa=(w_msa, emb, feats, 1))
+    pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, w)
+    msa_dev = msa_mod.MSA(1, 32, 8, 32, 4, w_msa)
+    rec = pairformer.TrunkRecycler(pf, w_rec, msa=msa_dev)
+    inputs = msa_mod.device_inputs(emb, feats, N, gpu)
+    s_got, z_got = rec(s_init.to(gpu), z_init.to(gpu), mask.to(gpu), 1, msa_inputs=inputs)
+    check("recycler+MSA z", z_got, z_ref)
+    check("recycler+MSA s", s_got, s_ref)
+
+
 def test_single_track_overlap_identical(gpu):
     """The single track on a second stream (overlapped with the next layer's pair
     operations) gives bit-identical s and z to the same stack run in reference order on

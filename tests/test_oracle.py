@@ -264,6 +264,33 @@ def test_recycle_zero_passes_is_one_stack_call():
     _close(s_r, s_e, 1e-6)
 
 
+def test_recycle_msa_handoff_adds_the_returned_pair():
+    """The MSA hand-off is z = z + msa_module(z) and the module returns the full updated z
+    (boltz2.py:5230): with zero MSA blocks the module returns z itself, so one pass equals
+    the stack on 2 (z_init + W b_norm)."""
+    N, S = 4, 3
+    g = torch.Generator().manual_seed(35)
+    s_init = torch.randn((1, N, 8), generator=g)
+    z_init = torch.randn((1, N, N, 8), generator=g)
+    mask = torch.ones((1, N))
+    w_stack = synthetic.draw({f"layers.0.{k}": v for k, v in synthetic.layer_shapes(
+        c_z=8, c_s=8, tri_heads=2, tri_dim=4, att_heads=2).items()}, 36)
+    w_rec = synthetic.draw(synthetic.recycle_shapes(c_z=8, c_s=8), 37)
+    w_msa = synthetic.draw(synthetic.msa_module_shapes(0, c_m=8, c_z=8, c_s=8), 38)
+    feats = {"msa": torch.randint(0, msa_ref.NUM_TOKENS, (1, S, N), generator=g),
+             "has_deletion": torch.zeros((1, S, N)), "deletion_value": torch.zeros((1, S, N)),
+             "msa_paired": torch.zeros((1, S, N)), "msa_mask": torch.ones((1, S, N)), "token_pad_mask": mask}
+    emb = torch.randn((1, N, 8), generator=g)
+    kw = dict(tri_att_heads=2, tri_att_head_dim=4, att_heads=2)
+    s_r, z_r = ref.recycle(s_init, z_init, mask, w_stack, w_rec, 1, 0, msa=(w_msa, emb, feats, 0), **kw)
+    s0 = s_init + w_rec["s_norm.bias"] @ w_rec["s_recycle.weight"].T
+    z0 = z_init + w_rec["z_norm.bias"] @ w_rec["z_recycle.weight"].T
+    pm = mask[:, :, None] * mask[:, None, :]
+    s_e, z_e = ref.pairformer_layer(s0, 2 * z0, mask, pm, ref.sub(w_stack, "layers.0"), 512, 2, 4, 2)
+    _close(z_r, z_e, 1e-6)
+    _close(s_r, s_e, 1e-6)
+
+
 # ----------------------------------------------------------------------------- fp8 emulator
 def test_e4m3_rounding_matches_torch_cast():
     g = torch.Generator().manual_seed(34)

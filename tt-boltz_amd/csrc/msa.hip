@@ -351,6 +351,49 @@ __global__ __launch_bounds__(256) void msa_embed_kernel(
   *reinterpret_cast<f32x4*>(m + r * CM + c0) = v;
 }
 
+// Per-pair mask counts cnt[b][i][j] = sum_s mask[s,i] mask[s,j] (reference.py:645-646)
+// from the k-major mask Mt [B][N][S'] (0/1 values, exact in fp32).  One workgroup per
+// 32x32 tile, D[i][j]; its 4 waves take interleaved 64-sequence slices (16-byte operand
+// loads straight from global, 4 k-steps in flight) and add their partial tiles in LDS.
+__global__ __launch_bounds__(256) void opm_count_kernel(const op_t* __restrict__ Mt, float* __restrict__ cnt,
+                                                        int B, int N, int Sp) {
+  __shared__ f32x4 part[3][4][64];
+  const int lane = threadIdx.x & 63, h = lane >> 5, mm = lane & 31;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nt = N / 32;
+  const long t = blockIdx.x;
+  const int tj = (int)(t % nt), ti = (int)((t / nt) % nt), b = (int)(t / ((long)nt * nt));
+  const op_t* ra = Mt + ((long)b * N + 32 * ti + mm) * Sp + 8 * h;
+  const op_t* rb = Mt + ((long)b * N + 32 * tj + mm) * Sp + 8 * h;
+  f32x16 acc = zero16();
+  for (int k0 = 64 * wid; k0 < Sp; k0 += 256) {
+    opx8 fa[4], fb[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      fa[u] = ld_x8(ra + k0 + 16 * u);
+      fb[u] = ld_x8(rb + k0 + 16 * u);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc = mfma32(fa[u], fb[u], acc);
+  }
+  if (wid > 0)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) part[wid - 1][g][lane] = f32x4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
+  __syncthreads();
+  if (wid > 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 p = part[w][g][lane];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[4 * g + e] += p[e];
+    }
+  float* out = cnt + ((long)b * N + 32 * ti) * N + 32 * tj + mm;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) out[(long)acc_row(r, h) * N] = acc[r];
+}
+
 }  // namespace
 
 // Workspace of pf_opm_fwd: At, Bt [B][32N][S'], mask [B][N][S'], Z [B][32N][32N] (op_t),
@@ -392,7 +435,8 @@ extern "C" int pf_opm_fwd(const pf_opm_args* a) {
   PF_CHECK_LAUNCH("opm_proj_kernel");
   int rc = pf_contract_rect(At, Bt, Z, 0, B, N * CH, N * CH, Sp, X_STORE_SCALE, st);
   if (rc) return rc;
-  if ((rc = pf_contract_rect(Mt, Mt, cnt, 1, B, N, N, Sp, 1.f, st))) return rc;
+  opm_count_kernel<<<(unsigned)((long)B * (N / 32) * (N / 32)), 256, 0, st>>>(Mt, cnt, B, N, Sp);
+  PF_CHECK_LAUNCH("opm_count_kernel");
   const long pairs = (long)B * N * N;
   opm_out_kernel<<<(unsigned)((pairs / 32 + 3) / 4), 256, 0, st>>>(Z, cnt, (const op_t*)a->w_o, a->b_o, a->z, B, N,
                                                                   X_LOAD_SCALE, a->accumulate);

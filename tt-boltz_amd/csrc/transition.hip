@@ -510,6 +510,28 @@ extern "C" int pf_pair_ln_linear_fwd(const float* x, const float* base, const fl
   return PF_OK;
 }
 
+__global__ __launch_bounds__(256) void add_kernel(const float* a, const float* b, float* out, long n) {
+  const long n4 = n / 4, stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    const f32x4 u = reinterpret_cast<const f32x4*>(a)[i], v = reinterpret_cast<const f32x4*>(b)[i];
+    reinterpret_cast<f32x4*>(out)[i] = u + v;
+  }
+  for (long i = 4 * n4 + (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = a[i] + b[i];
+}
+
+extern "C" int pf_add_fwd(const float* a, const float* b, float* out, long n, void* stream) {
+  if (!a || !b || !out) return pf_fail(PF_E_INVALID, "pf_add_fwd: null pointer");
+  if (n <= 0) return pf_fail(PF_E_INVALID, "pf_add_fwd: n = %ld", n);
+  if (((uintptr_t)a | (uintptr_t)b | (uintptr_t)out) & 15)
+    return pf_fail(PF_E_INVALID, "pf_add_fwd: pointers must be 16-byte aligned");
+  const int cus = device_cus();
+  if (cus <= 0) return pf_fail(PF_E_LAUNCH, "pf_add_fwd: cannot query the device");
+  const long blocks = min((long)cus * 8, (n / 4 + 255) / 256 + 1);
+  add_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(a, b, out, n);
+  PF_CHECK_LAUNCH("add_kernel");
+  return PF_OK;
+}
+
 extern "C" int pf_transition_pair_bias_fwd(const pf_transition_args* a, const pf_apb_args* apb) {
   if (!a || !apb) return pf_fail(PF_E_INVALID, "pf_transition_pair_bias_fwd: null args");
   if (a->C != C || a->hidden <= 0 || a->hidden % 32)

@@ -124,6 +124,25 @@ class MSA(Module):
         return z
 
 
+def device_inputs(emb: torch.Tensor, feats: Mapping[str, torch.Tensor], n_pad: int,
+                  device: torch.device) -> dict:
+    """The MSA features of ``feats`` and ``emb`` (``s_inputs``) zero-padded to ``n_pad`` tokens
+    on ``device``: the keyword arguments of ``MSA.__call__`` other than z, the pair mask and
+    ``n_valid``."""
+    B, S, N = feats["msa"].shape
+
+    def per_row(key, dtype):
+        t = torch.zeros((B, S, n_pad), dtype=dtype, device=device)
+        t[:, :, :N] = feats[key].to(device, dtype)
+        return t
+
+    emb_dev = torch.zeros((B, n_pad, emb.shape[-1]), dtype=torch.float32, device=device)
+    emb_dev[:, :N] = emb.to(device, torch.float32)
+    return {"emb": emb_dev, "msa": per_row("msa", torch.int32), "has_deletion": per_row("has_deletion", torch.float32),
+            "deletion_value": per_row("deletion_value", torch.float32),
+            "msa_paired": per_row("msa_paired", torch.float32), "msa_mask": per_row("msa_mask", torch.float32)}
+
+
 class MSAModule(nn.Module):
     """Drop-in for ``tenstorrent.MSAModule`` (``tenstorrent.py:2524-2621``) at
     ``boltz2.py:4993-5009``: ``forward(z, emb, feats) -> z_out`` (the caller adds it to z,
@@ -152,24 +171,11 @@ class MSAModule(nn.Module):
             raise RuntimeError("MSAModule has no weights: call load_state_dict() first")
         dev = get_device()
         B, N = z.shape[0], z.shape[1]
-        S = feats["msa"].shape[1]
         n_pad = ops.padded_len(N)
         z_dev = ops.pad_pair(z.to(dev, torch.float32), n_pad)
-        emb_dev = torch.zeros((B, n_pad, emb.shape[-1]), dtype=torch.float32, device=dev)
-        emb_dev[:, :N] = emb.to(dev, torch.float32)
-
-        def per_row(key, dtype):
-            t = torch.zeros((B, S, n_pad), dtype=dtype, device=dev)
-            t[:, :, :N] = feats[key].to(dev, dtype)
-            return t
-
-        msa = per_row("msa", torch.int32)
-        has_del = per_row("has_deletion", torch.float32)
-        del_val = per_row("deletion_value", torch.float32)
-        paired = per_row("msa_paired", torch.float32)
-        msa_mask = per_row("msa_mask", torch.float32)
+        inputs = device_inputs(emb, feats, n_pad, dev)
         tok = torch.zeros((B, n_pad), dtype=torch.float32, device=dev)
         tok[:, :N] = feats["token_pad_mask"].to(dev, torch.float32)
         pair_mask = (tok[:, :, None] * tok[:, None, :]).contiguous()
-        z_dev = self.module(z_dev, emb_dev, msa, has_del, del_val, paired, pair_mask, msa_mask, n_valid=N)
+        z_dev = self.module(z_dev, pair_mask=pair_mask, n_valid=N, **inputs)
         return z_dev[:, :N, :N].to(z.device)

@@ -217,6 +217,14 @@ def launch_pair_ln_linear(x: torch.Tensor, base: torch.Tensor, ln_w: torch.Tenso
                "pf_pair_ln_linear_fwd", variant)
 
 
+def launch_add(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, variant: str = DEFAULT_VARIANT) -> None:
+    """out = a + b (fp32, same element count): the ``z = z + module(z)`` hand-off of the trunk loop."""
+    if not (a.numel() == b.numel() == out.numel()):
+        raise ValueError(f"launch_add: element counts differ ({a.numel()}, {b.numel()}, {out.numel()})")
+    _lib.check(_lib.load(variant).pf_add_fwd(_ptr(a), _ptr(b), _ptr(out), a.numel(), _stream()), "pf_add_fwd",
+               variant)
+
+
 def launch_batched_nt_gemm(A: torch.Tensor, B: torch.Tensor, X: torch.Tensor, scale: float = 1.0,
                            variant: str = DEFAULT_VARIANT) -> None:
     """X[p] = scale * A[p] @ B[p]^T (pf_batched_nt_gemm): A [P,M,K], B [P,Nc,K] operand type,

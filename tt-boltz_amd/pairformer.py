@@ -514,14 +514,18 @@ class PairformerModule(nn.Module):
 
 class TrunkRecycler:
     """Device-resident trunk recycling loop of ``Boltz2.forward`` (``boltz2.py:5189-5248``)
-    with the template and MSA modules absent: s, z start at zero and each of the
-    ``recycling_steps + 1`` passes computes ``s = s_init + s_recycle(s_norm(s))``,
-    ``z = z_init + z_recycle(z_norm(z))`` (``boltz2.py:5213-5214``) and runs the
-    Pairformer stack, without leaving the GPU between passes."""
+    without the template module: s, z start at zero and each of the ``recycling_steps + 1``
+    passes computes ``s = s_init + s_recycle(s_norm(s))``, ``z = z_init + z_recycle(z_norm(z))``
+    (``boltz2.py:5213-5214``), with an MSA module ``z = z + msa(z, ...)`` (``boltz2.py:5230``),
+    and runs the Pairformer stack, without leaving the GPU between passes.
 
-    def __init__(self, pairformer: Pairformer, state_dict, options: Optional[Options] = None):
+    ``msa`` is a device ``MSA`` (``tt_boltz_amd.msa``); its padded inputs are passed to each
+    call as ``msa_inputs`` (``tt_boltz_amd.msa.device_inputs``)."""
+
+    def __init__(self, pairformer: Pairformer, state_dict, options: Optional[Options] = None, msa=None):
         w = WeightScope.wrap(state_dict)
         self.pairformer = pairformer
+        self.msa = msa
         self.options = options or pairformer.options
         v = self.options.operand
         dev = get_device()
@@ -531,8 +535,10 @@ class TrunkRecycler:
         self.z_rec = ops.opw(w["z_recycle.weight"], dev, v)
 
     def __call__(self, s_init: torch.Tensor, z_init: torch.Tensor, mask: Optional[torch.Tensor],
-                 recycling_steps: int, pass_hook=None, n_valid: int = 0):
+                 recycling_steps: int, pass_hook=None, n_valid: int = 0, msa_inputs: Optional[dict] = None):
         """Padded device tensors in (N % 64 == 0); returns device (s, z)."""
+        if (self.msa is None) != (msa_inputs is None):
+            raise ValueError("TrunkRecycler: msa_inputs must be given exactly when an MSA module is attached")
         B, N = z_init.shape[0], z_init.shape[1]
         v = self.options.operand
         dev = z_init.device
@@ -540,11 +546,16 @@ class TrunkRecycler:
         s = torch.zeros_like(s_init)
         z = torch.zeros_like(z_init)
         s_tmp = torch.empty_like(s_init)
+        z_msa = None if self.msa is None else torch.empty_like(z_init)
         ws = ops.workspace(self.pairformer.workspace_bytes(B, N), dev)
         for i in range(recycling_steps + 1):
             ops.launch_layernorm(s, self.s_norm_w, self.s_norm_b, s_tmp, self.options.eps, v)
             ops.launch_linear(s_tmp, self.s_rec, None, s_init, s, v)
             ops.launch_pair_ln_linear(z, z_init, self.z_norm_w, self.z_norm_b, self.z_rec, z, self.options.eps, v)
+            if self.msa is not None:
+                z_msa.copy_(z)
+                self.msa(z_msa, pair_mask=pair_mask, n_valid=n_valid, **msa_inputs)
+                ops.launch_add(z, z_msa, z, v)
             s, z = self.pairformer(s, z, pair_mask, mask, ws, n_valid)
             if pass_hook is not None:
                 pass_hook(i)
