@@ -209,6 +209,36 @@ def msa_bench(N: int = 512, S: int = 1024, seed: int = 5, steps: int = 3) -> dic
                         "masks all ones, seed 5 weights"}
 
 
+def diffusion_bench(N: int = 512, depth: int = 24, heads: int = 16, seed: int = 6, steps: int = 5) -> dict:
+    """Pair side of the diffusion conditioning at N tokens: PairwiseConditioning (projection
+    of cat(z, rel_pos) + 2 transitions) and the token-transformer pair bias (depth x heads
+    outputs per pair), each timed alone; the bias kernel's HBM rate against its algorithmic
+    bytes (z read once, the bias written once, fp32)."""
+    import torch
+    from tt_boltz_amd import diffusion, pairformer, synthetic
+    dev = pairformer.get_device()
+    stream = torch.cuda.current_stream()
+    w = synthetic.draw(synthetic.diffusion_pair_shapes(depth=depth, heads=heads), seed)
+    cond = diffusion.PairwiseConditioning(pairformer.WeightScope.wrap(w).child("pairwise_conditioner"))
+    bias = diffusion.TokenTransformerPairBias(depth, w)
+    g = torch.Generator().manual_seed(seed)
+    zt = torch.randn((1, N, N, 128), generator=g).to(dev).contiguous()
+    rp = torch.randn((1, N, N, 128), generator=g).to(dev).contiguous()
+    z = torch.empty_like(zt)
+    M = depth * heads
+    out0 = torch.empty((1, N, N, M), dtype=torch.float32, device=dev)
+    out1 = torch.empty((M, 1, N, N), dtype=torch.float32, device=dev)
+    ms_cond = time_events(lambda: cond(zt, rp, out=z), steps, stream)
+    ms_b0 = time_events(lambda: bias(z, 0, 1.0, out0), steps, stream)
+    ms_b1 = time_events(lambda: bias(z, 1, 1.0, out1), steps, stream)
+    nbytes = N * N * (128 + M) * 4
+    return {"N": N, "depth": depth, "heads": heads, "pairwise_conditioning_ms": round(ms_cond, 3),
+            "token_bias_ms": round(ms_b0, 3), "token_bias_head_major_ms": round(ms_b1, 3),
+            "token_bias_algorithmic_bytes": nbytes, "token_bias_TBps": round(nbytes / (ms_b0 * 1e-3) / 1e12, 2),
+            "token_bias_head_major_TBps": round(nbytes / (ms_b1 * 1e-3) / 1e12, 2),
+            "finite": bool(torch.isfinite(out0).all() and torch.isfinite(z).all())}
+
+
 def fast_bench(N: int = 1024, seed: int = 4, steps: int = 5) -> dict:
     """Config 4: one layer in fast mode (MXFP8 triangle multiplications and pair
     transition) at N=1024 next to the same layer in 16-bit, plus the fp8 contraction alone."""
@@ -415,6 +445,8 @@ def main() -> int:
         out["fast"] = fast_bench()
         torch.cuda.empty_cache()
         out["msa"] = msa_bench()
+        torch.cuda.empty_cache()
+        out["diffusion_pair"] = diffusion_bench()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(N, seed)
     print(json.dumps(out), flush=True)

@@ -357,6 +357,27 @@ int pf_linear_fwd(const float* x, const void* W, const float* bias, const float*
 int pf_pair_ln_linear_fwd(const float* x, const float* base, const float* ln_w, const float* ln_b,
                           const void* W, float* out, long rows, int C, float eps, void* stream);
 
+/* ------------------------------------------------------------------------------
+ * Diffusion conditioning, pair side (run once per trunk output; fixed for every
+ * sampling step).  z, rel_pos, out: fp32 [rows][128] (rows = B*N*N); LN params fp32.
+ * -------------------------------------------------------------------------- */
+/* PairwiseConditioning input projection (tt_bio/boltz2.py:1330-1333, 1349-1350):
+ *   out[p,:] = W . LN(cat(z[p,:], rel_pos[p,:]))   LN over 256 channels (ln_w, ln_b [256]),
+ *   W [128][256] in the operand type (LinearNoBias).  out must not alias an input. */
+int pf_pair_cond_proj_fwd(const float* z, const float* rel_pos, const float* ln_w, const float* ln_b,
+                          const void* W, float* out, long rows, int c_z, float eps, void* stream);
+
+/* Token-transformer pair bias of DiffusionConditioning (tt_bio/boltz2.py:2434-2441,
+ * 2472-2475; ttnn AttentionPairBias.compute_bias, tt_bio/tenstorrent.py:714-728):
+ *   bias[p, l*H + h] = scale * LN_l(z[p,:]) . W[l*H + h, :]   for l < n_layers, h < n_heads
+ * ln_w, ln_b [n_layers][128] (each layer's LayerNorm), W [n_layers*n_heads][128] (the layers'
+ * Linear(c_z, H, bias=False) weights stacked), n_layers*n_heads a multiple of 32, <= 512.
+ * layout 0: out [rows][L*H] (the reference's torch.cat(..., dim=-1)); layout 1: out
+ * [L*H][rows] (one contiguous plane per layer and head). */
+int pf_token_pair_bias_fwd(const float* z, const float* ln_w, const float* ln_b, const void* W, float* out,
+                           long rows, int c_z, int n_layers, int n_heads, int layout, float scale, float eps,
+                           void* stream);
+
 /* Residual hand-off of the trunk loop (tt_bio/boltz2.py:5221, 5230:
  *   z = z + template_module(z, ...), z = z + msa_module(z, ...)):
  *   out[i] = a[i] + b[i], fp32, 16-byte aligned pointers; out may alias a or b. */

@@ -16,6 +16,10 @@ Contents
                     (OCP e4m3 values, one power-of-two scale per 32 contiguous
                     elements along the contraction axis).  The reference has no
                     CPU fp8 path (``tt_bio/main.py:1648-1649``); this defines ours.
+``msa_ref``         fp32 restatement of the MSA module (outer product mean, pair
+                    weighted averaging, MSA layer, input embedding).
+``diffusion_ref``   fp32 restatement of the pair side of the diffusion conditioning
+                    (PairwiseConditioning, the token-transformer pair bias).
 ``brute``           scalar-loop restatements for tiny sizes (N <= 8), used by the
                     tests to pin ``pairformer_ref`` independently of torch's
                     einsum / matmul / softmax.

@@ -373,3 +373,42 @@ def pair_weighted_averaging(m, z, pair_mask, W, num_heads, c_h, inf=1e6):
                      for h in range(num_heads) for d in range(c_h)]
                 out[bb, s, i] = _matvec(W["proj_o.weight"], o)
     return out
+
+
+def pairwise_conditioning(z_trunk, rel_pos, W, n_transitions=2):
+    """PairwiseConditioning (boltz2.py:1344-1355) by loops: per pair, LN over the 2c
+    concatenated channels, the 2c -> c projection, then x += transition_i(x)."""
+    zt = _np(z_trunk); rp = _np(rel_pos)
+    W = {k: _np(v) for k, v in W.items()}
+    out = np.zeros(zt.shape)
+    for idx in np.ndindex(zt.shape[:-1]):
+        v = list(zt[idx]) + list(rp[idx])
+        x = _matvec(W["dim_pairwise_init_proj.1.weight"],
+                    _ln_vec(v, W["dim_pairwise_init_proj.0.weight"], W["dim_pairwise_init_proj.0.bias"]))
+        for i in range(n_transitions):
+            p = f"transitions.{i}."
+            xn = _ln_vec(x, W[p + "norm.weight"], W[p + "norm.bias"])
+            h1 = _matvec(W[p + "fc1.weight"], xn)
+            h2 = _matvec(W[p + "fc2.weight"], xn)
+            hh = [h1[t] * _sig(h1[t]) * h2[t] for t in range(len(h1))]
+            y = _matvec(W[p + "fc3.weight"], hh)
+            x = [x[c] + y[c] for c in range(len(x))]
+        out[idx] = x
+    return out
+
+
+def token_trans_bias(z, W, depth):
+    """DiffusionConditioning's token_trans_bias (boltz2.py:2472-2475) by loops: output
+    index l * H + h is layer l's LN (its own affine) followed by its head-h weight row."""
+    z = _np(z)
+    W = {k: _np(v) for k, v in W.items()}
+    H = W["token_trans_proj_z.0.1.weight"].shape[0]
+    out = np.zeros(z.shape[:-1] + (depth * H,))
+    for idx in np.ndindex(z.shape[:-1]):
+        for l in range(depth):
+            p = f"token_trans_proj_z.{l}."
+            xn = _ln_vec(list(z[idx]), W[p + "0.weight"], W[p + "0.bias"])
+            y = _matvec(W[p + "1.weight"], xn)
+            for h in range(H):
+                out[idx + (l * H + h,)] = y[h]
+    return out

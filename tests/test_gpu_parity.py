@@ -482,3 +482,52 @@ def test_msa_module_dropin(gpu):
     assert got.device.type == "cpu" and got.shape == z.shape
     v = N - 6
     check("MSA module 2 blocks (valid tokens)", got[:, :v, :v], want[:, :v, :v])
+
+
+# ------------------------------------------------------------------------------ diffusion conditioning (pair side)
+from oracle import diffusion_ref  # noqa: E402
+
+
+@pytest.mark.parametrize("shape,depth,heads", [((1, 64, 64), 24, 16), ((1, 37, 41), 2, 16), ((2, 32, 32), 4, 8)])
+def test_token_pair_bias(gpu, shape, depth, heads):
+    """pf_token_pair_bias_fwd (LN statistics once, each layer's affine folded into its
+    weights) vs the oracle's per-layer LayerNorm + Linear, both layouts; a row count that is
+    not a multiple of the 32-pair tile; the attention's log2(e) scale."""
+    from tt_boltz_amd import diffusion
+    w = synthetic.draw(synthetic.diffusion_pair_shapes(depth=depth, heads=heads, n_transitions=0), 95)
+    g = torch.Generator().manual_seed(96)
+    z = torch.randn((*shape, 128), generator=g) * 2 + 0.5
+    want = diffusion_ref.token_trans_bias(z, w, depth)
+    mod = diffusion.TokenTransformerPairBias(depth, w)
+    zd = z.to(gpu).contiguous()
+    check(f"token pair bias {shape} L={depth} H={heads} layout 0", mod(zd), want)
+    got1 = mod(zd, layout=1, scale=math.log2(math.e))
+    check(f"token pair bias {shape} layout 1", got1, want.permute(3, 0, 1, 2) * math.log2(math.e))
+
+
+def test_pairwise_conditioning(gpu):
+    from tt_boltz_amd import diffusion
+    w = ref.sub(synthetic.draw(synthetic.diffusion_pair_shapes(depth=1), 97), "pairwise_conditioner")
+    g = torch.Generator().manual_seed(98)
+    zt = torch.randn((1, 64, 64, 128), generator=g)
+    rp = torch.randn((1, 64, 64, 128), generator=g) * 0.5
+    want = diffusion_ref.pairwise_conditioning(zt, rp, w)
+    got = diffusion.PairwiseConditioning(w)(zt.to(gpu).contiguous(), rp.to(gpu).contiguous())
+    check("pairwise conditioning", got, want)
+
+
+def test_diffusion_pair_conditioning_dropin(gpu):
+    """The drop-in module on CPU tensors (N = 50, no padding needed): (z, token_trans_bias)."""
+    from tt_boltz_amd import diffusion
+    w = synthetic.draw(synthetic.diffusion_pair_shapes(depth=24, heads=16), 99)
+    g = torch.Generator().manual_seed(100)
+    zt = torch.randn((1, 50, 50, 128), generator=g)
+    rp = torch.randn((1, 50, 50, 128), generator=g)
+    z_want = diffusion_ref.pairwise_conditioning(zt, rp, ref.sub(w, "pairwise_conditioner"))
+    b_want = diffusion_ref.token_trans_bias(z_want, w, 24)
+    mod = diffusion.DiffusionPairConditioning(24)
+    mod.load_state_dict(w)
+    z_got, b_got = mod(zt, rp)
+    assert z_got.device.type == "cpu" and b_got.shape == (1, 50, 50, 384)
+    check("diffusion conditioning z", z_got, z_want)
+    check("diffusion conditioning token bias", b_got, b_want)

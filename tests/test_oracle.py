@@ -480,3 +480,37 @@ def test_msa_input_is_column_gather():
     want = (W[:, msa[0]].permute(1, 2, 0) + hd[0, ..., None] * W[:, 33] + dv[0, ..., None] * W[:, 34]
             + pr[0, ..., None] * W[:, 35] + (emb[0] @ w["s_proj.weight"].T)[None])
     _close(msa_ref.msa_input(msa, hd, dv, pr, emb, w)[0], want)
+
+
+# ----------------------------------------------------------------------------- diffusion conditioning (pair side)
+from oracle import diffusion_ref  # noqa: E402
+
+
+def test_pairwise_conditioning_matches_brute():
+    g = torch.Generator().manual_seed(90)
+    w = synthetic.draw(synthetic.diffusion_pair_shapes(c_z=8, depth=1, heads=2), 91)
+    w = ref.sub(w, "pairwise_conditioner")
+    zt = torch.randn((1, 3, 3, 8), generator=g)
+    rp = torch.randn((1, 3, 3, 8), generator=g)
+    got = diffusion_ref.pairwise_conditioning(zt, rp, w)
+    _close(got, torch.from_numpy(brute.pairwise_conditioning(zt, rp, w)), 1e-5)
+
+
+def test_token_trans_bias_matches_brute():
+    """Output l*H + h is layer l's own LayerNorm and head-h row (a swapped layer/head order or
+    a shared LayerNorm fails this)."""
+    g = torch.Generator().manual_seed(92)
+    w = synthetic.draw(synthetic.diffusion_pair_shapes(c_z=8, depth=3, heads=2, n_transitions=0), 93)
+    z = torch.randn((1, 3, 4, 8), generator=g)
+    got = diffusion_ref.token_trans_bias(z, w, 3)
+    assert got.shape == (1, 3, 4, 6)
+    _close(got, torch.from_numpy(brute.token_trans_bias(z, w, 3)), 1e-5)
+
+
+def test_token_trans_bias_constant_rows_closed_form():
+    """A constant pair row normalises to zero, so layer l's bias is W_l . beta_l."""
+    w = synthetic.draw(synthetic.diffusion_pair_shapes(c_z=8, depth=2, heads=3, n_transitions=0), 94)
+    z = torch.full((1, 2, 2, 8), 0.7)
+    got = diffusion_ref.token_trans_bias(z, w, 2)
+    want = torch.cat([w[f"token_trans_proj_z.{l}.1.weight"] @ w[f"token_trans_proj_z.{l}.0.bias"] for l in range(2)])
+    _close(got, want.expand(1, 2, 2, 6), 1e-6)

@@ -140,6 +140,10 @@ SIGNATURES = {
     "pf_pair_ln_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long,
                                       c_int, c_float, c_void_p]),
     "pf_add_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_long, c_void_p]),
+    "pf_pair_cond_proj_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int,
+                                      c_float, c_void_p]),
+    "pf_token_pair_bias_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_int,
+                                       c_int, c_int, c_float, c_float, c_void_p]),
     "pf_quantize_mx8": (c_int, [c_void_p, c_long, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "pf_trimul_mx8_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "pf_trimul_mx8_fwd": (c_int, [ctypes.POINTER(TrimulMx8Args)]),

@@ -225,6 +225,27 @@ def launch_add(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, variant: str
                variant)
 
 
+def launch_pair_cond_proj(z: torch.Tensor, rel_pos: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor,
+                          w: torch.Tensor, out: torch.Tensor, eps: float = 1e-5,
+                          variant: str = DEFAULT_VARIANT) -> None:
+    """out = W . LN(cat(z, rel_pos)) (PairwiseConditioning's input projection)."""
+    C = z.shape[-1]
+    _lib.check(_lib.load(variant).pf_pair_cond_proj_fwd(_ptr(z), _ptr(rel_pos), _ptr(ln_w), _ptr(ln_b), _ptr(w),
+                                                        _ptr(out), z.numel() // C, C, eps, _stream()),
+               "pf_pair_cond_proj_fwd", variant)
+
+
+def launch_token_pair_bias(z: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor, w: torch.Tensor,
+                           out: torch.Tensor, n_layers: int, n_heads: int, layout: int = 0, scale: float = 1.0,
+                           eps: float = 1e-5, variant: str = DEFAULT_VARIANT) -> None:
+    """Token-transformer pair bias: out = scale * cat_l(LN_l(z) W_l^T) (layout 0: [..., L*H];
+    layout 1: [L*H][rows])."""
+    C = z.shape[-1]
+    _lib.check(_lib.load(variant).pf_token_pair_bias_fwd(_ptr(z), _ptr(ln_w), _ptr(ln_b), _ptr(w), _ptr(out),
+                                                         z.numel() // C, C, n_layers, n_heads, layout, scale, eps,
+                                                         _stream()), "pf_token_pair_bias_fwd", variant)
+
+
 def launch_batched_nt_gemm(A: torch.Tensor, B: torch.Tensor, X: torch.Tensor, scale: float = 1.0,
                            variant: str = DEFAULT_VARIANT) -> None:
     """X[p] = scale * A[p] @ B[p]^T (pf_batched_nt_gemm): A [P,M,K], B [P,Nc,K] operand type,

@@ -203,13 +203,14 @@ class TriangleAttention(Module):
 class Transition(Module):
     """``tenstorrent.py:856-946`` / ``boltz2.py:1188-1258``."""
 
-    def __init__(self, state_dict, options: Optional[Options] = None):
+    def __init__(self, state_dict, options: Optional[Options] = None, allow_fast: bool = True):
         super().__init__(state_dict, options)
         self.w = {k: self.vec(k) for k in ("norm.weight", "norm.bias")}
         self.C = self.weights["fc1.weight"].shape[1]
         self.hidden = self.weights["fc1.weight"].shape[0]
-        # fast mode covers the pair transition (c_z = 128); the single-track one stays 16-bit
-        self.fast = self.fast and self.C == C_Z
+        # fast mode covers the Pairformer's pair transition (c_z = 128); the single-track
+        # one and those outside the Pairformer (allow_fast=False) stay 16-bit
+        self.fast = self.fast and allow_fast and self.C == C_Z
         if self.fast:
             self.w.update(ops.mx8_weights(self.weights, self.device, ops.TRANSITION_MX8_KEYS, self.variant))
         else:

@@ -85,6 +85,24 @@ def msa_module_shapes(n_blocks: int, c_m: int = 64, c_z: int = 128, c_s: int = 3
     return sh
 
 
+def diffusion_pair_shapes(c_z: int = 128, depth: int = 24, heads: int = 16, n_transitions: int = 2,
+                          prefix: str = "") -> Dict[str, tuple]:
+    """Pair side of DiffusionConditioning (boltz2.py:2396-2441): ``pairwise_conditioner.*``
+    (LN + projection of cat(z, rel_pos), transitions with hidden 2 c_z) and
+    ``token_trans_proj_z.{l}.*`` (LN + Linear(c_z, heads) per token-transformer layer)."""
+    sh = {"pairwise_conditioner.dim_pairwise_init_proj.0.weight": (2 * c_z,),
+          "pairwise_conditioner.dim_pairwise_init_proj.0.bias": (2 * c_z,),
+          "pairwise_conditioner.dim_pairwise_init_proj.1.weight": (c_z, 2 * c_z)}
+    for i in range(n_transitions):
+        p = f"pairwise_conditioner.transitions.{i}."
+        sh.update({p + "norm.weight": (c_z,), p + "norm.bias": (c_z,), p + "fc1.weight": (2 * c_z, c_z),
+                   p + "fc2.weight": (2 * c_z, c_z), p + "fc3.weight": (c_z, 2 * c_z)})
+    for l in range(depth):
+        sh.update({f"token_trans_proj_z.{l}.0.weight": (c_z,), f"token_trans_proj_z.{l}.0.bias": (c_z,),
+                   f"token_trans_proj_z.{l}.1.weight": (heads, c_z)})
+    return {prefix + k: v for k, v in sh.items()}
+
+
 def recycle_shapes(c_z: int = 128, c_s: int = 384) -> Dict[str, tuple]:
     """Boltz2 recycling parameters (boltz2.py:4961-4968)."""
     return {"s_norm.weight": (c_s,), "s_norm.bias": (c_s,), "z_norm.weight": (c_z,), "z_norm.bias": (c_z,),

@@ -14,4 +14,7 @@ from tt_boltz_amd.pairformer import (  # noqa: E402,F401
     TriangleAttention, TriangleMultiplication, TrunkRecycler, WeightScope, get_device, set_fast_mode,
 )
 from tt_boltz_amd.msa import MSA, MSALayer, MSAModule, OuterProductMean, PairWeightedAveraging  # noqa: E402,F401
+from tt_boltz_amd.diffusion import (  # noqa: E402,F401
+    DiffusionPairConditioning, PairwiseConditioning, TokenTransformerPairBias,
+)
 from tt_boltz_amd import ops  # noqa: E402,F401
