@@ -239,6 +239,32 @@ def diffusion_bench(N: int = 512, depth: int = 24, heads: int = 16, seed: int = 
             "finite": bool(torch.isfinite(out0).all() and torch.isfinite(z).all())}
 
 
+def template_bench(N: int = 512, T: int = 4, seed: int = 7, steps: int = 5) -> dict:
+    """The template stack's Pairformer (2 no-seq layers at c_z = 64, boltz2.py:3748-3761) on
+    T templates (the batch the template module runs it on) at N tokens: ms per 2-layer pass
+    and per layer, masks all ones."""
+    import torch
+    from tt_boltz_amd import ops, pairformer, synthetic
+    dev = pairformer.get_device()
+    stream = torch.cuda.current_stream()
+    w = synthetic.stack_weights(2, seed, c_z=64, transform_s=False)
+    pf = pairformer.Pairformer(2, 32, 4, None, None, False, w)
+    z = torch.randn((T, N, N, 64), generator=torch.Generator().manual_seed(seed)).to(dev).contiguous()
+    ws = ops.workspace(pf.workspace_bytes(T, N), dev)
+    ms = time_events(lambda: pf(None, z, None, None, ws), steps, stream)
+    layer = pf.blocks[0]
+    ops_ms = {
+        "trimul_out": time_events(lambda: layer.triangle_multiplication_start(z, None, out=z, accumulate=True, ws=ws),
+                                  steps, stream),
+        "triatt_start": time_events(lambda: layer.triangle_attention_start(z, None, out=z, accumulate=True, ws=ws),
+                                    steps, stream),
+        "transition_z": time_events(lambda: layer.transition_z(z, out=z, accumulate=True, ws=ws), steps, stream),
+    }
+    return {"N": N, "templates": T, "c_z": 64, "stack_ms": round(ms, 3), "layer_ms": round(ms / 2, 3),
+            "template_layers_per_s": round(2000.0 / ms, 2), "ops_ms": {k: round(v, 3) for k, v in ops_ms.items()},
+            "finite": bool(torch.isfinite(z).all())}
+
+
 def fast_bench(N: int = 1024, seed: int = 4, steps: int = 5) -> dict:
     """Config 4: one layer in fast mode (MXFP8 triangle multiplications and pair
     transition) at N=1024 next to the same layer in 16-bit, plus the fp8 contraction alone."""
@@ -447,6 +473,8 @@ def main() -> int:
         out["msa"] = msa_bench()
         torch.cuda.empty_cache()
         out["diffusion_pair"] = diffusion_bench()
+        torch.cuda.empty_cache()
+        out["template"] = template_bench()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(N, seed)
     print(json.dumps(out), flush=True)

@@ -55,8 +55,10 @@ def test_rejects_null_and_bad_shapes_without_launching():
     assert lib.pf_trimul_fwd(None) == -1 and "null args" in _err()
     a = _lib.TrimulArgs(B=1, N=100, C=128, hidden=128, direction=0)
     assert lib.pf_trimul_fwd(ctypes.byref(a)) == -1 and "multiple of 64" in _err()
-    a = _lib.TrimulArgs(B=1, N=128, C=64, hidden=64, direction=0)
-    assert lib.pf_trimul_fwd(ctypes.byref(a)) == -1 and "c_z = 128" in _err()
+    a = _lib.TrimulArgs(B=1, N=128, C=96, hidden=96, direction=0)
+    assert lib.pf_trimul_fwd(ctypes.byref(a)) == -1 and "128 or 64" in _err()
+    a = _lib.TrimulArgs(B=1, N=128, C=64, hidden=128, direction=0)
+    assert lib.pf_trimul_fwd(ctypes.byref(a)) == -1 and "hidden must equal c_z" in _err()
     t = _lib.TriattArgs(B=1, N=128, C=128, H=8, D=16)
     assert lib.pf_triatt_fwd(ctypes.byref(t)) == -1 and "H=4" in _err()
     assert lib.pf_layernorm_fwd(None, None, None, None, 4, 8, 1e-5, None) == -1

@@ -531,3 +531,65 @@ def test_diffusion_pair_conditioning_dropin(gpu):
     assert z_got.device.type == "cpu" and b_got.shape == (1, 50, 50, 384)
     check("diffusion conditioning z", z_got, z_want)
     check("diffusion conditioning token bias", b_got, b_want)
+
+
+# ------------------------------------------------------------------------------ template stack (c_z = 64)
+def _sub_w64(seed, prefix):
+    return ref.sub(synthetic.draw({k: v for k, v in synthetic.layer_shapes(c_z=64, transform_s=False).items()
+                                   if k.startswith(prefix + ".")}, seed), prefix)
+
+
+@pytest.mark.parametrize("N,direction", [(64, "outgoing"), (128, "incoming"), (448, "outgoing")])
+def test_trimul_c64(gpu, N, direction):
+    """c_z = 64 (the template stack's pair width): the same kernels built for 64 channels;
+    random pair mask with a padded tail; N = 448 takes the 256x256-tile contraction."""
+    prefix = "tri_mul_out" if direction == "outgoing" else "tri_mul_in"
+    w = _sub_w64(40 + N, prefix)
+    _, z, _, pm = synthetic.pair_inputs(N, 41 + N, c_z=64, pad_tail=N // 8, with_s=False)
+    pm = pm * (torch.rand(pm.shape, generator=torch.Generator().manual_seed(N)) > 0.15).float()
+    want = ref.triangle_multiplication(z, pm, w, direction)
+    mod = pairformer.TriangleMultiplication(direction == "incoming", w)
+    got = mod(z.to(gpu).contiguous(), pm.to(gpu).contiguous())
+    check(f"trimul c_z=64 {direction} N={N}", got, want)
+
+
+@pytest.mark.parametrize("N,ending", [(64, False), (128, True)])
+def test_triatt_c64(gpu, N, ending):
+    prefix = "tri_att_end" if ending else "tri_att_start"
+    w = _sub_w64(42 + N, prefix)
+    _, z, _, pm = synthetic.pair_inputs(N, 43 + N, c_z=64, pad_tail=N // 8, with_s=False)
+    want = ref.triangle_attention(z, pm, w, not ending, None)
+    mod = pairformer.TriangleAttention(32, 4, ending, {k[4:] if k.startswith("mha.") else k: v for k, v in w.items()})
+    got = mod(z.to(gpu).contiguous(), pm.to(gpu).contiguous())
+    check(f"triatt c_z=64 ending={ending} N={N}", got, want)
+
+
+def test_template_pairformer_module(gpu):
+    """The template stack's Pairformer (tenstorrent.PairformerModule(2, 32, 4, None, None, False)
+    on c_z = 64 weights, boltz2.py:3748-3761): N = 50 padded to 64 inside, masked tail."""
+    N = 50
+    w = synthetic.stack_weights(2, 44, c_z=64, transform_s=False)
+    _, z, _, _ = synthetic.pair_inputs(N, 45, c_z=64, with_s=False)
+    m = torch.ones((1, N)); m[0, 44:] = 0
+    pm = m[:, :, None] * m[:, None, :]
+    _, z_ref = ref.pairformer_stack(None, z, None, pm, w, 2)
+    mod = pairformer.PairformerModule(2, 32, 4, None, None, False)
+    mod.load_state_dict(w)
+    _, z_got = mod(None, z, pair_mask=pm)
+    check("template pairformer (c_z=64) valid", z_got[:, :44, :44], z_ref[:, :44, :44])
+    check("template pairformer (c_z=64) full", z_got, z_ref)
+
+
+def test_confidence_config_stack(gpu):
+    """The confidence module's stack (tenstorrent.PairformerModule(8, 32, 4, 24, 16, True),
+    boltz2.py:4502-4510): 8 layers with the single track, N = 64, masked tail."""
+    N = 64
+    w = synthetic.stack_weights(8, 46)
+    s, z, mask, pm = _inputs(N, 47, pad_tail=7)
+    s_ref, z_ref = ref.pairformer_stack(s, z, mask, pm, w, 8)
+    pf = pairformer.Pairformer(8, 32, 4, 24, 16, True, w)
+    s_got, z_got = pf(s.to(gpu).contiguous(), z.to(gpu).contiguous(), pm.to(gpu).contiguous(), mask.to(gpu),
+                      n_valid=N - 7)
+    nv = N - 7
+    check("confidence 8-layer stack z (valid)", z_got[:, :nv, :nv], z_ref[:, :nv, :nv])
+    check("confidence 8-layer stack s (valid)", s_got[:, :nv], s_ref[:, :nv])

@@ -113,55 +113,64 @@ PF_DEV opx8 zero_x8() {
 }
 
 // Load the x-hat fragment layout: lane (m = l & 31, h = l >> 5) reads channels
-// 16*s + 8*h + t (s = 0..7, t = 0..7) of a 128-channel fp32 vector.
-PF_DEV void load_row128_frag(const float* __restrict__ p, int h, float (&x)[64]) {
+// 16*s + 8*h + t (s < CC/16, t = 0..7) of a CC-channel fp32 vector (CC = 64 or 128).
+template <int CC>
+PF_DEV void load_row_frag(const float* __restrict__ p, int h, float (&x)[CC / 2]) {
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
+  for (int s = 0; s < CC / 16; ++s) {
     const f32x4 a = *reinterpret_cast<const f32x4*>(p + 16 * s + 8 * h);
     const f32x4 b = *reinterpret_cast<const f32x4*>(p + 16 * s + 8 * h + 4);
     x[8 * s + 0] = a[0]; x[8 * s + 1] = a[1]; x[8 * s + 2] = a[2]; x[8 * s + 3] = a[3];
     x[8 * s + 4] = b[0]; x[8 * s + 5] = b[1]; x[8 * s + 6] = b[2]; x[8 * s + 7] = b[3];
   }
 }
+PF_DEV void load_row128_frag(const float* __restrict__ p, int h, float (&x)[64]) { load_row_frag<128>(p, h, x); }
 
-// (x - mean) * rstd of a 128-vector (load_row128_frag order) as 8 MFMA fragments: the
+// (x - mean) * rstd of a CC-vector (load_row_frag order) as CC/16 MFMA fragments: the
 // LayerNorm without its affine part, for callers that fold gamma / beta into the weights.
-PF_DEV void ln128_norm_to_frag(const float (&x)[64], float eps, opx8 (&f)[8]) {
+template <int CC>
+PF_DEV void ln_norm_to_frag(const float (&x)[CC / 2], float eps, opx8 (&f)[CC / 16]) {
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 64; ++i) s += x[i];
-  const float mean = xor32_sum(s) * (1.f / 128.f);
+  for (int i = 0; i < CC / 2; ++i) s += x[i];
+  const float mean = xor32_sum(s) * (1.f / CC);
   float v = 0.f;
 #pragma unroll
-  for (int i = 0; i < 64; ++i) { const float d = x[i] - mean; v += d * d; }
-  const float rstd = rsqrtf(xor32_sum(v) * (1.f / 128.f) + eps);
+  for (int i = 0; i < CC / 2; ++i) { const float d = x[i] - mean; v += d * d; }
+  const float rstd = rsqrtf(xor32_sum(v) * (1.f / CC) + eps);
 #pragma unroll
-  for (int s8 = 0; s8 < 8; ++s8)
+  for (int s8 = 0; s8 < CC / 16; ++s8)
 #pragma unroll
     for (int t = 0; t < 8; ++t) f[s8][t] = (op_t)((x[8 * s8 + t] - mean) * rstd);
 }
+PF_DEV void ln128_norm_to_frag(const float (&x)[64], float eps, opx8 (&f)[8]) { ln_norm_to_frag<128>(x, eps, f); }
 
-// LayerNorm of a 128-vector split over the two halves of a wave (64 values per
-// lane, in load_row128_frag order), written as 8 opx8 MFMA fragments.
+// LayerNorm of a CC-vector split over the two halves of a wave (CC/2 values per
+// lane, in load_row_frag order), written as CC/16 opx8 MFMA fragments.
 // Two-pass (mean, then centred variance) in fp32, like torch's CPU kernel.
-PF_DEV void ln128_to_frag(const float (&x)[64], int h, const float* __restrict__ w,
-                          const float* __restrict__ b, float eps, opx8 (&f)[8]) {
+template <int CC>
+PF_DEV void ln_to_frag(const float (&x)[CC / 2], int h, const float* __restrict__ w,
+                       const float* __restrict__ b, float eps, opx8 (&f)[CC / 16]) {
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 64; ++i) s += x[i];
-  const float mean = xor32_sum(s) * (1.f / 128.f);
+  for (int i = 0; i < CC / 2; ++i) s += x[i];
+  const float mean = xor32_sum(s) * (1.f / CC);
   float v = 0.f;
 #pragma unroll
-  for (int i = 0; i < 64; ++i) { const float d = x[i] - mean; v += d * d; }
-  const float rstd = rsqrtf(xor32_sum(v) * (1.f / 128.f) + eps);
+  for (int i = 0; i < CC / 2; ++i) { const float d = x[i] - mean; v += d * d; }
+  const float rstd = rsqrtf(xor32_sum(v) * (1.f / CC) + eps);
 #pragma unroll
-  for (int s8 = 0; s8 < 8; ++s8) {
+  for (int s8 = 0; s8 < CC / 16; ++s8) {
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const int c = 16 * s8 + 8 * h + t;
       f[s8][t] = (op_t)((x[8 * s8 + t] - mean) * rstd * w[c] + b[c]);
     }
   }
+}
+PF_DEV void ln128_to_frag(const float (&x)[64], int h, const float* __restrict__ w, const float* __restrict__ b,
+                          float eps, opx8 (&f)[8]) {
+  ln_to_frag<128>(x, h, w, b, eps, f);
 }
 
 // 16-byte-chunk XOR swizzle for LDS rows of 64 op_t (128 bytes): the 32 rows one
@@ -337,32 +346,40 @@ PF_DEV float amax16(const float (&v)[16]) {
 // ---------------------------------------------------------------------------------
 PF_DEV int oa_channel(int q, int h) { return 32 * (q >> 2) + 8 * (q & 3) + 4 * h; }
 
-PF_DEV void load_row128_oa(const float* __restrict__ p, int h, float (&x)[64]) {
+template <int CC>
+PF_DEV void load_row_oa(const float* __restrict__ p, int h, float (&x)[CC / 2]) {
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
+  for (int q = 0; q < CC / 8; ++q) {
     const f32x4 a = *reinterpret_cast<const f32x4*>(p + oa_channel(q, h));
     x[4 * q + 0] = a[0]; x[4 * q + 1] = a[1]; x[4 * q + 2] = a[2]; x[4 * q + 3] = a[3];
   }
 }
+PF_DEV void load_row128_oa(const float* __restrict__ p, int h, float (&x)[64]) { load_row_oa<128>(p, h, x); }
 
-// LayerNorm (two-pass fp32) of a row held in output-aligned order, as 8 MFMA B fragments.
-PF_DEV void ln128_oa_to_frag(const float (&x)[64], int h, const float* __restrict__ w,
-                             const float* __restrict__ b, float eps, opx8 (&f)[8]) {
+// LayerNorm (two-pass fp32) of a CC-channel row held in output-aligned order, as CC/16
+// MFMA B fragments.
+template <int CC>
+PF_DEV void ln_oa_to_frag(const float (&x)[CC / 2], int h, const float* __restrict__ w,
+                          const float* __restrict__ b, float eps, opx8 (&f)[CC / 16]) {
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 64; ++i) s += x[i];
-  const float mean = xor32_sum(s) * (1.f / 128.f);
+  for (int i = 0; i < CC / 2; ++i) s += x[i];
+  const float mean = xor32_sum(s) * (1.f / CC);
   float v = 0.f;
 #pragma unroll
-  for (int i = 0; i < 64; ++i) { const float d = x[i] - mean; v += d * d; }
-  const float rstd = rsqrtf(xor32_sum(v) * (1.f / 128.f) + eps);
+  for (int i = 0; i < CC / 2; ++i) { const float d = x[i] - mean; v += d * d; }
+  const float rstd = rsqrtf(xor32_sum(v) * (1.f / CC) + eps);
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
+  for (int q = 0; q < CC / 8; ++q) {
     const int c = oa_channel(q, h);
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       f[q >> 1][4 * (q & 1) + e] = (op_t)((x[4 * q + e] - mean) * rstd * w[c + e] + b[c + e]);
   }
+}
+PF_DEV void ln128_oa_to_frag(const float (&x)[64], int h, const float* __restrict__ w, const float* __restrict__ b,
+                             float eps, opx8 (&f)[8]) {
+  ln_oa_to_frag<128>(x, h, w, b, eps, f);
 }
 
 // Weight fragment (A operand) of weight row `wrow` (128 op_t, contiguous) for K step s in

@@ -28,6 +28,8 @@
 
 namespace {
 
+// C = H * D: the attention width (q / k / v / o channels).  The pair width c_z (CC in the
+// projection kernels) is 128 in the trunk and 64 in the template stack.
 constexpr int C = 128, H = 4, D = 32, LDSW = 136;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_SLACK = 8.f;   // log2 units: P values stay <= 2^8 between rescales
@@ -64,8 +66,10 @@ PF_DEV op_t mask_term(bool pad, float mv) {
 // ---------------------------------------------------------------------------------
 constexpr int TAP_WAVES = 8;
 constexpr int TAP_ROWS = 3 * C + 32;   // q, k, v rows, then 32 bias rows (H used, rest zero)
-constexpr size_t TAP_LDS = (size_t)TAP_ROWS * LDSW * sizeof(op_t) + TAP_ROWS * sizeof(float);
+template <int CC>
+constexpr size_t tap_lds() { return (size_t)TAP_ROWS * (CC + 8) * sizeof(op_t) + TAP_ROWS * sizeof(float); }
 
+template <int CC>
 __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
     const float* __restrict__ z, const float* __restrict__ pair_mask,
     const float* __restrict__ lnw, const float* __restrict__ lnb,
@@ -73,29 +77,30 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
     const op_t* __restrict__ wb, op_t* __restrict__ Q, op_t* __restrict__ K,
     op_t* __restrict__ Vt, op_t* __restrict__ bias16, op_t* __restrict__ mask16,
     int B, int N, int n_valid, int ending, float qscale, float eps) {
+  constexpr int LW = CC + 8, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t plds[];
-  float* cb = reinterpret_cast<float*>(plds + TAP_ROWS * LDSW);
+  float* cb = reinterpret_cast<float*>(plds + TAP_ROWS * LW);
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  auto wrow = [&](int row) -> const op_t* {
-    return row < C ? wq + row * C : row < 2 * C ? wk + (row - C) * C
-         : row < 3 * C ? wv + (row - 2 * C) * C : wb + (row - 3 * C) * C;
+  auto wrow = [&](int row) -> const op_t* {   // weight rows have CC inputs
+    return row < C ? wq + row * CC : row < 2 * C ? wk + (row - C) * CC
+         : row < 3 * C ? wv + (row - 2 * C) * CC : wb + (row - 3 * C) * CC;
   };
-  for (int c = tid; c < TAP_ROWS * 16; c += 64 * TAP_WAVES) {
-    const int row = c >> 4, col = (c & 15) * 8;
+  for (int c = tid; c < TAP_ROWS * (CC / 8); c += 64 * TAP_WAVES) {
+    const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
     opx8 v = zero_x8();
     if (row < 3 * C + H) {
       const opx8 w = ld_x8(wrow(row) + col);
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = (op_t)((float)w[e] * lnw[col + e]);
     }
-    st_x8(plds + row * LDSW + col, v);
+    st_x8(plds + row * LW + col, v);
   }
   for (int row = tid; row < TAP_ROWS; row += 64 * TAP_WAVES) {
     float acc = 0.f;
     if (row < 3 * C + H) {
       const op_t* w = wrow(row);
-      for (int c = 0; c < C; ++c) acc += (float)w[c] * lnb[c];
+      for (int c = 0; c < CC; ++c) acc += (float)w[c] * lnb[c];
     }
     cb[row] = acc;
   }
@@ -113,28 +118,28 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
   auto zpair = [&](int b, int ip, int j0) -> long {
     return ((long)b * N + (ending ? j0 + m : ip)) * N + (ending ? ip : j0 + m);
   };
-  float xn[64];
+  float xn[CC / 2];
   uint32_t t = blockIdx.x * TAP_WAVES + wid;
   if (t < tiles) {
     int b, ip, j0;
     decode(t, b, ip, j0);
-    load_row128_frag(z + zpair(b, ip, j0) * C, h, xn);
+    load_row_frag<CC>(z + zpair(b, ip, j0) * CC, h, xn);
   }
   for (; t < tiles; t += stride) {
     int b, ip, j0;
     decode(t, b, ip, j0);
     const long pair = zpair(b, ip, j0);
-    opx8 xf[8];
+    opx8 xf[KS];
     {
-      float x[64];
+      float x[CC / 2];
 #pragma unroll
-      for (int i = 0; i < 64; ++i) x[i] = xn[i];
+      for (int i = 0; i < CC / 2; ++i) x[i] = xn[i];
       if (t + stride < tiles) {   // next tile's rows, in flight during this tile
         int b2, ip2, j02;
         decode(t + stride, b2, ip2, j02);
-        load_row128_frag(z + zpair(b2, ip2, j02) * C, h, xn);
+        load_row_frag<CC>(z + zpair(b2, ip2, j02) * CC, h, xn);
       }
-      ln128_norm_to_frag(x, eps, xf);
+      ln_norm_to_frag<CC>(x, eps, xf);
     }
     if (h == 0) {
       // frame key j0+m of row ip: padding -> excluded; otherwise inf*(mask-1) (log2 units)
@@ -153,7 +158,7 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
         for (int e = 0; e < 4; ++e) acc[4 * g + e] = c4[e];
       }
 #pragma unroll
-      for (int s2 = 0; s2 < 8; ++s2) acc = mfma32(ld_x8(plds + (32 * blk + m) * LDSW + 16 * s2 + 8 * h), xf[s2], acc);
+      for (int s2 = 0; s2 < KS; ++s2) acc = mfma32(ld_x8(plds + (32 * blk + m) * LW + 16 * s2 + 8 * h), xf[s2], acc);
       op_t* dst = blk < 4 ? Q : K;
       store_runs16(dst + ((rowh + (blk & 3)) * N + j0 + m) * D, acc, blk < 4 ? qscale : 1.f, h);
     }
@@ -165,8 +170,8 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = c0;
 #pragma unroll
-      for (int s2 = 0; s2 < 8; ++s2)
-        acc = mfma32(xf[s2], ld_x8(plds + (2 * C + 32 * hd + m) * LDSW + 16 * s2 + 8 * h), acc);
+      for (int s2 = 0; s2 < KS; ++s2)
+        acc = mfma32(xf[s2], ld_x8(plds + (2 * C + 32 * hd + m) * LW + 16 * s2 + 8 * h), acc);
       // keys 8g + 4h + e of runs g = 2p, 2p+1 sit at storage 16p + 8h .. +7 (perm16)
       op_t* row = Vt + ((rowh + hd) * D + m) * (long)N + j0;
 #pragma unroll
@@ -187,7 +192,7 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
         for (int e = 0; e < 4; ++e) acc[4 * g + e] = c4[e];
       }
 #pragma unroll
-      for (int s2 = 0; s2 < 8; ++s2) acc = mfma32(ld_x8(plds + (3 * C + m) * LDSW + 16 * s2 + 8 * h), xf[s2], acc);
+      for (int s2 = 0; s2 < KS; ++s2) acc = mfma32(ld_x8(plds + (3 * C + m) * LW + 16 * s2 + 8 * h), xf[s2], acc);
       if (h == 0) {
 #pragma unroll
         for (int r = 0; r < H; ++r) bias16[(((long)b * H + r) * N + ip) * N + j0 + m] = (op_t)(acc[r] * LOG2E);
@@ -452,21 +457,28 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
 // operand of D[out][position] = W_o . (o * g), and the residual is the z the lane loaded.
 // ---------------------------------------------------------------------------------
 constexpr int TAO_WAVES = 8;
-constexpr size_t TAO_LDS = (size_t)2 * C * LDSW * sizeof(op_t);
+// W_g [C][CC] (rows padded to CC + 8), W_o [CC][C] (rows padded to C + 8 = LDSW)
+template <int CC>
+constexpr size_t tao_lds() { return ((size_t)C * (CC + 8) + (size_t)CC * LDSW) * sizeof(op_t); }
 
 // resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
+template <int CC>
 __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
     const op_t* __restrict__ O, const float* z_in, float* out, const float* __restrict__ lnw,
     const float* __restrict__ lnb, const op_t* __restrict__ wg, const op_t* __restrict__ wo,
     int B, int N, int ending, int resid, float eps) {
+  constexpr int LWG = CC + 8, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t tlds[];
   op_t* sWg = tlds;
-  op_t* sWo = tlds + C * LDSW;
+  op_t* sWo = tlds + C * LWG;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  for (int c = tid; c < C * 16; c += 64 * TAO_WAVES) {
+  for (int c = tid; c < C * (CC / 8); c += 64 * TAO_WAVES) {
+    const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
+    st_x8(&sWg[row * LWG + col], ld_x8(wg + row * CC + col));
+  }
+  for (int c = tid; c < CC * 16; c += 64 * TAO_WAVES) {
     const int row = c >> 4, col = (c & 15) * 8;
-    st_x8(&sWg[row * LDSW + col], ld_x8(wg + row * C + col));
     st_x8(&sWo[row * LDSW + col], ld_x8(wo + row * C + col));
   }
   __syncthreads();
@@ -477,19 +489,19 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
     const PosTile pt = pos_tile(t, N);
     const int b = pt.b, ip = pt.r, j = pt.c0 + m;
     const long zp = ending ? ((long)b * N + j) * N + ip : ((long)b * N + ip) * N + j;
-    float zr[64];
-    opx8 xf[8];
-    load_row128_oa(z_in + zp * C, h, zr);
-    ln128_oa_to_frag(zr, h, lnw, lnb, eps, xf);
+    float zr[CC / 2];
+    opx8 xf[KS];
+    load_row_oa<CC>(z_in + zp * CC, h, zr);
+    ln_oa_to_frag<CC>(zr, h, lnw, lnb, eps, xf);
     // o * sigmoid(g) as the B operand of the output projection (k order = output-aligned)
     opx8 og[8];
     const op_t* orow = O + (pos0 + m) * C;
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
-      const op_t* wrow = &sWg[(32 * cb + m) * LDSW];
+      const op_t* wrow = &sWg[(32 * cb + m) * LWG];
       f32x16 g = zero16();
 #pragma unroll
-      for (int s = 0; s < 8; ++s) g = mfma32(wfrag_oa(wrow, s, h), xf[s], g);   // D[channel][position]
+      for (int s = 0; s < KS; ++s) g = mfma32(wfrag_oa(wrow, s, h), xf[s], g);   // D[channel][position]
 #pragma unroll
       for (int gg = 0; gg < 4; ++gg) {
         const int q = 4 * cb + gg;            // chunk: channels oa_channel(q, h) + 0..3
@@ -500,7 +512,7 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
       }
     }
 #pragma unroll
-    for (int ob = 0; ob < 4; ++ob) {
+    for (int ob = 0; ob < CC / 32; ++ob) {
       const op_t* wrow = &sWo[(32 * ob + m) * LDSW];
       f32x16 acc = zero16();
 #pragma unroll
@@ -508,7 +520,7 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
 #pragma unroll
       for (int gg = 0; gg < 4; ++gg) {
         const int q = 4 * ob + gg;
-        float* dst = out + zp * C + oa_channel(q, h);
+        float* dst = out + zp * CC + oa_channel(q, h);
         f32x4 v;
         if (resid == 2) v = *reinterpret_cast<const f32x4*>(dst);
 #pragma unroll
@@ -584,20 +596,64 @@ int launch_attn(const TaBuffers& t, float* o32, int B, int N, int n_valid, hipSt
   return PF_OK;
 }
 
+template <int CC>
+int triatt_run(const pf_triatt_args* a) {
+  hipStream_t st = (hipStream_t)a->stream;
+  const int B = a->B, N = a->N;
+  const int n_valid = a->n_valid ? a->n_valid : N;
+  TaBuffers t = ta_buffers(a->workspace, B, N);
+  const float qscale = LOG2E / sqrtf((float)D);
+  const long positions = (long)B * N * N;
+  const int cus = device_cus();
+  if (cus <= 0) return pf_fail(PF_E_LAUNCH, "pf_triatt_fwd: cannot query the device");
+  {
+    static bool attr = false;
+    if (!attr) {
+      if (hipFuncSetAttribute((const void*)ta_proj_kernel<CC>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)tap_lds<CC>()) != hipSuccess)
+        return pf_fail(PF_E_LAUNCH, "ta_proj_kernel: cannot reserve %zu bytes of LDS", tap_lds<CC>());
+      attr = true;
+    }
+    const int grid = (int)min((long)cus, (positions / 32 + TAP_WAVES - 1) / TAP_WAVES);
+    ta_proj_kernel<CC><<<grid, 64 * TAP_WAVES, tap_lds<CC>(), st>>>(
+        a->z_in, a->pair_mask, a->ln_w, a->ln_b, (const op_t*)a->w_q, (const op_t*)a->w_k, (const op_t*)a->w_v,
+        (const op_t*)a->w_bias, t.Q, t.K, t.Vt, t.bias16, t.mask16, B, N, n_valid, a->ending, qscale, a->eps);
+    PF_CHECK_LAUNCH("ta_proj_kernel");
+  }
+  int rc = launch_attn<false>(t, nullptr, B, N, n_valid, st);
+  if (rc) return rc;
+  {
+    static bool attr = false;
+    if (!attr) {
+      if (hipFuncSetAttribute((const void*)ta_out_kernel<CC>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)tao_lds<CC>()) != hipSuccess)
+        return pf_fail(PF_E_LAUNCH, "ta_out_kernel: cannot reserve %zu bytes of LDS", tao_lds<CC>());
+      attr = true;
+    }
+    const int grid = (int)min((long)cus, (positions / 32 + TAO_WAVES - 1) / TAO_WAVES);
+    const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);
+    ta_out_kernel<CC><<<grid, 64 * TAO_WAVES, tao_lds<CC>(), st>>>(t.O, a->z_in, a->out, a->ln_w, a->ln_b,
+                                                                  (const op_t*)a->w_g, (const op_t*)a->w_o, B, N,
+                                                                  a->ending, resid, a->eps);
+    PF_CHECK_LAUNCH("ta_out_kernel");
+  }
+  return PF_OK;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------------
 // C-ABI
 // ---------------------------------------------------------------------------------
 extern "C" size_t pf_triatt_workspace_size(int B, int N, int C_, int H_, int D_) {
-  if (B <= 0 || N <= 0 || C_ != C || H_ != H || D_ != D) return 0;
+  if (B <= 0 || N <= 0 || (C_ != 128 && C_ != 64) || H_ != H || D_ != D) return 0;
   return ta_buffers_size(B, N);
 }
 
 extern "C" int pf_triatt_fwd(const pf_triatt_args* a) {
   if (!a) return pf_fail(PF_E_INVALID, "pf_triatt_fwd: null args");
-  if (a->C != C || a->H != H || a->D != D)
-    return pf_fail(PF_E_INVALID, "pf_triatt_fwd: only C=128, H=4, D=32 supported (got C=%d H=%d D=%d)",
+  if ((a->C != 128 && a->C != 64) || a->H != H || a->D != D)
+    return pf_fail(PF_E_INVALID, "pf_triatt_fwd: only C = 128 or 64, H=4, D=32 supported (got C=%d H=%d D=%d)",
                    a->C, a->H, a->D);
   if (a->B <= 0 || a->N <= 0 || a->N % 64)
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: need B > 0 and N a positive multiple of 64 (B=%d N=%d)", a->B, a->N);
@@ -611,46 +667,7 @@ extern "C" int pf_triatt_fwd(const pf_triatt_args* a) {
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: workspace too small (%zu < %zu bytes)", a->workspace_bytes, need);
   if (a->n_valid < 0 || a->n_valid > a->N)
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: n_valid %d outside [0, N=%d]", a->n_valid, a->N);
-  hipStream_t st = (hipStream_t)a->stream;
-  const int B = a->B, N = a->N;
-  const int n_valid = a->n_valid ? a->n_valid : N;
-  TaBuffers t = ta_buffers(a->workspace, B, N);
-  const float qscale = LOG2E / sqrtf((float)D);
-  const long positions = (long)B * N * N;
-  {
-    static bool attr = false;
-    if (!attr) {
-      if (hipFuncSetAttribute((const void*)ta_proj_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)TAP_LDS) != hipSuccess)
-        return pf_fail(PF_E_LAUNCH, "ta_proj_kernel: cannot reserve %zu bytes of LDS", TAP_LDS);
-      attr = true;
-    }
-    const int grid = (int)min((long)device_cus(), (positions / 32 + TAP_WAVES - 1) / TAP_WAVES);
-    ta_proj_kernel<<<grid, 64 * TAP_WAVES, TAP_LDS, st>>>(a->z_in, a->pair_mask, a->ln_w, a->ln_b,
-                                                           (const op_t*)a->w_q, (const op_t*)a->w_k,
-                                                           (const op_t*)a->w_v, (const op_t*)a->w_bias, t.Q, t.K,
-                                                           t.Vt, t.bias16, t.mask16, B, N, n_valid, a->ending,
-                                                           qscale, a->eps);
-  }
-  PF_CHECK_LAUNCH("ta_proj_kernel");
-  int rc = launch_attn<false>(t, nullptr, B, N, n_valid, st);
-  if (rc) return rc;
-  {
-    static bool attr = false;
-    if (!attr) {
-      if (hipFuncSetAttribute((const void*)ta_out_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)TAO_LDS) != hipSuccess)
-        return pf_fail(PF_E_LAUNCH, "ta_out_kernel: cannot reserve %zu bytes of LDS", TAO_LDS);
-      attr = true;
-    }
-    const int grid = (int)min((long)device_cus(), (positions / 32 + TAO_WAVES - 1) / TAO_WAVES);
-    const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);
-    ta_out_kernel<<<grid, 64 * TAO_WAVES, TAO_LDS, st>>>(t.O, a->z_in, a->out, a->ln_w, a->ln_b,
-                                                         (const op_t*)a->w_g, (const op_t*)a->w_o, B, N, a->ending,
-                                                         resid, a->eps);
-  }
-  PF_CHECK_LAUNCH("ta_out_kernel");
-  return PF_OK;
+  return a->C == 128 ? triatt_run<128>(a) : triatt_run<64>(a);
 }
 
 extern "C" size_t pf_tri_attention_workspace_size(int B, int N, int H_, int D_) {

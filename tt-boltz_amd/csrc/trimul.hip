@@ -52,24 +52,30 @@ PF_DEV void blk32_store(op_t* lds, int tid, const Blk32& r) {
 // ---------------------------------------------------------------------------------
 constexpr int TMP_WAVES = 8;
 constexpr int SPITCH = 40;     // output staging pitch (elements): one 32-position row + 16 B
-constexpr size_t TMP_LDS = (size_t)2 * 256 * LDSW * sizeof(op_t) + (size_t)TMP_WAVES * 32 * SPITCH * sizeof(op_t);
+// CC = c_z (64 or 128): p_in / g_in are [2 CC][CC], LDS rows padded to CC + 8 elements
+template <int CC>
+constexpr size_t tmp_lds() {
+  return (size_t)2 * 2 * CC * (CC + 8) * sizeof(op_t) + (size_t)TMP_WAVES * 32 * SPITCH * sizeof(op_t);
+}
 
+template <int CC>
 __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
     const float* __restrict__ z, const float* __restrict__ mask,
     const float* __restrict__ lnw, const float* __restrict__ lnb,
     const op_t* __restrict__ w_p, const op_t* __restrict__ w_g,
     op_t* __restrict__ opA, op_t* __restrict__ opB, int B, int N, int incoming, float eps) {
+  constexpr int LW = CC + 8, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t wlds[];
   op_t* lp = wlds;
-  op_t* lg = wlds + 256 * LDSW;
+  op_t* lg = wlds + 2 * CC * LW;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  op_t* stg = wlds + 2 * 256 * LDSW + wid * 32 * SPITCH;   // this wave's output stage
+  op_t* stg = wlds + 2 * 2 * CC * LW + wid * 32 * SPITCH;   // this wave's output stage
 #pragma unroll 4
-  for (int c = tid; c < 256 * 16; c += 64 * TMP_WAVES) {
-    const int row = c >> 4, col = (c & 15) * 8;
-    st_x8(lp + row * LDSW + col, ld_x8(w_p + row * C + col));
-    st_x8(lg + row * LDSW + col, ld_x8(w_g + row * C + col));
+  for (int c = tid; c < 2 * CC * (CC / 8); c += 64 * TMP_WAVES) {
+    const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
+    st_x8(lp + row * LW + col, ld_x8(w_p + row * CC + col));
+    st_x8(lg + row * LW + col, ld_x8(w_g + row * CC + col));
   }
   __syncthreads();
 
@@ -89,24 +95,24 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
     asm volatile("" ::: "memory");   // LayerNorm parameters are re-read each tile, not pinned in VGPRs
     int cb_b, cb_orow, cb_ocol0;
     const long pair = tile_pair(t, cb_b, cb_orow, cb_ocol0);
-    opx8 xf[8];
+    opx8 xf[KS];
     float maskv = 1.f;
     {
-      float x[64];
-      load_row128_frag(z + pair * C, h, x);
+      float x[CC / 2];
+      load_row_frag<CC>(z + pair * CC, h, x);
       if (mask) maskv = mask[pair];
-      ln128_to_frag(x, h, lnw, lnb, eps, xf);
+      ln_to_frag<CC>(x, h, lnw, lnb, eps, xf);
     }
     float mr[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) mr[r] = __shfl(maskv, acc_row(r, h));
 #pragma unroll 1
-    for (int cb = 0; cb < 8; ++cb) {
-      const op_t* wp = lp + (32 * cb + m) * LDSW + 8 * h;
-      const op_t* wg = lg + (32 * cb + m) * LDSW + 8 * h;
+    for (int cb = 0; cb < 2 * CC / 32; ++cb) {
+      const op_t* wp = lp + (32 * cb + m) * LW + 8 * h;
+      const op_t* wg = lg + (32 * cb + m) * LW + 8 * h;
       f32x16 ap = zero16(), ag = zero16();
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
+      for (int s = 0; s < KS; ++s) {
         ap = mfma32(xf[s], ld_x8(wp + 16 * s), ap);   // rows = position, cols = output channel
         ag = mfma32(xf[s], ld_x8(wg + 16 * s), ag);
       }
@@ -121,7 +127,7 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
         }
         st_x4(stg + m * SPITCH + 8 * g + 4 * h, v);
       }
-      op_t* dst = (cb < 4 ? opA : opB) + (((long)cb_b * C + 32 * (cb & 3)) * N + cb_orow) * N + cb_ocol0;
+      op_t* dst = (cb < CC / 32 ? opA : opB) + (((long)cb_b * CC + 32 * (cb % (CC / 32))) * N + cb_orow) * N + cb_ocol0;
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int row = 16 * q + (lane >> 2), chunk = lane & 3;
@@ -365,27 +371,31 @@ __global__ __launch_bounds__(256, 1) void tm_contract_dma_kernel(
 // layout, so the residual z values the wave loaded for LN_in are the ones it adds to (no
 // second read of z).
 // ---------------------------------------------------------------------------------
-constexpr int TMO_WAVES = 8, XSP = 40;   // per-wave X stage: [128 channels][32 pairs + 8]
-constexpr size_t TMO_LDS = (size_t)2 * C * LDSW * sizeof(op_t) + (size_t)TMO_WAVES * C * XSP * sizeof(op_t);
+constexpr int TMO_WAVES = 8, XSP = 40;   // per-wave X stage: [CC channels][32 pairs + 8]
+template <int CC>
+constexpr size_t tmo_lds() {
+  return (size_t)2 * CC * (CC + 8) * sizeof(op_t) + (size_t)TMO_WAVES * CC * XSP * sizeof(op_t);
+}
 
 // resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
-template <typename XT>
+template <typename XT, int CC>
 __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
     const XT* __restrict__ X, float x_scale, const float* z_in, float* out,
     const float* __restrict__ lni_w, const float* __restrict__ lni_b,
     const float* __restrict__ lno_w, const float* __restrict__ lno_b,
     const op_t* __restrict__ w_pout, const op_t* __restrict__ w_gout,
     int B, int N, int resid, float eps) {
+  constexpr int LW = CC + 8, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t olds[];
   op_t* sWp = olds;
-  op_t* sWg = olds + C * LDSW;
+  op_t* sWg = olds + CC * LW;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  XT* xs = reinterpret_cast<XT*>(olds + 2 * C * LDSW) + wid * C * XSP;   // this wave's X stage
-  for (int c = tid; c < C * 16; c += 64 * TMO_WAVES) {
-    const int row = c >> 4, col = (c & 15) * 8;
-    st_x8(&sWp[row * LDSW + col], ld_x8(w_pout + row * C + col));
-    st_x8(&sWg[row * LDSW + col], ld_x8(w_gout + row * C + col));
+  XT* xs = reinterpret_cast<XT*>(olds + 2 * CC * LW) + wid * CC * XSP;   // this wave's X stage
+  for (int c = tid; c < CC * (CC / 8); c += 64 * TMO_WAVES) {
+    const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
+    st_x8(&sWp[row * LW + col], ld_x8(w_pout + row * CC + col));
+    st_x8(&sWg[row * LW + col], ld_x8(w_gout + row * CC + col));
   }
   __syncthreads();
   const long NN = (long)N * N;
@@ -396,37 +406,37 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
     const int b = pos_tile(t, N).b;
     {
       // X[b][ch][q0 .. q0+31]: 16-byte chunk c -> channel c >> 2, pairs 8*(c & 3) ..
-      const XT* src = X + (long)b * C * NN + (p0 - (long)b * NN);
+      const XT* src = X + (long)b * CC * NN + (p0 - (long)b * NN);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
+      for (int k = 0; k < CC / 16; ++k) {
         const int c = lane + 64 * k, ch = c >> 2, col = (c & 3) * 8;
         *reinterpret_cast<opx8*>(xs + ch * XSP + col) = *reinterpret_cast<const opx8*>(src + (long)ch * NN + col);
       }
     }
     const long pair = p0 + m;
-    opx8 xo[8], xi[8];
-    float zr[64];
+    opx8 xo[KS], xi[KS];
+    float zr[CC / 2];
     {
-      float xv[64];
+      float xv[CC / 2];
 #pragma unroll
-      for (int q = 0; q < 16; ++q)
+      for (int q = 0; q < CC / 8; ++q)
 #pragma unroll
         for (int e = 0; e < 4; ++e) xv[4 * q + e] = (float)xs[(oa_channel(q, h) + e) * XSP + m] * x_scale;
-      ln128_oa_to_frag(xv, h, lno_w, lno_b, eps, xo);
+      ln_oa_to_frag<CC>(xv, h, lno_w, lno_b, eps, xo);
     }
-    load_row128_oa(z_in + pair * C, h, zr);
-    ln128_oa_to_frag(zr, h, lni_w, lni_b, eps, xi);
+    load_row_oa<CC>(z_in + pair * CC, h, zr);
+    ln_oa_to_frag<CC>(zr, h, lni_w, lni_b, eps, xi);
 #pragma unroll   // fully unrolled: zr[] must be indexed with constants to stay in VGPRs
-    for (int ob = 0; ob < 4; ++ob) {
-      const op_t* wp = &sWp[(32 * ob + m) * LDSW];
-      const op_t* wg = &sWg[(32 * ob + m) * LDSW];
+    for (int ob = 0; ob < CC / 32; ++ob) {
+      const op_t* wp = &sWp[(32 * ob + m) * LW];
+      const op_t* wg = &sWg[(32 * ob + m) * LW];
       f32x16 P = zero16(), G = zero16();
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
+      for (int s = 0; s < KS; ++s) {
         P = mfma32(wfrag_oa(wp, s, h), xo[s], P);   // rows = output channel, cols = pair
         G = mfma32(wfrag_oa(wg, s, h), xi[s], G);
       }
-      float* orow = out + pair * C;
+      float* orow = out + pair * CC;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int q = 4 * ob + g;
@@ -477,21 +487,67 @@ int launch_contract(const op_t* opA, const op_t* opB, OutT* X, int planes, int N
   return PF_OK;
 }
 
+template <int CC>
+int trimul_run(const pf_trimul_args* a) {
+  hipStream_t st = (hipStream_t)a->stream;
+  const int B = a->B, N = a->N;
+  const size_t planes = (size_t)B * CC * N * N;
+  op_t* opA = (op_t*)a->workspace;
+  op_t* opB = opA + planes;
+  op_t* X = opB + planes;
+  const long positions = (long)B * N * N;
+  const int cus = device_cus();
+  if (cus <= 0) return pf_fail(PF_E_LAUNCH, "pf_trimul_fwd: cannot query the device");
+  const int grid_proj = (int)min((long)cus, (positions / 32 + TMP_WAVES - 1) / TMP_WAVES);
+  const int grid_out = (int)min((long)cus, (positions / 32 + TMO_WAVES - 1) / TMO_WAVES);
+  {
+    static bool attr = false;
+    if (!attr) {
+      if (hipFuncSetAttribute((const void*)tm_proj_kernel<CC>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)tmp_lds<CC>()) != hipSuccess)
+        return pf_fail(PF_E_LAUNCH, "tm_proj_kernel: cannot reserve %zu bytes of LDS", tmp_lds<CC>());
+      attr = true;
+    }
+    tm_proj_kernel<CC><<<grid_proj, 64 * TMP_WAVES, tmp_lds<CC>(), st>>>(
+        a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b, (const op_t*)a->p_in_w, (const op_t*)a->g_in_w, opA, opB, B,
+        N, a->direction, a->eps);
+    PF_CHECK_LAUNCH("tm_proj_kernel");
+  }
+  const int rc = launch_contract<op_t>(opA, opB, X, B * CC, N, X_STORE_SCALE, st);
+  if (rc != PF_OK) return rc;
+  {
+    static bool attr = false;
+    if (!attr) {
+      if (hipFuncSetAttribute((const void*)tm_out_kernel<op_t, CC>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)tmo_lds<CC>()) != hipSuccess)
+        return pf_fail(PF_E_LAUNCH, "tm_out_kernel: cannot reserve %zu bytes of LDS", tmo_lds<CC>());
+      attr = true;
+    }
+    const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);
+    tm_out_kernel<op_t, CC><<<grid_out, 64 * TMO_WAVES, tmo_lds<CC>(), st>>>(
+        X, X_LOAD_SCALE, a->z_in, a->out, a->norm_in_w, a->norm_in_b, a->norm_out_w, a->norm_out_b,
+        (const op_t*)a->p_out_w, (const op_t*)a->g_out_w, B, N, resid, a->eps);
+    PF_CHECK_LAUNCH("tm_out_kernel");
+  }
+  return PF_OK;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------------
 // C-ABI
 // ---------------------------------------------------------------------------------
 extern "C" size_t pf_trimul_workspace_size(int B, int N, int C_) {
-  if (B <= 0 || N <= 0 || C_ != C) return 0;
-  const size_t planes = (size_t)B * C * N * N;
+  if (B <= 0 || N <= 0 || (C_ != 128 && C_ != 64)) return 0;
+  const size_t planes = (size_t)B * C_ * N * N;
   return planes * 3 * sizeof(op_t);   // opA, opB, X
 }
 
 extern "C" int pf_trimul_fwd(const pf_trimul_args* a) {
   if (!a) return pf_fail(PF_E_INVALID, "pf_trimul_fwd: null args");
-  if (a->C != C) return pf_fail(PF_E_INVALID, "pf_trimul_fwd: only c_z = 128 is supported (got %d)", a->C);
-  if (a->hidden != C) return pf_fail(PF_E_INVALID, "pf_trimul_fwd: hidden must equal c_z = 128 (got %d)", a->hidden);
+  if (a->C != 128 && a->C != 64)
+    return pf_fail(PF_E_INVALID, "pf_trimul_fwd: c_z must be 128 or 64 (got %d)", a->C);
+  if (a->hidden != a->C) return pf_fail(PF_E_INVALID, "pf_trimul_fwd: hidden must equal c_z (got %d, %d)", a->hidden, a->C);
   if (a->B <= 0 || a->N <= 0 || a->N % 64)
     return pf_fail(PF_E_INVALID, "pf_trimul_fwd: need B > 0 and N a positive multiple of 64 (B=%d N=%d)", a->B, a->N);
   if ((unsigned long long)a->B * a->N * a->N >= (1ull << 32))
@@ -504,52 +560,7 @@ extern "C" int pf_trimul_fwd(const pf_trimul_args* a) {
   const size_t need = pf_trimul_workspace_size(a->B, a->N, a->C);
   if (a->workspace_bytes < need)
     return pf_fail(PF_E_INVALID, "pf_trimul_fwd: workspace too small (%zu < %zu bytes)", a->workspace_bytes, need);
-
-  hipStream_t st = (hipStream_t)a->stream;
-  const int B = a->B, N = a->N;
-  const size_t planes = (size_t)B * C * N * N;
-  op_t* opA = (op_t*)a->workspace;
-  op_t* opB = opA + planes;
-  op_t* X = opB + planes;
-
-  const long positions = (long)B * N * N;
-  {
-    static bool attr = false;
-    if (!attr) {
-      if (hipFuncSetAttribute((const void*)tm_proj_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)TMP_LDS) != hipSuccess)
-        return pf_fail(PF_E_LAUNCH, "tm_proj_kernel: cannot reserve %zu bytes of LDS", TMP_LDS);
-      attr = true;
-    }
-    const int cus = device_cus();
-    if (cus <= 0) return pf_fail(PF_E_LAUNCH, "tm_proj_kernel: cannot query the device");
-    const int grid = (int)min((long)cus, (positions / 32 + TMP_WAVES - 1) / TMP_WAVES);
-    tm_proj_kernel<<<grid, 64 * TMP_WAVES, TMP_LDS, st>>>(a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b,
-                                               (const op_t*)a->p_in_w, (const op_t*)a->g_in_w, opA, opB, B, N,
-                                               a->direction, a->eps);
-    PF_CHECK_LAUNCH("tm_proj_kernel");
-  }
-
-  const int rc = launch_contract<op_t>(opA, opB, X, B * C, N, X_STORE_SCALE, st);
-  if (rc != PF_OK) return rc;
-
-  {
-    static bool attr = false;
-    if (!attr) {
-      if (hipFuncSetAttribute((const void*)tm_out_kernel<op_t>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)TMO_LDS) != hipSuccess)
-        return pf_fail(PF_E_LAUNCH, "tm_out_kernel: cannot reserve %zu bytes of LDS", TMO_LDS);
-      attr = true;
-    }
-    const int grid = (int)min((long)device_cus(), (positions / 32 + TMO_WAVES - 1) / TMO_WAVES);
-    const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);
-    tm_out_kernel<op_t><<<grid, 64 * TMO_WAVES, TMO_LDS, st>>>(X, X_LOAD_SCALE, a->z_in, a->out, a->norm_in_w,
-                                                               a->norm_in_b, a->norm_out_w, a->norm_out_b,
-                                                               (const op_t*)a->p_out_w, (const op_t*)a->g_out_w, B, N,
-                                                               resid, a->eps);
-  }
-  PF_CHECK_LAUNCH("tm_out_kernel");
-  return PF_OK;
+  return a->C == 128 ? trimul_run<128>(a) : trimul_run<64>(a);
 }
 
 int pf_contract_rect(const void* A, const void* B, void* X, int x_fp32, int planes, int M, int Nc, int K,

@@ -102,8 +102,8 @@ def pad_pair_mask(pair_mask: Optional[torch.Tensor], B: int, N: int, n_pad: int,
 # --------------------------------------------------------------------------------------
 # launchers (padded, contiguous, device-resident inputs; weights pre-converted)
 # --------------------------------------------------------------------------------------
-def trimul_workspace_bytes(B: int, N: int, variant: str = DEFAULT_VARIANT) -> int:
-    return _lib.load(variant).pf_trimul_workspace_size(B, N, C_Z)
+def trimul_workspace_bytes(B: int, N: int, variant: str = DEFAULT_VARIANT, C: int = C_Z) -> int:
+    return _lib.load(variant).pf_trimul_workspace_size(B, N, C)
 
 
 def launch_trimul(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional[torch.Tensor],
@@ -121,8 +121,9 @@ def launch_trimul(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional[tor
     _lib.check(_lib.load(variant).pf_trimul_fwd(ctypes.byref(a)), "pf_trimul_fwd", variant)
 
 
-def triatt_workspace_bytes(B: int, N: int, H: int = 4, D: int = 32, variant: str = DEFAULT_VARIANT) -> int:
-    return _lib.load(variant).pf_triatt_workspace_size(B, N, C_Z, H, D)
+def triatt_workspace_bytes(B: int, N: int, H: int = 4, D: int = 32, variant: str = DEFAULT_VARIANT,
+                           C: int = C_Z) -> int:
+    return _lib.load(variant).pf_triatt_workspace_size(B, N, C, H, D)
 
 
 def launch_triatt(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional[torch.Tensor],

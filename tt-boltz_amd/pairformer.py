@@ -36,6 +36,8 @@ _FAST_MODE = False
 _device: Optional[torch.device] = None
 
 C_Z = 128
+#: pair widths the kernels are built for: the trunk (128) and the template stack (64)
+C_Z_SUPPORTED = (128, 64)
 
 
 def set_fast_mode(enabled: bool) -> None:
@@ -141,8 +143,12 @@ class TriangleMultiplication(Module):
     def __init__(self, ending: bool, state_dict, options: Optional[Options] = None):
         super().__init__(state_dict, options)
         self.ending = ending
-        if self.weights["p_in.weight"].shape != (2 * C_Z, C_Z):
-            raise NotImplementedError(f"only c_z = {C_Z} is supported (p_in {tuple(self.weights['p_in.weight'].shape)})")
+        self.C = self.weights["p_in.weight"].shape[1]
+        if self.C not in C_Z_SUPPORTED or self.weights["p_in.weight"].shape != (2 * self.C, self.C):
+            raise NotImplementedError(f"only c_z in {C_Z_SUPPORTED} is supported "
+                                      f"(p_in {tuple(self.weights['p_in.weight'].shape)})")
+        # the fp8 kernels are built for c_z = 128; the template stack (c_z = 64) stays 16-bit
+        self.fast = self.fast and self.C == C_Z
         self.w = {k: self.vec(k) for k in ("norm_in.weight", "norm_in.bias", "norm_out.weight", "norm_out.bias")}
         if self.fast:
             self.w.update(ops.mx8_weights(self.weights, self.device, ops.TRIMUL_MX8_KEYS, self.variant))
@@ -152,11 +158,11 @@ class TriangleMultiplication(Module):
     def workspace_bytes(self, B: int, N: int) -> int:
         if self.fast:
             return ops.trimul_mx8_workspace_bytes(B, N, self.variant)
-        return ops.trimul_workspace_bytes(B, N, self.variant)
+        return ops.trimul_workspace_bytes(B, N, self.variant, self.C)
 
     def __call__(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                  accumulate: bool = False, ws: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """x [B,N,N,128] fp32 device, N % 64 == 0 (N % 128 == 0 in fast mode).
+        """x [B,N,N,c_z] fp32 device, N % 64 == 0 (N % 128 == 0 in fast mode).
         Returns the update (or ``out`` += update)."""
         B, N = x.shape[0], x.shape[1]
         if ws is None:
@@ -180,12 +186,15 @@ class TriangleAttention(Module):
         if (head_dim, n_heads) != (32, 4):
             raise NotImplementedError(f"only 4 heads x 32 are supported (got {n_heads} x {head_dim})")
         self.head_dim, self.n_heads, self.ending, self.affinity = head_dim, n_heads, ending, affinity
+        self.C = self.weights["layer_norm.weight"].shape[0]
+        if self.C not in C_Z_SUPPORTED:
+            raise NotImplementedError(f"only c_z in {C_Z_SUPPORTED} is supported (got {self.C})")
         self.w = {k: self.vec(k) for k in ("layer_norm.weight", "layer_norm.bias")}
         self.w.update({k: self.mat(k) for k in ("linear.weight", "linear_q.weight", "linear_k.weight",
                                                 "linear_v.weight", "linear_g.weight", "linear_o.weight")})
 
     def workspace_bytes(self, B: int, N: int) -> int:
-        return ops.triatt_workspace_bytes(B, N, self.n_heads, self.head_dim, self.variant)
+        return ops.triatt_workspace_bytes(B, N, self.n_heads, self.head_dim, self.variant, self.C)
 
     def __call__(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                  accumulate: bool = False, ws: Optional[torch.Tensor] = None, n_valid: int = 0) -> torch.Tensor:
