@@ -593,3 +593,36 @@ def test_confidence_config_stack(gpu):
     nv = N - 7
     check("confidence 8-layer stack z (valid)", z_got[:, :nv, :nv], z_ref[:, :nv, :nv])
     check("confidence 8-layer stack s (valid)", s_got[:, :nv], s_ref[:, :nv])
+
+
+def test_msa_module_batch2(gpu):
+    """Two structures in one batch (B = 2, different masks and MSA depths' padding) through
+    the device MSA stack, each compared with the oracle run on its own."""
+    from tt_boltz_amd import msa as msa_mod
+    N, S = 64, 24
+    w = synthetic.draw(synthetic.msa_module_shapes(1), 84)
+    g = torch.Generator().manual_seed(85)
+    z = torch.randn((2, N, N, 128), generator=g)
+    emb = torch.randn((2, N, 384), generator=g)
+    f0, f1 = _msa_feats(S, N, 86, pad_tail=5), _msa_feats(S, N, 87)
+    f1["msa_mask"][:, S - 6:] = 0.0   # the second structure has fewer sequences
+    feats = {k: torch.cat([f0[k], f1[k]]) for k in f0}
+    want = torch.cat([msa_ref.msa_module(z[i:i + 1], emb[i:i + 1], f, w, 1) for i, f in enumerate((f0, f1))])
+    mod = msa_mod.MSAModule(1, 32, 8, 32, 4)
+    mod.load_state_dict(w)
+    got = mod(z, emb, feats)
+    check("MSA module B=2 (structure 0, valid)", got[0, :N - 5, :N - 5], want[0, :N - 5, :N - 5])
+    check("MSA module B=2 (structure 1)", got[1], want[1])
+
+
+def test_template_stack_batch(gpu):
+    """c_z = 64 stack on a batch of 3 templates (the template module's batch axis), each
+    against the oracle on its own."""
+    N = 64
+    w = synthetic.stack_weights(1, 48, c_z=64, transform_s=False)
+    z = torch.randn((3, N, N, 64), generator=torch.Generator().manual_seed(49))
+    pm = torch.ones((1, N, N))
+    want = torch.cat([ref.pairformer_stack(None, z[i:i + 1], None, pm, w, 1)[1] for i in range(3)])
+    pf = pairformer.Pairformer(1, 32, 4, None, None, False, w)
+    _, got = pf(None, z.to(gpu).contiguous(), None, None)
+    check("template stack batch of 3", got, want)
