@@ -265,6 +265,47 @@ def template_bench(N: int = 512, T: int = 4, seed: int = 7, steps: int = 5) -> d
             "finite": bool(torch.isfinite(z).all())}
 
 
+def msa_trunk_bench(N: int = 768, S: int = 1024, msa_blocks: int = 4, n_layers: int = 64, recycling_steps: int = 3,
+                    seed: int = 8) -> dict:
+    """The trunk loop with the MSA module on the device: each of the 4 passes runs the
+    recycling projections, z = z + MSA(z) (4 MSA blocks over S sequences) and the 64-layer
+    Pairformer (boltz2.py:5203-5248), nothing leaving the GPU; reported next to the same loop
+    without the MSA module (the stack object)."""
+    import torch
+    from tt_boltz_amd import msa as msa_mod, pairformer, synthetic
+    dev = pairformer.get_device()
+    stream = torch.cuda.current_stream()
+    w = synthetic.stack_weights(n_layers, seed)
+    w_rec = synthetic.draw(synthetic.recycle_shapes(), seed + 1000)
+    w_msa = synthetic.draw(synthetic.msa_module_shapes(msa_blocks), seed + 2000)
+    s_cpu, z_cpu, mask_cpu, _ = synthetic.pair_inputs(N, seed, z_scale=0.5)
+    g = torch.Generator().manual_seed(seed)
+    feats = {"msa": torch.randint(0, msa_mod.NUM_TOKENS, (1, S, N), generator=g),
+             "has_deletion": (torch.rand((1, S, N), generator=g) > 0.8).float(),
+             "deletion_value": torch.rand((1, S, N), generator=g),
+             "msa_paired": (torch.rand((1, S, N), generator=g) > 0.5).float(),
+             "msa_mask": torch.ones((1, S, N))}
+    emb = torch.randn((1, N, 384), generator=g)
+    pf = pairformer.Pairformer(n_layers, 32, 4, 24, 16, True, w)
+    rec = pairformer.TrunkRecycler(pf, w_rec, msa=msa_mod.MSA(msa_blocks, 32, 8, 32, 4, w_msa))
+    inputs = msa_mod.device_inputs(emb, feats, N, dev)
+    s0, z0, mask = s_cpu.to(dev), z_cpu.to(dev), mask_cpu.to(dev)
+    rec(s0, z0, mask, 0, msa_inputs=inputs)   # warm-up pass
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    s_out, z_out = rec(s0, z0, mask, recycling_steps, msa_inputs=inputs)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    trunk_s = e0.elapsed_time(e1) / 1e3
+    passes = recycling_steps + 1
+    return {"N": N, "S": S, "msa_blocks": msa_blocks, "layers": n_layers, "passes": passes,
+            "trunk_s": round(trunk_s, 4), "pass_s": round(trunk_s / passes, 4),
+            "finite": bool(torch.isfinite(z_out).all() and torch.isfinite(s_out).all()),
+            "workload": f"Boltz-2 trunk with the MSA module on the device: {msa_blocks} MSA blocks over S={S} "
+                        f"sequences + {n_layers} Pairformer layers per pass, N={N}, {passes} passes, masks all ones"}
+
+
 def fast_bench(N: int = 1024, seed: int = 4, steps: int = 5) -> dict:
     """Config 4: one layer in fast mode (MXFP8 triangle multiplications and pair
     transition) at N=1024 next to the same layer in 16-bit, plus the fp8 contraction alone."""
@@ -475,6 +516,8 @@ def main() -> int:
         out["diffusion_pair"] = diffusion_bench()
         torch.cuda.empty_cache()
         out["template"] = template_bench()
+        torch.cuda.empty_cache()
+        out["msa_trunk"] = msa_trunk_bench()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(N, seed)
     print(json.dumps(out), flush=True)
