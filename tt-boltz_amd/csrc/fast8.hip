@@ -221,24 +221,24 @@ __global__ __launch_bounds__(256, 2) void tm8_proj_kernel(
 
 // ---------------------------------------------------------------------------------
 // Contraction X[p][i][j] = sum_k A[p][i][k] * B[p][j][k] on MXFP8 planes.
-// 256x256 output tile per workgroup, 4 waves of 128x128 (as the 16-bit kernel); slabs
-// of 128 k (128 bytes per row) move global -> LDS by DMA through a 2-deep ring with the
-// same XOR row swizzle; the scale dwords (4 blocks of the slab) are prefetched into
-// registers one slab ahead.
+// 256x256 output tile per workgroup of 8 waves (two per SIMD), each 128 (i) x 64 (j), as
+// the 16-bit kernel; slabs of 128 k (128 bytes per row) move global -> LDS by DMA through a
+// 2-deep ring with the same XOR row swizzle; the scale dwords (4 blocks of the slab) are
+// prefetched into registers one slab ahead.
 // ---------------------------------------------------------------------------------
-constexpr int BT = 256, SK = 128;
+constexpr int BT = 256, SK = 128, TM8C_WAVES = 8;
 constexpr int SLAB8 = BT * SK;                        // bytes per operand slab
 constexpr size_t TM8C_LDS = (size_t)2 * 2 * SLAB8;
 PF_DEV int slab_swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 
 template <typename OutT>
-__global__ __launch_bounds__(256, 1) void tm8_contract_kernel(
+__global__ __launch_bounds__(64 * TM8C_WAVES, 1) void tm8_contract_kernel(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bop, const uint8_t* __restrict__ SA,
     const uint8_t* __restrict__ SB, OutT* __restrict__ X, int N, int tpd, int total, float out_scale) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem8[];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wid >> 1, wn = wid & 1;
+  const int wm = wid >> 2, wn = wid & 3;
   const int w = xcd_remap(blockIdx.x, total);
   const int tiles = tpd * tpd;
   const long plane = w / tiles;
@@ -247,59 +247,59 @@ __global__ __launch_bounds__(256, 1) void tm8_contract_kernel(
   const long NN = (long)N * N;
   const int NB = N / 32;
 
-  int offA[8], offB[8];
+  // DMA: instruction q (0..3) of this wave covers slab rows (4*wid + q)*8 + (lane >> 3)
+  int offA[4], offB[4];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int r = (8 * wid + q) * 8 + (lane >> 3);
+  for (int q = 0; q < 4; ++q) {
+    const int r = (4 * wid + q) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ slab_swz8(r);
     offA[q] = min(i0 + r, N - 1) * N + 16 * c;
     offB[q] = min(j0 + r, N - 1) * N + 16 * c;
   }
   const uint8_t* Ap = A + plane * NN;
   const uint8_t* Bp = Bop + plane * NN;
-  // scale rows of this lane's fragments: A rows i0 + wm*128 + 32x + m, B rows j0 + wn*128 + 32y + m
+  // scale rows of this lane's fragments: A rows i0 + wm*128 + 32x + m, B rows j0 + wn*64 + 32y + m
   const uint8_t* sArow[4];
-  const uint8_t* sBrow[4];
+  const uint8_t* sBrow[2];
 #pragma unroll
-  for (int x = 0; x < 4; ++x) {
-    sArow[x] = SA + (plane * N + min(i0 + wm * 128 + 32 * x + m, N - 1)) * NB;
-    sBrow[x] = SB + (plane * N + min(j0 + wn * 128 + 32 * x + m, N - 1)) * NB;
-  }
+  for (int x = 0; x < 4; ++x) sArow[x] = SA + (plane * N + min(i0 + wm * 128 + 32 * x + m, N - 1)) * NB;
+#pragma unroll
+  for (int y = 0; y < 2; ++y) sBrow[y] = SB + (plane * N + min(j0 + wn * 64 + 32 * y + m, N - 1)) * NB;
   auto issue = [&](int kt) {
     uint8_t* sa = smem8 + (kt & 1) * 2 * SLAB8;
     uint8_t* sb = sa + SLAB8;
     const int ko = kt * SK;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      __builtin_amdgcn_global_load_lds(Ap + offA[q] + ko, sa + (8 * wid + q) * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(Bp + offB[q] + ko, sb + (8 * wid + q) * 1024, 16, 0, 0);
+    for (int q = 0; q < 4; ++q) {
+      __builtin_amdgcn_global_load_lds(Ap + offA[q] + ko, sa + (4 * wid + q) * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(Bp + offB[q] + ko, sb + (4 * wid + q) * 1024, 16, 0, 0);
     }
   };
-  int scA[4], scB[4], nscA[4], nscB[4];
-  auto load_scales = [&](int kt, int (&a)[4], int (&b)[4]) {
+  int scA[4], scB[2], nscA[4], nscB[2];
+  auto load_scales = [&](int kt, int (&a)[4], int (&b)[2]) {
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      a[x] = *reinterpret_cast<const int*>(sArow[x] + 4 * kt);
-      b[x] = *reinterpret_cast<const int*>(sBrow[x] + 4 * kt);
-    }
+    for (int x = 0; x < 4; ++x) a[x] = *reinterpret_cast<const int*>(sArow[x] + 4 * kt);
+#pragma unroll
+    for (int y = 0; y < 2; ++y) b[y] = *reinterpret_cast<const int*>(sBrow[y] + 4 * kt);
   };
   const int swz = slab_swz8(m);
-  const int rdA = (wm * 128 + m) * SK, rdB = (wn * 128 + m) * SK;
-  auto read_frags = [&](int kt, int s, i32x8 (&fa)[4], i32x8 (&fb)[4]) {
+  const int rdA = (wm * 128 + m) * SK, rdB = (wn * 64 + m) * SK;
+  auto read_frags = [&](int kt, int s, i32x8 (&fa)[4], i32x8 (&fb)[2]) {
     const uint8_t* sa = smem8 + (kt & 1) * 2 * SLAB8;
     const uint8_t* sb = sa + SLAB8;
     const int c0 = 16 * ((4 * s + h) ^ swz), c1 = 16 * ((4 * s + 2 + h) ^ swz);
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
+    for (int x = 0; x < 4; ++x)
       fa[x] = cat_i32x4(*reinterpret_cast<const i32x4*>(sa + rdA + 32 * x * SK + c0),
                         *reinterpret_cast<const i32x4*>(sa + rdA + 32 * x * SK + c1));
-      fb[x] = cat_i32x4(*reinterpret_cast<const i32x4*>(sb + rdB + 32 * x * SK + c0),
-                        *reinterpret_cast<const i32x4*>(sb + rdB + 32 * x * SK + c1));
-    }
-  };
-  f32x16 acc[4][4];
 #pragma unroll
-  for (int y = 0; y < 4; ++y)
+    for (int y = 0; y < 2; ++y)
+      fb[y] = cat_i32x4(*reinterpret_cast<const i32x4*>(sb + rdB + 32 * y * SK + c0),
+                        *reinterpret_cast<const i32x4*>(sb + rdB + 32 * y * SK + c1));
+  };
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int y = 0; y < 2; ++y)
 #pragma unroll
     for (int x = 0; x < 4; ++x) acc[y][x] = zero16();
 
@@ -311,7 +311,9 @@ __global__ __launch_bounds__(256, 1) void tm8_contract_kernel(
     __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
     __builtin_amdgcn_s_barrier();
 #pragma unroll
-    for (int x = 0; x < 4; ++x) { scA[x] = nscA[x]; scB[x] = nscB[x]; }
+    for (int x = 0; x < 4; ++x) scA[x] = nscA[x];
+#pragma unroll
+    for (int y = 0; y < 2; ++y) scB[y] = nscB[y];
     if (kt + 1 < nk) {
       issue(kt + 1);
       load_scales(kt + 1, nscA, nscB);
@@ -319,11 +321,11 @@ __global__ __launch_bounds__(256, 1) void tm8_contract_kernel(
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      i32x8 fa[4], fb[4];
+      i32x8 fa[4], fb[2];
       read_frags(kt, s, fa, fb);
       const int sh = 8 * (2 * s + h);    // this lane supplies the scale of block 2s + h
 #pragma unroll
-      for (int y = 0; y < 4; ++y)
+      for (int y = 0; y < 2; ++y)
 #pragma unroll
         for (int x = 0; x < 4; ++x)
           acc[y][x] = mfma8(fb[y], fa[x], acc[y][x], (scB[y] >> sh) & 0xFF, (scA[x] >> sh) & 0xFF);
@@ -335,23 +337,19 @@ __global__ __launch_bounds__(256, 1) void tm8_contract_kernel(
   for (int x = 0; x < 4; ++x) {
     const int ib = i0 + wm * 128 + 32 * x;
 #pragma unroll
-    for (int y = 0; y < 4; ++y) {
-      const int jb = j0 + wn * 128 + 32 * y;
+    for (int y = 0; y < 2; ++y) {
+      const int jb = j0 + wn * 64 + 32 * y;
       if (ib >= N || jb >= N) continue;
+      if constexpr (sizeof(OutT) == 4) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        OutT* dst = Xp + (long)(ib + m) * N + jb + 8 * g + 4 * h;
-        if constexpr (sizeof(OutT) == 4) {
+        for (int g = 0; g < 4; ++g) {
           f32x4 v;
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = acc[y][x][4 * g + e] * out_scale;
-          *reinterpret_cast<f32x4*>(dst) = v;
-        } else {
-          opx4 v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (op_t)(acc[y][x][4 * g + e] * out_scale);
-          st_x4((op_t*)dst, v);
+          *reinterpret_cast<f32x4*>(Xp + (long)(ib + m) * N + jb + 8 * g + 4 * h) = v;
         }
+      } else {
+        store_runs16((op_t*)(Xp + (long)(ib + m) * N + jb), acc[y][x], out_scale, h);   // 16-byte runs
       }
     }
   }
@@ -656,7 +654,7 @@ extern "C" int pf_trimul_mx8_fwd(const pf_trimul_mx8_args* a) {
   PF_CHECK_LAUNCH("tm8_proj_kernel");
   const int tpd = (N + BT - 1) / BT;
   const int total = B * C * tpd * tpd;
-  tm8_contract_kernel<op_t><<<total, 256, TM8C_LDS, st>>>(t.A8, t.B8, t.SA, t.SB, t.X, N, tpd, total, X_STORE_SCALE);
+  tm8_contract_kernel<op_t><<<total, 64 * TM8C_WAVES, TM8C_LDS, st>>>(t.A8, t.B8, t.SA, t.SB, t.X, N, tpd, total, X_STORE_SCALE);
   PF_CHECK_LAUNCH("tm8_contract_kernel");
   const long nsteps = (long)B * N * N / 128;
   tm8_out_kernel<op_t><<<(int)(nsteps < 2048 ? nsteps : 2048), 256, TM8O_LDS, st>>>(t.X, X_LOAD_SCALE, a->z_in, a->out, a->norm_in_w,
@@ -681,7 +679,7 @@ extern "C" int pf_trimul_mx8_contract(const void* A8, const void* B8, const void
   }
   const int tpd = (N + BT - 1) / BT;
   const int total = planes * tpd * tpd;
-  tm8_contract_kernel<float><<<total, 256, TM8C_LDS, (hipStream_t)stream>>>(
+  tm8_contract_kernel<float><<<total, 64 * TM8C_WAVES, TM8C_LDS, (hipStream_t)stream>>>(
       (const uint8_t*)A8, (const uint8_t*)B8, (const uint8_t*)SA, (const uint8_t*)SB, X, N, tpd, total, 1.f);
   PF_CHECK_LAUNCH("tm8_contract_kernel");
   return PF_OK;
