@@ -4,8 +4,8 @@
 //   cond_proj_kernel   PairwiseConditioning's input projection (tt_bio/boltz2.py:1318-1355):
 //                      out = W . LN(cat(z_trunk, rel_pos)) over 256 channels (LayerNorm with
 //                      affine, folded into W as below; LinearNoBias 256 -> 128).  The two
-//                      transitions that follow
-//                      run on the pair transition kernel (transition.hip).
+//                      transitions that follow run on the pair transition kernel
+//                      (transition.hip).
 //   token_bias_kernel  DiffusionConditioning's token-transformer pair bias
 //                      (tt_bio/boltz2.py:2434-2441, 2472-2475; the ttnn compute_bias of
 //                      tt_bio/tenstorrent.py:714-728): for each of L layers,
