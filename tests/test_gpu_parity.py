@@ -626,3 +626,28 @@ def test_template_stack_batch(gpu):
     pf = pairformer.Pairformer(1, 32, 4, None, None, False, w)
     _, got = pf(None, z.to(gpu).contiguous(), None, None)
     check("template stack batch of 3", got, want)
+
+
+def test_msa_ops_deep_msa(gpu):
+    """A deep MSA (S = 4096 sequences, N = 256): the outer product mean (K = 4096 in its
+    contraction, mask counts up to 4096) and the pair weighted averaging against the fp32
+    oracle evaluated on the GPU (the same torch code, fp32 on the device for speed)."""
+    S, N = 4096, 256
+    g = torch.Generator().manual_seed(88)
+    m = torch.randn((1, S, N, 64), generator=g).to(gpu)
+    mask = (torch.rand((1, S, N), generator=g) > 0.3).float().to(gpu)
+    z = torch.randn((1, N, N, 128), generator=g).to(gpu)
+    w_o = {k: v.to(gpu) for k, v in _msa_sub(73, "outer_product_mean").items()}
+    want = z + msa_ref.outer_product_mean(m, mask, w_o)
+    zd = z.clone()
+    ws = ops.workspace(ops.opm_workspace_bytes(1, S, N), gpu)
+    ops.launch_opm(m.contiguous(), mask.contiguous(), zd, _dev_w(w_o, gpu), ws)
+    check(f"outer product mean S={S} N={N}", zd, want)
+    del ws, want, zd
+    w_p = {k: v.to(gpu) for k, v in _msa_sub(74, "pair_weighted_averaging").items()}
+    pm = torch.ones((1, N, N), device=gpu)
+    want = m + msa_ref.pair_weighted_averaging(m, z, pm, w_p)
+    md = m.clone()
+    ws = ops.workspace(ops.pwa_workspace_bytes(1, S, N), gpu)
+    ops.launch_pwa(md, z, pm, md, _dev_w(w_p, gpu), ws)
+    check(f"pair weighted averaging S={S} N={N}", md, want)
