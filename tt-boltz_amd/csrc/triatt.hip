@@ -351,48 +351,84 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
       }
     return ls;
   };
-  // One 32-key half of a step: scores S'^T = K.Q^T + I.bias^T + [1, mask].[-m, 1]^T, the
-  // softmax (P against the current reference; if a query has no reference yet or the
-  // row sum exceeds LSTEP_MAX the reference moves, o and lsum are rescaled and P is packed
-  // again -- after a move P <= 2^RESCALE_SLACK, so once is enough), then P.V.
-  auto half = [&](const char* st, int kb0, auto kbt) PF_INLINE {
-    constexpr int kb = decltype(kbt)::value;
-    const opx8 k0 = lds_x8(st + aK[0] + 2048 * kb), k1 = lds_x8(st + aK[1] + 2048 * kb);
-    const opx8 b0 = lds_x8(st + aB[2 * kb]), b1 = lds_x8(st + aB[2 * kb + 1]);
-    uint32_t mk;
-    if (live) mk = *reinterpret_cast<const uint16_t*>(st + aM + 64 * kb);
-    else mk = half_bits((op_t)(kb0 + 32 * kb + m < n_valid ? 0.f : -INFINITY));
-    f32x16 sc = mfma32(k0, qf[0], zero16());
-    sc = mfma32(k1, qf[1], sc);
-    sc = mfma32(iden[0], b0, sc);
-    sc = mfma32(iden[1], b1, sc);
-    sc = mfma32(slots01(h, ONE | mk << 16), fb, sc);
-    const opx8 v0 = lds_x8(st + dV + aB[2 * kb]), v1 = lds_x8(st + dV + aB[2 * kb + 1]);
-    u32x4 pf[2];
-    float l = exp_pack(sc, pf);
-    if (__ballot(!mset || l > LSTEP_MAX) != 0) {
-      float mx = sc[0];
+  // One step = two 32-key halves.  Each half forms its scores S'^T = K.Q^T + I.bias^T +
+  // [1, mask].[-m, 1]^T, the softmax (P against the current reference; if a query has no
+  // reference yet or the row sum exceeds LSTEP_MAX the reference moves, o and lsum are
+  // rescaled and P is packed again -- after a move P <= 2^RESCALE_SLACK, so once is
+  // enough), then P.V.  The halves are software-pipelined: the scores of half 1 are issued
+  // before the softmax of half 0, so half 0's exp / pack VALU work runs while half 1's
+  // score MFMAs execute, and half 1's while half 0's P.V MFMAs execute.  A rescale in
+  // half 0 moves the reference under half 1's already formed scores: they are shifted by
+  // the same amount.
+  auto rescale = [&](f32x16& sc, u32x4 (&pf)[2], float& l, f32x16* other) PF_INLINE {
+    float mx = sc[0];
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[r]);
-      mx = xor32_max(mx);
-      const float d = mset ? (mx > RESCALE_SLACK ? mx : 0.f) : (mx == -INFINITY ? 0.f : mx);
-      const float mnew = (float)(op_t)(mh + d);
-      const float dsub = mnew - mh;
-      const float alpha = mset ? exp2_fast(-dsub) : 1.f;
-      lsum *= alpha;
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[r]);
+    mx = xor32_max(mx);
+    const float d = mset ? (mx > RESCALE_SLACK ? mx : 0.f) : (mx == -INFINITY ? 0.f : mx);
+    const float mnew = (float)(op_t)(mh + d);
+    const float dsub = mnew - mh;
+    const float alpha = mset ? exp2_fast(-dsub) : 1.f;
+    lsum *= alpha;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        o[r] *= alpha;
-        sc[r] -= dsub;
-      }
-      mset = mset || mx != -INFINITY;
-      mh = mnew;
-      fb = fold_b(mnew);
-      l = exp_pack(sc, pf);
+    for (int r = 0; r < 16; ++r) {
+      o[r] *= alpha;
+      sc[r] -= dsub;
     }
+    if (other) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) (*other)[r] -= dsub;
+    }
+    mset = mset || mx != -INFINITY;
+    mh = mnew;
+    fb = fold_b(mnew);
+    l = exp_pack(sc, pf);
+  };
+  auto step2 = [&](const char* st, int kb0) PF_INLINE {
+    uint32_t mk0, mk1;
+    if (live) {
+      mk0 = *reinterpret_cast<const uint16_t*>(st + aM);
+      mk1 = *reinterpret_cast<const uint16_t*>(st + aM + 64);
+    } else {
+      mk0 = half_bits((op_t)(kb0 + m < n_valid ? 0.f : -INFINITY));
+      mk1 = half_bits((op_t)(kb0 + 32 + m < n_valid ? 0.f : -INFINITY));
+    }
+    f32x16 sc0, sc1;
+    {
+      const opx8 k0 = lds_x8(st + aK[0]), k1 = lds_x8(st + aK[1]);
+      const opx8 b0 = lds_x8(st + aB[0]), b1 = lds_x8(st + aB[1]);
+      sc0 = mfma32(k0, qf[0], zero16());
+      sc0 = mfma32(k1, qf[1], sc0);
+      sc0 = mfma32(iden[0], b0, sc0);
+      sc0 = mfma32(iden[1], b1, sc0);
+      sc0 = mfma32(slots01(h, ONE | mk0 << 16), fb, sc0);
+    }
+    {
+      const opx8 k0 = lds_x8(st + aK[0] + 2048), k1 = lds_x8(st + aK[1] + 2048);
+      const opx8 b0 = lds_x8(st + aB[2]), b1 = lds_x8(st + aB[3]);
+      sc1 = mfma32(k0, qf[0], zero16());
+      sc1 = mfma32(k1, qf[1], sc1);
+      sc1 = mfma32(iden[0], b0, sc1);
+      sc1 = mfma32(iden[1], b1, sc1);
+      sc1 = mfma32(slots01(h, ONE | mk1 << 16), fb, sc1);
+    }
+    u32x4 pf[2];
+    float l = exp_pack(sc0, pf);
+    if (__ballot(!mset || l > LSTEP_MAX) != 0) rescale(sc0, pf, l, &sc1);
     lsum += l;
-    o = mfma32(v0, as_x8(pf[0]), o);
-    o = mfma32(v1, as_x8(pf[1]), o);
+    {
+      const opx8 v0 = lds_x8(st + dV + aB[0]), v1 = lds_x8(st + dV + aB[1]);
+      o = mfma32(v0, as_x8(pf[0]), o);
+      o = mfma32(v1, as_x8(pf[1]), o);
+    }
+    l = exp_pack(sc1, pf);
+    if (__ballot(!mset || l > LSTEP_MAX) != 0) rescale(sc1, pf, l, nullptr);
+    lsum += l;
+    {
+      const opx8 v0 = lds_x8(st + dV + aB[2]), v1 = lds_x8(st + dV + aB[3]);
+      o = mfma32(v0, as_x8(pf[0]), o);
+      o = mfma32(v1, as_x8(pf[1]), o);
+    }
   };
   auto finalize = [&](int hd) PF_INLINE {
     const float inv = rcp_fast(xor32_sum(lsum));
@@ -413,8 +449,6 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
 
   // Step loop: T steps, one barrier each (the loop-top wait + barrier), the DMA of the
   // next stage and, at a head's last tile, the next head's Q prefetch; then the two halves.
-  using K0 = std::integral_constant<int, 0>;
-  using K1 = std::integral_constant<int, 1>;
   int cur = 0;          // stage byte offset of step it
   int kbi = 0, hd = 0;  // step it = hd * nKB + kbi
   q_load(0);
@@ -436,8 +470,7 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
     if (qvalid) {
       if (kbi == 0) head_start();
       const char* st = alds + cur;
-      half(st, 64 * kbi, K0{});
-      half(st, 64 * kbi, K1{});
+      step2(st, 64 * kbi);
       if (kbi == nKB - 1) finalize(hd);
     }
     cur = nst;
