@@ -176,3 +176,27 @@ def test_module_fast_mode(gpu):
         assert mn_e <= 3e-2 and mx_e <= 0.5, (name, mx_e, mn_e)
         assert mn_f <= F32_MEAN and mx_f <= F32_MAX, (name, mx_f, mn_f)
         assert mn_e <= 0.6 * mn_f, (name, mn_e, mn_f)
+
+
+def test_template_stack_in_fast_mode_stays_16bit(gpu):
+    """With fast mode on, a c_z = 64 stack (the template module's) keeps its 16-bit kernels
+    (the MXFP8 kernels are built for c_z = 128): same tolerance as the 16-bit path."""
+    N = 64
+    w = synthetic.stack_weights(1, 52, c_z=64, transform_s=False)
+    _, z, _, _ = synthetic.pair_inputs(N, 53, c_z=64, with_s=False)
+    pm = torch.ones((1, N, N))
+    _, want = ref.pairformer_stack(None, z, None, pm, w, 1)
+    pairformer.set_fast_mode(True)
+    try:
+        mod = pairformer.PairformerModule(1, 32, 4, None, None, False)
+        mod.load_state_dict(w)
+    finally:
+        pairformer.set_fast_mode(False)
+    assert not mod.module.blocks[0].triangle_multiplication_start.fast
+    assert not mod.module.blocks[0].transition_z.fast
+    _, got = mod(None, z, pair_mask=pm)
+    r = want.pow(2).mean().sqrt()
+    d = (got - want).abs()
+    print(f"[fast] template stack in fast mode: max/rms={(d.max() / r).item():.3e} mean/rms={(d.mean() / r).item():.3e}",
+          flush=True)
+    assert (d.max() / r).item() <= 2e-2 and (d.mean() / r).item() <= 2e-3
