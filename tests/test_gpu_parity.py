@@ -79,6 +79,24 @@ def test_contract_matches_fp32_matmul(gpu, N, variant):
     assert bool(((got - want).abs() <= rel * want.abs() + slack).all())
 
 
+def test_contract_768_full_chip(gpu):
+    """128 planes at N = 768 (the north-star stack's contraction, edge-free 256x256 tiles
+    over 4.5 rounds of the chip) against an fp32 matmul of the same operand-type values on
+    the device (one rounding of the fp16 output)."""
+    N = 768
+    g = torch.Generator().manual_seed(768)
+    A = torch.randn((128, N, N), generator=g).half().to(gpu)
+    Bm = torch.randn((128, N, N), generator=g).half().to(gpu)
+    want = torch.bmm(A.float(), Bm.float().transpose(1, 2).contiguous())
+    X = torch.empty((128, N, N), dtype=torch.float16, device=gpu)
+    ops.launch_trimul_contract(A, Bm, X, "fp16")
+    got = X.float() * 256.0
+    slack = 1e-5 * want.pow(2).mean().sqrt()
+    bad = ((got - want).abs() > 2 ** -10 * want.abs() + slack).sum().item()
+    print(f"[parity] contract N=768 x128: elements outside one rounding: {bad}", flush=True)
+    assert bad == 0
+
+
 # ------------------------------------------------------------------------------ triangle multiplication
 @pytest.mark.parametrize("N,direction,rand_mask", [(64, "outgoing", False), (64, "incoming", True),
                                                    (192, "outgoing", True), (192, "incoming", False)])
