@@ -669,3 +669,21 @@ def test_msa_ops_deep_msa(gpu):
     ws = ops.workspace(ops.pwa_workspace_bytes(1, S, N), gpu)
     ops.launch_pwa(md, z, pm, md, _dev_w(w_p, gpu), ws)
     check(f"pair weighted averaging S={S} N={N}", md, want)
+
+
+@pytest.mark.parametrize("ending", [False, True])
+def test_triatt_n1024(gpu, ending):
+    """N = 1024 (the flash kernel never materialises the N^3 logits), padded tail of 100
+    tokens, against the fp32 oracle evaluated on the device in row chunks of 64."""
+    N, pad = 1024, 100
+    prefix = "tri_att_end" if ending else "tri_att_start"
+    w = _sub_w(60, prefix)
+    _, z, _, pm = _inputs(N, 61, pad_tail=pad)
+    zd, pmd = z.to(gpu).contiguous(), pm.to(gpu).contiguous()
+    want = ref.triangle_attention(zd, pmd, {k: v.to(gpu) for k, v in w.items()}, not ending, 64)
+    out = torch.empty_like(zd)
+    ws = ops.workspace(ops.triatt_workspace_bytes(1, N), gpu)
+    ops.launch_triatt(zd, out, pmd, _dev_w(w, gpu, "mha."), ending, ws, accumulate=False)
+    nv = N - pad
+    check(f"triatt N=1024 ending={ending} valid", out[:, :nv, :nv], want[:, :nv, :nv])
+    check(f"triatt N=1024 ending={ending} full", out, want)
