@@ -687,3 +687,19 @@ def test_triatt_n1024(gpu, ending):
     nv = N - pad
     check(f"triatt N=1024 ending={ending} valid", out[:, :nv, :nv], want[:, :nv, :nv])
     check(f"triatt N=1024 ending={ending} full", out, want)
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_n1024(gpu, direction):
+    """16-bit triangle multiplication at N = 1024 (contraction past the ridge point), random
+    pair mask with a padded tail, against the fp32 oracle evaluated on the device."""
+    N = 1024
+    prefix = "tri_mul_out" if direction == "outgoing" else "tri_mul_in"
+    w = _sub_w(62, prefix)
+    _, z, _, pm = _inputs(N, 63, pad_tail=80, rand_mask=True)
+    zd, pmd = z.to(gpu).contiguous(), pm.to(gpu).contiguous()
+    want = ref.triangle_multiplication(zd, pmd, {k: v.to(gpu) for k, v in w.items()}, direction)
+    out = torch.empty_like(zd)
+    ws = ops.workspace(ops.trimul_workspace_bytes(1, N), gpu)
+    ops.launch_trimul(zd, out, pmd, _dev_w(w, gpu), 0 if direction == "outgoing" else 1, ws, accumulate=False)
+    check(f"trimul N=1024 {direction}", out, want)
