@@ -703,3 +703,17 @@ def test_trimul_n1024(gpu, direction):
     ws = ops.workspace(ops.trimul_workspace_bytes(1, N), gpu)
     ops.launch_trimul(zd, out, pmd, _dev_w(w, gpu), 0 if direction == "outgoing" else 1, ws, accumulate=False)
     check(f"trimul N=1024 {direction}", out, want)
+
+
+def test_layer_n768(gpu):
+    """One full PairformerLayer (pair and single tracks) at the north-star size N = 768
+    against the fp32 oracle evaluated on the device (z ~ 0.5 N(0,1) as in the stack config)."""
+    N = 768
+    w = synthetic.stack_weights(1, 64)
+    s, z, mask, pm = synthetic.pair_inputs(N, 65, z_scale=0.5)
+    wd = {k: v.to(gpu) for k, v in ref.sub(w, "layers.0").items()}
+    s_ref, z_ref = ref.pairformer_layer(s.to(gpu), z.to(gpu), mask.to(gpu), pm.to(gpu), wd, ref.chunk_size_for(N))
+    pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, w)
+    s_got, z_got = pf(s.to(gpu).contiguous(), z.to(gpu).contiguous(), pm.to(gpu).contiguous(), mask.to(gpu))
+    check("layer N=768 z", z_got, z_ref)
+    check("layer N=768 s", s_got, s_ref)
