@@ -96,3 +96,14 @@ def test_python_check_raises_with_message():
     lib.pf_trimul_fwd(None)
     with pytest.raises(RuntimeError, match="null args"):
         _lib.check(-1, "pf_trimul_fwd")
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus 2 prints why and runs nothing (no GPU needed)."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120, cwd=root)
+    assert "exactly one GPU" in r.stdout + r.stderr
+    assert '"metric"' not in r.stdout
