@@ -520,6 +520,14 @@ def main() -> int:
         out["msa_trunk"] = msa_trunk_bench()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(N, seed)
+        if "stack" in out:
+            # config 3 on the CPU: one layer at N=768 timed once, extrapolated to 64 layers x 4 passes
+            c3 = cpu_baseline(out["stack"]["N"], 3, reps=1)
+            layer_s = 1.0 / c3["value"]
+            out["stack"]["cpu_extrapolated"] = {
+                "trunk_s": round(layer_s * out["stack"]["layers"] * out["stack"]["passes"], 1),
+                "layer_s": round(layer_s, 2), "cores": c3["cores"], "kind": "port",
+                "note": "extrapolated: 1 PairformerLayer at N=768 on the fp32 CPU oracle, x64 layers x4 passes"}
     print(json.dumps(out), flush=True)
     return 0
 
