@@ -306,6 +306,41 @@ def msa_trunk_bench(N: int = 768, S: int = 1024, msa_blocks: int = 4, n_layers: 
                         f"sequences + {n_layers} Pairformer layers per pass, N={N}, {passes} passes, masks all ones"}
 
 
+def module_bench(N: int = 512, n_layers: int = 4, seed: int = 9, reps: int = 3) -> dict:
+    """The drop-in PairformerModule on CPU tensors (as tt-bio calls it): padding, H2D of s/z,
+    n_layers layers, D2H of the outputs, timed with the host clock around forward (second
+    call onwards, masks cached), next to the same layers on device-resident tensors."""
+    import torch
+    from tt_boltz_amd import pairformer, synthetic
+    dev = pairformer.get_device()
+    w = synthetic.stack_weights(n_layers, seed)
+    s, z, mask, pm = synthetic.pair_inputs(N, seed)
+    mod = pairformer.PairformerModule(n_layers, 32, 4, 24, 16, True)
+    mod.load_state_dict(w)
+    mod(s, z, mask=mask, pair_mask=pm)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        s_out, z_out = mod(s, z, mask=mask, pair_mask=pm)
+        ts.append(time.perf_counter() - t0)
+    e2e = sorted(ts)[len(ts) // 2]
+    sd, zd, md, pmd = s.to(dev), z.to(dev), mask.to(dev), pm.to(dev).contiguous()
+    pf = mod.module
+    pf(sd.clone(), zd.clone(), pmd, md)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        pf(sd.clone(), zd.clone(), pmd, md)
+    torch.cuda.synchronize()
+    dev_s = (time.perf_counter() - t0) / reps
+    return {"N": N, "layers": n_layers, "end_to_end_s": round(e2e, 4), "device_resident_s": round(dev_s, 4),
+            "host_copy_overhead_s": round(e2e - dev_s, 4),
+            "end_to_end_layers_per_s": round(n_layers / e2e, 1),
+            "note": "PairformerModule.forward on CPU fp32 tensors (pad, H2D, layers, D2H; PCIe-inclusive) vs the "
+                    "device-resident stack on the same inputs; host clock, median of 3"}
+
+
 def fast_bench(N: int = 1024, seed: int = 4, steps: int = 5) -> dict:
     """Config 4: one layer in fast mode (MXFP8 triangle multiplications and pair
     transition) at N=1024 next to the same layer in 16-bit, plus the fp8 contraction alone."""
@@ -518,6 +553,8 @@ def main() -> int:
         out["template"] = template_bench()
         torch.cuda.empty_cache()
         out["msa_trunk"] = msa_trunk_bench()
+        torch.cuda.empty_cache()
+        out["module_end_to_end"] = module_bench()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(N, seed)
         if "stack" in out:
