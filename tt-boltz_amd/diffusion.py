@@ -42,9 +42,8 @@ class PairwiseConditioning(Module):
             out = torch.empty_like(z_trunk)
         ops.launch_pair_cond_proj(z_trunk, rel_pos, self.ln_w, self.ln_b, self.w, out, self.options.eps, self.variant)
         for t in self.transitions:
-            ws = ops.workspace(t.workspace_bytes(out.numel() // C_Z), out.device) if t.workspace_bytes(
-                out.numel() // C_Z) else None
-            t(out, out=out, accumulate=True, ws=ws)
+            nb = t.workspace_bytes(out.numel() // C_Z)   # 0: the fused pair transition needs none
+            t(out, out=out, accumulate=True, ws=ops.workspace(nb, out.device) if nb else None)
         return out
 
 
