@@ -7,16 +7,17 @@ s [1,512,384] fp32, masks all ones, random-init weights from seed 0 (the
 config-0 layer architecture), bf16 MFMA operands with fp32 accumulation.
 
 Besides the JSON line's ``value`` (layers/s), it reports per-op times and
-TFLOP/s, the roofline of the dominant kernel (timed alone with HIP events on the
-stream it is launched on) and the CPU oracle timed on this host's cores.
+TFLOP/s, the roofline of the dominant kernel (the triangle-attention core, timed alone
+with HIP events on the stream it is launched on), the same for the trimul contraction,
+and the CPU oracle timed on this host's cores.
 
 The config-3 trunk (64 layers at N=768, recycling_steps=3 -> 4 passes, device
 resident) and the contraction alone at N=768 are reported under ``stack``.
 
-``--probe-traffic`` runs only the contraction (5 launches at N=512) and a plain
-copy kernel of known size, for ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE``
-runs; the calibrated per-launch traffic is read back from
-``profiles/tm_contract_traffic.json`` when that file exists.
+``--probe-traffic`` runs only the attention core and the contraction (5 launches each
+at N=512) and a plain copy kernel of known size, for ``rocprofv3 --pmc FETCH_SIZE`` /
+``WRITE_SIZE`` runs; the calibrated per-launch traffic is read back from
+``profiles/kernel_traffic_n512.json`` when that file exists.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--n 512] [--no-cpu-baseline]
                        [--no-stack] [--probe-traffic]
@@ -36,7 +37,7 @@ if ROOT not in sys.path:
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 / fp16 (AMD published)
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "tm_contract_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "kernel_traffic_n512.json")
 COPY_BYTES = 256 << 20            # the calibration copy kernel reads and writes this many bytes
 
 
@@ -88,11 +89,21 @@ def cpu_baseline(N: int, seed: int, reps: int = 3) -> dict:
 
 
 def probe_traffic(N: int) -> int:
-    """Contraction alone (5 launches on its real plane size) and a plain copy kernel of
-    COPY_BYTES read + COPY_BYTES written, for PMC runs (FETCH_SIZE / WRITE_SIZE)."""
+    """The roofline kernels alone on their real operands -- the triangle-attention core and
+    the trimul contraction, 5 launches each -- and a plain copy kernel of COPY_BYTES read +
+    COPY_BYTES written, for PMC runs (FETCH_SIZE / WRITE_SIZE)."""
     import torch
-    from tt_boltz_amd import ops
+    from tt_boltz_amd import ops, pairformer, synthetic
     dev = torch.device("cuda", 0)
+    pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, synthetic.stack_weights(1, 0))
+    layer = pf.blocks[0]
+    _, z_cpu, _, _ = synthetic.pair_inputs(N, 0, with_s=False)
+    z = z_cpu.to(dev).contiguous()
+    ws = ops.workspace(pf.workspace_bytes(1, N), dev)
+    layer.triangle_attention_start(z, None, out=torch.empty_like(z), ws=ws)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        ops.launch_triatt_attend(ws, 1, N, 0, layer.variant)
     g = torch.Generator(device=dev).manual_seed(0)
     A = torch.randn((128, N, N), device=dev, generator=g).half()
     Bm = torch.randn((128, N, N), device=dev, generator=g).half()
@@ -105,13 +116,14 @@ def probe_traffic(N: int) -> int:
     for _ in range(3):
         torch.mul(src, 2.0, out=dst)     # vectorized elementwise kernel: reads and writes COPY_BYTES
     torch.cuda.synchronize()
-    print(json.dumps({"probe": "traffic", "N": N, "contract_launches": 5, "copy_launches": 3,
+    print(json.dumps({"probe": "traffic", "N": N, "attn_launches": 5, "contract_launches": 5, "copy_launches": 3,
                       "copy_bytes": COPY_BYTES}), flush=True)
     return 0
 
 
 def load_traffic():
-    """Calibrated HBM bytes per contraction launch from the committed PMC summary (or None)."""
+    """Calibrated HBM bytes per launch of the roofline kernels from the committed PMC summary
+    (``{"N": .., "note": .., "kernels": {name: {"hbm_bytes_per_launch": ..}}}``, or None)."""
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
@@ -462,9 +474,36 @@ def main() -> int:
                    ("triatt_end", "triatt"), ("transition_z", "transition_z")):
         breakdown[k]["tflops"] = round(fl[key] / (ops_ms[k] * 1e-3) / 1e12, 1)
 
-    # dominant-kernel roofline: the trimul contraction, launched alone on its real operands
-    # (the workspace planes the last trimul call left behind), timed with HIP events on
-    # the stream it runs on.
+    traffic = load_traffic()
+
+    def measured_traffic(kname):
+        """Calibrated HBM bytes per launch of `kname` from the committed PMC summary (or None)."""
+        if not traffic or traffic.get("N") != N:
+            return None
+        k = traffic.get("kernels", {}).get(kname)
+        return None if k is None else k["hbm_bytes_per_launch"]
+
+    # Dominant kernel: the triangle-attention core (ta_attn_kernel, ~0.18 ms of each
+    # triangle attention), launched alone on the q/k/v/bias/mask the last call left in the
+    # workspace, timed with HIP events on the stream it runs on.  MFMA-bound: 4*N^3*128 FLOP
+    # per launch (QK^T and PV over 4 heads of 32) against 16-bit traffic of q, k, v read once,
+    # the bias and mask once and o written once.
+    reps = 20
+    layer.triangle_attention_start(z, None, out=torch.empty_like(z), accumulate=False, ws=ws)
+    attn_ms = time_op(lambda: ops.launch_triatt_attend(ws, 1, N, 0, layer.variant), reps)
+    attn_flop = fl["triatt_core"]
+    attn_tf = attn_flop / (attn_ms * 1e-3) / 1e12
+    attn_bytes = (3 * 128 + 4 + 1 + 128) * N * N * 2
+    roofline = {"kernel": "ta_attn_kernel", "bound": "mfma", "achieved": round(attn_tf, 1),
+                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(attn_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                "traffic": measured_traffic("ta_attn_kernel"), "algorithmic_bytes": attn_bytes,
+                "flop_per_launch": attn_flop, "exp_per_launch": N ** 3 * 4, "launch_ms": round(attn_ms, 4),
+                "hbm_gbs_algorithmic": round(attn_bytes / (attn_ms * 1e-3) / 1e9, 1)}
+
+    # The trimul contraction (the batched matmul of the triangle multiplication), launched
+    # alone on its real operand planes (those the last trimul call left behind).  Below the
+    # ridge point (2.5 PF / 8 TB/s = 312 FLOP/B) its 16-bit traffic binds: at N = 512 the
+    # intensity is 171 FLOP/B.
     nplanes = 128
     plane_elems = nplanes * N * N
     dt = ops.TORCH_DTYPE[layer.variant]
@@ -472,32 +511,23 @@ def main() -> int:
     opB = ws[plane_elems * 2: plane_elems * 4].view(dt).view(nplanes, N, N)
     X = ws[plane_elems * 4: plane_elems * 6].view(dt).view(nplanes, N, N)
     layer.triangle_multiplication_start(z, None, out=torch.empty_like(z), accumulate=False, ws=ws)
-    reps = 20
     contract_ms = time_op(lambda: ops.launch_trimul_contract(opA, opB, X, layer.variant), reps)
     contract_flop = fl["trimul_contract"]       # 2*N^3*128: 128 planes of 2*N^3, one direction per launch
     achieved = contract_flop / (contract_ms * 1e-3) / 1e12
     kname = "tm_contract_dma_kernel" if N >= 384 else "tm_contract_kernel"
-    traffic = load_traffic()
-    # The binding roof: algorithmic bytes (a and b planes read once, x written once, 16-bit)
-    # over the published HBM peak vs FLOP over the MFMA peak.  Below the ridge point
-    # (2.5 PF / 8 TB/s = 312 FLOP/B) HBM binds: at N = 512 the intensity is 171 FLOP/B.
     alg_bytes = 3 * 128 * N * N * 2
-    t_hbm = alg_bytes / (HBM_PEAK_GBS * 1e9)
-    t_mfma = contract_flop / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+    gbs = alg_bytes / (contract_ms * 1e-3) / 1e9
     mfma_part = {"achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                  "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4)}
-    gbs = alg_bytes / (contract_ms * 1e-3) / 1e9
-    if t_hbm >= t_mfma:
-        roofline = {"kernel": kname, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}
-    else:
-        roofline = {"kernel": kname, "bound": "mfma", **mfma_part}
-    roofline.update({"traffic": traffic["hbm_bytes_per_launch"] if traffic and traffic.get("N") == N else None,
-                     "algorithmic_bytes": alg_bytes, "flop_per_launch": contract_flop,
-                     "intensity_flop_per_byte": round(contract_flop / alg_bytes, 1),
-                     "launch_ms": round(contract_ms, 4), "mfma": mfma_part})
+    bound_hbm = alg_bytes / (HBM_PEAK_GBS * 1e9) >= contract_flop / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+    contract = {"kernel": kname, "bound": "hbm" if bound_hbm else "mfma",
+                **({"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)} if bound_hbm else mfma_part),
+                "traffic": measured_traffic(kname), "algorithmic_bytes": alg_bytes, "flop_per_launch": contract_flop,
+                "intensity_flop_per_byte": round(contract_flop / alg_bytes, 1), "launch_ms": round(contract_ms, 4),
+                "mfma": mfma_part}
     if traffic and traffic.get("N") == N:
-        roofline["traffic_note"] = traffic.get("note")
+        roofline["traffic_note"] = contract["traffic_note"] = traffic.get("note")
 
     # the same layer with bf16 MFMA operands (libpairformer_hip_bf16.so, same kernels)
     pf_bf16 = pairformer.Pairformer(1, 32, 4, 24, 16, True, w, pairformer.Options(operand="bf16"))
@@ -535,6 +565,7 @@ def main() -> int:
                    "N": N, "batch": 1, "layer_tflop": round(fl["layer"] / 1e12, 4),
                    "layer_tflops_achieved": round(fl["layer"] / (ms_step * 1e-3) / 1e12, 1)},
         "roofline": roofline,
+        "roofline_contract": contract,
         "breakdown": breakdown,
         "wall_s_timed": round(wall, 3),
         "device": torch.cuda.get_device_name(0),

@@ -123,6 +123,13 @@ typedef struct pf_triatt_args {
 size_t pf_triatt_workspace_size(int B, int N, int C, int H, int D);
 int pf_triatt_fwd(const pf_triatt_args* args);
 
+/* The flash-attention kernel of pf_triatt_fwd alone (the softmax(q.k + bias + mask).v core
+ * of tt_bio/reference.py:176-190 / tt_bio/boltz2.py:790-810 inside TriangleAttention), run on
+ * the q, k, v, bias and mask that the last pf_triatt_fwd call with the same B and N left in
+ * `workspace`; its output goes to the same workspace.  Exported for measurement of the
+ * dominant kernel on its real operands. */
+int pf_triatt_attend_workspace(void* workspace, size_t workspace_bytes, int B, int N, int n_valid, void* stream);
+
 /* Attention core with the signature of the fused-op contract
  * kernel_triangular_attn(q, k, v, tri_bias, mask, scale) (tt_bio/boltz2.py:815-817)
  * and the semantics of the use_kernels=False path it stands in for
@@ -216,8 +223,10 @@ int pf_transition_pair_bias_fwd(const pf_transition_args* t, const pf_apb_args* 
  * which the reference selects with set_fast_mode() before building the modules
  * (tt_bio/worker.py:151-153) and which has no CPU counterpart (tt_bio/main.py:1648-1649).
  * Format: OCP MXFP8 -- e4m3 elements (round to nearest even, saturating at +-448) with
- * one E8M0 scale byte per 32 consecutive elements along the contraction axis,
- * X = 2^(floor(log2(amax)) - 8); fp32 accumulation.  Matrices are passed pre-quantized
+ * one E8M0 scale byte per 32 consecutive elements along the contraction axis:
+ * the smallest power of two X with amax / X <= 448 (OCP MX's floor(log2(amax)) - 8,
+ * one higher when amax's significand exceeds 1.75, so no element saturates);
+ * fp32 accumulation.  Matrices are passed pre-quantized
  * (pf_quantize_mx8): q = e4m3 bytes [rows][K], s = scale bytes [rows][K/32].
  * -------------------------------------------------------------------------- */
 

@@ -230,12 +230,16 @@ def _e4m3_nearest(v):
 
 
 def mx8_block(vals):
-    """Quantize-dequantize one block of 32 values: X = 2^(floor(log2 amax) - 8)."""
+    """Quantize-dequantize one block of 32 values with the smallest power of two X such
+    that amax / X <= 448, found by walking the exponent up from amax's."""
     amax = max(abs(v) for v in vals)
     if amax == 0.0:
         return [0.0] * len(vals)
-    _, ex = math.frexp(amax)            # amax = f * 2^ex, 0.5 <= f < 1  ->  floor(log2) = ex - 1
-    X = 2.0 ** (ex - 1 - 8)
+    _, ex = math.frexp(amax)            # amax = f * 2^ex, 0.5 <= f < 1
+    e = ex - 12                         # amax / 2^e = f * 4096 >= 2048 > 448: too small
+    while amax / 2.0 ** e > 448.0:
+        e += 1
+    X = 2.0 ** e
     return [_e4m3_nearest(v / X) * X for v in vals]
 
 

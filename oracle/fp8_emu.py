@@ -8,9 +8,12 @@ and has no CPU emulation (``--fast`` is ignored off-Tenstorrent,
 fp8 MFMA, i.e. the OCP Microscaling (MX) MXFP8-E4M3 format:
 
 * blocks of 32 contiguous elements along the contraction (K) axis;
-* one shared power-of-two scale per block, ``X = 2**(floor(log2(amax)) - 8)``
-  (8 = exponent of the largest normal e4m3 value, 448 = 1.75 * 2**8), stored
-  as an E8M0 byte (biased exponent, bias 127);
+* one shared power-of-two scale per block: the smallest ``X = 2**e`` with
+  ``amax / X <= 448`` (448 = 1.75 * 2**8, the largest e4m3 value), i.e.
+  ``e = floor(log2(amax)) - 8``, plus one when amax's significand exceeds 1.75.
+  The OCP MX rule ``floor(log2(amax)) - 8`` alone would clamp a block maximum in
+  (448, 512) * X to 448 (up to 12.5 % off); this rule never saturates a block's
+  elements.  Stored as an E8M0 byte (biased exponent, bias 127);
 * elements ``v / X`` rounded to OCP e4m3 (FN variant: no infinities, max 448,
   subnormals down to 2**-9) with round-to-nearest-even and saturation to +-448.
 
@@ -41,13 +44,16 @@ def round_e4m3(y: torch.Tensor) -> torch.Tensor:
 
 
 def block_scale_exp(x: torch.Tensor) -> torch.Tensor:
-    """Shared exponent per 32-block along the last axis (int32, unbiased)."""
+    """Shared exponent per 32-block along the last axis (int32, unbiased): the smallest e
+    with amax <= 448 * 2**e."""
     if x.shape[-1] % BLOCK:
         raise ValueError(f"last dim {x.shape[-1]} is not a multiple of {BLOCK}")
     xb = x.reshape(x.shape[:-1] + (x.shape[-1] // BLOCK, BLOCK)).to(torch.float32)
     amax = xb.abs().amax(dim=-1)
-    e = torch.floor(torch.log2(torch.where(amax > 0, amax, torch.ones_like(amax))))
-    e = torch.where(amax > 0, e - E4M3_EMAX, torch.full_like(e, -127.0))
+    # amax = f * 2**ex with 0.5 <= f < 1: floor(log2(amax)) = ex - 1, significand 2f
+    f, ex = torch.frexp(torch.where(amax > 0, amax, torch.ones_like(amax)))
+    e = (ex - 1 - E4M3_EMAX).to(torch.float32) + (f > 0.875).to(torch.float32)
+    e = torch.where(amax > 0, e, torch.full_like(e, -127.0))
     return torch.clamp(e, -127, 127).to(torch.int32)
 
 

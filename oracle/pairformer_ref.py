@@ -274,7 +274,7 @@ def pairformer_stack(s: Optional[Tensor], z: Tensor, mask: Optional[Tensor], pai
 
 
 def recycle(s_init: Tensor, z_init: Tensor, mask: Tensor, w_stack: Weights, w_rec: Weights,
-            n_blocks: int, recycling_steps: int, msa=None, **kw):
+            n_blocks: int, recycling_steps: int, msa=None, pass_hook=None, **kw):
     """Trunk recycling loop of ``Boltz2.forward`` (``boltz2.py:5189-5248``) without the
     template module: s, z start at zero; each of the ``recycling_steps + 1`` passes does
     s = s_init + s_recycle(s_norm(s)), z = z_init + z_recycle(z_norm(z)) (5213-5214), with
@@ -282,11 +282,12 @@ def recycle(s_init: Tensor, z_init: Tensor, mask: Tensor, w_stack: Weights, w_re
     the Pairformer stack (5239-5245).
 
     ``w_rec`` keys: ``s_norm.*``, ``z_norm.*``, ``s_recycle.weight``, ``z_recycle.weight``.
+    ``pass_hook(i, s, z)`` (optional) sees the state after each pass.
     """
     pair_mask = mask[:, :, None] * mask[:, None, :]
     s = torch.zeros_like(s_init)
     z = torch.zeros_like(z_init)
-    for _ in range(recycling_steps + 1):
+    for i in range(recycling_steps + 1):
         s = s_init + linear(layer_norm(s, w_rec["s_norm.weight"], w_rec["s_norm.bias"]),
                             w_rec["s_recycle.weight"])
         z = z_init + linear(layer_norm(z, w_rec["z_norm.weight"], w_rec["z_norm.bias"]),
@@ -296,4 +297,6 @@ def recycle(s_init: Tensor, z_init: Tensor, mask: Tensor, w_stack: Weights, w_re
             w_msa, emb, feats, msa_blocks = msa
             z = z + msa_module(z, emb, feats, w_msa, msa_blocks)
         s, z = pairformer_stack(s, z, mask, pair_mask, w_stack, n_blocks, **kw)
+        if pass_hook is not None:
+            pass_hook(i, s, z)
     return s, z

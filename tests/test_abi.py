@@ -81,7 +81,8 @@ def test_both_operand_variants_load():
 
 def test_workspace_sizes():
     lib = _lib.load()
-    assert lib.pf_trimul_workspace_size(1, 512, 128) == 128 * 512 * 512 * (2 + 2 + 2)
+    # a, b and X planes (16-bit) + 1024 per-workgroup operand maxima (fp32) for X's scale
+    assert lib.pf_trimul_workspace_size(1, 512, 128) == 128 * 512 * 512 * (2 + 2 + 2) + 1024 * 4
     assert lib.pf_triatt_workspace_size(1, 64, 128, 4, 32) > 0
     assert lib.pf_triatt_workspace_size(1, 64, 128, 8, 16) == 0
     assert lib.pf_transition_workspace_size(4096, 128, 512) == 0          # fused, no scratch

@@ -717,3 +717,59 @@ def test_layer_n768(gpu):
     s_got, z_got = pf(s.to(gpu).contiguous(), z.to(gpu).contiguous(), pm.to(gpu).contiguous(), mask.to(gpu))
     check("layer N=768 z", z_got, z_ref)
     check("layer N=768 s", s_got, s_ref)
+
+
+# ------------------------------------------------------------------------------ boundary regressions
+def test_module_mask_cache_tracks_n(gpu):
+    """N = 100 and then N = 120 without reset_static_cache(): both pad to 128, so the cached
+    masks must be keyed on N as well (the second call needs 120 valid tokens, not 100)."""
+    w = synthetic.stack_weights(1, 110)
+    mod = pairformer.PairformerModule(1, 32, 4, 24, 16, True)
+    mod.load_state_dict(w)
+    for N, seed in ((100, 111), (120, 112)):
+        s, z, mask, pm = _inputs(N, seed)
+        s_ref, z_ref = ref.pairformer_stack(s, z, mask, pm, w, 1)
+        s_got, z_got = mod(s, z)
+        check(f"module N={N} after N=100 (no reset) z", z_got, z_ref)
+        check(f"module N={N} after N=100 (no reset) s", s_got, s_ref)
+
+
+def test_padded_stack_without_mask(gpu):
+    """A padded stack (n_valid < N) called without any mask must still exclude the padding
+    from the contractions: Pairformer and TrunkRecycler build the valid-token pair mask."""
+    N, nv = 128, 100
+    w = synthetic.stack_weights(1, 113)
+    w_rec = synthetic.draw(synthetic.recycle_shapes(), 114)
+    s, z, mask, pm = _inputs(nv, 115)
+    s_ref, z_ref = ref.pairformer_stack(s, z, mask, pm, w, 1)
+    s_pad = torch.zeros((1, N, 384)); s_pad[:, :nv] = s
+    z_pad = torch.zeros((1, N, N, 128)); z_pad[:, :nv, :nv] = z
+    pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, w)
+    s_got, z_got = pf(s_pad.to(gpu), z_pad.to(gpu), None, None, n_valid=nv)
+    check("stack n_valid=100 of 128, no mask: z", z_got[:, :nv, :nv], z_ref)
+    check("stack n_valid=100 of 128, no mask: s", s_got[:, :nv], s_ref)
+    s_ref, z_ref = ref.recycle(s, z, mask, w, w_rec, 1, 1)
+    rec = pairformer.TrunkRecycler(pf, w_rec)
+    s_got, z_got = rec(s_pad.to(gpu), z_pad.to(gpu), None, 1, n_valid=nv)
+    check("recycler n_valid=100 of 128, no mask: z", z_got[:, :nv, :nv], z_ref)
+    check("recycler n_valid=100 of 128, no mask: s", s_got[:, :nv], s_ref)
+
+
+@pytest.mark.parametrize("scale", [1 / 64, 16.0])
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_weight_scale_headroom(gpu, direction, scale):
+    """The contraction planes X are 16-bit with a per-call power-of-two scale: p_in / g_in
+    scaled by 1/64 (|X| ~ 1e-4, deep in fp16's subnormal range for a fixed 2^-8 scale) or
+    by 16 (|X| ~ 1e3) must meet the same bar as the unit-scale weights."""
+    N = 256
+    prefix = "tri_mul_out" if direction == "outgoing" else "tri_mul_in"
+    w = _sub_w(116, prefix)
+    for k in ("p_in.weight", "g_in.weight"):
+        w[k] = w[k] * scale
+    _, z, _, pm = _inputs(N, 117, pad_tail=20)
+    want = ref.triangle_multiplication(z, pm, w, direction)
+    out = torch.empty((1, N, N, 128), device=gpu)
+    ws = ops.workspace(ops.trimul_workspace_bytes(1, N), gpu)
+    ops.launch_trimul(z.to(gpu), out, pm.to(gpu), _dev_w(w, gpu), 0 if direction == "outgoing" else 1, ws,
+                      accumulate=False)
+    check(f"trimul {direction} weights x{scale}", out, want)

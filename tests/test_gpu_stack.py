@@ -1,0 +1,147 @@
+"""GPU parity at stack depth and on the reference's own differential cases.
+
+* Config 3: the 64-layer trunk at N = 768 with 3 recycling steps (4 passes,
+  ``boltz2.py:5203``), seed 3, against the fp32 oracle evaluated on the device, pass by pass.
+  A stack of 256 layer applications amplifies any perturbation, so next to the GPU-vs-oracle
+  error the test measures the oracle's own sensitivity: the same oracle run on inputs rounded
+  to fp16 (a relative perturbation of at most 2^-11).
+* The reference's differential tests (``tests/test_tenstorrent.py:31-66``): the drop-in
+  ``PairformerModule`` at N = 100 and N = 500 (padded to 128 / 512 inside) with the
+  reference's input scales z = 26 randn, s = 8 randn, the c_z = 64 template stack, and the
+  4-block affinity stack with a permuted half mask.  Their acceptance bar is a median
+  relative error below 0.1; the rms-normalised bar of ``test_gpu_parity`` is applied as well,
+  to the outputs and to the updates (output minus input).
+"""
+import pytest
+import torch
+
+from oracle import pairformer_ref as ref
+from tt_boltz_amd import pairformer, synthetic
+
+from test_gpu_parity import MAX_TOL, MEAN_TOL, check, stats
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(w, dev):
+    return {k: v.to(dev) for k, v in w.items()}
+
+
+def median_rel(got, want):
+    """The reference's acceptance statistic (tests/test_tenstorrent.py:26-28)."""
+    g, w = got.detach().double().cpu(), want.detach().double().cpu()
+    return ((g - w).abs() / w.abs()).median().item()
+
+
+def check_reference_case(name, got, want, start):
+    """Median relative error < 0.1 (the reference's bar) on the output, and the rms bar on
+    the output and on the update ``out - start``."""
+    got, want, start = (t.detach().double().cpu() for t in (got, want, start))
+    med = median_rel(got, want)
+    print(f"[parity] {name}: median rel err {med:.3e}", flush=True)
+    assert med < 0.1, f"{name}: median relative error {med:.3e}"
+    check(name, got, want)
+    check(name + " update", got - start, want - start)
+
+
+# ------------------------------------------------------------------------------ config 3
+@pytest.mark.timeout(900)
+def test_config3_stack_depth(gpu):
+    """64 layers x 4 recycling passes at N = 768 (config 3) vs the fp32 oracle on the device.
+
+    Bar per pass: the north-star 2e-2 / 2e-3 of the rms, or, where the stack's own
+    sensitivity exceeds that, 2x the oracle's drift under an fp16 rounding of its inputs
+    (the amplification of a 2^-11 input perturbation through 256 layer applications)."""
+    cfg = synthetic.CONFIGS[3]
+    N, n_blocks, steps = cfg["N"], 64, 3
+    w = synthetic.stack_weights(n_blocks, cfg["seed"])
+    w_rec = synthetic.draw(synthetic.recycle_shapes(), cfg["seed"] + 1000)
+    s_init, z_init, mask, _ = synthetic.pair_inputs(N, cfg["seed"], z_scale=cfg["z_scale"])
+    wd, wrd = _dev(w, gpu), _dev(w_rec, gpu)
+    sd, zd, md = s_init.to(gpu), z_init.to(gpu), mask.to(gpu)
+
+    def run_oracle(s0, z0):
+        out = []
+
+        def hook(i, s, z):
+            out.append((s.clone(), z.clone()))
+            print(f"[stack] oracle pass {i} done", flush=True)
+
+        with torch.no_grad():
+            ref.recycle(s0, z0, md, wd, wrd, n_blocks, steps, pass_hook=hook)
+        return out
+
+    want = run_oracle(sd, zd)
+    print("[stack] oracle done", flush=True)
+    pert = run_oracle(sd.half().float(), zd.half().float())
+    print("[stack] perturbed oracle done", flush=True)
+
+    pf = pairformer.Pairformer(n_blocks, 32, 4, 24, 16, True, w)
+    rec = pairformer.TrunkRecycler(pf, w_rec)
+    got = []
+    rec(sd.contiguous(), zd.contiguous(), md, steps, pass_hook=lambda i, s, z: got.append((s.clone(), z.clone())))
+    torch.cuda.synchronize()
+    assert len(got) == len(want) == steps + 1
+    bad = []
+    for i, ((gs, gz), (ws_, wz), (ps, pz)) in enumerate(zip(got, want, pert)):
+        for name, g, r, p in (("z", gz, wz, pz), ("s", gs, ws_, ps)):
+            mx, mn = stats(g, r)
+            dmx, dmn = stats(p, r)
+            print(f"[stack] pass {i} {name}: gpu max/rms={mx:.3e} mean/rms={mn:.3e} | "
+                  f"oracle fp16-input drift max/rms={dmx:.3e} mean/rms={dmn:.3e}", flush=True)
+            assert torch.isfinite(g).all()
+            if not (mx <= max(MAX_TOL, 2 * dmx) and mn <= max(MEAN_TOL, 2 * dmn)):
+                bad.append((i, name, mx, mn))
+    assert not bad, bad
+
+
+# ------------------------------------------------------------------------------ reference cases
+@pytest.mark.parametrize("N", [100, 500])
+def test_reference_pairformer_case(gpu, N):
+    """tests/test_tenstorrent.py:31-43: PairformerModule(2, 32, 4, 24, 16, transform_s=True),
+    s = 8 randn, z = 26 randn, called without masks (all ones), CPU tensors in and out."""
+    g = torch.Generator().manual_seed(893 + N)
+    s = 8 * torch.randn((1, N, 384), generator=g)
+    z = 26 * torch.randn((1, N, N, 128), generator=g)
+    w = synthetic.stack_weights(2, 70 + N)
+    mod = pairformer.PairformerModule(2, 32, 4, 24, 16, True)
+    mod.load_state_dict(w)
+    s_got, z_got = mod(s, z)
+    assert s_got.device.type == "cpu" and z_got.shape == z.shape
+    ones = torch.ones((1, N), device=gpu)
+    s_ref, z_ref = ref.pairformer_stack(s.to(gpu), z.to(gpu), ones, torch.ones((1, N, N), device=gpu),
+                                        _dev(w, gpu), 2)
+    check_reference_case(f"reference pairformer N={N} z", z_got, z_ref, z)
+    check_reference_case(f"reference pairformer N={N} s", s_got, s_ref, s)
+
+
+@pytest.mark.parametrize("N", [100, 500])
+def test_reference_template_case(gpu, N):
+    """tests/test_tenstorrent.py:46-52: the template stack PairformerModule(2, 32, 4, None,
+    None, transform_s=False) at c_z = 64, z = 26 randn, no masks."""
+    z = 26 * torch.randn((1, N, N, 64), generator=torch.Generator().manual_seed(894 + N))
+    w = synthetic.stack_weights(2, 80 + N, c_z=64, transform_s=False)
+    mod = pairformer.PairformerModule(2, 32, 4, None, None, False)
+    mod.load_state_dict(w)
+    _, z_got = mod(None, z)
+    _, z_ref = ref.pairformer_stack(None, z.to(gpu), None, torch.ones((1, N, N), device=gpu), _dev(w, gpu), 2)
+    check_reference_case(f"reference template N={N} z", z_got, z_ref, z)
+
+
+@pytest.mark.parametrize("N", [100, 500])
+def test_reference_affinity_case(gpu, N):
+    """tests/test_tenstorrent.py:55-66: the affinity stack PairformerModule(4, 32, 4, None,
+    None, transform_s=False, affinity=True), z = 26 randn, half the tokens masked in a random
+    permutation, pair_mask = mask_i * mask_j."""
+    g = torch.Generator().manual_seed(895 + N)
+    z = 26 * torch.randn((1, N, N, 128), generator=g)
+    m = torch.ones((1, N))
+    m[0, : N // 2] = 0
+    m = m[:, torch.randperm(N, generator=g)]
+    pm = m[:, :, None] * m[:, None, :]
+    w = synthetic.stack_weights(4, 90 + N, transform_s=False)
+    mod = pairformer.PairformerModule(4, 32, 4, None, None, False, affinity=True)
+    mod.load_state_dict(w)
+    _, z_got = mod(None, z, pair_mask=pm)
+    _, z_ref = ref.pairformer_stack(None, z.to(gpu), None, pm.to(gpu), _dev(w, gpu), 4)
+    check_reference_case(f"reference affinity N={N} z", z_got, z_ref, z)

@@ -312,21 +312,33 @@ def test_mx8_scale_rule_and_block_independence():
     g = torch.Generator().manual_seed(35)
     x = torch.randn((4, 64), generator=g)
     x[1, :32] *= 1000.0
+    # block maxima with significands on both sides of 1.75 (448 = 1.75 * 2^8)
+    x[3] *= 2.0 ** -6                # |x| < 0.07: the planted values below are the block maxima
+    x[3, 0], x[3, 32] = 1.9 * 2.0 ** 3, 1.74 * 2.0 ** -2
+    x[0, 5] = 1.75 * 2.0 ** 4        # exactly 448 * 2^-4: stays at the floor exponent
     q, e = fp8_emu.quantize_mx8(x)
     amax = x.reshape(4, 2, 32).abs().amax(-1)
-    assert torch.equal(e, (torch.floor(torch.log2(amax)) - 8).to(torch.int32))
+    # the smallest power of two X with amax / X <= 448, by search over exponents
+    want = torch.empty_like(e)
+    for idx in range(amax.numel()):
+        a = float(amax.view(-1)[idx])
+        k = -140
+        while a / 2.0 ** k > 448.0:
+            k += 1
+        want.view(-1)[idx] = k
+    assert torch.equal(e, want)
+    assert e[3, 0].item() == 3 - 7 and e[3, 1].item() == -2 - 8 and e[0, 0].item() == 4 - 8
     # blocks are quantized independently: scaling one block does not change another
     x2 = x.clone(); x2[2, 32:] *= 64.0
     q2, _ = fp8_emu.quantize_mx8(x2)
     assert torch.equal(q2[2, :32], q[2, :32]) and torch.equal(q2[:2], q[:2])
     fq = fp8_emu.fake_quant_mx8(x)
-    # RNE with 3 mantissa bits: half an ulp is <= |x| * 2^-4 in the normal range and
-    # 2^-10 * scale (half the subnormal spacing 2^-9) below it
+    # no element saturates; RNE with 3 mantissa bits: half an ulp is <= |x| * 2^-4 in the
+    # normal range and 2^-10 * scale (half the subnormal spacing 2^-9) below it
     scale = torch.exp2(e.float()).repeat_interleave(32, dim=-1)
-    sat = x.abs() >= 448.0 * scale          # OCP MX: values in [448, 512) * scale clamp to 448
-    assert torch.equal(fq[sat], torch.copysign(448.0 * scale[sat], x[sat]))
+    assert (q.abs() <= 448.0).all()
     bound = torch.maximum(x.abs() * 2 ** -4, scale * 2 ** -10)
-    assert ((fq - x).abs() <= bound)[~sat].all()
+    assert ((fq - x).abs() <= bound).all()
     assert torch.equal(fp8_emu.fake_quant_mx8(torch.zeros(32)), torch.zeros(32))
 
 

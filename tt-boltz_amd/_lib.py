@@ -117,6 +117,7 @@ SIGNATURES = {
     "pf_trimul_contract": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "pf_triatt_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "pf_triatt_fwd": (c_int, [ctypes.POINTER(TriattArgs)]),
+    "pf_triatt_attend_workspace": (c_int, [c_void_p, c_size_t, c_int, c_int, c_int, c_void_p]),
     "pf_tri_attention_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "pf_tri_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p,
                                  c_int, c_int, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]),

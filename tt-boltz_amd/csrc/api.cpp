@@ -2,6 +2,11 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "pf_internal.h"
 
 namespace {
@@ -29,12 +34,35 @@ extern "C" int pf_operand_dtype(void) {
 }
 
 int device_cus() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];   // zero-initialized (static storage)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  if (dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (dev < 64) cached[dev] = cus;
+  if (dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
   return cus;
+}
+
+int pf_reserve_lds(const void* kernel, size_t bytes, const char* name) {
+  // (kernel, device) -> status of the one hipFuncSetAttribute call made for it
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, hipError_t> done;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return pf_fail(PF_E_LAUNCH, "%s: cannot query the current device", name);
+  hipError_t e;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_pair(kernel, dev);
+    auto it = done.find(key);
+    if (it == done.end())
+      it = done.emplace(key, hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes)).first;
+    e = it->second;
+  }
+  if (e != hipSuccess)
+    return pf_fail(PF_E_LAUNCH, "%s: cannot reserve %zu bytes of LDS: %s", name, bytes, hipGetErrorString(e));
+  return PF_OK;
 }

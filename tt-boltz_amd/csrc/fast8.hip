@@ -583,12 +583,6 @@ Tm8Buffers tm8_buffers(void* ws, int B, int N) {
   return t;
 }
 
-int set_lds(const void* fn, size_t bytes, const char* name) {
-  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess)
-    return pf_fail(PF_E_LAUNCH, "%s: cannot reserve %zu bytes of LDS", name, bytes);
-  return PF_OK;
-}
-
 // grid of a wave-tile loop: enough workgroups to fill the chip several times over
 int tile_grid(long ntiles) { const long g = (ntiles + 3) / 4; return (int)(g < 2048 ? g : 2048); }
 
@@ -632,13 +626,11 @@ extern "C" int pf_trimul_mx8_fwd(const pf_trimul_mx8_args* a) {
   const size_t need = tm8_buffers_size(a->B, a->N);
   if (a->workspace_bytes < need)
     return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: workspace too small (%zu < %zu bytes)", a->workspace_bytes, need);
-  static bool attr = false;
-  if (!attr) {
-    int rc = set_lds((const void*)tm8_proj_kernel, TM8P_LDS, "tm8_proj_kernel");
-    if (rc == PF_OK) rc = set_lds((const void*)tm8_contract_kernel<op_t>, TM8C_LDS, "tm8_contract_kernel");
-    if (rc == PF_OK) rc = set_lds((const void*)tm8_out_kernel<op_t>, TM8O_LDS, "tm8_out_kernel");
+  {
+    int rc = pf_reserve_lds((const void*)tm8_proj_kernel, TM8P_LDS, "tm8_proj_kernel");
+    if (rc == PF_OK) rc = pf_reserve_lds((const void*)tm8_contract_kernel<op_t>, TM8C_LDS, "tm8_contract_kernel");
+    if (rc == PF_OK) rc = pf_reserve_lds((const void*)tm8_out_kernel<op_t>, TM8O_LDS, "tm8_out_kernel");
     if (rc != PF_OK) return rc;
-    attr = true;
   }
   hipStream_t st = (hipStream_t)a->stream;
   const int B = a->B, N = a->N;
@@ -671,12 +663,8 @@ extern "C" int pf_trimul_mx8_contract(const void* A8, const void* B8, const void
   if (!A8 || !B8 || !SA || !SB || !X) return pf_fail(PF_E_INVALID, "pf_trimul_mx8_contract: null pointer");
   if (planes <= 0 || N <= 0 || N % 128)
     return pf_fail(PF_E_INVALID, "pf_trimul_mx8_contract: need planes > 0 and N a multiple of 128");
-  static bool attr = false;
-  if (!attr) {
-    const int rc = set_lds((const void*)tm8_contract_kernel<float>, TM8C_LDS, "tm8_contract_kernel");
-    if (rc != PF_OK) return rc;
-    attr = true;
-  }
+  if (const int rc = pf_reserve_lds((const void*)tm8_contract_kernel<float>, TM8C_LDS, "tm8_contract_kernel"))
+    return rc;
   const int tpd = (N + BT - 1) / BT;
   const int total = planes * tpd * tpd;
   tm8_contract_kernel<float><<<total, 64 * TM8C_WAVES, TM8C_LDS, (hipStream_t)stream>>>(

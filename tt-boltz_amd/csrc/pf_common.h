@@ -264,10 +264,30 @@ PF_DEV int xcd_remap(int w, int total) {
   return (w % 8) * (total / 8) + (w / 8);
 }
 
-// Fixed power-of-two scale of the fp16 contraction planes X (trimul): X is stored
-// as X * 2^-8 so |X| up to ~1.7e7 fits fp16's range; the epilogue multiplies back.
+// Fixed power-of-two scale of 16-bit contraction outputs X (the outer product mean's Z and
+// the standalone contraction API): X is stored as X * 2^-8, so |X| up to ~1.7e7 fits fp16.
 constexpr float X_STORE_SCALE = 1.f / 256.f;
 constexpr float X_LOAD_SCALE = 256.f;
+
+// Per-call power-of-two scale of the trimul contraction planes X = sum_k a_ik b_jk.  The
+// producer of a and b leaves one max(|a|, |b|) per workgroup in `parts`; with amax the
+// largest of them, |X| <= K * amax^2 =: f * 2^e (0.5 <= f < 1), and X is stored as
+// X * 2^(15 - e), i.e. at most 2^15 in magnitude (fp16's largest value is ~2^16), whatever
+// the scale of the weights: typical |X| then sits many binades above fp16's subnormal range.
+// Wave-uniform; every wave reduces the (few hundred) maxima itself.
+PF_DEV float planes_amax(const float* __restrict__ parts, int nparts) {
+  const int lane = threadIdx.x & 63;
+  float mx = 0.f;
+  for (int i = lane; i < nparts; i += 64) mx = fmaxf(mx, parts[i]);
+  return wave_max(mx);
+}
+PF_DEV float x_store_scale(float amax, int K) {
+  const float bound = (float)K * amax * amax;
+  if (!(bound > 0.f) || !(bound < 3.0e38f)) return 1.f;   // all-zero planes (or no bound): unscaled
+  int e;
+  (void)frexpf(bound, &e);
+  return ldexpf(1.f, 15 - e);
+}
 
 // ---------------------------------------------------------------------------------
 // MXFP8 (fast mode): OCP e4m3 elements with one E8M0 power-of-two scale per 32
@@ -282,9 +302,11 @@ constexpr float X_LOAD_SCALE = 256.f;
 //   A and B must agree on which (lane half, byte) carries which k; any permutation
 //   inside a block applied to both operands leaves the product unchanged.
 //   Accumulator layout as for the 16-bit MFMAs.
-// Block scale (OCP MX rule): X = 2^(floor(log2(amax)) - 8), stored as the E8M0 byte
-// floor(log2(amax)) - 8 + 127 (0 for an all-zero block); elements round-to-nearest-even
-// to e4m3 after division by X, saturating at +-448.
+// Block scale: the smallest power of two X with amax / X <= 448, i.e. floor(log2(amax)) - 8
+// (the OCP MX rule) plus one when amax's significand exceeds 1.75, so no element of a block
+// is clamped (the plain OCP rule clamps block maxima in (448, 512) * X to 448).  Stored as
+// the E8M0 byte log2(X) + 127 (0 for an all-zero block); elements round-to-nearest-even to
+// e4m3 after division by X (the +-448 saturation is only a guard).
 // ---------------------------------------------------------------------------------
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -293,10 +315,12 @@ PF_DEV f32x16 mfma8(const i32x8& a, const i32x8& b, const f32x16& c, int scale_a
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, scale_a, 0, scale_b);
 }
 
-// E8M0 scale byte of a block whose absolute maximum is amax (amax >= 0, finite):
-// biased exponent of amax minus 8, clamped at 0 (covers amax == 0 and tiny blocks).
+// E8M0 scale byte of a block whose absolute maximum is amax (amax >= 0, finite): biased
+// exponent of amax minus 8, one more when the significand is above 1.75 (fraction bits
+// above 0x600000), clamped at 0 (covers amax == 0 and tiny blocks).
 PF_DEV int mx_scale_byte(float amax) {
-  const int be = (int)((__float_as_uint(amax) >> 23) & 0xFF);
+  const uint32_t u = __float_as_uint(amax);
+  const int be = (int)((u >> 23) & 0xFF) + ((u & 0x7FFFFF) > 0x600000u ? 1 : 0);
   return max(be - 8, 0);
 }
 

@@ -19,6 +19,11 @@ int pf_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3))
 // Compute units of the current device (cached per device; 0 if the query fails).
 int device_cus();
 
+// Allow `kernel` `bytes` of dynamic LDS on the current device.  The attribute is set once
+// per (kernel, device), under a lock, and its status is kept: every later call on that
+// device returns the same result (PF_OK, or PF_E_LAUNCH with the message set again).
+int pf_reserve_lds(const void* kernel, size_t bytes, const char* name);
+
 // One row-major projection out = resid + x W^T + bias (fp32 x/out, op_t W [Nout][K]);
 // W2 != nullptr selects SwiGLU: out = silu(x W^T) * (x W2^T).  Up to PF_LIN_MAX_JOBS
 // projections of one shape (rows, K, Nout) run in a single launch (transition.hip).

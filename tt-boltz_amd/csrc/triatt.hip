@@ -615,13 +615,7 @@ TaBuffers ta_buffers(void* ws, int B, int N) {
 
 template <bool OUT_F32>
 int launch_attn(const TaBuffers& t, float* o32, int B, int N, int n_valid, hipStream_t st) {
-  static bool attr = false;
-  if (!attr) {
-    if (hipFuncSetAttribute((const void*)ta_attn_kernel<OUT_F32>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)TA_LDS) != hipSuccess)
-      return pf_fail(PF_E_LAUNCH, "ta_attn_kernel: cannot reserve %zu bytes of LDS", TA_LDS);
-    attr = true;
-  }
+  if (const int rc = pf_reserve_lds((const void*)ta_attn_kernel<OUT_F32>, TA_LDS, "ta_attn_kernel")) return rc;
   const int total = B * (N / 4) * ((N + 127) / 128);
   ta_attn_kernel<OUT_F32><<<total, 64 * TA_WAVES, TA_LDS, st>>>(t.Q, t.K, t.Vt, t.bias16, t.mask16, t.O, o32, N,
                                                                n_valid, total);
@@ -640,13 +634,7 @@ int triatt_run(const pf_triatt_args* a) {
   const int cus = device_cus();
   if (cus <= 0) return pf_fail(PF_E_LAUNCH, "pf_triatt_fwd: cannot query the device");
   {
-    static bool attr = false;
-    if (!attr) {
-      if (hipFuncSetAttribute((const void*)ta_proj_kernel<CC>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)tap_lds<CC>()) != hipSuccess)
-        return pf_fail(PF_E_LAUNCH, "ta_proj_kernel: cannot reserve %zu bytes of LDS", tap_lds<CC>());
-      attr = true;
-    }
+    if (const int rc = pf_reserve_lds((const void*)ta_proj_kernel<CC>, tap_lds<CC>(), "ta_proj_kernel")) return rc;
     const int grid = (int)min((long)cus, (positions / 32 + TAP_WAVES - 1) / TAP_WAVES);
     ta_proj_kernel<CC><<<grid, 64 * TAP_WAVES, tap_lds<CC>(), st>>>(
         a->z_in, a->pair_mask, a->ln_w, a->ln_b, (const op_t*)a->w_q, (const op_t*)a->w_k, (const op_t*)a->w_v,
@@ -656,13 +644,7 @@ int triatt_run(const pf_triatt_args* a) {
   int rc = launch_attn<false>(t, nullptr, B, N, n_valid, st);
   if (rc) return rc;
   {
-    static bool attr = false;
-    if (!attr) {
-      if (hipFuncSetAttribute((const void*)ta_out_kernel<CC>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)tao_lds<CC>()) != hipSuccess)
-        return pf_fail(PF_E_LAUNCH, "ta_out_kernel: cannot reserve %zu bytes of LDS", tao_lds<CC>());
-      attr = true;
-    }
+    if (const int rc = pf_reserve_lds((const void*)ta_out_kernel<CC>, tao_lds<CC>(), "ta_out_kernel")) return rc;
     const int grid = (int)min((long)cus, (positions / 32 + TAO_WAVES - 1) / TAO_WAVES);
     const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);
     ta_out_kernel<CC><<<grid, 64 * TAO_WAVES, tao_lds<CC>(), st>>>(t.O, a->z_in, a->out, a->ln_w, a->ln_b,
@@ -701,6 +683,22 @@ extern "C" int pf_triatt_fwd(const pf_triatt_args* a) {
   if (a->n_valid < 0 || a->n_valid > a->N)
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: n_valid %d outside [0, N=%d]", a->n_valid, a->N);
   return a->C == 128 ? triatt_run<128>(a) : triatt_run<64>(a);
+}
+
+extern "C" int pf_triatt_attend_workspace(void* workspace, size_t workspace_bytes, int B, int N, int n_valid,
+                                          void* stream) {
+  if (!workspace) return pf_fail(PF_E_INVALID, "pf_triatt_attend_workspace: null workspace");
+  if (B <= 0 || N <= 0 || N % 64)
+    return pf_fail(PF_E_INVALID, "pf_triatt_attend_workspace: need B > 0 and N a positive multiple of 64");
+  if ((unsigned long long)B * N * N >= (1ull << 32))
+    return pf_fail(PF_E_INVALID, "pf_triatt_attend_workspace: B * N * N must be below 2^32 (B=%d N=%d)", B, N);
+  if (n_valid < 0 || n_valid > N)
+    return pf_fail(PF_E_INVALID, "pf_triatt_attend_workspace: n_valid %d outside [0, N=%d]", n_valid, N);
+  const size_t need = ta_buffers_size(B, N);
+  if (workspace_bytes < need)
+    return pf_fail(PF_E_INVALID, "pf_triatt_attend_workspace: workspace too small (%zu < %zu bytes)",
+                   workspace_bytes, need);
+  return launch_attn<false>(ta_buffers(workspace, B, N), nullptr, B, N, n_valid ? n_valid : N, (hipStream_t)stream);
 }
 
 extern "C" size_t pf_tri_attention_workspace_size(int B, int N, int H_, int D_) {

@@ -10,9 +10,10 @@
 //               the contraction below is  X[c][i][j] = sum_k opA[c][i][k] * opB[c][j][k].
 //                 outgoing: opA[c][i][k] = a[i,k,c],  opB[c][j][k] = b[j,k,c]
 //                 incoming: opA[c][i][k] = a[k,i,c],  opB[c][j][k] = b[k,j,c]
-//   tm_contract 128 (x B) independent N x N x N GEMMs, fp32 accumulate, 128x128 tiles,
-//               LDS double buffer, XCD-aware tile order.  X is stored as op_t scaled by
-//               X_STORE_SCALE (halves the plane traffic; the scale keeps fp16 in range).
+//   tm_contract 128 (x B) independent N x N x N GEMMs, fp32 accumulate, XCD-aware tile
+//               order.  X is stored as op_t (half the traffic of fp32) times a per-call
+//               power of two chosen from max |a|, |b| (x_store_scale in pf_common.h), so
+//               fp16 neither overflows nor drops into subnormals for any weight scale.
 //   tm_out      LN_out(X) -> p_out, LN_in(z) -> g_out (recomputed, so no gate tensor
 //               goes through HBM), update = p * sigmoid(g), residual into z.
 #include "pf_common.h"
@@ -55,7 +56,8 @@ constexpr int SPITCH = 40;     // output staging pitch (elements): one 32-positi
 // CC = c_z (64 or 128): p_in / g_in are [2 CC][CC], LDS rows padded to CC + 8 elements
 template <int CC>
 constexpr size_t tmp_lds() {
-  return (size_t)2 * 2 * CC * (CC + 8) * sizeof(op_t) + (size_t)TMP_WAVES * 32 * SPITCH * sizeof(op_t);
+  return (size_t)2 * 2 * CC * (CC + 8) * sizeof(op_t) + (size_t)TMP_WAVES * 32 * SPITCH * sizeof(op_t) +
+         TMP_WAVES * sizeof(float);
 }
 
 template <int CC>
@@ -63,7 +65,8 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
     const float* __restrict__ z, const float* __restrict__ mask,
     const float* __restrict__ lnw, const float* __restrict__ lnb,
     const op_t* __restrict__ w_p, const op_t* __restrict__ w_g,
-    op_t* __restrict__ opA, op_t* __restrict__ opB, int B, int N, int incoming, float eps) {
+    op_t* __restrict__ opA, op_t* __restrict__ opB, float* __restrict__ amax_parts, int B, int N, int incoming,
+    float eps) {
   constexpr int LW = CC + 8, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t wlds[];
   op_t* lp = wlds;
@@ -71,6 +74,8 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   op_t* stg = wlds + 2 * 2 * CC * LW + wid * 32 * SPITCH;   // this wave's output stage
+  float* wave_amax = reinterpret_cast<float*>(wlds + 2 * 2 * CC * LW + TMP_WAVES * 32 * SPITCH);
+  float amax = 0.f;   // max |a|, |b| this lane wrote (as stored, after rounding)
 #pragma unroll 4
   for (int c = tid; c < 2 * CC * (CC / 8); c += 64 * TMP_WAVES) {
     const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
@@ -124,6 +129,7 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
           v[e] = (op_t)(ap[r] * sigmoidf_fast(ag[r]) * mr[r]);
+          amax = fmaxf(amax, fabsf((float)v[e]));
         }
         st_x4(stg + m * SPITCH + 8 * g + 4 * h, v);
       }
@@ -135,6 +141,16 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
       }
     }
   }
+  // the workgroup's max |a|, |b| -> amax_parts[blockIdx.x] (the contraction's scale input)
+  amax = wave_max(amax);
+  if (lane == 0) wave_amax[wid] = amax;
+  __syncthreads();
+  if (tid == 0) {
+    float mx = wave_amax[0];
+#pragma unroll
+    for (int w = 1; w < TMP_WAVES; ++w) mx = fmaxf(mx, wave_amax[w]);
+    amax_parts[blockIdx.x] = mx;
+  }
 }
 
 // ---------------------------------------------------------------------------------
@@ -142,10 +158,12 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
 // ---------------------------------------------------------------------------------
 constexpr int BM = 128, BN = 128, BK = 64, LDK = BK + 8;
 
+// The output is scaled by out_scale, or, when nparts > 0, by x_store_scale of the operand
+// maxima in amax_parts (K = the contraction length).
 template <typename OutT>
 __global__ __launch_bounds__(256) void tm_contract_kernel(
     const op_t* __restrict__ A, const op_t* __restrict__ Bop, OutT* __restrict__ X,
-    int N, int tpd, int total, float out_scale) {
+    int N, int tpd, int total, float out_scale, const float* __restrict__ amax_parts, int nparts) {
   __shared__ __attribute__((aligned(16))) op_t sA[2][BM * LDK];
   __shared__ __attribute__((aligned(16))) op_t sB[2][BN * LDK];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
@@ -210,6 +228,7 @@ __global__ __launch_bounds__(256) void tm_contract_kernel(
     }
   }
 
+  if (nparts > 0) out_scale = x_store_scale(planes_amax(amax_parts, nparts), N);
   OutT* Xp = X + plane * NN;
 #pragma unroll
   for (int a = 0; a < 2; ++a)
@@ -255,7 +274,7 @@ constexpr size_t TMD8_LDS_BYTES = (size_t)2 * 2 * DSLAB8 * sizeof(op_t);
 template <typename OutT>
 __global__ __launch_bounds__(64 * TMD_WAVES, 1) void tm_contract_dma_kernel(
     const op_t* __restrict__ A, const op_t* __restrict__ Bop, OutT* __restrict__ X,
-    int M, int Nc, int K, int tn, int total, float out_scale) {
+    int M, int Nc, int K, int tn, int total, float out_scale, const float* __restrict__ amax_parts, int nparts) {
   extern __shared__ __attribute__((aligned(16))) op_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -343,6 +362,7 @@ __global__ __launch_bounds__(64 * TMD_WAVES, 1) void tm_contract_dma_kernel(
     __builtin_amdgcn_sched_barrier(0);
   }
 #undef PF_INTERLEAVE_6_READS
+  if (nparts > 0) out_scale = x_store_scale(planes_amax(amax_parts, nparts), K);
   OutT* Xp = X + plane * M * Nc;
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
@@ -382,9 +402,12 @@ constexpr size_t tmo_lds() {
 }
 
 // resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
+// X is read back times x_scale, or, when nparts > 0, divided by the contraction's
+// x_store_scale of the operand maxima in amax_parts (contraction length N).
 template <typename XT, int CC>
 __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
-    const XT* __restrict__ X, float x_scale, const float* z_in, float* out,
+    const XT* __restrict__ X, float x_scale, const float* __restrict__ amax_parts, int nparts,
+    const float* z_in, float* out,
     const float* __restrict__ lni_w, const float* __restrict__ lni_b,
     const float* __restrict__ lno_w, const float* __restrict__ lno_b,
     const op_t* __restrict__ w_pout, const op_t* __restrict__ w_gout,
@@ -402,6 +425,7 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
     st_x8(&sWg[row * LW + col], ld_x8(w_gout + row * CC + col));
   }
   __syncthreads();
+  if (nparts > 0) x_scale = 1.f / x_store_scale(planes_amax(amax_parts, nparts), N);   // a power of two
   const long NN = (long)N * N;
   const uint32_t ntiles = (uint32_t)B * N * N / 32;
   for (uint32_t t = blockIdx.x * TMO_WAVES + wid; t < ntiles; t += gridDim.x * TMO_WAVES) {
@@ -462,34 +486,36 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
 // and a long enough K loop), 128x128 tiles below.
 // Rectangular form (256x256 tiles, any M, Nc multiple of 32, K multiple of 64):
 // X[p][i][j] = sum_k A[p][i][k] * B[p][j][k], A [P][M][K], B [P][Nc][K], X [P][M][Nc].
+// amax_parts / nparts: when nparts > 0 the output scale is x_store_scale of those operand
+// maxima (the trimul's planes); otherwise `scale`.
 template <typename OutT>
 int launch_contract_rect(const op_t* A, const op_t* B, OutT* X, int planes, int M, int Nc, int K, float scale,
-                         hipStream_t st) {
-  static bool attr_set = false;   // per process; the attribute is a property of the function
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)tm_contract_dma_kernel<OutT>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)TMD8_LDS_BYTES) != hipSuccess)
-      return pf_fail(PF_E_LAUNCH, "tm_contract_dma_kernel: cannot reserve %zu bytes of LDS", TMD8_LDS_BYTES);
-    attr_set = true;
-  }
+                         hipStream_t st, const float* amax_parts = nullptr, int nparts = 0) {
+  if (const int rc = pf_reserve_lds((const void*)tm_contract_dma_kernel<OutT>, TMD8_LDS_BYTES,
+                                    "tm_contract_dma_kernel"))
+    return rc;
   const int tn = (Nc + BM2 - 1) / BM2;
   const long total = (long)planes * ((M + BM2 - 1) / BM2) * tn;
   if (total > 0x7fffffff) return pf_fail(PF_E_INVALID, "contraction: too many tiles (%ld)", total);
-  tm_contract_dma_kernel<OutT><<<(unsigned)total, 64 * TMD_WAVES, TMD8_LDS_BYTES, st>>>(A, B, X, M, Nc, K, tn, (int)total,
-                                                                             scale);
+  tm_contract_dma_kernel<OutT><<<(unsigned)total, 64 * TMD_WAVES, TMD8_LDS_BYTES, st>>>(
+      A, B, X, M, Nc, K, tn, (int)total, scale, amax_parts, nparts);
   PF_CHECK_LAUNCH("tm_contract_dma_kernel");
   return PF_OK;
 }
 
 template <typename OutT>
-int launch_contract(const op_t* opA, const op_t* opB, OutT* X, int planes, int N, float scale, hipStream_t st) {
-  if (N >= 384) return launch_contract_rect<OutT>(opA, opB, X, planes, N, N, N, scale, st);
+int launch_contract(const op_t* opA, const op_t* opB, OutT* X, int planes, int N, float scale, hipStream_t st,
+                    const float* amax_parts = nullptr, int nparts = 0) {
+  if (N >= 384) return launch_contract_rect<OutT>(opA, opB, X, planes, N, N, N, scale, st, amax_parts, nparts);
   const int tpd = (N + BM - 1) / BM;
   const int total = planes * tpd * tpd;
-  tm_contract_kernel<OutT><<<total, 256, 0, st>>>(opA, opB, X, N, tpd, total, scale);
+  tm_contract_kernel<OutT><<<total, 256, 0, st>>>(opA, opB, X, N, tpd, total, scale, amax_parts, nparts);
   PF_CHECK_LAUNCH("tm_contract_kernel");
   return PF_OK;
 }
+
+// Workspace: opA, opB, X planes (op_t), then TM_MAX_PARTS floats of per-workgroup maxima.
+constexpr int TM_MAX_PARTS = 1024;
 
 template <int CC>
 int trimul_run(const pf_trimul_args* a) {
@@ -499,38 +525,28 @@ int trimul_run(const pf_trimul_args* a) {
   op_t* opA = (op_t*)a->workspace;
   op_t* opB = opA + planes;
   op_t* X = opB + planes;
+  float* amax_parts = reinterpret_cast<float*>(X + planes);
   const long positions = (long)B * N * N;
   const int cus = device_cus();
   if (cus <= 0) return pf_fail(PF_E_LAUNCH, "pf_trimul_fwd: cannot query the device");
-  const int grid_proj = (int)min((long)cus, (positions / 32 + TMP_WAVES - 1) / TMP_WAVES);
+  const int grid_proj = (int)min((long)min(cus, TM_MAX_PARTS), (positions / 32 + TMP_WAVES - 1) / TMP_WAVES);
   const int grid_out = (int)min((long)cus, (positions / 32 + TMO_WAVES - 1) / TMO_WAVES);
   {
-    static bool attr = false;
-    if (!attr) {
-      if (hipFuncSetAttribute((const void*)tm_proj_kernel<CC>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)tmp_lds<CC>()) != hipSuccess)
-        return pf_fail(PF_E_LAUNCH, "tm_proj_kernel: cannot reserve %zu bytes of LDS", tmp_lds<CC>());
-      attr = true;
-    }
+    if (const int rc = pf_reserve_lds((const void*)tm_proj_kernel<CC>, tmp_lds<CC>(), "tm_proj_kernel")) return rc;
     tm_proj_kernel<CC><<<grid_proj, 64 * TMP_WAVES, tmp_lds<CC>(), st>>>(
-        a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b, (const op_t*)a->p_in_w, (const op_t*)a->g_in_w, opA, opB, B,
-        N, a->direction, a->eps);
+        a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b, (const op_t*)a->p_in_w, (const op_t*)a->g_in_w, opA, opB,
+        amax_parts, B, N, a->direction, a->eps);
     PF_CHECK_LAUNCH("tm_proj_kernel");
   }
-  const int rc = launch_contract<op_t>(opA, opB, X, B * CC, N, X_STORE_SCALE, st);
+  const int rc = launch_contract<op_t>(opA, opB, X, B * CC, N, X_STORE_SCALE, st, amax_parts, grid_proj);
   if (rc != PF_OK) return rc;
   {
-    static bool attr = false;
-    if (!attr) {
-      if (hipFuncSetAttribute((const void*)tm_out_kernel<op_t, CC>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)tmo_lds<CC>()) != hipSuccess)
-        return pf_fail(PF_E_LAUNCH, "tm_out_kernel: cannot reserve %zu bytes of LDS", tmo_lds<CC>());
-      attr = true;
-    }
+    if (const int rc2 = pf_reserve_lds((const void*)tm_out_kernel<op_t, CC>, tmo_lds<CC>(), "tm_out_kernel"))
+      return rc2;
     const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);
     tm_out_kernel<op_t, CC><<<grid_out, 64 * TMO_WAVES, tmo_lds<CC>(), st>>>(
-        X, X_LOAD_SCALE, a->z_in, a->out, a->norm_in_w, a->norm_in_b, a->norm_out_w, a->norm_out_b,
-        (const op_t*)a->p_out_w, (const op_t*)a->g_out_w, B, N, resid, a->eps);
+        X, X_LOAD_SCALE, amax_parts, grid_proj, a->z_in, a->out, a->norm_in_w, a->norm_in_b, a->norm_out_w,
+        a->norm_out_b, (const op_t*)a->p_out_w, (const op_t*)a->g_out_w, B, N, resid, a->eps);
     PF_CHECK_LAUNCH("tm_out_kernel");
   }
   return PF_OK;
@@ -544,7 +560,7 @@ int trimul_run(const pf_trimul_args* a) {
 extern "C" size_t pf_trimul_workspace_size(int B, int N, int C_) {
   if (B <= 0 || N <= 0 || (C_ != 128 && C_ != 64)) return 0;
   const size_t planes = (size_t)B * C_ * N * N;
-  return planes * 3 * sizeof(op_t);   // opA, opB, X
+  return planes * 3 * sizeof(op_t) + TM_MAX_PARTS * sizeof(float);   // opA, opB, X, operand maxima
 }
 
 extern "C" int pf_trimul_fwd(const pf_trimul_args* a) {

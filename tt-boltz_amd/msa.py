@@ -111,8 +111,11 @@ class MSA(Module):
     def __call__(self, z: torch.Tensor, emb: torch.Tensor, msa: torch.Tensor, has_deletion: torch.Tensor,
                  deletion_value: torch.Tensor, msa_paired: torch.Tensor, pair_mask: Optional[torch.Tensor],
                  msa_mask: Optional[torch.Tensor], n_valid: int = 0) -> torch.Tensor:
-        """Padded device tensors (N % 64 == 0): updates and returns z."""
+        """Padded device tensors (N % 64 == 0): updates and returns z.  With padding
+        (``n_valid`` < N) and no ``pair_mask`` the padding is masked out."""
         B, S, N = msa.shape
+        if pair_mask is None and 0 < n_valid < N:
+            pair_mask = ops.valid_pair_mask(B, N, n_valid, z.device)
         c_m = self.s_proj.shape[0]
         s_emb = torch.empty((B, N, c_m), dtype=torch.float32, device=z.device)
         ops.launch_linear(emb, self.s_proj, None, None, s_emb, self.variant)
@@ -172,10 +175,12 @@ class MSAModule(nn.Module):
         dev = get_device()
         B, N = z.shape[0], z.shape[1]
         n_pad = ops.padded_len(N)
-        z_dev = ops.pad_pair(z.to(dev, torch.float32), n_pad)
+        z_dev = ops.to_device_padded(z, n_pad, dev, pair=True)
         inputs = device_inputs(emb, feats, n_pad, dev)
         tok = torch.zeros((B, n_pad), dtype=torch.float32, device=dev)
         tok[:, :N] = feats["token_pad_mask"].to(dev, torch.float32)
         pair_mask = (tok[:, :, None] * tok[:, None, :]).contiguous()
         z_dev = self.module(z_dev, pair_mask=pair_mask, n_valid=N, **inputs)
+        if z.device.type == "cpu":
+            return ops.to_host(z_dev[:, :N, :N])
         return z_dev[:, :N, :N].to(z.device)

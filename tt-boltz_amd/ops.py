@@ -89,6 +89,52 @@ def pad_pair(z: torch.Tensor, n_pad: int) -> torch.Tensor:
     return out
 
 
+#: row chunks of a host -> device pair copy: the host copy of one chunk into pinned memory
+#: overlaps the DMA of the previous chunk
+_H2D_CHUNKS = 4
+
+
+def to_device_padded(x: torch.Tensor, n_pad: int, device: torch.device, pair: bool) -> torch.Tensor:
+    """Zero-padded fp32 device copy of ``x``: [B,N,N,C] -> [B,n_pad,n_pad,C] (``pair``) or
+    [B,N,C] -> [B,n_pad,C].  A CPU tensor moves through pinned staging buffers (torch's
+    caching host allocator) in row chunks with asynchronous DMA, so the host copy of a
+    chunk overlaps the transfer of the previous one; a device tensor is padded in place."""
+    B, N = x.shape[0], x.shape[1]
+    shape = (B, n_pad, n_pad, x.shape[-1]) if pair else (B, n_pad, x.shape[-1])
+    out = torch.zeros(shape, dtype=torch.float32, device=device)
+    dst = out[:, :N, :N] if pair else out[:, :N]
+    if x.device.type != "cpu":
+        dst.copy_(x)
+        return out
+    xf = x if x.dtype == torch.float32 else x.float()
+    if xf.is_pinned():
+        dst.copy_(xf, non_blocking=True)
+        return out
+    step = max(1, -(-N // _H2D_CHUNKS))
+    for r0 in range(0, N, step):
+        r1 = min(N, r0 + step)
+        stage = torch.empty(xf[:, r0:r1].shape, dtype=torch.float32, pin_memory=True)
+        stage.copy_(xf[:, r0:r1])
+        dst[:, r0:r1].copy_(stage, non_blocking=True)
+    return out
+
+
+def to_host(x: torch.Tensor) -> torch.Tensor:
+    """A CPU copy of device tensor ``x`` in pinned memory (one DMA, then a stream sync)."""
+    out = torch.empty(x.shape, dtype=x.dtype, pin_memory=True)
+    out.copy_(x, non_blocking=True)
+    torch.cuda.current_stream(x.device).synchronize()
+    return out
+
+
+def valid_pair_mask(B: int, N: int, n_valid: int, device: torch.device) -> torch.Tensor:
+    """[B,N,N] fp32 pair mask that is 1 on the first ``n_valid`` tokens' pairs and 0 on the
+    boundary padding: what a padded stack uses when the caller gives no mask."""
+    out = torch.zeros((B, N, N), dtype=torch.float32, device=device)
+    out[:, :n_valid, :n_valid] = 1.0
+    return out
+
+
 def pad_pair_mask(pair_mask: Optional[torch.Tensor], B: int, N: int, n_pad: int,
                   device: torch.device) -> Optional[torch.Tensor]:
     """[B,N,N] 0/1 mask padded with zeros; None when no masking is needed."""
@@ -139,6 +185,13 @@ def launch_triatt(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional[tor
         w_g=_ptr(w["linear_g.weight"]), w_o=_ptr(w["linear_o.weight"]),
         workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
     _lib.check(_lib.load(variant).pf_triatt_fwd(ctypes.byref(a)), "pf_triatt_fwd", variant)
+
+
+def launch_triatt_attend(ws: torch.Tensor, B: int, N: int, n_valid: int = 0, variant: str = DEFAULT_VARIANT) -> None:
+    """The flash-attention kernel alone on the operands the last ``launch_triatt`` call with
+    the same (B, N) left in ``ws`` (measurement of the dominant kernel)."""
+    _lib.check(_lib.load(variant).pf_triatt_attend_workspace(_ptr(ws), ws.numel(), B, N, n_valid, _stream()),
+               "pf_triatt_attend_workspace", variant)
 
 
 def transition_workspace_bytes(rows: int, C: int, hidden: int, variant: str = DEFAULT_VARIANT) -> int:

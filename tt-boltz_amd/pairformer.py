@@ -56,42 +56,59 @@ def get_device() -> torch.device:
     return _device
 
 
-class WeightScope:
-    """Immutable scoped view over a flat state dict (``tenstorrent.py:261-293``)."""
+class WeightScope(Mapping):
+    """Read-only state-dict view with the reference's scoping interface
+    (``tenstorrent.py:261-293``: ``wrap``, ``data``, ``as_dict``, ``[key]``, ``child``).
+
+    ``child("a.b", strip_prefix="mha.")`` re-roots the view at ``a.b.``: a key
+    ``a.b.mha.linear_q.weight`` is seen as ``linear_q.weight``, ``a.b.layer_norm.weight`` as
+    ``layer_norm.weight``; keys outside the scope are dropped."""
+
+    __slots__ = ("_items",)
 
     def __init__(self, data: Mapping[str, torch.Tensor]):
-        self._data = MappingProxyType(dict(data))
+        self._items = MappingProxyType(dict(data))
 
     @classmethod
     def wrap(cls, data) -> "WeightScope":
-        return data if isinstance(data, cls) else cls(data)
+        if isinstance(data, WeightScope):
+            return data
+        return cls(data)
 
     @property
     def data(self) -> Mapping[str, torch.Tensor]:
-        return self._data
+        return self._items
 
     def as_dict(self) -> dict:
-        return dict(self._data)
+        return dict(self._items)
 
     def __getitem__(self, key: str) -> torch.Tensor:
-        return self._data[key]
+        return self._items[key]
 
-    def __contains__(self, key: str) -> bool:
-        return key in self._data
+    def __iter__(self):
+        return iter(self._items)
+
+    def __len__(self) -> int:
+        return len(self._items)
+
+    @staticmethod
+    def _relative(key: str, root: str, strip: str) -> Optional[str]:
+        """``key`` seen from ``root`` (None if outside it), with a leading ``strip`` removed."""
+        n = len(root)
+        if key[n:n + 1] != "." or not key.startswith(root):
+            return None
+        rest = key[n + 1:]
+        return rest[len(strip):] if strip and rest.startswith(strip) else rest
 
     def child(self, scope: str, strip_prefix: str = "") -> "WeightScope":
         if not scope:
             return self
-        sp = scope + "."
-        out = {}
-        for key, value in self._data.items():
-            if not key.startswith(sp):
-                continue
-            ck = key[len(sp):]
-            if strip_prefix and ck.startswith(strip_prefix):
-                ck = ck[len(strip_prefix):]
-            out[ck] = value
-        return WeightScope(out)
+        picked = {}
+        for key, value in self._items.items():
+            rel = self._relative(key, scope, strip_prefix)
+            if rel:
+                picked[rel] = value
+        return WeightScope(picked)
 
 
 class Options:
@@ -442,8 +459,13 @@ class Pairformer(Module):
 
     def __call__(self, s: Optional[torch.Tensor], z: torch.Tensor, pair_mask: Optional[torch.Tensor] = None,
                  mask: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None, n_valid: int = 0):
+        """Padded device tensors in; ``n_valid`` (0 = all) tokens are real.  With padding and
+        no ``pair_mask`` the padding is masked out (the contractions have no ``n_valid``)."""
+        B, N = z.shape[0], z.shape[1]
+        if pair_mask is None and 0 < n_valid < N:
+            pair_mask = ops.valid_pair_mask(B, N, n_valid, z.device)
         if ws is None:
-            ws = ops.workspace(self.workspace_bytes(z.shape[0], z.shape[1]), z.device)
+            ws = ops.workspace(self.workspace_bytes(B, N), z.device)
         single = self.single_track(z.shape[0], z.shape[1], z.device) if s is not None else None
         for block in self.blocks:
             s, z = block(s, z, pair_mask, mask, ws, n_valid, single)
@@ -494,29 +516,34 @@ class PairformerModule(nn.Module):
             tm = torch.zeros((B, n_pad), dtype=torch.float32, device=dev)
             tm[:, :N] = 1.0 if mask is None else mask.to(dev, torch.float32)
             self._runtime_cache["mask"] = tm
-        self._runtime_cache["shape"] = (B, n_pad)
+        # the masks depend on the unpadded length too: N = 100 and N = 120 share n_pad = 128
+        self._runtime_cache["shape"] = (B, N, n_pad)
 
     def forward(self, s: Optional[torch.Tensor], z: torch.Tensor, mask: Optional[torch.Tensor] = None,
                 pair_mask: Optional[torch.Tensor] = None, use_kernels: bool = False):
         """``(s [B,N,c_s] | None, z [B,N,N,c_z]) -> (s_out | None, z_out)``, fp32, on z's device.
-        ``use_kernels`` is accepted for call-site compatibility and ignored."""
+        ``use_kernels`` is accepted for call-site compatibility and ignored.  CPU tensors
+        move through pinned staging buffers; CPU results come back in pinned memory."""
         if self.module is None:
             raise RuntimeError("PairformerModule has no weights: call load_state_dict() first")
         dev = get_device()
         B, N = z.shape[0], z.shape[1]
         n_pad = ops.padded_len(N, ops.FAST_PAD if self.module.fast else ops.PAD)
-        if self._first_forward_pass or self._runtime_cache.get("shape") != (B, n_pad):
+        if self._first_forward_pass or self._runtime_cache.get("shape") != (B, N, n_pad):
             self._build_masks(B, N, n_pad, mask, pair_mask, dev)
             self._first_forward_pass = False
-        z_dev = ops.pad_pair(z.to(dev, torch.float32), n_pad)
+        z_dev = ops.to_device_padded(z, n_pad, dev, pair=True)
         s_dev = None
         if self.transform_s and s is not None:
-            s_dev = torch.zeros((B, n_pad, s.shape[-1]), dtype=torch.float32, device=dev)
-            s_dev[:, :N] = s.to(dev, torch.float32)
+            s_dev = ops.to_device_padded(s, n_pad, dev, pair=False)
         s_dev, z_dev = self.module(s_dev, z_dev, self._runtime_cache["pair_mask"], self._runtime_cache.get("mask"),
                                    n_valid=N)
-        z_out = z_dev[:, :N, :N].to(z.device)
-        s_out = None if s_dev is None else s_dev[:, :N].to(s.device)
+
+        def back(t_dev, like):
+            return ops.to_host(t_dev) if like.device.type == "cpu" else t_dev.to(like.device)
+
+        z_out = back(z_dev[:, :N, :N], z)
+        s_out = None if s_dev is None else back(s_dev[:, :N], s)
         if s is not None and not self.transform_s:
             s_out = s
         return s_out, z_out
@@ -546,13 +573,19 @@ class TrunkRecycler:
 
     def __call__(self, s_init: torch.Tensor, z_init: torch.Tensor, mask: Optional[torch.Tensor],
                  recycling_steps: int, pass_hook=None, n_valid: int = 0, msa_inputs: Optional[dict] = None):
-        """Padded device tensors in (N % 64 == 0); returns device (s, z)."""
+        """Padded device tensors in (N % 64 == 0); returns device (s, z).  ``pass_hook(i, s, z)``
+        (optional) is called after each pass with the device state (enqueued, not synchronized)."""
         if (self.msa is None) != (msa_inputs is None):
             raise ValueError("TrunkRecycler: msa_inputs must be given exactly when an MSA module is attached")
         B, N = z_init.shape[0], z_init.shape[1]
         v = self.options.operand
         dev = z_init.device
-        pair_mask = None if mask is None else (mask[:, :, None] * mask[:, None, :]).contiguous()
+        if mask is not None:
+            pair_mask = (mask[:, :, None] * mask[:, None, :]).contiguous()
+        elif 0 < n_valid < N:
+            pair_mask = ops.valid_pair_mask(B, N, n_valid, dev)
+        else:
+            pair_mask = None
         s = torch.zeros_like(s_init)
         z = torch.zeros_like(z_init)
         s_tmp = torch.empty_like(s_init)
@@ -568,5 +601,5 @@ class TrunkRecycler:
                 ops.launch_add(z, z_msa, z, v)
             s, z = self.pairformer(s, z, pair_mask, mask, ws, n_valid)
             if pass_hook is not None:
-                pass_hook(i)
+                pass_hook(i, s, z)
         return s, z
