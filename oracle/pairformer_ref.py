@@ -15,7 +15,8 @@ source tree.
 """
 from __future__ import annotations
 
-from math import sqrt
+from contextlib import contextmanager
+from math import ceil, log2, sqrt
 from typing import Mapping, Optional
 
 import torch
@@ -27,6 +28,41 @@ Weights = Mapping[str, Tensor]
 #: ``tt_bio/data/const.py:775`` -- above this N the reference chunks triangle
 #: attention rows by 128, otherwise by 512 (``tt_bio/reference.py:982-988``).
 CHUNK_SIZE_THRESHOLD = 384
+
+
+#: Rounding of every product operand: None (exact fp32, the reference semantics) or a 16-bit
+#: torch dtype.  ``operand_rounding(torch.float16)`` turns the oracle into a precision model of
+#: a 16-bit-operand implementation (operands of every matmul / einsum rounded once, products
+#: accumulated and everything else computed in fp32); tests use it to bound the drift that the
+#: operand format alone causes.  It is not the reference and is off by default.
+_OPERAND: Optional[torch.dtype] = None
+
+
+@contextmanager
+def operand_rounding(dtype: Optional[torch.dtype]):
+    global _OPERAND
+    prev, _OPERAND = _OPERAND, dtype
+    try:
+        yield
+    finally:
+        _OPERAND = prev
+
+
+def _op(t: Tensor) -> Tensor:
+    """A product operand, rounded to the operand type when a precision model is active."""
+    return t if _OPERAND is None else t.to(_OPERAND).to(t.dtype)
+
+
+def _op_scaled(t: Tensor) -> Tensor:
+    """A stored intermediate (the trimul contraction output) rounded to the operand type under
+    a power-of-two scale that keeps its largest value in the type's normal range."""
+    if _OPERAND is None:
+        return t
+    amax = float(t.abs().max())
+    if amax == 0.0:
+        return t
+    scale = 2.0 ** (15 - ceil(log2(amax)))
+    return (t * scale).to(_OPERAND).to(t.dtype) / scale
 
 
 def sub(w: Weights, prefix: str) -> dict:
@@ -42,7 +78,7 @@ def layer_norm(x: Tensor, weight: Tensor, bias: Tensor, eps: float = 1e-5) -> Te
 
 def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Tensor:
     """``nn.Linear`` / ``tt_bio/boltz2.py:720-731`` (fp32 branch)."""
-    return F.linear(x, weight, bias)
+    return F.linear(_op(x), _op(weight), bias)
 
 
 # --------------------------------------------------------------------------------------
@@ -63,10 +99,12 @@ def triangle_multiplication(z: Tensor, pair_mask: Tensor, w: Weights, direction:
     x = linear(x, w["p_in.weight"]) * torch.sigmoid(linear(x, w["g_in.weight"]))  # :458
     x = x * pair_mask.unsqueeze(-1)                                         # :461
     a, b = torch.chunk(x.float(), 2, dim=-1)                                # :464
+    a, b = _op(a), _op(b)
     if direction == "outgoing":
         x = torch.einsum("bikd,bjkd->bijd", a, b)                           # :467
     else:
         x = torch.einsum("bkid,bkjd->bijd", a, b)                           # :556
+    x = _op_scaled(x)
     x = linear(layer_norm(x, w["norm_out.weight"], w["norm_out.bias"]), w["p_out.weight"])
     return x * torch.sigmoid(linear(x_in, w["g_out.weight"]))               # :470
 
@@ -117,13 +155,13 @@ def _mha_rows(x: Tensor, tri_bias: Tensor, mask_bias: Tensor, w: Weights,
     k = linear(x, w["linear_k.weight"]).view(shp + (n_heads, head_dim)).transpose(-2, -3)
     v = linear(x, w["linear_v.weight"]).view(shp + (n_heads, head_dim)).transpose(-2, -3)
     q = q / sqrt(head_dim)
-    a = torch.matmul(q, k.transpose(-1, -2))      # [B,I,H,J,K]
+    a = torch.matmul(_op(q), _op(k).transpose(-1, -2))      # [B,I,H,J,K]
     a = a + mask_bias
     a = a + tri_bias
     a = torch.softmax(a, dim=-1)
-    o = torch.matmul(a, v).transpose(-2, -3)      # [B,I,J,H,d]
+    o = torch.matmul(_op(a), _op(v)).transpose(-2, -3)      # [B,I,J,H,d]
     g = torch.sigmoid(linear(x, w["linear_g.weight"])).view(shp + (n_heads, head_dim))
-    o = (o * g).reshape(shp + (n_heads * head_dim,))
+    o = (_op(o) * g).reshape(shp + (n_heads * head_dim,))
     return linear(o, w["linear_o.weight"])
 
 
@@ -218,11 +256,11 @@ def attention_pair_bias(s: Tensor, z: Tensor, mask: Tensor, k_in: Tensor, w: Wei
     bias = linear(layer_norm(z, w["proj_z.0.weight"], w["proj_z.0.bias"]), w["proj_z.1.weight"])
     bias = bias.permute(0, 3, 1, 2)                                       # "b ... h -> b h ..."
     g = torch.sigmoid(linear(s, w["proj_g.weight"]))
-    attn = torch.einsum("bihd,bjhd->bhij", q.float(), k.float())
+    attn = torch.einsum("bihd,bjhd->bhij", _op(q.float()), _op(k.float()))
     attn = attn / (d ** 0.5) + bias.float()
     attn = attn + (1 - mask[:, None, None].float()) * -inf
     attn = attn.softmax(dim=-1)
-    o = torch.einsum("bhij,bjhd->bihd", attn, v.float()).to(v.dtype)
+    o = torch.einsum("bhij,bjhd->bihd", _op(attn), _op(v.float())).to(v.dtype)
     o = o.reshape(B, -1, c_s)
     return linear(g * o, w["proj_o.weight"])
 

@@ -2,9 +2,13 @@
 
 * Config 3: the 64-layer trunk at N = 768 with 3 recycling steps (4 passes,
   ``boltz2.py:5203``), seed 3, against the fp32 oracle evaluated on the device, pass by pass.
-  A stack of 256 layer applications amplifies any perturbation, so next to the GPU-vs-oracle
-  error the test measures the oracle's own sensitivity: the same oracle run on inputs rounded
-  to fp16 (a relative perturbation of at most 2^-11).
+  The bar is the oracle's own precision model of 16-bit operands
+  (``pairformer_ref.operand_rounding(torch.float16)``: every matmul operand rounded to fp16,
+  fp32 accumulation and statistics -- this build's numerics contract): per pass, the GPU may
+  drift from fp32 by at most 2x what exact arithmetic on fp16 operands drifts (or the
+  north-star 2e-2 / 2e-3 of the rms, if larger).  The stack is not contractive across
+  recycling passes, so the drift grows from pass to pass in both; the test also reports the
+  oracle's sensitivity to an fp16 rounding of its inputs alone.
 * The reference's differential tests (``tests/test_tenstorrent.py:31-66``): the drop-in
   ``PairformerModule`` at N = 100 and N = 500 (padded to 128 / 512 inside) with the
   reference's input scales z = 26 randn, s = 8 randn, the c_z = 64 template stack, and the
@@ -47,11 +51,8 @@ def check_reference_case(name, got, want, start):
 # ------------------------------------------------------------------------------ config 3
 @pytest.mark.timeout(900)
 def test_config3_stack_depth(gpu):
-    """64 layers x 4 recycling passes at N = 768 (config 3) vs the fp32 oracle on the device.
-
-    Bar per pass: the north-star 2e-2 / 2e-3 of the rms, or, where the stack's own
-    sensitivity exceeds that, 2x the oracle's drift under an fp16 rounding of its inputs
-    (the amplification of a 2^-11 input perturbation through 256 layer applications)."""
+    """64 layers x 4 recycling passes at N = 768 (config 3) vs the fp32 oracle on the device,
+    with the fp16-operand precision model of the oracle as the bar."""
     cfg = synthetic.CONFIGS[3]
     N, n_blocks, steps = cfg["N"], 64, 3
     w = synthetic.stack_weights(n_blocks, cfg["seed"])
@@ -60,38 +61,40 @@ def test_config3_stack_depth(gpu):
     wd, wrd = _dev(w, gpu), _dev(w_rec, gpu)
     sd, zd, md = s_init.to(gpu), z_init.to(gpu), mask.to(gpu)
 
-    def run_oracle(s0, z0):
+    def run_oracle(s0, z0, tag, operand=None):
         out = []
 
         def hook(i, s, z):
             out.append((s.clone(), z.clone()))
-            print(f"[stack] oracle pass {i} done", flush=True)
+            print(f"[stack] {tag} pass {i} done", flush=True)
 
-        with torch.no_grad():
+        with torch.no_grad(), ref.operand_rounding(operand):
             ref.recycle(s0, z0, md, wd, wrd, n_blocks, steps, pass_hook=hook)
         return out
 
-    want = run_oracle(sd, zd)
-    print("[stack] oracle done", flush=True)
-    pert = run_oracle(sd.half().float(), zd.half().float())
-    print("[stack] perturbed oracle done", flush=True)
+    want = run_oracle(sd, zd, "fp32 oracle")
+    emu = run_oracle(sd, zd, "fp16-operand oracle", torch.float16)
+    pert = run_oracle(sd.half().float(), zd.half().float(), "fp32 oracle, fp16-rounded inputs")
 
     pf = pairformer.Pairformer(n_blocks, 32, 4, 24, 16, True, w)
     rec = pairformer.TrunkRecycler(pf, w_rec)
     got = []
     rec(sd.contiguous(), zd.contiguous(), md, steps, pass_hook=lambda i, s, z: got.append((s.clone(), z.clone())))
     torch.cuda.synchronize()
-    assert len(got) == len(want) == steps + 1
+    assert len(got) == len(want) == len(emu) == steps + 1
     bad = []
-    for i, ((gs, gz), (ws_, wz), (ps, pz)) in enumerate(zip(got, want, pert)):
-        for name, g, r, p in (("z", gz, wz, pz), ("s", gs, ws_, ps)):
+    for i in range(steps + 1):
+        for k, name in ((1, "z"), (0, "s")):
+            g, r, e, p = got[i][k], want[i][k], emu[i][k], pert[i][k]
             mx, mn = stats(g, r)
+            emx, emn = stats(e, r)
             dmx, dmn = stats(p, r)
-            print(f"[stack] pass {i} {name}: gpu max/rms={mx:.3e} mean/rms={mn:.3e} | "
-                  f"oracle fp16-input drift max/rms={dmx:.3e} mean/rms={dmn:.3e}", flush=True)
+            print(f"[stack] pass {i} {name}: gpu max/rms={mx:.3e} mean/rms={mn:.3e} | fp16-operand model "
+                  f"max/rms={emx:.3e} mean/rms={emn:.3e} | fp16-rounded inputs max/rms={dmx:.3e} "
+                  f"mean/rms={dmn:.3e}", flush=True)
             assert torch.isfinite(g).all()
-            if not (mx <= max(MAX_TOL, 2 * dmx) and mn <= max(MEAN_TOL, 2 * dmn)):
-                bad.append((i, name, mx, mn))
+            if not (mx <= max(MAX_TOL, 2 * emx) and mn <= max(MEAN_TOL, 2 * emn)):
+                bad.append((i, name, mx, mn, emx, emn))
     assert not bad, bad
 
 

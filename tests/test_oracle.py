@@ -526,3 +526,34 @@ def test_token_trans_bias_constant_rows_closed_form():
     got = diffusion_ref.token_trans_bias(z, w, 2)
     want = torch.cat([w[f"token_trans_proj_z.{l}.1.weight"] @ w[f"token_trans_proj_z.{l}.0.bias"] for l in range(2)])
     _close(got, want.expand(1, 2, 2, 6), 1e-6)
+
+
+# ----------------------------------------------------------------------------- operand-precision model
+def test_operand_rounding_is_off_by_default_and_restored():
+    g = torch.Generator().manual_seed(120)
+    x, w = torch.randn(5, 16, generator=g), torch.randn(8, 16, generator=g)
+    exact = F.linear(x, w)
+    assert torch.equal(ref.linear(x, w), exact)
+    with ref.operand_rounding(torch.float16):
+        assert torch.equal(ref.linear(x, w), F.linear(x.half().float(), w.half().float()))
+        with ref.operand_rounding(None):
+            assert torch.equal(ref.linear(x, w), exact)
+    assert ref._OPERAND is None and torch.equal(ref.linear(x, w), exact)
+
+
+def test_operand_rounding_layer_drift_scales_with_operand_precision():
+    """One layer under the 16-bit-operand precision model drifts from fp32 by about the
+    operand type's relative precision: fp16 (2^-11) well below bf16 (2^-8), both far above
+    fp32 noise -- a rounding site dropped from the model or applied twice breaks the ratio."""
+    N = 24
+    w = ref.sub(synthetic.stack_weights(1, 121), "layers.0")
+    s, z, mask, pm = synthetic.pair_inputs(N, 122)
+    s0, z0 = ref.pairformer_layer(s, z, mask, pm, w)
+    err = {}
+    for dt in (torch.float16, torch.bfloat16):
+        with ref.operand_rounding(dt):
+            s1, z1 = ref.pairformer_layer(s, z, mask, pm, w)
+        upd = z0 - z
+        err[dt] = ((z1 - z0).abs().mean() / upd.pow(2).mean().sqrt()).item()
+    assert 1e-5 < err[torch.float16] < 3e-3, err
+    assert 4 < err[torch.bfloat16] / err[torch.float16] < 16, err

@@ -13,7 +13,7 @@
 //              Q, K    op_t [B][N(row i)][H][N(j)][D]
 //              Vt      op_t [B][N(row i)][H][D][N(k)], keys stored at perm16(k) (bits 2
 //                      and 3 swapped) so a P.V operand fragment is one 16-byte run
-//              bias16  op_t [B][H][N(j)][N(k)]   (shared by all rows i)
+//              bias32  fp32 [B][H][N(j)][N(k)]   (shared by all rows i)
 //              mask16  op_t [B][N(i)][N(k)]      0, or -inf for masked / padding keys
 //   ta_attn  flash attention (see the kernel's comment): 16-wave workgroups of 4 frame rows
 //            x 128 queries, LDS-DMA ring, bias / mask / reference max folded into MFMAs,
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
     const float* __restrict__ lnw, const float* __restrict__ lnb,
     const op_t* __restrict__ wq, const op_t* __restrict__ wk, const op_t* __restrict__ wv,
     const op_t* __restrict__ wb, op_t* __restrict__ Q, op_t* __restrict__ K,
-    op_t* __restrict__ Vt, op_t* __restrict__ bias16, op_t* __restrict__ mask16,
+    op_t* __restrict__ Vt, float* __restrict__ bias32, op_t* __restrict__ mask16,
     int B, int N, int n_valid, int ending, float qscale, float eps) {
   constexpr int LW = CC + 8, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t plds[];
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
       for (int s2 = 0; s2 < KS; ++s2) acc = mfma32(ld_x8(plds + (3 * C + m) * LW + 16 * s2 + 8 * h), xf[s2], acc);
       if (h == 0) {
 #pragma unroll
-        for (int r = 0; r < H; ++r) bias16[(((long)b * H + r) * N + ip) * N + j0 + m] = (op_t)(acc[r] * LOG2E);
+        for (int r = 0; r < H; ++r) bias32[(((long)b * H + r) * N + ip) * N + j0 + m] = acc[r] * LOG2E;
       }
     }
   }
@@ -205,34 +205,47 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
 // Flash attention.  OUT_F32 = false: O op_t [B][N][N][H*D] (frame pair layout);
 // OUT_F32 = true: O fp32 [B][N][H][N][D] (the standalone attention-core API).
 //
-// A workgroup is 16 waves: 4 frame rows (ip0 .. ip0+3) x 4 blocks of 32 queries; it walks
-// 4 heads x N/64 key tiles.  Per step the workgroup's bias tile [128 q][64 k], the four
-// rows' K [64 k][32 d] and V^T [32 d][64 k] tiles and their mask entries move
-// global -> LDS by DMA (global_load_lds, no VGPR staging) through a 3-deep ring, one
-// barrier per step.  Scores S'^T[key][query] come out of five MFMAs per 32x32 tile:
-//     K.Q^T (2)  +  I.bias^T (2: identity A operand, op_t bias as the B operand)
-//                +  [1, mask[key]] . [-m[q], 1]^T (1: two used k-slots)
-// so the bias, the key mask and the reference max cost no VALU; the softmax is exp2,
-// an fp16 pair pack and v_dot2 row sums.  The reference max m[q] is kept as an op_t
-// value (exact as an MFMA operand) and moves lazily: at a head's first tile, while a
-// query has seen no unmasked key, or when a tile's row sum exceeds 2^14 (some P above
-// 2^9).  A P that would overflow op_t fails the same test before it reaches the P.V
-// MFMA, and the tile is then repacked from S' with the new reference.
-// Each wave takes its two 32-key halves in turn (128 VGPRs: four waves per SIMD).  On
-// gfx950 the step is bound by the SIMD's MFMA + v_exp_f32 time (the two largely
-// serialize), not by latency: 2, 4 or 8 waves per SIMD all measure alike.
+// A workgroup is 8 waves (two per SIMD): 4 frame rows (ip0 .. ip0+3) x 2 blocks of 64 queries;
+// each wave owns one row and two 32-query blocks and walks 4 heads x N/64 key tiles.  Per step
+// the workgroup's fp32 bias tile [128 q][64 k], the four rows' K [64 k][32 d] and V^T
+// [32 d][64 k] tiles and their mask entries move global -> LDS by DMA (global_load_lds, no
+// VGPR staging) through a 2-deep ring, one barrier per step.  Scores S'^T[key][query] come out
+// of three MFMAs per 32x32 tile:
+//     bias^T (fp32, the accumulator's start value, read from LDS in accumulator order)
+//     + K.Q^T (2)  +  [1, mask[key]] . [-m[q], 1]^T (1: two used k-slots)
+// so the bias, the key mask and the reference max cost no VALU and the bias is not rounded;
+// the softmax is exp2, an fp16 pair pack and v_dot2 row sums.  A wave's K and V^T fragments
+// serve both of its query blocks.  The reference max m[q] is kept as an op_t value (exact as
+// an MFMA operand) and moves lazily: at a head's first tile, while a query has seen no unmasked
+// key, or when a tile's row sum exceeds 2^14 (some P above 2^9).  A P that would overflow op_t
+// fails the same test before it reaches the P.V MFMA, and the tile is then repacked from S'
+// with the new reference.  Within a step the four 32x32 tiles (query block c, key half u) are
+// ordered so that every softmax has independent score MFMAs queued ahead of it and a tile's
+// scores are formed only after the softmax of the previous tile of the same query block (so
+// a rescale never has to shift already formed scores).
+// Each stage of a section sits right after the other, so the loop (unrolled by two) selects
+// the stage with the LDS instructions' immediate offsets.
 // Rows whose valid keys are all masked: the fp32 reference adds -1e9 to every logit,
 // which rounds them all to -1e9 (|logit| < 32), i.e. a uniform average over the keys.
-// Such a row zeroes Q and the identity operand and feeds mask 0 for its valid keys.
+// Such a row's waves skip the tiles (still taking part in every barrier and DMA) and write
+// the mean of v after the loop.
 // ---------------------------------------------------------------------------------
-constexpr int TA_WAVES = 16;
-constexpr int TS_BIAS = 0, TS_K = 16384, TS_V = 32768, TS_MASK = 49152, TS_STAGE = 50176;   // bytes
-constexpr size_t TA_LDS = 3 * (size_t)TS_STAGE;
+constexpr int TA_WAVES = 8;
+// LDS sections (bytes), each holding stage 0 then stage 1:
+//   bias fp32 [128 q][64 k]: rows of 256 B, 16-byte chunk c of row q at position c ^ (q & 15)
+//   K   op_t  [4 rows][64 k][32 d]: rows of 64 B, chunk swizzle swz4
+//   V^T op_t  [4 rows][32 d][64 k]: rows of 128 B, chunk swizzle swz8
+//   mask op_t [4 rows][64 k] (wave 0's 1 KB DMA; the upper 512 B repeat the lower)
+constexpr int TS_BIAS = 0, TB_STAGE = 32768;
+constexpr int TS_K = 65536, TK_STAGE = 16384;
+constexpr int TS_V = 98304, TV_STAGE = 16384;
+constexpr int TS_MASK = 131072, TM_STAGE = 1024;
+constexpr size_t TA_LDS = (size_t)TS_MASK + 2 * TM_STAGE;
 constexpr float LSTEP_MAX = 16384.f;   // per-lane row sum of one tile that forces a rescale
 
-// 16-byte chunk swizzles: rows of 8 chunks (bias, V^T) and of 4 chunks (K).  A fragment
-// read takes one chunk from each of 32 consecutive rows; any 16 consecutive rows land in
-// 16 distinct 16-byte bank groups.
+// 16-byte chunk swizzles: rows of 8 chunks (V^T) and of 4 chunks (K).  A fragment read takes
+// one chunk from each of 32 consecutive rows; any 16 consecutive rows land in 16 distinct
+// 16-byte bank groups.
 PF_DEV int swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 PF_DEV int swz4(int r) { return (r >> 2) & 3; }
 PF_DEV opx8 lds_x8(const char* p) { return *reinterpret_cast<const opx8*>(p); }
@@ -244,16 +257,37 @@ PF_DEV opx8 slots01(int h, uint32_t lo_hi) {
   const u32x4 v = {h ? 0u : lo_hi, 0u, 0u, 0u};
   return as_x8(v);
 }
+template <int V>
+using ic = std::integral_constant<int, V>;
+// LDS reads from absolute LDS byte addresses (the per-lane address registers already hold the
+// allocation base, so the loop's reads need no address arithmetic beyond the immediate offset)
+typedef __attribute__((address_space(3))) const char* lds_ptr;
+PF_DEV lds_ptr lds_at(uint32_t a) { return (lds_ptr)(uintptr_t)a; }
+PF_DEV opx8 lds_rd8(uint32_t a) { return *reinterpret_cast<__attribute__((address_space(3))) const opx8*>(lds_at(a)); }
+PF_DEV f32x4 lds_rd4f(uint32_t a) {
+  return *reinterpret_cast<__attribute__((address_space(3))) const f32x4*>(lds_at(a));
+}
+PF_DEV uint32_t lds_rd16(uint32_t a) {
+  return *reinterpret_cast<__attribute__((address_space(3))) const uint16_t*>(lds_at(a));
+}
+// Raw buffer resource over `bytes` bytes at `p` (stride 0, reads beyond `bytes` return zero).
+PF_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* p, long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)min(bytes, 0x7fffffffl), 0x00020000);
+}
+// 16 bytes per lane from resource byte offset voff + soff into LDS at lds + 16 * lane.
+PF_DEV void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
 
 template <bool OUT_F32>
 __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
     const op_t* __restrict__ Q, const op_t* __restrict__ K, const op_t* __restrict__ Vt,
-    const op_t* __restrict__ bias16, const op_t* __restrict__ mask16, op_t* __restrict__ O16,
+    const float* __restrict__ bias32, const op_t* __restrict__ mask16, op_t* __restrict__ O16,
     float* __restrict__ O32, int N, int n_valid, int total) {
   extern __shared__ __attribute__((aligned(16))) char alds[];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int row = wid & 3, qw = wid >> 2;   // frame row, block of 32 queries
+  const int row = wid & 3, qp = wid >> 2;   // frame row, pair of 32-query blocks
   const int nQP = (N + 127) >> 7, nKB = N >> 6, T = H * nKB;
   const int w = xcd_remap(blockIdx.x, total);
   const int per_b = (N >> 2) * nQP;
@@ -262,40 +296,71 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   const int rg = rem / nQP;
   const int jw0 = (rem - rg * nQP) * 128;
   const int ip0 = 4 * rg, ip = ip0 + row;
-  const int jq0 = jw0 + 32 * qw;
-  const bool qvalid = jq0 < N;            // query blocks past N (trailing part tile) idle
   const long NN = (long)N * N;
   const int seqD = N * D;                 // elements of one (row, head) Q / K / V^T block
 
-  // ---- DMA: chunk tid of each 16 KB tile; byte offsets from wave-uniform bases ----
-  const op_t* bias_b = bias16 + (long)b * H * NN;
-  const op_t* k_b = K + ((long)b * N + ip0) * H * seqD;
-  const op_t* v_b = Vt + ((long)b * N + ip0) * H * seqD;
-  const op_t* mask_b = mask16 + ((long)b * N + ip0) * N;
-  const uint32_t offB = 2u * (min(jw0 + (tid >> 3), N - 1) * N + 8 * ((tid & 7) ^ swz8(tid >> 3)));
-  const int rk = tid >> 8, kk = (tid >> 2) & 63, dd = (tid >> 3) & 31;
-  const uint32_t offK = 2u * (rk * H * seqD + kk * D + 8 * ((tid & 3) ^ swz4(kk)));
-  const uint32_t offV = 2u * (rk * H * seqD + dd * N + 8 * ((tid & 7) ^ swz8(dd)));
+  // ---- DMA: buffer resources (SGPRs) over this workgroup's operands, per-lane 32-bit source
+  // offsets, the step's offset as the uniform soffset; reads outside a resource return 0 ----
+  // bias: wave w's instruction j fills LDS bytes 4096 w + 1024 j .. of the stage, i.e. rows
+  // q = 16 w + 4 j + (lane >> 4), position lane & 15, which holds chunk (lane & 15) ^ (q & 15).
+  // K and V^T: chunk tid + 512 j of the 16 KB tile (instruction j); mask: wave 0, 1 KB.
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(bias32 + (long)b * H * NN, (long)H * NN * 4);
+  const __amdgpu_buffer_rsrc_t rK = make_rsrc(K + ((long)b * N + ip0) * H * seqD, 4l * H * seqD * 2);
+  const __amdgpu_buffer_rsrc_t rV = make_rsrc(Vt + ((long)b * N + ip0) * H * seqD, 4l * H * seqD * 2);
+  const __amdgpu_buffer_rsrc_t rM = make_rsrc(mask16 + ((long)b * N + ip0) * N, 4l * N * 2);
+  uint32_t offB[4], offK[2], offV[2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int q = 16 * wid + 4 * j + (lane >> 4);
+    offB[j] = 4u * ((uint32_t)min(jw0 + q, N - 1) * (uint32_t)N + 4u * (uint32_t)((lane & 15) ^ (q & 15)));
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = tid + 512 * j;
+    const int rk = c >> 8, kk = (c >> 2) & 63, dd = (c >> 3) & 31;
+    offK[j] = 2u * (rk * H * seqD + kk * D + 8 * ((c & 3) ^ swz4(kk)));
+    offV[j] = 2u * (rk * H * seqD + dd * N + 8 * ((c & 7) ^ swz8(dd)));
+  }
   const uint32_t offM = 2u * (((lane >> 3) & 3) * N + 8 * (lane & 7));
-  auto issue = [&](int st_off, int hd, int kb0) PF_INLINE {
-    char* st = alds + st_off + 1024 * wid;
-    __builtin_amdgcn_global_load_lds((const char*)(bias_b + (long)hd * NN + kb0) + offB, st + TS_BIAS, 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const char*)(k_b + hd * seqD + kb0 * D) + offK, st + TS_K, 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const char*)(v_b + hd * seqD + kb0) + offV, st + TS_V, 16, 0, 0);
-    if (wid == 0)
-      __builtin_amdgcn_global_load_lds((const char*)(mask_b + kb0) + offM, alds + st_off + TS_MASK, 16, 0, 0);
+  // stage `s` of step (hd, kb0)
+  auto issue = [&](int s, int hd, int kb0) PF_INLINE {
+    const uint32_t sb = 4u * ((uint32_t)hd * (uint32_t)NN + (uint32_t)kb0);
+    const uint32_t skv = 2u * ((uint32_t)(hd * seqD) + (uint32_t)kb0 * D);
+    const uint32_t sv = 2u * ((uint32_t)(hd * seqD) + (uint32_t)kb0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(rB, alds + TS_BIAS + s * TB_STAGE + 4096 * wid + 1024 * j, offB[j], sb);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      dma16(rK, alds + TS_K + s * TK_STAGE + 1024 * wid + 8192 * j, offK[j], skv);
+      dma16(rV, alds + TS_V + s * TV_STAGE + 1024 * wid + 8192 * j, offV[j], sv);
+    }
+    if (wid == 0) dma16(rM, alds + TS_MASK + s * TM_STAGE, offM, 2u * (uint32_t)kb0);
   };
 
-  // ---- per-lane LDS read addresses (bytes from a stage base) ----
-  const int sw = swz8(m), ksw = swz4(m);
-  int aB[4], aK[2];
+  // ---- per-lane LDS read addresses (stage 0; stage 1 adds the section's stage size) ----
+  // bias of query block c (rows 64 qp + 32 c + m): 32 c rows further = 8192 B
+  const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)alds;
+  const int qrow = 64 * qp + m;
+  uint32_t aB[8], aV[4], aK[2];
 #pragma unroll
-  for (int u = 0; u < 4; ++u)            // u = 2*kb + s: chunk 2u + h of a 64-key row
-    aB[u] = TS_BIAS + 128 * (32 * qw + m) + 16 * ((2 * u + h) ^ sw);
+  for (int u = 0; u < 2; ++u)            // key half u, accumulator register group g
 #pragma unroll
-  for (int s = 0; s < 2; ++s) aK[s] = TS_K + 4096 * row + 64 * m + 16 * ((2 * s + h) ^ ksw);
-  const int dV = TS_V - TS_BIAS + 4096 * row - 4096 * qw;   // V^T chunk (m, c) sits at aB + dV
-  const int aM = TS_MASK + 128 * row + 2 * m;
+    for (int g = 0; g < 4; ++g)
+      aB[4 * u + g] = base + TS_BIAS + 256 * qrow + 16 * ((8 * u + 2 * g + h) ^ (qrow & 15));
+#pragma unroll
+  for (int c = 0; c < 4; ++c)            // c = 2 u + s: chunk 2c + h of a 64-key V^T row
+    aV[c] = base + TS_V + 4096 * row + 128 * m + 16 * ((2 * c + h) ^ swz8(m));
+  const int ksw = swz4(m);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) aK[s] = base + TS_K + 4096 * row + 64 * m + 16 * ((2 * s + h) ^ ksw);
+  uint32_t aM = base + TS_MASK + 128 * row + 2 * m;
+  // opaque to the optimizer: each read is then one address register + an immediate offset
+  // (otherwise the sums are split up again and re-added at every read)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(aB[i]));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(aV[i]));
+  asm volatile("" : "+v"(aK[0]), "+v"(aK[1]), "+v"(aM));
 
   // rows whose valid keys are all masked (wave-uniform)
   bool live_l = false;
@@ -305,40 +370,51 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   }
   const bool live = __ballot(live_l) != 0;
 
-  // identity A operand of k-step s: lane (row m, half h) slot t is 1 iff m == 16s + 8h + t
   const uint32_t ONE = half_bits((op_t)1.f);
-  opx8 iden[2];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int t = m - 16 * s - 8 * h;   // the slot holding the 1, if in 0..7
-    u32x4 v;
-#pragma unroll
-    for (int wd = 0; wd < 4; ++wd)
-      v[wd] = !live || (t >> 1) != wd ? 0u : (t & 1) ? ONE << 16 : ONE;
-    iden[s] = as_x8(v);
-  }
-  auto fold_b = [&](float mv) PF_INLINE { return slots01(h, half_bits((op_t)(-mv)) | ONE << 16); };
+  // the rank-1 operands are 4-register tuples whose words 1..3 stay zero: only word 0 changes
+  // ([-m, 1] of a block's reference in fb, [1, mask] of a key half in ra), half 1 of the wave
+  // holds zero
+  u32x4 fb[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}}, ra[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  auto set_fb = [&](int c, float mv) PF_INLINE {
+    fb[c][0] = h ? 0u : (half_bits((op_t)(-mv)) | ONE << 16);
+    asm volatile("" : "+v"(fb[c]));
+  };
 
-  const int jq = min(jq0, N - 32);
-  opx8 qf[2], qn[2], fb;
-  f32x16 o;
-  float mh, lsum;
-  bool mset;
-  auto q_load = [&](int hd) PF_INLINE {
-    const op_t* qp = Q + ((((long)b * N + ip) * H + hd) * N + jq + m) * D + 8 * h;
+  // per query block c: first query jq0[c]; blocks past N (trailing part tile) idle
+  int jq0[2];
+  bool qvalid[2];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) qn[s] = ld_x8(qp + 16 * s);
+  for (int c = 0; c < 2; ++c) {
+    jq0[c] = jw0 + 64 * qp + 32 * c;
+    qvalid[c] = jq0[c] < N;
+  }
+  const bool any_valid = qvalid[0];
+  opx8 qf[2][2], qn[2][2];
+  f32x16 o[2];
+  float mh[2], lsum[2];
+  bool mset[2];
+  auto q_load = [&](int hd) PF_INLINE {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int jq = min(jq0[c], N - 32);
+      const op_t* qptr = Q + ((((long)b * N + ip) * H + hd) * N + jq + m) * D + 8 * h;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) qn[c][s] = ld_x8(qptr + 16 * s);
+    }
   };
   auto head_start = [&]() PF_INLINE {
-    o = zero16();
-    lsum = 0.f;
-    mh = 0.f;
-    mset = false;
-    fb = fold_b(0.f);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      o[c] = zero16();
+      lsum[c] = 0.f;
+      mh[c] = 0.f;
+      mset[c] = false;
+      set_fb(c, 0.f);
+    }
   };
   // P = exp2(S') packed into the two P.V operands; returns the lane's row sum
   auto exp_pack = [&](const f32x16& sc, u32x4 (&pf)[2]) PF_INLINE {
-    float ls = 0.f;
+    float ls[2] = {0.f, 0.f};   // two partial sums: half as long a v_dot2 chain
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -346,137 +422,194 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
         opx2 pk;
         pk[0] = (op_t)exp2_fast(sc[8 * ks + t2]);
         pk[1] = (op_t)exp2_fast(sc[8 * ks + t2 + 1]);
-        ls = dot2_ones(pk, ls);
+        ls[ks] = dot2_ones(pk, ls[ks]);
         pf[ks][t2 >> 1] = __builtin_bit_cast(uint32_t, pk);
       }
-    return ls;
+    return ls[0] + ls[1];
   };
-  // One step = two 32-key halves.  Each half forms its scores S'^T = K.Q^T + I.bias^T +
-  // [1, mask].[-m, 1]^T, the softmax (P against the current reference; if a query has no
-  // reference yet or the row sum exceeds LSTEP_MAX the reference moves, o and lsum are
-  // rescaled and P is packed again -- after a move P <= 2^RESCALE_SLACK, so once is
-  // enough), then P.V.  The halves are software-pipelined: the scores of half 1 are issued
-  // before the softmax of half 0, so half 0's exp / pack VALU work runs while half 1's
-  // score MFMAs execute, and half 1's while half 0's P.V MFMAs execute.  A rescale in
-  // half 0 moves the reference under half 1's already formed scores: they are shifted by
-  // the same amount.
-  auto rescale = [&](f32x16& sc, u32x4 (&pf)[2], float& l, f32x16* other) PF_INLINE {
-    float mx = sc[0];
+  // One step (stage STG) of a live row, per query block c: the scores of its two 32x32 tiles
+  // (key halves u), their softmax against the current reference, one check, and the four P.V
+  // MFMAs.  When the check fails (a query without a reference yet -- every head's first step
+  // -- or a tile row sum above LSTEP_MAX) the reference moves to the tiles' maxima first.
+  auto step4 = [&](auto stg) PF_INLINE {
+    constexpr int STG = decltype(stg)::value;
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[r]);
-    mx = xor32_max(mx);
-    const float d = mset ? (mx > RESCALE_SLACK ? mx : 0.f) : (mx == -INFINITY ? 0.f : mx);
-    const float mnew = (float)(op_t)(mh + d);
-    const float dsub = mnew - mh;
-    const float alpha = mset ? exp2_fast(-dsub) : 1.f;
-    lsum *= alpha;
+    for (int u = 0; u < 2; ++u) {   // [1, mask[key]] rank-1 operands of the two key halves
+      ra[u][0] = h ? 0u : (ONE | lds_rd16(aM + STG * TM_STAGE + 64 * u) << 16);
+      asm volatile("" : "+v"(ra[u]));
+    }
+    opx8 kf[2][2];   // [key half][k step]
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      o[r] *= alpha;
-      sc[r] -= dsub;
-    }
-    if (other) {
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) (*other)[r] -= dsub;
-    }
-    mset = mset || mx != -INFINITY;
-    mh = mnew;
-    fb = fold_b(mnew);
-    l = exp_pack(sc, pf);
-  };
-  auto step2 = [&](const char* st, int kb0) PF_INLINE {
-    uint32_t mk0, mk1;
-    if (live) {
-      mk0 = *reinterpret_cast<const uint16_t*>(st + aM);
-      mk1 = *reinterpret_cast<const uint16_t*>(st + aM + 64);
-    } else {
-      mk0 = half_bits((op_t)(kb0 + m < n_valid ? 0.f : -INFINITY));
-      mk1 = half_bits((op_t)(kb0 + 32 + m < n_valid ? 0.f : -INFINITY));
-    }
-    f32x16 sc0, sc1;
-    {
-      const opx8 k0 = lds_x8(st + aK[0]), k1 = lds_x8(st + aK[1]);
-      const opx8 b0 = lds_x8(st + aB[0]), b1 = lds_x8(st + aB[1]);
-      sc0 = mfma32(k0, qf[0], zero16());
-      sc0 = mfma32(k1, qf[1], sc0);
-      sc0 = mfma32(iden[0], b0, sc0);
-      sc0 = mfma32(iden[1], b1, sc0);
-      sc0 = mfma32(slots01(h, ONE | mk0 << 16), fb, sc0);
-    }
-    {
-      const opx8 k0 = lds_x8(st + aK[0] + 2048), k1 = lds_x8(st + aK[1] + 2048);
-      const opx8 b0 = lds_x8(st + aB[2]), b1 = lds_x8(st + aB[3]);
-      sc1 = mfma32(k0, qf[0], zero16());
-      sc1 = mfma32(k1, qf[1], sc1);
-      sc1 = mfma32(iden[0], b0, sc1);
-      sc1 = mfma32(iden[1], b1, sc1);
-      sc1 = mfma32(slots01(h, ONE | mk1 << 16), fb, sc1);
-    }
-    u32x4 pf[2];
-    float l = exp_pack(sc0, pf);
-    if (__ballot(!mset || l > LSTEP_MAX) != 0) rescale(sc0, pf, l, &sc1);
-    lsum += l;
-    {
-      const opx8 v0 = lds_x8(st + dV + aB[0]), v1 = lds_x8(st + dV + aB[1]);
-      o = mfma32(v0, as_x8(pf[0]), o);
-      o = mfma32(v1, as_x8(pf[1]), o);
-    }
-    l = exp_pack(sc1, pf);
-    if (__ballot(!mset || l > LSTEP_MAX) != 0) rescale(sc1, pf, l, nullptr);
-    lsum += l;
-    {
-      const opx8 v0 = lds_x8(st + dV + aB[2]), v1 = lds_x8(st + dV + aB[3]);
-      o = mfma32(v0, as_x8(pf[0]), o);
-      o = mfma32(v1, as_x8(pf[1]), o);
-    }
+      for (int s = 0; s < 2; ++s) kf[u][s] = lds_rd8(aK[s] + STG * TK_STAGE + 2048 * u);
+    // scores of block c: bias as the accumulator start, then K.Q^T and the mask / max fold
+    auto scores = [&](auto cc, f32x16 (&sc)[2]) PF_INLINE {
+      constexpr int c = decltype(cc)::value;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 bv = lds_rd4f(aB[4 * u + g] + STG * TB_STAGE + 8192 * c);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sc[u][4 * g + e] = bv[e];
+        }
+        sc[u] = mfma32(kf[u][0], qf[c][0], sc[u]);
+        sc[u] = mfma32(kf[u][1], qf[c][1], sc[u]);
+        sc[u] = mfma32(as_x8(ra[u]), as_x8(fb[c]), sc[u]);
+      }
+    };
+    // Move block c's reference to its two tiles' maxima (none set yet: to the max; set: by the
+    // max when it exceeds RESCALE_SLACK), rescale o and lsum, repack P.
+    auto rescale = [&](auto cc, f32x16 (&sc)[2], u32x4 (&pf)[2][2], float& ls0, float& ls1) PF_INLINE {
+      constexpr int c = decltype(cc)::value;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[u][r]);
+      mx = xor32_max(mx);
+      const float d = mset[c] ? (mx > RESCALE_SLACK ? mx : 0.f) : (mx == -INFINITY ? 0.f : mx);
+      const float mnew = (float)(op_t)(mh[c] + d);
+      const float dsub = mnew - mh[c];
+      const float alpha = mset[c] ? exp2_fast(-dsub) : 1.f;
+      lsum[c] *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[c][r] *= alpha;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[u][r] -= dsub;
+      ls0 = exp_pack(sc[0], pf[0]);
+      ls1 = exp_pack(sc[1], pf[1]);
+      mset[c] = mset[c] || mx != -INFINITY;
+      mh[c] = mnew;
+      set_fb(c, mnew);
+    };
+    auto pv = [&](auto cc, const u32x4 (&pf)[2][2]) PF_INLINE {
+      constexpr int c = decltype(cc)::value;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const opx8 v0 = lds_rd8(aV[2 * u] + STG * TV_STAGE), v1 = lds_rd8(aV[2 * u + 1] + STG * TV_STAGE);
+        o[c] = mfma32(v0, as_x8(pf[u][0]), o[c]);
+        o[c] = mfma32(v1, as_x8(pf[u][1]), o[c]);
+      }
+    };
+    // Block 1's score MFMAs are issued before block 0's softmax and block 0's P.V before block
+    // 1's, so each softmax has independent MFMA work in flight.  At a head's first step no
+    // reference is set (mset false), so the check sends both blocks through the rescale.
+    f32x16 s0[2], s1[2];
+    u32x4 p0[2][2], p1[2][2];
+    float l00, l01, l10, l11;
+    scores(ic<0>{}, s0);
+    scores(ic<1>{}, s1);
+    l00 = exp_pack(s0[0], p0[0]);
+    l01 = exp_pack(s0[1], p0[1]);
+    if (__ballot(!mset[0] || fmaxf(l00, l01) > LSTEP_MAX) != 0) rescale(ic<0>{}, s0, p0, l00, l01);
+    lsum[0] += l00 + l01;
+    pv(ic<0>{}, p0);
+    l10 = exp_pack(s1[0], p1[0]);
+    l11 = exp_pack(s1[1], p1[1]);
+    if (__ballot(!mset[1] || fmaxf(l10, l11) > LSTEP_MAX) != 0) rescale(ic<1>{}, s1, p1, l10, l11);
+    lsum[1] += l10 + l11;
+    pv(ic<1>{}, p1);
   };
   auto finalize = [&](int hd) PF_INLINE {
-    const float inv = rcp_fast(xor32_sum(lsum));
-    const int j = jq0 + m;
-    const long rowbase = ((long)b * N + ip) * H;
-    if (OUT_F32) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        f32x4 v;
+    for (int c = 0; c < 2; ++c) {
+      if (!qvalid[c]) continue;
+      const float inv = rcp_fast(xor32_sum(lsum[c]));
+      const int j = jq0[c] + m;
+      const long rowbase = ((long)b * N + ip) * H;
+      if (OUT_F32) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = o[4 * g + e] * inv;
-        *reinterpret_cast<f32x4*>(O32 + ((rowbase + hd) * N + j) * D + 8 * g + 4 * h) = v;
+        for (int g = 0; g < 4; ++g) {
+          f32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = o[c][4 * g + e] * inv;
+          *reinterpret_cast<f32x4*>(O32 + ((rowbase + hd) * N + j) * D + 8 * g + 4 * h) = v;
+        }
+      } else {
+        store_runs16(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd, o[c], inv, h);   // 16-byte runs
       }
-    } else {
-      store_runs16(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd, o, inv, h);   // 16-byte runs
     }
   };
 
-  // Step loop: T steps, one barrier each (the loop-top wait + barrier), the DMA of the
-  // next stage and, at a head's last tile, the next head's Q prefetch; then the two halves.
-  int cur = 0;          // stage byte offset of step it
+  // Step loop: T steps (T = 4 N / 64, even), one barrier each (the loop-top wait + barrier),
+  // the DMA of the next step into the other stage and, at a head's last tile, the next head's
+  // Q prefetch; then the four tiles.  The barrier also tells every wave that the other stage
+  // (read in the previous step) is free.
   int kbi = 0, hd = 0;  // step it = hd * nKB + kbi
   q_load(0);
   issue(0, 0, 0);
-  for (int it = 0; it < T; ++it) {
-    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));   // stage it landed ...
-    __builtin_amdgcn_s_barrier();              // ... for every wave; stage it-2 is free
+  auto one_step = [&](auto stg, int it) PF_INLINE {
+    constexpr int STG = decltype(stg)::value;
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));   // this wave's part of stage STG landed ...
+    __builtin_amdgcn_s_barrier();              // ... for every wave; stage STG ^ 1 is free
     asm volatile("" ::: "memory");
     if (kbi == 0) {   // take this head's Q before qn is reused
 #pragma unroll
-      for (int s = 0; s < 2; ++s) qf[s] = live ? qn[s] : zero_x8();
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) qf[c][s] = qn[c][s];
     }
-    const int nst = cur == 2 * TS_STAGE ? 0 : cur + TS_STAGE;
     if (it + 1 < T) {
       const bool wrap = kbi + 1 == nKB;
-      issue(nst, wrap ? hd + 1 : hd, wrap ? 0 : 64 * (kbi + 1));
+      issue(STG ^ 1, wrap ? hd + 1 : hd, wrap ? 0 : 64 * (kbi + 1));
       if (wrap) q_load(hd + 1);
     }
-    if (qvalid) {
+    if (any_valid && live) {
       if (kbi == 0) head_start();
-      const char* st = alds + cur;
-      step2(st, 64 * kbi);
+      step4(stg);
       if (kbi == nKB - 1) finalize(hd);
     }
-    cur = nst;
     if (++kbi == nKB) {
       kbi = 0;
       ++hd;
+    }
+  };
+  for (int it = 0; it < T; it += 2) {
+    one_step(ic<0>{}, it);
+    one_step(ic<1>{}, it + 1);
+  }
+
+  // A dead row (every valid key masked): the reference's logits all round to -1e9, so each
+  // query's output is the plain mean of v over the n_valid keys.  The wave sums its row's V^T
+  // (keys stored at perm16 positions) for d = m, the two lane halves taking alternate keys.
+  if (!live && any_valid) {
+    const float inv_n = 1.f / (float)n_valid;
+    for (int hd2 = 0; hd2 < H; ++hd2) {
+      const op_t* vrow = Vt + ((((long)b * N + ip) * H + hd2) * D + m) * (long)N;
+      float acc = 0.f;
+      for (int p0 = 8 * h; p0 < N; p0 += 16) {   // 8 stored keys per 16-byte load
+        const opx8 v8 = ld_x8(vrow + p0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (perm16(p0 + e) < n_valid) acc += (float)v8[e];
+      }
+      const float mean = xor32_sum(acc) * inv_n;   // lanes m and m + 32 both hold d = m
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        if (!qvalid[c]) continue;
+        const int j = jq0[c] + m;
+        if (OUT_F32) {
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = __shfl(mean, 16 * h + 4 * q4 + e);
+            *reinterpret_cast<f32x4*>(O32 + ((((long)b * N + ip) * H + hd2) * N + j) * D + 16 * h + 4 * q4) = v;
+          }
+        } else {
+#pragma unroll
+          for (int q8 = 0; q8 < 2; ++q8) {
+            opx8 v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = (op_t)__shfl(mean, 16 * h + 8 * q8 + e);
+            st_x8(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd2 + 16 * h + 8 * q8, v);
+          }
+        }
+      }
     }
   }
 }
@@ -584,21 +717,25 @@ __global__ void ta_prep_qkv_kernel(const float* __restrict__ q, const float* __r
 }
 
 __global__ void ta_prep_bias_kernel(const float* __restrict__ bias, const float* __restrict__ mask,
-                                    op_t* __restrict__ bias16, op_t* __restrict__ mask16,
+                                    float* __restrict__ bias32, op_t* __restrict__ mask16,
                                     long nbias, long nmask, int N, int n_valid) {
   for (long e = (long)blockIdx.x * blockDim.x + threadIdx.x; e < nbias; e += (long)gridDim.x * blockDim.x) {
-    bias16[e] = (op_t)(bias[e] * LOG2E);
+    bias32[e] = bias[e] * LOG2E;
     if (e < nmask) mask16[e] = mask_term((int)(e % N) >= n_valid, mask ? mask[e] : 1.f);
   }
 }
 
 struct TaBuffers {
-  op_t *Q, *K, *Vt, *O, *bias16, *mask16;
+  op_t *Q, *K, *Vt, *O;
+  float* bias32;
+  op_t* mask16;
 };
 
+// Workspace: Q, K, V^T, O (op_t, [B][N][H][N][D] each), the fp32 bias [B][H][N][N], the op_t
+// mask term [B][N][N].
 size_t ta_buffers_size(int B, int N) {
   const size_t e = (size_t)B * N * H * N * D;
-  return (4 * e + (size_t)B * H * N * N + (size_t)B * N * N) * sizeof(op_t);
+  return 4 * e * sizeof(op_t) + (size_t)B * H * N * N * sizeof(float) + (size_t)B * N * N * sizeof(op_t);
 }
 
 TaBuffers ta_buffers(void* ws, int B, int N) {
@@ -608,8 +745,8 @@ TaBuffers ta_buffers(void* ws, int B, int N) {
   t.K = t.Q + e;
   t.Vt = t.K + e;
   t.O = t.Vt + e;
-  t.bias16 = t.O + e;
-  t.mask16 = t.bias16 + (size_t)B * H * N * N;
+  t.bias32 = reinterpret_cast<float*>(t.O + e);
+  t.mask16 = reinterpret_cast<op_t*>(t.bias32 + (size_t)B * H * N * N);
   return t;
 }
 
@@ -617,7 +754,7 @@ template <bool OUT_F32>
 int launch_attn(const TaBuffers& t, float* o32, int B, int N, int n_valid, hipStream_t st) {
   if (const int rc = pf_reserve_lds((const void*)ta_attn_kernel<OUT_F32>, TA_LDS, "ta_attn_kernel")) return rc;
   const int total = B * (N / 4) * ((N + 127) / 128);
-  ta_attn_kernel<OUT_F32><<<total, 64 * TA_WAVES, TA_LDS, st>>>(t.Q, t.K, t.Vt, t.bias16, t.mask16, t.O, o32, N,
+  ta_attn_kernel<OUT_F32><<<total, 64 * TA_WAVES, TA_LDS, st>>>(t.Q, t.K, t.Vt, t.bias32, t.mask16, t.O, o32, N,
                                                                n_valid, total);
   PF_CHECK_LAUNCH("ta_attn_kernel");
   return PF_OK;
@@ -638,7 +775,7 @@ int triatt_run(const pf_triatt_args* a) {
     const int grid = (int)min((long)cus, (positions / 32 + TAP_WAVES - 1) / TAP_WAVES);
     ta_proj_kernel<CC><<<grid, 64 * TAP_WAVES, tap_lds<CC>(), st>>>(
         a->z_in, a->pair_mask, a->ln_w, a->ln_b, (const op_t*)a->w_q, (const op_t*)a->w_k, (const op_t*)a->w_v,
-        (const op_t*)a->w_bias, t.Q, t.K, t.Vt, t.bias16, t.mask16, B, N, n_valid, a->ending, qscale, a->eps);
+        (const op_t*)a->w_bias, t.Q, t.K, t.Vt, t.bias32, t.mask16, B, N, n_valid, a->ending, qscale, a->eps);
     PF_CHECK_LAUNCH("ta_proj_kernel");
   }
   int rc = launch_attn<false>(t, nullptr, B, N, n_valid, st);
@@ -654,6 +791,10 @@ int triatt_run(const pf_triatt_args* a) {
   }
   return PF_OK;
 }
+
+// The attention kernel addresses a batch's bias ([H][N][N] fp32) through one raw buffer
+// resource, whose range is below 2^31 bytes.
+bool ta_shape_ok(int N) { return (long)H * N * N * 4 < (1l << 31); }
 
 }  // namespace
 
@@ -672,8 +813,8 @@ extern "C" int pf_triatt_fwd(const pf_triatt_args* a) {
                    a->C, a->H, a->D);
   if (a->B <= 0 || a->N <= 0 || a->N % 64)
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: need B > 0 and N a positive multiple of 64 (B=%d N=%d)", a->B, a->N);
-  if ((unsigned long long)a->B * a->N * a->N >= (1ull << 32))
-    return pf_fail(PF_E_INVALID, "pf_triatt_fwd: B * N * N must be below 2^32 (B=%d N=%d)", a->B, a->N);
+  if ((unsigned long long)a->B * a->N * a->N >= (1ull << 32) || !ta_shape_ok(a->N))
+    return pf_fail(PF_E_INVALID, "pf_triatt_fwd: need B * N * N < 2^32 and N <= 11584 (B=%d N=%d)", a->B, a->N);
   if (!a->z_in || !a->out || !a->ln_w || !a->ln_b || !a->w_bias || !a->w_q || !a->w_k ||
       !a->w_v || !a->w_g || !a->w_o || !a->workspace)
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: null pointer argument");
@@ -690,8 +831,9 @@ extern "C" int pf_triatt_attend_workspace(void* workspace, size_t workspace_byte
   if (!workspace) return pf_fail(PF_E_INVALID, "pf_triatt_attend_workspace: null workspace");
   if (B <= 0 || N <= 0 || N % 64)
     return pf_fail(PF_E_INVALID, "pf_triatt_attend_workspace: need B > 0 and N a positive multiple of 64");
-  if ((unsigned long long)B * N * N >= (1ull << 32))
-    return pf_fail(PF_E_INVALID, "pf_triatt_attend_workspace: B * N * N must be below 2^32 (B=%d N=%d)", B, N);
+  if ((unsigned long long)B * N * N >= (1ull << 32) || !ta_shape_ok(N))
+    return pf_fail(PF_E_INVALID, "pf_triatt_attend_workspace: need B * N * N < 2^32 and N <= 11584 (B=%d N=%d)",
+                   B, N);
   if (n_valid < 0 || n_valid > N)
     return pf_fail(PF_E_INVALID, "pf_triatt_attend_workspace: n_valid %d outside [0, N=%d]", n_valid, N);
   const size_t need = ta_buffers_size(B, N);
@@ -713,6 +855,8 @@ extern "C" int pf_tri_attention(const float* q, const float* k, const float* v, 
     return pf_fail(PF_E_INVALID, "pf_tri_attention: only H=4, D=32 supported (got H=%d D=%d)", H_, D_);
   if (B <= 0 || N <= 0 || N % 64)
     return pf_fail(PF_E_INVALID, "pf_tri_attention: need B > 0 and N a positive multiple of 64 (B=%d N=%d)", B, N);
+  if ((unsigned long long)B * N * N >= (1ull << 32) || !ta_shape_ok(N))
+    return pf_fail(PF_E_INVALID, "pf_tri_attention: need B * N * N < 2^32 and N <= 11584 (B=%d N=%d)", B, N);
   if (n_valid < 0 || n_valid > N)
     return pf_fail(PF_E_INVALID, "pf_tri_attention: n_valid %d outside [0, N=%d]", n_valid, N);
   if (n_valid == 0) n_valid = N;
@@ -726,7 +870,7 @@ extern "C" int pf_tri_attention(const float* q, const float* k, const float* v, 
   const long rows = (long)B * N * H;
   ta_prep_qkv_kernel<<<2048, 256, 0, st>>>(q, k, v, scale * LOG2E, t.Q, t.K, t.Vt, rows, N);
   PF_CHECK_LAUNCH("ta_prep_qkv_kernel");
-  ta_prep_bias_kernel<<<1024, 256, 0, st>>>(bias, mask, t.bias16, t.mask16, (long)B * H * N * N, (long)B * N * N,
+  ta_prep_bias_kernel<<<1024, 256, 0, st>>>(bias, mask, t.bias32, t.mask16, (long)B * H * N * N, (long)B * N * N,
                                             N, n_valid);
   PF_CHECK_LAUNCH("ta_prep_bias_kernel");
   return launch_attn<true>(t, o, B, N, n_valid, st);
