@@ -208,6 +208,18 @@ int pf_apb_fwd(const pf_apb_args* args);
 int pf_apb_pair_bias(const pf_apb_args* args);
 int pf_apb_attend(const pf_apb_args* args);
 
+/* pf_apb_fwd for callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops that forbid hipMalloc).  No counterpart in the reference.  Same arguments and
+ * result as pf_apb_fwd, except that args->workspace / workspace_bytes are ignored: the scratch
+ * is a static device array of PF_APB_NOALLOC_SCRATCH_BYTES per GPU, which holds
+ * pf_apb_workspace_size(B, N, c_s, H) up to that size (e.g. B = 1, N = 512, c_s = 384,
+ * H = 16: 20.7 MiB); larger shapes are rejected with PF_E_INVALID.  Allocates nothing; the
+ * array lives until the process ends.  Every call on one GPU shares that GPU's scratch, so
+ * calls that overlap on one GPU (other streams or threads) race: serialize them.  The scratch
+ * needs no clearing (each call writes every byte it reads). */
+#define PF_APB_NOALLOC_SCRATCH_BYTES (24u << 20)
+int pf_apb_fwd_noalloc(const pf_apb_args* args);
+
 /* The pair transition (pf_transition_fwd, C = 128 only) with pf_apb_pair_bias of its
  * result fused into the same kernel: after writing out = [x_in +] Transition(x_in) for a
  * pair, the kernel also writes that pair's single-track bias log2(e)*proj_z(LN(out)) into

@@ -127,6 +127,7 @@ SIGNATURES = {
     "pf_apb_fwd": (c_int, [ctypes.POINTER(ApbArgs)]),
     "pf_apb_pair_bias": (c_int, [ctypes.POINTER(ApbArgs)]),
     "pf_apb_attend": (c_int, [ctypes.POINTER(ApbArgs)]),
+    "pf_apb_fwd_noalloc": (c_int, [ctypes.POINTER(ApbArgs)]),
     "pf_transition_pair_bias_fwd": (c_int, [ctypes.POINTER(TransitionArgs), ctypes.POINTER(ApbArgs)]),
     "pf_opm_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "pf_opm_fwd": (c_int, [ctypes.POINTER(OpmArgs)]),

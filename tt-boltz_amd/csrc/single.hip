@@ -13,6 +13,8 @@
 //                     o * sigmoid(g) is written for the output projection.
 //   q/k/v/g (one launch, four jobs) and the output projection use linear_rows_kernel
 //   (transition.hip).
+#include <mutex>
+
 #include "pf_common.h"
 #include "pf_internal.h"
 
@@ -277,3 +279,51 @@ extern "C" int pf_apb_fwd(const pf_apb_args* a) {
   if ((rc = pf_apb_pair_bias(a))) return rc;
   return pf_apb_attend(a);
 }
+
+// ---------------------------------------------------------------------------------
+// pf_apb_fwd without a caller workspace: the scratch (q, k, v, g, o*sigmoid(g) and the pair
+// bias, every byte written before it is read) is a file-scope device array.  In host code
+// `scratch` only names the symbol: its device address comes from hipGetSymbolAddress, once
+// per device with that device current, and only that address is passed to the kernels.
+// ---------------------------------------------------------------------------------
+constexpr size_t APB_SCRATCH_BYTES = PF_APB_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[APB_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[MAX_DEVICES] = {};   // device address of `scratch` per device
+
+int apb_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return pf_fail(PF_E_LAUNCH, "pf_apb_fwd_noalloc: no usable current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return pf_fail(PF_E_LAUNCH, "pf_apb_fwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                     hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return PF_OK;
+}
+}  // namespace
+
+extern "C" int pf_apb_fwd_noalloc(const pf_apb_args* a) {
+  if (!a) return pf_fail(PF_E_INVALID, "pf_apb_fwd_noalloc: null args");
+  const size_t need = pf_apb_workspace_size(a->B, a->N, a->c_s, a->H);
+  if (need == 0 || need > APB_SCRATCH_BYTES)
+    return pf_fail(PF_E_INVALID,
+                   "pf_apb_fwd_noalloc: B=%d N=%d c_s=%d H=%d needs %zu bytes of scratch, above the static %zu "
+                   "(call pf_apb_fwd with a workspace)", a->B, a->N, a->c_s, a->H, need, APB_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (const int rc = apb_scratch(&ws)) return rc;
+  pf_apb_args b = *a;
+  b.workspace = ws;
+  b.workspace_bytes = APB_SCRATCH_BYTES;
+  return pf_apb_fwd(&b);
+}
+
