@@ -116,8 +116,13 @@ def probe_traffic(N: int) -> int:
     for _ in range(3):
         torch.mul(src, 2.0, out=dst)     # vectorized elementwise kernel: reads and writes COPY_BYTES
     torch.cuda.synchronize()
+    # three full layers (serial schedule, single track included) for the per-kernel summary
+    s = synthetic.pair_inputs(N, 0)[0].to(dev).contiguous()
+    for _ in range(3):
+        layer(s, z, None, None, ws)
+    torch.cuda.synchronize()
     print(json.dumps({"probe": "traffic", "N": N, "attn_launches": 5, "contract_launches": 5, "copy_launches": 3,
-                      "copy_bytes": COPY_BYTES}), flush=True)
+                      "copy_bytes": COPY_BYTES, "layer_launches": 3}), flush=True)
     return 0
 
 

@@ -24,6 +24,7 @@
 // or the producer's rows are pre-permuted so the runs come out contiguous (perm16()).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 
 #ifdef PF_OPERAND_BF16
@@ -73,6 +74,10 @@ PF_DEV float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }   // v_exp
 PF_DEV float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
 
 // sigmoid(x) = 1 / (1 + 2^(-x log2 e)): saturates cleanly to 0 / 1 for large |x|.
+// compile-time index for unrolled, stage-selected lambdas
+template <int V>
+using ic = std::integral_constant<int, V>;
+
 PF_DEV float sigmoidf_fast(float x) { return rcp_fast(1.f + exp2_fast(-1.4426950408889634f * x)); }
 
 PF_DEV float siluf(float x) { return x * sigmoidf_fast(x); }

@@ -257,8 +257,6 @@ PF_DEV opx8 slots01(int h, uint32_t lo_hi) {
   const u32x4 v = {h ? 0u : lo_hi, 0u, 0u, 0u};
   return as_x8(v);
 }
-template <int V>
-using ic = std::integral_constant<int, V>;
 // LDS reads from absolute LDS byte addresses (the per-lane address registers already hold the
 // allocation base, so the loop's reads need no address arithmetic beyond the immediate offset)
 typedef __attribute__((address_space(3))) const char* lds_ptr;

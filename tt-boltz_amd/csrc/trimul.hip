@@ -22,6 +22,7 @@
 namespace {
 
 constexpr int C = 128;        // c_z
+constexpr float LOG2E = 1.4426950408889634f;
 constexpr int LDSW = 136;     // padded LDS row stride (elements) for [rows][128] tiles
 
 // A [32][128] op_t block moved by 256 threads: 512 chunks of 16 B, 2 per thread.
@@ -42,25 +43,31 @@ PF_DEV void blk32_store(op_t* lds, int tid, const Blk32& r) {
 }
 
 // ---------------------------------------------------------------------------------
-// Input projection.  Persistent: one workgroup (8 waves, two per SIMD, so one wave's
-// loads, LayerNorm and sigmoid work overlap the other's MFMAs) per CU keeps p_in and
-// g_in ([256][128] each) resident in LDS, and every wave walks tiles of 32 consecutive
-// positions of one operand-plane row (orow, ocol0 .. ocol0+31).  The projection is formed
-// as D[position][channel]; each 32x32 output block goes through a per-wave LDS stage
-// so that it leaves as 16-byte stores, four lanes per 64-byte plane-row segment.  The projection is formed as
-// D[position][channel], so a lane holds one channel for 16 positions and writes them
-// as 8-byte runs of 4 consecutive positions.
+// Input projection.  Persistent: one workgroup (8 waves, two per SIMD) per CU keeps p_in and
+// g_in ([2 CC][CC] each) resident in LDS with the LayerNorm affine folded in (W' = W diag(gamma)
+// as op_t; W beta in fp32, added in the epilogue; the gate rows are scaled by -log2(e), so
+// sigmoid(g) = 1 / (1 + 2^g')), so a tile only normalizes.  Every wave walks tiles of 32
+// consecutive positions of one operand-plane row (orow, ocol0 .. ocol0+31) and loads the next
+// tile's z rows while it computes the current one.  The projection is formed as
+// D[position][channel]; each 32x32 output block goes through a per-wave LDS stage so that it
+// leaves as 16-byte stores, four lanes per 64-byte plane-row segment (a full segment per
+// instruction writes faster than register-permuted 32-byte halves).  The channel-block loop is
+// unrolled, so the number of stores issued after the prefetch is static, with a scheduling
+// barrier per block to keep each block's LDS reads and MFMAs inside its own iteration.
 // ---------------------------------------------------------------------------------
 constexpr int TMP_WAVES = 8;
 constexpr int SPITCH = 40;     // output staging pitch (elements): one 32-position row + 16 B
-// CC = c_z (64 or 128): p_in / g_in are [2 CC][CC], LDS rows padded to CC + 8 elements
+template <int CC>
+constexpr int tmp_waves() { return TMP_WAVES; }
+// CC = c_z (64 or 128).  LDS: W_p', W_g' [2 CC][CC + 8] op_t, the per-wave output stages, the
+// per-wave maxima, then the fp32 offsets W_p beta [2 CC] and -log2(e) W_g beta [2 CC].
 template <int CC>
 constexpr size_t tmp_lds() {
   return (size_t)2 * 2 * CC * (CC + 8) * sizeof(op_t) + (size_t)TMP_WAVES * 32 * SPITCH * sizeof(op_t) +
-         TMP_WAVES * sizeof(float);
+         TMP_WAVES * sizeof(float) + 4 * CC * sizeof(float);
 }
 
-template <int CC>
+template <int CC, bool MASK>
 __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
     const float* __restrict__ z, const float* __restrict__ mask,
     const float* __restrict__ lnw, const float* __restrict__ lnb,
@@ -73,9 +80,9 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
   op_t* lg = wlds + 2 * CC * LW;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  op_t* stg = wlds + 2 * 2 * CC * LW + wid * 32 * SPITCH;   // this wave's output stage
+  op_t* stg = wlds + 2 * 2 * CC * LW + wid * 32 * SPITCH;
   float* wave_amax = reinterpret_cast<float*>(wlds + 2 * 2 * CC * LW + TMP_WAVES * 32 * SPITCH);
-  float amax = 0.f;   // max |a|, |b| this lane wrote (as stored, after rounding)
+  float* cbias = wave_amax + TMP_WAVES;   // [0, 2 CC): p, [2 CC, 4 CC): g
 #pragma unroll 4
   for (int c = tid; c < 2 * CC * (CC / 8); c += 64 * TMP_WAVES) {
     const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
@@ -83,7 +90,25 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
     st_x8(lg + row * LW + col, ld_x8(w_g + row * CC + col));
   }
   __syncthreads();
-
+  // weights -> LDS as they are (coalesced), then one thread per row folds the affine in place
+  for (int row = tid; row < 4 * CC; row += 64 * TMP_WAVES) {
+    op_t* w = row < 2 * CC ? lp + row * LW : lg + (row - 2 * CC) * LW;
+    const float f = row < 2 * CC ? 1.f : -LOG2E;
+    float acc = 0.f;
+#pragma unroll 4
+    for (int c = 0; c < CC; c += 8) {
+      opx8 v = ld_x8(w + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float wf = (float)v[e] * f;
+        acc += wf * lnb[c + e];
+        v[e] = (op_t)(wf * lnw[c + e]);
+      }
+      st_x8(w + c, v);
+    }
+    cbias[row] = acc;
+  }
+  __syncthreads();
   const uint32_t ntiles = (uint32_t)B * N * N / 32;
   const uint32_t stride = gridDim.x * TMP_WAVES;
   auto tile_pair = [&](uint32_t t, int& b, int& orow, int& ocol0) PF_INLINE -> long {
@@ -95,26 +120,39 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
     const int zj = incoming ? orow : ocol0 + m;
     return ((long)b * N + zi) * N + zj;
   };
-
-  for (uint32_t t = blockIdx.x * TMP_WAVES + wid; t < ntiles; t += stride) {
-    asm volatile("" ::: "memory");   // LayerNorm parameters are re-read each tile, not pinned in VGPRs
+  float amax = 0.f;   // max |a|, |b| before rounding (rounding is monotonic: round it once at the end)
+  float x[CC / 2];    // this tile's z rows, then the next tile's (in flight during the MFMAs)
+  float maskn = 1.f;
+  uint32_t t = blockIdx.x * TMP_WAVES + wid;
+  if (t < ntiles) {
+    int b_, r_, c_;
+    const long pair = tile_pair(t, b_, r_, c_);
+    load_row_frag<CC>(z + pair * CC, h, x);
+    if (MASK) maskn = mask[pair];
+  }
+  for (; t < ntiles; t += stride) {
     int cb_b, cb_orow, cb_ocol0;
-    const long pair = tile_pair(t, cb_b, cb_orow, cb_ocol0);
+    tile_pair(t, cb_b, cb_orow, cb_ocol0);
     opx8 xf[KS];
-    float maskv = 1.f;
-    {
-      float x[CC / 2];
-      load_row_frag<CC>(z + pair * CC, h, x);
-      if (mask) maskv = mask[pair];
-      ln_to_frag<CC>(x, h, lnw, lnb, eps, xf);
-    }
+    const float maskv = maskn;
+    ln_norm_to_frag<CC>(x, eps, xf);
     float mr[16];
+    if (MASK) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mr[r] = __shfl(maskv, acc_row(r, h));
-#pragma unroll 1
+      for (int r = 0; r < 16; ++r) mr[r] = __shfl(maskv, acc_row(r, h));
+    }
+    if (t + stride < ntiles) {
+      int b_, r_, c_;
+      const long pn = tile_pair(t + stride, b_, r_, c_);
+      load_row_frag<CC>(z + pn * CC, h, x);
+      if (MASK) maskn = mask[pn];
+    }
+#pragma unroll
     for (int cb = 0; cb < 2 * CC / 32; ++cb) {
+      __builtin_amdgcn_sched_barrier(0);
       const op_t* wp = lp + (32 * cb + m) * LW + 8 * h;
       const op_t* wg = lg + (32 * cb + m) * LW + 8 * h;
+      const float cp = cbias[32 * cb + m], cg = cbias[2 * CC + 32 * cb + m];
       f32x16 ap = zero16(), ag = zero16();
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
@@ -128,8 +166,10 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
-          v[e] = (op_t)(ap[r] * sigmoidf_fast(ag[r]) * mr[r]);
-          amax = fmaxf(amax, fabsf((float)v[e]));
+          float u = (ap[r] + cp) * rcp_fast(1.f + exp2_fast(ag[r] + cg));
+          if (MASK) u *= mr[r];
+          amax = fmaxf(amax, fabsf(u));
+          v[e] = (op_t)u;
         }
         st_x4(stg + m * SPITCH + 8 * g + 4 * h, v);
       }
@@ -141,8 +181,8 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
       }
     }
   }
-  // the workgroup's max |a|, |b| -> amax_parts[blockIdx.x] (the contraction's scale input)
-  amax = wave_max(amax);
+  // the workgroup's max |a|, |b| as stored -> amax_parts[blockIdx.x] (the contraction's scale input)
+  amax = fabsf((float)(op_t)wave_max(amax));
   if (lane == 0) wave_amax[wid] = amax;
   __syncthreads();
   if (tid == 0) {
@@ -532,8 +572,9 @@ int trimul_run(const pf_trimul_args* a) {
   const int grid_proj = (int)min((long)min(cus, TM_MAX_PARTS), (positions / 32 + TMP_WAVES - 1) / TMP_WAVES);
   const int grid_out = (int)min((long)cus, (positions / 32 + TMO_WAVES - 1) / TMO_WAVES);
   {
-    if (const int rc = pf_reserve_lds((const void*)tm_proj_kernel<CC>, tmp_lds<CC>(), "tm_proj_kernel")) return rc;
-    tm_proj_kernel<CC><<<grid_proj, 64 * TMP_WAVES, tmp_lds<CC>(), st>>>(
+    auto kern = a->pair_mask ? tm_proj_kernel<CC, true> : tm_proj_kernel<CC, false>;
+    if (const int rc = pf_reserve_lds((const void*)kern, tmp_lds<CC>(), "tm_proj_kernel")) return rc;
+    kern<<<grid_proj, 64 * tmp_waves<CC>(), tmp_lds<CC>(), st>>>(
         a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b, (const op_t*)a->p_in_w, (const op_t*)a->g_in_w, opA, opB,
         amax_parts, B, N, a->direction, a->eps);
     PF_CHECK_LAUNCH("tm_proj_kernel");
