@@ -428,17 +428,23 @@ __global__ __launch_bounds__(64 * TMD_WAVES, 1) void tm_contract_dma_kernel(
 
 // ---------------------------------------------------------------------------------
 // Output: z[i,j,:] (+)= p_out(LN_out(X[:,i,j])) * sigmoid(g_out(LN_in(z[i,j,:]))).
-// Persistent: one workgroup (8 waves) per CU keeps p_out / g_out in LDS; each wave walks
-// tiles of 32 consecutive pairs.  The tile's X slice (128 channels x 32 pairs, 64-byte
-// rows of the planes) comes in with 16-byte loads into a per-wave LDS stage and is read
-// back per channel.  Both products are formed as D[channel][pair] in the output-aligned
-// layout, so the residual z values the wave loaded for LN_in are the ones it adds to (no
-// second read of z).
+// Persistent: one workgroup (8 waves) per CU keeps p_out / g_out in LDS with both LayerNorm
+// affines folded in (W_p' = W_p diag(gamma_out); W_g' = -log2(e) W_g diag(gamma_in), so
+// sigmoid(g) = 1 / (1 + 2^g'); the fp32 offsets W_p beta_out and -log2(e) W_g beta_in are each
+// accumulator's start value), so a tile only normalizes; each wave walks tiles of 32
+// consecutive pairs.  The tile's X slice (CC channels x 32 pairs, 64-byte rows of the planes)
+// comes in with 16-byte loads into a per-wave LDS stage and is read back per channel.  Both
+// products are formed as D[channel][pair] in the output-aligned layout, so the residual z
+// values the wave loaded for LN_in are the ones it adds to (no second read of z).  Weight rows
+// are CC + 4 op_t apart, so the 8-byte fragment reads of 32 rows fall on distinct banks.
 // ---------------------------------------------------------------------------------
 constexpr int TMO_WAVES = 8, XSP = 40;   // per-wave X stage: [CC channels][32 pairs + 8]
+// LDS: the offsets [2 CC] fp32 (first, so that their reads use small immediate offsets), then
+// W_p', W_g' [CC][CC + 4] op_t, then the per-wave X stages
 template <int CC>
 constexpr size_t tmo_lds() {
-  return (size_t)2 * CC * (CC + 8) * sizeof(op_t) + (size_t)TMO_WAVES * CC * XSP * sizeof(op_t);
+  return (size_t)2 * CC * (CC + 4) * sizeof(op_t) + (size_t)TMO_WAVES * CC * XSP * sizeof(op_t) +
+         2 * CC * sizeof(float);
 }
 
 // resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
@@ -452,24 +458,51 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
     const float* __restrict__ lno_w, const float* __restrict__ lno_b,
     const op_t* __restrict__ w_pout, const op_t* __restrict__ w_gout,
     int B, int N, int resid, float eps) {
-  constexpr int LW = CC + 8, KS = CC / 16;
+  constexpr int LW = CC + 4, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t olds[];
-  op_t* sWp = olds;
-  op_t* sWg = olds + CC * LW;
+  float* cbias = reinterpret_cast<float*>(olds);   // [0, CC): p, [CC, 2 CC): g
+  op_t* sWp = olds + 2 * CC * 2;
+  op_t* sWg = sWp + CC * LW;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  XT* xs = reinterpret_cast<XT*>(olds + 2 * CC * LW) + wid * CC * XSP;   // this wave's X stage
+  XT* xs = reinterpret_cast<XT*>(sWg + CC * LW) + wid * CC * XSP;   // this wave's X stage
+  // weights -> LDS as they are (rows are 8-byte aligned: two 8-byte stores per 16-byte load),
+  // then one thread per row folds the affine in place
   for (int c = tid; c < CC * (CC / 8); c += 64 * TMO_WAVES) {
     const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
-    st_x8(&sWp[row * LW + col], ld_x8(w_pout + row * CC + col));
-    st_x8(&sWg[row * LW + col], ld_x8(w_gout + row * CC + col));
+    const opx8 vp = ld_x8(w_pout + row * CC + col), vg = ld_x8(w_gout + row * CC + col);
+    *reinterpret_cast<opx4*>(&sWp[row * LW + col]) = opx4{vp[0], vp[1], vp[2], vp[3]};
+    *reinterpret_cast<opx4*>(&sWp[row * LW + col + 4]) = opx4{vp[4], vp[5], vp[6], vp[7]};
+    *reinterpret_cast<opx4*>(&sWg[row * LW + col]) = opx4{vg[0], vg[1], vg[2], vg[3]};
+    *reinterpret_cast<opx4*>(&sWg[row * LW + col + 4]) = opx4{vg[4], vg[5], vg[6], vg[7]};
+  }
+  __syncthreads();
+  for (int row = tid; row < 2 * CC; row += 64 * TMO_WAVES) {
+    const bool g = row >= CC;
+    op_t* w = g ? sWg + (row - CC) * LW : sWp + row * LW;
+    const float* gam = g ? lni_w : lno_w;
+    const float* bet = g ? lni_b : lno_b;
+    const float f = g ? -LOG2E : 1.f;
+    float acc = 0.f;
+#pragma unroll 4
+    for (int c = 0; c < CC; c += 4) {
+      opx4 v = ld_x4(w + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float wf = (float)v[e] * f;
+        acc += wf * bet[c + e];
+        v[e] = (op_t)(wf * gam[c + e]);
+      }
+      *reinterpret_cast<opx4*>(w + c) = v;
+    }
+    cbias[row] = acc;
   }
   __syncthreads();
   if (nparts > 0) x_scale = 1.f / x_store_scale(planes_amax(amax_parts, nparts), N);   // a power of two
   const long NN = (long)N * N;
   const uint32_t ntiles = (uint32_t)B * N * N / 32;
   for (uint32_t t = blockIdx.x * TMO_WAVES + wid; t < ntiles; t += gridDim.x * TMO_WAVES) {
-    asm volatile("" ::: "memory");   // LayerNorm parameters are re-read, not pinned in VGPRs
+    asm volatile("" ::: "memory");   // the offsets are re-read from LDS each tile, not pinned in VGPRs
     const long p0 = 32l * t;                       // first pair (global index b*NN + i*N + j)
     const int b = pos_tile(t, N).b;
     {
@@ -490,10 +523,10 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
       for (int q = 0; q < CC / 8; ++q)
 #pragma unroll
         for (int e = 0; e < 4; ++e) xv[4 * q + e] = (float)xs[(oa_channel(q, h) + e) * XSP + m] * x_scale;
-      ln_oa_to_frag<CC>(xv, h, lno_w, lno_b, eps, xo);
+      ln_oa_norm_to_frag<CC>(xv, eps, xo);
     }
     load_row_oa<CC>(z_in + pair * CC, h, zr);
-    ln_oa_to_frag<CC>(zr, h, lni_w, lni_b, eps, xi);
+    ln_oa_norm_to_frag<CC>(zr, eps, xi);
 #pragma unroll   // fully unrolled: zr[] must be indexed with constants to stay in VGPRs
     for (int ob = 0; ob < CC / 32; ++ob) {
       const op_t* wp = &sWp[(32 * ob + m) * LW];
@@ -509,11 +542,14 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
       for (int g = 0; g < 4; ++g) {
         const int q = 4 * ob + g;
         float* dst = orow + oa_channel(q, h);
+        asm volatile("" ::: "memory");   // read each group's offsets where they are used
+        const f32x4 cp = *reinterpret_cast<const f32x4*>(cbias + oa_channel(q, h));
+        const f32x4 cg = *reinterpret_cast<const f32x4*>(cbias + CC + oa_channel(q, h));
         f32x4 v;
         if (resid == 2) v = *reinterpret_cast<const f32x4*>(dst);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float u = P[4 * g + e] * sigmoidf_fast(G[4 * g + e]);
+          const float u = (P[4 * g + e] + cp[e]) * rcp_fast(1.f + exp2_fast(G[4 * g + e] + cg[e]));
           v[e] = resid == 1 ? zr[4 * q + e] + u : resid == 2 ? v[e] + u : u;
         }
         *reinterpret_cast<f32x4*>(dst) = v;
