@@ -96,11 +96,16 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
     }
     st_x8(plds + row * LW + col, v);
   }
-  for (int row = tid; row < TAP_ROWS; row += 64 * TAP_WAVES) {
+  for (int row = tid; row < TAP_ROWS; row += 64 * TAP_WAVES) {   // accumulator starts W beta
     float acc = 0.f;
     if (row < 3 * C + H) {
       const op_t* w = wrow(row);
-      for (int c = 0; c < CC; ++c) acc += (float)w[c] * lnb[c];
+#pragma unroll 4
+      for (int c = 0; c < CC; c += 8) {
+        const opx8 w8 = ld_x8(w + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[c + e];
+      }
     }
     cb[row] = acc;
   }
@@ -614,16 +619,20 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
 
 // ---------------------------------------------------------------------------------
 // Output projection: z[pair(i, j)] (+)= linear_o(O[i, j] * sigmoid(linear_g(LN(z[pair])))).
-// Persistent: one workgroup (8 waves) per CU keeps W_g and W_o in LDS; each wave walks
-// tiles of 32 frame positions (ip, j0 .. j0+31).  Everything is in the output-aligned
-// layout (pf_common.h): the gate comes out of D[channel][position] = W_g . LN(z) in the
-// same channel order as the O values the lane loads, o * sigmoid(g) is directly the B
-// operand of D[out][position] = W_o . (o * g), and the residual is the z the lane loaded.
+// Persistent: one workgroup (8 waves) per CU keeps W_g and W_o in LDS, W_g with the LayerNorm
+// affine folded in (W_g' = -log2(e) W_g diag(gamma), so sigmoid(g) = 1 / (1 + 2^g'); the offsets
+// -log2(e) W_g beta in fp32 are added to the gate); each wave walks tiles of 32 frame positions
+// (ip, j0 .. j0+31).  Everything is in the output-aligned layout (pf_common.h): the gate comes
+// out of D[channel][position] = W_g' . LN(z) in the same channel order as the O values the lane
+// loads, o * sigmoid(g) is directly the B operand of D[out][position] = W_o . (o * g), and the
+// residual is the z the lane loaded.  Weight rows are 4 op_t longer than their width, so the
+// 8-byte fragment reads of 32 rows fall on distinct banks.
 // ---------------------------------------------------------------------------------
 constexpr int TAO_WAVES = 8;
-// W_g [C][CC] (rows padded to CC + 8), W_o [CC][C] (rows padded to C + 8 = LDSW)
+// LDS: the gate offsets [C] fp32 first (small immediate offsets), then W_g' [C][CC + 4] and
+// W_o [CC][C + 4] op_t
 template <int CC>
-constexpr size_t tao_lds() { return ((size_t)C * (CC + 8) + (size_t)CC * LDSW) * sizeof(op_t); }
+constexpr size_t tao_lds() { return C * sizeof(float) + ((size_t)C * (CC + 4) + (size_t)CC * (C + 4)) * sizeof(op_t); }
 
 // resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
 template <int CC>
@@ -631,35 +640,72 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
     const op_t* __restrict__ O, const float* z_in, float* out, const float* __restrict__ lnw,
     const float* __restrict__ lnb, const op_t* __restrict__ wg, const op_t* __restrict__ wo,
     int B, int N, int ending, int resid, float eps) {
-  constexpr int LWG = CC + 8, KS = CC / 16;
+  constexpr int LWG = CC + 4, LWO = C + 4, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t tlds[];
-  op_t* sWg = tlds;
-  op_t* sWo = tlds + C * LWG;
+  float* cgate = reinterpret_cast<float*>(tlds);
+  op_t* sWg = tlds + 2 * C;
+  op_t* sWo = sWg + C * LWG;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // weights -> LDS (rows are 8-byte aligned: two 8-byte stores per 16-byte load)
   for (int c = tid; c < C * (CC / 8); c += 64 * TAO_WAVES) {
     const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
-    st_x8(&sWg[row * LWG + col], ld_x8(wg + row * CC + col));
+    const opx8 v = ld_x8(wg + row * CC + col);
+    *reinterpret_cast<opx4*>(&sWg[row * LWG + col]) = opx4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<opx4*>(&sWg[row * LWG + col + 4]) = opx4{v[4], v[5], v[6], v[7]};
   }
-  for (int c = tid; c < CC * 16; c += 64 * TAO_WAVES) {
-    const int row = c >> 4, col = (c & 15) * 8;
-    st_x8(&sWo[row * LDSW + col], ld_x8(wo + row * C + col));
+  for (int c = tid; c < CC * (C / 8); c += 64 * TAO_WAVES) {
+    const int row = c / (C / 8), col = (c % (C / 8)) * 8;
+    const opx8 v = ld_x8(wo + row * C + col);
+    *reinterpret_cast<opx4*>(&sWo[row * LWO + col]) = opx4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<opx4*>(&sWo[row * LWO + col + 4]) = opx4{v[4], v[5], v[6], v[7]};
+  }
+  __syncthreads();
+  for (int row = tid; row < C; row += 64 * TAO_WAVES) {   // fold the affine into W_g, in place
+    op_t* w = sWg + row * LWG;
+    float acc = 0.f;
+#pragma unroll 4
+    for (int c = 0; c < CC; c += 4) {
+      opx4 v = ld_x4(w + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float wf = -LOG2E * (float)v[e];
+        acc += wf * lnb[c + e];
+        v[e] = (op_t)(wf * lnw[c + e]);
+      }
+      *reinterpret_cast<opx4*>(w + c) = v;
+    }
+    cgate[row] = acc;
   }
   __syncthreads();
   const uint32_t ntiles = (uint32_t)B * N * N / 32;
-  for (uint32_t t = blockIdx.x * TAO_WAVES + wid; t < ntiles; t += gridDim.x * TAO_WAVES) {
-    asm volatile("" ::: "memory");   // LayerNorm parameters are re-read, not pinned in VGPRs
-    const long pos0 = 32l * t;
+  const uint32_t stride = gridDim.x * TAO_WAVES;
+  // this tile's O values (channels oa_channel(q, h) + 0..3 of position pos0 + m), then the next
+  // tile's, in flight while this tile is computed
+  opx4 on[CC / 8];
+  uint32_t t = blockIdx.x * TAO_WAVES + wid;
+  if (t < ntiles) {
+#pragma unroll
+    for (int q = 0; q < CC / 8; ++q) on[q] = ld_x4(O + (32l * t + m) * C + oa_channel(q, h));
+  }
+  for (; t < ntiles; t += stride) {
+    asm volatile("" ::: "memory");   // the gate offsets are re-read from LDS each tile, not pinned in VGPRs
     const PosTile pt = pos_tile(t, N);
     const int b = pt.b, ip = pt.r, j = pt.c0 + m;
     const long zp = ending ? ((long)b * N + j) * N + ip : ((long)b * N + ip) * N + j;
     float zr[CC / 2];
     opx8 xf[KS];
     load_row_oa<CC>(z_in + zp * CC, h, zr);
-    ln_oa_to_frag<CC>(zr, h, lnw, lnb, eps, xf);
+    ln_oa_norm_to_frag<CC>(zr, eps, xf);
     // o * sigmoid(g) as the B operand of the output projection (k order = output-aligned)
+    opx4 ov4[CC / 8];
+#pragma unroll
+    for (int q = 0; q < CC / 8; ++q) ov4[q] = on[q];
+    if (t + stride < ntiles) {
+#pragma unroll
+      for (int q = 0; q < CC / 8; ++q) on[q] = ld_x4(O + (32l * (t + stride) + m) * C + oa_channel(q, h));
+    }
     opx8 og[8];
-    const op_t* orow = O + (pos0 + m) * C;
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
       const op_t* wrow = &sWg[(32 * cb + m) * LWG];
@@ -669,15 +715,16 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
 #pragma unroll
       for (int gg = 0; gg < 4; ++gg) {
         const int q = 4 * cb + gg;            // chunk: channels oa_channel(q, h) + 0..3
-        const opx4 ov = ld_x4(orow + oa_channel(q, h));
+        const opx4 ov = ov4[q];
+        const f32x4 cg = *reinterpret_cast<const f32x4*>(cgate + oa_channel(q, h));
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          og[q >> 1][4 * (q & 1) + e] = (op_t)((float)ov[e] * sigmoidf_fast(g[4 * gg + e]));
+          og[q >> 1][4 * (q & 1) + e] = (op_t)((float)ov[e] * rcp_fast(1.f + exp2_fast(g[4 * gg + e] + cg[e])));
       }
     }
 #pragma unroll
     for (int ob = 0; ob < CC / 32; ++ob) {
-      const op_t* wrow = &sWo[(32 * ob + m) * LDSW];
+      const op_t* wrow = &sWo[(32 * ob + m) * LWO];
       f32x16 acc = zero16();
 #pragma unroll
       for (int s = 0; s < 8; ++s) acc = mfma32(wfrag_oa(wrow, s, h), og[s], acc);   // D[out][position]
