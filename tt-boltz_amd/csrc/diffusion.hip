@@ -28,7 +28,7 @@ namespace {
 constexpr int C = 128;       // c_z
 constexpr int DF_WAVES = 8;
 constexpr int TB_MAX_OUT = 512;
-constexpr int TB_WAVES = 16;   // token bias: 100 VGPRs, so 16 waves fit one CU (more stores in flight)
+constexpr int TB_WAVES = 12;   // token bias: three waves per SIMD (<= 168 VGPRs: no scratch spills)
 
 PF_DEV int slot16(int R, int c) { return R * C + 8 * (c ^ (R & 15)); }
 

@@ -131,6 +131,32 @@ PF_DEV void load_row_frag(const float* __restrict__ p, int h, float (&x)[CC / 2]
 }
 PF_DEV void load_row128_frag(const float* __restrict__ p, int h, float (&x)[64]) { load_row_frag<128>(p, h, x); }
 
+// (x - mean) * rstd * gamma[c] of a CC-vector (load_row_frag order: x[8 s + t] is channel
+// 16 s + 8 h + t) as CC/16 MFMA fragments: the LayerNorm without beta, for callers that add
+// W beta to the product in fp32 (gamma stays on the activation side, so the op_t weights are
+// rounded once).  gamma may live in LDS.
+template <int CC>
+PF_DEV void ln_gamma_to_frag(const float (&x)[CC / 2], int h, const float* gamma, float eps, opx8 (&f)[CC / 16]) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < CC / 2; ++i) s += x[i];
+  const float mean = xor32_sum(s) * (1.f / CC);
+  float v = 0.f;
+#pragma unroll
+  for (int i = 0; i < CC / 2; ++i) { const float d = x[i] - mean; v += d * d; }
+  const float rstd = rsqrtf(xor32_sum(v) * (1.f / CC) + eps);
+#pragma unroll
+  for (int s8 = 0; s8 < CC / 16; ++s8) {
+    const f32x4 g0 = *reinterpret_cast<const f32x4*>(gamma + 16 * s8 + 8 * h);
+    const f32x4 g1 = *reinterpret_cast<const f32x4*>(gamma + 16 * s8 + 8 * h + 4);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f[s8][t] = (op_t)((x[8 * s8 + t] - mean) * (rstd * g0[t]));
+      f[s8][4 + t] = (op_t)((x[8 * s8 + 4 + t] - mean) * (rstd * g1[t]));
+    }
+  }
+}
+
 // (x - mean) * rstd of a CC-vector (load_row_frag order) as CC/16 MFMA fragments: the
 // LayerNorm without its affine part, for callers that fold gamma / beta into the weights.
 template <int CC>
@@ -409,6 +435,28 @@ PF_DEV void ln_oa_to_frag(const float (&x)[CC / 2], int h, const float* __restri
 PF_DEV void ln128_oa_to_frag(const float (&x)[64], int h, const float* __restrict__ w, const float* __restrict__ b,
                              float eps, opx8 (&f)[8]) {
   ln_oa_to_frag<128>(x, h, w, b, eps, f);
+}
+
+// (x - mean) * rstd * gamma[c] of a CC-channel row held in output-aligned order (x[4 q + e] is
+// channel oa_channel(q, h) + e), as CC/16 MFMA B fragments: the LayerNorm without beta, for
+// callers that add W beta in fp32 (the op_t weights stay rounded once).  gamma may live in LDS.
+template <int CC>
+PF_DEV void ln_oa_gamma_to_frag(const float (&x)[CC / 2], int h, const float* gamma, float eps,
+                                opx8 (&f)[CC / 16]) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < CC / 2; ++i) s += x[i];
+  const float mean = xor32_sum(s) * (1.f / CC);
+  float v = 0.f;
+#pragma unroll
+  for (int i = 0; i < CC / 2; ++i) { const float d = x[i] - mean; v += d * d; }
+  const float rstd = rsqrtf(xor32_sum(v) * (1.f / CC) + eps);
+#pragma unroll
+  for (int q = 0; q < CC / 8; ++q) {
+    const f32x4 g = *reinterpret_cast<const f32x4*>(gamma + oa_channel(q, h));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[q >> 1][4 * (q & 1) + e] = (op_t)((x[4 * q + e] - mean) * (rstd * g[e]));
+  }
 }
 
 // (x - mean) * rstd of a CC-channel row held in output-aligned order, as CC/16 MFMA B fragments:

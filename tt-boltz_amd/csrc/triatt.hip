@@ -619,20 +619,22 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
 
 // ---------------------------------------------------------------------------------
 // Output projection: z[pair(i, j)] (+)= linear_o(O[i, j] * sigmoid(linear_g(LN(z[pair])))).
-// Persistent: one workgroup (8 waves) per CU keeps W_g and W_o in LDS, W_g with the LayerNorm
-// affine folded in (W_g' = -log2(e) W_g diag(gamma), so sigmoid(g) = 1 / (1 + 2^g'); the offsets
-// -log2(e) W_g beta in fp32 are added to the gate); each wave walks tiles of 32 frame positions
+// Persistent: one workgroup (8 waves) per CU keeps W_g and W_o in LDS (op_t as given, so rounded
+// once) with the LayerNorm's beta folded into fp32 gate offsets -log2(e) W_g beta (gamma scales
+// the normalized z before its rounding to op_t); each wave walks tiles of 32 frame positions
 // (ip, j0 .. j0+31).  Everything is in the output-aligned layout (pf_common.h): the gate comes
-// out of D[channel][position] = W_g' . LN(z) in the same channel order as the O values the lane
+// out of D[channel][position] = W_g . LN(z) in the same channel order as the O values the lane
 // loads, o * sigmoid(g) is directly the B operand of D[out][position] = W_o . (o * g), and the
 // residual is the z the lane loaded.  Weight rows are 4 op_t longer than their width, so the
 // 8-byte fragment reads of 32 rows fall on distinct banks.
 // ---------------------------------------------------------------------------------
 constexpr int TAO_WAVES = 8;
-// LDS: the gate offsets [C] fp32 first (small immediate offsets), then W_g' [C][CC + 4] and
-// W_o [CC][C + 4] op_t
+// LDS: the gate offsets [C] and gamma [CC] (fp32, first: small immediate offsets), then
+// W_g [C][CC + 4] and W_o [CC][C + 4] op_t
 template <int CC>
-constexpr size_t tao_lds() { return C * sizeof(float) + ((size_t)C * (CC + 4) + (size_t)CC * (C + 4)) * sizeof(op_t); }
+constexpr size_t tao_lds() {
+  return (C + CC) * sizeof(float) + ((size_t)C * (CC + 4) + (size_t)CC * (C + 4)) * sizeof(op_t);
+}
 
 // resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
 template <int CC>
@@ -643,7 +645,8 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
   constexpr int LWG = CC + 4, LWO = C + 4, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t tlds[];
   float* cgate = reinterpret_cast<float*>(tlds);
-  op_t* sWg = tlds + 2 * C;
+  float* gam = cgate + C;
+  op_t* sWg = tlds + 2 * (C + CC);
   op_t* sWo = sWg + C * LWG;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -661,50 +664,35 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
     *reinterpret_cast<opx4*>(&sWo[row * LWO + col + 4]) = opx4{v[4], v[5], v[6], v[7]};
   }
   __syncthreads();
-  for (int row = tid; row < C; row += 64 * TAO_WAVES) {   // fold the affine into W_g, in place
-    op_t* w = sWg + row * LWG;
+  for (int c = tid; c < CC; c += 64 * TAO_WAVES) gam[c] = lnw[c];
+  for (int row = tid; row < C; row += 64 * TAO_WAVES) {   // gate offsets -log2(e) W_g beta
+    const op_t* w = wg + row * CC;
     float acc = 0.f;
 #pragma unroll 4
-    for (int c = 0; c < CC; c += 4) {
-      opx4 v = ld_x4(w + c);
+    for (int c = 0; c < CC; c += 8) {
+      const opx8 w8 = ld_x8(w + c);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float wf = -LOG2E * (float)v[e];
-        acc += wf * lnb[c + e];
-        v[e] = (op_t)(wf * lnw[c + e]);
-      }
-      *reinterpret_cast<opx4*>(w + c) = v;
+      for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[c + e];
     }
-    cgate[row] = acc;
+    cgate[row] = -LOG2E * acc;
   }
   __syncthreads();
   const uint32_t ntiles = (uint32_t)B * N * N / 32;
   const uint32_t stride = gridDim.x * TAO_WAVES;
-  // this tile's O values (channels oa_channel(q, h) + 0..3 of position pos0 + m), then the next
-  // tile's, in flight while this tile is computed
-  opx4 on[CC / 8];
   uint32_t t = blockIdx.x * TAO_WAVES + wid;
-  if (t < ntiles) {
-#pragma unroll
-    for (int q = 0; q < CC / 8; ++q) on[q] = ld_x4(O + (32l * t + m) * C + oa_channel(q, h));
-  }
   for (; t < ntiles; t += stride) {
     asm volatile("" ::: "memory");   // the gate offsets are re-read from LDS each tile, not pinned in VGPRs
     const PosTile pt = pos_tile(t, N);
     const int b = pt.b, ip = pt.r, j = pt.c0 + m;
     const long zp = ending ? ((long)b * N + j) * N + ip : ((long)b * N + ip) * N + j;
-    float zr[CC / 2];
     opx8 xf[KS];
+    float zr[CC / 2];
     load_row_oa<CC>(z_in + zp * CC, h, zr);
-    ln_oa_norm_to_frag<CC>(zr, eps, xf);
+    ln_oa_gamma_to_frag<CC>(zr, h, gam, eps, xf);
     // o * sigmoid(g) as the B operand of the output projection (k order = output-aligned)
-    opx4 ov4[CC / 8];
+    opx4 ov4[C / 8];   // O values (C = H * D channels): oa_channel(q, h) + 0..3 of position 32 t + m
 #pragma unroll
-    for (int q = 0; q < CC / 8; ++q) ov4[q] = on[q];
-    if (t + stride < ntiles) {
-#pragma unroll
-      for (int q = 0; q < CC / 8; ++q) on[q] = ld_x4(O + (32l * (t + stride) + m) * C + oa_channel(q, h));
-    }
+    for (int q = 0; q < C / 8; ++q) ov4[q] = ld_x4(O + (32l * t + m) * C + oa_channel(q, h));
     opx8 og[8];
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
@@ -719,7 +707,8 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
         const f32x4 cg = *reinterpret_cast<const f32x4*>(cgate + oa_channel(q, h));
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          og[q >> 1][4 * (q & 1) + e] = (op_t)((float)ov[e] * rcp_fast(1.f + exp2_fast(g[4 * gg + e] + cg[e])));
+          og[q >> 1][4 * (q & 1) + e] =
+              (op_t)((float)ov[e] * rcp_fast(1.f + exp2_fast(fmaf(g[4 * gg + e], -LOG2E, cg[e]))));
       }
     }
 #pragma unroll
@@ -733,12 +722,10 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
         const int q = 4 * ob + gg;
         float* dst = out + zp * CC + oa_channel(q, h);
         f32x4 v;
+        if (resid == 1) v = f32x4{zr[4 * q], zr[4 * q + 1], zr[4 * q + 2], zr[4 * q + 3]};
         if (resid == 2) v = *reinterpret_cast<const f32x4*>(dst);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float u = acc[4 * gg + e];
-          v[e] = resid == 1 ? zr[4 * q + e] + u : resid == 2 ? v[e] + u : u;
-        }
+        for (int e = 0; e < 4; ++e) v[e] = resid == 0 ? acc[4 * gg + e] : v[e] + acc[4 * gg + e];
         *reinterpret_cast<f32x4*>(dst) = v;
       }
     }

@@ -44,9 +44,9 @@ PF_DEV void blk32_store(op_t* lds, int tid, const Blk32& r) {
 
 // ---------------------------------------------------------------------------------
 // Input projection.  Persistent: one workgroup (8 waves, two per SIMD) per CU keeps p_in and
-// g_in ([2 CC][CC] each) resident in LDS with the LayerNorm affine folded in (W' = W diag(gamma)
-// as op_t; W beta in fp32, added in the epilogue; the gate rows are scaled by -log2(e), so
-// sigmoid(g) = 1 / (1 + 2^g')), so a tile only normalizes.  Every wave walks tiles of 32
+// g_in ([2 CC][CC] each, op_t as given, so rounded once) resident in LDS, with the LayerNorm's
+// beta folded into fp32 offsets W beta added in the epilogue (gamma scales the normalized z
+// before its rounding to op_t).  Every wave walks tiles of 32
 // consecutive positions of one operand-plane row (orow, ocol0 .. ocol0+31) and loads the next
 // tile's z rows while it computes the current one.  The projection is formed as
 // D[position][channel]; each 32x32 output block goes through a per-wave LDS stage so that it
@@ -59,12 +59,13 @@ constexpr int TMP_WAVES = 8;
 constexpr int SPITCH = 40;     // output staging pitch (elements): one 32-position row + 16 B
 template <int CC>
 constexpr int tmp_waves() { return TMP_WAVES; }
-// CC = c_z (64 or 128).  LDS: W_p', W_g' [2 CC][CC + 8] op_t, the per-wave output stages, the
-// per-wave maxima, then the fp32 offsets W_p beta [2 CC] and -log2(e) W_g beta [2 CC].
+// CC = c_z (64 or 128).  LDS: gamma [CC] and the offsets W_p beta [2 CC], -log2(e) W_g beta
+// [2 CC] (fp32, first: small immediate offsets), then W_p, W_g [2 CC][CC + 8] op_t, the per-wave
+// output stages and the per-wave maxima.
 template <int CC>
 constexpr size_t tmp_lds() {
-  return (size_t)2 * 2 * CC * (CC + 8) * sizeof(op_t) + (size_t)TMP_WAVES * 32 * SPITCH * sizeof(op_t) +
-         TMP_WAVES * sizeof(float) + 4 * CC * sizeof(float);
+  return 5 * CC * sizeof(float) + (size_t)2 * 2 * CC * (CC + 8) * sizeof(op_t) +
+         (size_t)TMP_WAVES * 32 * SPITCH * sizeof(op_t) + TMP_WAVES * sizeof(float);
 }
 
 template <int CC, bool MASK>
@@ -76,37 +77,31 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
     float eps) {
   constexpr int LW = CC + 8, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t wlds[];
-  op_t* lp = wlds;
-  op_t* lg = wlds + 2 * CC * LW;
+  float* gam = reinterpret_cast<float*>(wlds);
+  float* cbias = gam + CC;   // [0, 2 CC): W_p beta, [2 CC, 4 CC): -log2(e) W_g beta
+  op_t* lp = wlds + 5 * CC * 2;
+  op_t* lg = lp + 2 * CC * LW;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  op_t* stg = wlds + 2 * 2 * CC * LW + wid * 32 * SPITCH;
-  float* wave_amax = reinterpret_cast<float*>(wlds + 2 * 2 * CC * LW + TMP_WAVES * 32 * SPITCH);
-  float* cbias = wave_amax + TMP_WAVES;   // [0, 2 CC): p, [2 CC, 4 CC): g
+  op_t* stg = lg + 2 * CC * LW + wid * 32 * SPITCH;
+  float* wave_amax = reinterpret_cast<float*>(lg + 2 * CC * LW + TMP_WAVES * 32 * SPITCH);
 #pragma unroll 4
   for (int c = tid; c < 2 * CC * (CC / 8); c += 64 * TMP_WAVES) {
     const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
     st_x8(lp + row * LW + col, ld_x8(w_p + row * CC + col));
     st_x8(lg + row * LW + col, ld_x8(w_g + row * CC + col));
   }
-  __syncthreads();
-  // weights -> LDS as they are (coalesced), then one thread per row folds the affine in place
-  for (int row = tid; row < 4 * CC; row += 64 * TMP_WAVES) {
-    op_t* w = row < 2 * CC ? lp + row * LW : lg + (row - 2 * CC) * LW;
-    const float f = row < 2 * CC ? 1.f : -LOG2E;
+  for (int c = tid; c < CC; c += 64 * TMP_WAVES) gam[c] = lnw[c];
+  for (int row = tid; row < 4 * CC; row += 64 * TMP_WAVES) {   // offsets W beta (one row per thread)
+    const op_t* w = row < 2 * CC ? w_p + row * CC : w_g + (row - 2 * CC) * CC;
     float acc = 0.f;
 #pragma unroll 4
     for (int c = 0; c < CC; c += 8) {
-      opx8 v = ld_x8(w + c);
+      const opx8 w8 = ld_x8(w + c);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float wf = (float)v[e] * f;
-        acc += wf * lnb[c + e];
-        v[e] = (op_t)(wf * lnw[c + e]);
-      }
-      st_x8(w + c, v);
+      for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[c + e];
     }
-    cbias[row] = acc;
+    cbias[row] = row < 2 * CC ? acc : -LOG2E * acc;
   }
   __syncthreads();
   const uint32_t ntiles = (uint32_t)B * N * N / 32;
@@ -135,7 +130,7 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
     tile_pair(t, cb_b, cb_orow, cb_ocol0);
     opx8 xf[KS];
     const float maskv = maskn;
-    ln_norm_to_frag<CC>(x, eps, xf);
+    ln_gamma_to_frag<CC>(x, h, gam, eps, xf);
     float mr[16];
     if (MASK) {
 #pragma unroll
@@ -166,7 +161,7 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
-          float u = (ap[r] + cp) * rcp_fast(1.f + exp2_fast(ag[r] + cg));
+          float u = (ap[r] + cp) * rcp_fast(1.f + exp2_fast(fmaf(ag[r], -LOG2E, cg)));
           if (MASK) u *= mr[r];
           amax = fmaxf(amax, fabsf(u));
           v[e] = (op_t)u;
@@ -428,23 +423,24 @@ __global__ __launch_bounds__(64 * TMD_WAVES, 1) void tm_contract_dma_kernel(
 
 // ---------------------------------------------------------------------------------
 // Output: z[i,j,:] (+)= p_out(LN_out(X[:,i,j])) * sigmoid(g_out(LN_in(z[i,j,:]))).
-// Persistent: one workgroup (8 waves) per CU keeps p_out / g_out in LDS with both LayerNorm
-// affines folded in (W_p' = W_p diag(gamma_out); W_g' = -log2(e) W_g diag(gamma_in), so
-// sigmoid(g) = 1 / (1 + 2^g'); the fp32 offsets W_p beta_out and -log2(e) W_g beta_in are each
-// accumulator's start value), so a tile only normalizes; each wave walks tiles of 32
-// consecutive pairs.  The tile's X slice (CC channels x 32 pairs, 64-byte rows of the planes)
-// comes in with 16-byte loads into a per-wave LDS stage and is read back per channel.  Both
-// products are formed as D[channel][pair] in the output-aligned layout, so the residual z
-// values the wave loaded for LN_in are the ones it adds to (no second read of z).  Weight rows
-// are CC + 4 op_t apart, so the 8-byte fragment reads of 32 rows fall on distinct banks.
+// Persistent: one workgroup (8 waves) per CU keeps p_out / g_out in LDS (op_t as given, so
+// rounded once) with both LayerNorms' beta folded into fp32 offsets W beta, added to the
+// products (gamma scales the normalized values before their rounding to op_t); each wave walks
+// tiles of 32 consecutive pairs.  The tile's X slice (CC channels x 32 pairs, 64-byte rows of
+// the planes) comes in with 16-byte loads into a per-wave LDS stage and is read back per
+// channel.  Both products are formed as D[channel][pair] in the output-aligned layout, so the
+// residual z values the wave loaded for LN_in are the ones it adds to (no second read of z).
+// Weight rows are CC + 4 op_t apart, so the 8-byte fragment reads of 32 rows fall on distinct
+// banks.
 // ---------------------------------------------------------------------------------
 constexpr int TMO_WAVES = 8, XSP = 40;   // per-wave X stage: [CC channels][32 pairs + 8]
-// LDS: the offsets [2 CC] fp32 (first, so that their reads use small immediate offsets), then
-// W_p', W_g' [CC][CC + 4] op_t, then the per-wave X stages
+// LDS: the offsets W_p beta_out [CC], -log2(e) W_g beta_in [CC] and gamma_out [CC], gamma_in [CC]
+// (fp32, first: small immediate offsets), then W_p, W_g [CC][CC + 4] op_t, then the per-wave
+// X stages
 template <int CC>
 constexpr size_t tmo_lds() {
-  return (size_t)2 * CC * (CC + 4) * sizeof(op_t) + (size_t)TMO_WAVES * CC * XSP * sizeof(op_t) +
-         2 * CC * sizeof(float);
+  return 4 * CC * sizeof(float) + (size_t)2 * CC * (CC + 4) * sizeof(op_t) +
+         (size_t)TMO_WAVES * CC * XSP * sizeof(op_t);
 }
 
 // resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
@@ -461,13 +457,15 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
   constexpr int LW = CC + 4, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t olds[];
   float* cbias = reinterpret_cast<float*>(olds);   // [0, CC): p, [CC, 2 CC): g
-  op_t* sWp = olds + 2 * CC * 2;
+  float* gam_o = cbias + 2 * CC;
+  float* gam_i = gam_o + CC;
+  op_t* sWp = olds + 4 * CC * 2;
   op_t* sWg = sWp + CC * LW;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   XT* xs = reinterpret_cast<XT*>(sWg + CC * LW) + wid * CC * XSP;   // this wave's X stage
-  // weights -> LDS as they are (rows are 8-byte aligned: two 8-byte stores per 16-byte load),
-  // then one thread per row folds the affine in place
+  // weights -> LDS (rows are 8-byte aligned: two 8-byte stores per 16-byte load), gamma, and
+  // the offsets W beta (one row per thread)
   for (int c = tid; c < CC * (CC / 8); c += 64 * TMO_WAVES) {
     const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
     const opx8 vp = ld_x8(w_pout + row * CC + col), vg = ld_x8(w_gout + row * CC + col);
@@ -476,26 +474,22 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
     *reinterpret_cast<opx4*>(&sWg[row * LW + col]) = opx4{vg[0], vg[1], vg[2], vg[3]};
     *reinterpret_cast<opx4*>(&sWg[row * LW + col + 4]) = opx4{vg[4], vg[5], vg[6], vg[7]};
   }
-  __syncthreads();
+  for (int c = tid; c < CC; c += 64 * TMO_WAVES) {
+    gam_o[c] = lno_w[c];
+    gam_i[c] = lni_w[c];
+  }
   for (int row = tid; row < 2 * CC; row += 64 * TMO_WAVES) {
     const bool g = row >= CC;
-    op_t* w = g ? sWg + (row - CC) * LW : sWp + row * LW;
-    const float* gam = g ? lni_w : lno_w;
+    const op_t* w = g ? w_gout + (row - CC) * CC : w_pout + row * CC;
     const float* bet = g ? lni_b : lno_b;
-    const float f = g ? -LOG2E : 1.f;
     float acc = 0.f;
 #pragma unroll 4
-    for (int c = 0; c < CC; c += 4) {
-      opx4 v = ld_x4(w + c);
+    for (int c = 0; c < CC; c += 8) {
+      const opx8 w8 = ld_x8(w + c);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float wf = (float)v[e] * f;
-        acc += wf * bet[c + e];
-        v[e] = (op_t)(wf * gam[c + e]);
-      }
-      *reinterpret_cast<opx4*>(w + c) = v;
+      for (int e = 0; e < 8; ++e) acc += (float)w8[e] * bet[c + e];
     }
-    cbias[row] = acc;
+    cbias[row] = g ? -LOG2E * acc : acc;
   }
   __syncthreads();
   if (nparts > 0) x_scale = 1.f / x_store_scale(planes_amax(amax_parts, nparts), N);   // a power of two
@@ -516,17 +510,17 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
     }
     const long pair = p0 + m;
     opx8 xo[KS], xi[KS];
-    float zr[CC / 2];
     {
       float xv[CC / 2];
 #pragma unroll
       for (int q = 0; q < CC / 8; ++q)
 #pragma unroll
         for (int e = 0; e < 4; ++e) xv[4 * q + e] = (float)xs[(oa_channel(q, h) + e) * XSP + m] * x_scale;
-      ln_oa_norm_to_frag<CC>(xv, eps, xo);
+      ln_oa_gamma_to_frag<CC>(xv, h, gam_o, eps, xo);
     }
+    float zr[CC / 2];
     load_row_oa<CC>(z_in + pair * CC, h, zr);
-    ln_oa_norm_to_frag<CC>(zr, eps, xi);
+    ln_oa_gamma_to_frag<CC>(zr, h, gam_i, eps, xi);
 #pragma unroll   // fully unrolled: zr[] must be indexed with constants to stay in VGPRs
     for (int ob = 0; ob < CC / 32; ++ob) {
       const op_t* wp = &sWp[(32 * ob + m) * LW];
@@ -546,11 +540,12 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
         const f32x4 cp = *reinterpret_cast<const f32x4*>(cbias + oa_channel(q, h));
         const f32x4 cg = *reinterpret_cast<const f32x4*>(cbias + CC + oa_channel(q, h));
         f32x4 v;
+        if (resid == 1) v = f32x4{zr[4 * q], zr[4 * q + 1], zr[4 * q + 2], zr[4 * q + 3]};
         if (resid == 2) v = *reinterpret_cast<const f32x4*>(dst);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float u = (P[4 * g + e] + cp[e]) * rcp_fast(1.f + exp2_fast(G[4 * g + e] + cg[e]));
-          v[e] = resid == 1 ? zr[4 * q + e] + u : resid == 2 ? v[e] + u : u;
+          const float u = (P[4 * g + e] + cp[e]) * rcp_fast(1.f + exp2_fast(fmaf(G[4 * g + e], -LOG2E, cg[e])));
+          v[e] = resid == 0 ? u : v[e] + u;
         }
         *reinterpret_cast<f32x4*>(dst) = v;
       }
