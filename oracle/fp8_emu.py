@@ -74,7 +74,7 @@ def fake_quant_mx8(x: torch.Tensor) -> torch.Tensor:
     K = x.shape[-1]
     if K % BLOCK:
         pad = BLOCK - K % BLOCK
-        xp = torch.cat([x, torch.zeros(x.shape[:-1] + (pad,), dtype=x.dtype)], dim=-1)
+        xp = torch.cat([x, torch.zeros(x.shape[:-1] + (pad,), dtype=x.dtype, device=x.device)], dim=-1)
         return fake_quant_mx8(xp)[..., :K]
     q, e = quantize_mx8(x)
     qb = q.reshape(x.shape[:-1] + (x.shape[-1] // BLOCK, BLOCK))

@@ -143,6 +143,63 @@ def test_transition_mx8(gpu):
     check("transition vs fp32 oracle", out, exact, F32_MAX, F32_MEAN)
 
 
+def test_transition_mx8_config4(gpu):
+    """The fp8 pair transition at config 4's shape (N = 1024, seed 4), against the emulator and
+    the fp32 oracle evaluated on the device (same formulas; the CPU would take minutes)."""
+    cfg = synthetic.CONFIGS[4]
+    N = cfg["N"]
+    w = _sub_w(cfg["seed"] + 1, "transition_z")
+    _, z, _, _ = synthetic.pair_inputs(N, cfg["seed"], with_s=False)
+    zd = z.to(gpu)
+    wd = {k: v.to(gpu) for k, v in w.items()}
+    with torch.no_grad():
+        want = ref.transition_mx8(zd, wd)
+    dw = ops.convert_weights({k: v for k, v in w.items() if v.dim() == 1}, gpu)
+    dw.update(ops.mx8_weights(w, gpu, ops.TRANSITION_MX8_KEYS))
+    out = torch.empty_like(zd)
+    ops.launch_transition_mx8(zd, out, dw, accumulate=False)
+    check("config4 transition N=1024 vs fp8 emulator", out, want, EMU_MAX, EMU_MEAN)
+    del want
+    with torch.no_grad():
+        exact = ref.transition(zd, wd)
+    check("config4 transition N=1024 vs fp32 oracle", out, exact, F32_MAX, F32_MEAN)
+
+
+@pytest.mark.timeout(600)
+def test_fast_layer_config4(gpu):
+    """A whole PairformerLayer in fast mode at config 4's shape (N = 1024, seed 4), against
+    the emulated-fp8 layer and the fp32 layer, both evaluated on the device.  Same bars as
+    test_module_fast_mode (the ops feed each other, so the layer drifts from the emulator by
+    re-rounded e4m3 steps): within 3e-2 mean of the emulated-fp8 layer, within the fp8 bound
+    of the fp32 layer, and clearly closer to the former."""
+    cfg = synthetic.CONFIGS[4]
+    N = cfg["N"]
+    w = synthetic.stack_weights(1, cfg["seed"])
+    s, z, mask, pm = synthetic.pair_inputs(N, cfg["seed"])
+    sd, zd, md, pmd = s.to(gpu), z.to(gpu), mask.to(gpu), pm.to(gpu)
+    wd = {k: v.to(gpu) for k, v in w.items()}
+    with torch.no_grad():
+        s_ref, z_ref = ref.pairformer_stack(sd, zd, md, pmd, wd, 1, fast=True)
+        s_32, z_32 = ref.pairformer_stack(sd, zd, md, pmd, wd, 1)
+    pairformer.set_fast_mode(True)
+    try:
+        pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, w)
+    finally:
+        pairformer.set_fast_mode(False)
+    assert pf.blocks[0].triangle_multiplication_start.fast and pf.blocks[0].transition_z.fast
+    s_got, z_got = pf(sd.clone(), zd.clone(), pmd, md)
+    torch.cuda.synchronize()
+    for name, got, emu, f32 in (("z", z_got, z_ref, z_32), ("s", s_got, s_ref, s_32)):
+        mx_e, mn_e = stats(got, emu)
+        mx_f, mn_f = stats(got, f32)
+        print(f"[fast] layer N=1024 {name}: vs emulator max/rms={mx_e:.3e} mean/rms={mn_e:.3e}; "
+              f"vs fp32 max/rms={mx_f:.3e} mean/rms={mn_f:.3e}", flush=True)
+        assert torch.isfinite(got).all()
+        assert mn_e <= 3e-2 and mx_e <= 0.5, (name, mx_e, mn_e)
+        assert mn_f <= F32_MEAN and mx_f <= F32_MAX, (name, mx_f, mn_f)
+        assert mn_e <= 0.6 * mn_f, (name, mn_e, mn_f)
+
+
 def test_module_fast_mode(gpu):
     """set_fast_mode(True) before construction (tenstorrent.py:178-181): a 1-block
     PairformerModule at N = 100 (padded to 128).
