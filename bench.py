@@ -491,14 +491,14 @@ def main() -> int:
     # Dominant kernel: the triangle-attention core (ta_attn_kernel, ~0.18 ms of each
     # triangle attention), launched alone on the q/k/v/bias/mask the last call left in the
     # workspace, timed with HIP events on the stream it runs on.  MFMA-bound: 4*N^3*128 FLOP
-    # per launch (QK^T and PV over 4 heads of 32) against 16-bit traffic of q, k, v read once,
-    # the bias and mask once and o written once.
+    # per launch (QK^T and PV over 4 heads of 32) against the traffic of q, k, v (16-bit) read
+    # once, the fp32 bias of the 4 heads and the 16-bit mask once and o (16-bit) written once.
     reps = 20
     layer.triangle_attention_start(z, None, out=torch.empty_like(z), accumulate=False, ws=ws)
     attn_ms = time_op(lambda: ops.launch_triatt_attend(ws, 1, N, 0, layer.variant), reps)
     attn_flop = fl["triatt_core"]
     attn_tf = attn_flop / (attn_ms * 1e-3) / 1e12
-    attn_bytes = (3 * 128 + 4 + 1 + 128) * N * N * 2
+    attn_bytes = (3 * 128 + 1 + 128) * N * N * 2 + 4 * N * N * 4
     roofline = {"kernel": "ta_attn_kernel", "bound": "mfma", "achieved": round(attn_tf, 1),
                 "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(attn_tf / MFMA_BF16_PEAK_TFLOPS, 4),
                 "traffic": measured_traffic("ta_attn_kernel"), "algorithmic_bytes": attn_bytes,
