@@ -88,7 +88,8 @@ int pf_trimul_fwd(const pf_trimul_args* args);
 
 /* The contraction alone: X[p][i][j] = sum_k A[p][i][k] * Bm[p][j][k] for `planes`
  * independent N x N operand-type planes.  x_fp32 = 1: X is fp32; x_fp32 = 0: X is the
- * operand type scaled by 2^-8 (the format pf_trimul_fwd uses internally).  The batched
+ * operand type scaled by 2^-8 (pf_trimul_fwd itself scales its X planes by a per-call power of
+ * two chosen from the largest |a|, |b| it wrote).  The batched
  * matmul inside TriangleMultiplication (tt_bio/tenstorrent.py:453-460; einsum at
  * tt_bio/reference.py:467, 556). */
 int pf_trimul_contract(const void* A, const void* Bm, void* X, int x_fp32, int planes, int N, void* stream);
