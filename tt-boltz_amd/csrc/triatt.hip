@@ -210,32 +210,28 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
 // Flash attention.  OUT_F32 = false: O op_t [B][N][N][H*D] (frame pair layout);
 // OUT_F32 = true: O fp32 [B][N][H][N][D] (the standalone attention-core API).
 //
-// A workgroup is 8 waves (two per SIMD): 4 frame rows (ip0 .. ip0+3) x 2 blocks of 64 queries;
-// each wave owns one row and two 32-query blocks and walks 4 heads x N/64 key tiles.  Per step
+// A workgroup is 16 waves (four per SIMD): 4 frame rows (ip0 .. ip0+3) x 4 blocks of 32 queries;
+// each wave owns one row and one 32-query block and walks 4 heads x N/64 key tiles.  Per step
 // the workgroup's fp32 bias tile [128 q][64 k], the four rows' K [64 k][32 d] and V^T
-// [32 d][64 k] tiles and their mask entries move global -> LDS by DMA (global_load_lds, no
-// VGPR staging) through a 2-deep ring, one barrier per step.  Scores S'^T[key][query] come out
-// of three MFMAs per 32x32 tile:
+// [32 d][64 k] tiles and their mask entries move global -> LDS by DMA (buffer loads straight to
+// LDS, no VGPR staging) through a 2-deep ring, one barrier per step.  Scores S'^T[key][query]
+// come out of three MFMAs per 32x32 tile:
 //     bias^T (fp32, the accumulator's start value, read from LDS in accumulator order)
 //     + K.Q^T (2)  +  [1, mask[key]] . [-m[q], 1]^T (1: two used k-slots)
 // so the bias, the key mask and the reference max cost no VALU and the bias is not rounded;
-// the softmax is exp2, an fp16 pair pack and v_dot2 row sums.  A wave's K and V^T fragments
-// serve both of its query blocks.  The reference max m[q] is kept as an op_t value (exact as
-// an MFMA operand) and moves lazily: at a head's first tile, while a query has seen no unmasked
-// key, or when a tile's row sum exceeds 2^14 (some P above 2^9).  A P that would overflow op_t
-// fails the same test before it reaches the P.V MFMA, and the tile is then repacked from S'
-// with the new reference.  Within a step the four 32x32 tiles (query block c, key half u) are
-// ordered so that every softmax has independent score MFMAs queued ahead of it and a tile's
-// scores are formed only after the softmax of the previous tile of the same query block (so
-// a rescale never has to shift already formed scores).
-// Each stage of a section sits right after the other, so the loop (unrolled by two) selects
-// the stage with the LDS instructions' immediate offsets.
+// the softmax is exp2, an fp16 pair pack and v_dot2 row sums.  The reference max m[q] is kept
+// as an op_t value (exact as an MFMA operand) and moves lazily: at a head's first tile, while a
+// query has seen no unmasked key, or when a tile's row sum exceeds 2^14 (some P above 2^9).  A P
+// that would overflow op_t fails the same test before it reaches the P.V MFMA, and the tile is
+// then repacked from S' with the new reference.  A wave's two key halves of a step are processed
+// one after the other (so a tile's scores always use the reference the previous tile left);
+// four waves per SIMD (about 100 VGPRs each) hide each other's MFMA and LDS latencies.
 // Rows whose valid keys are all masked: the fp32 reference adds -1e9 to every logit,
 // which rounds them all to -1e9 (|logit| < 32), i.e. a uniform average over the keys.
 // Such a row's waves skip the tiles (still taking part in every barrier and DMA) and write
 // the mean of v after the loop.
 // ---------------------------------------------------------------------------------
-constexpr int TA_WAVES = 8;
+constexpr int TA_WAVES = 16;
 // LDS sections (bytes), each holding stage 0 then stage 1:
 //   bias fp32 [128 q][64 k]: rows of 256 B, 16-byte chunk c of row q at position c ^ (q & 15)
 //   K   op_t  [4 rows][64 k][32 d]: rows of 64 B, chunk swizzle swz4
@@ -290,7 +286,7 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   extern __shared__ __attribute__((aligned(16))) char alds[];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int row = wid & 3, qp = wid >> 2;   // frame row, pair of 32-query blocks
+  const int row = wid & 3, qb = wid >> 2;   // frame row, 32-query block
   const int nQP = (N + 127) >> 7, nKB = N >> 6, T = H * nKB;
   const int w = xcd_remap(blockIdx.x, total);
   const int per_b = (N >> 2) * nQP;
@@ -304,25 +300,24 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
 
   // ---- DMA: buffer resources (SGPRs) over this workgroup's operands, per-lane 32-bit source
   // offsets, the step's offset as the uniform soffset; reads outside a resource return 0 ----
-  // bias: wave w's instruction j fills LDS bytes 4096 w + 1024 j .. of the stage, i.e. rows
-  // q = 16 w + 4 j + (lane >> 4), position lane & 15, which holds chunk (lane & 15) ^ (q & 15).
-  // K and V^T: chunk tid + 512 j of the 16 KB tile (instruction j); mask: wave 0, 1 KB.
+  // bias: wave w's instruction j fills LDS bytes 2048 w + 1024 j .. of the stage, i.e. rows
+  // q = 8 w + 4 j + (lane >> 4), position lane & 15, which holds chunk (lane & 15) ^ (q & 15).
+  // K and V^T: chunk tid of the 16 KB tile (one instruction each); mask: wave 0, 1 KB.
   const __amdgpu_buffer_rsrc_t rB = make_rsrc(bias32 + (long)b * H * NN, (long)H * NN * 4);
   const __amdgpu_buffer_rsrc_t rK = make_rsrc(K + ((long)b * N + ip0) * H * seqD, 4l * H * seqD * 2);
   const __amdgpu_buffer_rsrc_t rV = make_rsrc(Vt + ((long)b * N + ip0) * H * seqD, 4l * H * seqD * 2);
   const __amdgpu_buffer_rsrc_t rM = make_rsrc(mask16 + ((long)b * N + ip0) * N, 4l * N * 2);
-  uint32_t offB[4], offK[2], offV[2];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int q = 16 * wid + 4 * j + (lane >> 4);
-    offB[j] = 4u * ((uint32_t)min(jw0 + q, N - 1) * (uint32_t)N + 4u * (uint32_t)((lane & 15) ^ (q & 15)));
-  }
+  uint32_t offB[2], offK, offV;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int c = tid + 512 * j;
+    const int q = 8 * wid + 4 * j + (lane >> 4);
+    offB[j] = 4u * ((uint32_t)min(jw0 + q, N - 1) * (uint32_t)N + 4u * (uint32_t)((lane & 15) ^ (q & 15)));
+  }
+  {
+    const int c = tid;
     const int rk = c >> 8, kk = (c >> 2) & 63, dd = (c >> 3) & 31;
-    offK[j] = 2u * (rk * H * seqD + kk * D + 8 * ((c & 3) ^ swz4(kk)));
-    offV[j] = 2u * (rk * H * seqD + dd * N + 8 * ((c & 7) ^ swz8(dd)));
+    offK = 2u * (rk * H * seqD + kk * D + 8 * ((c & 3) ^ swz4(kk)));
+    offV = 2u * (rk * H * seqD + dd * N + 8 * ((c & 7) ^ swz8(dd)));
   }
   const uint32_t offM = 2u * (((lane >> 3) & 3) * N + 8 * (lane & 7));
   // stage `s` of step (hd, kb0)
@@ -331,19 +326,15 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
     const uint32_t skv = 2u * ((uint32_t)(hd * seqD) + (uint32_t)kb0 * D);
     const uint32_t sv = 2u * ((uint32_t)(hd * seqD) + (uint32_t)kb0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(rB, alds + TS_BIAS + s * TB_STAGE + 4096 * wid + 1024 * j, offB[j], sb);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      dma16(rK, alds + TS_K + s * TK_STAGE + 1024 * wid + 8192 * j, offK[j], skv);
-      dma16(rV, alds + TS_V + s * TV_STAGE + 1024 * wid + 8192 * j, offV[j], sv);
-    }
+    for (int j = 0; j < 2; ++j) dma16(rB, alds + TS_BIAS + s * TB_STAGE + 2048 * wid + 1024 * j, offB[j], sb);
+    dma16(rK, alds + TS_K + s * TK_STAGE + 1024 * wid, offK, skv);
+    dma16(rV, alds + TS_V + s * TV_STAGE + 1024 * wid, offV, sv);
     if (wid == 0) dma16(rM, alds + TS_MASK + s * TM_STAGE, offM, 2u * (uint32_t)kb0);
   };
 
   // ---- per-lane LDS read addresses (stage 0; stage 1 adds the section's stage size) ----
-  // bias of query block c (rows 64 qp + 32 c + m): 32 c rows further = 8192 B
   const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)alds;
-  const int qrow = 64 * qp + m;
+  const int qrow = 32 * qb + m;
   uint32_t aB[8], aV[4], aK[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u)            // key half u, accumulator register group g
@@ -358,7 +349,6 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   for (int s = 0; s < 2; ++s) aK[s] = base + TS_K + 4096 * row + 64 * m + 16 * ((2 * s + h) ^ ksw);
   uint32_t aM = base + TS_MASK + 128 * row + 2 * m;
   // opaque to the optimizer: each read is then one address register + an immediate offset
-  // (otherwise the sums are split up again and re-added at every read)
 #pragma unroll
   for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(aB[i]));
 #pragma unroll
@@ -375,45 +365,32 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
 
   const uint32_t ONE = half_bits((op_t)1.f);
   // the rank-1 operands are 4-register tuples whose words 1..3 stay zero: only word 0 changes
-  // ([-m, 1] of a block's reference in fb, [1, mask] of a key half in ra), half 1 of the wave
-  // holds zero
-  u32x4 fb[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}}, ra[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-  auto set_fb = [&](int c, float mv) PF_INLINE {
-    fb[c][0] = h ? 0u : (half_bits((op_t)(-mv)) | ONE << 16);
-    asm volatile("" : "+v"(fb[c]));
+  // ([-m, 1] of the block's reference in fb, [1, mask] of the key half in ra), half 1 of the
+  // wave holds zero
+  u32x4 fb = {0u, 0u, 0u, 0u}, ra = {0u, 0u, 0u, 0u};
+  auto set_fb = [&](float mv) PF_INLINE {
+    fb[0] = h ? 0u : (half_bits((op_t)(-mv)) | ONE << 16);
+    asm volatile("" : "+v"(fb));
   };
 
-  // per query block c: first query jq0[c]; blocks past N (trailing part tile) idle
-  int jq0[2];
-  bool qvalid[2];
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    jq0[c] = jw0 + 64 * qp + 32 * c;
-    qvalid[c] = jq0[c] < N;
-  }
-  const bool any_valid = qvalid[0];
-  opx8 qf[2][2], qn[2][2];
-  f32x16 o[2];
-  float mh[2], lsum[2];
-  bool mset[2];
+  const int jq0 = jw0 + 32 * qb;   // first query of this wave's block; blocks past N idle
+  const bool qvalid = jq0 < N;
+  opx8 qf[2];
+  f32x16 o;
+  float mh, lsum;
+  bool mset;
   auto q_load = [&](int hd) PF_INLINE {
+    const int jq = min(jq0, N - 32);
+    const op_t* qptr = Q + ((((long)b * N + ip) * H + hd) * N + jq + m) * D + 8 * h;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int jq = min(jq0[c], N - 32);
-      const op_t* qptr = Q + ((((long)b * N + ip) * H + hd) * N + jq + m) * D + 8 * h;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) qn[c][s] = ld_x8(qptr + 16 * s);
-    }
+    for (int s = 0; s < 2; ++s) qf[s] = ld_x8(qptr + 16 * s);
   };
   auto head_start = [&]() PF_INLINE {
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      o[c] = zero16();
-      lsum[c] = 0.f;
-      mh[c] = 0.f;
-      mset[c] = false;
-      set_fb(c, 0.f);
-    }
+    o = zero16();
+    lsum = 0.f;
+    mh = 0.f;
+    mset = false;
+    set_fb(0.f);
   };
   // P = exp2(S') packed into the two P.V operands; returns the lane's row sum
   auto exp_pack = [&](const f32x16& sc, u32x4 (&pf)[2]) PF_INLINE {
@@ -430,140 +407,91 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
       }
     return ls[0] + ls[1];
   };
-  // One step (stage STG) of a live row, per query block c: the scores of its two 32x32 tiles
-  // (key halves u), their softmax against the current reference, one check, and the four P.V
-  // MFMAs.  When the check fails (a query without a reference yet -- every head's first step
-  // -- or a tile row sum above LSTEP_MAX) the reference moves to the tiles' maxima first.
-  auto step4 = [&](auto stg) PF_INLINE {
+  // One step (stage STG) of a live row: the block's two 32x32 tiles (key halves u) one after the
+  // other: scores (bias as the accumulator start, K.Q^T, the mask / reference fold), the softmax
+  // against the current reference, one check, and the two P.V MFMAs.  When the check fails (no
+  // reference yet -- every head's first tile -- or a tile row sum above LSTEP_MAX) the reference
+  // moves to the tile's maximum first; the next tile's scores already use the new reference.
+  auto step2 = [&](auto stg) PF_INLINE {
     constexpr int STG = decltype(stg)::value;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {   // [1, mask[key]] rank-1 operands of the two key halves
-      ra[u][0] = h ? 0u : (ONE | lds_rd16(aM + STG * TM_STAGE + 64 * u) << 16);
-      asm volatile("" : "+v"(ra[u]));
+    for (int u = 0; u < 2; ++u) {
+      ra[0] = h ? 0u : (ONE | lds_rd16(aM + STG * TM_STAGE + 64 * u) << 16);
+      asm volatile("" : "+v"(ra));
+      f32x16 sc;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 bv = lds_rd4f(aB[4 * u + g] + STG * TB_STAGE);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[4 * g + e] = bv[e];
+      }
+#pragma unroll
+      for (int s = 0; s < 2; ++s) sc = mfma32(lds_rd8(aK[s] + STG * TK_STAGE + 2048 * u), qf[s], sc);
+      sc = mfma32(as_x8(ra), as_x8(fb), sc);
+      u32x4 pf[2];
+      float l = exp_pack(sc, pf);
+      if (__ballot(!mset || l > LSTEP_MAX) != 0) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[r]);
+        mx = xor32_max(mx);
+        const float d = mset ? (mx > RESCALE_SLACK ? mx : 0.f) : (mx == -INFINITY ? 0.f : mx);
+        const float mnew = (float)(op_t)(mh + d);
+        const float dsub = mnew - mh;
+        const float alpha = mset ? exp2_fast(-dsub) : 1.f;
+        lsum *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[r] *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[r] -= dsub;
+        l = exp_pack(sc, pf);
+        mset = mset || mx != -INFINITY;
+        mh = mnew;
+        set_fb(mnew);
+      }
+      lsum += l;
+      const opx8 v0 = lds_rd8(aV[2 * u] + STG * TV_STAGE), v1 = lds_rd8(aV[2 * u + 1] + STG * TV_STAGE);
+      o = mfma32(v0, as_x8(pf[0]), o);
+      o = mfma32(v1, as_x8(pf[1]), o);
     }
-    opx8 kf[2][2];   // [key half][k step]
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) kf[u][s] = lds_rd8(aK[s] + STG * TK_STAGE + 2048 * u);
-    // scores of block c: bias as the accumulator start, then K.Q^T and the mask / max fold
-    auto scores = [&](auto cc, f32x16 (&sc)[2]) PF_INLINE {
-      constexpr int c = decltype(cc)::value;
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 bv = lds_rd4f(aB[4 * u + g] + STG * TB_STAGE + 8192 * c);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sc[u][4 * g + e] = bv[e];
-        }
-        sc[u] = mfma32(kf[u][0], qf[c][0], sc[u]);
-        sc[u] = mfma32(kf[u][1], qf[c][1], sc[u]);
-        sc[u] = mfma32(as_x8(ra[u]), as_x8(fb[c]), sc[u]);
-      }
-    };
-    // Move block c's reference to its two tiles' maxima (none set yet: to the max; set: by the
-    // max when it exceeds RESCALE_SLACK), rescale o and lsum, repack P.
-    auto rescale = [&](auto cc, f32x16 (&sc)[2], u32x4 (&pf)[2][2], float& ls0, float& ls1) PF_INLINE {
-      constexpr int c = decltype(cc)::value;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[u][r]);
-      mx = xor32_max(mx);
-      const float d = mset[c] ? (mx > RESCALE_SLACK ? mx : 0.f) : (mx == -INFINITY ? 0.f : mx);
-      const float mnew = (float)(op_t)(mh[c] + d);
-      const float dsub = mnew - mh[c];
-      const float alpha = mset[c] ? exp2_fast(-dsub) : 1.f;
-      lsum[c] *= alpha;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[c][r] *= alpha;
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sc[u][r] -= dsub;
-      ls0 = exp_pack(sc[0], pf[0]);
-      ls1 = exp_pack(sc[1], pf[1]);
-      mset[c] = mset[c] || mx != -INFINITY;
-      mh[c] = mnew;
-      set_fb(c, mnew);
-    };
-    auto pv = [&](auto cc, const u32x4 (&pf)[2][2]) PF_INLINE {
-      constexpr int c = decltype(cc)::value;
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const opx8 v0 = lds_rd8(aV[2 * u] + STG * TV_STAGE), v1 = lds_rd8(aV[2 * u + 1] + STG * TV_STAGE);
-        o[c] = mfma32(v0, as_x8(pf[u][0]), o[c]);
-        o[c] = mfma32(v1, as_x8(pf[u][1]), o[c]);
-      }
-    };
-    // Block 1's score MFMAs are issued before block 0's softmax and block 0's P.V before block
-    // 1's, so each softmax has independent MFMA work in flight.  At a head's first step no
-    // reference is set (mset false), so the check sends both blocks through the rescale.
-    f32x16 s0[2], s1[2];
-    u32x4 p0[2][2], p1[2][2];
-    float l00, l01, l10, l11;
-    scores(ic<0>{}, s0);
-    scores(ic<1>{}, s1);
-    l00 = exp_pack(s0[0], p0[0]);
-    l01 = exp_pack(s0[1], p0[1]);
-    if (__ballot(!mset[0] || fmaxf(l00, l01) > LSTEP_MAX) != 0) rescale(ic<0>{}, s0, p0, l00, l01);
-    lsum[0] += l00 + l01;
-    pv(ic<0>{}, p0);
-    l10 = exp_pack(s1[0], p1[0]);
-    l11 = exp_pack(s1[1], p1[1]);
-    if (__ballot(!mset[1] || fmaxf(l10, l11) > LSTEP_MAX) != 0) rescale(ic<1>{}, s1, p1, l10, l11);
-    lsum[1] += l10 + l11;
-    pv(ic<1>{}, p1);
   };
   auto finalize = [&](int hd) PF_INLINE {
+    if (!qvalid) return;
+    const float inv = rcp_fast(xor32_sum(lsum));
+    const int j = jq0 + m;
+    const long rowbase = ((long)b * N + ip) * H;
+    if (OUT_F32) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      if (!qvalid[c]) continue;
-      const float inv = rcp_fast(xor32_sum(lsum[c]));
-      const int j = jq0[c] + m;
-      const long rowbase = ((long)b * N + ip) * H;
-      if (OUT_F32) {
+      for (int g = 0; g < 4; ++g) {
+        f32x4 v;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          f32x4 v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = o[c][4 * g + e] * inv;
-          *reinterpret_cast<f32x4*>(O32 + ((rowbase + hd) * N + j) * D + 8 * g + 4 * h) = v;
-        }
-      } else {
-        store_runs16(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd, o[c], inv, h);   // 16-byte runs
+        for (int e = 0; e < 4; ++e) v[e] = o[4 * g + e] * inv;
+        *reinterpret_cast<f32x4*>(O32 + ((rowbase + hd) * N + j) * D + 8 * g + 4 * h) = v;
       }
+    } else {
+      store_runs16(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd, o, inv, h);   // 16-byte runs
     }
   };
 
   // Step loop: T steps (T = 4 N / 64, even), one barrier each (the loop-top wait + barrier),
-  // the DMA of the next step into the other stage and, at a head's last tile, the next head's
-  // Q prefetch; then the four tiles.  The barrier also tells every wave that the other stage
-  // (read in the previous step) is free.
+  // the DMA of the next step into the other stage; at a head's first tile the head's Q is
+  // loaded.  The barrier also tells every wave that the other stage (read in the previous step)
+  // is free.
   int kbi = 0, hd = 0;  // step it = hd * nKB + kbi
-  q_load(0);
   issue(0, 0, 0);
   auto one_step = [&](auto stg, int it) PF_INLINE {
     constexpr int STG = decltype(stg)::value;
-    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));   // this wave's part of stage STG landed ...
+    if (kbi == 0 && qvalid && live) q_load(hd);
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));   // this wave's part of stage STG (and Q) landed ...
     __builtin_amdgcn_s_barrier();              // ... for every wave; stage STG ^ 1 is free
     asm volatile("" ::: "memory");
-    if (kbi == 0) {   // take this head's Q before qn is reused
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int s = 0; s < 2; ++s) qf[c][s] = qn[c][s];
-    }
     if (it + 1 < T) {
       const bool wrap = kbi + 1 == nKB;
       issue(STG ^ 1, wrap ? hd + 1 : hd, wrap ? 0 : 64 * (kbi + 1));
-      if (wrap) q_load(hd + 1);
     }
-    if (any_valid && live) {
+    if (qvalid && live) {
       if (kbi == 0) head_start();
-      step4(stg);
+      step2(stg);
       if (kbi == nKB - 1) finalize(hd);
     }
     if (++kbi == nKB) {
@@ -579,7 +507,7 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   // A dead row (every valid key masked): the reference's logits all round to -1e9, so each
   // query's output is the plain mean of v over the n_valid keys.  The wave sums its row's V^T
   // (keys stored at perm16 positions) for d = m, the two lane halves taking alternate keys.
-  if (!live && any_valid) {
+  if (!live && qvalid) {
     const float inv_n = 1.f / (float)n_valid;
     for (int hd2 = 0; hd2 < H; ++hd2) {
       const op_t* vrow = Vt + ((((long)b * N + ip) * H + hd2) * D + m) * (long)N;
@@ -591,26 +519,22 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
           if (perm16(p0 + e) < n_valid) acc += (float)v8[e];
       }
       const float mean = xor32_sum(acc) * inv_n;   // lanes m and m + 32 both hold d = m
+      const int j = jq0 + m;
+      if (OUT_F32) {
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        if (!qvalid[c]) continue;
-        const int j = jq0[c] + m;
-        if (OUT_F32) {
+        for (int q4 = 0; q4 < 4; ++q4) {
+          f32x4 v;
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            f32x4 v;
+          for (int e = 0; e < 4; ++e) v[e] = __shfl(mean, 16 * h + 4 * q4 + e);
+          *reinterpret_cast<f32x4*>(O32 + ((((long)b * N + ip) * H + hd2) * N + j) * D + 16 * h + 4 * q4) = v;
+        }
+      } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = __shfl(mean, 16 * h + 4 * q4 + e);
-            *reinterpret_cast<f32x4*>(O32 + ((((long)b * N + ip) * H + hd2) * N + j) * D + 16 * h + 4 * q4) = v;
-          }
-        } else {
+        for (int q8 = 0; q8 < 2; ++q8) {
+          opx8 v;
 #pragma unroll
-          for (int q8 = 0; q8 < 2; ++q8) {
-            opx8 v;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = (op_t)__shfl(mean, 16 * h + 8 * q8 + e);
-            st_x8(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd2 + 16 * h + 8 * q8, v);
-          }
+          for (int e = 0; e < 8; ++e) v[e] = (op_t)__shfl(mean, 16 * h + 8 * q8 + e);
+          st_x8(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd2 + 16 * h + 8 * q8, v);
         }
       }
     }
