@@ -290,6 +290,44 @@ typedef struct pf_transition_mx8_args {
 
 int pf_transition_mx8_fwd(const pf_transition_mx8_args* args);
 
+/* Triangle attention in fast mode (same semantics and argument meaning as pf_triatt_fwd,
+ * C = 128).  The block-fp8 points are those of the ttnn TriangleAttention under --fast
+ * (tt_bio/tenstorrent.py:526-539 weights, 603-614 / 628-639 projections, 580-590 output):
+ * linear_{q,k,v,g}.weight MXFP8 along C (pf_quantize_mx8, dequantized per call into the
+ * workspace, so the LayerNorm output stays 16-bit as in the reference); q, k, v and g
+ * quantize-dequantized per head (32 channels) right after their projections; the
+ * o-projection's output per 32 channels before the residual.  linear.weight (the triangle
+ * bias) and linear_o.weight stay 16-bit, as the reference keeps them bfloat16. */
+typedef struct pf_triatt_mx8_args {
+  int B, N, C;            /* C = 128 */
+  int H, D;               /* heads = 4, head dim = 32 */
+  int ending;
+  int accumulate;
+  int n_valid;
+  float eps;
+  const float* z_in;
+  float* out;
+  const float* pair_mask;
+  const float* ln_w; const float* ln_b;
+  const void* w_bias;                        /* linear.weight op_t [H][C] */
+  const void* w_q_q; const void* w_q_s;      /* mha.linear_q.weight [H*D][C] e4m3, [H*D][C/32] E8M0 */
+  const void* w_k_q; const void* w_k_s;
+  const void* w_v_q; const void* w_v_s;
+  const void* w_g_q; const void* w_g_s;
+  const void* w_o;                           /* mha.linear_o.weight op_t [C][H*D] */
+  void* workspace; size_t workspace_bytes;
+  void* stream;
+} pf_triatt_mx8_args;
+
+size_t pf_triatt_mx8_workspace_size(int B, int N, int C, int H, int D);
+int pf_triatt_mx8_fwd(const pf_triatt_mx8_args* args);
+
+/* AttentionPairBias in fast mode: pf_apb_fwd / pf_apb_attend with o * sigmoid(g)
+ * quantize-dequantized along c_s (32-channel blocks) before the output projection, the
+ * reference's multiply(..., dtype=_dtype()) (tt_bio/tenstorrent.py:844-846).  c_s % 32 == 0. */
+int pf_apb_fwd_mx8(const pf_apb_args* args);
+int pf_apb_attend_mx8(const pf_apb_args* args);
+
 /* ------------------------------------------------------------------------------
  * MSA module (widening beyond the Pairformer: tt_bio/reference.py:1150-1398, the ttnn
  * MSA / MSALayer in tt_bio/tenstorrent.py:1723-1855).

@@ -87,14 +87,20 @@ def triangle_multiplication(z, pair_mask, W, direction):
     return out
 
 
-def triangle_attention(z, pair_mask, W, starting, n_heads, head_dim, inf=1e9):
+def triangle_attention(z, pair_mask, W, starting, n_heads, head_dim, inf=1e9, fast=False):
     """Starting node: for each row i, head h, query j:
         logit[k] = (q[i,j]/sqrt(d)) . k[i,k] + inf*(mask[i,k]-1) + bias[h][j][k],
         bias[h][j][k] = LN(z)[j,k] . Wb[h]   (shared by all rows i)
     Ending node: the same on z^T / mask^T, output transposed back.
+    ``fast``: the rows of W_q, W_k, W_v, W_g, the vectors q, k, v, g (before the sigmoid)
+    and the output vector pass through mx8_vec.
     """
     z = _np(z)[0]; m = _np(pair_mask)[0]
     W = {k: _np(v) for k, v in W.items()}
+    fq = mx8_vec if fast else (lambda vec: vec)
+    if fast:
+        for key in ("mha.linear_q.weight", "mha.linear_k.weight", "mha.linear_v.weight", "mha.linear_g.weight"):
+            W[key] = np.array([mx8_vec(list(r)) for r in W[key]])
     if not starting:
         z = z.transpose(1, 0, 2); m = m.T
     N = z.shape[0]
@@ -103,10 +109,10 @@ def triangle_attention(z, pair_mask, W, starting, n_heads, head_dim, inf=1e9):
          for i in range(N)]
     bias = [[[sum(x[j][kk][c] * W["linear.weight"][h][c] for c in range(len(x[j][kk])))
               for kk in range(N)] for j in range(N)] for h in range(H)]
-    q = [[_matvec(W["mha.linear_q.weight"], x[i][j]) for j in range(N)] for i in range(N)]
-    k = [[_matvec(W["mha.linear_k.weight"], x[i][j]) for j in range(N)] for i in range(N)]
-    v = [[_matvec(W["mha.linear_v.weight"], x[i][j]) for j in range(N)] for i in range(N)]
-    g = [[[_sig(t) for t in _matvec(W["mha.linear_g.weight"], x[i][j])] for j in range(N)]
+    q = [[fq(_matvec(W["mha.linear_q.weight"], x[i][j])) for j in range(N)] for i in range(N)]
+    k = [[fq(_matvec(W["mha.linear_k.weight"], x[i][j])) for j in range(N)] for i in range(N)]
+    v = [[fq(_matvec(W["mha.linear_v.weight"], x[i][j])) for j in range(N)] for i in range(N)]
+    g = [[[_sig(t) for t in fq(_matvec(W["mha.linear_g.weight"], x[i][j]))] for j in range(N)]
          for i in range(N)]
     out = np.zeros((1, N, N, W["mha.linear_o.weight"].shape[0]))
     for i in range(N):
@@ -129,7 +135,7 @@ def triangle_attention(z, pair_mask, W, starting, n_heads, head_dim, inf=1e9):
                 for d in range(D):
                     o[h * D + d] = sum(e[kk] / s * v[i][kk][h * D + d] for kk in range(N))
             o = [o[c] * g[i][j][c] for c in range(H * D)]
-            out[0, i, j] = _matvec(W["mha.linear_o.weight"], o)
+            out[0, i, j] = fq(_matvec(W["mha.linear_o.weight"], o))
     if not starting:
         out = out.transpose(0, 2, 1, 3)
     return out
@@ -148,9 +154,10 @@ def transition(x, W):
     return out
 
 
-def attention_pair_bias(s, z, mask, k_in, W, num_heads, inf=1e6):
+def attention_pair_bias(s, z, mask, k_in, W, num_heads, inf=1e6, fast=False):
     """out_i = proj_o( sigmoid(proj_g s_i) * concat_h sum_j p_hij v_jh ),
     p_hij = softmax_j( q_ih . k_jh / sqrt(d) + LN(z_ij) . Wz[h] - inf*(1-mask_j) ).
+    ``fast``: the gated vector passes through mx8_vec before proj_o.
     """
     s = _np(s)[0]; z = _np(z)[0]; mask = _np(mask)[0]; k_in = _np(k_in)[0]
     W = {k: _np(v) for k, v in W.items()}
@@ -175,7 +182,8 @@ def attention_pair_bias(s, z, mask, k_in, W, num_heads, inf=1e6):
             ssum = sum(e)
             for d in range(D):
                 o[h * D + d] = sum(e[j] / ssum * vv[j][h * D + d] for j in range(N))
-        out[0, i] = _matvec(W["proj_o.weight"], [g[i][c] * o[c] for c in range(C)])
+        go = [g[i][c] * o[c] for c in range(C)]
+        out[0, i] = _matvec(W["proj_o.weight"], mx8_vec(go) if fast else go)
     return out
 
 

@@ -141,33 +141,35 @@ def triangle_multiplication_mx8(z: Tensor, pair_mask: Tensor, w: Weights, direct
 # Triangle attention  (tt_bio/reference.py:219-376 + Attention 33-194 + boltz2.py:790-810)
 # --------------------------------------------------------------------------------------
 def _mha_rows(x: Tensor, tri_bias: Tensor, mask_bias: Tensor, w: Weights,
-              n_heads: int, head_dim: int) -> Tensor:
+              n_heads: int, head_dim: int, fq=None) -> Tensor:
     """``Attention.forward`` with ``use_kernels=False`` on a block of rows.
 
     x [B,I,J,C]; tri_bias [B,1,H,J,K]; mask_bias [B,I,1,1,K].
     ``reference.py:96-121`` (_prep_qkv: q scaled by 1/sqrt(d) before QK^T),
     ``boltz2.py:790-810`` (_attention: a = qk; a += mask_bias; a += tri_bias;
     softmax; a @ v), ``reference.py:123-136`` (_wrap_up: sigmoid gate, flatten,
-    linear_o).
+    linear_o).  ``fq`` (fast mode): the quantizer applied, along channels, to the q, k,
+    v and g projections and to linear_o's output (``tenstorrent.py:580-590, 603-614``).
     """
+    fq = fq or (lambda t: t)
     shp = x.shape[:-1]
-    q = linear(x, w["linear_q.weight"]).view(shp + (n_heads, head_dim)).transpose(-2, -3)
-    k = linear(x, w["linear_k.weight"]).view(shp + (n_heads, head_dim)).transpose(-2, -3)
-    v = linear(x, w["linear_v.weight"]).view(shp + (n_heads, head_dim)).transpose(-2, -3)
+    q = fq(linear(x, w["linear_q.weight"])).view(shp + (n_heads, head_dim)).transpose(-2, -3)
+    k = fq(linear(x, w["linear_k.weight"])).view(shp + (n_heads, head_dim)).transpose(-2, -3)
+    v = fq(linear(x, w["linear_v.weight"])).view(shp + (n_heads, head_dim)).transpose(-2, -3)
     q = q / sqrt(head_dim)
     a = torch.matmul(_op(q), _op(k).transpose(-1, -2))      # [B,I,H,J,K]
     a = a + mask_bias
     a = a + tri_bias
     a = torch.softmax(a, dim=-1)
     o = torch.matmul(_op(a), _op(v)).transpose(-2, -3)      # [B,I,J,H,d]
-    g = torch.sigmoid(linear(x, w["linear_g.weight"])).view(shp + (n_heads, head_dim))
+    g = torch.sigmoid(fq(linear(x, w["linear_g.weight"]))).view(shp + (n_heads, head_dim))
     o = (_op(o) * g).reshape(shp + (n_heads * head_dim,))
-    return linear(o, w["linear_o.weight"])
+    return fq(linear(o, w["linear_o.weight"]))
 
 
 def triangle_attention(z: Tensor, pair_mask: Optional[Tensor], w: Weights, starting: bool = True,
                        chunk_size: Optional[int] = None, n_heads: int = 4, head_dim: int = 32,
-                       inf: float = 1e9) -> Tensor:
+                       inf: float = 1e9, fast: bool = False) -> Tensor:
     """Return the update of ``TriangleAttention{Starting,Ending}Node.forward``.
 
     ``reference.py:294-365``: transpose for the ending node; LN; additive
@@ -177,6 +179,12 @@ def triangle_attention(z: Tensor, pair_mask: Optional[Tensor], w: Weights, start
 
     Weight keys are those of the reference module: ``layer_norm.*``,
     ``linear.weight`` and ``mha.linear_{q,k,v,g,o}.weight``.
+
+    ``fast``: the fast-mode (``--fast``) restatement in this build's MXFP8 format
+    (``fp8_emu``) at the reference's block-fp8 points (``tenstorrent.py:526-539, 580-590,
+    603-614, 628-639``): linear_{q,k,v,g}.weight along their input channels, the q, k, v, g
+    projections along channels (one block per head) and linear_o's output along channels.
+    The LayerNorm output, the triangle bias and linear_o.weight stay exact.
     """
     if pair_mask is None:
         pair_mask = z.new_ones(z.shape[:-1])
@@ -188,12 +196,17 @@ def triangle_attention(z: Tensor, pair_mask: Optional[Tensor], w: Weights, start
     mask_bias = inf * (mask - 1)                                         # :335
     tri_bias = linear(x, w["linear.weight"]).permute(0, 3, 1, 2).unsqueeze(-4)  # :338-341
     mw = sub(w, "mha")
+    fq = None
+    if fast:
+        from .fp8_emu import fake_quant_mx8 as fq
+        mw = {k: (fq(t) if k in ("linear_q.weight", "linear_k.weight", "linear_v.weight", "linear_g.weight")
+                  else t) for k, t in mw.items()}
     n_rows = x.shape[1]
     step = n_rows if chunk_size is None else chunk_size
     outs = []
     for r0 in range(0, n_rows, step):
         r1 = min(r0 + step, n_rows)
-        outs.append(_mha_rows(x[:, r0:r1], tri_bias, mask_bias[:, r0:r1], mw, n_heads, head_dim))
+        outs.append(_mha_rows(x[:, r0:r1], tri_bias, mask_bias[:, r0:r1], mw, n_heads, head_dim, fq))
     out = torch.cat(outs, dim=1)
     if not starting:
         out = out.transpose(-2, -3)
@@ -241,12 +254,13 @@ def transition_mx8(x: Tensor, w: Weights) -> Tensor:
 # Single attention with pair bias  (tt_bio/boltz2.py:307-367)
 # --------------------------------------------------------------------------------------
 def attention_pair_bias(s: Tensor, z: Tensor, mask: Tensor, k_in: Tensor, w: Weights,
-                        num_heads: int = 16, inf: float = 1e6) -> Tensor:
+                        num_heads: int = 16, inf: float = 1e6, fast: bool = False) -> Tensor:
     """``AttentionPairBias.forward`` (``boltz2.py:343-367``), multiplicity 1.
 
     q = proj_q(s) (+bias), k/v from ``k_in``; bias = proj_z(z) =
     Linear(LN(z)) -> [B,H,N,N]; logits = qk^T/sqrt(d) + bias - inf*(1-mask_key);
-    softmax; o = P v; proj_o(sigmoid(proj_g(s)) * o).
+    softmax; o = P v; proj_o(sigmoid(proj_g(s)) * o).  ``fast``: sigmoid(g) * o in this
+    build's MXFP8 format along channels before proj_o (``tenstorrent.py:846``).
     """
     B, N, c_s = s.shape
     d = c_s // num_heads
@@ -262,7 +276,11 @@ def attention_pair_bias(s: Tensor, z: Tensor, mask: Tensor, k_in: Tensor, w: Wei
     attn = attn.softmax(dim=-1)
     o = torch.einsum("bhij,bjhd->bihd", _op(attn), _op(v.float())).to(v.dtype)
     o = o.reshape(B, -1, c_s)
-    return linear(g * o, w["proj_o.weight"])
+    go = g * o
+    if fast:
+        from .fp8_emu import fake_quant_mx8
+        go = fake_quant_mx8(go)
+    return linear(go, w["proj_o.weight"])
 
 
 # --------------------------------------------------------------------------------------
@@ -282,21 +300,23 @@ def pairformer_layer(s: Optional[Tensor], z: Tensor, mask: Optional[Tensor], pai
 
     z += TMo; z += TMi; z += TAs; z += TAe; z += Tr_z;
     s_n = LN(s); s += APB(s_n, z, mask, k_in=s_n); s += Tr_s(s).
-    ``fast``: the triangle multiplications and the pair transition in MXFP8.
+    ``fast``: the reference's fast mode in MXFP8: the triangle multiplications, the triangle
+    attentions' block-fp8 points, the pair transition and the single track's gated
+    attention output.
     """
     tm = triangle_multiplication_mx8 if fast else triangle_multiplication
     z = z + tm(z, pair_mask, sub(w, "tri_mul_out"), "outgoing")
     z = z + tm(z, pair_mask, sub(w, "tri_mul_in"), "incoming")
     z = z + triangle_attention(z, pair_mask, sub(w, "tri_att_start"), True, chunk_size,
-                               tri_att_heads, tri_att_head_dim)
+                               tri_att_heads, tri_att_head_dim, fast=fast)
     z = z + triangle_attention(z, pair_mask, sub(w, "tri_att_end"), False, chunk_size,
-                               tri_att_heads, tri_att_head_dim)
+                               tri_att_heads, tri_att_head_dim, fast=fast)
     z = z + (transition_mx8 if fast else transition)(z, sub(w, "transition_z"))
     if s is None:
         return None, z
     s_normed = layer_norm(s.float(), w["pre_norm_s.weight"], w["pre_norm_s.bias"])
     s = s.float() + attention_pair_bias(s_normed, z.float(), mask.float(), s_normed,
-                                        sub(w, "attention"), att_heads)
+                                        sub(w, "attention"), att_heads, fast=fast)
     s = s + transition(s, sub(w, "transition_s"))
     return s, z
 

@@ -369,6 +369,59 @@ def test_trimul_mx8_matches_brute(direction):
     assert 1e-3 < rel < 0.15, rel
 
 
+@pytest.mark.parametrize("starting", [True, False])
+def test_triatt_mx8_matches_brute(starting):
+    """Emulated-fp8 triangle attention vs the scalar-loop version (independent quantizer):
+    weights, q/k/v/g and the output quantized along channels (c = 32: one MX block)."""
+    N, c, H, D = 4, 32, 2, 16
+    z = torch.randn((1, N, N, c), generator=torch.Generator().manual_seed(60))
+    m = _rand_mask(N, 61, 0.25)
+    w = _triatt_w(c, H, D, 62)
+    got = ref.triangle_attention(z, m, w, starting, None, H, D, fast=True)
+    _close(got, brute.triangle_attention(z, m, w, starting, H, D, fast=True), 1e-4)
+    exact = ref.triangle_attention(z, m, w, starting, None, H, D)
+    rel = ((got - exact).abs().mean() / exact.abs().mean()).item()
+    assert 1e-3 < rel < 0.15, rel
+
+
+def test_triatt_mx8_quantization_points():
+    """With the quantizer replaced by the identity the fast triangle attention is the fp32
+    one, and it quantizes exactly: the four projection weights, then per row chunk q, k, v,
+    g and the output (a dropped or extra point changes the count or the shapes)."""
+    N, c, H, D = 6, 32, 2, 16
+    z = torch.randn((1, N, N, c), generator=torch.Generator().manual_seed(63))
+    m = _rand_mask(N, 64)
+    w = _triatt_w(c, H, D, 65)
+    seen = []
+
+    def ident(t):
+        seen.append(tuple(t.shape))
+        return t
+
+    real = fp8_emu.fake_quant_mx8
+    fp8_emu.fake_quant_mx8 = ident
+    try:
+        got = ref.triangle_attention(z, m, w, True, 3, H, D, fast=True)
+    finally:
+        fp8_emu.fake_quant_mx8 = real
+    assert torch.equal(got, ref.triangle_attention(z, m, w, True, 3, H, D))
+    assert seen == [(H * D, c)] * 4 + ([(1, 3, N, H * D)] * 4 + [(1, 3, N, c)]) * 2, seen
+
+
+def test_apb_mx8_matches_brute():
+    N, c_s, c_z, H = 5, 32, 8, 2
+    g = torch.Generator().manual_seed(66)
+    s = torch.randn((1, N, c_s), generator=g)
+    z = torch.randn((1, N, N, c_z), generator=g)
+    mask = torch.ones((1, N)); mask[0, 2] = 0
+    w = _apb_w(c_s, c_z, H, 67)
+    got = ref.attention_pair_bias(s, z, mask, s, w, H, fast=True)
+    _close(got, brute.attention_pair_bias(s, z, mask, s, w, H, fast=True), 1e-4)
+    exact = ref.attention_pair_bias(s, z, mask, s, w, H)
+    rel = ((got - exact).abs().mean() / exact.abs().mean()).item()
+    assert 1e-3 < rel < 0.15, rel
+
+
 def test_transition_mx8_matches_brute():
     c = 32
     w = _w({"norm.weight": (c,), "norm.bias": (c,), "fc1.weight": (4 * c, c), "fc2.weight": (4 * c, c),

@@ -44,6 +44,18 @@ class TriattArgs(ctypes.Structure):
     ]
 
 
+class TriattMx8Args(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int), ("N", c_int), ("C", c_int), ("H", c_int), ("D", c_int), ("ending", c_int),
+        ("accumulate", c_int), ("n_valid", c_int), ("eps", c_float),
+        ("z_in", c_void_p), ("out", c_void_p), ("pair_mask", c_void_p),
+        ("ln_w", c_void_p), ("ln_b", c_void_p), ("w_bias", c_void_p),
+        ("w_q_q", c_void_p), ("w_q_s", c_void_p), ("w_k_q", c_void_p), ("w_k_s", c_void_p),
+        ("w_v_q", c_void_p), ("w_v_s", c_void_p), ("w_g_q", c_void_p), ("w_g_s", c_void_p), ("w_o", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
+    ]
+
+
 class TransitionArgs(ctypes.Structure):
     _fields_ = [
         ("rows", c_long), ("C", c_int), ("hidden", c_int), ("accumulate", c_int), ("eps", c_float),
@@ -128,6 +140,8 @@ SIGNATURES = {
     "pf_apb_pair_bias": (c_int, [ctypes.POINTER(ApbArgs)]),
     "pf_apb_attend": (c_int, [ctypes.POINTER(ApbArgs)]),
     "pf_apb_fwd_noalloc": (c_int, [ctypes.POINTER(ApbArgs)]),
+    "pf_apb_fwd_mx8": (c_int, [ctypes.POINTER(ApbArgs)]),
+    "pf_apb_attend_mx8": (c_int, [ctypes.POINTER(ApbArgs)]),
     "pf_transition_pair_bias_fwd": (c_int, [ctypes.POINTER(TransitionArgs), ctypes.POINTER(ApbArgs)]),
     "pf_opm_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "pf_opm_fwd": (c_int, [ctypes.POINTER(OpmArgs)]),
@@ -149,6 +163,8 @@ SIGNATURES = {
     "pf_quantize_mx8": (c_int, [c_void_p, c_long, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "pf_trimul_mx8_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "pf_trimul_mx8_fwd": (c_int, [ctypes.POINTER(TrimulMx8Args)]),
+    "pf_triatt_mx8_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "pf_triatt_mx8_fwd": (c_int, [ctypes.POINTER(TriattMx8Args)]),
     "pf_trimul_mx8_contract": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "pf_transition_mx8_fwd": (c_int, [ctypes.POINTER(TransitionMx8Args)]),
 }

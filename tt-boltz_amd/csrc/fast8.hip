@@ -49,7 +49,7 @@ PF_DEV void load_row128_x8order(const float* __restrict__ p, int h, float (&x)[4
 // returns the packed bytes and the block's scale byte.
 PF_DEV i32x4 quantize16(const float (&y)[16], int& byte) {
   float a = amax16(y);
-  a = fmaxf(a, __shfl_xor(a, 32));
+  a = xor32_max(a);
   byte = mx_scale_byte(a);
   return e4m3_pack16(y, mx_inv_scale(byte));
 }

@@ -73,16 +73,18 @@ PF_DEV float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }   // v_exp
 // v_rcp_f32 (1 ulp) instead of the IEEE division sequence HIP emits for '/'.
 PF_DEV float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
 
-// sigmoid(x) = 1 / (1 + 2^(-x log2 e)): saturates cleanly to 0 / 1 for large |x|.
 // compile-time index for unrolled, stage-selected lambdas
 template <int V>
 using ic = std::integral_constant<int, V>;
 
+// sigmoid(x) = 1 / (1 + 2^(-x log2 e)): saturates cleanly to 0 / 1 for large |x|.
 PF_DEV float sigmoidf_fast(float x) { return rcp_fast(1.f + exp2_fast(-1.4426950408889634f * x)); }
 
 PF_DEV float siluf(float x) { return x * sigmoidf_fast(x); }
 
-// Sum across the two 32-lane halves of a wave64.
+// Sum / maximum over the lane pair (n, n + 32) of a wave64.  (A v_permlane32_swap form
+// avoids the LDS round trip of ds_bpermute but measured slower in tm_out_kernel: +8-10 us
+// at N = 512, the other pair kernels unchanged.)
 PF_DEV float xor32_sum(float v) { return v + __shfl_xor(v, 32); }
 PF_DEV float xor32_max(float v) { return fmaxf(v, __shfl_xor(v, 32)); }
 
@@ -387,6 +389,42 @@ PF_DEV float amax16(const float (&v)[16]) {
 #pragma unroll
   for (int t = 0; t < 16; ++t) a = fmaxf(a, fabsf(v[t]));
   return a;
+}
+
+// ---------------------------------------------------------------------------------
+// Quantize-dequantize ("fake quantization") in the format above, for values that stay in
+// fp32 / op_t registers but must carry the block-fp8 rounding: v <- e4m3(v / X) * X.
+// v_cvt_scalef32_pk_fp8_f32 divides by X and v_cvt_scalef32_pk_f32_fp8 multiplies by it,
+// exactly (X is a power of two); neither saturates, which the scale rule makes unnecessary
+// (|v / X| <= 448).  X is floored at 2^-126 (scale byte 1): only blocks whose maximum is
+// below 2^-118 differ from the format's 2^-127, and all-zero blocks stay zero.
+// ---------------------------------------------------------------------------------
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+
+PF_DEV float mx_block_scale(float amax) { return __uint_as_float((uint32_t)max(mx_scale_byte(amax), 1) << 23); }
+
+// One value with its own block scale X; `lim` = 448 X bounds v first (the block maximum
+// was taken from a separately computed copy of the values, which may differ in the last bit).
+PF_DEV float mx_fake_quant1(float v, float X, float lim) {
+  const i16x2 w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(i16x2{0, 0}, __builtin_amdgcn_fmed3f(v, -lim, lim), 0.f,
+                                                           X, false);
+  return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(__builtin_bit_cast(int, w), X, false)[0];
+}
+
+// One 32-element block held as 16 values by each lane of the pair (n, n + 32), in place.
+template <class V16>
+PF_DEV void mx_fake_quant16(V16& v) {
+  float a = 0.f;
+#pragma unroll
+  for (int t = 0; t < 16; ++t) a = fmaxf(a, fabsf(v[t]));
+  const float X = mx_block_scale(xor32_max(a));
+#pragma unroll
+  for (int t = 0; t < 16; t += 2) {
+    const i16x2 w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(i16x2{0, 0}, v[t], v[t + 1], X, false);
+    const auto f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(__builtin_bit_cast(int, w), X, false);
+    v[t] = f[0];
+    v[t + 1] = f[1];
+  }
 }
 
 // ---------------------------------------------------------------------------------

@@ -188,6 +188,29 @@ __global__ __launch_bounds__(64 * APB_SPLIT) void apb_attn_kernel(
   }
 }
 
+// In-place quantize-dequantize of `blocks` consecutive 32-float blocks (MXFP8, fast mode):
+// each wave takes 32 blocks, the lane pair (n, n + 32) one block as 16 + 16 values.  Lanes
+// past the end compute on block 0 (every lane takes part in the pair exchange) and store
+// nothing.
+__global__ __launch_bounds__(256) void mx8_fake_quant_rows_kernel(float* __restrict__ x, long blocks) {
+  const int lane = threadIdx.x & 63, h = lane >> 5, m = lane & 31;
+  const long blk = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 32 + m;
+  const bool live = blk < blocks;
+  float* p = x + (live ? blk : 0) * 32 + 16 * h;
+  f32x16 v;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(p + 4 * q);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * q + e] = t[e];
+  }
+  mx_fake_quant16(v);
+  if (live) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<f32x4*>(p + 4 * q) = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+  }
+}
+
 }  // namespace
 
 // linear_rows (transition.hip)
@@ -243,8 +266,10 @@ extern "C" int pf_apb_pair_bias(const pf_apb_args* a) {
   return PF_OK;
 }
 
-extern "C" int pf_apb_attend(const pf_apb_args* a) {
-  int rc = pf_apb_check(a, "pf_apb_attend", false);
+namespace {
+// fast: o * sigmoid(g) is quantize-dequantized (MXFP8 along c_s) before the output projection.
+int apb_attend_impl(const pf_apb_args* a, const char* fn, bool fast) {
+  int rc = pf_apb_check(a, fn, false);
   if (rc) return rc;
   const int n_valid = a->n_valid ? a->n_valid : a->N;
   hipStream_t st = (hipStream_t)a->stream;
@@ -270,14 +295,30 @@ extern "C" int pf_apb_attend(const pf_apb_args* a) {
     apb_attn_kernel<32><<<grid, 64 * APB_SPLIT, 0, st>>>(q, k, v, g, bias, a->mask, og, a->B, a->N, n_valid, cs,
                                                         a->H, 1e6f);
   PF_CHECK_LAUNCH("apb_attn_kernel");
+  if (fast) {
+    const long blocks = rows * cs / 32;
+    mx8_fake_quant_rows_kernel<<<(unsigned)((blocks + 127) / 128), 256, 0, st>>>(og, blocks);
+    PF_CHECK_LAUNCH("mx8_fake_quant_rows_kernel");
+  }
   return pf_linear_fwd(og, a->w_o, nullptr, a->accumulate ? a->out : nullptr, a->out, rows, cs, cs, a->stream);
 }
+}  // namespace
+
+extern "C" int pf_apb_attend(const pf_apb_args* a) { return apb_attend_impl(a, "pf_apb_attend", false); }
+extern "C" int pf_apb_attend_mx8(const pf_apb_args* a) { return apb_attend_impl(a, "pf_apb_attend_mx8", true); }
 
 extern "C" int pf_apb_fwd(const pf_apb_args* a) {
   int rc = pf_apb_check(a, "pf_apb_fwd", false);
   if (rc) return rc;
   if ((rc = pf_apb_pair_bias(a))) return rc;
   return pf_apb_attend(a);
+}
+
+extern "C" int pf_apb_fwd_mx8(const pf_apb_args* a) {
+  int rc = pf_apb_check(a, "pf_apb_fwd_mx8", false);
+  if (rc) return rc;
+  if ((rc = pf_apb_pair_bias(a))) return rc;
+  return pf_apb_attend_mx8(a);
 }
 
 // ---------------------------------------------------------------------------------

@@ -63,13 +63,20 @@ PF_DEV op_t mask_term(bool pad, float mv) {
 //   Q, K  [j][d]:  D[d][pos]   runs of 4 d, paired across lane halves (store_runs16)
 //   V^T   [d][k]:  D[pos][d]   a lane's key runs g = 2p, 2p+1 are 8 adjacent slots
 //   bias  [hd][j]: D[hd][pos]  a lane holds the 4 heads of its position
+// FAST (the fast mode's block-fp8 points): q, k and v are quantize-dequantized per head (one
+// 32-channel block per position) before they are stored.  Q and K blocks are lane pairs of
+// the D[d][pos] accumulator; V's D[pos][d] orientation spreads a block over 32 lanes, so a
+// D[d][pos] copy of V gives each key's block scale, passed through 32 floats of LDS per wave.
 // ---------------------------------------------------------------------------------
 constexpr int TAP_WAVES = 8;
 constexpr int TAP_ROWS = 3 * C + 32;   // q, k, v rows, then 32 bias rows (H used, rest zero)
-template <int CC>
-constexpr size_t tap_lds() { return (size_t)TAP_ROWS * (CC + 8) * sizeof(op_t) + TAP_ROWS * sizeof(float); }
+template <int CC, bool FAST = false>
+constexpr size_t tap_lds() {
+  return (size_t)TAP_ROWS * (CC + 8) * sizeof(op_t) + TAP_ROWS * sizeof(float) +
+         (FAST ? TAP_WAVES * 32 * sizeof(float) : 0);
+}
 
-template <int CC>
+template <int CC, bool FAST>
 __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
     const float* __restrict__ z, const float* __restrict__ pair_mask,
     const float* __restrict__ lnw, const float* __restrict__ lnb,
@@ -82,6 +89,7 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
   float* cb = reinterpret_cast<float*>(plds + TAP_ROWS * LW);
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  float* vsc = cb + TAP_ROWS + 32 * wid;   // FAST: this wave's per-key V block scales
   auto wrow = [&](int row) -> const op_t* {   // weight rows have CC inputs
     return row < C ? wq + row * CC : row < 2 * C ? wk + (row - C) * CC
          : row < 3 * C ? wv + (row - 2 * C) * CC : wb + (row - 3 * C) * CC;
@@ -164,12 +172,30 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
       }
 #pragma unroll
       for (int s2 = 0; s2 < KS; ++s2) acc = mfma32(ld_x8(plds + (32 * blk + m) * LW + 16 * s2 + 8 * h), xf[s2], acc);
+      if constexpr (FAST) mx_fake_quant16(acc);
       op_t* dst = blk < 4 ? Q : K;
       store_runs16(dst + ((rowh + (blk & 3)) * N + j0 + m) * D, acc, blk < 4 ? qscale : 1.f, h);
     }
     // V^T: D[pos][d]; lane (d m, h) holds keys j0 + 8g + 4h + e in acc[4g + e]
 #pragma unroll 1
     for (int hd = 0; hd < H; ++hd) {
+      if constexpr (FAST) {   // block scale of key j0 + m -> vsc[m]
+        f32x16 at;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 c4 = *reinterpret_cast<const f32x4*>(cb + 2 * C + 32 * hd + 8 * g + 4 * h);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) at[4 * g + e] = c4[e];
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < KS; ++s2)
+          at = mfma32(ld_x8(plds + (2 * C + 32 * hd + m) * LW + 16 * s2 + 8 * h), xf[s2], at);
+        float a = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a = fmaxf(a, fabsf(at[r]));
+        a = xor32_max(a);
+        if (h == 0) vsc[m] = mx_block_scale(a);
+      }
       const float c0 = cb[2 * C + 32 * hd + m];
       f32x16 acc;
 #pragma unroll
@@ -177,6 +203,14 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
 #pragma unroll
       for (int s2 = 0; s2 < KS; ++s2)
         acc = mfma32(xf[s2], ld_x8(plds + (2 * C + 32 * hd + m) * LW + 16 * s2 + 8 * h), acc);
+      if constexpr (FAST) {   // same wave: its LDS accesses complete in order
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 X4 = *reinterpret_cast<const f32x4*>(vsc + 8 * g + 4 * h);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[4 * g + e] = mx_fake_quant1(acc[4 * g + e], X4[e], 448.f * X4[e]);
+        }
+      }
       // keys 8g + 4h + e of runs g = 2p, 2p+1 sit at storage 16p + 8h .. +7 (perm16)
       op_t* row = Vt + ((rowh + hd) * D + m) * (long)N + j0;
 #pragma unroll
@@ -551,6 +585,10 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
 // loads, o * sigmoid(g) is directly the B operand of D[out][position] = W_o . (o * g), and the
 // residual is the z the lane loaded.  Weight rows are 4 op_t longer than their width, so the
 // 8-byte fragment reads of 32 rows fall on distinct banks.
+// FAST (the fast mode's block-fp8 points): the gate's offsets are W_g beta itself, and g
+// (per head: one 32-channel block, a lane pair's 16 + 16 registers) and the projection's
+// output (per 32 output channels) are quantize-dequantized before the sigmoid and before
+// the residual.
 // ---------------------------------------------------------------------------------
 constexpr int TAO_WAVES = 8;
 // LDS: the gate offsets [C] and gamma [CC] (fp32, first: small immediate offsets), then
@@ -561,7 +599,7 @@ constexpr size_t tao_lds() {
 }
 
 // resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
-template <int CC>
+template <int CC, bool FAST>
 __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
     const op_t* __restrict__ O, const float* z_in, float* out, const float* __restrict__ lnw,
     const float* __restrict__ lnb, const op_t* __restrict__ wg, const op_t* __restrict__ wo,
@@ -598,7 +636,7 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[c + e];
     }
-    cgate[row] = -LOG2E * acc;
+    cgate[row] = FAST ? acc : -LOG2E * acc;
   }
   __syncthreads();
   const uint32_t ntiles = (uint32_t)B * N * N / 32;
@@ -629,10 +667,26 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
         const int q = 4 * cb + gg;            // chunk: channels oa_channel(q, h) + 0..3
         const opx4 ov = ov4[q];
         const f32x4 cg = *reinterpret_cast<const f32x4*>(cgate + oa_channel(q, h));
+        if constexpr (FAST) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          og[q >> 1][4 * (q & 1) + e] =
-              (op_t)((float)ov[e] * rcp_fast(1.f + exp2_fast(fmaf(g[4 * gg + e], -LOG2E, cg[e]))));
+          for (int e = 0; e < 4; ++e) g[4 * gg + e] += cg[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            og[q >> 1][4 * (q & 1) + e] =
+                (op_t)((float)ov[e] * rcp_fast(1.f + exp2_fast(fmaf(g[4 * gg + e], -LOG2E, cg[e]))));
+        }
+      }
+      if constexpr (FAST) {
+        mx_fake_quant16(g);
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) {
+          const int q = 4 * cb + gg;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            og[q >> 1][4 * (q & 1) + e] =
+                (op_t)((float)ov4[q][e] * rcp_fast(1.f + exp2_fast(-LOG2E * g[4 * gg + e])));
+        }
       }
     }
 #pragma unroll
@@ -641,6 +695,7 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
       f32x16 acc = zero16();
 #pragma unroll
       for (int s = 0; s < 8; ++s) acc = mfma32(wfrag_oa(wrow, s, h), og[s], acc);   // D[out][position]
+      if constexpr (FAST) mx_fake_quant16(acc);
 #pragma unroll
       for (int gg = 0; gg < 4; ++gg) {
         const int q = 4 * ob + gg;
@@ -716,8 +771,26 @@ int launch_attn(const TaBuffers& t, float* o32, int B, int N, int n_valid, hipSt
   return PF_OK;
 }
 
-template <int CC>
-int triatt_run(const pf_triatt_args* a) {
+// e4m3 bytes q [rows][K] with E8M0 scale bytes s [rows][K / 32] (pf_quantize_mx8) -> op_t
+// values e4m3 * 2^(s - 127), exact in op_t for the weights' range; n % 4 == 0, K % 32 == 0.
+// A scale byte 0 (an all-zero block) gives zeros.
+__global__ void mx8_dequant_kernel(const uint8_t* __restrict__ q, const uint8_t* __restrict__ s,
+                                   op_t* __restrict__ out, long n, int K) {
+  for (long e = 4 * ((long)blockIdx.x * blockDim.x + threadIdx.x); e < n; e += 4l * gridDim.x * blockDim.x) {
+    const int word = *reinterpret_cast<const int*>(q + e);
+    const long row = e / K;
+    const float X = __uint_as_float((uint32_t)s[row * (K / 32) + (e - row * K) / 32] << 23);
+    const auto lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, X, false);
+    const auto hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, X, true);
+    st_x4(out + e, opx4{(op_t)lo[0], (op_t)lo[1], (op_t)hi[0], (op_t)hi[1]});
+  }
+}
+
+// W_q, W_k, W_v, W_g as the kernels read them (op_t [C][CC]).
+struct TaWeights { const op_t *q, *k, *v, *g; };
+
+template <int CC, bool FAST>
+int triatt_run(const pf_triatt_args* a, const TaWeights& w) {
   hipStream_t st = (hipStream_t)a->stream;
   const int B = a->B, N = a->N;
   const int n_valid = a->n_valid ? a->n_valid : N;
@@ -727,22 +800,23 @@ int triatt_run(const pf_triatt_args* a) {
   const int cus = device_cus();
   if (cus <= 0) return pf_fail(PF_E_LAUNCH, "pf_triatt_fwd: cannot query the device");
   {
-    if (const int rc = pf_reserve_lds((const void*)ta_proj_kernel<CC>, tap_lds<CC>(), "ta_proj_kernel")) return rc;
+    const void* fn = (const void*)ta_proj_kernel<CC, FAST>;
+    if (const int rc = pf_reserve_lds(fn, tap_lds<CC, FAST>(), "ta_proj_kernel")) return rc;
     const int grid = (int)min((long)cus, (positions / 32 + TAP_WAVES - 1) / TAP_WAVES);
-    ta_proj_kernel<CC><<<grid, 64 * TAP_WAVES, tap_lds<CC>(), st>>>(
-        a->z_in, a->pair_mask, a->ln_w, a->ln_b, (const op_t*)a->w_q, (const op_t*)a->w_k, (const op_t*)a->w_v,
-        (const op_t*)a->w_bias, t.Q, t.K, t.Vt, t.bias32, t.mask16, B, N, n_valid, a->ending, qscale, a->eps);
+    ta_proj_kernel<CC, FAST><<<grid, 64 * TAP_WAVES, tap_lds<CC, FAST>(), st>>>(
+        a->z_in, a->pair_mask, a->ln_w, a->ln_b, w.q, w.k, w.v, (const op_t*)a->w_bias, t.Q, t.K, t.Vt, t.bias32,
+        t.mask16, B, N, n_valid, a->ending, qscale, a->eps);
     PF_CHECK_LAUNCH("ta_proj_kernel");
   }
   int rc = launch_attn<false>(t, nullptr, B, N, n_valid, st);
   if (rc) return rc;
   {
-    if (const int rc = pf_reserve_lds((const void*)ta_out_kernel<CC>, tao_lds<CC>(), "ta_out_kernel")) return rc;
+    const void* fn = (const void*)ta_out_kernel<CC, FAST>;
+    if (const int rc = pf_reserve_lds(fn, tao_lds<CC>(), "ta_out_kernel")) return rc;
     const int grid = (int)min((long)cus, (positions / 32 + TAO_WAVES - 1) / TAO_WAVES);
     const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);
-    ta_out_kernel<CC><<<grid, 64 * TAO_WAVES, tao_lds<CC>(), st>>>(t.O, a->z_in, a->out, a->ln_w, a->ln_b,
-                                                                  (const op_t*)a->w_g, (const op_t*)a->w_o, B, N,
-                                                                  a->ending, resid, a->eps);
+    ta_out_kernel<CC, FAST><<<grid, 64 * TAO_WAVES, tao_lds<CC>(), st>>>(
+        t.O, a->z_in, a->out, a->ln_w, a->ln_b, w.g, (const op_t*)a->w_o, B, N, a->ending, resid, a->eps);
     PF_CHECK_LAUNCH("ta_out_kernel");
   }
   return PF_OK;
@@ -779,7 +853,50 @@ extern "C" int pf_triatt_fwd(const pf_triatt_args* a) {
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: workspace too small (%zu < %zu bytes)", a->workspace_bytes, need);
   if (a->n_valid < 0 || a->n_valid > a->N)
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: n_valid %d outside [0, N=%d]", a->n_valid, a->N);
-  return a->C == 128 ? triatt_run<128>(a) : triatt_run<64>(a);
+  const TaWeights w = {(const op_t*)a->w_q, (const op_t*)a->w_k, (const op_t*)a->w_v, (const op_t*)a->w_g};
+  return a->C == 128 ? triatt_run<128, false>(a, w) : triatt_run<64, false>(a, w);
+}
+
+// Fast mode: the 16-bit workspace, then W_q, W_k, W_v, W_g dequantized to op_t [4][C][C].
+extern "C" size_t pf_triatt_mx8_workspace_size(int B, int N, int C_, int H_, int D_) {
+  if (B <= 0 || N <= 0 || C_ != 128 || H_ != H || D_ != D) return 0;
+  return ta_buffers_size(B, N) + 4 * (size_t)C * C * sizeof(op_t);
+}
+
+extern "C" int pf_triatt_mx8_fwd(const pf_triatt_mx8_args* m) {
+  if (!m) return pf_fail(PF_E_INVALID, "pf_triatt_mx8_fwd: null args");
+  if (m->C != 128 || m->H != H || m->D != D)
+    return pf_fail(PF_E_INVALID, "pf_triatt_mx8_fwd: only C = 128, H=4, D=32 supported (got C=%d H=%d D=%d)", m->C,
+                   m->H, m->D);
+  if (m->B <= 0 || m->N <= 0 || m->N % 64)
+    return pf_fail(PF_E_INVALID, "pf_triatt_mx8_fwd: need B > 0 and N a positive multiple of 64 (B=%d N=%d)", m->B,
+                   m->N);
+  if ((unsigned long long)m->B * m->N * m->N >= (1ull << 32) || !ta_shape_ok(m->N))
+    return pf_fail(PF_E_INVALID, "pf_triatt_mx8_fwd: need B * N * N < 2^32 and N <= 11584 (B=%d N=%d)", m->B, m->N);
+  if (!m->z_in || !m->out || !m->ln_w || !m->ln_b || !m->w_bias || !m->w_q_q || !m->w_q_s || !m->w_k_q ||
+      !m->w_k_s || !m->w_v_q || !m->w_v_s || !m->w_g_q || !m->w_g_s || !m->w_o || !m->workspace)
+    return pf_fail(PF_E_INVALID, "pf_triatt_mx8_fwd: null pointer argument");
+  const size_t need = pf_triatt_mx8_workspace_size(m->B, m->N, m->C, m->H, m->D);
+  if (m->workspace_bytes < need)
+    return pf_fail(PF_E_INVALID, "pf_triatt_mx8_fwd: workspace too small (%zu < %zu bytes)", m->workspace_bytes, need);
+  if (m->n_valid < 0 || m->n_valid > m->N)
+    return pf_fail(PF_E_INVALID, "pf_triatt_mx8_fwd: n_valid %d outside [0, N=%d]", m->n_valid, m->N);
+  hipStream_t st = (hipStream_t)m->stream;
+  op_t* wd = reinterpret_cast<op_t*>((char*)m->workspace + ta_buffers_size(m->B, m->N));
+  const void* src[4][2] = {{m->w_q_q, m->w_q_s}, {m->w_k_q, m->w_k_s}, {m->w_v_q, m->w_v_s}, {m->w_g_q, m->w_g_s}};
+  for (int i = 0; i < 4; ++i) {
+    mx8_dequant_kernel<<<16, 256, 0, st>>>((const uint8_t*)src[i][0], (const uint8_t*)src[i][1], wd + i * C * C,
+                                          (long)C * C, C);
+    PF_CHECK_LAUNCH("mx8_dequant_kernel");
+  }
+  pf_triatt_args a = {};
+  a.B = m->B; a.N = m->N; a.C = m->C; a.H = m->H; a.D = m->D;
+  a.ending = m->ending; a.accumulate = m->accumulate; a.n_valid = m->n_valid; a.eps = m->eps;
+  a.z_in = m->z_in; a.out = m->out; a.pair_mask = m->pair_mask; a.ln_w = m->ln_w; a.ln_b = m->ln_b;
+  a.w_bias = m->w_bias; a.w_o = m->w_o;
+  a.workspace = m->workspace; a.workspace_bytes = m->workspace_bytes; a.stream = m->stream;
+  const TaWeights w = {wd, wd + C * C, wd + 2 * C * C, wd + 3 * C * C};
+  return triatt_run<128, true>(&a, w);
 }
 
 extern "C" int pf_triatt_attend_workspace(void* workspace, size_t workspace_bytes, int B, int N, int n_valid,

@@ -239,12 +239,16 @@ def _apb_args(s: torch.Tensor, k_in: torch.Tensor, z: torch.Tensor, mask: Option
 def launch_apb(s: torch.Tensor, k_in: torch.Tensor, z: torch.Tensor, mask: Optional[torch.Tensor],
                out: torch.Tensor, w: Mapping[str, torch.Tensor], n_heads: int, ws: torch.Tensor,
                accumulate: bool, eps: float = 1e-5, n_valid: int = 0, variant: str = DEFAULT_VARIANT,
-               part: str = "all") -> None:
+               part: str = "all", fast: bool = False) -> None:
     """AttentionPairBias on the current stream.  ``part``: "all" (pf_apb_fwd), "bias" (only
     the z-dependent pair bias into ``ws``, pf_apb_pair_bias) or "attend" (the rest, reading
-    the bias a previous "bias" call left in ``ws``, pf_apb_attend)."""
+    the bias a previous "bias" call left in ``ws``, pf_apb_attend).  ``fast``: the fast-mode
+    entry points (o * sigmoid(g) in MXFP8 before the output projection)."""
     a = _apb_args(s, k_in, z, mask, out, w, n_heads, ws, accumulate, eps, n_valid)
-    fn = {"all": "pf_apb_fwd", "bias": "pf_apb_pair_bias", "attend": "pf_apb_attend"}[part]
+    if fast:
+        fn = {"all": "pf_apb_fwd_mx8", "bias": "pf_apb_pair_bias", "attend": "pf_apb_attend_mx8"}[part]
+    else:
+        fn = {"all": "pf_apb_fwd", "bias": "pf_apb_pair_bias", "attend": "pf_apb_attend"}[part]
     _lib.check(getattr(_lib.load(variant), fn)(ctypes.byref(a)), fn, variant)
 
 
@@ -370,6 +374,30 @@ def launch_trimul_mx8(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional
     _lib.check(_lib.load(variant).pf_trimul_mx8_fwd(ctypes.byref(a)), "pf_trimul_mx8_fwd", variant)
 
 
+def triatt_mx8_workspace_bytes(B: int, N: int, n_heads: int = 4, head_dim: int = 32,
+                               variant: str = DEFAULT_VARIANT) -> int:
+    return _lib.load(variant).pf_triatt_mx8_workspace_size(B, N, C_Z, n_heads, head_dim)
+
+
+def launch_triatt_mx8(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional[torch.Tensor],
+                      w: Mapping[str, torch.Tensor], ending: bool, ws: torch.Tensor, accumulate: bool,
+                      n_heads: int = 4, head_dim: int = 32, eps: float = 1e-5, n_valid: int = 0,
+                      variant: str = DEFAULT_VARIANT) -> None:
+    """``w``: fp32 LayerNorm params, op-type ``linear.weight`` / ``linear_o.weight`` and
+    ``linear_{q,k,v,g}.weight.q`` / ``.s`` from mx8_weights."""
+    B, N, _, C = z_in.shape
+    a = _lib.TriattMx8Args(
+        B=B, N=N, C=C, H=n_heads, D=head_dim, ending=int(ending), accumulate=int(accumulate), n_valid=n_valid,
+        eps=eps, z_in=_ptr(z_in), out=_ptr(out), pair_mask=_ptr(pair_mask),
+        ln_w=_ptr(w["layer_norm.weight"]), ln_b=_ptr(w["layer_norm.bias"]), w_bias=_ptr(w["linear.weight"]),
+        w_q_q=_ptr(w["linear_q.weight.q"]), w_q_s=_ptr(w["linear_q.weight.s"]),
+        w_k_q=_ptr(w["linear_k.weight.q"]), w_k_s=_ptr(w["linear_k.weight.s"]),
+        w_v_q=_ptr(w["linear_v.weight.q"]), w_v_s=_ptr(w["linear_v.weight.s"]),
+        w_g_q=_ptr(w["linear_g.weight.q"]), w_g_s=_ptr(w["linear_g.weight.s"]), w_o=_ptr(w["linear_o.weight"]),
+        workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
+    _lib.check(_lib.load(variant).pf_triatt_mx8_fwd(ctypes.byref(a)), "pf_triatt_mx8_fwd", variant)
+
+
 def launch_transition_mx8(x_in: torch.Tensor, out: torch.Tensor, w: Mapping[str, torch.Tensor],
                           accumulate: bool, eps: float = 1e-5, variant: str = DEFAULT_VARIANT) -> None:
     C = x_in.shape[-1]
@@ -390,6 +418,9 @@ def launch_trimul_mx8_contract(A8: torch.Tensor, B8: torch.Tensor, SA: torch.Ten
 
 
 TRIMUL_MX8_KEYS = {"p_in.weight": 0, "g_in.weight": 0, "p_out.weight": 0, "g_out.weight": 0}
+#: fast-mode triangle attention: the q/k/v/g projections (the reference's bfloat8_b weights,
+#: ``tenstorrent.py:526-539``); the triangle-bias and output weights stay 16-bit
+TRIATT_MX8_KEYS = {"linear_q.weight": 0, "linear_k.weight": 0, "linear_v.weight": 0, "linear_g.weight": 0}
 TRANSITION_MX8_KEYS = {"fc1.weight": 0, "fc2.weight": 0, "fc3.weight": 1}
 
 
@@ -488,9 +519,10 @@ def transition(x: torch.Tensor, norm_weight, norm_bias, fc1_weight, fc2_weight, 
 
 def attention_pair_bias(s: torch.Tensor, z: torch.Tensor, mask: Optional[torch.Tensor], k_in: torch.Tensor,
                         weights: Mapping[str, torch.Tensor], num_heads: int = 16,
-                        eps: float = 1e-5, variant: str = DEFAULT_VARIANT) -> torch.Tensor:
+                        eps: float = 1e-5, variant: str = DEFAULT_VARIANT, fast: bool = False) -> torch.Tensor:
     """``AttentionPairBias.forward`` (``tt_bio/boltz2.py:343-367``, multiplicity 1).
-    ``weights`` uses the module's state-dict keys (``proj_q.weight`` ...)."""
+    ``weights`` uses the module's state-dict keys (``proj_q.weight`` ...).  ``fast``: the
+    fast-mode entry point (o * sigmoid(g) in MXFP8, ``tt_bio/tenstorrent.py:846``)."""
     dev = _require_gpu(s, z, k_in)
     B, N, c_s = s.shape
     n_pad = padded_len(N)
@@ -504,7 +536,8 @@ def attention_pair_bias(s: torch.Tensor, z: torch.Tensor, mask: Optional[torch.T
     w = convert_weights(weights, dev, variant)
     out = torch.empty_like(sp)
     ws = workspace(apb_workspace_bytes(B, n_pad, c_s, num_heads, variant), dev)
-    launch_apb(sp, kp, zp, mp, out, w, num_heads, ws, accumulate=False, eps=eps, n_valid=N, variant=variant)
+    launch_apb(sp, kp, zp, mp, out, w, num_heads, ws, accumulate=False, eps=eps, n_valid=N, variant=variant,
+               fast=fast)
     return out[:, :N]
 
 

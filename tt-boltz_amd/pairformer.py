@@ -131,8 +131,9 @@ class Module:
 
     ``fast`` is the process-global fast mode at construction time (the reference reads
     it when it builds the modules, ``tenstorrent.py:537-539``): the triangle
-    multiplications and the pair transition then keep MXFP8 weights and run the fp8
-    kernels."""
+    multiplications, the triangle attentions' q/k/v/g projections and the pair transition
+    then keep MXFP8 weights and run the fast-mode kernels, and the single-track attention
+    quantizes its gated output (``tenstorrent.py:846``)."""
 
     def __init__(self, state_dict, options: Optional[Options] = None):
         self.weights = WeightScope.wrap(state_dict)
@@ -206,11 +207,18 @@ class TriangleAttention(Module):
         self.C = self.weights["layer_norm.weight"].shape[0]
         if self.C not in C_Z_SUPPORTED:
             raise NotImplementedError(f"only c_z in {C_Z_SUPPORTED} is supported (got {self.C})")
+        # the fast-mode kernels are built for c_z = 128; the template stack (c_z = 64) stays 16-bit
+        self.fast = self.fast and self.C == C_Z
         self.w = {k: self.vec(k) for k in ("layer_norm.weight", "layer_norm.bias")}
-        self.w.update({k: self.mat(k) for k in ("linear.weight", "linear_q.weight", "linear_k.weight",
-                                                "linear_v.weight", "linear_g.weight", "linear_o.weight")})
+        self.w.update({k: self.mat(k) for k in ("linear.weight", "linear_o.weight")})
+        if self.fast:
+            self.w.update(ops.mx8_weights(self.weights, self.device, ops.TRIATT_MX8_KEYS, self.variant))
+        else:
+            self.w.update({k: self.mat(k) for k in ops.TRIATT_MX8_KEYS})
 
     def workspace_bytes(self, B: int, N: int) -> int:
+        if self.fast:
+            return ops.triatt_mx8_workspace_bytes(B, N, self.n_heads, self.head_dim, self.variant)
         return ops.triatt_workspace_bytes(B, N, self.n_heads, self.head_dim, self.variant, self.C)
 
     def __call__(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
@@ -221,8 +229,9 @@ class TriangleAttention(Module):
             ws = ops.workspace(self.workspace_bytes(B, N), x.device)
         if out is None:
             out = torch.empty_like(x)
-        ops.launch_triatt(x, out, mask, self.w, self.ending, ws, accumulate, self.n_heads, self.head_dim,
-                          self.options.eps, n_valid, self.variant)
+        launch = ops.launch_triatt_mx8 if self.fast else ops.launch_triatt
+        launch(x, out, mask, self.w, self.ending, ws, accumulate, self.n_heads, self.head_dim, self.options.eps,
+               n_valid, self.variant)
         return out
 
 
@@ -303,7 +312,7 @@ class AttentionPairBias(Module):
         if out is None:
             out = torch.empty_like(s)
         ops.launch_apb(s, s if k_in is None else k_in, z, mask, out, self.w, self.n_heads, ws, accumulate,
-                       self.options.eps, n_valid, self.variant, part)
+                       self.options.eps, n_valid, self.variant, part, fast=self.fast)
         return out
 
 
