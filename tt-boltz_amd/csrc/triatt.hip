@@ -389,6 +389,7 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(aV[i]));
   asm volatile("" : "+v"(aK[0]), "+v"(aK[1]), "+v"(aM));
 
+  issue(0, 0, 0);   // the first stage's DMA overlaps the scan below
   // rows whose valid keys are all masked (wave-uniform)
   bool live_l = false;
   {
@@ -409,15 +410,15 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
 
   const int jq0 = jw0 + 32 * qb;   // first query of this wave's block; blocks past N idle
   const bool qvalid = jq0 < N;
-  opx8 qf[2];
+  opx8 qf[2], qn[2];   // this head's Q fragments, the next head's (loaded a step ahead)
   f32x16 o;
   float mh, lsum;
   bool mset;
-  auto q_load = [&](int hd) PF_INLINE {
+  auto q_fetch = [&](int hd) PF_INLINE {
     const int jq = min(jq0, N - 32);
     const op_t* qptr = Q + ((((long)b * N + ip) * H + hd) * N + jq + m) * D + 8 * h;
 #pragma unroll
-    for (int s = 0; s < 2; ++s) qf[s] = ld_x8(qptr + 16 * s);
+    for (int s = 0; s < 2; ++s) qn[s] = ld_x8(qptr + 16 * s);
   };
   auto head_start = [&]() PF_INLINE {
     o = zero16();
@@ -459,8 +460,12 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) sc[4 * g + e] = bv[e];
       }
-#pragma unroll
-      for (int s = 0; s < 2; ++s) sc = mfma32(lds_rd8(aK[s] + STG * TK_STAGE + 2048 * u), qf[s], sc);
+      // every fragment of the tile is read before the first MFMA (one LDS round trip, and the
+      // P.V operands are not behind the rescale branch)
+      const opx8 k0 = lds_rd8(aK[0] + STG * TK_STAGE + 2048 * u), k1 = lds_rd8(aK[1] + STG * TK_STAGE + 2048 * u);
+      const opx8 v0 = lds_rd8(aV[2 * u] + STG * TV_STAGE), v1 = lds_rd8(aV[2 * u + 1] + STG * TV_STAGE);
+      sc = mfma32(k0, qf[0], sc);
+      sc = mfma32(k1, qf[1], sc);
       sc = mfma32(as_x8(ra), as_x8(fb), sc);
       u32x4 pf[2];
       float l = exp_pack(sc, pf);
@@ -484,7 +489,6 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
         set_fb(mnew);
       }
       lsum += l;
-      const opx8 v0 = lds_rd8(aV[2 * u] + STG * TV_STAGE), v1 = lds_rd8(aV[2 * u + 1] + STG * TV_STAGE);
       o = mfma32(v0, as_x8(pf[0]), o);
       o = mfma32(v1, as_x8(pf[1]), o);
     }
@@ -508,14 +512,13 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   };
 
   // Step loop: T steps (T = 4 N / 64, even), one barrier each (the loop-top wait + barrier),
-  // the DMA of the next step into the other stage; at a head's first tile the head's Q is
-  // loaded.  The barrier also tells every wave that the other stage (read in the previous step)
-  // is free.
+  // the DMA of the next step into the other stage; during a head's last step the next head's
+  // Q is loaded (it lands by the next loop-top wait).  The barrier also tells every wave that
+  // the other stage (read in the previous step) is free.
   int kbi = 0, hd = 0;  // step it = hd * nKB + kbi
-  issue(0, 0, 0);
+  if (qvalid && live) q_fetch(0);
   auto one_step = [&](auto stg, int it) PF_INLINE {
     constexpr int STG = decltype(stg)::value;
-    if (kbi == 0 && qvalid && live) q_load(hd);
     __builtin_amdgcn_s_waitcnt(vmcnt_le(0));   // this wave's part of stage STG (and Q) landed ...
     __builtin_amdgcn_s_barrier();              // ... for every wave; stage STG ^ 1 is free
     asm volatile("" ::: "memory");
@@ -524,7 +527,12 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
       issue(STG ^ 1, wrap ? hd + 1 : hd, wrap ? 0 : 64 * (kbi + 1));
     }
     if (qvalid && live) {
-      if (kbi == 0) head_start();
+      if (kbi == 0) {
+        head_start();
+        qf[0] = qn[0];
+        qf[1] = qn[1];
+      }
+      if (kbi == nKB - 1 && hd + 1 < H) q_fetch(hd + 1);   // lands by the next step's wait
       step2(stg);
       if (kbi == nKB - 1) finalize(hd);
     }
