@@ -259,12 +259,12 @@ __global__ __launch_bounds__(64 * TM8C_WAVES, 1) void tm8_contract_kernel(
   const uint8_t* Ap = A + plane * NN;
   const uint8_t* Bp = Bop + plane * NN;
   // scale rows of this lane's fragments: A rows i0 + wm*128 + 32x + m, B rows j0 + wn*64 + 32y + m
-  const uint8_t* sArow[4];
-  const uint8_t* sBrow[2];
+  // (32-bit offsets from SA / SB: fewer registers than pointers)
+  int sArow[4], sBrow[2];
 #pragma unroll
-  for (int x = 0; x < 4; ++x) sArow[x] = SA + (plane * N + min(i0 + wm * 128 + 32 * x + m, N - 1)) * NB;
+  for (int x = 0; x < 4; ++x) sArow[x] = (int)((plane * N + min(i0 + wm * 128 + 32 * x + m, N - 1)) * NB);
 #pragma unroll
-  for (int y = 0; y < 2; ++y) sBrow[y] = SB + (plane * N + min(j0 + wn * 64 + 32 * y + m, N - 1)) * NB;
+  for (int y = 0; y < 2; ++y) sBrow[y] = (int)((plane * N + min(j0 + wn * 64 + 32 * y + m, N - 1)) * NB);
   auto issue = [&](int kt) {
     uint8_t* sa = smem8 + (kt & 1) * 2 * SLAB8;
     uint8_t* sb = sa + SLAB8;
@@ -278,9 +278,9 @@ __global__ __launch_bounds__(64 * TM8C_WAVES, 1) void tm8_contract_kernel(
   int scA[4], scB[2], nscA[4], nscB[2];
   auto load_scales = [&](int kt, int (&a)[4], int (&b)[2]) {
 #pragma unroll
-    for (int x = 0; x < 4; ++x) a[x] = *reinterpret_cast<const int*>(sArow[x] + 4 * kt);
+    for (int x = 0; x < 4; ++x) a[x] = *reinterpret_cast<const int*>(SA + sArow[x] + 4 * kt);
 #pragma unroll
-    for (int y = 0; y < 2; ++y) b[y] = *reinterpret_cast<const int*>(sBrow[y] + 4 * kt);
+    for (int y = 0; y < 2; ++y) b[y] = *reinterpret_cast<const int*>(SB + sBrow[y] + 4 * kt);
   };
   const int swz = slab_swz8(m);
   const int rdA = (wm * 128 + m) * SK, rdB = (wn * 64 + m) * SK;
@@ -319,17 +319,36 @@ __global__ __launch_bounds__(64 * TM8C_WAVES, 1) void tm8_contract_kernel(
       load_scales(kt + 1, nscA, nscB);
     }
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      i32x8 fa[4], fb[2];
-      read_frags(kt, s, fa, fb);
-      const int sh = 8 * (2 * s + h);    // this lane supplies the scale of block 2s + h
+    // k-step 0's fragments, then step 1's reads interleaved with step 0's MFMAs (two reads
+    // after each of the first six), then step 1's MFMAs
+    i32x8 f0a[4], f0b[2], f1a[4], f1b[2];
+    read_frags(kt, 0, f0a, f0b);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(kt, 1, f1a, f1b);
+    {
+      const int sh = 8 * h;
 #pragma unroll
       for (int y = 0; y < 2; ++y)
 #pragma unroll
         for (int x = 0; x < 4; ++x)
-          acc[y][x] = mfma8(fb[y], fa[x], acc[y][x], (scB[y] >> sh) & 0xFF, (scA[x] >> sh) & 0xFF);
+          acc[y][x] = mfma8(f0b[y], f0a[x], acc[y][x], (scB[y] >> sh) & 0xFF, (scA[x] >> sh) & 0xFF);
     }
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      const int sh = 8 * (2 + h);
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+          acc[y][x] = mfma8(f1b[y], f1a[x], acc[y][x], (scB[y] >> sh) & 0xFF, (scA[x] >> sh) & 0xFF);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   OutT* Xp = X + plane * NN;
@@ -623,6 +642,8 @@ extern "C" int pf_trimul_mx8_fwd(const pf_trimul_mx8_args* a) {
       !a->g_in_s || !a->norm_out_w || !a->norm_out_b || !a->p_out_q || !a->p_out_s || !a->g_out_q ||
       !a->g_out_s || !a->workspace)
     return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: null pointer argument");
+  if ((long)a->B * C * a->N * (a->N / 32) >= (1l << 31))   // scale bytes are addressed with 32-bit offsets
+    return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: B * C * N * N / 32 must stay below 2^31 (B=%d N=%d)", a->B, a->N);
   const size_t need = tm8_buffers_size(a->B, a->N);
   if (a->workspace_bytes < need)
     return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: workspace too small (%zu < %zu bytes)", a->workspace_bytes, need);
@@ -663,6 +684,9 @@ extern "C" int pf_trimul_mx8_contract(const void* A8, const void* B8, const void
   if (!A8 || !B8 || !SA || !SB || !X) return pf_fail(PF_E_INVALID, "pf_trimul_mx8_contract: null pointer");
   if (planes <= 0 || N <= 0 || N % 128)
     return pf_fail(PF_E_INVALID, "pf_trimul_mx8_contract: need planes > 0 and N a multiple of 128");
+  if ((long)planes * N * (N / 32) >= (1l << 31))   // scale bytes are addressed with 32-bit offsets
+    return pf_fail(PF_E_INVALID, "pf_trimul_mx8_contract: planes * N * N / 32 must stay below 2^31 (planes=%d N=%d)",
+                   planes, N);
   if (const int rc = pf_reserve_lds((const void*)tm8_contract_kernel<float>, TM8C_LDS, "tm8_contract_kernel"))
     return rc;
   const int tpd = (N + BT - 1) / BT;
