@@ -290,6 +290,13 @@ typedef struct pf_transition_mx8_args {
 
 int pf_transition_mx8_fwd(const pf_transition_mx8_args* args);
 
+/* pf_transition_mx8_fwd with the single-track pair bias of its result fused in, as
+ * pf_transition_pair_bias_fwd does for the 16-bit transition: after writing a pair of out,
+ * the kernel also writes that pair's log2(e)*proj_z(LN(out)) into apb's workspace (the
+ * projection in the operand type, as pf_apb_pair_bias computes it).  t->rows must equal
+ * apb->B * apb->N^2 and be a multiple of 128. */
+int pf_transition_mx8_pair_bias_fwd(const pf_transition_mx8_args* t, const pf_apb_args* apb);
+
 /* Triangle attention in fast mode (same semantics and argument meaning as pf_triatt_fwd,
  * C = 128).  The block-fp8 points are those of the ttnn TriangleAttention under --fast
  * (tt_bio/tenstorrent.py:526-539 weights, 603-614 / 628-639 projections, 580-590 output):

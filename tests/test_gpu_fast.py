@@ -168,6 +168,41 @@ def test_transition_mx8_config4(gpu):
     check("config4 transition N=1024 vs fp32 oracle", out, exact, F32_MAX, F32_MEAN)
 
 
+def test_transition_mx8_fused_pair_bias(gpu):
+    """pf_transition_mx8_pair_bias_fwd: z is bit-identical to pf_transition_mx8_fwd, and the pair
+    bias it writes matches pf_apb_pair_bias on that z (same formula, different summation order
+    and LayerNorm lane layout) and an fp64 proj_z of that z."""
+    import math
+    N, c_s, H = 128, 384, 16
+    w_tr = _sub_w(84, "transition_z")
+    w_apb = _sub_w(85, "attention")
+    s, z, _, _ = synthetic.pair_inputs(N, 86)
+    pairformer.set_fast_mode(True)
+    try:
+        tr = pairformer.Transition(w_tr)
+        apb = pairformer.AttentionPairBias(24, H, w_apb)
+    finally:
+        pairformer.set_fast_mode(False)
+    assert tr.fast and tr.fuses_pair_bias()
+    z1, z2 = z.to(gpu).contiguous(), z.to(gpu).contiguous()
+    s_d = s.to(gpu).contiguous()
+    nb = apb.workspace_bytes(1, N)
+    ws1, ws2 = ops.workspace(nb, gpu), ops.workspace(nb, gpu)
+    tr(z1, out=z1, accumulate=True)
+    apb(s_d, z1, None, out=s_d.clone(), ws=ws1, part="bias")
+    tr(z2, out=z2, accumulate=True, pair_bias=(apb, s_d, ws2))
+    torch.cuda.synchronize()
+    assert torch.equal(z1, z2)
+    off = 5 * N * c_s * 4
+    b1 = ws1[off: off + H * N * N * 4].view(torch.float32).view(H, N, N)
+    b2 = ws2[off: off + H * N * N * 4].view(torch.float32).view(H, N, N)
+    check("fp8 transition fused pair bias vs pf_apb_pair_bias", b2, b1, 1e-2, 1e-3)
+    zn = torch.nn.functional.layer_norm(z2.cpu().double()[0], (128,), w_apb["proj_z.0.weight"].double(),
+                                        w_apb["proj_z.0.bias"].double(), 1e-5)
+    want = torch.einsum("ijc,hc->hij", zn, w_apb["proj_z.1.weight"].double()) * math.log2(math.e)
+    check("fp8 transition fused pair bias vs fp64 proj_z", b2, want, 2e-2, 2e-3)
+
+
 def _mx8_triatt_w(w, gpu):
     """Triangle-attention weights as launch_triatt_mx8 takes them (``mha.`` prefix stripped)."""
     flat = {k[4:] if k.startswith("mha.") else k: v for k, v in w.items()}

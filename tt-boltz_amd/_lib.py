@@ -167,6 +167,7 @@ SIGNATURES = {
     "pf_triatt_mx8_fwd": (c_int, [ctypes.POINTER(TriattMx8Args)]),
     "pf_trimul_mx8_contract": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "pf_transition_mx8_fwd": (c_int, [ctypes.POINTER(TransitionMx8Args)]),
+    "pf_transition_mx8_pair_bias_fwd": (c_int, [ctypes.POINTER(TransitionMx8Args), ctypes.POINTER(ApbArgs)]),
 }
 
 _lock = threading.Lock()

@@ -470,11 +470,12 @@ constexpr int TR8_STAGE = 25600;   // bytes of one ring stage
 PF_DEV int tr8_swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 PF_DEV int tr8_swz4(int r) { return (r >> 2) & 3; }
 
+template <bool ZBIAS>
 __global__ __launch_bounds__(256, 3) void tr8_pair_kernel(
     const float* x_in, float* out, const float* __restrict__ lnw, const float* __restrict__ lnb,
     const uint8_t* __restrict__ w1q, const uint8_t* __restrict__ w1s, const uint8_t* __restrict__ w2q,
     const uint8_t* __restrict__ w2s, const uint8_t* __restrict__ w3q, const uint8_t* __restrict__ w3s,
-    long rows, int hidden, int accumulate, float eps) {
+    long rows, int hidden, int accumulate, float eps, ZBiasArgs zb) {
   __shared__ __attribute__((aligned(16))) uint8_t tl[2 * TR8_STAGE];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -563,23 +564,7 @@ __global__ __launch_bounds__(256, 3) void tr8_pair_kernel(
       acc[ob] = mfma8(wf, hop, acc[ob], st[TR8_S3 + 4 * orow + sb], hsc);   // rows = channel, cols = pair
     }
   }
-  // lane (m, h) owns pair pos0 + m; acc[ob][4g + e] is channel 32 ob + 8 g + 4 h + e.  The
-  // residual (x_in may alias out) is loaded in 16-byte runs, all before the first store.
-  const long p = pos0 + m;
-  if (p < rows) {
-    float* dst = out + p * C;
-    f32x4 res[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q)
-      res[q] = accumulate ? *reinterpret_cast<const f32x4*>(dst + oa_channel(q, h)) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      f32x4 v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = acc[q >> 2][4 * (q & 3) + e] + res[q][e];
-      *reinterpret_cast<f32x4*>(dst + oa_channel(q, h)) = v;
-    }
-  }
+  pair_update_epilogue<ZBIAS>(acc, out, rows, pos0, m, h, accumulate, zb);
 }
 
 // Workspace layout of the fp8 triangle multiplication.
@@ -708,10 +693,36 @@ extern "C" int pf_transition_mx8_fwd(const pf_transition_mx8_args* a) {
     return pf_fail(PF_E_INVALID, "pf_transition_mx8_fwd: null pointer argument");
   const long waves = (a->rows + 31) / 32;
   const int grid = (int)((waves + 3) / 4);
-  tr8_pair_kernel<<<grid, 256, 0, (hipStream_t)a->stream>>>(
+  tr8_pair_kernel<false><<<grid, 256, 0, (hipStream_t)a->stream>>>(
       a->x_in, a->out, a->norm_w, a->norm_b, (const uint8_t*)a->fc1_q, (const uint8_t*)a->fc1_s,
       (const uint8_t*)a->fc2_q, (const uint8_t*)a->fc2_s, (const uint8_t*)a->fc3_q, (const uint8_t*)a->fc3_s,
-      a->rows, a->hidden, a->accumulate, a->eps);
+      a->rows, a->hidden, a->accumulate, a->eps, ZBiasArgs{});
+  PF_CHECK_LAUNCH("tr8_pair_kernel");
+  return PF_OK;
+}
+
+extern "C" int pf_transition_mx8_pair_bias_fwd(const pf_transition_mx8_args* a, const pf_apb_args* apb) {
+  if (!a || !apb) return pf_fail(PF_E_INVALID, "pf_transition_mx8_pair_bias_fwd: null args");
+  if (a->C != C || a->hidden <= 0 || a->hidden % 128)
+    return pf_fail(PF_E_INVALID,
+                   "pf_transition_mx8_pair_bias_fwd: need C = 128 and hidden a multiple of 128 (got %d, %d)", a->C,
+                   a->hidden);
+  if (!a->x_in || !a->out || !a->norm_w || !a->norm_b || !a->fc1_q || !a->fc1_s || !a->fc2_q || !a->fc2_s ||
+      !a->fc3_q || !a->fc3_s)
+    return pf_fail(PF_E_INVALID, "pf_transition_mx8_pair_bias_fwd: null pointer argument");
+  pf_apb_args chk = *apb;
+  chk.z = a->out;   // the bias is computed from the transition's output
+  int rc = pf_apb_check(&chk, "pf_transition_mx8_pair_bias_fwd", true);
+  if (rc) return rc;
+  const long NN = (long)apb->N * apb->N;
+  if (a->rows != (long)apb->B * NN || a->rows % 128)
+    return pf_fail(PF_E_INVALID, "pf_transition_mx8_pair_bias_fwd: rows %ld must equal B*N*N = %ld (a multiple of 128)",
+                   a->rows, (long)apb->B * NN);
+  const ZBiasArgs zb{apb->zln_w, apb->zln_b, (const op_t*)apb->w_z, pf_apb_bias_ptr(apb), NN, apb->H, apb->eps};
+  tr8_pair_kernel<true><<<(unsigned)(a->rows / 128), 256, 0, (hipStream_t)a->stream>>>(
+      a->x_in, a->out, a->norm_w, a->norm_b, (const uint8_t*)a->fc1_q, (const uint8_t*)a->fc1_s,
+      (const uint8_t*)a->fc2_q, (const uint8_t*)a->fc2_s, (const uint8_t*)a->fc3_q, (const uint8_t*)a->fc3_s,
+      a->rows, a->hidden, a->accumulate, a->eps, zb);
   PF_CHECK_LAUNCH("tr8_pair_kernel");
   return PF_OK;
 }

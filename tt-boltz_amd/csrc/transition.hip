@@ -38,14 +38,6 @@ constexpr int TR_BLK = 8192;                 // bytes of one fp16 weight block
 constexpr int TR_STAGE = 3 * TR_BLK;
 PF_DEV int tr_swz4(int r) { return (r >> 2) & 3; }
 
-// Optional epilogue (ZBIAS): the single-track pair bias of the updated pair row,
-// bias[b][hd][i][j] = log2(e) * LN_zb(out[b,i,j,:]) . W_z[hd], from the values the lane
-// has just written (no second pass over z).
-struct ZBiasArgs {
-  const float* lnw; const float* lnb; const op_t* wz; float* bias;
-  long NN; int H; float eps;
-};
-
 template <bool ZBIAS>
 __global__ __launch_bounds__(64 * TRW, 3) void tr_pair_kernel(
     const float* x_in, float* out, const float* __restrict__ lnw, const float* __restrict__ lnb,
@@ -116,86 +108,7 @@ __global__ __launch_bounds__(64 * TRW, 3) void tr_pair_kernel(
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) acc[ob] = mfma32(lds_x8(st + a3[ks] + 2048 * ob), hf[ks], acc[ob]);
   }
-  // lane (m, h) owns pair pos0 + m; acc[ob][4g + e] is channel 32 ob + 8 g + 4 h + e.  The
-  // residual (x_in may alias out) is loaded in 16-byte runs, all before the first store.
-  const long p = pos0 + m;
-  if (!ZBIAS) {
-    if (p < rows) {
-      float* dst = out + p * C;
-      f32x4 res[16];
-#pragma unroll
-      for (int q = 0; q < 16; ++q)
-        res[q] = accumulate ? *reinterpret_cast<const f32x4*>(dst + oa_channel(q, h)) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        f32x4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[q >> 2][4 * (q & 3) + e] + res[q][e];
-        *reinterpret_cast<f32x4*>(dst + oa_channel(q, h)) = v;
-      }
-    }
-    return;
-  }
-  // ZBIAS: whole tiles only (rows is a multiple of 32, checked on the host)
-  float* dst = out + p * C;
-  __builtin_amdgcn_sched_barrier(0);
-  float zv[64];   // residual, then the updated row, in output-aligned order (in place)
-#pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const f32x4 r = accumulate ? *reinterpret_cast<const f32x4*>(dst + oa_channel(q, h)) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) zv[4 * q + e] = r[e];
-  }
-#pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    f32x4 v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      zv[4 * q + e] += acc[q >> 2][4 * (q & 3) + e];
-      v[e] = zv[4 * q + e];
-    }
-    *reinterpret_cast<f32x4*>(dst + oa_channel(q, h)) = v;
-  }
-  opx8 zf[8];
-  {
-    float sm = 0.f;
-#pragma unroll
-    for (int i = 0; i < 64; ++i) sm += zv[i];
-    const float mean = xor32_sum(sm) * (1.f / 128.f);
-    float var = 0.f;
-#pragma unroll
-    for (int i = 0; i < 64; ++i) { const float d = zv[i] - mean; var += d * d; }
-    const float rstd = rsqrtf(xor32_sum(var) * (1.f / 128.f) + zb.eps);
-    // the affine parameters are read 8 channels at a time (the scheduling barrier keeps
-    // their loads from being hoisted together, which would need 128 more registers)
-#pragma unroll
-    for (int q2 = 0; q2 < 8; ++q2) {
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int q = 2 * q2 + u, c0 = oa_channel(q, h);
-        const f32x4 g4 = *reinterpret_cast<const f32x4*>(zb.lnw + c0);
-        const f32x4 b4 = *reinterpret_cast<const f32x4*>(zb.lnb + c0);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) zf[q2][4 * u + e] = (op_t)((zv[4 * q + e] - mean) * rstd * g4[e] + b4[e]);
-      }
-    }
-  }
-  // D[head][pair]: weight row m from global memory (4 KB, cache-resident); lanes m >= H
-  // repeat row H - 1 and their output rows (heads >= H) are not stored
-  __builtin_amdgcn_sched_barrier(0);
-  f32x16 hb = zero16();
-  const op_t* wrow = zb.wz + min(m, zb.H - 1) * C;
-#pragma unroll
-  for (int s2 = 0; s2 < 8; ++s2) hb = mfma32(wfrag_oa(wrow, s2, h), zf[s2], hb);
-  // lane (pair m, h) holds heads acc_row(r, h); the tile's 32 pairs are consecutive (i, j)
-  const long b = pos0 / zb.NN;
-  float* brow = zb.bias + b * zb.H * zb.NN + (pos0 - b * zb.NN) + m;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int hd = acc_row(r, h);
-    if (hd < zb.H) brow[hd * zb.NN] = hb[r] * 1.4426950408889634f;
-  }
+  pair_update_epilogue<ZBIAS>(acc, out, rows, pos0, m, h, accumulate, zb);
 }
 
 // Transition with C = 64, hidden = 256 (the MSA transition, tt_bio/reference.py:1333,

@@ -399,7 +399,9 @@ def launch_triatt_mx8(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional
 
 
 def launch_transition_mx8(x_in: torch.Tensor, out: torch.Tensor, w: Mapping[str, torch.Tensor],
-                          accumulate: bool, eps: float = 1e-5, variant: str = DEFAULT_VARIANT) -> None:
+                          accumulate: bool, eps: float = 1e-5, variant: str = DEFAULT_VARIANT,
+                          pair_bias: Optional[tuple] = None) -> None:
+    """``pair_bias`` as in :func:`launch_transition` (pf_transition_mx8_pair_bias_fwd)."""
     C = x_in.shape[-1]
     a = _lib.TransitionMx8Args(
         rows=x_in.numel() // C, C=C, hidden=w["fc1.weight.q"].shape[0], accumulate=int(accumulate), eps=eps,
@@ -407,7 +409,13 @@ def launch_transition_mx8(x_in: torch.Tensor, out: torch.Tensor, w: Mapping[str,
         fc1_q=_ptr(w["fc1.weight.q"]), fc1_s=_ptr(w["fc1.weight.s"]),
         fc2_q=_ptr(w["fc2.weight.q"]), fc2_s=_ptr(w["fc2.weight.s"]),
         fc3_q=_ptr(w["fc3.weight.q"]), fc3_s=_ptr(w["fc3.weight.s"]), stream=_stream())
-    _lib.check(_lib.load(variant).pf_transition_mx8_fwd(ctypes.byref(a)), "pf_transition_mx8_fwd", variant)
+    if pair_bias is None:
+        _lib.check(_lib.load(variant).pf_transition_mx8_fwd(ctypes.byref(a)), "pf_transition_mx8_fwd", variant)
+        return
+    s, w_apb, n_heads, apb_ws, eps_apb = pair_bias
+    b = _apb_args(s, s, out, None, s, w_apb, n_heads, apb_ws, False, eps_apb, 0)
+    _lib.check(_lib.load(variant).pf_transition_mx8_pair_bias_fwd(ctypes.byref(a), ctypes.byref(b)),
+               "pf_transition_mx8_pair_bias_fwd", variant)
 
 
 def launch_trimul_mx8_contract(A8: torch.Tensor, B8: torch.Tensor, SA: torch.Tensor, SB: torch.Tensor,

@@ -258,7 +258,7 @@ class Transition(Module):
 
     def fuses_pair_bias(self) -> bool:
         """Whether ``__call__`` can also produce the single-track pair bias of its output."""
-        return not self.fast and self.C == C_Z
+        return self.C == C_Z
 
     def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, accumulate: bool = False,
                  ws: Optional[torch.Tensor] = None, pair_bias: Optional[tuple] = None) -> torch.Tensor:
@@ -268,18 +268,16 @@ class Transition(Module):
         rows = x.numel() // self.C
         if out is None:
             out = torch.empty_like(x)
-        if self.fast:
-            if pair_bias is not None:
-                raise ValueError("Transition: the fp8 transition does not fuse the pair bias")
-            ops.launch_transition_mx8(x, out, self.w, accumulate, self.options.eps, self.variant)
-            return out
-        if ws is None:
-            nb = self.workspace_bytes(rows)
-            ws = ops.workspace(nb, x.device) if nb else None
         pb = None
         if pair_bias is not None:
             apb, s, apb_ws = pair_bias
             pb = (s, apb.w, apb.n_heads, apb_ws, apb.options.eps)
+        if self.fast:
+            ops.launch_transition_mx8(x, out, self.w, accumulate, self.options.eps, self.variant, pb)
+            return out
+        if ws is None:
+            nb = self.workspace_bytes(rows)
+            ws = ops.workspace(nb, x.device) if nb else None
         ops.launch_transition(x, out, self.w, ws, accumulate, self.options.eps, self.variant, pb)
         return out
 
