@@ -399,6 +399,7 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   const bool live = __ballot(live_l) != 0;
 
   const uint32_t ONE = half_bits((op_t)1.f);
+  const uint32_t lo_half = h ? 0u : ~0u;   // keeps a value in lanes 0-31, zero in 32-63
   // the rank-1 operands are 4-register tuples whose words 1..3 stay zero: only word 0 changes
   // ([-m, 1] of the block's reference in fb, [1, mask] of the key half in ra), half 1 of the
   // wave holds zero
@@ -451,8 +452,10 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
     constexpr int STG = decltype(stg)::value;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      ra[0] = h ? 0u : (ONE | lds_rd16(aM + STG * TM_STAGE + 64 * u) << 16);
-      asm volatile("" : "+v"(ra));
+      // every lane reads its key's mask entry (an in-bounds address for all lanes; half 1
+      // discards it) together with the tile's other reads: a read inside an h == 0 branch
+      // would get an LDS wait of its own ahead of them
+      const uint32_t mk = lds_rd16(aM + STG * TM_STAGE + 64 * u);
       f32x16 sc;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -466,6 +469,8 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
       const opx8 v0 = lds_rd8(aV[2 * u] + STG * TV_STAGE), v1 = lds_rd8(aV[2 * u + 1] + STG * TV_STAGE);
       sc = mfma32(k0, qf[0], sc);
       sc = mfma32(k1, qf[1], sc);
+      ra[0] = (ONE | mk << 16) & lo_half;
+      asm volatile("" : "+v"(ra));
       sc = mfma32(as_x8(ra), as_x8(fb), sc);
       u32x4 pf[2];
       float l = exp_pack(sc, pf);
