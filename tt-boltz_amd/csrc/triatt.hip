@@ -467,11 +467,15 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
       // P.V operands are not behind the rescale branch)
       const opx8 k0 = lds_rd8(aK[0] + STG * TK_STAGE + 2048 * u), k1 = lds_rd8(aK[1] + STG * TK_STAGE + 2048 * u);
       const opx8 v0 = lds_rd8(aV[2 * u] + STG * TV_STAGE), v1 = lds_rd8(aV[2 * u + 1] + STG * TV_STAGE);
+      // raised issue priority while the wave issues its score MFMAs, so a wave that has its
+      // operands gets the MFMA pipe ahead of the others' exponentials (2-3 % at N = 512)
+      __builtin_amdgcn_s_setprio(2);
       sc = mfma32(k0, qf[0], sc);
       sc = mfma32(k1, qf[1], sc);
       ra[0] = (ONE | mk << 16) & lo_half;
       asm volatile("" : "+v"(ra));
       sc = mfma32(as_x8(ra), as_x8(fb), sc);
+      __builtin_amdgcn_s_setprio(0);
       u32x4 pf[2];
       float l = exp_pack(sc, pf);
       if (__ballot(!mset || l > LSTEP_MAX) != 0) {
