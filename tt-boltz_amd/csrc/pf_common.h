@@ -447,33 +447,6 @@ PF_DEV void load_row_oa(const float* __restrict__ p, int h, float (&x)[CC / 2]) 
     x[4 * q + 0] = a[0]; x[4 * q + 1] = a[1]; x[4 * q + 2] = a[2]; x[4 * q + 3] = a[3];
   }
 }
-PF_DEV void load_row128_oa(const float* __restrict__ p, int h, float (&x)[64]) { load_row_oa<128>(p, h, x); }
-
-// LayerNorm (two-pass fp32) of a CC-channel row held in output-aligned order, as CC/16
-// MFMA B fragments.
-template <int CC>
-PF_DEV void ln_oa_to_frag(const float (&x)[CC / 2], int h, const float* __restrict__ w,
-                          const float* __restrict__ b, float eps, opx8 (&f)[CC / 16]) {
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < CC / 2; ++i) s += x[i];
-  const float mean = xor32_sum(s) * (1.f / CC);
-  float v = 0.f;
-#pragma unroll
-  for (int i = 0; i < CC / 2; ++i) { const float d = x[i] - mean; v += d * d; }
-  const float rstd = rsqrtf(xor32_sum(v) * (1.f / CC) + eps);
-#pragma unroll
-  for (int q = 0; q < CC / 8; ++q) {
-    const int c = oa_channel(q, h);
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      f[q >> 1][4 * (q & 1) + e] = (op_t)((x[4 * q + e] - mean) * rstd * w[c + e] + b[c + e]);
-  }
-}
-PF_DEV void ln128_oa_to_frag(const float (&x)[64], int h, const float* __restrict__ w, const float* __restrict__ b,
-                             float eps, opx8 (&f)[8]) {
-  ln_oa_to_frag<128>(x, h, w, b, eps, f);
-}
 
 // (x - mean) * rstd * gamma[c] of a CC-channel row held in output-aligned order (x[4 q + e] is
 // channel oa_channel(q, h) + e), as CC/16 MFMA B fragments: the LayerNorm without beta, for
@@ -495,24 +468,6 @@ PF_DEV void ln_oa_gamma_to_frag(const float (&x)[CC / 2], int h, const float* ga
 #pragma unroll
     for (int e = 0; e < 4; ++e) f[q >> 1][4 * (q & 1) + e] = (op_t)((x[4 * q + e] - mean) * (rstd * g[e]));
   }
-}
-
-// (x - mean) * rstd of a CC-channel row held in output-aligned order, as CC/16 MFMA B fragments:
-// the LayerNorm without its affine part, for callers that fold gamma / beta into the weights.
-template <int CC>
-PF_DEV void ln_oa_norm_to_frag(const float (&x)[CC / 2], float eps, opx8 (&f)[CC / 16]) {
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < CC / 2; ++i) s += x[i];
-  const float mean = xor32_sum(s) * (1.f / CC);
-  float v = 0.f;
-#pragma unroll
-  for (int i = 0; i < CC / 2; ++i) { const float d = x[i] - mean; v += d * d; }
-  const float rstd = rsqrtf(xor32_sum(v) * (1.f / CC) + eps);
-#pragma unroll
-  for (int q = 0; q < CC / 8; ++q)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) f[q >> 1][4 * (q & 1) + e] = (op_t)((x[4 * q + e] - mean) * rstd);
 }
 
 // Weight fragment (A operand) of weight row `wrow` (128 op_t, contiguous) for K step s in
