@@ -115,6 +115,30 @@ def test_trimul_mx8(gpu, N, direction, pad_tail):
     check(f"trimul {direction} N={N} vs fp32 oracle", out, exact, F32_MAX, F32_MEAN)
 
 
+def test_trimul_mx8_residual_modes(gpu):
+    """The output kernel's three residual modes agree: the plain update (accumulate=False), the
+    in-place update of z (its LN_in row is the residual) and accumulation into a distinct out.
+    One fp32 rounding apart at most (the kernel adds the residual inside one fma)."""
+    N = 128
+    w = _sub_w(72, "tri_mul_out")
+    _, z, _, pm = synthetic.pair_inputs(N, 73, pad_tail=9)
+    zd, pmd, wd = z.to(gpu), pm.to(gpu).contiguous(), _mx8_trimul_w(w, gpu)
+    ws = ops.workspace(ops.trimul_mx8_workspace_bytes(1, N), gpu)
+    upd = torch.empty_like(zd)
+    ops.launch_trimul_mx8(zd, upd, pmd, wd, 0, ws, accumulate=False)
+    inplace = zd.clone()
+    ops.launch_trimul_mx8(inplace, inplace, pmd, wd, 0, ws, accumulate=True)
+    base = torch.randn(zd.shape, generator=torch.Generator().manual_seed(74)).to(gpu)
+    acc = base.clone()
+    ops.launch_trimul_mx8(zd, acc, pmd, wd, 0, ws, accumulate=True)
+    torch.cuda.synchronize()
+    for name, got, want in (("in place", inplace, zd + upd), ("into out", acc, base + upd)):
+        err = (got - want).abs().max().item()
+        print(f"[fast] trimul residual {name}: max difference {err:.2e}", flush=True)
+        assert torch.isfinite(got).all()
+        assert torch.allclose(got, want, rtol=2e-7, atol=1e-6), f"{name}: {err:.2e}"
+
+
 def test_trimul_mx8_config4(gpu):
     """BASELINE config 4 shape: N = 1024, seed 4, z ~ N(0,1), outgoing."""
     cfg = synthetic.CONFIGS[4]

@@ -89,6 +89,47 @@ PF_DEV void ln128_to_x8(const float (&x)[4][16], int h, const float* __restrict_
   }
 }
 
+// The same LayerNorm with gamma and beta staged in LDS as [128] floats each, beta 512 bytes after
+// gamma.  `lane_base` is the LDS byte address of gamma + 64 h (the lane half's first channel),
+// held in one register so that every read is that register plus an immediate offset.
+PF_DEV void ln128_to_x8_lds(const float (&x)[4][16], uint32_t lane_base, float eps, X8& out, int h) {
+  typedef __attribute__((address_space(3))) const f32x4* lds_f4;
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int t = 0; t < 16; ++t) s += x[j][t];
+  const float mean = xor32_sum(s) * (1.f / 128.f);
+  float v = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int t = 0; t < 16; ++t) { const float d = x[j][t] - mean; v += d * d; }
+  const float rstd = rsqrtf(xor32_sum(v) * (1.f / 128.f) + eps);
+  i32x4 q[4];
+  int byte[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float y[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 w = *(lds_f4)(uintptr_t)(lane_base + 4 * (32 * j + 4 * g));
+      const f32x4 b = *(lds_f4)(uintptr_t)(lane_base + 512 + 4 * (32 * j + 4 * g));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[4 * g + e] = (x[j][4 * g + e] - mean) * rstd * w[e] + b[e];
+    }
+    q[j] = quantize16(y, byte[j]);
+  }
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    out.q[s2] = cat_i32x4(q[2 * s2], q[2 * s2 + 1]);
+    out.sc[s2] = h ? byte[2 * s2 + 1] : byte[2 * s2];
+  }
+}
+PF_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)p;
+}
+
 // Weight fragment (MFMA operand) of row `row` of an fp8 [rows][128] matrix staged in LDS
 // with pitch WROW, K step s, plus its scale byte (scales staged as [rows][4]).
 PF_DEV i32x8 wfrag128(const uint8_t* lds, int row, int s, int h) {
@@ -141,11 +182,14 @@ __global__ void mx8_quantize_kernel(const float* __restrict__ x, uint8_t* __rest
 // one operand-plane row; p_in / g_in ([256][128] fp8 each) resident in LDS.  The
 // projection is computed as D[position][channel], so a lane holds one channel for 16
 // of the 32 positions and the partner lane the other 16: the MX block of the
-// contraction (32 consecutive k = positions) is reduced with one exchange.
+// contraction (32 consecutive k = positions) is reduced with one exchange.  The LayerNorm's
+// gamma / beta sit in LDS after the weights; the next tile's z rows (and mask entry) are
+// loaded while a tile is computed; MASKED = false skips the mask.
 //   A8/B8 planes [B][128][N][N] e4m3, scales SA/SB [B][128][N][N/32] E8M0.
 // ---------------------------------------------------------------------------------
-constexpr size_t TM8P_LDS = 2 * 256 * WROW + 2 * 256 * 4;
+constexpr size_t TM8P_LDS = 2 * 256 * WROW + 2 * 256 * 4 + 2 * C * 4;   // + LayerNorm gamma, beta
 
+template <bool MASKED>
 __global__ __launch_bounds__(256, 2) void tm8_proj_kernel(
     const float* __restrict__ z, const float* __restrict__ mask, const float* __restrict__ lnw,
     const float* __restrict__ lnb, const uint8_t* __restrict__ wp_q, const uint8_t* __restrict__ wp_s,
@@ -157,37 +201,68 @@ __global__ __launch_bounds__(256, 2) void tm8_proj_kernel(
   uint8_t* lg = lp + 256 * WROW;
   uint8_t* lps = lg + 256 * WROW;
   uint8_t* lgs = lps + 256 * 4;
+  float* lnp = reinterpret_cast<float*>(lgs + 256 * 4);   // gamma [128], beta [128]
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   stage_w128(wp_q, wp_s, 256, lp, lps, tid, 256);
   stage_w128(wg_q, wg_s, 256, lg, lgs, tid, 256);
+  if (tid < C) {
+    lnp[tid] = lnw[tid];
+    lnp[C + tid] = lnb[tid];
+  }
   __syncthreads();
 
-  const long NN = (long)N * N;
+  uint32_t ln_a = lds_addr(lnp) + 64 * h;   // gamma of this lane half's first channel
+  asm volatile("" : "+v"(ln_a));
   const uint32_t ntiles = (uint32_t)B * N * N / 32;
+  const uint32_t stride = gridDim.x * 4;
   const int NB = N / 32;
-  for (uint32_t tile = blockIdx.x * 4 + wid; tile < ntiles; tile += gridDim.x * 4) {
-    // keep the LayerNorm parameters out of registers across iterations (they are re-read
-    // from cache each tile instead of pinning 128 VGPRs)
+  auto zpair = [&](uint32_t tile) -> long {
+    const PosTile pt = pos_tile(tile, N);
+    const int zi = incoming ? pt.c0 + m : pt.r;
+    const int zj = incoming ? pt.r : pt.c0 + m;
+    return ((long)pt.b * N + zi) * N + zj;
+  };
+  // the next tile's z row (and mask entry) are loaded while this tile is computed
+  float xn[4][16];
+  float mn = 1.f;
+  uint32_t tile = blockIdx.x * 4 + wid;
+  if (tile < ntiles) {
+    const long pair = zpair(tile);
+    load_row128_x8order(z + pair * C, h, xn);
+    if (MASKED) mn = mask[pair];
+  }
+  for (; tile < ntiles; tile += stride) {
+    // the LayerNorm parameters are re-read from LDS each tile instead of pinning 128 VGPRs
     asm volatile("" ::: "memory");
     const PosTile pt = pos_tile(tile, N);
     const int b = pt.b, orow = pt.r, ocol0 = pt.c0;
-    const int zi = incoming ? ocol0 + m : orow;
-    const int zj = incoming ? orow : ocol0 + m;
-    const long pair = ((long)b * N + zi) * N + zj;
     X8 xq;
+    float mr[16];
     {
       float x[4][16];
-      load_row128_x8order(z + pair * C, h, x);
-      ln128_to_x8(x, h, lnw, lnb, eps, xq);
-    }
-    const float maskv = mask ? mask[pair] : 1.f;
-    float mr[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mr[r] = __shfl(maskv, acc_row(r, h));
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int t = 0; t < 16; ++t) x[j][t] = xn[j][t];
+      const float maskv = mn;
+      if (tile + stride < ntiles) {
+        const long pair2 = zpair(tile + stride);
+        load_row128_x8order(z + pair2 * C, h, xn);
+        if (MASKED) mn = mask[pair2];
+      }
+      ln128_to_x8_lds(x, ln_a, eps, xq, h);
+      if (MASKED) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mr[r] = __shfl(maskv, acc_row(r, h));
+      }
+    }
 
-#pragma unroll 1
+    // unrolled, so that the next tile's wait for its prefetched rows can count the stores issued
+    // after them; the empty asm keeps each block's LDS reads in its own block
+#pragma unroll
     for (int cb = 0; cb < 8; ++cb) {
+      asm volatile("" ::: "memory");
       const int row = 32 * cb + m;   // weight row = output unit of this lane's column
       f32x16 P = zero16(), G = zero16();
 #pragma unroll
@@ -197,7 +272,10 @@ __global__ __launch_bounds__(256, 2) void tm8_proj_kernel(
       }
       float v[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) v[r] = P[r] * sigmoidf_fast(G[r]) * mr[r];
+      for (int r = 0; r < 16; ++r) {
+        v[r] = P[r] * sigmoidf_fast(G[r]);
+        if (MASKED) v[r] *= mr[r];
+      }
       int byte;
       const i32x4 q = quantize16(v, byte);
       const int ch = 32 * (cb & 3) + m;
@@ -376,20 +454,39 @@ __global__ __launch_bounds__(64 * TM8C_WAVES, 1) void tm8_contract_kernel(
 
 // ---------------------------------------------------------------------------------
 // Triangle multiplication output: z[i,j,:] (+)= p_out(q(LN_out(X))) * sigmoid(g_out(q(LN_in(z)))).
-// A workgroup takes 128 consecutive pairs (i, j0..j0+127) per step: the X slice
-// X[b][0..127][i][j0..j0+127] (32 KB, 256-byte rows) comes in with 16-byte loads and is
-// read back from LDS channel by channel; wave w owns pairs j0 + 32w .. j0 + 32w + 31.
-// p_out/g_out ([128][128] fp8) stay in LDS.
+// Persistent; a workgroup takes 128 consecutive pairs (i, j0..j0+127) per step: the X slice
+// X[b][0..127][i][j0..j0+127] (32 KB, 256-byte rows) is loaded a step ahead into registers
+// (16-byte loads), written to LDS and read back channel by channel; wave w owns pairs
+// j0 + 32w .. j0 + 32w + 31.  p_out/g_out ([128][128] fp8, rows half-major) and both
+// LayerNorms' parameters stay in LDS.  The projections run as D[channel][pair], so a lane
+// half holds 16 consecutive output channels of its pair: the z row it loaded for LN_in is the
+// residual and every store is a 64-byte run.
 // ---------------------------------------------------------------------------------
 constexpr int XP = 136;        // LDS pitch (halves) of one channel row of the X slice
-constexpr size_t TM8O_LDS = 2 * 128 * WROW + 2 * 128 * 4 + (size_t)C * XP * 2;
+constexpr size_t TM8O_LDS = 2 * 128 * WROW + 2 * 128 * 4 + (size_t)C * XP * 2 + 4 * C * 4;
 
-template <typename XT>
+// Stage an fp8 [128][128] matrix (and its [128][4] scales) from global to LDS with the rows
+// of each 32-row block permuted: LDS row 32 o + 8 q + 4 h + e holds row 32 o + 16 h + 4 q + e.
+// A 32x32 MFMA with these rows as its A operand then leaves, in lane half h, register r, the
+// output channel 32 o + 16 h + r: a lane half owns 16 consecutive channels per block.
+PF_DEV int half_major_row(int R) { return (R & ~31) + 16 * ((R >> 2) & 1) + 4 * ((R >> 3) & 3) + (R & 3); }
+PF_DEV void stage_w128_half_major(const uint8_t* __restrict__ q, const uint8_t* __restrict__ sc, uint8_t* lq,
+                                  uint8_t* ls, int tid, int nthreads) {
+  for (int c = tid; c < 128 * 8; c += nthreads)
+    *reinterpret_cast<i32x4*>(lq + (c >> 3) * WROW + (c & 7) * 16) =
+        *reinterpret_cast<const i32x4*>(q + half_major_row(c >> 3) * 128 + (c & 7) * 16);
+  for (int c = tid; c < 128; c += nthreads)
+    *reinterpret_cast<int*>(ls + 4 * c) = *reinterpret_cast<const int*>(sc + 4 * half_major_row(c));
+}
+
+// RESID: 0 = no residual (out = update), 1 = out is z_in (the LN_in row is the residual),
+// 2 = out += update (out distinct from z_in)
+template <typename XT, int RESID>
 __global__ __launch_bounds__(256, 2) void tm8_out_kernel(
     const XT* __restrict__ X, float x_scale, const float* z_in, float* out, const float* __restrict__ lni_w,
     const float* __restrict__ lni_b, const float* __restrict__ lno_w, const float* __restrict__ lno_b,
     const uint8_t* __restrict__ wp_q, const uint8_t* __restrict__ wp_s, const uint8_t* __restrict__ wg_q,
-    const uint8_t* __restrict__ wg_s, int B, int N, int accumulate, float eps) {
+    const uint8_t* __restrict__ wg_s, int B, int N, float eps) {
   static_assert(sizeof(XT) == 2, "X slice staging assumes 16-bit X");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
   uint8_t* lp = lds8;
@@ -397,31 +494,57 @@ __global__ __launch_bounds__(256, 2) void tm8_out_kernel(
   uint8_t* lps = lg + 128 * WROW;
   uint8_t* lgs = lps + 128 * 4;
   XT* lx = reinterpret_cast<XT*>(lgs + 128 * 4);
+  float* lnp = reinterpret_cast<float*>(lx + C * XP);   // LN_out gamma, beta, LN_in gamma, beta
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
-  stage_w128(wp_q, wp_s, 128, lp, lps, tid, 256);
-  stage_w128(wg_q, wg_s, 128, lg, lgs, tid, 256);
+  stage_w128_half_major(wp_q, wp_s, lp, lps, tid, 256);
+  stage_w128_half_major(wg_q, wg_s, lg, lgs, tid, 256);
+  if (tid < C) {
+    lnp[tid] = lno_w[tid];
+    lnp[C + tid] = lno_b[tid];
+    lnp[2 * C + tid] = lni_w[tid];
+    lnp[3 * C + tid] = lni_b[tid];
+  }
+  uint32_t ln_o = lds_addr(lnp) + 64 * h, ln_i = ln_o + 1024;   // LN_out / LN_in gamma of this half
+  asm volatile("" : "+v"(ln_o), "+v"(ln_i));
 
   const long NN = (long)N * N;
   const long nsteps = (long)B * NN / 128;
-  for (long step = blockIdx.x; step < nsteps; step += gridDim.x) {
-    asm volatile("" ::: "memory");             // LayerNorm parameters are re-read, not pinned
-    const long pair0 = step * 128;               // first pair of the step (same b and i)
-    const int b = (int)(pair0 / NN);
-    const long t0 = pair0 - (long)b * NN;
-    const int i = (int)(t0 / N);
-    const int j0 = (int)(t0 - (long)i * N);
+  // X slice of a step: thread tid moves chunks tid + 256 q (channel c >> 4, 8 pairs at (c & 15) * 8)
+  auto x_src = [&](long step) -> const XT* {
+    const long pair0 = step * 128;
+    const long b = pair0 / NN;
+    return X + b * C * NN + (pair0 - b * NN);
+  };
+  opx8 xr[8];   // the next step's X chunks, in flight during this step
+  long step = blockIdx.x;
+  if (step < nsteps) {
+    const XT* src = x_src(step);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int c = tid + 256 * q;
+      xr[q] = *reinterpret_cast<const opx8*>(src + (long)(c >> 4) * NN + (c & 15) * 8);
+    }
+  }
+  for (; step < nsteps; step += gridDim.x) {
+    asm volatile("" ::: "memory");               // LayerNorm parameters are re-read, not pinned
+    const long pos0 = step * 128 + 32 * wid;     // this wave's 32 pairs
+    float zr[4][16];                             // LN_in input and (resid 1) the residual
+    load_row128_x8order(z_in + (pos0 + m) * C, h, zr);
     __syncthreads();                             // previous step's readers are done
-    {
-      const XT* src = X + (long)b * C * NN + (long)i * N + j0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int c = tid + 256 * q;
+      *reinterpret_cast<opx8*>(lx + (c >> 4) * XP + (c & 15) * 8) = xr[q];
+    }
+    if (step + gridDim.x < nsteps) {             // issued after the z row: its wait does not cover these
+      const XT* src = x_src(step + gridDim.x);
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const int c = tid + 256 * q;             // 2048 chunks of 8 halves: channel c >> 4
-        const int ch = c >> 4, col = (c & 15) * 8;
-        *reinterpret_cast<opx8*>(lx + ch * XP + col) = *reinterpret_cast<const opx8*>(src + (long)ch * NN + col);
+        const int c = tid + 256 * q;
+        xr[q] = *reinterpret_cast<const opx8*>(src + (long)(c >> 4) * NN + (c & 15) * 8);
       }
     }
     __syncthreads();
-    const long pos0 = pair0 + 32 * wid;          // this wave's 32 pairs
     X8 xo, xi;
     {
       float x[4][16];
@@ -429,26 +552,36 @@ __global__ __launch_bounds__(256, 2) void tm8_out_kernel(
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int tt = 0; tt < 16; ++tt) x[j][tt] = (float)lx[(32 * j + 16 * h + tt) * XP + 32 * wid + m] * x_scale;
-      ln128_to_x8(x, h, lno_w, lno_b, eps, xo);
-      load_row128_x8order(z_in + (pos0 + m) * C, h, x);
-      ln128_to_x8(x, h, lni_w, lni_b, eps, xi);
+      ln128_to_x8_lds(x, ln_o, eps, xo, h);
     }
-#pragma unroll 1
+    ln128_to_x8_lds(zr, ln_i, eps, xi, h);
+    // D[channel][pair] with half-major weight rows: lane (pair m, half h) holds channels
+    // 32 ob + 16 h + r, 64 contiguous bytes of its output row, the same channels as zr[ob]
+    float* orow = out + (pos0 + m) * C + 16 * h;
+#pragma unroll
     for (int ob = 0; ob < 4; ++ob) {
+      asm volatile("" ::: "memory");   // keeps each block's LDS fragment reads in its block
       const int row = 32 * ob + m;
       f32x16 P = zero16(), G = zero16();
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        P = mfma8(xo.q[s], wfrag128(lp, row, s, h), P, xo.sc[s], lps[4 * row + 2 * s + h]);
-        G = mfma8(xi.q[s], wfrag128(lg, row, s, h), G, xi.sc[s], lgs[4 * row + 2 * s + h]);
+        P = mfma8(wfrag128(lp, row, s, h), xo.q[s], P, lps[4 * row + 2 * s + h], xo.sc[s]);
+        G = mfma8(wfrag128(lg, row, s, h), xi.q[s], G, lgs[4 * row + 2 * s + h], xi.sc[s]);
       }
-      // residuals first (all loads ahead of the stores, so they overlap)
-      float res[16];
+      f32x4 res[4];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) res[r] = accumulate ? out[(pos0 + acc_row(r, h)) * C + 32 * ob + m] : 0.f;
+      for (int q = 0; q < 4; ++q) {
+        if (RESID == 2) res[q] = *reinterpret_cast<const f32x4*>(orow + 32 * ob + 4 * q);
+        else if (RESID == 1) res[q] = f32x4{zr[ob][4 * q], zr[ob][4 * q + 1], zr[ob][4 * q + 2], zr[ob][4 * q + 3]};
+        else res[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        out[(pos0 + acc_row(r, h)) * C + 32 * ob + m] = P[r] * sigmoidf_fast(G[r]) + res[r];
+      for (int q = 0; q < 4; ++q) {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = P[4 * q + e] * sigmoidf_fast(G[4 * q + e]) + res[q][e];
+        *reinterpret_cast<f32x4*>(orow + 32 * ob + 4 * q) = v;
+      }
     }
   }
 }
@@ -633,33 +766,41 @@ extern "C" int pf_trimul_mx8_fwd(const pf_trimul_mx8_args* a) {
   if (a->workspace_bytes < need)
     return pf_fail(PF_E_INVALID, "pf_trimul_mx8_fwd: workspace too small (%zu < %zu bytes)", a->workspace_bytes, need);
   {
-    int rc = pf_reserve_lds((const void*)tm8_proj_kernel, TM8P_LDS, "tm8_proj_kernel");
+    int rc = pf_reserve_lds((const void*)tm8_proj_kernel<true>, TM8P_LDS, "tm8_proj_kernel");
+    if (rc == PF_OK) rc = pf_reserve_lds((const void*)tm8_proj_kernel<false>, TM8P_LDS, "tm8_proj_kernel");
     if (rc == PF_OK) rc = pf_reserve_lds((const void*)tm8_contract_kernel<op_t>, TM8C_LDS, "tm8_contract_kernel");
-    if (rc == PF_OK) rc = pf_reserve_lds((const void*)tm8_out_kernel<op_t>, TM8O_LDS, "tm8_out_kernel");
+    if (rc == PF_OK) rc = pf_reserve_lds((const void*)tm8_out_kernel<op_t, 0>, TM8O_LDS, "tm8_out_kernel");
+    if (rc == PF_OK) rc = pf_reserve_lds((const void*)tm8_out_kernel<op_t, 1>, TM8O_LDS, "tm8_out_kernel");
+    if (rc == PF_OK) rc = pf_reserve_lds((const void*)tm8_out_kernel<op_t, 2>, TM8O_LDS, "tm8_out_kernel");
     if (rc != PF_OK) return rc;
   }
   hipStream_t st = (hipStream_t)a->stream;
   const int B = a->B, N = a->N;
   Tm8Buffers t = tm8_buffers(a->workspace, B, N);
   const long ntiles = (long)B * N * N / 32;
+  const int cus = device_cus();
+  if (cus <= 0) return pf_fail(PF_E_LAUNCH, "pf_trimul_mx8_fwd: cannot query the device");
+  // up to 2048 workgroups (several rounds per CU): a persistent grid of two per CU projects
+  // as fast but leaves the planes in an order the contraction reads 6 % slower
   const int grid = tile_grid(ntiles);
   // the A plane (channels 0..127 of the projection) holds a, the B plane b; the
   // 2C-row p_in / g_in matrices are [a rows ; b rows]
-  tm8_proj_kernel<<<grid, 256, TM8P_LDS, st>>>(a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b,
-                                               (const uint8_t*)a->p_in_q, (const uint8_t*)a->p_in_s,
-                                               (const uint8_t*)a->g_in_q, (const uint8_t*)a->g_in_s, t.A8, t.B8,
-                                               t.SA, t.SB, B, N, a->direction, a->eps);
+  (a->pair_mask ? tm8_proj_kernel<true> : tm8_proj_kernel<false>)<<<grid, 256, TM8P_LDS, st>>>(
+      a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b, (const uint8_t*)a->p_in_q, (const uint8_t*)a->p_in_s,
+      (const uint8_t*)a->g_in_q, (const uint8_t*)a->g_in_s, t.A8, t.B8, t.SA, t.SB, B, N, a->direction, a->eps);
   PF_CHECK_LAUNCH("tm8_proj_kernel");
   const int tpd = (N + BT - 1) / BT;
   const int total = B * C * tpd * tpd;
   tm8_contract_kernel<op_t><<<total, 64 * TM8C_WAVES, TM8C_LDS, st>>>(t.A8, t.B8, t.SA, t.SB, t.X, N, tpd, total, X_STORE_SCALE);
   PF_CHECK_LAUNCH("tm8_contract_kernel");
   const long nsteps = (long)B * N * N / 128;
-  tm8_out_kernel<op_t><<<(int)(nsteps < 2048 ? nsteps : 2048), 256, TM8O_LDS, st>>>(t.X, X_LOAD_SCALE, a->z_in, a->out, a->norm_in_w,
-                                                    a->norm_in_b, a->norm_out_w, a->norm_out_b,
-                                                    (const uint8_t*)a->p_out_q, (const uint8_t*)a->p_out_s,
-                                                    (const uint8_t*)a->g_out_q, (const uint8_t*)a->g_out_s, B, N,
-                                                    a->accumulate, a->eps);
+  // persistent: two 4-wave workgroups per CU, each staging the weights once
+  const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);
+  auto out_kern = resid == 0 ? tm8_out_kernel<op_t, 0> : resid == 1 ? tm8_out_kernel<op_t, 1> : tm8_out_kernel<op_t, 2>;
+  out_kern<<<(int)min((long)2 * cus, nsteps), 256, TM8O_LDS, st>>>(
+      t.X, X_LOAD_SCALE, a->z_in, a->out, a->norm_in_w, a->norm_in_b, a->norm_out_w, a->norm_out_b,
+      (const uint8_t*)a->p_out_q, (const uint8_t*)a->p_out_s, (const uint8_t*)a->g_out_q, (const uint8_t*)a->g_out_s,
+      B, N, a->eps);
   PF_CHECK_LAUNCH("tm8_out_kernel");
   return PF_OK;
 }
