@@ -283,6 +283,27 @@ def test_module_noseq_affinity_masks(gpu):
     check("module no-seq affinity z", z_got, z_ref)
 
 
+def test_module_out_of_memory_raises(gpu):
+    """A request beyond the device's memory surfaces as a RuntimeError containing "out of
+    memory", the text boltz2.py:5584-5591 catches to skip a batch.  z is a stride-0 view of a
+    512 GiB pair tensor (512 real bytes), so the module's padded device copy cannot be
+    allocated and nothing runs; the module works normally afterwards."""
+    w = synthetic.stack_weights(1, 26, transform_s=False)
+    mod = pairformer.PairformerModule(1, 32, 4, None, None, False)
+    mod.load_state_dict(w)
+    N = 32768
+    huge = torch.zeros((1, 1, 1, 128), device=gpu).expand(1, N, N, 128)
+    with pytest.raises(RuntimeError, match="out of memory"):
+        mod(None, huge)
+    del huge
+    torch.cuda.empty_cache()
+    _, z, _, pm = _inputs(64, 27)
+    _, z_ref = ref.pairformer_stack(None, z, None, pm, w, 1)
+    mod.reset_static_cache()
+    _, z_got = mod(None, z.to(gpu))
+    check("module after an out-of-memory error z", z_got, z_ref)
+
+
 def test_recycler(gpu):
     N = 64
     w = synthetic.stack_weights(1, 26)
