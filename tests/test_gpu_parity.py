@@ -740,6 +740,23 @@ def test_layer_n768(gpu):
     check("layer N=768 s", s_got, s_ref)
 
 
+def test_layer_config1_bf16_operands(gpu):
+    """The bf16-operand library (the metric's dtype) on one full PairformerLayer at the
+    config 1/2 shape: N = 512 with the last 51 tokens masked, against the fp32 oracle evaluated
+    on the device.  Bar as for config 0 with bf16 operands: max 5e-2 / mean 6e-3 of the rms."""
+    cfg = synthetic.CONFIGS[1]
+    N = cfg["N"]
+    w = synthetic.stack_weights(1, cfg["seed"])
+    s, z, mask, pm = synthetic.pair_inputs(N, cfg["seed"], pad_tail=cfg["pad_tail"])
+    wd = {k: v.to(gpu) for k, v in ref.sub(w, "layers.0").items()}
+    s_ref, z_ref = ref.pairformer_layer(s.to(gpu), z.to(gpu), mask.to(gpu), pm.to(gpu), wd, ref.chunk_size_for(N))
+    mod = pairformer.PairformerModule(1, 32, 4, 24, 16, True, options=pairformer.Options(operand="bf16"))
+    mod.load_state_dict(w)
+    s_got, z_got = mod(s.to(gpu), z.to(gpu), mask.to(gpu), pm.to(gpu))
+    check("config1 layer z (bf16 operands, 51 masked tokens)", z_got, z_ref, 5e-2, 6e-3)
+    check("config1 layer s (bf16 operands, 51 masked tokens)", s_got, s_ref, 5e-2, 6e-3)
+
+
 # ------------------------------------------------------------------------------ boundary regressions
 def test_module_mask_cache_tracks_n(gpu):
     """N = 100 and then N = 120 without reset_static_cache(): both pad to 128, so the cached
