@@ -342,22 +342,24 @@ def test_recycler_msa(gpu):
 
 def test_single_track_overlap_identical(gpu):
     """The single track on a second stream (overlapped with the next layer's pair
-    operations) gives bit-identical s and z to the same stack run in reference order on
-    one stream: same kernels, same inputs, only the schedule differs."""
+    operations, started after 0, 1, 2 or 4 of them) gives bit-identical s and z to the same
+    stack run in reference order on one stream: same kernels, same inputs, only the schedule
+    differs."""
     N, n_blocks = 128, 3
     w = synthetic.stack_weights(n_blocks, 31)
     s, z, mask, pm = _inputs(N, 32)
     out = {}
-    for overlap in (False, True):
-        pf = pairformer.Pairformer(n_blocks, 32, 4, 24, 16, True, w,
-                                   options=pairformer.Options(overlap_single=overlap))
+    for key, opts in (("serial", pairformer.Options(overlap_single=False)),
+                      *((d, pairformer.Options(single_delay=d)) for d in (0, 1, 2, 4))):
+        pf = pairformer.Pairformer(n_blocks, 32, 4, 24, 16, True, w, options=opts)
         s_d, z_d = s.to(gpu).contiguous(), z.to(gpu).contiguous()
-        out[overlap] = pf(s_d, z_d, pm.to(gpu), mask.to(gpu))
+        out[key] = pf(s_d, z_d, pm.to(gpu), mask.to(gpu))
         torch.cuda.synchronize()
-    assert torch.equal(out[True][0], out[False][0]) and torch.equal(out[True][1], out[False][1])
+    for d in (0, 1, 2, 4):
+        assert torch.equal(out[d][0], out["serial"][0]) and torch.equal(out[d][1], out["serial"][1]), d
     s_ref, z_ref = ref.pairformer_stack(s, z, mask, pm, w, n_blocks)
-    check("overlapped 3-layer stack z", out[True][1], z_ref)
-    check("overlapped 3-layer stack s", out[True][0], s_ref)
+    check("overlapped 3-layer stack z", out[1][1], z_ref)
+    check("overlapped 3-layer stack s", out[1][0], s_ref)
 
 
 def test_transition_fused_pair_bias(gpu):

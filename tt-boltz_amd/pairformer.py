@@ -116,14 +116,22 @@ class Options:
 
     ``operand``: MFMA operand type, ``"fp16"`` (default) or ``"bf16"``.
     ``overlap_single``: run each layer's single-track update on a second stream, overlapped
-    with the next layer's pair operations (results are identical; default on)."""
+    with the next layer's pair operations (results are identical; default on).
+    ``single_delay``: how many of the next layer's pair operations (0-4) go ahead of the
+    overlapped single track (it then starts beside the following ones).  The default 1 keeps it
+    off the outgoing triangle multiplication, whose contraction it slows the most (N = 512:
+    1.254 vs 1.263 ms per layer with 0; 1.269 with 2, 1.308 with 4)."""
 
-    def __init__(self, eps: float = 1e-5, operand: str = ops.DEFAULT_VARIANT, overlap_single: bool = True):
+    def __init__(self, eps: float = 1e-5, operand: str = ops.DEFAULT_VARIANT, overlap_single: bool = True,
+                 single_delay: int = 1):
         if operand not in ops.TORCH_DTYPE:
             raise ValueError(f"operand must be one of {sorted(ops.TORCH_DTYPE)}, got {operand!r}")
+        if not 0 <= single_delay <= 4:
+            raise ValueError(f"single_delay must be in 0..4, got {single_delay}")
         self.eps = eps
         self.operand = operand
         self.overlap_single = overlap_single
+        self.single_delay = single_delay
 
 
 class Module:
@@ -325,12 +333,21 @@ class SingleTrackStream:
     the previous single track on the caller's stream.
     """
 
-    def __init__(self, nbytes: int, device: torch.device):
+    def __init__(self, nbytes: int, device: torch.device, delay: int = 0):
         self.stream = torch.cuda.Stream(device=device)
         self.ws = ops.workspace(nbytes, device)
         self.done: Optional[torch.cuda.Event] = None
+        self.delay = delay
+        self.pending = None   # a single track waiting for `delay` pair operations to be queued
+
+    def issue_pending(self) -> None:
+        """Queue a deferred single track now (it starts after the caller's queued work)."""
+        if self.pending is not None:
+            fn, self.pending = self.pending, None
+            fn()
 
     def wait_previous(self) -> None:
+        self.issue_pending()
         if self.done is not None:
             torch.cuda.current_stream().wait_event(self.done)
 
@@ -389,10 +406,16 @@ class PairformerLayer(Module):
         B, N = z.shape[0], z.shape[1]
         if ws is None:
             ws = ops.workspace(self.workspace_bytes(B, N), z.device)
-        self.triangle_multiplication_start(z, pair_mask, out=z, accumulate=True, ws=ws)
-        self.triangle_multiplication_end(z, pair_mask, out=z, accumulate=True, ws=ws)
-        self.triangle_attention_start(z, pair_mask, out=z, accumulate=True, ws=ws, n_valid=n_valid)
-        self.triangle_attention_end(z, pair_mask, out=z, accumulate=True, ws=ws, n_valid=n_valid)
+        pair_ops = (
+            lambda: self.triangle_multiplication_start(z, pair_mask, out=z, accumulate=True, ws=ws),
+            lambda: self.triangle_multiplication_end(z, pair_mask, out=z, accumulate=True, ws=ws),
+            lambda: self.triangle_attention_start(z, pair_mask, out=z, accumulate=True, ws=ws, n_valid=n_valid),
+            lambda: self.triangle_attention_end(z, pair_mask, out=z, accumulate=True, ws=ws, n_valid=n_valid),
+        )
+        for i, op in enumerate(pair_ops):
+            op()
+            if single is not None and i + 1 == single.delay:
+                single.issue_pending()   # the previous layer's single track starts beside the rest
         if not (self.transform_s and s is not None):
             self.transition_z(z, out=z, accumulate=True, ws=ws)
             return s, z
@@ -418,21 +441,27 @@ class PairformerLayer(Module):
                                      n_valid=n_valid, part="attend")
             self.transition_s(s, out=s, accumulate=True, ws=sws)
             return s, z
-        ready = torch.cuda.Event()
-        ready.record(torch.cuda.current_stream())
-        with torch.cuda.stream(single.stream):
-            single.stream.wait_event(ready)
-            ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps,
-                                 self.variant)
-            self.attention_pair_bias(s_norm, z, mask, k_in=s_norm, out=s, accumulate=True, ws=apb_ws,
-                                     n_valid=n_valid, part="attend")
-            self.transition_s(s, out=s, accumulate=True, ws=sws)
-            done = torch.cuda.Event()
-            done.record(single.stream)
-        for t in (s, mask, sws):
-            if t is not None:
-                t.record_stream(single.stream)
-        single.done = done
+        def issue():
+            ready = torch.cuda.Event()
+            ready.record(torch.cuda.current_stream())
+            with torch.cuda.stream(single.stream):
+                single.stream.wait_event(ready)
+                ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps,
+                                     self.variant)
+                self.attention_pair_bias(s_norm, z, mask, k_in=s_norm, out=s, accumulate=True, ws=apb_ws,
+                                         n_valid=n_valid, part="attend")
+                self.transition_s(s, out=s, accumulate=True, ws=sws)
+                done = torch.cuda.Event()
+                done.record(single.stream)
+            for t in (s, mask, sws):
+                if t is not None:
+                    t.record_stream(single.stream)
+            single.done = done
+
+        if single.delay == 0:
+            issue()
+        else:
+            single.pending = issue
         return s, z
 
 
@@ -460,7 +489,7 @@ class Pairformer(Module):
         nb = max((b.single_workspace_bytes(B, N) for b in self.blocks), default=16)
         key = (B, N, str(device))
         if getattr(self, "_single_key", None) != key:
-            self._single = SingleTrackStream(nb, device)
+            self._single = SingleTrackStream(nb, device, self.options.single_delay)
             self._single_key = key
         return self._single
 
