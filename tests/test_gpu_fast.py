@@ -307,6 +307,37 @@ def test_triatt_mx8_output_stage(gpu):
     check_grid(f"output stage N={N} vs fp8 emulator", out, want)
 
 
+@pytest.mark.parametrize("op", ["trimul_incoming", "triatt_ending"])
+def test_fast_ops_batch_of_two(gpu, op):
+    """B = 2 (two different pair tensors, one of them with a masked tail) gives each batch
+    element exactly what a B = 1 call on it gives: the fp8 kernels' batch indexing, in the
+    transposed (incoming / ending) addressing."""
+    N = 128
+    zs, pms = [], []
+    for k, pad in enumerate((0, 17)):
+        _, z, _, pm = synthetic.pair_inputs(N, 90 + k, pad_tail=pad)
+        zs.append(z.to(gpu)); pms.append(pm.to(gpu))
+    if op == "trimul_incoming":
+        dw = _mx8_trimul_w(_sub_w(92, "tri_mul_in"), gpu)
+        wsb = lambda B: ops.workspace(ops.trimul_mx8_workspace_bytes(B, N), gpu)
+        run = lambda z, pm, out, ws: ops.launch_trimul_mx8(z, out, pm, dw, 1, ws, accumulate=False)
+    else:
+        dw = _mx8_triatt_w(_sub_w(93, "tri_att_end"), gpu)
+        wsb = lambda B: ops.workspace(ops.triatt_mx8_workspace_bytes(B, N), gpu)
+        run = lambda z, pm, out, ws: ops.launch_triatt_mx8(z, out, pm, dw, True, ws, accumulate=False)
+    z2, pm2 = torch.cat(zs).contiguous(), torch.cat(pms).contiguous()
+    out2 = torch.empty_like(z2)
+    run(z2, pm2, out2, wsb(2))
+    ws1 = wsb(1)
+    for k in range(2):
+        out1 = torch.empty_like(zs[k])
+        run(zs[k].contiguous(), pms[k].contiguous(), out1, ws1)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out1).all()
+        assert torch.equal(out2[k:k + 1], out1), f"{op}: batch element {k} differs from its B = 1 call"
+    print(f"[fast] {op}: B = 2 equals two B = 1 calls bit for bit", flush=True)
+
+
 @pytest.mark.parametrize("N,ending,pad_tail", [(128, False, 0), (256, True, 20)])
 def test_triatt_mx8(gpu, N, ending, pad_tail):
     """Fast-mode triangle attention (starting / ending node) against the emulated-fp8 oracle
