@@ -71,6 +71,44 @@ def test_rejects_null_and_bad_shapes_without_launching():
     assert lib.pf_transition_mx8_fwd(ctypes.byref(tr)) == -1 and "C = 128" in _err()
 
 
+def test_fast_mode_entry_points_reject_bad_arguments_without_launching():
+    """pf_triatt_mx8_fwd, pf_apb_fwd_mx8 / pf_apb_attend_mx8, pf_transition_mx8_pair_bias_fwd
+    and pf_trimul_mx8_contract check shapes, pointers, workspace and n_valid before any HIP
+    call (dummy non-null pointers are never dereferenced on these paths)."""
+    lib = _lib.load()
+    assert lib.pf_triatt_mx8_fwd(None) == -1 and "null args" in _err()
+    t = _lib.TriattMx8Args(B=1, N=128, C=64, H=4, D=32)
+    assert lib.pf_triatt_mx8_fwd(ctypes.byref(t)) == -1 and "only C = 128" in _err()
+    t = _lib.TriattMx8Args(B=1, N=96, C=128, H=4, D=32)
+    assert lib.pf_triatt_mx8_fwd(ctypes.byref(t)) == -1 and "multiple of 64" in _err()
+    t = _lib.TriattMx8Args(B=1, N=128, C=128, H=4, D=32)
+    assert lib.pf_triatt_mx8_fwd(ctypes.byref(t)) == -1 and "null pointer" in _err()
+    dummy = {f: 16 for f, ty in _lib.TriattMx8Args._fields_ if ty is ctypes.c_void_p and f not in ("pair_mask", "stream")}
+    t = _lib.TriattMx8Args(B=1, N=128, C=128, H=4, D=32, workspace_bytes=16, **dummy)
+    assert lib.pf_triatt_mx8_fwd(ctypes.byref(t)) == -1 and "workspace too small" in _err()
+    need = lib.pf_triatt_mx8_workspace_size(1, 128, 128, 4, 32)
+    assert need > 0
+    t = _lib.TriattMx8Args(B=1, N=128, C=128, H=4, D=32, workspace_bytes=need, n_valid=129, **dummy)
+    assert lib.pf_triatt_mx8_fwd(ctypes.byref(t)) == -1 and "n_valid 129 outside" in _err()
+
+    assert lib.pf_apb_fwd_mx8(None) == -1 and "null args" in _err()
+    a = _lib.ApbArgs(B=1, N=100, c_s=384, C=128, H=16)
+    assert lib.pf_apb_attend_mx8(ctypes.byref(a)) == -1 and "unsupported shape" in _err()
+
+    tr_ptrs = {f: 16 for f, ty in _lib.TransitionMx8Args._fields_ if ty is ctypes.c_void_p and f != "stream"}
+    tr = _lib.TransitionMx8Args(rows=128 * 128 - 128, C=128, hidden=512, **tr_ptrs)
+    apb = _lib.ApbArgs(B=1, N=128, c_s=384, C=128, H=16, zln_w=16, zln_b=16, w_z=16, workspace=16,
+                       workspace_bytes=lib.pf_apb_workspace_size(1, 128, 384, 16))
+    assert lib.pf_transition_mx8_pair_bias_fwd(ctypes.byref(tr), ctypes.byref(apb)) == -1
+    assert "must equal B*N*N" in _err()
+    tr = _lib.TransitionMx8Args(rows=128 * 128, C=128, hidden=500, **tr_ptrs)
+    assert lib.pf_transition_mx8_pair_bias_fwd(ctypes.byref(tr), ctypes.byref(apb)) == -1
+    assert "hidden a multiple of 128" in _err()
+
+    assert lib.pf_trimul_mx8_contract(16, 16, 16, 16, 16, 2, 100, None) == -1 and "multiple of 128" in _err()
+    assert lib.pf_trimul_mx8_contract(16, 16, 16, 16, 16, 1 << 20, 4096, None) == -1 and "2^31" in _err()
+
+
 def test_both_operand_variants_load():
     for variant, code in _lib.OPERAND_CODE.items():
         lib = _lib.load(variant)
