@@ -146,3 +146,14 @@ def test_bench_refuses_more_than_one_gpu():
                        timeout=120, cwd=root)
     assert "exactly one GPU" in r.stdout + r.stderr
     assert '"metric"' not in r.stdout
+
+
+def test_options_validate_schedule_and_operand():
+    """Host-side option checks: the single-track delay is 0-4 and the operand type is known."""
+    from tt_boltz_amd import pairformer
+    assert pairformer.Options().single_delay == 1 and pairformer.Options().overlap_single
+    for bad in (-1, 5):
+        with pytest.raises(ValueError, match="single_delay"):
+            pairformer.Options(single_delay=bad)
+    with pytest.raises(ValueError, match="operand"):
+        pairformer.Options(operand="fp8")
