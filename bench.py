@@ -4,12 +4,14 @@ A step is one full Boltz-2 PairformerLayer (triangle multiplication out+in,
 triangle attention start+end, pair transition, single attention with pair bias,
 single transition) applied in place to device-resident z [1,512,512,128] fp32 and
 s [1,512,384] fp32, masks all ones, random-init weights from seed 0 (the
-config-0 layer architecture), bf16 MFMA operands with fp32 accumulation.
+config-0 layer architecture), fp16 MFMA operands with fp32 accumulation (the bf16-operand
+build of the same kernels is timed beside it).
 
 Besides the JSON line's ``value`` (layers/s), it reports per-op times and
-TFLOP/s, the roofline of the dominant kernel (the triangle-attention core, timed alone
-with HIP events on the stream it is launched on), the same for the trimul contraction,
-and the CPU oracle timed on this host's cores.
+TFLOP/s, the roofline of the dominant kernel (the triangle-attention core, its launches
+timed inside the layer loop with HIP events on the stream it is launched on, with its VALU
+roof and the chip's sustained MFMA rate beside the nameplate peak), the same for the trimul
+contraction, and the CPU oracle timed on this host's cores.
 
 The config-3 trunk (64 layers at N=768, recycling_steps=3 -> 4 passes, device
 resident) and the contraction alone at N=768 are reported under ``stack``.
@@ -25,6 +27,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--n 512] [--no-cpu-b
 from __future__ import annotations
 
 import argparse
+from typing import Optional
 import json
 import os
 import platform
@@ -126,6 +129,112 @@ def probe_traffic(N: int) -> int:
     return 0
 
 
+# ----------------------------------------------------------------------------- profile summaries
+PROBE_PMC_PASSES = ("SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS "
+                    "SQ_VALU_MFMA_BUSY_CYCLES SQ_WAIT_INST_ANY GRBM_GUI_ACTIVE",
+                    "FETCH_SIZE GRBM_GUI_ACTIVE", "WRITE_SIZE GRBM_GUI_ACTIVE")
+
+
+def _kernel_short(name: str) -> str:
+    import re
+    m = re.search(r"N_\d+([a-z0-9_]+_kernel)|([a-z0-9_]+_kernel)", name)
+    k = (m.group(1) or m.group(2)) if m else name[:40]
+    return "copy (torch.mul, calibration)" if "MulFunctor" in name else k
+
+
+def summarize_probe(N: int, kt_dir: str, pmc_dirs) -> None:
+    """Write profiles/layer_n{N}_kernel_stats.txt, profiles/layer_n{N}_counters.md and (N = 512)
+    profiles/kernel_traffic_n512.json from rocprofv3 CSV output of ``bench.py --probe-traffic
+    --n N``: one --kernel-trace run (``kt_dir``) and one --pmc run per PROBE_PMC_PASSES entry
+    (``pmc_dirs``), each written with ``--output-format csv -o run``."""
+    import collections
+    import csv
+    mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")
+    dur = collections.defaultdict(list)
+    for r in csv.DictReader(open(os.path.join(kt_dir, "run_kernel_trace.csv"))):
+        dur[_kernel_short(r["Kernel_Name"])].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    cnt = collections.defaultdict(lambda: collections.defaultdict(list))
+    for d in pmc_dirs:
+        for r in csv.DictReader(open(os.path.join(d, "run_counter_collection.csv"))):
+            k, v = _kernel_short(r["Kernel_Name"]), float(r["Counter_Value"])
+            if k.startswith("copy") and r["Counter_Name"] in ("FETCH_SIZE", "WRITE_SIZE") and v < 100 * 1024:
+                continue   # small torch.mul calls elsewhere in the probe are not the calibration copy
+            cnt[k][r["Counter_Name"]].append(v)
+    copy = cnt["copy (torch.mul, calibration)"]
+    f_fac = COPY_BYTES / (mean(copy["FETCH_SIZE"]) * 1024)
+    w_fac = COPY_BYTES / (mean(copy["WRITE_SIZE"]) * 1024)
+    copy_us = mean([d for d in dur["copy (torch.mul, calibration)"] if d > 20])
+    P = N * N
+    alg = {"tm_proj_kernel": P * 128 * 4 + 2 * P * 128 * 2,
+           "tm_contract_dma_kernel": 3 * P * 128 * 2,
+           "tm_out_kernel": P * 128 * 2 + 2 * P * 128 * 4,
+           "ta_proj_kernel": P * 128 * 4 + 3 * P * 128 * 2 + 4 * P * 4 + P * 2,
+           "ta_attn_kernel": 3 * P * 128 * 2 + 4 * P * 4 + P * 2 + P * 128 * 2,
+           "ta_out_kernel": P * 128 * 2 + 2 * P * 128 * 4,
+           "tr_pair_kernel": 2 * P * 128 * 4 + 16 * P * 4}
+    rows = []
+    for k in sorted(cnt, key=lambda k: -sum(dur.get(k, [0]))):
+        c, d = cnt[k], dur.get(k, [])
+        if not d or k.startswith(("distribution", "reduce", "__amd")):
+            continue
+        fe = mean(c["FETCH_SIZE"]) * 1024 * f_fac if c.get("FETCH_SIZE") else float("nan")
+        wr = mean(c["WRITE_SIZE"]) * 1024 * w_fac if c.get("WRITE_SIZE") else float("nan")
+        gr = mean(c["GRBM_GUI_ACTIVE"])
+        us = mean(d)
+        rows.append(dict(kernel=k, us=us, fetch=fe, write=wr, gbs=(fe + wr) / (us * 1e3), alg=alg.get(k),
+                         mfma=mean(c["SQ_INSTS_MFMA"]) if c.get("SQ_INSTS_MFMA") else 0.0,
+                         busy=mean(c["SQ_VALU_MFMA_BUSY_CYCLES"]) / (128 * gr) if c.get("SQ_VALU_MFMA_BUSY_CYCLES")
+                         else float("nan"),
+                         valu=mean(c["SQ_INSTS_VALU"]) if c.get("SQ_INSTS_VALU") else float("nan"),
+                         wait=mean(c["SQ_WAIT_INST_ANY"]) / mean(c["SQ_WAVE_CYCLES"]) if c.get("SQ_WAIT_INST_ANY")
+                         else float("nan")))
+    cmd_kt = (f"rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- python3 bench.py "
+              f"--probe-traffic --n {N}")
+    lines = [f"# Kernel durations, bench.py --probe-traffic at N={N} (MI355X, one GPU)", f"# command: {cmd_kt}",
+             "# workload: the triangle-attention core x5 and the trimul contraction x5 on their real operands,",
+             "# a 256 MiB copy x3 (calibration), then 3 full PairformerLayers (serial schedule, single track included)",
+             f"# {'kernel':34s} {'calls':>6s} {'avg_us':>9s} {'total_ms':>9s}"]
+    for k, d in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
+        if not k.startswith(("distribution", "__amd", "reduce")):
+            lines.append(f"  {k:34s} {len(d):6d} {mean(d):9.1f} {sum(d) / 1e3:9.3f}")
+    open(os.path.join(ROOT, "profiles", f"layer_n{N}_kernel_stats.txt"), "w").write("\n".join(lines) + "\n")
+    md = [f"# Per-kernel counters, N = {N} (MI355X, one GPU)", "",
+          f"Workload: `bench.py --probe-traffic --n {N}` (attention core x5, trimul contraction x5, a 256 MiB copy x3 "
+          "for calibration, three full PairformerLayers).  Commands (one counter pass each; durations from the kernel "
+          "trace; the tables are made by `bench.py --summarize-probe`):", "", f"    {cmd_kt}"]
+    md += [f"    rocprofv3 --pmc {c} --output-format csv -d <dir> -o run -- python3 bench.py --probe-traffic --n {N}"
+           for c in PROBE_PMC_PASSES]
+    md += ["", "Values are means per dispatch over every dispatch of the kernel in the run.",
+           f"HBM bytes: `FETCH_SIZE` x {f_fac:.3f} and `WRITE_SIZE` x {w_fac:.3f} (KiB): the factors that make the "
+           f"plain copy kernel's counters read its known 256 MiB in / 256 MiB out (the copy itself ran at "
+           f"{2 * COPY_BYTES / (copy_us * 1e3):.0f} GB/s).",
+           "MFMA busy = `SQ_VALU_MFMA_BUSY_CYCLES / (128 GRBM_GUI_ACTIVE)` (GRBM summed over the 8 XCDs, 1024 SIMDs).",
+           "wait = `SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES` (fraction of wave time stalled on s_waitcnt).", "",
+           "MFMA TF/s = issued `SQ_INSTS_MFMA` x 32768 FLOP (one 32x32x16 f16 MFMA) per second.", "",
+           "| kernel | us | HBM read MB | HBM write MB | GB/s | of 8 TB/s | algorithmic MB | traffic / algorithmic "
+           "| MFMA instr | MFMA busy | MFMA TF/s | VALU instr | wait |",
+           "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for r in rows:
+        ratio = (r["fetch"] + r["write"]) / r["alg"] if r["alg"] else float("nan")
+        tf = r["mfma"] * 32768 / (r["us"] * 1e-6) / 1e12
+        md.append(f"| {r['kernel']} | {r['us']:.1f} | {r['fetch'] / 1e6:.1f} | {r['write'] / 1e6:.1f} | "
+                  f"{r['gbs']:.0f} | {r['gbs'] / 8000:.2f} | {(r['alg'] or float('nan')) / 1e6:.1f} | {ratio:.2f} | "
+                  f"{r['mfma']:.0f} | {r['busy']:.3f} | {tf:.0f} | {r['valu']:.3g} | {r['wait']:.2f} |")
+    open(os.path.join(ROOT, "profiles", f"layer_n{N}_counters.md"), "w").write("\n".join(md) + "\n")
+    if N == 512:
+        t = {"N": N, "note": ("HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over bench.py "
+                              f"--probe-traffic (mean per dispatch, scaled by {f_fac:.3f} / {w_fac:.3f}: the factors "
+                              "that make a plain 256 MiB copy read its known bytes); VALU and MFMA instructions per "
+                              "launch from SQ_INSTS_VALU / SQ_INSTS_MFMA"),
+             "kernels": {r["kernel"]: {"hbm_bytes_per_launch": round(r["fetch"] + r["write"]),
+                                        "read_bytes": round(r["fetch"]), "write_bytes": round(r["write"]),
+                                        "algorithmic_bytes": r["alg"], "launch_us": round(r["us"], 1),
+                                        "valu_instr_per_launch": round(r["valu"]),
+                                        "mfma_instr_per_launch": round(r["mfma"])}
+                         for r in rows if r["alg"]}}
+        json.dump(t, open(TRAFFIC_FILE, "w"), indent=1)
+
+
 def load_traffic():
     """Calibrated HBM bytes per launch of the roofline kernels from the committed PMC summary
     (``{"N": .., "note": .., "kernels": {name: {"hbm_bytes_per_launch": ..}}}``, or None)."""
@@ -135,6 +244,30 @@ def load_traffic():
         return t
     except (OSError, ValueError):
         return None
+
+
+#: Issue cost of one wave64 VALU instruction per SIMD on this chip under load (ns), from in-bounds
+#: throughput microbenchmarks (8 waves per SIMD): v_exp_f32 (transcendental, quarter rate) and
+#: v_fma_f32 (every other 32-bit VALU instruction is priced at the FMA rate).
+VALU_NS = {"v_exp_f32": 3.74, "other": 2.12}
+
+
+def valu_roof(kname: str, N: int, launch_ms: float, simds: int, counters_for) -> Optional[dict]:
+    """The VALU / transcendental roof of the attention core: its VALU instructions per launch
+    (SQ_INSTS_VALU from the committed PMC summary) priced at the measured issue costs, one v_exp_f32
+    per score (N^3 * 4 heads, 64 per wave instruction), spread over every SIMD: the time the VALU
+    pipe alone needs, and its fraction of the launch time."""
+    k = counters_for(kname)
+    if not k or not k.get("valu_instr_per_launch"):
+        return None
+    valu = float(k["valu_instr_per_launch"])
+    exp_instr = N ** 3 * 4 / 64
+    floor_ns = (exp_instr * VALU_NS["v_exp_f32"] + max(valu - exp_instr, 0.0) * VALU_NS["other"]) / simds
+    return {"bound": "valu", "instructions_per_launch": valu, "exp_instructions_per_launch": exp_instr,
+            "issue_ns_per_wave_instr": VALU_NS, "simds": simds, "floor_ms": round(floor_ns * 1e-6, 4),
+            "frac": round(floor_ns * 1e-6 / launch_ms, 4),
+            "note": "floor = the VALU pipe's issue time for this launch's instruction count (counters: "
+                    "profiles/kernel_traffic_n%d.json); frac = floor / in-layer launch time" % N}
 
 
 def time_events(fn, reps: int, stream) -> float:
@@ -403,6 +536,42 @@ def fast_bench(N: int = 1024, seed: int = 4, steps: int = 5) -> dict:
     return res
 
 
+def fast_trunk_bench(N: int = 1024, n_layers: int = 64, seed: int = 4) -> dict:
+    """Config 4 as a trunk: one pass of the 64-layer Pairformer stack at N=1024 in fast mode
+    (every block-fp8 point) next to the same stack in 16-bit, device-resident, masks all ones;
+    each after one untimed pass."""
+    import torch
+    from tt_boltz_amd import ops, pairformer, synthetic
+    dev = pairformer.get_device()
+    stream = torch.cuda.current_stream()
+    w = synthetic.stack_weights(n_layers, seed)
+    s_cpu, z_cpu, mask_cpu, _ = synthetic.pair_inputs(N, seed)
+    res = {"N": N, "layers": n_layers, "seed": seed}
+    for mode in ("fp8", "fp16"):
+        pairformer.set_fast_mode(mode == "fp8")
+        try:
+            pf = pairformer.Pairformer(n_layers, 32, 4, 24, 16, True, w)
+        finally:
+            pairformer.set_fast_mode(False)
+        ws = ops.workspace(pf.workspace_bytes(1, N), dev)
+        z, s, mask = z_cpu.to(dev).contiguous(), s_cpu.to(dev).contiguous(), mask_cpu.to(dev)
+        pf(s.clone(), z.clone(), None, mask, ws)   # untimed pass
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        s_out, z_out = pf(s, z, None, mask, ws)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        sec = e0.elapsed_time(e1) / 1e3
+        res[f"{mode}_pass_s"] = round(sec, 4)
+        res[f"{mode}_layers_per_s"] = round(n_layers / sec, 2)
+        res[f"{mode}_finite"] = bool(torch.isfinite(z_out).all() and torch.isfinite(s_out).all())
+        del pf, ws, z, s, mask, s_out, z_out
+        torch.cuda.empty_cache()
+    res["speedup"] = round(res["fp16_pass_s"] / res["fp8_pass_s"], 3)
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -412,7 +581,12 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--probe-traffic", action="store_true")
+    ap.add_argument("--summarize-probe", nargs="+", metavar="DIR",
+                    help="KT_DIR PMC_DIR...: write the profiles/ summaries for --n from rocprofv3 CSV output")
     args = ap.parse_args()
+    if args.summarize_probe:
+        summarize_probe(args.n, args.summarize_probe[0], args.summarize_probe[1:])
+        return 0
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}): this build measures the "
               "single-GPU Pairformer path; multi-GPU sharding is a design note only.", file=sys.stderr)
@@ -482,11 +656,15 @@ def main() -> int:
 
     traffic = load_traffic()
 
-    def measured_traffic(kname):
-        """Calibrated HBM bytes per launch of `kname` from the committed PMC summary (or None)."""
+    def counters_for(kname):
+        """The committed PMC summary's entry for `kname` at this N (or None)."""
         if not traffic or traffic.get("N") != N:
             return None
-        k = traffic.get("kernels", {}).get(kname)
+        return traffic.get("kernels", {}).get(kname)
+
+    def measured_traffic(kname):
+        """Calibrated HBM bytes per launch of `kname` from the committed PMC summary (or None)."""
+        k = counters_for(kname)
         return None if k is None else k["hbm_bytes_per_launch"]
 
     # Dominant kernel: the triangle-attention core (ta_attn_kernel, ~0.18 ms of each
@@ -494,17 +672,40 @@ def main() -> int:
     # workspace, timed with HIP events on the stream it runs on.  MFMA-bound: 4*N^3*128 FLOP
     # per launch (QK^T and PV over 4 heads of 32) against the traffic of q, k, v (16-bit) read
     # once, the fp32 bias of the 4 heads and the 16-bit mask once and o (16-bit) written once.
+    # Its launch time is taken inside the layer loop: K more steps of the timed loop's schedule
+    # (single track overlapped on the second stream) with every attention-core launch bracketed
+    # by HIP events on the pair stream; the same kernel launched back to back on the operands
+    # one call left in the workspace is reported beside it (warm caches, no neighbours).
+    ops.attend_timing(True, layer.variant)
+    for _ in range(args.steps):
+        step()
+    single.join()
+    att_total_ms, att_launches = ops.attend_timing_read(layer.variant)
+    ops.attend_timing(False, layer.variant)
+    attn_ms = att_total_ms / max(att_launches, 1)
     reps = 20
     layer.triangle_attention_start(z, None, out=torch.empty_like(z), accumulate=False, ws=ws)
-    attn_ms = time_op(lambda: ops.launch_triatt_attend(ws, 1, N, 0, layer.variant), reps)
+    iso_ms = time_op(lambda: ops.launch_triatt_attend(ws, 1, N, 0, layer.variant), reps)
     attn_flop = fl["triatt_core"]
     attn_tf = attn_flop / (attn_ms * 1e-3) / 1e12
+    iso_tf = attn_flop / (iso_ms * 1e-3) / 1e12
     attn_bytes = (3 * 128 + 1 + 128) * N * N * 2 + 4 * N * N * 4
+    mfma_live = ops.mfma_rate_probe(dev, variant=layer.variant)
+    simds = 4 * torch.cuda.get_device_properties(dev).multi_processor_count
     roofline = {"kernel": "ta_attn_kernel", "bound": "mfma", "achieved": round(attn_tf, 1),
                 "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(attn_tf / MFMA_BF16_PEAK_TFLOPS, 4),
                 "traffic": measured_traffic("ta_attn_kernel"), "algorithmic_bytes": attn_bytes,
                 "flop_per_launch": attn_flop, "exp_per_launch": N ** 3 * 4, "launch_ms": round(attn_ms, 4),
-                "hbm_gbs_algorithmic": round(attn_bytes / (attn_ms * 1e-3) / 1e9, 1)}
+                "launch_ms_source": f"in-layer: mean of {att_launches} attention-core launches inside "
+                                    f"{args.steps} layer steps (HIP events on the pair stream)",
+                "isolated": {"launch_ms": round(iso_ms, 4), "achieved": round(iso_tf, 1),
+                             "frac": round(iso_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                             "note": f"{reps} back-to-back launches on one call's operands"},
+                "hbm_gbs_algorithmic": round(attn_bytes / (attn_ms * 1e-3) / 1e9, 1),
+                "measured_peak": {**mfma_live, "frac": round(attn_tf / mfma_live["tflops"], 4),
+                                  "note": "sustained 16-bit MFMA rate of this chip under load (mfma_rate_kernel, "
+                                          "random operands); achieved / this = frac of the loaded-clock peak"},
+                "valu": valu_roof("ta_attn_kernel", N, attn_ms, simds, counters_for)}
 
     # The trimul contraction (the batched matmul of the triangle multiplication), launched
     # alone on its real operand planes (those the last trimul call left behind).  Below the
@@ -545,9 +746,34 @@ def main() -> int:
         single_bf16.join()
 
     bf16_ms = time_op(step_bf16, args.steps)
+    del pf_bf16, single_bf16
+
+    # the same layer without the weight-precision paths (plain 16-bit weights: no hi + lo
+    # residuals, no mean correction), for the cost of those paths
+    pf_plain = pairformer.Pairformer(1, 32, 4, 24, 16, True, w,
+                                     pairformer.Options(weight_residuals=False, mean_correction=False))
+    zp, sp = z_cpu.to(dev).contiguous(), s_cpu.to(dev).contiguous()
+    single_plain = pf_plain.single_track(1, N, dev)
+
+    def step_plain():
+        pf_plain.blocks[0](sp, zp, None, None, ws, 0, single_plain)
+
+    for _ in range(args.warmup):
+        step_plain()
+    single_plain.join()
+    torch.cuda.synchronize()
+    pe0, pe1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    pe0.record(stream)
+    for _ in range(args.steps):
+        step_plain()
+    single_plain.join()
+    pe1.record(stream)
+    torch.cuda.synchronize()
+    plain_ms = pe0.elapsed_time(pe1) / args.steps
+    del pf_plain, single_plain, zp, sp
 
     out = {
-        "metric": "Pairformer layers/sec at N=512 bf16",
+        "metric": "Pairformer layers/sec at N=512, fp16 MFMA operands (bf16-operand rate in operand_variants)",
         "value": round(1000.0 / ms_step, 3),
         "unit": "layers/s",
         "n_gpus": 1,
@@ -560,9 +786,17 @@ def main() -> int:
         "dtype": "fp16",
         "operand_variants": {"fp16_layers_per_s": round(1000.0 / ms_step, 3),
                              "bf16_layers_per_s": round(1000.0 / bf16_ms, 3),
-                             "note": "MFMA operand type (fp32 accumulate, fp32 residual stream); fp16 is the "
-                                     "default because bf16 operands miss the 2e-3 mean-error bar"},
+                             "note": "MFMA operand type (fp32 accumulate, fp32 residual stream). BASELINE names "
+                                     "bf16; value is the fp16-operand layer (same 16-bit MFMA rate, 3 more "
+                                     "mantissa bits), the default because bf16 operands miss the 2e-3 "
+                                     "mean-error bar; bf16_layers_per_s is the bf16-operand build"},
         "single_stream_layers_per_s": round(1000.0 / serial_ms, 3),
+        "precision_paths": {"plain16_layers_per_s": round(1000.0 / plain_ms, 3),
+                            "cost_pct": round(100.0 * (ms_step / plain_ms - 1.0), 2),
+                            "note": "value runs the weight-precision paths (hi + lo weights in the trimul "
+                                    "output, triangle-attention output and recycling projections; the "
+                                    "trimul's mean correction); plain16 is the same layer with every weight "
+                                    "a single 16-bit rounding"},
         "data": "synthetic (seeded N(0,1) inputs, random-init weights, seed 0)",
         "config": {"workload": f"one Boltz-2 PairformerLayer, N={N}, c_z=128, c_s=384, tri-att 4x32, "
                                f"single-att 16x24, masks all ones, device-resident fp32 z/s; layers back to "
@@ -578,10 +812,12 @@ def main() -> int:
         "host": platform.node(),
     }
     if not args.no_stack:
-        del pf_bf16, zb, sb
+        del zb, sb
         out["stack"] = stack_bench()
         torch.cuda.empty_cache()
         out["fast"] = fast_bench()
+        torch.cuda.empty_cache()
+        out["fast_trunk"] = fast_trunk_bench()
         torch.cuda.empty_cache()
         out["msa"] = msa_bench()
         torch.cuda.empty_cache()

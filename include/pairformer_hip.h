@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define PF_ABI_VERSION 1
+#define PF_ABI_VERSION 2
 
 enum {
   PF_OK = 0,
@@ -81,6 +81,19 @@ typedef struct pf_trimul_args {
   const void* g_out_w;    /* g_out.weight bf16 [C][C] */
   void* workspace; size_t workspace_bytes;
   void* stream;
+  /* Optional (NULL = unused; C = 128 only): the residual p_out - p_out16 of p_out.weight,
+   * rounded to the operand type.  The output projection then runs on p_out16 + residual (two
+   * MFMAs per fragment), with weights good to ~2^-22 of their size (see pf_triatt_args). */
+  const void* p_out_lo;
+  /* Optional (NULL = unused; C = 128 only): in_offsets fp32 [5C] = p_in.weight . beta [2C],
+   * g_in.weight . beta [2C], g_out.weight . beta [C] in fp32 from the unrounded weights (beta =
+   * norm_in.bias); the kernels then add these instead of the 16-bit weights' W16 . beta.  With
+   * also the residuals p_in_lo, g_in_lo, g_out_lo (W - W16 in the operand type) and B == 1,
+   * the mean correction: each of those rows' offsets also gets W_lo . (norm_in.weight * mu),
+   * mu = the mean over positions of the normalized z (estimated from up to 32768 sampled
+   * positions): the part of a 16-bit weight's rounding error that every position shares. */
+  const float* in_offsets;
+  const void* p_in_lo; const void* g_in_lo; const void* g_out_lo;
 } pf_trimul_args;
 
 size_t pf_trimul_workspace_size(int B, int N, int C);
@@ -119,6 +132,12 @@ typedef struct pf_triatt_args {
   const void* w_o;        /* mha.linear_o.weight bf16 [C][H*D] */
   void* workspace; size_t workspace_bytes;
   void* stream;
+  /* Optional (NULL = unused; C = 128 only): the residuals W - W16 of linear_g and linear_o,
+   * rounded to the operand type.  With both given, the gate and the output projection run on
+   * W16 + residual (two MFMAs per fragment), i.e. with weights good to ~2^-22 of their size:
+   * the 2^-12 rounding of 16-bit weights is the same at every position, and it is what makes
+   * a deep stack drift from the fp32 reference. */
+  const void* w_g_lo; const void* w_o_lo;
 } pf_triatt_args;
 
 size_t pf_triatt_workspace_size(int B, int N, int C, int H, int D);
@@ -420,9 +439,13 @@ int pf_linear_fwd(const float* x, const void* W, const float* bias, const float*
 
 /* Pair-track recycling step of the trunk loop (tt_bio/boltz2.py:5213-5214):
  *   out[p,:] = base[p,:] + W . LN(x[p,:])   for every pair p, C = 128.
- * (z = z_init + z_recycle(z_norm(z))); out may alias x but not base unless equal. */
+ * (z = z_init + z_recycle(z_norm(z))); out may alias x but not base unless equal.
+ * W_lo (optional, NULL = unused): the residual W - W16 in the operand type; with it the product
+ * takes both the weight and the normalized activation as 16-bit hi + lo pairs (three MFMAs per
+ * fragment), i.e. it is computed to ~fp32 accuracy.  At a pass's start z is zero, LN(z) is the
+ * same beta at every pair, and a 16-bit rounding of W or beta would shift every pair alike. */
 int pf_pair_ln_linear_fwd(const float* x, const float* base, const float* ln_w, const float* ln_b,
-                          const void* W, float* out, long rows, int C, float eps, void* stream);
+                          const void* W, const void* W_lo, float* out, long rows, int C, float eps, void* stream);
 
 /* ------------------------------------------------------------------------------
  * Diffusion conditioning, pair side (run once per trunk output; fixed for every
@@ -449,6 +472,26 @@ int pf_token_pair_bias_fwd(const float* z, const float* ln_w, const float* ln_b,
  *   z = z + template_module(z, ...), z = z + msa_module(z, ...)):
  *   out[i] = a[i] + b[i], fp32, 16-byte aligned pointers; out may alias a or b. */
 int pf_add_fwd(const float* a, const float* b, float* out, long n, void* stream);
+
+/* ------------------------------------------------------------------------------
+ * Measurement aids (no counterpart in the reference: they serve the benchmark's roofline
+ * figures and allocate no device memory).
+ * -------------------------------------------------------------------------- */
+/* In-layer launch timing of the triangle-attention core: pf_attend_timing(1) clears and starts
+ * the calling host thread's record, after which every ta_attn_kernel launch that thread makes
+ * (pf_triatt_fwd, pf_triatt_mx8_fwd, pf_triatt_attend_workspace, pf_tri_attention) is bracketed
+ * by HIP events on its stream; pf_attend_timing(0) stops recording.  pf_attend_timing_read
+ * waits for the last recorded launch and returns the summed launch durations (ms) and the
+ * number of launches. */
+int pf_attend_timing(int enable);
+int pf_attend_timing_read(double* total_ms, int* launches);
+
+/* MFMA issue rate under load: `workgroups` workgroups of 16 waves each issue `iters` rounds
+ * of four dependent-free 32x32x16 16-bit MFMAs (pseudo-random operands in (-1, 1) that change
+ * every MFMA), i.e. pf_mfma_rate_probe_waves(workgroups) * iters * 4 * 32768 FLOP; every wave
+ * writes one float of `sink` (workgroups * 16 floats). */
+long pf_mfma_rate_probe_waves(int workgroups);
+int pf_mfma_rate_probe(int workgroups, int iters, float* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -30,33 +30,114 @@ Weights = Mapping[str, Tensor]
 CHUNK_SIZE_THRESHOLD = 384
 
 
-#: Rounding of every product operand: None (exact fp32, the reference semantics) or a 16-bit
-#: torch dtype.  ``operand_rounding(torch.float16)`` turns the oracle into a precision model of
-#: a 16-bit-operand implementation (operands of every matmul / einsum rounded once, products
+#: Rounding of product operands: None (exact fp32, the reference semantics) or a 16-bit torch
+#: dtype.  ``operand_rounding(torch.float16)`` turns the oracle into a precision model of a
+#: 16-bit-operand implementation (operands of every matmul / einsum rounded once, products
 #: accumulated and everything else computed in fp32); tests use it to bound the drift that the
 #: operand format alone causes.  It is not the reference and is off by default.
 _OPERAND: Optional[torch.dtype] = None
 
+#: Operand families of the precision model.  Every rounding site carries one name
+#: ``"<family>.<x|w>"`` (activation or weight side); a selector rounds the sites it matches.
+FAMILIES = (
+    "tm_in",    # trimul: LN_in(z) . p_in
+    "tm_gin",   # trimul: LN_in(z) . g_in
+    "tm_ab",    # trimul: the gated planes a, b of the contraction
+    "tm_x",     # trimul: the stored contraction output X
+    "tm_out",   # trimul: LN_out(X) . p_out
+    "tm_gate",  # trimul: LN_in(z) . g_out
+    "ta_in",    # triangle attention: LN(z) . W_q / W_k / W_v
+    "ta_g",     # triangle attention: LN(z) . W_g
+    "ta_bias",  # triangle attention: LN(z) . W_bias (the per-head triangle bias)
+    "ta_qk",    # triangle attention: q, k of the logits
+    "ta_p",     # triangle attention: the probabilities P of P.v
+    "ta_v",     # triangle attention: v of P.v
+    "ta_o",     # triangle attention: the stored attention output o
+    "ta_out",   # triangle attention: o . sigmoid(g) . W_o
+    "tr_in",    # pair transition: LN(z) . fc1 / fc2
+    "tr_hid",   # pair transition: silu(fc1) * fc2 . fc3
+    "s_apb",    # single track: attention with pair bias (projections, logits, P.v, z bias)
+    "s_tr",     # single track: transition
+    "rec",      # pair recycling projection z_recycle(z_norm(z))
+    "s_rec",    # single recycling projection s_recycle(s_norm(s))
+    "misc",     # every other linear (MSA module, diffusion conditioning)
+)
+_SELECT: Optional[frozenset] = None
+
+#: The precision model of this build's 16-bit kernels (``operand_rounding(dtype, **BUILD_MODEL)``):
+#: every product operand rounded to the operand type, except where the kernels carry a weight as
+#: a 16-bit hi + lo pair -- the trimul output projection p_out, the triangle attention's gate and
+#: output projections, the pair recycling projection (its activation too) -- and with the mean
+#: correction at the trimul's LN_in-side weights (p_in, g_in, g_out).
+BUILD_MODEL = {"families": ("!tm_out.w", "!ta_out.w", "!ta_g.w", "!rec"),
+               "mean_fix": ("tm_in", "tm_gin", "tm_gate")}
+_MEAN_FIX = None          # None, or the selector of weight sites whose error gets the mean correction
+_MEAN_SAMPLE = 1          # the correction's mean is taken over every k-th position
+
+
+def _parse_selector(families):
+    if families is None:
+        return None
+    families = frozenset(families)
+    unknown = {f for f in families
+               if f.lstrip("!") not in ("x", "w") and f.lstrip("!").split(".")[0] not in FAMILIES}
+    if unknown:
+        raise ValueError(f"unknown operand families {sorted(unknown)}")
+    return families
+
+
+def _matches(select, site: str) -> bool:
+    if select is None:
+        return True
+    fam, side = site.split(".")
+    names = (fam, site, side)
+    if any("!" + n in select for n in names):
+        return False
+    if all(f.startswith("!") for f in select):
+        return True
+    return any(n in select for n in names)
+
 
 @contextmanager
-def operand_rounding(dtype: Optional[torch.dtype]):
-    global _OPERAND
-    prev, _OPERAND = _OPERAND, dtype
+def operand_rounding(dtype: Optional[torch.dtype], families=None, mean_fix=False, mean_sample: int = 1):
+    """Round the operands of the sites selected by ``families`` to ``dtype`` (all sites when
+    None).  A selector item is a family name from ``FAMILIES`` (both sides), a site name
+    ``"<family>.x"`` / ``"<family>.w"``, or ``"x"`` / ``"w"`` (that side of every family); an
+    item starting with ``"!"`` excludes what it names (with exclusions only, every other site
+    is selected).  ``mean_fix`` (True, or a selector of weight sites): at those rounded weights
+    the rounding error only meets the activation's deviation from its mean over positions (the
+    model of an implementation that adds (W - round(W)) . mean(x) in fp32), the mean taken over
+    every ``mean_sample``-th position."""
+    global _OPERAND, _SELECT, _MEAN_FIX, _MEAN_SAMPLE
+    families = _parse_selector(families)
+    fix = None if mean_fix is False or mean_fix is None else (
+        frozenset() if mean_fix is True else _parse_selector(mean_fix))
+    prev = _OPERAND, _SELECT, _MEAN_FIX, _MEAN_SAMPLE
+    _OPERAND, _SELECT, _MEAN_FIX, _MEAN_SAMPLE = dtype, families, fix, int(mean_sample)
     try:
         yield
     finally:
-        _OPERAND = prev
+        _OPERAND, _SELECT, _MEAN_FIX, _MEAN_SAMPLE = prev
 
 
-def _op(t: Tensor) -> Tensor:
-    """A product operand, rounded to the operand type when a precision model is active."""
-    return t if _OPERAND is None else t.to(_OPERAND).to(t.dtype)
+def _selected(site: str) -> bool:
+    return _OPERAND is not None and _matches(_SELECT, site)
 
 
-def _op_scaled(t: Tensor) -> Tensor:
+def _mean_fixed(site: str) -> bool:
+    return _MEAN_FIX is not None and _selected(site) and (not _MEAN_FIX or _matches(_MEAN_FIX, site))
+
+
+def _op(t: Tensor, site: str) -> Tensor:
+    """A product operand at rounding site ``site``, rounded to the operand type when the
+    precision model selects that site."""
+    return t.to(_OPERAND).to(t.dtype) if _selected(site) else t
+
+
+def _op_scaled(t: Tensor, site: str) -> Tensor:
     """A stored intermediate (the trimul contraction output) rounded to the operand type under
     a power-of-two scale that keeps its largest value in the type's normal range."""
-    if _OPERAND is None:
+    if not _selected(site):
         return t
     amax = float(t.abs().max())
     if amax == 0.0:
@@ -76,9 +157,15 @@ def layer_norm(x: Tensor, weight: Tensor, bias: Tensor, eps: float = 1e-5) -> Te
     return F.layer_norm(x, (x.shape[-1],), weight, bias, eps)
 
 
-def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None) -> Tensor:
-    """``nn.Linear`` / ``tt_bio/boltz2.py:720-731`` (fp32 branch)."""
-    return F.linear(_op(x), _op(weight), bias)
+def linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None, fam: str = "misc") -> Tensor:
+    """``nn.Linear`` / ``tt_bio/boltz2.py:720-731`` (fp32 branch); ``fam`` names the
+    operand family of the precision model."""
+    y = F.linear(_op(x, fam + ".x"), _op(weight, fam + ".w"), bias)
+    if _mean_fixed(fam + ".w") and x.dim() > 2:
+        flat = x.reshape(x.shape[0], -1, x.shape[-1])[:, ::_MEAN_SAMPLE]
+        mu = flat.mean(dim=1).view((x.shape[0],) + (1,) * (x.dim() - 2) + (x.shape[-1],))
+        y = y + F.linear(mu, weight - _op(weight, fam + ".w"))
+    return y
 
 
 # --------------------------------------------------------------------------------------
@@ -96,17 +183,17 @@ def triangle_multiplication(z: Tensor, pair_mask: Tensor, w: Weights, direction:
         raise ValueError(f"direction must be 'outgoing' or 'incoming', got {direction!r}")
     x = layer_norm(z, w["norm_in.weight"], w["norm_in.bias"])              # reference.py:456
     x_in = x                                                                # :457
-    x = linear(x, w["p_in.weight"]) * torch.sigmoid(linear(x, w["g_in.weight"]))  # :458
+    x = linear(x, w["p_in.weight"], fam="tm_in") * torch.sigmoid(linear(x, w["g_in.weight"], fam="tm_gin"))  # :458
     x = x * pair_mask.unsqueeze(-1)                                         # :461
     a, b = torch.chunk(x.float(), 2, dim=-1)                                # :464
-    a, b = _op(a), _op(b)
+    a, b = _op(a, "tm_ab.x"), _op(b, "tm_ab.x")
     if direction == "outgoing":
         x = torch.einsum("bikd,bjkd->bijd", a, b)                           # :467
     else:
         x = torch.einsum("bkid,bkjd->bijd", a, b)                           # :556
-    x = _op_scaled(x)
-    x = linear(layer_norm(x, w["norm_out.weight"], w["norm_out.bias"]), w["p_out.weight"])
-    return x * torch.sigmoid(linear(x_in, w["g_out.weight"]))               # :470
+    x = _op_scaled(x, "tm_x.x")
+    x = linear(layer_norm(x, w["norm_out.weight"], w["norm_out.bias"]), w["p_out.weight"], fam="tm_out")
+    return x * torch.sigmoid(linear(x_in, w["g_out.weight"], fam="tm_gate"))  # :470
 
 
 def triangle_multiplication_mx8(z: Tensor, pair_mask: Tensor, w: Weights, direction: str) -> Tensor:
@@ -153,18 +240,18 @@ def _mha_rows(x: Tensor, tri_bias: Tensor, mask_bias: Tensor, w: Weights,
     """
     fq = fq or (lambda t: t)
     shp = x.shape[:-1]
-    q = fq(linear(x, w["linear_q.weight"])).view(shp + (n_heads, head_dim)).transpose(-2, -3)
-    k = fq(linear(x, w["linear_k.weight"])).view(shp + (n_heads, head_dim)).transpose(-2, -3)
-    v = fq(linear(x, w["linear_v.weight"])).view(shp + (n_heads, head_dim)).transpose(-2, -3)
+    q = fq(linear(x, w["linear_q.weight"], fam="ta_in")).view(shp + (n_heads, head_dim)).transpose(-2, -3)
+    k = fq(linear(x, w["linear_k.weight"], fam="ta_in")).view(shp + (n_heads, head_dim)).transpose(-2, -3)
+    v = fq(linear(x, w["linear_v.weight"], fam="ta_in")).view(shp + (n_heads, head_dim)).transpose(-2, -3)
     q = q / sqrt(head_dim)
-    a = torch.matmul(_op(q), _op(k).transpose(-1, -2))      # [B,I,H,J,K]
+    a = torch.matmul(_op(q, "ta_qk.x"), _op(k, "ta_qk.x").transpose(-1, -2))      # [B,I,H,J,K]
     a = a + mask_bias
     a = a + tri_bias
     a = torch.softmax(a, dim=-1)
-    o = torch.matmul(_op(a), _op(v)).transpose(-2, -3)      # [B,I,J,H,d]
-    g = torch.sigmoid(fq(linear(x, w["linear_g.weight"]))).view(shp + (n_heads, head_dim))
-    o = (_op(o) * g).reshape(shp + (n_heads * head_dim,))
-    return fq(linear(o, w["linear_o.weight"]))
+    o = torch.matmul(_op(a, "ta_p.x"), _op(v, "ta_v.x")).transpose(-2, -3)      # [B,I,J,H,d]
+    g = torch.sigmoid(fq(linear(x, w["linear_g.weight"], fam="ta_g"))).view(shp + (n_heads, head_dim))
+    o = (_op(o, "ta_o.x") * g).reshape(shp + (n_heads * head_dim,))
+    return fq(linear(o, w["linear_o.weight"], fam="ta_out"))
 
 
 def triangle_attention(z: Tensor, pair_mask: Optional[Tensor], w: Weights, starting: bool = True,
@@ -194,7 +281,7 @@ def triangle_attention(z: Tensor, pair_mask: Optional[Tensor], w: Weights, start
     x = layer_norm(z, w["layer_norm.weight"], w["layer_norm.bias"])      # :331
     mask = pair_mask[..., :, None, None, :]                              # :334
     mask_bias = inf * (mask - 1)                                         # :335
-    tri_bias = linear(x, w["linear.weight"]).permute(0, 3, 1, 2).unsqueeze(-4)  # :338-341
+    tri_bias = linear(x, w["linear.weight"], fam="ta_bias").permute(0, 3, 1, 2).unsqueeze(-4)  # :338-341
     mw = sub(w, "mha")
     fq = None
     if fast:
@@ -233,12 +320,14 @@ def triangle_attention_core(q: Tensor, k: Tensor, v: Tensor, tri_bias: Tensor,
 # --------------------------------------------------------------------------------------
 # Transition  (tt_bio/boltz2.py:1188-1258)
 # --------------------------------------------------------------------------------------
-def transition(x: Tensor, w: Weights) -> Tensor:
+def transition(x: Tensor, w: Weights, fam: str = "tr") -> Tensor:
     """``Transition.forward`` with ``chunk_size=None`` (``boltz2.py:1240-1245``):
-    LN -> silu(fc1) * fc2 -> fc3 (no biases)."""
+    LN -> silu(fc1) * fc2 -> fc3 (no biases).  ``fam``: the precision model's family prefix
+    (``<fam>_in`` for fc1 / fc2, ``<fam>_hid`` for fc3; "s_tr" / "misc" as one family)."""
+    f_in, f_hid = (fam + "_in", fam + "_hid") if fam == "tr" else (fam, fam)
     x = layer_norm(x, w["norm.weight"], w["norm.bias"])
-    x = F.silu(linear(x, w["fc1.weight"])) * linear(x, w["fc2.weight"])
-    return linear(x, w["fc3.weight"])
+    x = F.silu(linear(x, w["fc1.weight"], fam=f_in)) * linear(x, w["fc2.weight"], fam=f_in)
+    return linear(x, w["fc3.weight"], fam=f_hid)
 
 
 def transition_mx8(x: Tensor, w: Weights) -> Tensor:
@@ -264,23 +353,23 @@ def attention_pair_bias(s: Tensor, z: Tensor, mask: Tensor, k_in: Tensor, w: Wei
     """
     B, N, c_s = s.shape
     d = c_s // num_heads
-    q = linear(s, w["proj_q.weight"], w["proj_q.bias"]).view(B, -1, num_heads, d)
-    k = linear(k_in, w["proj_k.weight"]).view(B, -1, num_heads, d)
-    v = linear(k_in, w["proj_v.weight"]).view(B, -1, num_heads, d)
-    bias = linear(layer_norm(z, w["proj_z.0.weight"], w["proj_z.0.bias"]), w["proj_z.1.weight"])
+    q = linear(s, w["proj_q.weight"], w["proj_q.bias"], fam="s_apb").view(B, -1, num_heads, d)
+    k = linear(k_in, w["proj_k.weight"], fam="s_apb").view(B, -1, num_heads, d)
+    v = linear(k_in, w["proj_v.weight"], fam="s_apb").view(B, -1, num_heads, d)
+    bias = linear(layer_norm(z, w["proj_z.0.weight"], w["proj_z.0.bias"]), w["proj_z.1.weight"], fam="s_apb")
     bias = bias.permute(0, 3, 1, 2)                                       # "b ... h -> b h ..."
-    g = torch.sigmoid(linear(s, w["proj_g.weight"]))
-    attn = torch.einsum("bihd,bjhd->bhij", _op(q.float()), _op(k.float()))
+    g = torch.sigmoid(linear(s, w["proj_g.weight"], fam="s_apb"))
+    attn = torch.einsum("bihd,bjhd->bhij", _op(q.float(), "s_apb.x"), _op(k.float(), "s_apb.x"))
     attn = attn / (d ** 0.5) + bias.float()
     attn = attn + (1 - mask[:, None, None].float()) * -inf
     attn = attn.softmax(dim=-1)
-    o = torch.einsum("bhij,bjhd->bihd", _op(attn), _op(v.float())).to(v.dtype)
+    o = torch.einsum("bhij,bjhd->bihd", _op(attn, "s_apb.x"), _op(v.float(), "s_apb.x")).to(v.dtype)
     o = o.reshape(B, -1, c_s)
     go = g * o
     if fast:
         from .fp8_emu import fake_quant_mx8
         go = fake_quant_mx8(go)
-    return linear(go, w["proj_o.weight"])
+    return linear(go, w["proj_o.weight"], fam="s_apb")
 
 
 # --------------------------------------------------------------------------------------
@@ -317,7 +406,7 @@ def pairformer_layer(s: Optional[Tensor], z: Tensor, mask: Optional[Tensor], pai
     s_normed = layer_norm(s.float(), w["pre_norm_s.weight"], w["pre_norm_s.bias"])
     s = s.float() + attention_pair_bias(s_normed, z.float(), mask.float(), s_normed,
                                         sub(w, "attention"), att_heads, fast=fast)
-    s = s + transition(s, sub(w, "transition_s"))
+    s = s + transition(s, sub(w, "transition_s"), fam="s_tr")
     return s, z
 
 
@@ -347,9 +436,9 @@ def recycle(s_init: Tensor, z_init: Tensor, mask: Tensor, w_stack: Weights, w_re
     z = torch.zeros_like(z_init)
     for i in range(recycling_steps + 1):
         s = s_init + linear(layer_norm(s, w_rec["s_norm.weight"], w_rec["s_norm.bias"]),
-                            w_rec["s_recycle.weight"])
+                            w_rec["s_recycle.weight"], fam="s_rec")
         z = z_init + linear(layer_norm(z, w_rec["z_norm.weight"], w_rec["z_norm.bias"]),
-                            w_rec["z_recycle.weight"])
+                            w_rec["z_recycle.weight"], fam="rec")
         if msa is not None:
             from .msa_ref import msa_module
             w_msa, emb, feats, msa_blocks = msa

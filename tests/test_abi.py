@@ -34,12 +34,12 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().pf_abi_version() == _lib.ABI_VERSION == 1
+    assert _lib.load().pf_abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_struct_layouts_match_header_order():
     # the ctypes structs mirror the C structs field by field; spot-check sizes/offsets
-    assert _lib.TrimulArgs.z_in.offset == 32 and ctypes.sizeof(_lib.TrimulArgs) == 32 + 14 * 8
+    assert _lib.TrimulArgs.z_in.offset == 32 and ctypes.sizeof(_lib.TrimulArgs) == 32 + 19 * 8
     assert _lib.TransitionArgs.x_in.offset == 24
     assert _lib.TriattArgs.z_in.offset == 40
     assert _lib.TrimulMx8Args.z_in.offset == 32 and ctypes.sizeof(_lib.TrimulMx8Args) == 32 + 18 * 8
@@ -92,6 +92,12 @@ def test_fast_mode_entry_points_reject_bad_arguments_without_launching():
     assert lib.pf_triatt_mx8_fwd(ctypes.byref(t)) == -1 and "n_valid 129 outside" in _err()
 
     assert lib.pf_apb_fwd_mx8(None) == -1 and "null args" in _err()
+    # the allocation-free entry point names an unsupported shape as such (not as a scratch size)
+    a = _lib.ApbArgs(B=1, N=100, c_s=384, C=128, H=16)
+    assert lib.pf_apb_fwd_noalloc(ctypes.byref(a)) == -1 and "unsupported shape" in _err()
+    a = _lib.ApbArgs(B=1, N=4096, c_s=384, C=128, H=16, **{f: 16 for f, ty in _lib.ApbArgs._fields_
+                                                         if ty is ctypes.c_void_p and f not in ("stream", "workspace")})
+    assert lib.pf_apb_fwd_noalloc(ctypes.byref(a)) == -1 and "bytes of scratch" in _err()
     a = _lib.ApbArgs(B=1, N=100, c_s=384, C=128, H=16)
     assert lib.pf_apb_attend_mx8(ctypes.byref(a)) == -1 and "unsupported shape" in _err()
 
@@ -112,15 +118,16 @@ def test_fast_mode_entry_points_reject_bad_arguments_without_launching():
 def test_both_operand_variants_load():
     for variant, code in _lib.OPERAND_CODE.items():
         lib = _lib.load(variant)
-        assert lib.pf_operand_dtype() == code and lib.pf_abi_version() == 1
+        assert lib.pf_operand_dtype() == code and lib.pf_abi_version() == 2
         for name in _declared():
             assert hasattr(lib, name), (variant, name)
 
 
 def test_workspace_sizes():
     lib = _lib.load()
-    # a, b and X planes (16-bit) + 1024 per-workgroup operand maxima (fp32) for X's scale
-    assert lib.pf_trimul_workspace_size(1, 512, 128) == 128 * 512 * 512 * (2 + 2 + 2) + 1024 * 4
+    # a, b and X planes (16-bit) + 1024 per-workgroup operand maxima (fp32) for X's scale + the
+    # 64 x 128 partial sums of the mean correction (fp32)
+    assert lib.pf_trimul_workspace_size(1, 512, 128) == 128 * 512 * 512 * (2 + 2 + 2) + 1024 * 4 + 64 * 128 * 4
     assert lib.pf_triatt_workspace_size(1, 64, 128, 4, 32) > 0
     assert lib.pf_triatt_workspace_size(1, 64, 128, 8, 16) == 0
     assert lib.pf_transition_workspace_size(4096, 128, 512) == 0          # fused, no scratch
@@ -157,3 +164,42 @@ def test_options_validate_schedule_and_operand():
             pairformer.Options(single_delay=bad)
     with pytest.raises(ValueError, match="operand"):
         pairformer.Options(operand="fp8")
+
+
+def test_failed_block_drops_deferred_single_track():
+    """A block that raises leaves no deferred single-track closure behind on the cached
+    second stream (the next call would otherwise run it on the failed call's tensors), and a
+    stale closure found at the start of a call is dropped, not run."""
+    import types
+
+    import torch
+    from tt_boltz_amd import pairformer
+
+    class FakeSingle:
+        def __init__(self):
+            self.pending, self.joined = None, False
+
+        def discard(self):
+            self.pending = None
+
+        def join(self):
+            self.joined = True
+
+    single, ran = FakeSingle(), []
+    single.pending = lambda: ran.append("stale from an earlier call")
+
+    def good(s, z, *rest):
+        single.pending = lambda: ran.append("deferred of this call")
+        return s, z
+
+    def bad(*rest):
+        raise RuntimeError("launch failed")
+
+    fake = types.SimpleNamespace(blocks=[good, bad], single_track=lambda *a: single, workspace_bytes=lambda B, N: 16)
+    s, z = torch.zeros(1, 4, 8), torch.zeros(1, 4, 4, 8)
+    with pytest.raises(RuntimeError, match="launch failed"):
+        pairformer.Pairformer.__call__(fake, s, z, ws=torch.zeros(1))
+    assert single.pending is None and not single.joined and ran == []
+    fake.blocks = [good]
+    pairformer.Pairformer.__call__(fake, s, z, ws=torch.zeros(1))
+    assert single.joined and single.pending is not None and ran == []   # join() of the fake issues nothing

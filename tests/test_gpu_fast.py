@@ -438,6 +438,54 @@ def test_fast_layer_config4(gpu):
             assert mn_e <= 0.6 * mn_f, (name, mn_e, mn_f)
 
 
+#: a 4-layer fast stack may drift this far (mean / rms) from the emulated-fp8 stack: each
+#: layer adds ~1.8e-2 of re-rounded e4m3 steps (test_fast_layer_config4), and they add up
+#: roughly like independent errors
+STACK_EMU_MEAN = 5e-2
+
+
+@pytest.mark.timeout(600)
+def test_fast_stack_config4(gpu):
+    """Config 4 as a trunk: 4 fast layers at N = 1024 (seed 4) against the emulated-fp8 stack
+    and the fp32 stack, both on the device, after every layer.  Bars: z within STACK_EMU_MEAN
+    (mean) and 1.0 (max) of the emulator after the last layer, within the fp8 bound of fp32,
+    and nearer the emulator than fp32 after every layer (a 16-bit or mis-wired fast path is
+    not)."""
+    cfg = synthetic.CONFIGS[4]
+    N, n_layers = cfg["N"], 4
+    w = synthetic.stack_weights(n_layers, cfg["seed"])
+    s, z, mask, pm = synthetic.pair_inputs(N, cfg["seed"])
+    sd, zd, md, pmd = s.to(gpu), z.to(gpu), mask.to(gpu), pm.to(gpu)
+    wd = {k: v.to(gpu) for k, v in w.items()}
+    pairformer.set_fast_mode(True)
+    try:
+        pf = pairformer.Pairformer(n_layers, 32, 4, 24, 16, True, w)
+    finally:
+        pairformer.set_fast_mode(False)
+    ws = ops.workspace(pf.workspace_bytes(1, N), gpu)
+    s_got, z_got = sd.clone(), zd.clone()
+    s_e, z_e, s_f, z_f = sd, zd, sd, zd
+    chunk = ref.chunk_size_for(N)
+    for i in range(n_layers):
+        lw = ref.sub(wd, f"layers.{i}")
+        with torch.no_grad():
+            s_e, z_e = ref.pairformer_layer(s_e, z_e, md, pmd, lw, chunk, fast=True)
+            s_f, z_f = ref.pairformer_layer(s_f, z_f, md, pmd, lw, chunk)
+        pf.blocks[i](s_got, z_got, pmd, md, ws)
+        torch.cuda.synchronize()
+        mx_e, mn_e = stats(z_got, z_e)
+        mx_f, mn_f = stats(z_got, z_f)
+        print(f"[fast] stack N=1024 after layer {i}: z vs emulator max/rms={mx_e:.3e} mean/rms={mn_e:.3e}; "
+              f"vs fp32 max/rms={mx_f:.3e} mean/rms={mn_f:.3e}", flush=True)
+        assert torch.isfinite(z_got).all() and torch.isfinite(s_got).all()
+        assert mn_e <= 0.6 * mn_f, (i, mn_e, mn_f)
+    assert mn_e <= STACK_EMU_MEAN and mx_e <= 1.0, (mx_e, mn_e)
+    assert mn_f <= F32_MEAN and mx_f <= 2 * F32_MAX, (mx_f, mn_f)
+    smx, smn = stats(s_got, s_e)
+    print(f"[fast] stack N=1024 s vs emulator max/rms={smx:.3e} mean/rms={smn:.3e}", flush=True)
+    assert smn <= STACK_EMU_MEAN
+
+
 @pytest.mark.parametrize("operand", ["fp16", "bf16"])
 def test_module_fast_mode(gpu, operand):
     """set_fast_mode(True) before construction (tenstorrent.py:178-181): a 1-block

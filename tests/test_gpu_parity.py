@@ -169,12 +169,15 @@ def test_triatt_small(gpu, N, ending, rand_mask):
 
 @pytest.mark.parametrize("ending", [False, True])
 def test_triatt_config2(gpu, ending):
-    """N=512, last 51 tokens padded, seed 2; oracle unchunked fp32."""
+    """N=512, last 51 tokens padded, seed 2; oracle unchunked fp32 (all 512
+    rows in one attention call, evaluated on the device: [1, 512, 4, 512, 512] fp32 logits)."""
     cfg = synthetic.CONFIGS[2]
     prefix = "tri_att_end" if ending else "tri_att_start"
     w = _sub_w(cfg["seed"], prefix)
     _, z, _, pm = _inputs(cfg["N"], cfg["seed"], pad_tail=cfg["pad_tail"])
-    want = ref.triangle_attention(z, pm, w, not ending, 64)
+    with torch.no_grad():
+        want = ref.triangle_attention(z.to(gpu), pm.to(gpu), {k: v.to(gpu) for k, v in w.items()}, not ending,
+                                      None).cpu()
     zd = z.to(gpu)
     out = torch.empty_like(zd)
     ws = ops.workspace(ops.triatt_workspace_bytes(1, cfg["N"]), gpu)

@@ -1,0 +1,144 @@
+"""GPU checks of the kernels' weight-precision paths.
+
+* hi + lo weights (``ta_out`` gate / output projection, ``tm_out`` output projection, the pair
+  recycling projection): wiring is checked by feeding the residual equal to the 16-bit weight
+  itself, which must give the result of the plain kernel on the doubled weight (an exact
+  doubling in the operand type) up to fp32 summation order; accuracy by the recycling
+  projection's agreement with fp32 to ~1e-6 (both sides split).
+* the mean correction of the trimul's LN_in-side weights: on a pair tensor whose rows share a
+  strong channel pattern, the per-channel mean over positions of the GPU's update error (the
+  coherent part that a deep stack accumulates) must fall well below the uncorrected kernel's.
+"""
+import pytest
+import torch
+
+from oracle import pairformer_ref as ref
+from tt_boltz_amd import ops, synthetic
+
+from test_gpu_parity import _dev_w, _inputs, _sub_w, check, stats
+
+pytestmark = pytest.mark.gpu
+
+
+def _same(a, b, name):
+    """Equal up to fp32 summation order: hi.x + lo.x and (2 hi).x differ in the last bits of an
+    fp32 sum, which now and then moves a later 16-bit rounding by one step (max ~1e-4 of the
+    rms); a wiring mistake (wrong row, pitch or operand) moves every element by O(1)."""
+    mx, mn = stats(a, b)
+    print(f"[precision] {name}: max/rms={mx:.3e} mean/rms={mn:.3e}", flush=True)
+    assert torch.isfinite(a).all() and mx <= 2e-3 and mn <= 2e-6, f"{name}: max/rms={mx:.3e} mean/rms={mn:.3e}"
+
+
+@pytest.mark.parametrize("ending", [False, True])
+def test_triatt_residual_weights_wiring(gpu, ending):
+    """ta_out with (hi, lo) = (W16, W16) equals the plain kernel on 2 W16 (gate and output)."""
+    N = 192
+    prefix = "tri_att_end" if ending else "tri_att_start"
+    w = _dev_w(_sub_w(21, prefix), gpu, "mha.")
+    _, z, _, pm = _inputs(N, 22, pad_tail=13)
+    zd, pmd = z.to(gpu), pm.to(gpu).contiguous()
+    ws = ops.workspace(ops.triatt_workspace_bytes(1, N), gpu)
+    hilo = dict(w)
+    hilo["linear_g.weight.lo"] = w["linear_g.weight"]
+    hilo["linear_o.weight.lo"] = w["linear_o.weight"]
+    doubled = dict(w)
+    doubled["linear_g.weight"] = (2 * w["linear_g.weight"].float()).to(w["linear_g.weight"].dtype)
+    doubled["linear_o.weight"] = (2 * w["linear_o.weight"].float()).to(w["linear_o.weight"].dtype)
+    a, b = torch.empty_like(zd), torch.empty_like(zd)
+    ops.launch_triatt(zd, a, pmd, hilo, ending, ws, accumulate=False)
+    ops.launch_triatt(zd, b, pmd, doubled, ending, ws, accumulate=False)
+    _same(a, b, f"triatt hi+lo(=hi) vs doubled weights ending={ending}")
+    # and the true residual brings the update to the fp32 oracle at least as close as before
+    true_lo = dict(w)
+    raw = _sub_w(21, prefix)
+    for k in ("linear_g.weight", "linear_o.weight"):
+        true_lo[k + ".lo"] = ops.opw_lo(raw["mha." + k], gpu)
+    c = torch.empty_like(zd)
+    ops.launch_triatt(zd, c, pmd, true_lo, ending, ws, accumulate=False)
+    want = ref.triangle_attention(z, pm, raw, not ending, None)
+    check(f"triatt with weight residuals ending={ending}", c, want)
+
+
+@pytest.mark.parametrize("direction", [0, 1])
+def test_trimul_residual_weight_wiring(gpu, direction):
+    """tm_out with p_out given as (W16, W16) equals the plain kernel on 2 W16; the two-fill X
+    stage of that path is covered by the same comparison."""
+    N = 256
+    prefix = "tri_mul_out" if direction == 0 else "tri_mul_in"
+    w = _dev_w(_sub_w(23, prefix), gpu)
+    _, z, _, pm = _inputs(N, 24, pad_tail=17, rand_mask=True)
+    zd, pmd = z.to(gpu), pm.to(gpu).contiguous()
+    ws = ops.workspace(ops.trimul_workspace_bytes(1, N), gpu)
+    hilo = dict(w)
+    hilo["p_out.weight.lo"] = w["p_out.weight"]
+    doubled = dict(w)
+    doubled["p_out.weight"] = (2 * w["p_out.weight"].float()).to(w["p_out.weight"].dtype)
+    a, b = torch.empty_like(zd), torch.empty_like(zd)
+    ops.launch_trimul(zd, a, pmd, hilo, direction, ws, accumulate=False)
+    ops.launch_trimul(zd, b, pmd, doubled, direction, ws, accumulate=False)
+    _same(a, b, f"trimul p_out hi+lo(=hi) vs doubled direction={direction}")
+
+
+def test_pair_recycling_projection_is_fp32_accurate(gpu):
+    """base + W . LN(x) with both W and LN(x) split hi + lo agrees with fp64 to ~2e-7 of the
+    update's rms in the mean (measured 2.2e-7; the plain 16-bit path: 2.4e-4), including the
+    pass-start case x = 0 where LN(x) is the same beta at every pair."""
+    g = torch.Generator().manual_seed(31)
+    rows = 64 * 64
+    w = synthetic.draw(synthetic.recycle_shapes(), 32)
+    W, lnw, lnb = w["z_recycle.weight"], w["z_norm.weight"], w["z_norm.bias"]
+    for name, x in (("random z", torch.randn((rows, 128), generator=g)), ("z = 0", torch.zeros((rows, 128)))):
+        base = torch.randn((rows, 128), generator=g)
+        want = ref.layer_norm(x.double(), lnw.double(), lnb.double()) @ W.double().t()
+        xd, bd = x.to(gpu), base.to(gpu)
+        out = torch.empty_like(bd)
+        ops.launch_pair_ln_linear(xd, bd, lnw.to(gpu), lnb.to(gpu), ops.opw(W, gpu), out, 1e-5, "fp16",
+                                  ops.opw_lo(W, gpu))
+        upd = out.double().cpu() - base.double()
+        mx, mn = stats(upd, want)
+        plain = torch.empty_like(bd)
+        ops.launch_pair_ln_linear(xd, bd, lnw.to(gpu), lnb.to(gpu), ops.opw(W, gpu), plain, 1e-5, "fp16")
+        pmx, pmn = stats(plain.double().cpu() - base.double(), want)
+        print(f"[precision] recycling projection, {name}: hi+lo max/rms={mx:.2e} mean/rms={mn:.2e}; "
+              f"plain max/rms={pmx:.2e} mean/rms={pmn:.2e}", flush=True)
+        assert mx < 1e-5 and mn < 1e-6, (name, mx, mn)
+        assert pmn > 100 * mn
+
+
+@pytest.mark.parametrize("direction", [0, 1])
+def test_trimul_mean_correction_removes_coherent_error(gpu, direction):
+    """z rows share a strong channel pattern (so the normalized rows have a large mean over
+    positions).  The error of the 16-bit weights then has a large coherent part: the same
+    offset at every position.  With the exact beta offsets and the mean correction, the
+    per-channel mean over positions of the update's error must drop well below the plain
+    kernel's, and the update must stay within the parity bar.  (The corrected run also carries
+    p_out as hi + lo, as the module does: the contraction output's LayerNorm has a mean over
+    positions too.)"""
+    N = 256
+    prefix = "tri_mul_out" if direction == 0 else "tri_mul_in"
+    raw = _sub_w(25, prefix)
+    g = torch.Generator().manual_seed(26)
+    pattern = 3.0 * torch.randn(128, generator=g)
+    z = pattern + torch.randn((1, N, N, 128), generator=g)
+    pm = torch.ones((1, N, N))
+    want = ref.triangle_multiplication(z.to(gpu), pm.to(gpu), {k: v.to(gpu) for k, v in raw.items()},
+                                       "outgoing" if direction == 0 else "incoming").cpu()
+    w = _dev_w(raw, gpu)
+    beta = raw["norm_in.bias"].double()
+    fixed = dict(w)
+    fixed["in_offsets"] = torch.cat([raw[k].double() @ beta for k in ("p_in.weight", "g_in.weight",
+                                                                      "g_out.weight")]).float().to(gpu)
+    for k in ("p_in.weight", "g_in.weight", "g_out.weight", "p_out.weight"):
+        fixed[k + ".lo"] = ops.opw_lo(raw[k], gpu)
+    zd = z.to(gpu).contiguous()
+    ws = ops.workspace(ops.trimul_workspace_bytes(1, N), gpu)
+    a, b = torch.empty_like(zd), torch.empty_like(zd)
+    ops.launch_trimul(zd, a, None, w, direction, ws, accumulate=False)
+    ops.launch_trimul(zd, b, None, fixed, direction, ws, accumulate=False)
+    rms = want.pow(2).mean().sqrt()
+    coh_plain = ((a.cpu() - want).mean(dim=(0, 1, 2)).abs().mean() / rms).item()
+    coh_fixed = ((b.cpu() - want).mean(dim=(0, 1, 2)).abs().mean() / rms).item()
+    print(f"[precision] trimul direction={direction}: coherent error plain {coh_plain:.3e}, "
+          f"mean-corrected {coh_fixed:.3e}", flush=True)
+    check(f"trimul mean-corrected direction={direction}", b, want)
+    assert coh_fixed < 0.35 * coh_plain

@@ -2,13 +2,15 @@
 
 * Config 3: the 64-layer trunk at N = 768 with 3 recycling steps (4 passes,
   ``boltz2.py:5203``), seed 3, against the fp32 oracle evaluated on the device, pass by pass.
-  The bar is the oracle's own precision model of 16-bit operands
-  (``pairformer_ref.operand_rounding(torch.float16)``: every matmul operand rounded to fp16,
-  fp32 accumulation and statistics -- this build's numerics contract): per pass, the GPU may
-  drift from fp32 by at most 2x what exact arithmetic on fp16 operands drifts (or the
-  north-star 2e-2 / 2e-3 of the rms, if larger).  The stack is not contractive across
-  recycling passes, so the drift grows from pass to pass in both; the test also reports the
-  oracle's sensitivity to an fp16 rounding of its inputs alone.
+  After the first pass z and s must meet the north-star bar itself: max |d| <= 2e-2 and mean
+  |d| <= 2e-3 of the fp32 result's rms.  The stack is not contractive across recycling passes
+  (each pass feeds the last one's z back through LayerNorm), so any per-pass error grows from
+  pass to pass, also in exact arithmetic on 16-bit operands; for the later passes the bar is
+  this build's precision model evaluated the same way (``pairformer_ref.BUILD_MODEL``: fp16
+  operands, the hi + lo weights and the mean correction where the kernels have them, fp32
+  accumulation and statistics): the GPU may drift at most 1.5x as far as the model.  The model
+  and the per-operand-family ablation it rests on come from ``tests/precision_ablation.py``.
+  The test also reports the oracle's sensitivity to an fp16 rounding of its inputs alone.
 * The reference's differential tests (``tests/test_tenstorrent.py:31-66``): the drop-in
   ``PairformerModule`` at N = 100 and N = 500 (padded to 128 / 512 inside) with the
   reference's input scales z = 26 randn, s = 8 randn, the c_z = 64 template stack, and the
@@ -49,10 +51,14 @@ def check_reference_case(name, got, want, start):
 
 
 # ------------------------------------------------------------------------------ config 3
+#: later passes: the GPU's drift from fp32 may be at most this multiple of the precision model's
+MODEL_FACTOR = 1.5
+
+
 @pytest.mark.timeout(900)
 def test_config3_stack_depth(gpu):
-    """64 layers x 4 recycling passes at N = 768 (config 3) vs the fp32 oracle on the device,
-    with the fp16-operand precision model of the oracle as the bar."""
+    """64 layers x 4 recycling passes at N = 768 (config 3) vs the fp32 oracle on the device:
+    the north-star bar after the first pass, this build's precision model after the others."""
     cfg = synthetic.CONFIGS[3]
     N, n_blocks, steps = cfg["N"], 64, 3
     w = synthetic.stack_weights(n_blocks, cfg["seed"])
@@ -61,19 +67,19 @@ def test_config3_stack_depth(gpu):
     wd, wrd = _dev(w, gpu), _dev(w_rec, gpu)
     sd, zd, md = s_init.to(gpu), z_init.to(gpu), mask.to(gpu)
 
-    def run_oracle(s0, z0, tag, operand=None):
+    def run_oracle(s0, z0, tag, operand=None, model=None):
         out = []
 
         def hook(i, s, z):
             out.append((s.clone(), z.clone()))
             print(f"[stack] {tag} pass {i} done", flush=True)
 
-        with torch.no_grad(), ref.operand_rounding(operand):
+        with torch.no_grad(), ref.operand_rounding(operand, **(model or {})):
             ref.recycle(s0, z0, md, wd, wrd, n_blocks, steps, pass_hook=hook)
         return out
 
     want = run_oracle(sd, zd, "fp32 oracle")
-    emu = run_oracle(sd, zd, "fp16-operand oracle", torch.float16)
+    emu = run_oracle(sd, zd, "precision model of this build", torch.float16, ref.BUILD_MODEL)
     pert = run_oracle(sd.half().float(), zd.half().float(), "fp32 oracle, fp16-rounded inputs")
 
     pf = pairformer.Pairformer(n_blocks, 32, 4, 24, 16, True, w)
@@ -89,11 +95,13 @@ def test_config3_stack_depth(gpu):
             mx, mn = stats(g, r)
             emx, emn = stats(e, r)
             dmx, dmn = stats(p, r)
-            print(f"[stack] pass {i} {name}: gpu max/rms={mx:.3e} mean/rms={mn:.3e} | fp16-operand model "
+            print(f"[stack] pass {i} {name}: gpu max/rms={mx:.3e} mean/rms={mn:.3e} | precision model "
                   f"max/rms={emx:.3e} mean/rms={emn:.3e} | fp16-rounded inputs max/rms={dmx:.3e} "
                   f"mean/rms={dmn:.3e}", flush=True)
             assert torch.isfinite(g).all()
-            if not (mx <= max(MAX_TOL, 2 * emx) and mn <= max(MEAN_TOL, 2 * emn)):
+            ok = (mx <= MAX_TOL and mn <= MEAN_TOL) if i == 0 else \
+                (mx <= max(MAX_TOL, MODEL_FACTOR * emx) and mn <= max(MEAN_TOL, MODEL_FACTOR * emn))
+            if not ok:
                 bad.append((i, name, mx, mn, emx, emn))
     assert not bad, bad
 

@@ -17,7 +17,7 @@ LIBS = {"fp16": "libpairformer_hip.so", "bf16": "libpairformer_hip_bf16.so"}
 OPERAND_CODE = {"fp16": 0, "bf16": 1}
 DEFAULT_VARIANT = "fp16"
 LIB_PATH = os.path.join(HERE, LIBS[DEFAULT_VARIANT])
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 c_int, c_float, c_long, c_size_t, c_void_p = ctypes.c_int, ctypes.c_float, ctypes.c_long, ctypes.c_size_t, ctypes.c_void_p
 
@@ -30,6 +30,8 @@ class TrimulArgs(ctypes.Structure):
         ("norm_in_w", c_void_p), ("norm_in_b", c_void_p), ("p_in_w", c_void_p), ("g_in_w", c_void_p),
         ("norm_out_w", c_void_p), ("norm_out_b", c_void_p), ("p_out_w", c_void_p), ("g_out_w", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
+        ("p_out_lo", c_void_p), ("in_offsets", c_void_p), ("p_in_lo", c_void_p), ("g_in_lo", c_void_p),
+        ("g_out_lo", c_void_p),
     ]
 
 
@@ -41,6 +43,7 @@ class TriattArgs(ctypes.Structure):
         ("ln_w", c_void_p), ("ln_b", c_void_p), ("w_bias", c_void_p),
         ("w_q", c_void_p), ("w_k", c_void_p), ("w_v", c_void_p), ("w_g", c_void_p), ("w_o", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
+        ("w_g_lo", c_void_p), ("w_o_lo", c_void_p),
     ]
 
 
@@ -153,8 +156,8 @@ SIGNATURES = {
                                    c_void_p]),
     "pf_layernorm_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_float, c_void_p]),
     "pf_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int, c_int, c_void_p]),
-    "pf_pair_ln_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long,
-                                      c_int, c_float, c_void_p]),
+    "pf_pair_ln_linear_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                      c_long, c_int, c_float, c_void_p]),
     "pf_add_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_long, c_void_p]),
     "pf_pair_cond_proj_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int,
                                       c_float, c_void_p]),
@@ -168,6 +171,10 @@ SIGNATURES = {
     "pf_trimul_mx8_contract": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "pf_transition_mx8_fwd": (c_int, [ctypes.POINTER(TransitionMx8Args)]),
     "pf_transition_mx8_pair_bias_fwd": (c_int, [ctypes.POINTER(TransitionMx8Args), ctypes.POINTER(ApbArgs)]),
+    "pf_attend_timing": (c_int, [c_int]),
+    "pf_attend_timing_read": (c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_int)]),
+    "pf_mfma_rate_probe_waves": (c_long, [c_int]),
+    "pf_mfma_rate_probe": (c_int, [c_int, c_int, c_void_p, c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -17,7 +17,8 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OBJDIR = os.path.join(HERE, "_build")
 
-SOURCES = ["api.cpp", "trimul.hip", "triatt.hip", "transition.hip", "single.hip", "fast8.hip", "msa.hip", "diffusion.hip"]
+SOURCES = ["api.cpp", "trimul.hip", "triatt.hip", "transition.hip", "single.hip", "fast8.hip", "msa.hip", "diffusion.hip",
+           "measure.hip"]
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

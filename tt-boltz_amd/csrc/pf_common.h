@@ -319,7 +319,10 @@ PF_DEV float x_store_scale(float amax, int K) {
   if (!(bound > 0.f) || !(bound < 3.0e38f)) return 1.f;   // all-zero planes (or no bound): unscaled
   int e;
   (void)frexpf(bound, &e);
-  return ldexpf(1.f, 15 - e);
+  // the exponent is capped so the scale and its inverse stay normal floats: planes whose
+  // bound lies below 2^-111 (tiny but nonzero operands, possible with bf16) are stored at
+  // most 2^126 times larger, not times inf
+  return ldexpf(1.f, min(15 - e, 126));
 }
 
 // ---------------------------------------------------------------------------------

@@ -41,7 +41,7 @@ int pf_linear_batch(const pf_lin_job* jobs, int njobs, long rows, int K, int Nou
 // Single-track attention workspace helpers (single.hip): argument checks shared by the
 // entry points (bias_only: only what the pair bias reads), and the address of the pair
 // bias [B][H][N][N] inside the workspace.
-int pf_apb_check(const pf_apb_args* a, const char* fn, bool bias_only);
+int pf_apb_check(const pf_apb_args* a, const char* fn, bool bias_only, bool check_ws = true);
 float* pf_apb_bias_ptr(const pf_apb_args* a);
 
 // Batched X[p][i][j] = scale * sum_k A[p][i][k] * B[p][j][k] (trimul.hip): A [P][M][K],
@@ -53,3 +53,8 @@ int pf_contract_rect(const void* A, const void* B, void* X, int x_fp32, int plan
 // multiple of 32 (single.hip: the single-track pair-bias kernel).
 int pf_pair_logits(const float* z, const float* lnw, const float* lnb, const void* wz, float* out, int B, int N,
                    int H, float eps, hipStream_t st);
+
+// Launch timing of the triangle-attention core (measure.hip): while pf_attend_timing(1) is on
+// for this host thread, the launcher records an event before (end = 0) and after (end = 1)
+// every ta_attn_kernel launch on its stream; otherwise a no-op.
+void pf_attend_mark(hipStream_t st, int end);

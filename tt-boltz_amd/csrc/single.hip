@@ -224,19 +224,22 @@ extern "C" size_t pf_apb_workspace_size(int B, int N, int c_s, int H) {
 }
 
 // Shape / pointer / workspace checks shared by the entry points.
-int pf_apb_check(const pf_apb_args* a, const char* fn, bool bias_only) {
+// check_ws = false skips the workspace pointer and size (the allocation-free entry point
+// brings its own scratch and checks its size itself).
+int pf_apb_check(const pf_apb_args* a, const char* fn, bool bias_only, bool check_ws) {
   if (!a) return pf_fail(PF_E_INVALID, "%s: null args", fn);
   if (a->B <= 0 || a->N <= 0 || a->C != C || a->H <= 0 || a->H > 32 || a->c_s % a->H ||
       (a->c_s / a->H != 24 && a->c_s / a->H != 32) || a->c_s % 32 || a->N > 4096 || (a->N % 32))
     return pf_fail(PF_E_INVALID, "%s: unsupported shape B=%d N=%d c_s=%d C=%d H=%d", fn, a->B, a->N, a->c_s, a->C,
                    a->H);
-  if (!a->z || !a->zln_w || !a->zln_b || !a->w_z || !a->workspace)
+  if (!a->z || !a->zln_w || !a->zln_b || !a->w_z || (check_ws && !a->workspace))
     return pf_fail(PF_E_INVALID, "%s: null pointer argument", fn);
   if (!bias_only && (!a->s || !a->k_in || !a->out || !a->w_q || !a->b_q || !a->w_k || !a->w_v || !a->w_g ||
                      !a->w_o))
     return pf_fail(PF_E_INVALID, "%s: null pointer argument", fn);
   if (a->n_valid < 0 || a->n_valid > a->N)
     return pf_fail(PF_E_INVALID, "%s: n_valid %d outside [0, N=%d]", fn, a->n_valid, a->N);
+  if (!check_ws) return PF_OK;
   const size_t need = pf_apb_workspace_size(a->B, a->N, a->c_s, a->H);
   if (a->workspace_bytes < need)
     return pf_fail(PF_E_INVALID, "%s: workspace too small (%zu < %zu bytes)", fn, a->workspace_bytes, need);
@@ -354,9 +357,10 @@ int apb_scratch(void** out) {
 }  // namespace
 
 extern "C" int pf_apb_fwd_noalloc(const pf_apb_args* a) {
-  if (!a) return pf_fail(PF_E_INVALID, "pf_apb_fwd_noalloc: null args");
+  // shape, pointers and n_valid first, so an unsupported shape is reported as such
+  if (const int rc = pf_apb_check(a, "pf_apb_fwd_noalloc", false, false)) return rc;
   const size_t need = pf_apb_workspace_size(a->B, a->N, a->c_s, a->H);
-  if (need == 0 || need > APB_SCRATCH_BYTES)
+  if (need > APB_SCRATCH_BYTES)
     return pf_fail(PF_E_INVALID,
                    "pf_apb_fwd_noalloc: B=%d N=%d c_s=%d H=%d needs %zu bytes of scratch, above the static %zu "
                    "(call pf_apb_fwd with a workspace)", a->B, a->N, a->c_s, a->H, need, APB_SCRATCH_BYTES);

@@ -285,29 +285,60 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinJobs jobs, long row
   }
 }
 
-// out[p, :] = base[p, :] + W . LN(x[p, :]),  C = 128; W resident in LDS.
+// out[p, :] = base[p, :] + W . LN(x[p, :]),  C = 128; W resident in LDS.  HILO: W = W + W_lo and
+// LN(x) = hi + lo (16-bit each), products hi.W + lo.W + hi.W_lo (the lo.W_lo term is below
+// fp32's resolution of the sum).
+template <bool HILO>
 __global__ __launch_bounds__(256) void pair_ln_linear_kernel(
     const float* x, const float* base, const float* __restrict__ lnw, const float* __restrict__ lnb,
-    const op_t* __restrict__ W, float* out, long rows, float eps) {
-  __shared__ __attribute__((aligned(16))) op_t sW[C * LDSW];
+    const op_t* __restrict__ W, const op_t* __restrict__ W_lo, float* out, long rows, float eps) {
+  __shared__ __attribute__((aligned(16))) op_t sW[(HILO ? 2 : 1) * C * LDSW];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, h = lane >> 5, m = lane & 31;
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     const int c = tid + 256 * q;
     st_x8(&sW[(c >> 4) * LDSW + (c & 15) * 8], ld_x8(W + (c >> 4) * C + (c & 15) * 8));
+    if constexpr (HILO) st_x8(&sW[C * LDSW + (c >> 4) * LDSW + (c & 15) * 8], ld_x8(W_lo + (c >> 4) * C + (c & 15) * 8));
   }
   __syncthreads();
   const long pos0 = ((long)blockIdx.x * 4 + wid) * 32;
   if (pos0 >= rows) return;
   float xv[64];
-  opx8 xf[8];
+  opx8 xf[8], xl[8];
   load_row128_frag(x + min(pos0 + m, rows - 1) * C, h, xv);
-  ln128_to_frag(xv, h, lnw, lnb, eps, xf);
+  if constexpr (HILO) {
+    float sm = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) sm += xv[i];
+    const float mean = xor32_sum(sm) * (1.f / C);
+    float var = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) { const float d = xv[i] - mean; var += d * d; }
+    const float rstd = rsqrtf(xor32_sum(var) * (1.f / C) + eps);
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int c = 16 * s + 8 * h + t;
+        const float y = (xv[8 * s + t] - mean) * rstd * lnw[c] + lnb[c];
+        xf[s][t] = (op_t)y;
+        xl[s][t] = (op_t)(y - (float)xf[s][t]);
+      }
+  } else {
+    ln128_to_frag(xv, h, lnw, lnb, eps, xf);
+  }
 #pragma unroll
   for (int ob = 0; ob < 4; ++ob) {
     f32x16 acc = zero16();
 #pragma unroll
     for (int s = 0; s < 8; ++s) acc = mfma32(xf[s], ld_x8(&sW[(32 * ob + m) * LDSW + 16 * s + 8 * h]), acc);
+    if constexpr (HILO) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        acc = mfma32(xl[s], ld_x8(&sW[(32 * ob + m) * LDSW + 16 * s + 8 * h]), acc);
+        acc = mfma32(xf[s], ld_x8(&sW[C * LDSW + (32 * ob + m) * LDSW + 16 * s + 8 * h]), acc);
+      }
+    }
     // base may alias out: all loads ahead of the stores, so they overlap
     float res[16];
 #pragma unroll
@@ -414,11 +445,16 @@ extern "C" int pf_transition_fwd(const pf_transition_args* a) {
 }
 
 extern "C" int pf_pair_ln_linear_fwd(const float* x, const float* base, const float* ln_w, const float* ln_b,
-                                     const void* W, float* out, long rows, int C_, float eps, void* stream) {
+                                     const void* W, const void* W_lo, float* out, long rows, int C_, float eps,
+                                     void* stream) {
   if (!x || !base || !ln_w || !ln_b || !W || !out) return pf_fail(PF_E_INVALID, "pf_pair_ln_linear_fwd: null pointer");
   if (C_ != C || rows <= 0) return pf_fail(PF_E_INVALID, "pf_pair_ln_linear_fwd: only C = 128 (got %d)", C_);
-  pair_ln_linear_kernel<<<(unsigned)((rows + 127) / 128), 256, 0, (hipStream_t)stream>>>(
-      x, base, ln_w, ln_b, (const op_t*)W, out, rows, eps);
+  if (W_lo)
+    pair_ln_linear_kernel<true><<<(unsigned)((rows + 127) / 128), 256, 0, (hipStream_t)stream>>>(
+        x, base, ln_w, ln_b, (const op_t*)W, (const op_t*)W_lo, out, rows, eps);
+  else
+    pair_ln_linear_kernel<false><<<(unsigned)((rows + 127) / 128), 256, 0, (hipStream_t)stream>>>(
+        x, base, ln_w, ln_b, (const op_t*)W, nullptr, out, rows, eps);
   PF_CHECK_LAUNCH("pair_ln_linear_kernel");
   return PF_OK;
 }

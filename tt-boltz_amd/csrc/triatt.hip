@@ -609,17 +609,33 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
 // ---------------------------------------------------------------------------------
 constexpr int TAO_WAVES = 8;
 // LDS: the gate offsets [C] and gamma [CC] (fp32, first: small immediate offsets), then
-// W_g [C][CC + 4] and W_o [CC][C + 4] op_t
-template <int CC>
+// W_g [C][CC + 4] and W_o [CC][C + 4] op_t, then (HILO) their residuals in the same layout
+template <int CC, bool HILO = false>
 constexpr size_t tao_lds() {
-  return (C + CC) * sizeof(float) + ((size_t)C * (CC + 4) + (size_t)CC * (C + 4)) * sizeof(op_t);
+  return (C + CC) * sizeof(float) + (HILO ? 2 : 1) * ((size_t)C * (CC + 4) + (size_t)CC * (C + 4)) * sizeof(op_t);
+}
+
+// [rows][cols] op_t weights -> LDS rows `pitch` apart (8-byte aligned: two 8-byte stores per
+// 16-byte load)
+template <int NT>
+PF_DEV void stage_rows(op_t* dst, const op_t* __restrict__ src, int rows, int cols, int pitch) {
+  for (int c = threadIdx.x; c < rows * (cols / 8); c += NT) {
+    const int row = c / (cols / 8), col = (c % (cols / 8)) * 8;
+    const opx8 v = ld_x8(src + row * cols + col);
+    *reinterpret_cast<opx4*>(&dst[row * pitch + col]) = opx4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<opx4*>(&dst[row * pitch + col + 4]) = opx4{v[4], v[5], v[6], v[7]};
+  }
 }
 
 // resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
-template <int CC, bool FAST>
+// HILO: W_g and W_o come with their residuals wg_lo = W_g - W_g16, wo_lo = W_o - W_o16 (rounded
+// to op_t), and both products run on hi + lo (two MFMAs per fragment): weights good to ~2^-22
+// of their size instead of the 2^-12 of one 16-bit rounding.  The gate's offsets use hi + lo.
+template <int CC, bool FAST, bool HILO = false>
 __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
     const op_t* __restrict__ O, const float* z_in, float* out, const float* __restrict__ lnw,
     const float* __restrict__ lnb, const op_t* __restrict__ wg, const op_t* __restrict__ wo,
+    const op_t* __restrict__ wg_lo, const op_t* __restrict__ wo_lo,
     int B, int N, int ending, int resid, float eps) {
   constexpr int LWG = CC + 4, LWO = C + 4, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t tlds[];
@@ -627,31 +643,32 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
   float* gam = cgate + C;
   op_t* sWg = tlds + 2 * (C + CC);
   op_t* sWo = sWg + C * LWG;
+  op_t* sWgl = sWo + CC * LWO;   // HILO only
+  op_t* sWol = sWgl + C * LWG;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // weights -> LDS (rows are 8-byte aligned: two 8-byte stores per 16-byte load)
-  for (int c = tid; c < C * (CC / 8); c += 64 * TAO_WAVES) {
-    const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
-    const opx8 v = ld_x8(wg + row * CC + col);
-    *reinterpret_cast<opx4*>(&sWg[row * LWG + col]) = opx4{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<opx4*>(&sWg[row * LWG + col + 4]) = opx4{v[4], v[5], v[6], v[7]};
-  }
-  for (int c = tid; c < CC * (C / 8); c += 64 * TAO_WAVES) {
-    const int row = c / (C / 8), col = (c % (C / 8)) * 8;
-    const opx8 v = ld_x8(wo + row * C + col);
-    *reinterpret_cast<opx4*>(&sWo[row * LWO + col]) = opx4{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<opx4*>(&sWo[row * LWO + col + 4]) = opx4{v[4], v[5], v[6], v[7]};
+  stage_rows<64 * TAO_WAVES>(sWg, wg, C, CC, LWG);
+  stage_rows<64 * TAO_WAVES>(sWo, wo, CC, C, LWO);
+  if constexpr (HILO) {
+    stage_rows<64 * TAO_WAVES>(sWgl, wg_lo, C, CC, LWG);
+    stage_rows<64 * TAO_WAVES>(sWol, wo_lo, CC, C, LWO);
   }
   __syncthreads();
   for (int c = tid; c < CC; c += 64 * TAO_WAVES) gam[c] = lnw[c];
   for (int row = tid; row < C; row += 64 * TAO_WAVES) {   // gate offsets -log2(e) W_g beta
     const op_t* w = wg + row * CC;
+    const op_t* wl = wg_lo + row * CC;
     float acc = 0.f;
 #pragma unroll 4
     for (int c = 0; c < CC; c += 8) {
       const opx8 w8 = ld_x8(w + c);
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[c + e];
+      if constexpr (HILO) {
+        const opx8 l8 = ld_x8(wl + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += (float)l8[e] * lnb[c + e];
+      }
     }
     cgate[row] = FAST ? acc : -LOG2E * acc;
   }
@@ -679,6 +696,11 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
       f32x16 g = zero16();
 #pragma unroll
       for (int s = 0; s < KS; ++s) g = mfma32(wfrag_oa(wrow, s, h), xf[s], g);   // D[channel][position]
+      if constexpr (HILO) {
+        const op_t* wlrow = &sWgl[(32 * cb + m) * LWG];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) g = mfma32(wfrag_oa(wlrow, s, h), xf[s], g);
+      }
 #pragma unroll
       for (int gg = 0; gg < 4; ++gg) {
         const int q = 4 * cb + gg;            // chunk: channels oa_channel(q, h) + 0..3
@@ -712,6 +734,11 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
       f32x16 acc = zero16();
 #pragma unroll
       for (int s = 0; s < 8; ++s) acc = mfma32(wfrag_oa(wrow, s, h), og[s], acc);   // D[out][position]
+      if constexpr (HILO) {
+        const op_t* wlrow = &sWol[(32 * ob + m) * LWO];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) acc = mfma32(wfrag_oa(wlrow, s, h), og[s], acc);
+      }
       if constexpr (FAST) mx_fake_quant16(acc);
 #pragma unroll
       for (int gg = 0; gg < 4; ++gg) {
@@ -782,9 +809,11 @@ template <bool OUT_F32>
 int launch_attn(const TaBuffers& t, float* o32, int B, int N, int n_valid, hipStream_t st) {
   if (const int rc = pf_reserve_lds((const void*)ta_attn_kernel<OUT_F32>, TA_LDS, "ta_attn_kernel")) return rc;
   const int total = B * (N / 4) * ((N + 127) / 128);
+  pf_attend_mark(st, 0);
   ta_attn_kernel<OUT_F32><<<total, 64 * TA_WAVES, TA_LDS, st>>>(t.Q, t.K, t.Vt, t.bias32, t.mask16, t.O, o32, N,
                                                                n_valid, total);
   PF_CHECK_LAUNCH("ta_attn_kernel");
+  pf_attend_mark(st, 1);
   return PF_OK;
 }
 
@@ -803,8 +832,9 @@ __global__ void mx8_dequant_kernel(const uint8_t* __restrict__ q, const uint8_t*
   }
 }
 
-// W_q, W_k, W_v, W_g as the kernels read them (op_t [C][CC]).
-struct TaWeights { const op_t *q, *k, *v, *g; };
+// W_q, W_k, W_v, W_g as the kernels read them (op_t [C][CC]); the residuals of W_g and W_o
+// (op_t, or null).
+struct TaWeights { const op_t *q, *k, *v, *g, *g_lo = nullptr, *o_lo = nullptr; };
 
 template <int CC, bool FAST>
 int triatt_run(const pf_triatt_args* a, const TaWeights& w) {
@@ -828,12 +858,26 @@ int triatt_run(const pf_triatt_args* a, const TaWeights& w) {
   int rc = launch_attn<false>(t, nullptr, B, N, n_valid, st);
   if (rc) return rc;
   {
-    const void* fn = (const void*)ta_out_kernel<CC, FAST>;
-    if (const int rc = pf_reserve_lds(fn, tao_lds<CC>(), "ta_out_kernel")) return rc;
     const int grid = (int)min((long)cus, (positions / 32 + TAO_WAVES - 1) / TAO_WAVES);
     const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);
-    ta_out_kernel<CC, FAST><<<grid, 64 * TAO_WAVES, tao_lds<CC>(), st>>>(
-        t.O, a->z_in, a->out, a->ln_w, a->ln_b, w.g, (const op_t*)a->w_o, B, N, a->ending, resid, a->eps);
+    bool hilo = false;
+    if constexpr (!FAST && CC == 128) {   // the residual weights exist for the 16-bit c_z = 128 path
+      if (w.g_lo && w.o_lo) {
+        hilo = true;
+        const void* fn = (const void*)ta_out_kernel<CC, FAST, true>;
+        if (const int rc = pf_reserve_lds(fn, tao_lds<CC, true>(), "ta_out_kernel")) return rc;
+        ta_out_kernel<CC, FAST, true><<<grid, 64 * TAO_WAVES, tao_lds<CC, true>(), st>>>(
+            t.O, a->z_in, a->out, a->ln_w, a->ln_b, w.g, (const op_t*)a->w_o, w.g_lo, w.o_lo, B, N, a->ending, resid,
+            a->eps);
+      }
+    }
+    if (!hilo) {
+      const void* fn = (const void*)ta_out_kernel<CC, FAST>;
+      if (const int rc = pf_reserve_lds(fn, tao_lds<CC>(), "ta_out_kernel")) return rc;
+      ta_out_kernel<CC, FAST><<<grid, 64 * TAO_WAVES, tao_lds<CC>(), st>>>(
+          t.O, a->z_in, a->out, a->ln_w, a->ln_b, w.g, (const op_t*)a->w_o, nullptr, nullptr, B, N, a->ending,
+          resid, a->eps);
+    }
     PF_CHECK_LAUNCH("ta_out_kernel");
   }
   return PF_OK;
@@ -870,7 +914,10 @@ extern "C" int pf_triatt_fwd(const pf_triatt_args* a) {
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: workspace too small (%zu < %zu bytes)", a->workspace_bytes, need);
   if (a->n_valid < 0 || a->n_valid > a->N)
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: n_valid %d outside [0, N=%d]", a->n_valid, a->N);
-  const TaWeights w = {(const op_t*)a->w_q, (const op_t*)a->w_k, (const op_t*)a->w_v, (const op_t*)a->w_g};
+  if ((a->w_g_lo != nullptr) != (a->w_o_lo != nullptr) || (a->w_g_lo && a->C != 128))
+    return pf_fail(PF_E_INVALID, "pf_triatt_fwd: give both weight residuals (w_g_lo, w_o_lo) or neither, C = 128 only");
+  const TaWeights w = {(const op_t*)a->w_q, (const op_t*)a->w_k, (const op_t*)a->w_v, (const op_t*)a->w_g,
+                       (const op_t*)a->w_g_lo, (const op_t*)a->w_o_lo};
   return a->C == 128 ? triatt_run<128, false>(a, w) : triatt_run<64, false>(a, w);
 }
 

@@ -43,6 +43,86 @@ PF_DEV void blk32_store(op_t* lds, int tid, const Blk32& r) {
 }
 
 // ---------------------------------------------------------------------------------
+// Mean correction of the 16-bit input-side weights.  A weight W rounded to W16 makes the same
+// error W_lo = W - W16 at every position; what survives a deep stack is its product with the
+// mean of the normalized activation over positions.  The kernels therefore add, per output row,
+// the fp32 offset  W . beta + W_lo . (gamma * mu),  mu = the mean over positions of the LayerNorm
+// input normalized without its affine part (x_hat), and multiply the rounded activation by W16
+// alone: the remaining error only meets the activation's deviation from its mean.
+//   pair_stats_kernel  mu of z (batch 0) from PS_TILES tiles of 32 consecutive positions spread
+//                      over the grid by Fibonacci hashing (every tile when there are fewer), as
+//                      PS_WG partial sums already divided by the sample size
+//   stats_mu           a workgroup sums the partials into mu (LDS) in its prologue
+// ---------------------------------------------------------------------------------
+#ifndef PF_PS_TILES
+#define PF_PS_TILES 1024
+#endif
+constexpr int PS_WG = 64, PS_WAVES = 4, PS_TILES = PF_PS_TILES;
+constexpr size_t PS_PARTIAL_FLOATS = (size_t)PS_WG * C;
+
+__global__ __launch_bounds__(64 * PS_WAVES) void pair_stats_kernel(const float* __restrict__ z, int N, float eps,
+                                                                   float* __restrict__ partials) {
+  __shared__ float red[PS_WAVES][C][33];   // [wave][channel][lane m] (+1 pad)
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31, wid = tid >> 6;
+  const uint32_t ntiles = (uint32_t)N * N / 32;
+  const uint32_t ns = ntiles < (uint32_t)PS_TILES ? ntiles : (uint32_t)PS_TILES;
+  float acc[64];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) acc[i] = 0.f;
+  for (uint32_t k = blockIdx.x * PS_WAVES + wid; k < ns; k += PS_WG * PS_WAVES) {
+    const uint32_t t = ns == ntiles ? k : (uint32_t)(((uint64_t)k * 2654435761ull) % ntiles);
+    float x[64];
+    load_row_frag<C>(z + ((size_t)t * 32 + m) * C, h, x);
+    float sm = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) sm += x[i];
+    const float mean = xor32_sum(sm) * (1.f / C);
+    float var = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) { const float d = x[i] - mean; var += d * d; }
+    const float rstd = rsqrtf(xor32_sum(var) * (1.f / C) + eps);
+#pragma unroll
+    for (int i = 0; i < 64; ++i) acc[i] += (x[i] - mean) * rstd;
+  }
+  // lane (m, h) holds channels 16 s + 8 h + t in acc[8 s + t]
+#pragma unroll
+  for (int i = 0; i < 64; ++i) red[wid][16 * (i >> 3) + 8 * h + (i & 7)][m] = acc[i];
+  __syncthreads();
+  if (tid < C) {
+    float sum = 0.f;
+    for (int w = 0; w < PS_WAVES; ++w)
+#pragma unroll 8
+      for (int l = 0; l < 32; ++l) sum += red[w][tid][l];
+    partials[blockIdx.x * C + tid] = sum / (32.f * (float)ns);
+  }
+}
+
+// mu[c] (LDS, 128 floats) = the sum of the PS_WG partials; the caller synchronizes.
+PF_DEV void stats_mu(const float* __restrict__ partials, float* mu) {
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    float sum = 0.f;
+#pragma unroll 8
+    for (int g = 0; g < PS_WG; ++g) sum += partials[g * C + c];
+    mu[c] = sum;
+  }
+}
+
+// Offset of one output row: offb (the fp32 W . beta) plus, with the mean correction, the row of
+// the weight residual against gamma * mu (gamma, mu: 128 floats, LDS or global).
+PF_DEV float corrected_offset(float offb, const op_t* __restrict__ lo_row, const float* gamma, const float* mu) {
+  float acc = offb;
+  if (lo_row) {
+#pragma unroll 4
+    for (int c = 0; c < C; c += 8) {
+      const opx8 l8 = ld_x8(lo_row + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (float)l8[e] * gamma[c + e] * mu[c + e];
+    }
+  }
+  return acc;
+}
+
+// ---------------------------------------------------------------------------------
 // Input projection.  Persistent: one workgroup (8 waves, two per SIMD) per CU keeps p_in and
 // g_in ([2 CC][CC] each, op_t as given, so rounded once) resident in LDS, with the LayerNorm's
 // beta folded into fp32 offsets W beta added in the epilogue (gamma scales the normalized z
@@ -68,13 +148,17 @@ constexpr size_t tmp_lds() {
          (size_t)TMP_WAVES * 32 * SPITCH * sizeof(op_t) + TMP_WAVES * sizeof(float);
 }
 
+// offb (optional, fp32 [4 CC]): the exact W_p beta, W_g beta (else computed from the op_t
+// weights); with p_lo / g_lo (the weights' residuals) and the stats partials also the mean
+// correction (see pair_stats_kernel).
 template <int CC, bool MASK>
 __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
     const float* __restrict__ z, const float* __restrict__ mask,
     const float* __restrict__ lnw, const float* __restrict__ lnb,
     const op_t* __restrict__ w_p, const op_t* __restrict__ w_g,
     op_t* __restrict__ opA, op_t* __restrict__ opB, float* __restrict__ amax_parts, int B, int N, int incoming,
-    float eps) {
+    float eps, const float* __restrict__ offb, const op_t* __restrict__ p_lo, const op_t* __restrict__ g_lo,
+    const float* __restrict__ stats) {
   constexpr int LW = CC + 8, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t wlds[];
   float* gam = reinterpret_cast<float*>(wlds);
@@ -92,14 +176,22 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
     st_x8(lg + row * LW + col, ld_x8(w_g + row * CC + col));
   }
   for (int c = tid; c < CC; c += 64 * TMP_WAVES) gam[c] = lnw[c];
+  float* mu = reinterpret_cast<float*>(lg + 2 * CC * LW);   // the output stages, free until the tile loop
+  if (offb && stats) stats_mu(stats, mu);
+  __syncthreads();
   for (int row = tid; row < 4 * CC; row += 64 * TMP_WAVES) {   // offsets W beta (one row per thread)
-    const op_t* w = row < 2 * CC ? w_p + row * CC : w_g + (row - 2 * CC) * CC;
     float acc = 0.f;
+    if (offb) {
+      const op_t* lo = !stats ? nullptr : row < 2 * CC ? p_lo + row * CC : g_lo + (row - 2 * CC) * CC;
+      if constexpr (CC == C) acc = corrected_offset(offb[row], lo, gam, mu);
+    } else {
+      const op_t* w = row < 2 * CC ? w_p + row * CC : w_g + (row - 2 * CC) * CC;
 #pragma unroll 4
-    for (int c = 0; c < CC; c += 8) {
-      const opx8 w8 = ld_x8(w + c);
+      for (int c = 0; c < CC; c += 8) {
+        const opx8 w8 = ld_x8(w + c);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[c + e];
+        for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[c + e];
+      }
     }
     cbias[row] = row < 2 * CC ? acc : -LOG2E * acc;
   }
@@ -435,35 +527,40 @@ __global__ __launch_bounds__(64 * TMD_WAVES, 1) void tm_contract_dma_kernel(
 // ---------------------------------------------------------------------------------
 constexpr int TMO_WAVES = 8, XSP = 40;   // per-wave X stage: [CC channels][32 pairs + 8]
 // LDS: the offsets W_p beta_out [CC], -log2(e) W_g beta_in [CC] and gamma_out [CC], gamma_in [CC]
-// (fp32, first: small immediate offsets), then W_p, W_g [CC][CC + 4] op_t, then the per-wave
-// X stages
-template <int CC>
+// (fp32, first: small immediate offsets), then W_p, W_g [CC][CC + 4] op_t, (HILO) W_p's residual
+// in the same layout, then the per-wave X stages (HILO: half the channels, filled twice a tile)
+template <int CC, bool HILO = false>
 constexpr size_t tmo_lds() {
-  return 4 * CC * sizeof(float) + (size_t)2 * CC * (CC + 4) * sizeof(op_t) +
-         (size_t)TMO_WAVES * CC * XSP * sizeof(op_t);
+  return 4 * CC * sizeof(float) + (size_t)(HILO ? 3 : 2) * CC * (CC + 4) * sizeof(op_t) +
+         (size_t)TMO_WAVES * (HILO ? CC / 2 : CC) * XSP * sizeof(op_t);
 }
 
 // resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
 // X is read back times x_scale, or, when nparts > 0, divided by the contraction's
 // x_store_scale of the operand maxima in amax_parts (contraction length N).
-template <typename XT, int CC>
+// HILO: p_out comes with its rounding residual w_pout_lo = p_out - p_out16 (op_t) and the
+// output projection runs on both (two MFMAs per fragment: weights good to ~2^-22 of their size).
+template <typename XT, int CC, bool HILO = false>
 __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
     const XT* __restrict__ X, float x_scale, const float* __restrict__ amax_parts, int nparts,
     const float* z_in, float* out,
     const float* __restrict__ lni_w, const float* __restrict__ lni_b,
     const float* __restrict__ lno_w, const float* __restrict__ lno_b,
-    const op_t* __restrict__ w_pout, const op_t* __restrict__ w_gout,
-    int B, int N, int resid, float eps) {
+    const op_t* __restrict__ w_pout, const op_t* __restrict__ w_gout, const op_t* __restrict__ w_pout_lo,
+    int B, int N, int resid, float eps, const float* __restrict__ offb_g, const op_t* __restrict__ gout_lo,
+    const float* __restrict__ stats) {
   constexpr int LW = CC + 4, KS = CC / 16;
+  constexpr int XCH = HILO ? CC / 2 : CC;   // channels per X stage fill
   extern __shared__ __attribute__((aligned(16))) op_t olds[];
   float* cbias = reinterpret_cast<float*>(olds);   // [0, CC): p, [CC, 2 CC): g
   float* gam_o = cbias + 2 * CC;
   float* gam_i = gam_o + CC;
   op_t* sWp = olds + 4 * CC * 2;
   op_t* sWg = sWp + CC * LW;
+  op_t* sWpl = sWg + CC * LW;   // HILO only
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  XT* xs = reinterpret_cast<XT*>(sWg + CC * LW) + wid * CC * XSP;   // this wave's X stage
+  XT* xs = reinterpret_cast<XT*>(sWg + (HILO ? 2 : 1) * CC * LW) + wid * XCH * XSP;   // this wave's X stage
   // weights -> LDS (rows are 8-byte aligned: two 8-byte stores per 16-byte load), gamma, and
   // the offsets W beta (one row per thread)
   for (int c = tid; c < CC * (CC / 8); c += 64 * TMO_WAVES) {
@@ -473,13 +570,27 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
     *reinterpret_cast<opx4*>(&sWp[row * LW + col + 4]) = opx4{vp[4], vp[5], vp[6], vp[7]};
     *reinterpret_cast<opx4*>(&sWg[row * LW + col]) = opx4{vg[0], vg[1], vg[2], vg[3]};
     *reinterpret_cast<opx4*>(&sWg[row * LW + col + 4]) = opx4{vg[4], vg[5], vg[6], vg[7]};
+    if constexpr (HILO) {
+      const opx8 vl = ld_x8(w_pout_lo + row * CC + col);
+      *reinterpret_cast<opx4*>(&sWpl[row * LW + col]) = opx4{vl[0], vl[1], vl[2], vl[3]};
+      *reinterpret_cast<opx4*>(&sWpl[row * LW + col + 4]) = opx4{vl[4], vl[5], vl[6], vl[7]};
+    }
   }
   for (int c = tid; c < CC; c += 64 * TMO_WAVES) {
     gam_o[c] = lno_w[c];
     gam_i[c] = lni_w[c];
   }
+  float* mu = reinterpret_cast<float*>(xs - wid * XCH * XSP);   // the X stages, free until the tile loop
+  if (offb_g && stats) stats_mu(stats, mu);
+  __syncthreads();
   for (int row = tid; row < 2 * CC; row += 64 * TMO_WAVES) {
     const bool g = row >= CC;
+    if (g && offb_g) {   // gate offsets from the exact g_out beta (+ the mean correction)
+      if constexpr (CC == C)
+        cbias[row] = -LOG2E * corrected_offset(offb_g[row - CC], stats ? gout_lo + (row - CC) * CC : nullptr,
+                                               gam_i, mu);
+      continue;
+    }
     const op_t* w = g ? w_gout + (row - CC) * CC : w_pout + row * CC;
     const float* bet = g ? lni_b : lno_b;
     float acc = 0.f;
@@ -488,6 +599,13 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
       const opx8 w8 = ld_x8(w + c);
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc += (float)w8[e] * bet[c + e];
+      if constexpr (HILO) {
+        if (!g) {
+          const opx8 l8 = ld_x8(w_pout_lo + row * CC + c);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc += (float)l8[e] * bet[c + e];
+        }
+      }
     }
     cbias[row] = g ? -LOG2E * acc : acc;
   }
@@ -499,23 +617,29 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
     asm volatile("" ::: "memory");   // the offsets are re-read from LDS each tile, not pinned in VGPRs
     const long p0 = 32l * t;                       // first pair (global index b*NN + i*N + j)
     const int b = pos_tile(t, N).b;
-    {
-      // X[b][ch][q0 .. q0+31]: 16-byte chunk c -> channel c >> 2, pairs 8*(c & 3) ..
-      const XT* src = X + (long)b * CC * NN + (p0 - (long)b * NN);
-#pragma unroll
-      for (int k = 0; k < CC / 16; ++k) {
-        const int c = lane + 64 * k, ch = c >> 2, col = (c & 3) * 8;
-        *reinterpret_cast<opx8*>(xs + ch * XSP + col) = *reinterpret_cast<const opx8*>(src + (long)ch * NN + col);
-      }
-    }
     const long pair = p0 + m;
     opx8 xo[KS], xi[KS];
     {
+      // X[b][ch][q0 .. q0+31]: 16-byte chunk c -> channel c >> 2, pairs 8*(c & 3) ..; with HILO
+      // in two fills of CC/2 channels (chunks q < CC/16 of the output-aligned order are
+      // channels < CC/2).  A wave's LDS accesses complete in order, so the second fill does not
+      // overtake the first one's reads.
+      const XT* src = X + (long)b * CC * NN + (p0 - (long)b * NN);
       float xv[CC / 2];
 #pragma unroll
-      for (int q = 0; q < CC / 8; ++q)
+      for (int half = 0; half < CC / XCH; ++half) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xv[4 * q + e] = (float)xs[(oa_channel(q, h) + e) * XSP + m] * x_scale;
+        for (int k = 0; k < XCH / 16; ++k) {
+          const int c = lane + 64 * k, ch = c >> 2, col = (c & 3) * 8;
+          *reinterpret_cast<opx8*>(xs + ch * XSP + col) =
+              *reinterpret_cast<const opx8*>(src + (long)(ch + half * XCH) * NN + col);
+        }
+#pragma unroll
+        for (int q = half * XCH / 8; q < (half + 1) * XCH / 8; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            xv[4 * q + e] = (float)xs[(oa_channel(q, h) - half * XCH + e) * XSP + m] * x_scale;
+      }
       ln_oa_gamma_to_frag<CC>(xv, h, gam_o, eps, xo);
     }
     float zr[CC / 2];
@@ -530,6 +654,11 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
       for (int s = 0; s < KS; ++s) {
         P = mfma32(wfrag_oa(wp, s, h), xo[s], P);   // rows = output channel, cols = pair
         G = mfma32(wfrag_oa(wg, s, h), xi[s], G);
+      }
+      if constexpr (HILO) {
+        const op_t* wpl = &sWpl[(32 * ob + m) * LW];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) P = mfma32(wfrag_oa(wpl, s, h), xo[s], P);
       }
       float* orow = out + pair * CC;
 #pragma unroll
@@ -585,7 +714,8 @@ int launch_contract(const op_t* opA, const op_t* opB, OutT* X, int planes, int N
   return PF_OK;
 }
 
-// Workspace: opA, opB, X planes (op_t), then TM_MAX_PARTS floats of per-workgroup maxima.
+// Workspace: opA, opB, X planes (op_t), then TM_MAX_PARTS floats of per-workgroup maxima, then
+// the PS_WG x 128 partial sums of the mean correction.
 constexpr int TM_MAX_PARTS = 1024;
 
 template <int CC>
@@ -597,6 +727,16 @@ int trimul_run(const pf_trimul_args* a) {
   op_t* opB = opA + planes;
   op_t* X = opB + planes;
   float* amax_parts = reinterpret_cast<float*>(X + planes);
+  float* stats = amax_parts + TM_MAX_PARTS;
+  // mean correction: exact beta offsets, the three residuals, one batch element (c_z = 128)
+  const bool meanfix = CC == C && B == 1 && a->in_offsets && a->p_in_lo && a->g_in_lo && a->g_out_lo;
+  if (meanfix) {
+    pair_stats_kernel<<<PS_WG, 64 * PS_WAVES, 0, st>>>(a->z_in, N, a->eps, stats);
+    PF_CHECK_LAUNCH("pair_stats_kernel");
+  } else {
+    stats = nullptr;
+  }
+  const float* offb = CC == C ? a->in_offsets : nullptr;
   const long positions = (long)B * N * N;
   const int cus = device_cus();
   if (cus <= 0) return pf_fail(PF_E_LAUNCH, "pf_trimul_fwd: cannot query the device");
@@ -607,18 +747,34 @@ int trimul_run(const pf_trimul_args* a) {
     if (const int rc = pf_reserve_lds((const void*)kern, tmp_lds<CC>(), "tm_proj_kernel")) return rc;
     kern<<<grid_proj, 64 * tmp_waves<CC>(), tmp_lds<CC>(), st>>>(
         a->z_in, a->pair_mask, a->norm_in_w, a->norm_in_b, (const op_t*)a->p_in_w, (const op_t*)a->g_in_w, opA, opB,
-        amax_parts, B, N, a->direction, a->eps);
+        amax_parts, B, N, a->direction, a->eps, offb, (const op_t*)a->p_in_lo, (const op_t*)a->g_in_lo, stats);
     PF_CHECK_LAUNCH("tm_proj_kernel");
   }
   const int rc = launch_contract<op_t>(opA, opB, X, B * CC, N, X_STORE_SCALE, st, amax_parts, grid_proj);
   if (rc != PF_OK) return rc;
   {
-    if (const int rc2 = pf_reserve_lds((const void*)tm_out_kernel<op_t, CC>, tmo_lds<CC>(), "tm_out_kernel"))
-      return rc2;
     const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);
-    tm_out_kernel<op_t, CC><<<grid_out, 64 * TMO_WAVES, tmo_lds<CC>(), st>>>(
-        X, X_LOAD_SCALE, amax_parts, grid_proj, a->z_in, a->out, a->norm_in_w, a->norm_in_b, a->norm_out_w,
-        a->norm_out_b, (const op_t*)a->p_out_w, (const op_t*)a->g_out_w, B, N, resid, a->eps);
+    bool hilo = false;
+    if constexpr (CC == 128) {   // the residual weights exist for c_z = 128
+      if (a->p_out_lo) {
+        hilo = true;
+        if (const int rc2 = pf_reserve_lds((const void*)tm_out_kernel<op_t, CC, true>, tmo_lds<CC, true>(),
+                                           "tm_out_kernel"))
+          return rc2;
+        tm_out_kernel<op_t, CC, true><<<grid_out, 64 * TMO_WAVES, tmo_lds<CC, true>(), st>>>(
+            X, X_LOAD_SCALE, amax_parts, grid_proj, a->z_in, a->out, a->norm_in_w, a->norm_in_b, a->norm_out_w,
+            a->norm_out_b, (const op_t*)a->p_out_w, (const op_t*)a->g_out_w, (const op_t*)a->p_out_lo, B, N, resid,
+            a->eps, offb ? offb + 4 * CC : nullptr, (const op_t*)a->g_out_lo, stats);
+      }
+    }
+    if (!hilo) {
+      if (const int rc2 = pf_reserve_lds((const void*)tm_out_kernel<op_t, CC>, tmo_lds<CC>(), "tm_out_kernel"))
+        return rc2;
+      tm_out_kernel<op_t, CC><<<grid_out, 64 * TMO_WAVES, tmo_lds<CC>(), st>>>(
+          X, X_LOAD_SCALE, amax_parts, grid_proj, a->z_in, a->out, a->norm_in_w, a->norm_in_b, a->norm_out_w,
+          a->norm_out_b, (const op_t*)a->p_out_w, (const op_t*)a->g_out_w, nullptr, B, N, resid, a->eps,
+          offb ? offb + 4 * CC : nullptr, (const op_t*)a->g_out_lo, stats);
+    }
     PF_CHECK_LAUNCH("tm_out_kernel");
   }
   return PF_OK;
@@ -632,7 +788,8 @@ int trimul_run(const pf_trimul_args* a) {
 extern "C" size_t pf_trimul_workspace_size(int B, int N, int C_) {
   if (B <= 0 || N <= 0 || (C_ != 128 && C_ != 64)) return 0;
   const size_t planes = (size_t)B * C_ * N * N;
-  return planes * 3 * sizeof(op_t) + TM_MAX_PARTS * sizeof(float);   // opA, opB, X, operand maxima
+  // opA, opB, X, operand maxima, mean-correction partials
+  return planes * 3 * sizeof(op_t) + (TM_MAX_PARTS + PS_PARTIAL_FLOATS) * sizeof(float);
 }
 
 extern "C" int pf_trimul_fwd(const pf_trimul_args* a) {
@@ -649,6 +806,10 @@ extern "C" int pf_trimul_fwd(const pf_trimul_args* a) {
   if (!a->z_in || !a->out || !a->norm_in_w || !a->norm_in_b || !a->p_in_w || !a->g_in_w ||
       !a->norm_out_w || !a->norm_out_b || !a->p_out_w || !a->g_out_w || !a->workspace)
     return pf_fail(PF_E_INVALID, "pf_trimul_fwd: null pointer argument");
+  if ((a->p_out_lo || a->in_offsets || a->p_in_lo || a->g_in_lo || a->g_out_lo) && a->C != 128)
+    return pf_fail(PF_E_INVALID, "pf_trimul_fwd: weight residuals and exact offsets are supported for c_z = 128 only");
+  if ((a->p_in_lo || a->g_in_lo || a->g_out_lo) && !(a->in_offsets && a->p_in_lo && a->g_in_lo && a->g_out_lo))
+    return pf_fail(PF_E_INVALID, "pf_trimul_fwd: the mean correction needs in_offsets, p_in_lo, g_in_lo and g_out_lo");
   const size_t need = pf_trimul_workspace_size(a->B, a->N, a->C);
   if (a->workspace_bytes < need)
     return pf_fail(PF_E_INVALID, "pf_trimul_fwd: workspace too small (%zu < %zu bytes)", a->workspace_bytes, need);

@@ -63,6 +63,14 @@ def opw(w: torch.Tensor, device: torch.device, variant: str = DEFAULT_VARIANT) -
     return w.detach().to(device=device, dtype=TORCH_DTYPE[variant]).contiguous()
 
 
+def opw_lo(w: torch.Tensor, device: torch.device, variant: str = DEFAULT_VARIANT) -> torch.Tensor:
+    """The residual of ``opw``: w - float(opw(w)), itself in the operand type, so that hi + lo
+    carries w to ~2^-22 of its size (for kernels that take a weight as two MFMA operands)."""
+    w32 = w.detach().to(device=device, dtype=torch.float32)
+    dt = TORCH_DTYPE[variant]
+    return (w32 - w32.to(dt).to(torch.float32)).to(dt).contiguous()
+
+
 def f32(t: Optional[torch.Tensor], device: torch.device) -> Optional[torch.Tensor]:
     return None if t is None else t.detach().to(device=device, dtype=torch.float32).contiguous()
 
@@ -163,7 +171,10 @@ def launch_trimul(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional[tor
         p_in_w=_ptr(w["p_in.weight"]), g_in_w=_ptr(w["g_in.weight"]),
         norm_out_w=_ptr(w["norm_out.weight"]), norm_out_b=_ptr(w["norm_out.bias"]),
         p_out_w=_ptr(w["p_out.weight"]), g_out_w=_ptr(w["g_out.weight"]),
-        workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
+        workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream(),
+        p_out_lo=_ptr(w.get("p_out.weight.lo")), in_offsets=_ptr(w.get("in_offsets")),
+        p_in_lo=_ptr(w.get("p_in.weight.lo")), g_in_lo=_ptr(w.get("g_in.weight.lo")),
+        g_out_lo=_ptr(w.get("g_out.weight.lo")))
     _lib.check(_lib.load(variant).pf_trimul_fwd(ctypes.byref(a)), "pf_trimul_fwd", variant)
 
 
@@ -183,7 +194,8 @@ def launch_triatt(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional[tor
         ln_w=_ptr(w["layer_norm.weight"]), ln_b=_ptr(w["layer_norm.bias"]), w_bias=_ptr(w["linear.weight"]),
         w_q=_ptr(w["linear_q.weight"]), w_k=_ptr(w["linear_k.weight"]), w_v=_ptr(w["linear_v.weight"]),
         w_g=_ptr(w["linear_g.weight"]), w_o=_ptr(w["linear_o.weight"]),
-        workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream())
+        workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream(),
+        w_g_lo=_ptr(w.get("linear_g.weight.lo")), w_o_lo=_ptr(w.get("linear_o.weight.lo")))
     _lib.check(_lib.load(variant).pf_triatt_fwd(ctypes.byref(a)), "pf_triatt_fwd", variant)
 
 
@@ -192,6 +204,48 @@ def launch_triatt_attend(ws: torch.Tensor, B: int, N: int, n_valid: int = 0, var
     the same (B, N) left in ``ws`` (measurement of the dominant kernel)."""
     _lib.check(_lib.load(variant).pf_triatt_attend_workspace(_ptr(ws), ws.numel(), B, N, n_valid, _stream()),
                "pf_triatt_attend_workspace", variant)
+
+
+def attend_timing(enable: bool, variant: str = DEFAULT_VARIANT) -> None:
+    """Start (clearing the record) or stop in-layer launch timing of the triangle-attention core
+    on this host thread: every attention-core launch made meanwhile is bracketed by HIP events
+    on its stream (a measurement aid; see ``attend_timing_read``)."""
+    _lib.check(_lib.load(variant).pf_attend_timing(1 if enable else 0), "pf_attend_timing", variant)
+
+
+def attend_timing_read(variant: str = DEFAULT_VARIANT):
+    """(summed launch ms, launches) of the attention-core launches recorded since
+    ``attend_timing(True)``; waits for the last one."""
+    ms, n = ctypes.c_double(0.0), ctypes.c_int(0)
+    _lib.check(_lib.load(variant).pf_attend_timing_read(ctypes.byref(ms), ctypes.byref(n)),
+               "pf_attend_timing_read", variant)
+    return ms.value, n.value
+
+
+def mfma_rate_probe(device: torch.device, iters: int = 20000, per_cu: int = 2, reps: int = 3,
+                    variant: str = DEFAULT_VARIANT) -> dict:
+    """Sustained 16-bit MFMA rate of the chip under load (pseudo-random operands, every SIMD
+    issuing back-to-back 32x32x16 MFMAs from ``4 * per_cu`` waves), timed with HIP events: the
+    best of ``reps`` launches after one warm-up."""
+    lib = _lib.load(variant)
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    wgs = cus * per_cu
+    waves = lib.pf_mfma_rate_probe_waves(wgs)
+    sink = torch.empty(waves, dtype=torch.float32, device=device)
+    stream = _stream()
+    best = None
+    for r in range(reps + 1):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        _lib.check(lib.pf_mfma_rate_probe(wgs, iters, _ptr(sink), stream), "pf_mfma_rate_probe", variant)
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b)
+        if r and (best is None or ms < best):
+            best = ms
+    flop = waves * iters * 4 * 32768
+    return {"tflops": round(flop / (best * 1e-3) / 1e12, 1), "launch_ms": round(best, 3), "waves": waves,
+            "mfma_per_wave": iters * 4, "finite": bool(torch.isfinite(sink).all())}
 
 
 def transition_workspace_bytes(rows: int, C: int, hidden: int, variant: str = DEFAULT_VARIANT) -> int:
@@ -268,10 +322,11 @@ def launch_linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor]
 
 def launch_pair_ln_linear(x: torch.Tensor, base: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor,
                           w: torch.Tensor, out: torch.Tensor, eps: float = 1e-5,
-                          variant: str = DEFAULT_VARIANT) -> None:
+                          variant: str = DEFAULT_VARIANT, w_lo: Optional[torch.Tensor] = None) -> None:
+    """out = base + W . LN(x) per pair; with ``w_lo`` (``opw_lo`` of the weight) to ~fp32 accuracy."""
     C = x.shape[-1]
     _lib.check(_lib.load(variant).pf_pair_ln_linear_fwd(_ptr(x), _ptr(base), _ptr(ln_w), _ptr(ln_b), _ptr(w),
-                                                        _ptr(out), x.numel() // C, C, eps, _stream()),
+                                                        _ptr(w_lo), _ptr(out), x.numel() // C, C, eps, _stream()),
                "pf_pair_ln_linear_fwd", variant)
 
 

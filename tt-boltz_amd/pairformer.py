@@ -120,10 +120,21 @@ class Options:
     ``single_delay``: how many of the next layer's pair operations (0-4) go ahead of the
     overlapped single track (it then starts beside the following ones).  The default 1 keeps it
     off the outgoing triangle multiplication, whose contraction it slows the most (N = 512:
-    1.254 vs 1.263 ms per layer with 0; 1.269 with 2, 1.308 with 4)."""
+    1.254 vs 1.263 ms per layer with 0; 1.269 with 2, 1.308 with 4).
+    ``weight_residuals``: the pair kernels whose weights fit twice in LDS (the triangle
+    attention's gate and output projection, the triangle multiplication's output projection,
+    the recycling projection) take each 16-bit weight together with its rounding residual and
+    multiply by both (default on).  A 16-bit weight's rounding error is the same at every
+    position, so it adds up coherently through a deep stack; with the residual the weights are
+    good to ~2^-22 of their size.
+    ``mean_correction``: the triangle multiplication's LN_in-side weights (p_in, g_in, g_out),
+    whose LDS does not hold them twice, get the exact W . beta offsets plus the mean correction
+    (W - W16) . (gamma * mu), mu the mean over positions of the normalized input, estimated per
+    call from sampled positions: the part of their rounding error that every position shares
+    (default on; c_z = 128, batch 1)."""
 
     def __init__(self, eps: float = 1e-5, operand: str = ops.DEFAULT_VARIANT, overlap_single: bool = True,
-                 single_delay: int = 1):
+                 single_delay: int = 1, weight_residuals: bool = True, mean_correction: bool = True):
         if operand not in ops.TORCH_DTYPE:
             raise ValueError(f"operand must be one of {sorted(ops.TORCH_DTYPE)}, got {operand!r}")
         if not 0 <= single_delay <= 4:
@@ -132,6 +143,8 @@ class Options:
         self.operand = operand
         self.overlap_single = overlap_single
         self.single_delay = single_delay
+        self.weight_residuals = weight_residuals
+        self.mean_correction = mean_correction
 
 
 class Module:
@@ -159,6 +172,10 @@ class Module:
     def mat(self, key: str) -> torch.Tensor:
         return ops.opw(self.weights[key], self.device, self.variant)
 
+    def mat_lo(self, key: str) -> torch.Tensor:
+        """The rounding residual of ``mat(key)`` (``ops.opw_lo``)."""
+        return ops.opw_lo(self.weights[key], self.device, self.variant)
+
     def vec(self, key: str) -> torch.Tensor:
         return ops.f32(self.weights[key], self.device)
 
@@ -180,6 +197,16 @@ class TriangleMultiplication(Module):
             self.w.update(ops.mx8_weights(self.weights, self.device, ops.TRIMUL_MX8_KEYS, self.variant))
         else:
             self.w.update({k: self.mat(k) for k in ("p_in.weight", "g_in.weight", "p_out.weight", "g_out.weight")})
+            if self.options.weight_residuals and self.C == C_Z:   # p_out to ~fp32 (hi + lo)
+                self.w["p_out.weight.lo"] = self.mat_lo("p_out.weight")
+            if self.options.mean_correction and self.C == C_Z:
+                # the mean correction of the LN_in-side weights: exact W . beta offsets and the
+                # residuals of p_in, g_in, g_out
+                beta = self.weights["norm_in.bias"].detach().double().cpu()
+                self.w["in_offsets"] = torch.cat([self.weights[k].detach().double().cpu() @ beta for k in
+                                                  ("p_in.weight", "g_in.weight", "g_out.weight")]).to(
+                    device=self.device, dtype=torch.float32)
+                self.w.update({k + ".lo": self.mat_lo(k) for k in ("p_in.weight", "g_in.weight", "g_out.weight")})
 
     def workspace_bytes(self, B: int, N: int) -> int:
         if self.fast:
@@ -223,6 +250,8 @@ class TriangleAttention(Module):
             self.w.update(ops.mx8_weights(self.weights, self.device, ops.TRIATT_MX8_KEYS, self.variant))
         else:
             self.w.update({k: self.mat(k) for k in ops.TRIATT_MX8_KEYS})
+            if self.options.weight_residuals and self.C == C_Z:
+                self.w.update({k + ".lo": self.mat_lo(k) for k in ("linear_g.weight", "linear_o.weight")})
 
     def workspace_bytes(self, B: int, N: int) -> int:
         if self.fast:
@@ -355,6 +384,10 @@ class SingleTrackStream:
         """Make the caller's stream wait for every single-track update issued so far."""
         self.wait_previous()
         self.done = None
+
+    def discard(self) -> None:
+        """Drop a deferred single track that was never queued (its call raised)."""
+        self.pending = None
 
 
 class PairformerLayer(Module):
@@ -503,10 +536,18 @@ class Pairformer(Module):
         if ws is None:
             ws = ops.workspace(self.workspace_bytes(B, N), z.device)
         single = self.single_track(z.shape[0], z.shape[1], z.device) if s is not None else None
-        for block in self.blocks:
-            s, z = block(s, z, pair_mask, mask, ws, n_valid, single)
-        if single is not None:
-            single.join()
+        if single is None:
+            for block in self.blocks:
+                s, z = block(s, z, pair_mask, mask, ws, n_valid, single)
+            return s, z
+        single.discard()   # a cached stream never carries a closure over another call's tensors
+        try:
+            for block in self.blocks:
+                s, z = block(s, z, pair_mask, mask, ws, n_valid, single)
+        except BaseException:
+            single.discard()
+            raise
+        single.join()
         return s, z
 
 
@@ -606,6 +647,9 @@ class TrunkRecycler:
         self.z_norm_w, self.z_norm_b = ops.f32(w["z_norm.weight"], dev), ops.f32(w["z_norm.bias"], dev)
         self.s_rec = ops.opw(w["s_recycle.weight"], dev, v)
         self.z_rec = ops.opw(w["z_recycle.weight"], dev, v)
+        # the pair recycling projection to ~fp32 (its input is the same beta at every pair at
+        # a pass's start, so a 16-bit rounding would shift all of z alike)
+        self.z_rec_lo = ops.opw_lo(w["z_recycle.weight"], dev, v) if self.options.weight_residuals else None
 
     def __call__(self, s_init: torch.Tensor, z_init: torch.Tensor, mask: Optional[torch.Tensor],
                  recycling_steps: int, pass_hook=None, n_valid: int = 0, msa_inputs: Optional[dict] = None):
@@ -630,7 +674,8 @@ class TrunkRecycler:
         for i in range(recycling_steps + 1):
             ops.launch_layernorm(s, self.s_norm_w, self.s_norm_b, s_tmp, self.options.eps, v)
             ops.launch_linear(s_tmp, self.s_rec, None, s_init, s, v)
-            ops.launch_pair_ln_linear(z, z_init, self.z_norm_w, self.z_norm_b, self.z_rec, z, self.options.eps, v)
+            ops.launch_pair_ln_linear(z, z_init, self.z_norm_w, self.z_norm_b, self.z_rec, z, self.options.eps, v,
+                                      self.z_rec_lo)
             if self.msa is not None:
                 z_msa.copy_(z)
                 self.msa(z_msa, pair_mask=pair_mask, n_valid=n_valid, **msa_inputs)
