@@ -138,6 +138,14 @@ typedef struct pf_triatt_args {
    * the 2^-12 rounding of 16-bit weights is the same at every position, and it is what makes
    * a deep stack drift from the fp32 reference. */
   const void* w_g_lo; const void* w_o_lo;
+  /* Optional (NULL = unused; C = 128 only): in_offsets fp32 [3C + H] = linear_q / _k / _v
+   * .weight . beta and linear.weight . beta in fp32 from the unrounded weights (beta =
+   * layer_norm.bias), used instead of the 16-bit weights' W16 . beta; with also the residuals
+   * of the kernel's gamma-folded weights, w_*_lo = W diag(gamma) - op(op(W) diag(gamma)) in the
+   * operand type (op = rounding to it; [H*D][C] for q, k, v, [H][C] for the bias), and B == 1,
+   * the mean correction of pf_trimul_args for those rows. */
+  const float* in_offsets;
+  const void* w_q_lo; const void* w_k_lo; const void* w_v_lo; const void* w_bias_lo;
 } pf_triatt_args;
 
 size_t pf_triatt_workspace_size(int B, int N, int C, int H, int D);
@@ -180,6 +188,9 @@ typedef struct pf_transition_args {
   const void* fc3_w;                          /* bf16 [C][hidden] */
   void* workspace; size_t workspace_bytes;
   void* stream;
+  /* Optional (NULL = unused; C = 128 only): the residual fc3 - fc3_16 of fc3.weight in the
+   * operand type; the output projection then runs on fc3_16 + residual (see pf_triatt_args). */
+  const void* fc3_lo;
 } pf_transition_args;
 
 size_t pf_transition_workspace_size(long rows, int C, int hidden);

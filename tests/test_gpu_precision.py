@@ -20,13 +20,13 @@ from test_gpu_parity import _dev_w, _inputs, _sub_w, check, stats
 pytestmark = pytest.mark.gpu
 
 
-def _same(a, b, name):
+def _same(a, b, name, mean_tol=2e-6):
     """Equal up to fp32 summation order: hi.x + lo.x and (2 hi).x differ in the last bits of an
     fp32 sum, which now and then moves a later 16-bit rounding by one step (max ~1e-4 of the
     rms); a wiring mistake (wrong row, pitch or operand) moves every element by O(1)."""
     mx, mn = stats(a, b)
     print(f"[precision] {name}: max/rms={mx:.3e} mean/rms={mn:.3e}", flush=True)
-    assert torch.isfinite(a).all() and mx <= 2e-3 and mn <= 2e-6, f"{name}: max/rms={mx:.3e} mean/rms={mn:.3e}"
+    assert torch.isfinite(a).all() and mx <= 2e-3 and mn <= mean_tol, f"{name}: max/rms={mx:.3e} mean/rms={mn:.3e}"
 
 
 @pytest.mark.parametrize("ending", [False, True])
@@ -142,3 +142,35 @@ def test_trimul_mean_correction_removes_coherent_error(gpu, direction):
           f"mean-corrected {coh_fixed:.3e}", flush=True)
     check(f"trimul mean-corrected direction={direction}", b, want)
     assert coh_fixed < 0.35 * coh_plain
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_transition_residual_weight_wiring(gpu, with_bias):
+    """tr_pair with fc3 given as (W16, W16) equals the plain kernel on 2 W16 (the four-block
+    ring of that path, with and without the fused single-track pair bias)."""
+    N = 128
+    w = _dev_w(_sub_w(27, "transition_z"), gpu)
+    _, z, _, _ = _inputs(N, 28)
+    s = torch.randn((1, N, 384), generator=torch.Generator().manual_seed(29)).to(gpu)
+    zd = z.to(gpu).contiguous()
+    hilo = dict(w)
+    hilo["fc3.weight.lo"] = w["fc3.weight"]
+    doubled = dict(w)
+    doubled["fc3.weight"] = (2 * w["fc3.weight"].float()).to(w["fc3.weight"].dtype)
+    outs, biases = [], []
+    for ww in (hilo, doubled):
+        out = torch.empty_like(zd)
+        pb = None
+        if with_bias:
+            apb = _dev_w(_sub_w(30, "attention"), gpu)
+            apb_ws = ops.workspace(ops.apb_workspace_bytes(1, N, 384, 16), gpu)
+            pb = (s, apb, 16, apb_ws, 1e-5)
+        ops.launch_transition(zd, out, ww, None, accumulate=True, pair_bias=pb)
+        outs.append(out)
+        if with_bias:
+            off = 5 * N * 384 * 4   # q, k, v, g, o.g [N][384] fp32, then the bias [16][N][N]
+            biases.append(apb_ws[off: off + 16 * N * N * 4].view(torch.float32).clone())
+    _same(outs[0], outs[1], f"transition fc3 hi+lo(=hi) vs doubled (pair bias {with_bias})")
+    if with_bias:
+        # the bias is a 16-bit product of LN(z): each flipped z rounding moves it again (measured 2.7e-6)
+        _same(biases[0], biases[1], "transition fused pair bias with fc3 hi+lo(=hi) vs doubled", 1e-5)

@@ -43,7 +43,8 @@ class TriattArgs(ctypes.Structure):
         ("ln_w", c_void_p), ("ln_b", c_void_p), ("w_bias", c_void_p),
         ("w_q", c_void_p), ("w_k", c_void_p), ("w_v", c_void_p), ("w_g", c_void_p), ("w_o", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
-        ("w_g_lo", c_void_p), ("w_o_lo", c_void_p),
+        ("w_g_lo", c_void_p), ("w_o_lo", c_void_p), ("in_offsets", c_void_p), ("w_q_lo", c_void_p),
+        ("w_k_lo", c_void_p), ("w_v_lo", c_void_p), ("w_bias_lo", c_void_p),
     ]
 
 
@@ -65,6 +66,7 @@ class TransitionArgs(ctypes.Structure):
         ("x_in", c_void_p), ("out", c_void_p), ("norm_w", c_void_p), ("norm_b", c_void_p),
         ("fc1_w", c_void_p), ("fc2_w", c_void_p), ("fc3_w", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
+        ("fc3_lo", c_void_p),
     ]
 
 

@@ -575,3 +575,89 @@ PF_DEV void pair_update_epilogue(const f32x16 (&acc)[4], float* out, long rows, 
     if (hd < zb.H) brow[hd * zb.NN] = hb[r] * 1.4426950408889634f;
   }
 }
+
+namespace {
+
+// ---------------------------------------------------------------------------------
+// Mean correction of the 16-bit input-side weights.  A weight W rounded to W16 makes the same
+// error W_lo = W - W16 at every position; what survives a deep stack is its product with the
+// mean of the normalized activation over positions.  The kernels therefore add, per output row,
+// the fp32 offset  W . beta + W_lo . (gamma * mu),  mu = the mean over positions of the LayerNorm
+// input normalized without its affine part (x_hat), and multiply the rounded activation by W16
+// alone: the remaining error only meets the activation's deviation from its mean.
+//   pair_stats_kernel  mu of z (batch 0) from PS_TILES tiles of 32 consecutive positions spread
+//                      over the grid by Fibonacci hashing (every tile when there are fewer), as
+//                      PS_WG partial sums already divided by the sample size
+//   stats_mu           a workgroup sums the partials into mu (LDS) in its prologue
+// ---------------------------------------------------------------------------------
+#ifndef PF_PS_TILES
+#define PF_PS_TILES 1024
+#endif
+constexpr int PS_WG = 64, PS_WAVES = 4, PS_TILES = PF_PS_TILES;
+constexpr int PS_C = 128;   // channels of the pair rows the statistics are taken over
+constexpr size_t PS_PARTIAL_FLOATS = (size_t)PS_WG * PS_C;
+
+__global__ __launch_bounds__(64 * PS_WAVES) void pair_stats_kernel(const float* __restrict__ z, int N, float eps,
+                                                                   float* __restrict__ partials) {
+  __shared__ float red[PS_WAVES][PS_C][33];   // [wave][channel][lane m] (+1 pad)
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31, wid = tid >> 6;
+  const uint32_t ntiles = (uint32_t)N * N / 32;
+  const uint32_t ns = ntiles < (uint32_t)PS_TILES ? ntiles : (uint32_t)PS_TILES;
+  float acc[64];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) acc[i] = 0.f;
+  for (uint32_t k = blockIdx.x * PS_WAVES + wid; k < ns; k += PS_WG * PS_WAVES) {
+    const uint32_t t = ns == ntiles ? k : (uint32_t)(((uint64_t)k * 2654435761ull) % ntiles);
+    float x[64];
+    load_row_frag<PS_C>(z + ((size_t)t * 32 + m) * PS_C, h, x);
+    float sm = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) sm += x[i];
+    const float mean = xor32_sum(sm) * (1.f / PS_C);
+    float var = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i) { const float d = x[i] - mean; var += d * d; }
+    const float rstd = rsqrtf(xor32_sum(var) * (1.f / PS_C) + eps);
+#pragma unroll
+    for (int i = 0; i < 64; ++i) acc[i] += (x[i] - mean) * rstd;
+  }
+  // lane (m, h) holds channels 16 s + 8 h + t in acc[8 s + t]
+#pragma unroll
+  for (int i = 0; i < 64; ++i) red[wid][16 * (i >> 3) + 8 * h + (i & 7)][m] = acc[i];
+  __syncthreads();
+  if (tid < PS_C) {
+    float sum = 0.f;
+    for (int w = 0; w < PS_WAVES; ++w)
+#pragma unroll 8
+      for (int l = 0; l < 32; ++l) sum += red[w][tid][l];
+    partials[blockIdx.x * PS_C + tid] = sum / (32.f * (float)ns);
+  }
+}
+
+// mu[c] (LDS, 128 floats) = the sum of the PS_WG partials; the caller synchronizes.
+PF_DEV void stats_mu(const float* __restrict__ partials, float* mu) {
+  for (int c = threadIdx.x; c < PS_C; c += blockDim.x) {
+    float sum = 0.f;
+#pragma unroll 8
+    for (int g = 0; g < PS_WG; ++g) sum += partials[g * PS_C + c];
+    mu[c] = sum;
+  }
+}
+
+// Offset of one output row: offb (the fp32 W . beta) plus, with the mean correction, the row of
+// the weight residual against gamma * mu (gamma, mu: 128 floats, LDS or global; gamma = nullptr
+// when the kernel folds gamma into its weights, whose residual then already carries it).
+PF_DEV float corrected_offset(float offb, const op_t* __restrict__ lo_row, const float* gamma, const float* mu) {
+  float acc = offb;
+  if (lo_row) {
+#pragma unroll 4
+    for (int c = 0; c < PS_C; c += 8) {
+      const opx8 l8 = ld_x8(lo_row + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (float)l8[e] * (gamma ? gamma[c + e] : 1.f) * mu[c + e];
+    }
+  }
+  return acc;
+}
+
+}  // namespace

@@ -33,17 +33,24 @@ PF_DEV opx8 lds_x8(const char* p) { return *reinterpret_cast<const opx8*>(p); }
 //                  chunks, chunk c at slot c ^ swz4(R)
 // so every fragment read (one 16-byte chunk from each of 32 consecutive rows) is free of
 // bank conflicts.
+// HILO: fc3 also comes with its rounding residual w3_lo = fc3 - fc3_16 (op_t), staged as a
+// fourth block beside W3 and multiplied in as a second MFMA per fragment, so the output
+// projection runs on weights good to ~2^-22 of their size; the larger ring leaves room for two
+// workgroups per CU instead of three.
 constexpr int TRW = 4;
 constexpr int TR_BLK = 8192;                 // bytes of one fp16 weight block
 constexpr int TR_STAGE = 3 * TR_BLK;
+template <bool HILO>
+constexpr int tr_stage() { return (HILO ? 4 : 3) * TR_BLK; }
 PF_DEV int tr_swz4(int r) { return (r >> 2) & 3; }
 
-template <bool ZBIAS>
-__global__ __launch_bounds__(64 * TRW, 3) void tr_pair_kernel(
+template <bool ZBIAS, bool HILO = false>
+__global__ __launch_bounds__(64 * TRW, HILO ? 2 : 3) void tr_pair_kernel(
     const float* x_in, float* out, const float* __restrict__ lnw, const float* __restrict__ lnb,
     const op_t* __restrict__ w1, const op_t* __restrict__ w2, const op_t* __restrict__ w3,
-    long rows, int hidden, int accumulate, float eps, ZBiasArgs zb) {
-  __shared__ __attribute__((aligned(16))) char tl[2 * TR_STAGE];
+    const op_t* __restrict__ w3_lo, long rows, int hidden, int accumulate, float eps, ZBiasArgs zb) {
+  constexpr int STAGE = tr_stage<HILO>();
+  __shared__ __attribute__((aligned(16))) char tl[2 * STAGE];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const long pos0 = ((long)blockIdx.x * TRW + wid) * 32;
@@ -66,7 +73,7 @@ __global__ __launch_bounds__(64 * TRW, 3) void tr_pair_kernel(
   const uint32_t o3 = 2u * (R3 * hidden + 8 * ((tid & 3) ^ tr_swz4(R3)));
   const uint32_t o3b = 2u * 64 * hidden;
   auto issue = [&](int hb, int buf) {
-    char* st = tl + buf * TR_STAGE + 1024 * wid;
+    char* st = tl + buf * STAGE + 1024 * wid;
     const char* b1 = (const char*)(w1 + (long)32 * hb * C);
     const char* b2 = (const char*)(w2 + (long)32 * hb * C);
     const char* b3 = (const char*)(w3 + 32 * hb);
@@ -75,6 +82,9 @@ __global__ __launch_bounds__(64 * TRW, 3) void tr_pair_kernel(
       __builtin_amdgcn_global_load_lds(b1 + o12 + 4096 * i, st + 4096 * i, 16, 0, 0);
       __builtin_amdgcn_global_load_lds(b2 + o12 + 4096 * i, st + TR_BLK + 4096 * i, 16, 0, 0);
       __builtin_amdgcn_global_load_lds(b3 + o3 + o3b * i, st + 2 * TR_BLK + 4096 * i, 16, 0, 0);
+      if constexpr (HILO)
+        __builtin_amdgcn_global_load_lds((const char*)(w3_lo + 32 * hb) + o3 + o3b * i, st + 3 * TR_BLK + 4096 * i,
+                                         16, 0, 0);
     }
   };
   // fragment read addresses: fc1 / fc2 k-step s of row m; fc3 k-step ks of row 32 ob + m
@@ -91,7 +101,7 @@ __global__ __launch_bounds__(64 * TRW, 3) void tr_pair_kernel(
     __builtin_amdgcn_s_barrier();              // ... for every wave; the other stage is free
     asm volatile("" ::: "memory");
     if (hb + 1 < nhb) issue(hb + 1, (hb + 1) & 1);
-    const char* st = tl + (hb & 1) * TR_STAGE;
+    const char* st = tl + (hb & 1) * STAGE;
     f32x16 a1 = zero16(), a2 = zero16();
 #pragma unroll
     for (int s2 = 0; s2 < 8; ++s2) {
@@ -106,9 +116,28 @@ __global__ __launch_bounds__(64 * TRW, 3) void tr_pair_kernel(
 #pragma unroll
     for (int ob = 0; ob < 4; ++ob)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) acc[ob] = mfma32(lds_x8(st + a3[ks] + 2048 * ob), hf[ks], acc[ob]);
+      for (int ks = 0; ks < 2; ++ks) {
+        acc[ob] = mfma32(lds_x8(st + a3[ks] + 2048 * ob), hf[ks], acc[ob]);
+        if constexpr (HILO) acc[ob] = mfma32(lds_x8(st + TR_BLK + a3[ks] + 2048 * ob), hf[ks], acc[ob]);
+      }
   }
   pair_update_epilogue<ZBIAS>(acc, out, rows, pos0, m, h, accumulate, zb);
+}
+
+// The pair transition's launch: the plain or the residual (HILO) form.
+template <bool ZBIAS>
+int launch_tr_pair(const pf_transition_args* a, const ZBiasArgs& zb, unsigned grid) {
+  hipStream_t st = (hipStream_t)a->stream;
+  if (a->fc3_lo)
+    tr_pair_kernel<ZBIAS, true><<<grid, 64 * TRW, 0, st>>>(
+        a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w, (const op_t*)a->fc2_w, (const op_t*)a->fc3_w,
+        (const op_t*)a->fc3_lo, a->rows, a->hidden, a->accumulate, a->eps, zb);
+  else
+    tr_pair_kernel<ZBIAS, false><<<grid, 64 * TRW, 0, st>>>(
+        a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w, (const op_t*)a->fc2_w, (const op_t*)a->fc3_w,
+        nullptr, a->rows, a->hidden, a->accumulate, a->eps, zb);
+  PF_CHECK_LAUNCH("tr_pair_kernel");
+  return PF_OK;
 }
 
 // Transition with C = 64, hidden = 256 (the MSA transition, tt_bio/reference.py:1333,
@@ -412,14 +441,9 @@ extern "C" int pf_transition_fwd(const pf_transition_args* a) {
   if (!a->x_in || !a->out || !a->norm_w || !a->norm_b || !a->fc1_w || !a->fc2_w || !a->fc3_w)
     return pf_fail(PF_E_INVALID, "pf_transition_fwd: null pointer argument");
   hipStream_t st = (hipStream_t)a->stream;
-  if (a->C == C) {
-    const unsigned grid = (unsigned)((a->rows + 32 * TRW - 1) / (32 * TRW));
-    tr_pair_kernel<false><<<grid, 64 * TRW, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w,
-                                                     (const op_t*)a->fc2_w, (const op_t*)a->fc3_w, a->rows,
-                                                     a->hidden, a->accumulate, a->eps, ZBiasArgs{});
-    PF_CHECK_LAUNCH("tr_pair_kernel");
-    return PF_OK;
-  }
+  if (a->fc3_lo && a->C != C)
+    return pf_fail(PF_E_INVALID, "pf_transition_fwd: the fc3 residual (fc3_lo) is supported for C = 128 only");
+  if (a->C == C) return launch_tr_pair<false>(a, ZBiasArgs{}, (unsigned)((a->rows + 32 * TRW - 1) / (32 * TRW)));
   if (a->C == 64 && a->hidden == 256) {
     const int cus = device_cus();
     if (cus <= 0) return pf_fail(PF_E_LAUNCH, "tr64_kernel: cannot query the device");
@@ -496,10 +520,5 @@ extern "C" int pf_transition_pair_bias_fwd(const pf_transition_args* a, const pf
   if (a->rows != (long)apb->B * NN)
     return pf_fail(PF_E_INVALID, "pf_transition_pair_bias_fwd: rows %ld != B*N*N = %ld", a->rows, (long)apb->B * NN);
   const ZBiasArgs zb{apb->zln_w, apb->zln_b, (const op_t*)apb->w_z, pf_apb_bias_ptr(apb), NN, apb->H, apb->eps};
-  const unsigned grid = (unsigned)(a->rows / (32 * TRW));   // N % 32 == 0: whole workgroups
-  tr_pair_kernel<true><<<grid, 64 * TRW, 0, (hipStream_t)a->stream>>>(
-      a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w, (const op_t*)a->fc2_w, (const op_t*)a->fc3_w,
-      a->rows, a->hidden, a->accumulate, a->eps, zb);
-  PF_CHECK_LAUNCH("tr_pair_kernel");
-  return PF_OK;
+  return launch_tr_pair<true>(a, zb, (unsigned)(a->rows / (32 * TRW)));   // N % 32 == 0: whole workgroups
 }

@@ -70,11 +70,19 @@ PF_DEV op_t mask_term(bool pad, float mv) {
 // ---------------------------------------------------------------------------------
 constexpr int TAP_WAVES = 8;
 constexpr int TAP_ROWS = 3 * C + 32;   // q, k, v rows, then 32 bias rows (H used, rest zero)
+// LDS: the weights [TAP_ROWS][CC + 8] op_t, their accumulator starts [TAP_ROWS] fp32, then (FAST)
+// the per-wave V block scales or the mean-correction mu [128] (the two never coexist)
 template <int CC, bool FAST = false>
 constexpr size_t tap_lds() {
   return (size_t)TAP_ROWS * (CC + 8) * sizeof(op_t) + TAP_ROWS * sizeof(float) +
-         (FAST ? TAP_WAVES * 32 * sizeof(float) : 0);
+         (FAST ? TAP_WAVES * 32 * sizeof(float) : PS_C * sizeof(float));
 }
+
+// offb (optional, fp32 [3 C + H]): the exact W beta of the q, k, v and bias rows (else computed
+// from the op_t weights); with lo (the residuals of the kernel's gamma-folded weights, W diag(gamma)
+// - op_t(W16 diag(gamma)), four [rows][CC] arrays for q, k, v, bias) and the stats partials also
+// the mean correction of those weights (see pair_stats_kernel).
+struct TaMeanFix { const float* offb; const op_t* lo[4]; const float* stats; };
 
 template <int CC, bool FAST>
 __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
@@ -83,13 +91,14 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
     const op_t* __restrict__ wq, const op_t* __restrict__ wk, const op_t* __restrict__ wv,
     const op_t* __restrict__ wb, op_t* __restrict__ Q, op_t* __restrict__ K,
     op_t* __restrict__ Vt, float* __restrict__ bias32, op_t* __restrict__ mask16,
-    int B, int N, int n_valid, int ending, float qscale, float eps) {
+    int B, int N, int n_valid, int ending, float qscale, float eps, TaMeanFix mf) {
   constexpr int LW = CC + 8, KS = CC / 16;
   extern __shared__ __attribute__((aligned(16))) op_t plds[];
   float* cb = reinterpret_cast<float*>(plds + TAP_ROWS * LW);
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   float* vsc = cb + TAP_ROWS + 32 * wid;   // FAST: this wave's per-key V block scales
+  float* mu = cb + TAP_ROWS;               // !FAST: the mean correction's mu
   auto wrow = [&](int row) -> const op_t* {   // weight rows have CC inputs
     return row < C ? wq + row * CC : row < 2 * C ? wk + (row - C) * CC
          : row < 3 * C ? wv + (row - 2 * C) * CC : wb + (row - 3 * C) * CC;
@@ -104,15 +113,24 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
     }
     st_x8(plds + row * LW + col, v);
   }
+  if (!FAST && mf.offb && mf.stats) {
+    stats_mu(mf.stats, mu);
+    __syncthreads();
+  }
   for (int row = tid; row < TAP_ROWS; row += 64 * TAP_WAVES) {   // accumulator starts W beta
     float acc = 0.f;
     if (row < 3 * C + H) {
-      const op_t* w = wrow(row);
+      if (!FAST && mf.offb) {
+        const op_t* lo = !mf.stats ? nullptr : mf.lo[row < 3 * C ? row / C : 3] + (row < 3 * C ? row % C : row - 3 * C) * CC;
+        if constexpr (CC == PS_C) acc = corrected_offset(mf.offb[row], lo, nullptr, mu);
+      } else {
+        const op_t* w = wrow(row);
 #pragma unroll 4
-      for (int c = 0; c < CC; c += 8) {
-        const opx8 w8 = ld_x8(w + c);
+        for (int c = 0; c < CC; c += 8) {
+          const opx8 w8 = ld_x8(w + c);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[c + e];
+          for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[c + e];
+        }
       }
     }
     cb[row] = acc;
@@ -784,13 +802,15 @@ struct TaBuffers {
   op_t *Q, *K, *Vt, *O;
   float* bias32;
   op_t* mask16;
+  float* stats;   // the mean-correction partials
 };
 
 // Workspace: Q, K, V^T, O (op_t, [B][N][H][N][D] each), the fp32 bias [B][H][N][N], the op_t
 // mask term [B][N][N].
 size_t ta_buffers_size(int B, int N) {
   const size_t e = (size_t)B * N * H * N * D;
-  return 4 * e * sizeof(op_t) + (size_t)B * H * N * N * sizeof(float) + (size_t)B * N * N * sizeof(op_t);
+  const size_t bytes = 4 * e * sizeof(op_t) + (size_t)B * H * N * N * sizeof(float) + (size_t)B * N * N * sizeof(op_t);
+  return (bytes + 15) / 16 * 16 + PS_PARTIAL_FLOATS * sizeof(float);   // + the mean-correction partials
 }
 
 TaBuffers ta_buffers(void* ws, int B, int N) {
@@ -802,6 +822,8 @@ TaBuffers ta_buffers(void* ws, int B, int N) {
   t.O = t.Vt + e;
   t.bias32 = reinterpret_cast<float*>(t.O + e);
   t.mask16 = reinterpret_cast<op_t*>(t.bias32 + (size_t)B * H * N * N);
+  const size_t used = (size_t)((char*)(t.mask16 + (size_t)B * N * N) - (char*)ws);
+  t.stats = reinterpret_cast<float*>((char*)ws + (used + 15) / 16 * 16);
   return t;
 }
 
@@ -836,6 +858,25 @@ __global__ void mx8_dequant_kernel(const uint8_t* __restrict__ q, const uint8_t*
 // (op_t, or null).
 struct TaWeights { const op_t *q, *k, *v, *g, *g_lo = nullptr, *o_lo = nullptr; };
 
+// The mean correction of ta_proj's weights for a 16-bit call with the exact offsets and the
+// four folded-weight residuals, one batch element, c_z = 128 (else the plain W16 beta offsets).
+template <int CC, bool FAST>
+TaMeanFix ta_mean_fix(const pf_triatt_args* a, const TaBuffers& t, hipStream_t st, int* rc) {
+  TaMeanFix mf{nullptr, {nullptr, nullptr, nullptr, nullptr}, nullptr};
+  *rc = PF_OK;
+  if (FAST || CC != PS_C || !a->in_offsets) return mf;
+  mf.offb = a->in_offsets;
+  if (a->B == 1 && a->w_q_lo && a->w_k_lo && a->w_v_lo && a->w_bias_lo) {
+    mf.lo[0] = (const op_t*)a->w_q_lo; mf.lo[1] = (const op_t*)a->w_k_lo;
+    mf.lo[2] = (const op_t*)a->w_v_lo; mf.lo[3] = (const op_t*)a->w_bias_lo;
+    mf.stats = t.stats;
+    pair_stats_kernel<<<PS_WG, 64 * PS_WAVES, 0, st>>>(a->z_in, a->N, a->eps, t.stats);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) *rc = pf_fail(PF_E_LAUNCH, "pair_stats_kernel launch failed: %s", hipGetErrorString(e));
+  }
+  return mf;
+}
+
 template <int CC, bool FAST>
 int triatt_run(const pf_triatt_args* a, const TaWeights& w) {
   hipStream_t st = (hipStream_t)a->stream;
@@ -846,13 +887,16 @@ int triatt_run(const pf_triatt_args* a, const TaWeights& w) {
   const long positions = (long)B * N * N;
   const int cus = device_cus();
   if (cus <= 0) return pf_fail(PF_E_LAUNCH, "pf_triatt_fwd: cannot query the device");
+  int mrc = PF_OK;
+  const TaMeanFix mf = ta_mean_fix<CC, FAST>(a, t, st, &mrc);
+  if (mrc) return mrc;
   {
     const void* fn = (const void*)ta_proj_kernel<CC, FAST>;
     if (const int rc = pf_reserve_lds(fn, tap_lds<CC, FAST>(), "ta_proj_kernel")) return rc;
     const int grid = (int)min((long)cus, (positions / 32 + TAP_WAVES - 1) / TAP_WAVES);
     ta_proj_kernel<CC, FAST><<<grid, 64 * TAP_WAVES, tap_lds<CC, FAST>(), st>>>(
         a->z_in, a->pair_mask, a->ln_w, a->ln_b, w.q, w.k, w.v, (const op_t*)a->w_bias, t.Q, t.K, t.Vt, t.bias32,
-        t.mask16, B, N, n_valid, a->ending, qscale, a->eps);
+        t.mask16, B, N, n_valid, a->ending, qscale, a->eps, mf);
     PF_CHECK_LAUNCH("ta_proj_kernel");
   }
   int rc = launch_attn<false>(t, nullptr, B, N, n_valid, st);
@@ -916,6 +960,14 @@ extern "C" int pf_triatt_fwd(const pf_triatt_args* a) {
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: n_valid %d outside [0, N=%d]", a->n_valid, a->N);
   if ((a->w_g_lo != nullptr) != (a->w_o_lo != nullptr) || (a->w_g_lo && a->C != 128))
     return pf_fail(PF_E_INVALID, "pf_triatt_fwd: give both weight residuals (w_g_lo, w_o_lo) or neither, C = 128 only");
+  {
+    const bool any_lo = a->w_q_lo || a->w_k_lo || a->w_v_lo || a->w_bias_lo;
+    if ((a->in_offsets || any_lo) && a->C != 128)
+      return pf_fail(PF_E_INVALID, "pf_triatt_fwd: exact offsets and the mean correction need C = 128");
+    if (any_lo && !(a->in_offsets && a->w_q_lo && a->w_k_lo && a->w_v_lo && a->w_bias_lo))
+      return pf_fail(PF_E_INVALID, "pf_triatt_fwd: the mean correction needs in_offsets and all four residuals "
+                                   "(w_q_lo, w_k_lo, w_v_lo, w_bias_lo)");
+  }
   const TaWeights w = {(const op_t*)a->w_q, (const op_t*)a->w_k, (const op_t*)a->w_v, (const op_t*)a->w_g,
                        (const op_t*)a->w_g_lo, (const op_t*)a->w_o_lo};
   return a->C == 128 ? triatt_run<128, false>(a, w) : triatt_run<64, false>(a, w);

@@ -195,7 +195,10 @@ def launch_triatt(z_in: torch.Tensor, out: torch.Tensor, pair_mask: Optional[tor
         w_q=_ptr(w["linear_q.weight"]), w_k=_ptr(w["linear_k.weight"]), w_v=_ptr(w["linear_v.weight"]),
         w_g=_ptr(w["linear_g.weight"]), w_o=_ptr(w["linear_o.weight"]),
         workspace=_ptr(ws), workspace_bytes=ws.numel(), stream=_stream(),
-        w_g_lo=_ptr(w.get("linear_g.weight.lo")), w_o_lo=_ptr(w.get("linear_o.weight.lo")))
+        w_g_lo=_ptr(w.get("linear_g.weight.lo")), w_o_lo=_ptr(w.get("linear_o.weight.lo")),
+        in_offsets=_ptr(w.get("in_offsets")), w_q_lo=_ptr(w.get("linear_q.weight.lo")),
+        w_k_lo=_ptr(w.get("linear_k.weight.lo")), w_v_lo=_ptr(w.get("linear_v.weight.lo")),
+        w_bias_lo=_ptr(w.get("linear.weight.lo")))
     _lib.check(_lib.load(variant).pf_triatt_fwd(ctypes.byref(a)), "pf_triatt_fwd", variant)
 
 
@@ -263,7 +266,8 @@ def launch_transition(x_in: torch.Tensor, out: torch.Tensor, w: Mapping[str, tor
         rows=rows, C=C, hidden=w["fc1.weight"].shape[0], accumulate=int(accumulate), eps=eps,
         x_in=_ptr(x_in), out=_ptr(out), norm_w=_ptr(w["norm.weight"]), norm_b=_ptr(w["norm.bias"]),
         fc1_w=_ptr(w["fc1.weight"]), fc2_w=_ptr(w["fc2.weight"]), fc3_w=_ptr(w["fc3.weight"]),
-        workspace=_ptr(ws), workspace_bytes=0 if ws is None else ws.numel(), stream=_stream())
+        workspace=_ptr(ws), workspace_bytes=0 if ws is None else ws.numel(), stream=_stream(),
+        fc3_lo=_ptr(w.get("fc3.weight.lo")))
     if pair_bias is None:
         _lib.check(_lib.load(variant).pf_transition_fwd(ctypes.byref(a)), "pf_transition_fwd", variant)
         return

@@ -123,8 +123,8 @@ class Options:
     1.254 vs 1.263 ms per layer with 0; 1.269 with 2, 1.308 with 4).
     ``weight_residuals``: the pair kernels whose weights fit twice in LDS (the triangle
     attention's gate and output projection, the triangle multiplication's output projection,
-    the recycling projection) take each 16-bit weight together with its rounding residual and
-    multiply by both (default on).  A 16-bit weight's rounding error is the same at every
+    the pair transition's output projection, the recycling projection) take each 16-bit weight
+    together with its rounding residual and multiply by both (default on).  A 16-bit weight's rounding error is the same at every
     position, so it adds up coherently through a deep stack; with the residual the weights are
     good to ~2^-22 of their size.
     ``mean_correction``: the triangle multiplication's LN_in-side weights (p_in, g_in, g_out),
@@ -252,6 +252,19 @@ class TriangleAttention(Module):
             self.w.update({k: self.mat(k) for k in ops.TRIATT_MX8_KEYS})
             if self.options.weight_residuals and self.C == C_Z:
                 self.w.update({k + ".lo": self.mat_lo(k) for k in ("linear_g.weight", "linear_o.weight")})
+            if self.options.mean_correction and self.C == C_Z:
+                # the mean correction of the projection: exact W . beta offsets and the residuals of
+                # the kernel's gamma-folded weights op(op(W) diag(gamma))
+                keys = ("linear_q.weight", "linear_k.weight", "linear_v.weight", "linear.weight")
+                beta = self.weights["layer_norm.bias"].detach().double().cpu()
+                gamma = self.weights["layer_norm.weight"].detach().double().cpu()
+                self.w["in_offsets"] = torch.cat([self.weights[k].detach().double().cpu() @ beta for k in keys]).to(
+                    device=self.device, dtype=torch.float32)
+                dt = ops.TORCH_DTYPE[self.variant]
+                for k in keys:
+                    w64 = self.weights[k].detach().double().cpu()
+                    folded = (w64.to(dt).float() * gamma.float()).to(dt)   # as the kernel folds it
+                    self.w[k + ".lo"] = (w64 * gamma - folded.double()).to(dt).to(self.device).contiguous()
 
     def workspace_bytes(self, B: int, N: int) -> int:
         if self.fast:
@@ -287,6 +300,8 @@ class Transition(Module):
             self.w.update(ops.mx8_weights(self.weights, self.device, ops.TRANSITION_MX8_KEYS, self.variant))
         else:
             self.w.update({k: self.mat(k) for k in ("fc1.weight", "fc2.weight", "fc3.weight")})
+            if self.options.weight_residuals and allow_fast and self.C == C_Z:   # the pair transition
+                self.w["fc3.weight.lo"] = self.mat_lo("fc3.weight")
 
     def workspace_bytes(self, rows: int) -> int:
         if self.fast:
