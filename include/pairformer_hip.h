@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define PF_ABI_VERSION 2
+#define PF_ABI_VERSION 3
 
 enum {
   PF_OK = 0,
@@ -175,7 +175,8 @@ int pf_tri_attention(const float* q, const float* k, const float* v, const float
  * Replaces Transition.forward (tt_bio/boltz2.py:1227-1258) and the ttnn Transition
  * (tt_bio/tenstorrent.py:856-946).  rows = B*N*N for the pair track (C = 128,
  * hidden = 512: one fused kernel, hidden never leaves the CU) or B*N for the single
- * track (C = 384, hidden = 1536: LN + two GEMMs, hidden in workspace).
+ * track (C = 384, hidden = 1536: LN + two GEMMs, hidden in workspace).  The C = 128
+ * workspace (256.5 KB whatever rows) is used only by fc3_mean_fix.
  * -------------------------------------------------------------------------- */
 typedef struct pf_transition_args {
   long rows; int C; int hidden;
@@ -191,6 +192,12 @@ typedef struct pf_transition_args {
   /* Optional (NULL = unused; C = 128 only): the residual fc3 - fc3_16 of fc3.weight in the
    * operand type; the output projection then runs on fc3_16 + residual (see pf_triatt_args). */
   const void* fc3_lo;
+  /* With fc3_lo: 0 = multiply by fc3_16 + residual at every position; 1 = multiply by fc3_16
+   * and add residual . mean(h), h = silu(fc1 LN(x)) * fc2 LN(x) averaged over up to 256 sampled
+   * tiles of 32 consecutive rows (a pass over those rows before the main one): the part of the
+   * residual's error that every position shares, at a fraction of the cost.  Needs the
+   * workspace (pf_transition_workspace_size; C = 128) and hidden a multiple of 64, <= 512. */
+  int fc3_mean_fix;
 } pf_transition_args;
 
 size_t pf_transition_workspace_size(long rows, int C, int hidden);
@@ -497,8 +504,8 @@ int pf_add_fwd(const float* a, const float* b, float* out, long n, void* stream)
 int pf_attend_timing(int enable);
 int pf_attend_timing_read(double* total_ms, int* launches);
 
-/* MFMA issue rate under load: `workgroups` workgroups of 16 waves each issue `iters` rounds
- * of four dependent-free 32x32x16 16-bit MFMAs (pseudo-random operands in (-1, 1) that change
+/* MFMA issue rate under load: `workgroups` workgroups of 16 waves each issue `iters` (a
+ * multiple of 4) rounds of four mutually independent 32x32x16 16-bit MFMAs (pseudo-random operands in (-1, 1) that change
  * every MFMA), i.e. pf_mfma_rate_probe_waves(workgroups) * iters * 4 * 32768 FLOP; every wave
  * writes one float of `sink` (workgroups * 16 floats). */
 long pf_mfma_rate_probe_waves(int workgroups);

@@ -67,12 +67,12 @@ _SELECT: Optional[frozenset] = None
 #: The precision model of this build's 16-bit kernels (``operand_rounding(dtype, **BUILD_MODEL)``):
 #: every product operand rounded to the operand type, except where the kernels carry a weight as
 #: a 16-bit hi + lo pair -- the trimul output projection p_out, the triangle attention's gate and
-#: output projections, the pair transition's fc3, the pair recycling projection (its activation
-#: too) -- and with the mean
-#: correction at the trimul's LN_in-side weights (p_in, g_in, g_out) and the triangle
-#: attention's q / k / v and bias projections.
-BUILD_MODEL = {"families": ("!tm_out.w", "!ta_out.w", "!ta_g.w", "!tr_hid.w", "!rec"),
-               "mean_fix": ("tm_in", "tm_gin", "tm_gate", "ta_in", "ta_bias")}
+#: output projections, the pair recycling projection (its activation too) -- and with the mean
+#: correction at the trimul's LN_in-side weights (p_in, g_in, g_out), the triangle attention's
+#: q / k / v and bias projections and the pair transition's fc3 (the kernels take those means
+#: over sampled positions; the model over all of them).
+BUILD_MODEL = {"families": ("!tm_out.w", "!ta_out.w", "!ta_g.w", "!rec"),
+               "mean_fix": ("tm_in", "tm_gin", "tm_gate", "ta_in", "ta_bias", "tr_hid")}
 _MEAN_FIX = None          # None, or the selector of weight sites whose error gets the mean correction
 _MEAN_SAMPLE = 1          # the correction's mean is taken over every k-th position
 

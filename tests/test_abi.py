@@ -34,13 +34,13 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().pf_abi_version() == _lib.ABI_VERSION == 2
+    assert _lib.load().pf_abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_struct_layouts_match_header_order():
     # the ctypes structs mirror the C structs field by field; spot-check sizes/offsets
     assert _lib.TrimulArgs.z_in.offset == 32 and ctypes.sizeof(_lib.TrimulArgs) == 32 + 19 * 8
-    assert _lib.TransitionArgs.x_in.offset == 24
+    assert _lib.TransitionArgs.x_in.offset == 24 and ctypes.sizeof(_lib.TransitionArgs) == 24 + 12 * 8   # 11 pointers, fc3_mean_fix (padded)
     assert _lib.TriattArgs.z_in.offset == 40
     assert _lib.TrimulMx8Args.z_in.offset == 32 and ctypes.sizeof(_lib.TrimulMx8Args) == 32 + 18 * 8
     assert _lib.TransitionMx8Args.x_in.offset == 24 and ctypes.sizeof(_lib.TransitionMx8Args) == 24 + 11 * 8
@@ -69,6 +69,26 @@ def test_rejects_null_and_bad_shapes_without_launching():
     assert lib.pf_quantize_mx8(1, 4, 64, 2, 1, 1, None) == -1 and "perm" in _err()
     tr = _lib.TransitionMx8Args(rows=16, C=384, hidden=1536)
     assert lib.pf_transition_mx8_fwd(ctypes.byref(tr)) == -1 and "C = 128" in _err()
+    # the fc3 mean correction needs the residual and its workspace (dummy pointers: no launch)
+    d = 4096
+    t = _lib.TransitionArgs(rows=4096, C=128, hidden=512, x_in=d, out=d, norm_w=d, norm_b=d, fc1_w=d, fc2_w=d,
+                            fc3_w=d, fc3_mean_fix=1)
+    assert lib.pf_transition_fwd(ctypes.byref(t)) == -1 and "needs the fc3 residual" in _err()
+    t.fc3_lo = d
+    t.workspace, t.workspace_bytes = d, lib.pf_transition_workspace_size(4096, 128, 512) - 1
+    assert lib.pf_transition_fwd(ctypes.byref(t)) == -1 and "needs a workspace" in _err()
+    t.hidden, t.workspace_bytes = 480, lib.pf_transition_workspace_size(4096, 128, 480)
+    assert lib.pf_transition_fwd(ctypes.byref(t)) == -1 and "multiple of 64" in _err()
+    t.C, t.hidden, t.fc3_mean_fix = 384, 1536, 0
+    assert lib.pf_transition_fwd(ctypes.byref(t)) == -1 and "C = 128 only" in _err()
+    # with the fused pair bias, the transition's sums may not share the attention's workspace
+    apb_bytes = lib.pf_apb_workspace_size(1, 64, 384, 16)
+    apb = _lib.ApbArgs(B=1, N=64, c_s=384, C=128, H=16, zln_w=d, zln_b=d, w_z=d, workspace=1 << 20,
+                       workspace_bytes=apb_bytes)
+    t = _lib.TransitionArgs(rows=64 * 64, C=128, hidden=512, x_in=d, out=d, norm_w=d, norm_b=d, fc1_w=d, fc2_w=d,
+                            fc3_w=d, fc3_lo=d, fc3_mean_fix=1, workspace=(1 << 20) + apb_bytes - 256,
+                            workspace_bytes=lib.pf_transition_workspace_size(64 * 64, 128, 512))
+    assert lib.pf_transition_pair_bias_fwd(ctypes.byref(t), ctypes.byref(apb)) == -1 and "overlaps" in _err()
 
 
 def test_fast_mode_entry_points_reject_bad_arguments_without_launching():
@@ -118,7 +138,7 @@ def test_fast_mode_entry_points_reject_bad_arguments_without_launching():
 def test_both_operand_variants_load():
     for variant, code in _lib.OPERAND_CODE.items():
         lib = _lib.load(variant)
-        assert lib.pf_operand_dtype() == code and lib.pf_abi_version() == 2
+        assert lib.pf_operand_dtype() == code and lib.pf_abi_version() == 3
         for name in _declared():
             assert hasattr(lib, name), (variant, name)
 
@@ -130,7 +150,7 @@ def test_workspace_sizes():
     assert lib.pf_trimul_workspace_size(1, 512, 128) == 128 * 512 * 512 * (2 + 2 + 2) + 1024 * 4 + 64 * 128 * 4
     assert lib.pf_triatt_workspace_size(1, 64, 128, 4, 32) > 0
     assert lib.pf_triatt_workspace_size(1, 64, 128, 8, 16) == 0
-    assert lib.pf_transition_workspace_size(4096, 128, 512) == 0          # fused, no scratch
+    assert lib.pf_transition_workspace_size(4096, 128, 512) == 513 * 128 * 4   # fused: the fc3 mean-fix sums
     assert lib.pf_transition_workspace_size(100, 384, 1536) == 100 * (384 + 1536) * 4
     # e4m3 a/b planes + their E8M0 scales + the fp16 contraction output
     planes = 128 * 512 * 512

@@ -397,14 +397,21 @@ def test_transition_fused_pair_bias(gpu):
 def test_layer_batch2_matches_single(gpu):
     """B = 2 through the whole layer (every kernel's batch indexing: trimul planes,
     attention rows/bias, transitions, the single track) equals the two proteins run one at
-    a time, bit for bit, and the fp32 oracle on the batch."""
+    a time, bit for bit, and the fp32 oracle on the batch.  The mean correction of the
+    16-bit input-side weights is a single-protein (B = 1) feature, so the bit-for-bit part
+    runs without it; with the default options a batch (exact beta offsets, no correction) is
+    checked against the oracle as well."""
     N = 64
     w = synthetic.stack_weights(1, 51)
     s0, z0, m0, pm0 = _inputs(N, 52)
     s1, z1, m1, pm1 = _inputs(N, 53, pad_tail=9)
     S, Z, M, PM = (torch.cat(t, 0) for t in ((s0, s1), (z0, z1), (m0, m1), (pm0, pm1)))
-    pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, w)
+    pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, w, pairformer.Options(mean_correction=False))
     s_b, z_b = pf(S.to(gpu).contiguous(), Z.to(gpu).contiguous(), PM.to(gpu).contiguous(), M.to(gpu).contiguous())
+    pf_default = pairformer.Pairformer(1, 32, 4, 24, 16, True, w)
+    s_d, z_d = pf_default(S.to(gpu).contiguous(), Z.to(gpu).contiguous(), PM.to(gpu).contiguous(),
+                          M.to(gpu).contiguous())
+    check("batch-2 layer z, default options", z_d, ref.pairformer_stack(S, Z, M, PM, w, 1)[1])
     for i, (s, z, m, pm) in enumerate(((s0, z0, m0, pm0), (s1, z1, m1, pm1))):
         s_1, z_1 = pf(s.to(gpu).contiguous(), z.to(gpu).contiguous(), pm.to(gpu).contiguous(),
                       m.to(gpu).contiguous())

@@ -144,6 +144,38 @@ def test_trimul_mean_correction_removes_coherent_error(gpu, direction):
     assert coh_fixed < 0.35 * coh_plain
 
 
+@pytest.mark.parametrize("N", [64, 128, 192, 256])
+def test_pair_stats_sample_mean(gpu, N):
+    """The statistics the mean correction starts from: after a mean-corrected trimul call the
+    workspace holds 64 partial sums (after the three operand planes and the 1024 amax partials)
+    that add up to the mean over the sampled positions of the rows normalized without their
+    affine part.  The sample is every tile of 32 consecutive positions when there are at most
+    1024 tiles (N = 64, 128: a whole-grid mean) and otherwise the 1024 tiles
+    k * 2654435761 mod n_tiles (N = 192: 1152 tiles, some drawn twice; N = 256: half of the
+    2048 tiles, each once)."""
+    raw = _sub_w(27, "tri_mul_out")
+    g = torch.Generator().manual_seed(28)
+    z = 2.0 * torch.randn(128, generator=g) + torch.randn((1, N, N, 128), generator=g)
+    w = dict(_dev_w(raw, gpu))
+    w["in_offsets"] = torch.zeros(3 * 128, device=gpu)
+    for k in ("p_in.weight", "g_in.weight", "g_out.weight"):
+        w[k + ".lo"] = ops.opw_lo(raw[k], gpu)
+    zd = z.to(gpu).contiguous()
+    ws = ops.workspace(ops.trimul_workspace_bytes(1, N), gpu)
+    ops.launch_trimul(zd, torch.empty_like(zd), None, w, 0, ws, accumulate=False)
+    torch.cuda.synchronize()
+    start = 3 * 128 * N * N * 2 + 1024 * 4
+    mu = ws[start:start + 64 * 128 * 4].cpu().view(torch.float32).view(64, 128).double().sum(0)
+    ntiles = N * N // 32
+    tiles = range(ntiles) if ntiles <= 1024 else [k * 2654435761 % ntiles for k in range(1024)]
+    rows = z.double().reshape(-1, 32, 128)[list(tiles)].reshape(-1, 128)
+    xhat = (rows - rows.mean(1, keepdim=True)) / (rows.var(1, unbiased=False, keepdim=True) + 1e-5).sqrt()
+    want = xhat.mean(0)
+    err = (mu - want).abs().max().item()
+    print(f"[precision] pair stats N={N}: |mu| max {want.abs().max().item():.3f}, max error {err:.2e}", flush=True)
+    assert err < 1e-5
+
+
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_transition_residual_weight_wiring(gpu, with_bias):
     """tr_pair with fc3 given as (W16, W16) equals the plain kernel on 2 W16 (the four-block
@@ -159,7 +191,7 @@ def test_transition_residual_weight_wiring(gpu, with_bias):
     doubled["fc3.weight"] = (2 * w["fc3.weight"].float()).to(w["fc3.weight"].dtype)
     outs, biases = [], []
     for ww in (hilo, doubled):
-        out = torch.empty_like(zd)
+        out = zd.clone()   # out += update, as in the layer
         pb = None
         if with_bias:
             apb = _dev_w(_sub_w(30, "attention"), gpu)
@@ -174,3 +206,59 @@ def test_transition_residual_weight_wiring(gpu, with_bias):
     if with_bias:
         # the bias is a 16-bit product of LN(z): each flipped z rounding moves it again (measured 2.7e-6)
         _same(biases[0], biases[1], "transition fused pair bias with fc3 hi+lo(=hi) vs doubled", 1e-5)
+
+
+def _tr_sample_tiles(rows):
+    """The tiles of 32 rows the pair transition's sampling pass takes (at most 256, by
+    k * 2654435761 mod n_tiles when there are more)."""
+    ntiles = rows // 32
+    return list(range(ntiles)) if ntiles <= 256 else [k * 2654435761 % ntiles for k in range(256)]
+
+
+@pytest.mark.parametrize("N,with_bias", [(64, False), (192, False), (256, True)])
+def test_transition_mean_correction(gpu, N, with_bias):
+    """fc3_mean_fix: fc3_16 plus corr = (fc3 - fc3_16) . mean(h) over the sampled tiles.
+    corr (kept in the workspace after the 512 x 128 partial sums) must match fp64 on the same
+    tiles to 1% of its size (the kernel's h comes from 16-bit operands).  On z rows that share a
+    strong channel pattern (so h has a large mean), the fc3 rounding error alone is the plain
+    kernel's difference to the hi + lo one; its per-channel mean over positions (what a deep
+    stack accumulates) must mostly vanish from the mean-corrected kernel's difference to hi + lo
+    (all 128 tiles sampled at N = 64; 256 of 1152 / 2048 at N = 192 / 256).  The update must meet
+    the parity bar, and with the fused single-track pair bias it must be the same bits."""
+    raw = _sub_w(33, "transition_z")
+    g = torch.Generator().manual_seed(34)
+    z = 2.0 * torch.randn(128, generator=g) + torch.randn((1, N, N, 128), generator=g)
+    zd = z.to(gpu).contiguous()
+    want = ref.transition(zd, {k: v.to(gpu) for k, v in raw.items()}).cpu()
+    w = _dev_w(raw, gpu)
+    fixed = dict(w)
+    fixed["fc3.weight.lo"] = ops.opw_lo(raw["fc3.weight"], gpu)
+    rows = N * N
+    ws = ops.workspace(ops.transition_workspace_bytes(rows, 128, 512), gpu)
+    a, b, hl = torch.empty_like(zd), torch.empty_like(zd), torch.empty_like(zd)
+    ops.launch_transition(zd, a, w, None, accumulate=False)
+    ops.launch_transition(zd, hl, fixed, None, accumulate=False)
+    ops.launch_transition(zd, b, fixed, ws, accumulate=False, fc3_mean_fix=True)
+    torch.cuda.synchronize()
+    corr = ws[512 * 128 * 4: 513 * 128 * 4].cpu().view(torch.float32).double()
+    x = z.double().reshape(-1, 32, 128)[_tr_sample_tiles(rows)].reshape(-1, 128)
+    xn = ref.layer_norm(x, raw["norm.weight"].double(), raw["norm.bias"].double())
+    hmean = (torch.nn.functional.silu(xn @ raw["fc1.weight"].double().t()) * (xn @ raw["fc2.weight"].double().t())).mean(0)
+    corr_want = fixed["fc3.weight.lo"].double().cpu() @ hmean
+    cerr = (corr - corr_want).abs().max().item() / corr_want.abs().max().item()
+    rms = want.pow(2).mean().sqrt()
+    coh_plain = ((a - hl).mean(dim=(0, 1, 2)).abs().mean().cpu() / rms).item()
+    coh_fixed = ((b - hl).mean(dim=(0, 1, 2)).abs().mean().cpu() / rms).item()
+    print(f"[precision] transition mean fix N={N}: corr max {corr_want.abs().max().item():.2e}, rel error "
+          f"{cerr:.2e}; coherent fc3 error plain {coh_plain:.3e}, mean-corrected {coh_fixed:.3e}", flush=True)
+    assert cerr < 1e-2
+    check(f"transition mean-corrected N={N}", b, want)
+    assert coh_fixed < 0.2 * coh_plain
+    if with_bias:
+        s = torch.randn((1, N, 384), generator=torch.Generator().manual_seed(35)).to(gpu)
+        apb = _dev_w(_sub_w(36, "attention"), gpu)
+        apb_ws = ops.workspace(ops.apb_workspace_bytes(1, N, 384, 16), gpu)
+        c = torch.empty_like(zd)
+        ops.launch_transition(zd, c, fixed, ws, accumulate=False, pair_bias=(s, apb, 16, apb_ws, 1e-5),
+                              fc3_mean_fix=True)
+        assert torch.equal(b, c)

@@ -59,6 +59,9 @@ def test_noalloc_refuses_oversize(gpu):
     B, N, c_s, H = 1, 1024, 384, 16
     need = lib.pf_apb_workspace_size(B, N, c_s, H)
     assert need > (24 << 20)
-    a = _lib.ApbArgs(B=B, N=N, c_s=c_s, C=128, H=H)
+    # dummy non-null pointers: the shape and pointers pass, the scratch size is refused before any
+    # launch (nothing is dereferenced)
+    ptrs = {f: 16 for f, ty in _lib.ApbArgs._fields_ if ty is ctypes.c_void_p and f not in ("stream", "workspace")}
+    a = _lib.ApbArgs(B=B, N=N, c_s=c_s, C=128, H=H, **ptrs)
     assert lib.pf_apb_fwd_noalloc(ctypes.byref(a)) == -1
     assert "above the static" in lib.pf_last_error().decode()

@@ -17,7 +17,7 @@ LIBS = {"fp16": "libpairformer_hip.so", "bf16": "libpairformer_hip_bf16.so"}
 OPERAND_CODE = {"fp16": 0, "bf16": 1}
 DEFAULT_VARIANT = "fp16"
 LIB_PATH = os.path.join(HERE, LIBS[DEFAULT_VARIANT])
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 c_int, c_float, c_long, c_size_t, c_void_p = ctypes.c_int, ctypes.c_float, ctypes.c_long, ctypes.c_size_t, ctypes.c_void_p
 
@@ -66,7 +66,7 @@ class TransitionArgs(ctypes.Structure):
         ("x_in", c_void_p), ("out", c_void_p), ("norm_w", c_void_p), ("norm_b", c_void_p),
         ("fc1_w", c_void_p), ("fc2_w", c_void_p), ("fc3_w", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
-        ("fc3_lo", c_void_p),
+        ("fc3_lo", c_void_p), ("fc3_mean_fix", c_int),
     ]
 
 

@@ -92,9 +92,12 @@ __global__ __launch_bounds__(64 * PROBE_WAVES) void mfma_rate_kernel(int iters, 
       b[u][t] = (op_t)((float)(rb >> 8) * (2.f / 16777216.f) - 1.f);
     }
   f32x16 acc[4] = {zero16(), zero16(), zero16(), zero16()};
-  for (int i = 0; i < iters; ++i) {
+  // the rotation is unrolled so every operand index is a constant (registers, not scratch)
+  for (int i = 0; i < iters; i += 4) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc[u] = mfma32(a[(u + i) & 3], b[(u + 2 * i) & 3], acc[u]);
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[u] = mfma32(a[(u + j) & 3], b[(u + 2 * j) & 3], acc[u]);
   }
   float s = 0.f;
 #pragma unroll
@@ -112,9 +115,9 @@ extern "C" long pf_mfma_rate_probe_waves(int workgroups) {
 }
 
 extern "C" int pf_mfma_rate_probe(int workgroups, int iters, float* sink, void* stream) {
-  if (workgroups <= 0 || iters <= 0 || !sink)
-    return pf_fail(PF_E_INVALID, "pf_mfma_rate_probe: need workgroups > 0, iters > 0 and a sink of "
-                   "workgroups * %d floats (got %d, %d, %p)", PROBE_WAVES, workgroups, iters, (void*)sink);
+  if (workgroups <= 0 || iters <= 0 || iters % 4 || !sink)
+    return pf_fail(PF_E_INVALID, "pf_mfma_rate_probe: need workgroups > 0, iters > 0 a multiple of 4 and a sink "
+                   "of workgroups * %d floats (got %d, %d, %p)", PROBE_WAVES, workgroups, iters, (void*)sink);
   mfma_rate_kernel<<<workgroups, 64 * PROBE_WAVES, 0, (hipStream_t)stream>>>(iters, sink);
   PF_CHECK_LAUNCH("mfma_rate_kernel");
   return PF_OK;

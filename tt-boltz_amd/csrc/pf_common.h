@@ -593,54 +593,99 @@ namespace {
 #ifndef PF_PS_TILES
 #define PF_PS_TILES 1024
 #endif
-constexpr int PS_WG = 64, PS_WAVES = 4, PS_TILES = PF_PS_TILES;
+// 64 workgroups of 16 waves, one tile per wave (at the default sample size)
+constexpr int PS_WG = 64, PS_WAVES = 16, PS_TILES = PF_PS_TILES;
 constexpr int PS_C = 128;   // channels of the pair rows the statistics are taken over
 constexpr size_t PS_PARTIAL_FLOATS = (size_t)PS_WG * PS_C;
 
+// v of the lane that the DPP control CTRL selects (within each row of 16 lanes)
+template <int CTRL>
+PF_DEV float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Sum over each row of 16 lanes, left in every lane of the row: lane ^ 1, lane ^ 2 (quad
+// permutes), then the other quad (row_half_mirror: i <-> 7 - i) and the other half-row
+// (row_mirror: i <-> 15 - i).
+PF_DEV float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+  v += dpp_f<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+  v += dpp_f<0x141>(v);   // row_half_mirror
+  v += dpp_f<0x140>(v);   // row_mirror
+  return v;
+}
+
+// A wave reads its tile fully coalesced: lane l handles row 4 p + (l >> 4) of each group p of
+// four rows, channels 4 (l & 15) .. +3 and 64 + 4 (l & 15) .. +3 (so 16 lanes read a row's
+// 512 bytes as two 256-byte runs), and takes the row's LayerNorm statistics with DPP sums over
+// its row of 16 lanes.
 __global__ __launch_bounds__(64 * PS_WAVES) void pair_stats_kernel(const float* __restrict__ z, int N, float eps,
                                                                    float* __restrict__ partials) {
-  __shared__ float red[PS_WAVES][PS_C][33];   // [wave][channel][lane m] (+1 pad)
-  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31, wid = tid >> 6;
+  __shared__ float red[PS_WAVES][PS_C];
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, q = lane & 15, wid = tid >> 6;
   const uint32_t ntiles = (uint32_t)N * N / 32;
   const uint32_t ns = ntiles < (uint32_t)PS_TILES ? ntiles : (uint32_t)PS_TILES;
-  float acc[64];
+  float acc[8];
 #pragma unroll
-  for (int i = 0; i < 64; ++i) acc[i] = 0.f;
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
   for (uint32_t k = blockIdx.x * PS_WAVES + wid; k < ns; k += PS_WG * PS_WAVES) {
     const uint32_t t = ns == ntiles ? k : (uint32_t)(((uint64_t)k * 2654435761ull) % ntiles);
-    float x[64];
-    load_row_frag<PS_C>(z + ((size_t)t * 32 + m) * PS_C, h, x);
-    float sm = 0.f;
+    const float* tile = z + (size_t)t * 32 * PS_C + g * PS_C + 4 * q;
+    float4 x[16];   // [2 p]: channels 4 q .., [2 p + 1]: channels 64 + 4 q .., of row 4 p + g
 #pragma unroll
-    for (int i = 0; i < 64; ++i) sm += x[i];
-    const float mean = xor32_sum(sm) * (1.f / PS_C);
-    float var = 0.f;
+    for (int p = 0; p < 8; ++p) {
+      x[2 * p] = *reinterpret_cast<const float4*>(tile + 4 * p * PS_C);
+      x[2 * p + 1] = *reinterpret_cast<const float4*>(tile + 4 * p * PS_C + 64);
+    }
 #pragma unroll
-    for (int i = 0; i < 64; ++i) { const float d = x[i] - mean; var += d * d; }
-    const float rstd = rsqrtf(xor32_sum(var) * (1.f / PS_C) + eps);
+    for (int p = 0; p < 8; ++p) {
+      const float4 a = x[2 * p], b = x[2 * p + 1];
+      const float mean = row16_sum((a.x + a.y) + (a.z + a.w) + (b.x + b.y) + (b.z + b.w)) * (1.f / PS_C);
+      const float d[8] = {a.x - mean, a.y - mean, a.z - mean, a.w - mean,
+                          b.x - mean, b.y - mean, b.z - mean, b.w - mean};
+      float v = 0.f;
 #pragma unroll
-    for (int i = 0; i < 64; ++i) acc[i] += (x[i] - mean) * rstd;
+      for (int i = 0; i < 8; ++i) v += d[i] * d[i];
+      const float rstd = rsqrtf(row16_sum(v) * (1.f / PS_C) + eps);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += d[i] * rstd;
+    }
   }
-  // lane (m, h) holds channels 16 s + 8 h + t in acc[8 s + t]
+  // the four lanes of a channel quad (g = 0..3) hold partial sums of the same channels
 #pragma unroll
-  for (int i = 0; i < 64; ++i) red[wid][16 * (i >> 3) + 8 * h + (i & 7)][m] = acc[i];
+  for (int i = 0; i < 8; ++i) {
+    acc[i] += __shfl_xor(acc[i], 16);
+    acc[i] += __shfl_xor(acc[i], 32);
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      red[wid][4 * q + i] = acc[i];
+      red[wid][64 + 4 * q + i] = acc[4 + i];
+    }
+  }
   __syncthreads();
   if (tid < PS_C) {
     float sum = 0.f;
-    for (int w = 0; w < PS_WAVES; ++w)
-#pragma unroll 8
-      for (int l = 0; l < 32; ++l) sum += red[w][tid][l];
-    partials[blockIdx.x * PS_C + tid] = sum / (32.f * (float)ns);
+#pragma unroll
+    for (int w = 0; w < PS_WAVES; ++w) sum += red[w][tid];
+    partials[blockIdx.x * PS_C + tid] = ns ? sum / (32.f * (float)ns) : 0.f;   // no tile: no correction
   }
 }
 
-// mu[c] (LDS, 128 floats) = the sum of the PS_WG partials; the caller synchronizes.
-PF_DEV void stats_mu(const float* __restrict__ partials, float* mu) {
-  for (int c = threadIdx.x; c < PS_C; c += blockDim.x) {
-    float sum = 0.f;
-#pragma unroll 8
-    for (int g = 0; g < PS_WG; ++g) sum += partials[g * PS_C + c];
-    mu[c] = sum;
+// mu[c] (LDS, 128 floats) = the sum of the PS_WG partials, with every thread of the workgroup
+// (blockDim.x a multiple of 128) summing a share into `scratch` (LDS, blockDim.x floats) first;
+// the caller synchronizes before reading mu.
+PF_DEV void stats_mu(const float* __restrict__ partials, float* mu, float* scratch) {
+  const int nq = blockDim.x / PS_C, c = threadIdx.x % PS_C, q = threadIdx.x / PS_C;
+  float sum = 0.f;
+#pragma unroll 4
+  for (int g = q; g < PS_WG; g += nq) sum += partials[g * PS_C + c];
+  scratch[threadIdx.x] = sum;
+  __syncthreads();
+  if (threadIdx.x < PS_C) {
+    float t = 0.f;
+    for (int j = 0; j < nq; ++j) t += scratch[j * PS_C + threadIdx.x];
+    mu[threadIdx.x] = t;
   }
 }
 

@@ -33,38 +33,61 @@ PF_DEV opx8 lds_x8(const char* p) { return *reinterpret_cast<const opx8*>(p); }
 //                  chunks, chunk c at slot c ^ swz4(R)
 // so every fragment read (one 16-byte chunk from each of 32 consecutive rows) is free of
 // bank conflicts.
-// HILO: fc3 also comes with its rounding residual w3_lo = fc3 - fc3_16 (op_t), staged as a
-// fourth block beside W3 and multiplied in as a second MFMA per fragment, so the output
-// projection runs on weights good to ~2^-22 of their size; the larger ring leaves room for two
-// workgroups per CU instead of three.
-constexpr int TRW = 4;
+// The output projection fc3 comes in four forms (TrMode):
+//   TR_PLAIN    fc3_16 only.
+//   TR_HILO     fc3 also comes with its rounding residual w3_lo = fc3 - fc3_16 (op_t), staged
+//               as a fourth block beside W3 and multiplied in as a second MFMA per fragment, so
+//               the projection runs on weights good to ~2^-22 of their size; the larger ring
+//               leaves room for two workgroups per CU instead of three.
+//   TR_MEANFIX  fc3_16, plus corr = w3_lo . mean(h) on every output row: the part of the
+//               residual's error that every position shares, h the hidden activation
+//               silu(fc1 x) * fc2 x averaged over sampled positions (below).
+//   TR_STATS    the sampling pass behind corr: a workgroup of 4 waves takes 4 sampled tiles of
+//               32 pairs (Fibonacci hashing, as pair_stats_kernel) and two of the hidden blocks
+//               (both fetched at once, before the LayerNorm: the pass is latency-bound),
+//               multiplies their h by w3_lo (given as w3) and sums over its pairs into one
+//               partial per workgroup (already divided by the sample size).
+enum TrMode { TR_PLAIN = 0, TR_HILO = 1, TR_MEANFIX = 2, TR_STATS = 3 };
+constexpr int TRW = 4;                       // waves of a workgroup
 constexpr int TR_BLK = 8192;                 // bytes of one fp16 weight block
-constexpr int TR_STAGE = 3 * TR_BLK;
-template <bool HILO>
-constexpr int tr_stage() { return (HILO ? 4 : 3) * TR_BLK; }
+constexpr int TRS_TILES = 256;               // sampled tiles of the TR_STATS pass
+constexpr int TRS_MAX_HIDDEN = 512;          // its hidden sizes: multiples of 64 up to this
+constexpr int TRS_PARTIALS = TRS_TILES / TRW * (TRS_MAX_HIDDEN / 64);   // its workgroups (at most)
+template <int MODE>
+constexpr int tr_stage() { return (MODE == TR_HILO ? 4 : 3) * TR_BLK; }
 PF_DEV int tr_swz4(int r) { return (r >> 2) & 3; }
 
-template <bool ZBIAS, bool HILO = false>
-__global__ __launch_bounds__(64 * TRW, HILO ? 2 : 3) void tr_pair_kernel(
+template <bool ZBIAS, int MODE>
+__global__ __launch_bounds__(64 * TRW, MODE == TR_HILO || MODE == TR_STATS ? 2 : 3) void tr_pair_kernel(
     const float* x_in, float* out, const float* __restrict__ lnw, const float* __restrict__ lnb,
     const op_t* __restrict__ w1, const op_t* __restrict__ w2, const op_t* __restrict__ w3,
-    const op_t* __restrict__ w3_lo, long rows, int hidden, int accumulate, float eps, ZBiasArgs zb) {
-  constexpr int STAGE = tr_stage<HILO>();
+    const op_t* __restrict__ w3_lo, long rows, int hidden, int accumulate, float eps, ZBiasArgs zb,
+    const float* __restrict__ corr, float* __restrict__ partials) {
+  constexpr bool HILO = MODE == TR_HILO, STATS = MODE == TR_STATS;
+  constexpr int STAGE = tr_stage<MODE>();
   __shared__ __attribute__((aligned(16))) char tl[2 * STAGE];
+  __shared__ float red[STATS ? TRW * C : 1];   // the sampling pass's sums
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const long pos0 = ((long)blockIdx.x * TRW + wid) * 32;
-
-  // rows past the end are clamped on load and skipped on store
-  opx8 xf[8];
-  {
-    float x[64];
-    load_row128_frag(x_in + min(pos0 + m, rows - 1) * C, h, x);
-    ln128_to_frag(x, h, lnw, lnb, eps, xf);
+  const int nhb = hidden / 32;
+  long pos0;
+  int hb_lo = 0, hb_hi = nhb;
+  bool live = true;
+  uint32_t ns = 0;
+  if constexpr (STATS) {   // hidden blocks 2 hbg, 2 hbg + 1 of sampled tiles 4 g .. 4 g + 3
+    const uint32_t ntiles = (uint32_t)(rows / 32);
+    ns = ntiles < (uint32_t)TRS_TILES ? ntiles : (uint32_t)TRS_TILES;
+    const int ngroups = nhb / 2, hbg = blockIdx.x % ngroups;
+    const uint32_t k = blockIdx.x / ngroups * TRW + wid;
+    live = k < ns;   // a dead wave still takes its part in the weight DMA and the barriers
+    const uint32_t kk = live ? k : 0;
+    pos0 = 32l * (ns == ntiles ? kk : (uint32_t)(((uint64_t)kk * 2654435761ull) % ntiles));
+    hb_lo = 2 * hbg;
+    hb_hi = hb_lo + 2;
+  } else {
+    pos0 = ((long)blockIdx.x * TRW + wid) * 32;
   }
-  f32x16 acc[4];
-#pragma unroll
-  for (int ob = 0; ob < 4; ++ob) acc[ob] = zero16();
+
 
   // DMA: chunk e = tid + 256 i (i = 0, 1) of each block; chunk tid + 256 is row R + 16
   // (W1 / W2: same slot, perm16(R + 16) = perm16(R) + 16) or R + 64 (W3: same slot)
@@ -94,14 +117,31 @@ __global__ __launch_bounds__(64 * TRW, HILO ? 2 : 3) void tr_pair_kernel(
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) a3[ks] = 2 * TR_BLK + 64 * m + 16 * ((2 * ks + h) ^ tr_swz4(m));
 
-  const int nhb = hidden / 32;
-  issue(0, 0);
-  for (int hb = 0; hb < nhb; ++hb) {
+  // the first block (TR_STATS: both) is on its way during the LayerNorm
+  issue(hb_lo, 0);
+  if constexpr (STATS) issue(hb_lo + 1, 1);
+  // rows past the end are clamped on load and skipped on store
+  opx8 xf[8];
+  {
+    float x[64];
+    load_row128_frag(x_in + min(pos0 + m, rows - 1) * C, h, x);
+    ln128_to_frag(x, h, lnw, lnb, eps, xf);
+  }
+  f32x16 acc[4];
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob) acc[ob] = zero16();
+  float cm[4];   // TR_MEANFIX: corr of channels 32 ob + m
+  if constexpr (MODE == TR_MEANFIX)
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob) cm[ob] = corr[32 * ob + m];
+
+  for (int hb = hb_lo; hb < hb_hi; ++hb) {
+    const int buf = (hb - hb_lo) & 1;
     __builtin_amdgcn_s_waitcnt(vmcnt_le(0));   // block hb landed ...
     __builtin_amdgcn_s_barrier();              // ... for every wave; the other stage is free
     asm volatile("" ::: "memory");
-    if (hb + 1 < nhb) issue(hb + 1, (hb + 1) & 1);
-    const char* st = tl + (hb & 1) * STAGE;
+    if (!STATS && hb + 1 < hb_hi) issue(hb + 1, buf ^ 1);
+    const char* st = tl + buf * STAGE;
     f32x16 a1 = zero16(), a2 = zero16();
 #pragma unroll
     for (int s2 = 0; s2 < 8; ++s2) {
@@ -121,21 +161,124 @@ __global__ __launch_bounds__(64 * TRW, HILO ? 2 : 3) void tr_pair_kernel(
         if constexpr (HILO) acc[ob] = mfma32(lds_x8(st + TR_BLK + a3[ks] + 2048 * ob), hf[ks], acc[ob]);
       }
   }
-  pair_update_epilogue<ZBIAS>(acc, out, rows, pos0, m, h, accumulate, zb);
+  if constexpr (STATS) {
+    // sum over the wave's 32 pairs (the lanes of each half), then over the workgroup's waves
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float v = row16_sum(acc[ob][i]);
+        v += __shfl_xor(v, 16);
+        if (m == 0) red[wid * C + 32 * ob + 8 * (i >> 2) + 4 * h + (i & 3)] = live ? v : 0.f;
+      }
+    __syncthreads();
+    if (tid < C) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < TRW; ++w) sum += red[w * C + tid];
+      partials[blockIdx.x * C + tid] = sum / (32.f * (float)ns);
+    }
+  } else {
+    if constexpr (MODE == TR_MEANFIX) {
+      // acc[ob] += corr on every pair, as one more MFMA: A = corr * 2^10 in column k = 0 (row m
+      // = channel 32 ob + m, as for W3), B = 2^-10 (exact).  Accumulators that started from
+      // corr instead would keep a second copy of all 64 across the loop.
+      opx8 ones;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) ones[t] = (op_t)(1.f / 1024.f);
+#pragma unroll
+      for (int ob = 0; ob < 4; ++ob) {
+        opx8 a;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) a[t] = (op_t)0.f;
+        a[0] = (op_t)(h == 0 ? cm[ob] * 1024.f : 0.f);
+        acc[ob] = mfma32(a, ones, acc[ob]);
+      }
+    }
+    pair_update_epilogue<ZBIAS>(acc, out, rows, pos0, m, h, accumulate, zb);
+  }
 }
 
-// The pair transition's launch: the plain or the residual (HILO) form.
+// corr[c] = the sum of np partial rows [np][128]: one workgroup of 1024 threads, thread
+// (quad q of 4 channels, group g of 32) summing rows g, g + 32, ... with all its loads in
+// flight (np <= TRS_PARTIALS), then the 32 groups through LDS.
+__global__ __launch_bounds__(1024) void tr_corr_kernel(const float* __restrict__ partials, int np,
+                                                       float* __restrict__ corr) {
+  constexpr int G = 32, PER = TRS_PARTIALS / G;
+  __shared__ f32x4 part[G][C / 4 + 1];
+  const int q = threadIdx.x & (C / 4 - 1), g = threadIdx.x >> 5;
+  f32x4 v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int p = g + G * i;
+    v[i] = p < np ? *reinterpret_cast<const f32x4*>(partials + (size_t)p * C + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < PER; ++i) sum += v[i];
+  part[g][q] = sum;
+  __syncthreads();
+  if (threadIdx.x < C) {
+    const int c = threadIdx.x;
+    float t = 0.f;
+#pragma unroll
+    for (int j = 0; j < G; ++j) t += part[j][c >> 2][c & 3];
+    corr[c] = t;
+  }
+}
+
+// Workspace of the C = 128 pair transition: the TR_STATS partials and corr (fp32).
+constexpr size_t TR_WS_BYTES = ((size_t)TRS_PARTIALS + 1) * C * sizeof(float);
+
+// Checks of the fc3 residual options: C = 128 only; the mean correction needs the residual and
+// the workspace for its sums.
+int tr_check_fc3(const pf_transition_args* a, const char* fn) {
+  if (a->fc3_lo && a->C != C)
+    return pf_fail(PF_E_INVALID, "%s: the fc3 residual (fc3_lo) is supported for C = 128 only", fn);
+  if (a->fc3_mean_fix && !a->fc3_lo)
+    return pf_fail(PF_E_INVALID, "%s: fc3_mean_fix needs the fc3 residual (fc3_lo)", fn);
+  if (a->fc3_mean_fix && (a->hidden % 64 || a->hidden > TRS_MAX_HIDDEN))
+    return pf_fail(PF_E_INVALID, "%s: fc3_mean_fix needs hidden a multiple of 64 up to %d (got %d)", fn,
+                   TRS_MAX_HIDDEN, a->hidden);
+  if (a->fc3_mean_fix && (!a->workspace || a->workspace_bytes < TR_WS_BYTES))
+    return pf_fail(PF_E_INVALID, "%s: fc3_mean_fix needs a workspace of %zu bytes (got %zu)", fn, TR_WS_BYTES,
+                   a->workspace ? a->workspace_bytes : (size_t)0);
+  return PF_OK;
+}
+
+// The pair transition's launch over workgroups of TRW tiles of 32 pairs (the last one clamped):
+// plain, hi + lo, or the mean-corrected form after its sampling pass.
 template <bool ZBIAS>
-int launch_tr_pair(const pf_transition_args* a, const ZBiasArgs& zb, unsigned grid) {
+int launch_tr_pair(const pf_transition_args* a, const ZBiasArgs& zb) {
   hipStream_t st = (hipStream_t)a->stream;
-  if (a->fc3_lo)
-    tr_pair_kernel<ZBIAS, true><<<grid, 64 * TRW, 0, st>>>(
-        a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w, (const op_t*)a->fc2_w, (const op_t*)a->fc3_w,
-        (const op_t*)a->fc3_lo, a->rows, a->hidden, a->accumulate, a->eps, zb);
-  else
-    tr_pair_kernel<ZBIAS, false><<<grid, 64 * TRW, 0, st>>>(
-        a->x_in, a->out, a->norm_w, a->norm_b, (const op_t*)a->fc1_w, (const op_t*)a->fc2_w, (const op_t*)a->fc3_w,
-        nullptr, a->rows, a->hidden, a->accumulate, a->eps, zb);
+  const unsigned grid = (unsigned)((a->rows + 32 * TRW - 1) / (32 * TRW));
+  const op_t *w1 = (const op_t*)a->fc1_w, *w2 = (const op_t*)a->fc2_w, *w3 = (const op_t*)a->fc3_w;
+  const op_t* lo = (const op_t*)a->fc3_lo;
+  if (lo && a->fc3_mean_fix) {
+    float* partials = (float*)a->workspace;
+    float* corr = partials + (size_t)TRS_PARTIALS * C;
+    const long ntiles = a->rows / 32, ns = ntiles < TRS_TILES ? ntiles : TRS_TILES;
+    const int np = (int)((ns + TRW - 1) / TRW) * (a->hidden / 64);
+    if (ns > 0) {
+      tr_pair_kernel<false, TR_STATS><<<np, 64 * TRW, 0, st>>>(a->x_in, nullptr, a->norm_w, a->norm_b, w1, w2, lo,
+                                                              nullptr, a->rows, a->hidden, 0, a->eps, ZBiasArgs{},
+                                                              nullptr, partials);
+      PF_CHECK_LAUNCH("tr_pair_kernel (sampling pass)");
+    }
+    tr_corr_kernel<<<1, 1024, 0, st>>>(partials, ns > 0 ? np : 0, corr);   // no sample: corr = 0
+    PF_CHECK_LAUNCH("tr_corr_kernel");
+    tr_pair_kernel<ZBIAS, TR_MEANFIX><<<grid, 64 * TRW, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, w1, w2, w3,
+                                                                nullptr, a->rows, a->hidden, a->accumulate, a->eps,
+                                                                zb, corr, nullptr);
+  } else if (lo) {
+    tr_pair_kernel<ZBIAS, TR_HILO><<<grid, 64 * TRW, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, w1, w2, w3, lo,
+                                                             a->rows, a->hidden, a->accumulate, a->eps, zb, nullptr,
+                                                             nullptr);
+  } else {
+    tr_pair_kernel<ZBIAS, TR_PLAIN><<<grid, 64 * TRW, 0, st>>>(a->x_in, a->out, a->norm_w, a->norm_b, w1, w2, w3,
+                                                              nullptr, a->rows, a->hidden, a->accumulate, a->eps, zb,
+                                                              nullptr, nullptr);
+  }
   PF_CHECK_LAUNCH("tr_pair_kernel");
   return PF_OK;
 }
@@ -428,7 +571,7 @@ extern "C" int pf_linear_fwd(const float* x, const void* W, const float* bias, c
 
 extern "C" size_t pf_transition_workspace_size(long rows, int C_, int hidden) {
   if (rows <= 0 || C_ <= 0 || hidden <= 0) return 0;
-  if (C_ == C && hidden % 32 == 0) return 0;   // fused pair kernel: no scratch
+  if (C_ == C && hidden % 32 == 0) return TR_WS_BYTES;   // fused pair kernel: the mean-correction sums
   if (C_ == 64 && hidden == 256) return 0;      // fused C = 64 kernel: no scratch
   return (size_t)rows * (C_ + hidden) * sizeof(float);
 }
@@ -441,9 +584,8 @@ extern "C" int pf_transition_fwd(const pf_transition_args* a) {
   if (!a->x_in || !a->out || !a->norm_w || !a->norm_b || !a->fc1_w || !a->fc2_w || !a->fc3_w)
     return pf_fail(PF_E_INVALID, "pf_transition_fwd: null pointer argument");
   hipStream_t st = (hipStream_t)a->stream;
-  if (a->fc3_lo && a->C != C)
-    return pf_fail(PF_E_INVALID, "pf_transition_fwd: the fc3 residual (fc3_lo) is supported for C = 128 only");
-  if (a->C == C) return launch_tr_pair<false>(a, ZBiasArgs{}, (unsigned)((a->rows + 32 * TRW - 1) / (32 * TRW)));
+  if (const int rc = tr_check_fc3(a, "pf_transition_fwd")) return rc;
+  if (a->C == C) return launch_tr_pair<false>(a, ZBiasArgs{});
   if (a->C == 64 && a->hidden == 256) {
     const int cus = device_cus();
     if (cus <= 0) return pf_fail(PF_E_LAUNCH, "tr64_kernel: cannot query the device");
@@ -516,9 +658,15 @@ extern "C" int pf_transition_pair_bias_fwd(const pf_transition_args* a, const pf
   chk.z = a->out;   // the bias is computed from the transition's output
   int rc = pf_apb_check(&chk, "pf_transition_pair_bias_fwd", true);
   if (rc) return rc;
+  if ((rc = tr_check_fc3(a, "pf_transition_pair_bias_fwd"))) return rc;
+  if (a->fc3_mean_fix) {   // the sums must survive the bias writes of the same launch
+    const char *t0 = (const char*)a->workspace, *b0 = (const char*)apb->workspace;
+    if (t0 < b0 + apb->workspace_bytes && b0 < t0 + TR_WS_BYTES)
+      return pf_fail(PF_E_INVALID, "pf_transition_pair_bias_fwd: the transition workspace overlaps the attention's");
+  }
   const long NN = (long)apb->N * apb->N;
   if (a->rows != (long)apb->B * NN)
     return pf_fail(PF_E_INVALID, "pf_transition_pair_bias_fwd: rows %ld != B*N*N = %ld", a->rows, (long)apb->B * NN);
   const ZBiasArgs zb{apb->zln_w, apb->zln_b, (const op_t*)apb->w_z, pf_apb_bias_ptr(apb), NN, apb->H, apb->eps};
-  return launch_tr_pair<true>(a, zb, (unsigned)(a->rows / (32 * TRW)));   // N % 32 == 0: whole workgroups
+  return launch_tr_pair<true>(a, zb);   // N % 32 == 0: whole 32-pair tiles
 }

@@ -71,11 +71,12 @@ PF_DEV op_t mask_term(bool pad, float mv) {
 constexpr int TAP_WAVES = 8;
 constexpr int TAP_ROWS = 3 * C + 32;   // q, k, v rows, then 32 bias rows (H used, rest zero)
 // LDS: the weights [TAP_ROWS][CC + 8] op_t, their accumulator starts [TAP_ROWS] fp32, then (FAST)
-// the per-wave V block scales or the mean-correction mu [128] (the two never coexist)
+// the per-wave V block scales or the mean-correction mu [128] and its reduction scratch (the two
+// never coexist)
 template <int CC, bool FAST = false>
 constexpr size_t tap_lds() {
   return (size_t)TAP_ROWS * (CC + 8) * sizeof(op_t) + TAP_ROWS * sizeof(float) +
-         (FAST ? TAP_WAVES * 32 * sizeof(float) : PS_C * sizeof(float));
+         (FAST ? TAP_WAVES * 32 * sizeof(float) : (PS_C + 64 * TAP_WAVES) * sizeof(float));
 }
 
 // offb (optional, fp32 [3 C + H]): the exact W beta of the q, k, v and bias rows (else computed
@@ -114,7 +115,7 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
     st_x8(plds + row * LW + col, v);
   }
   if (!FAST && mf.offb && mf.stats) {
-    stats_mu(mf.stats, mu);
+    stats_mu(mf.stats, mu, mu + PS_C);
     __syncthreads();
   }
   for (int row = tid; row < TAP_ROWS; row += 64 * TAP_WAVES) {   // accumulator starts W beta

@@ -97,7 +97,7 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
   }
   for (int c = tid; c < CC; c += 64 * TMP_WAVES) gam[c] = lnw[c];
   float* mu = reinterpret_cast<float*>(lg + 2 * CC * LW);   // the output stages, free until the tile loop
-  if (offb && stats) stats_mu(stats, mu);
+  if (offb && stats) stats_mu(stats, mu, mu + PS_C);
   __syncthreads();
   for (int row = tid; row < 4 * CC; row += 64 * TMP_WAVES) {   // offsets W beta (one row per thread)
     float acc = 0.f;
@@ -501,7 +501,7 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
     gam_i[c] = lni_w[c];
   }
   float* mu = reinterpret_cast<float*>(xs - wid * XCH * XSP);   // the X stages, free until the tile loop
-  if (offb_g && stats) stats_mu(stats, mu);
+  if (offb_g && stats) stats_mu(stats, mu, mu + PS_C);
   __syncthreads();
   for (int row = tid; row < 2 * CC; row += 64 * TMO_WAVES) {
     const bool g = row >= CC;

@@ -257,9 +257,12 @@ def transition_workspace_bytes(rows: int, C: int, hidden: int, variant: str = DE
 
 def launch_transition(x_in: torch.Tensor, out: torch.Tensor, w: Mapping[str, torch.Tensor],
                       ws: Optional[torch.Tensor], accumulate: bool, eps: float = 1e-5,
-                      variant: str = DEFAULT_VARIANT, pair_bias: Optional[tuple] = None) -> None:
+                      variant: str = DEFAULT_VARIANT, pair_bias: Optional[tuple] = None,
+                      fc3_mean_fix: bool = False) -> None:
     """``pair_bias = (s, w_apb, n_heads, apb_ws, eps_apb)``: also write the single-track pair
-    bias of ``out`` into ``apb_ws`` in the same kernel (pf_transition_pair_bias_fwd; c_z = 128)."""
+    bias of ``out`` into ``apb_ws`` in the same kernel (pf_transition_pair_bias_fwd; c_z = 128).
+    ``fc3_mean_fix``: use ``w["fc3.weight.lo"]`` through the sampled mean correction instead of
+    the hi + lo product (needs ``ws``)."""
     C = x_in.shape[-1]
     rows = x_in.numel() // C
     a = _lib.TransitionArgs(
@@ -267,7 +270,7 @@ def launch_transition(x_in: torch.Tensor, out: torch.Tensor, w: Mapping[str, tor
         x_in=_ptr(x_in), out=_ptr(out), norm_w=_ptr(w["norm.weight"]), norm_b=_ptr(w["norm.bias"]),
         fc1_w=_ptr(w["fc1.weight"]), fc2_w=_ptr(w["fc2.weight"]), fc3_w=_ptr(w["fc3.weight"]),
         workspace=_ptr(ws), workspace_bytes=0 if ws is None else ws.numel(), stream=_stream(),
-        fc3_lo=_ptr(w.get("fc3.weight.lo")))
+        fc3_lo=_ptr(w.get("fc3.weight.lo")), fc3_mean_fix=int(fc3_mean_fix))
     if pair_bias is None:
         _lib.check(_lib.load(variant).pf_transition_fwd(ctypes.byref(a)), "pf_transition_fwd", variant)
         return

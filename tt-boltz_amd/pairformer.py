@@ -127,11 +127,14 @@ class Options:
     together with its rounding residual and multiply by both (default on).  A 16-bit weight's rounding error is the same at every
     position, so it adds up coherently through a deep stack; with the residual the weights are
     good to ~2^-22 of their size.
-    ``mean_correction``: the triangle multiplication's LN_in-side weights (p_in, g_in, g_out),
-    whose LDS does not hold them twice, get the exact W . beta offsets plus the mean correction
+    ``mean_correction``: the weights after a LayerNorm whose LDS does not hold them twice (the
+    triangle multiplication's p_in, g_in, g_out; the triangle attention's q, k, v and bias
+    projections) get the exact W . beta offsets plus the mean correction
     (W - W16) . (gamma * mu), mu the mean over positions of the normalized input, estimated per
-    call from sampled positions: the part of their rounding error that every position shares
-    (default on; c_z = 128, batch 1)."""
+    call from sampled positions: the part of their rounding error that every position shares.
+    The pair transition's fc3 then takes its residual the same way, (W - W16) . mean(h) over the
+    hidden activations of sampled positions, instead of as the hi + lo product (default on;
+    c_z = 128, batch 1)."""
 
     def __init__(self, eps: float = 1e-5, operand: str = ops.DEFAULT_VARIANT, overlap_single: bool = True,
                  single_delay: int = 1, weight_residuals: bool = True, mean_correction: bool = True):
@@ -330,7 +333,9 @@ class Transition(Module):
         if ws is None:
             nb = self.workspace_bytes(rows)
             ws = ops.workspace(nb, x.device) if nb else None
-        ops.launch_transition(x, out, self.w, ws, accumulate, self.options.eps, self.variant, pb)
+        # the sampled mean is one batch element's: batch 1 only (otherwise hi + lo)
+        mean_fix = self.options.mean_correction and "fc3.weight.lo" in self.w and x.dim() == 4 and x.shape[0] == 1
+        ops.launch_transition(x, out, self.w, ws, accumulate, self.options.eps, self.variant, pb, mean_fix)
         return out
 
 
@@ -440,10 +445,15 @@ class PairformerLayer(Module):
         return max(self.attention_pair_bias.workspace_bytes(B, N) + B * N * c_s * 4,
                    self.transition_s.workspace_bytes(B * N))
 
+    def transition_workspace_bytes(self, B: int, N: int) -> int:
+        """The pair transition's share at the start of the layer workspace (kept apart from
+        the single track's, which its fused pair bias writes in the same launch)."""
+        return (self.transition_z.workspace_bytes(B * N * N) + 255) // 256 * 256
+
     def workspace_bytes(self, B: int, N: int) -> int:
         n = max(self.triangle_multiplication_start.workspace_bytes(B, N),
                 self.triangle_attention_start.workspace_bytes(B, N))
-        return max(n, self.single_workspace_bytes(B, N))
+        return max(n, self.transition_workspace_bytes(B, N) + self.single_workspace_bytes(B, N))
 
     def __call__(self, s: Optional[torch.Tensor], z: torch.Tensor, pair_mask: Optional[torch.Tensor] = None,
                  mask: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None, n_valid: int = 0,
@@ -464,11 +474,13 @@ class PairformerLayer(Module):
             op()
             if single is not None and i + 1 == single.delay:
                 single.issue_pending()   # the previous layer's single track starts beside the rest
+        tr_nb = self.transition_workspace_bytes(B, N)
+        tr_ws = ws[:tr_nb] if tr_nb else None
         if not (self.transform_s and s is not None):
-            self.transition_z(z, out=z, accumulate=True, ws=ws)
+            self.transition_z(z, out=z, accumulate=True, ws=tr_ws)
             return s, z
         c_s = s.shape[-1]
-        sws = ws if single is None else single.ws
+        sws = ws[tr_nb:] if single is None else single.ws
         s_norm = sws[: B * N * c_s * 4].view(torch.float32).view(B, N, c_s)
         apb_ws = sws[B * N * c_s * 4:]
         if single is not None:
@@ -477,10 +489,10 @@ class PairformerLayer(Module):
         # the single track reads z only through the pair bias of the final z: with the 16-bit
         # pair transition it comes out of the same kernel
         if self.transition_z.fuses_pair_bias():
-            self.transition_z(z, out=z, accumulate=True, ws=ws,
+            self.transition_z(z, out=z, accumulate=True, ws=tr_ws,
                               pair_bias=(self.attention_pair_bias, s, apb_ws))
         else:
-            self.transition_z(z, out=z, accumulate=True, ws=ws)
+            self.transition_z(z, out=z, accumulate=True, ws=tr_ws)
             self.attention_pair_bias(s, z, mask, out=s, ws=apb_ws, n_valid=n_valid, part="bias")
         if single is None:
             ops.launch_layernorm(s, self.pre_norm_s_weight, self.pre_norm_s_bias, s_norm, self.options.eps,
