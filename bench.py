@@ -794,9 +794,10 @@ def main() -> int:
         "precision_paths": {"plain16_layers_per_s": round(1000.0 / plain_ms, 3),
                             "cost_pct": round(100.0 * (ms_step / plain_ms - 1.0), 2),
                             "note": "value runs the weight-precision paths (hi + lo weights in the trimul "
-                                    "output, triangle-attention output and recycling projections; the "
-                                    "trimul's mean correction); plain16 is the same layer with every weight "
-                                    "a single 16-bit rounding"},
+                                    "output, triangle-attention gate/output and recycling projections; the "
+                                    "mean correction of the trimul's and triangle attention's input "
+                                    "projections and of the pair transition's fc3); plain16 is the same "
+                                    "layer with every weight a single 16-bit rounding"},
         "data": "synthetic (seeded N(0,1) inputs, random-init weights, seed 0)",
         "config": {"workload": f"one Boltz-2 PairformerLayer, N={N}, c_z=128, c_s=384, tri-att 4x32, "
                                f"single-att 16x24, masks all ones, device-resident fp32 z/s; layers back to "

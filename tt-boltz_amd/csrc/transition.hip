@@ -50,7 +50,10 @@ PF_DEV opx8 lds_x8(const char* p) { return *reinterpret_cast<const opx8*>(p); }
 enum TrMode { TR_PLAIN = 0, TR_HILO = 1, TR_MEANFIX = 2, TR_STATS = 3 };
 constexpr int TRW = 4;                       // waves of a workgroup
 constexpr int TR_BLK = 8192;                 // bytes of one fp16 weight block
-constexpr int TRS_TILES = 256;               // sampled tiles of the TR_STATS pass
+#ifndef PF_TRS_TILES
+#define PF_TRS_TILES 256
+#endif
+constexpr int TRS_TILES = PF_TRS_TILES;      // sampled tiles of the TR_STATS pass
 constexpr int TRS_MAX_HIDDEN = 512;          // its hidden sizes: multiples of 64 up to this
 constexpr int TRS_PARTIALS = TRS_TILES / TRW * (TRS_MAX_HIDDEN / 64);   // its workgroups (at most)
 template <int MODE>
@@ -66,7 +69,7 @@ __global__ __launch_bounds__(64 * TRW, MODE == TR_HILO || MODE == TR_STATS ? 2 :
   constexpr bool HILO = MODE == TR_HILO, STATS = MODE == TR_STATS;
   constexpr int STAGE = tr_stage<MODE>();
   __shared__ __attribute__((aligned(16))) char tl[2 * STAGE];
-  __shared__ float red[STATS ? TRW * C : 1];   // the sampling pass's sums
+  __shared__ float red[STATS ? 2 * TRW * C : 1];   // the sampling pass's sums
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nhb = hidden / 32;
@@ -162,20 +165,24 @@ __global__ __launch_bounds__(64 * TRW, MODE == TR_HILO || MODE == TR_STATS ? 2 :
       }
   }
   if constexpr (STATS) {
-    // sum over the wave's 32 pairs (the lanes of each half), then over the workgroup's waves
+    // sums over each row of 16 lanes (16 pairs) for all 64 values first (independent DPP chains),
+    // then one store per row: red[2 wid + row16 parity][channel], the 8 rows summed below
 #pragma unroll
     for (int ob = 0; ob < 4; ++ob)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float v = row16_sum(acc[ob][i]);
-        v += __shfl_xor(v, 16);
-        if (m == 0) red[wid * C + 32 * ob + 8 * (i >> 2) + 4 * h + (i & 3)] = live ? v : 0.f;
-      }
+      for (int i = 0; i < 16; ++i) acc[ob][i] = row16_sum(acc[ob][i]);
+    if ((lane & 15) == 0) {
+      float* r = red + (2 * wid + ((lane >> 4) & 1)) * C + 4 * h;
+#pragma unroll
+      for (int ob = 0; ob < 4; ++ob)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) r[32 * ob + 8 * (i >> 2) + (i & 3)] = live ? acc[ob][i] : 0.f;
+    }
     __syncthreads();
     if (tid < C) {
       float sum = 0.f;
 #pragma unroll
-      for (int w = 0; w < TRW; ++w) sum += red[w * C + tid];
+      for (int w = 0; w < 2 * TRW; ++w) sum += red[w * C + tid];
       partials[blockIdx.x * C + tid] = sum / (32.f * (float)ns);
     }
   } else {
