@@ -22,7 +22,7 @@ at N=512) and a plain copy kernel of known size, for ``rocprofv3 --pmc FETCH_SIZ
 ``profiles/kernel_traffic_n512.json`` when that file exists.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--n 512] [--no-cpu-baseline]
-                       [--no-stack] [--probe-traffic]
+                       [--no-stack] [--probe-traffic] [--probe-contract]
 """
 from __future__ import annotations
 
@@ -129,6 +129,182 @@ def probe_traffic(N: int) -> int:
     return 0
 
 
+CONTRACT_SIZES = (512, 768, 1024)
+
+
+def probe_contract() -> int:
+    """The 16-bit trimul contraction and the vendor library on the same [128, N, N] fp16 planes at
+    N = 512, 768, 1024, 5 launches each, for rocprofv3 runs: X = A B^T through
+    pf_trimul_contract (fp16 output), then torch.bmm(A, B^T) (hipBLASLt; B^T materialized once,
+    so the library sees contiguous operands)."""
+    import torch
+    from tt_boltz_amd import ops
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    for N in CONTRACT_SIZES:
+        A = torch.randn((128, N, N), device=dev, generator=g).half()
+        Bm = torch.randn((128, N, N), device=dev, generator=g).half()
+        Bt = Bm.transpose(1, 2).contiguous()
+        X = torch.empty((128, N, N), dtype=torch.float16, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            ops.launch_trimul_contract(A, Bm, X)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            torch.bmm(A, Bt, out=X)
+        torch.cuda.synchronize()
+        del A, Bm, Bt, X
+        torch.cuda.empty_cache()
+    print(json.dumps({"probe": "contract", "sizes": CONTRACT_SIZES, "launches": 5}), flush=True)
+    return 0
+
+
+CONTRACT_PMC_PASSES = ("SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_INST_ANY SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT "
+                       "SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA GRBM_GUI_ACTIVE",
+                       "SQ_WAIT_ANY SQ_INSTS_VALU SQ_INSTS_SALU SQ_ACTIVE_INST_LDS SQ_INSTS_VMEM_RD SQ_WAVE_CYCLES "
+                       "GRBM_GUI_ACTIVE FETCH_SIZE")
+
+
+def summarize_contract(kt_dir: str, pmc_dirs) -> None:
+    """profiles/contract_vs_hipblaslt.md from rocprofv3 CSV output of ``bench.py --probe-contract``
+    (one --kernel-trace run and one --pmc run per CONTRACT_PMC_PASSES entry).  Dispatches are told
+    apart by kernel family (this build's tm_contract kernels, the library's Cijk kernels); the
+    k-th run of consecutive dispatches of a family is the k-th of CONTRACT_SIZES."""
+    import collections
+    import csv
+    mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")
+
+    def family(name):
+        return "this build" if "tm_contract" in name else "hipBLASLt" if "Cijk" in name else None
+
+    def runs(rows_in):
+        """dispatch id -> (family, N): the k-th run of consecutive dispatches of one family is
+        CONTRACT_SIZES[k] (the probe alternates the two families per size)."""
+        out, prev, seen = {}, None, collections.Counter()
+        for did, name in sorted(rows_in):
+            f = family(name)
+            if not f:
+                continue
+            if f != prev:
+                seen[f] += 1
+                prev = f
+            out[did] = (f, CONTRACT_SIZES[min(seen[f], len(CONTRACT_SIZES)) - 1])
+        return out
+
+    trace = list(csv.DictReader(open(os.path.join(kt_dir, "run_kernel_trace.csv"))))
+    tag = runs({(int(r["Dispatch_Id"]), r["Kernel_Name"]) for r in trace})
+    dur = collections.defaultdict(list)
+    names = {}
+    for r in trace:
+        key = tag.get(int(r["Dispatch_Id"]))
+        if key:
+            dur[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+            names[key[0]] = r["Kernel_Name"][:60]
+    cnt = collections.defaultdict(lambda: collections.defaultdict(list))
+    for d in pmc_dirs:
+        pmc = list(csv.DictReader(open(os.path.join(d, "run_counter_collection.csv"))))
+        ptag = runs({(int(r["Dispatch_Id"]), r["Kernel_Name"]) for r in pmc})
+        for r in pmc:
+            key = ptag.get(int(r["Dispatch_Id"]))
+            if key:
+                cnt[key][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    rows = []
+    for f in ("this build", "hipBLASLt"):
+        for N in CONTRACT_SIZES:
+            d, c = dur[(f, N)], cnt[(f, N)]
+            if not d:
+                continue
+            us = mean(d)
+            g = lambda k: mean(c[k]) if c.get(k) else float("nan")
+            rows.append(dict(f=f, N=N, us=us, tf=2 * N ** 3 * 128 / (us * 1e-6) / 1e12,
+                             busy=g("SQ_VALU_MFMA_BUSY_CYCLES") / (128 * g("GRBM_GUI_ACTIVE")),
+                             wait=g("SQ_WAIT_INST_ANY") / g("SQ_WAVE_CYCLES"), wany=g("SQ_WAIT_ANY") / g("SQ_WAVE_CYCLES"),
+                             lds=g("SQ_INSTS_LDS"), conf=g("SQ_LDS_BANK_CONFLICT"), mfma=g("SQ_INSTS_MFMA"),
+                             valu=g("SQ_INSTS_VALU"), salu=g("SQ_INSTS_SALU"), vmem=g("SQ_INSTS_VMEM_RD"),
+                             waves=g("SQ_WAVES"), fetch=g("FETCH_SIZE") * 1024))
+    cmd = "rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- python3 bench.py --probe-contract"
+    md = ["# Trimul contraction vs hipBLASLt (MI355X, one GPU)", "",
+          "Workload: `bench.py --probe-contract`: X = A B^T on [128, N, N] fp16 planes, fp32 accumulation, fp16 "
+          "output, 5 launches each of this build's `pf_trimul_contract` and of `torch.bmm` (hipBLASLt, B^T "
+          "contiguous) at N = 512, 768, 1024.  Commands (one counter pass each; the table is made by "
+          "`bench.py --summarize-contract`):", "", f"    {cmd}"]
+    md += [f"    rocprofv3 --pmc {c} --output-format csv -d <dir> -o run -- python3 bench.py --probe-contract"
+           for c in CONTRACT_PMC_PASSES]
+    md += ["", f"Kernels: this build `{names.get('this build', '?')}`, the library `{names.get('hipBLASLt', '?')}`.",
+           "Means per dispatch.  MFMA busy = `SQ_VALU_MFMA_BUSY_CYCLES / (128 GRBM_GUI_ACTIVE)`; wait(inst) = "
+           "`SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES` (stalled on s_waitcnt); wait(any) = `SQ_WAIT_ANY / SQ_WAVE_CYCLES`; "
+           "FETCH is the raw `FETCH_SIZE` (uncalibrated).", "",
+           "| N | kernel | us | TF/s | of 2.5 PF/s | MFMA busy | wait(inst) | wait(any) | waves | MFMA instr | LDS instr "
+           "| LDS bank conflict cycles | VALU instr | SALU instr | VMEM rd instr | FETCH MB |",
+           "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for r in sorted(rows, key=lambda r: (r["N"], r["f"] != "this build")):
+        md.append(f"| {r['N']} | {r['f']} | {r['us']:.1f} | {r['tf']:.0f} | {r['tf'] / 2500:.3f} | {r['busy']:.3f} | "
+                  f"{r['wait']:.2f} | {r['wany']:.2f} | {r['waves']:.0f} | {r['mfma']:.3g} | {r['lds']:.3g} | "
+                  f"{r['conf']:.3g} | {r['valu']:.3g} | {r['salu']:.3g} | {r['vmem']:.3g} | {r['fetch'] / 1e6:.0f} |")
+    open(os.path.join(ROOT, "profiles", "contract_vs_hipblaslt.md"), "w").write("\n".join(md) + "\n")
+
+
+def summarize_bench(kt_dir: str, bench_log: str) -> None:
+    """profiles/bench_n512_roofline_kernel_stats.txt from a --kernel-trace run of the bench itself
+    (``bench.py --no-stack --no-cpu-baseline``) and the JSON line it printed: the in-layer
+    attention-core dispatches (those right after a ta_proj dispatch on the same queue, i.e. inside a
+    layer) against the line's roofline.launch_ms, the contraction's longest run of back-to-back
+    dispatches against roofline_contract.launch_ms, and every kernel of the run."""
+    import collections
+    import csv
+    line = next(json.loads(l) for l in open(bench_log) if l.startswith('{"metric"'))
+    rows = sorted(csv.DictReader(open(os.path.join(kt_dir, "run_kernel_trace.csv"))),
+                  key=lambda r: int(r["Start_Timestamp"]))
+    us = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    fp16 = lambda r: "DF16_" in r["Kernel_Name"] and "DF16b" not in r["Kernel_Name"]
+    prev, inlayer = {}, []
+    for r in rows:
+        q = r["Queue_Id"]
+        k = _kernel_short(r["Kernel_Name"])
+        if k == "ta_attn_kernel" and fp16(r) and prev.get(q) == "ta_proj_kernel":
+            inlayer.append(us(r))
+        prev[q] = k
+    best, run, last = [], [], None
+    for r in rows:
+        k = _kernel_short(r["Kernel_Name"])
+        if k == "tm_contract_dma_kernel" and fp16(r) and last == k:
+            run.append(us(r))
+        elif k == "tm_contract_dma_kernel" and fp16(r):
+            run = [us(r)]
+        else:
+            run = run if k.startswith("__amd") else []
+        if len(run) > len(best):
+            best = list(run)
+        last = k if not k.startswith("__amd") else last
+    mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")
+    ro, rc = line["roofline"], line["roofline_contract"]
+    a_us, c_us = mean(inlayer), mean(best)
+    lines = ["# Roofline kernels of the bench, from a kernel trace of the bench itself (MI355X, one GPU)",
+             "# command: rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- python3 bench.py "
+             "--no-stack --no-cpu-baseline",
+             "# (this file: bench.py --summarize-bench <dir> <the run's stdout>)",
+             "# ta_attn_kernel inside the layers: the fp16 dispatches right after a ta_proj dispatch on their queue",
+             f"#   {len(inlayer)} dispatches, mean {a_us:.1f} us   | bench roofline.launch_ms = {ro['launch_ms']:.4f} ms "
+             f"({ro['launch_ms_source']})",
+             f"#   4 N^3 128 FLOP = {ro['flop_per_launch'] / 1e9:.2f} GFLOP / {a_us:.1f} us = "
+             f"{ro['flop_per_launch'] / (a_us * 1e-6) / 1e12:.0f} TF/s = "
+             f"{ro['flop_per_launch'] / (a_us * 1e-6) / 2.5e15:.3f} of 2.5 PF/s (bench frac {ro['frac']:.4f})",
+             f"# tm_contract_dma_kernel: {len(best)} consecutive fp16 dispatches, mean {c_us:.1f} us   | bench "
+             f"roofline_contract.launch_ms = {rc['launch_ms']:.4f} ms",
+             f"#   {rc['algorithmic_bytes'] / 1e6:.1f} MB / {c_us:.1f} us = {rc['algorithmic_bytes'] / (c_us * 1e3):.0f} "
+             f"GB/s = {rc['algorithmic_bytes'] / (c_us * 1e3) / 8000:.3f} of 8 TB/s (bench frac {rc['frac']:.4f})",
+             "# Every kernel of the run (warm-up, timed layers, serial layer, per-op breakdown, roofline loops):",
+             f"# {'kernel':40s} {'calls':>6s} {'avg_us':>9s} {'total_ms':>9s}"]
+    dur = collections.defaultdict(list)
+    for r in rows:
+        k = _kernel_short(r["Kernel_Name"]) + ("" if fp16(r) or "DF16b" not in r["Kernel_Name"] else " (bf16 lib)")
+        dur[k].append(us(r))
+    for k, d in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
+        if not k.startswith(("distribution", "reduce")):
+            lines.append(f"  {k:40s} {len(d):6d} {mean(d):9.1f} {sum(d) / 1e3:9.3f}")
+    open(os.path.join(ROOT, "profiles", "bench_n512_roofline_kernel_stats.txt"), "w").write("\n".join(lines) + "\n")
+
+
 # ----------------------------------------------------------------------------- profile summaries
 PROBE_PMC_PASSES = ("SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS "
                     "SQ_VALU_MFMA_BUSY_CYCLES SQ_WAIT_INST_ANY GRBM_GUI_ACTIVE",
@@ -139,6 +315,8 @@ def _kernel_short(name: str) -> str:
     import re
     m = re.search(r"N_\d+([a-z0-9_]+_kernel)|([a-z0-9_]+_kernel)", name)
     k = (m.group(1) or m.group(2)) if m else name[:40]
+    if k == "tr_pair_kernel" and ("Li3E" in name or ", 3>" in name):
+        return "tr_pair_kernel (fc3 sampling pass)"
     return "copy (torch.mul, calibration)" if "MulFunctor" in name else k
 
 
@@ -282,6 +460,32 @@ def time_events(fn, reps: int, stream) -> float:
     b.record(stream)
     torch.cuda.synchronize()
     return a.elapsed_time(b) / reps
+
+
+def contract_vs_library(reps: int = 10) -> dict:
+    """The 16-bit trimul contraction X = A B^T on [128, N, N] fp16 planes against torch.bmm
+    (hipBLASLt; B^T contiguous) at N = 512, 768, 1024, HIP events around `reps` launches each on
+    the current stream; TF/s = 2 N^3 128 / time."""
+    import torch
+    from tt_boltz_amd import ops
+    dev, stream = torch.device("cuda", 0), torch.cuda.current_stream()
+    g = torch.Generator(device=dev).manual_seed(0)
+    res = {}
+    for N in CONTRACT_SIZES:
+        A = torch.randn((128, N, N), device=dev, generator=g).half()
+        Bm = torch.randn((128, N, N), device=dev, generator=g).half()
+        Bt = Bm.transpose(1, 2).contiguous()
+        X = torch.empty((128, N, N), dtype=torch.float16, device=dev)
+        ours = time_events(lambda: ops.launch_trimul_contract(A, Bm, X), reps, stream)
+        lib = time_events(lambda: torch.bmm(A, Bt, out=X), reps, stream)
+        tf = lambda ms: round(2 * N ** 3 * 128 / (ms * 1e-3) / 1e12, 1)
+        res[str(N)] = {"this_build_ms": round(ours, 4), "hipblaslt_ms": round(lib, 4), "this_build_tflops": tf(ours),
+                       "hipblaslt_tflops": tf(lib), "speedup": round(lib / ours, 3)}
+        del A, Bm, Bt, X
+        torch.cuda.empty_cache()
+    res["note"] = ("pf_trimul_contract (fp16 output) vs torch.bmm(A, B^T) on the same random fp16 planes, fp32 "
+                   "accumulation; counters side by side in profiles/contract_vs_hipblaslt.md")
+    return res
 
 
 def stack_bench(N: int = 768, n_layers: int = 64, recycling_steps: int = 3, seed: int = 3) -> dict:
@@ -581,11 +785,22 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--probe-traffic", action="store_true")
+    ap.add_argument("--probe-contract", action="store_true")
+    ap.add_argument("--summarize-bench", nargs=2, metavar=("KT_DIR", "BENCH_LOG"),
+                    help="write profiles/bench_n512_roofline_kernel_stats.txt from a kernel trace of the bench")
+    ap.add_argument("--summarize-contract", nargs="+", metavar="DIR",
+                    help="KT_DIR PMC_DIR...: write profiles/contract_vs_hipblaslt.md from rocprofv3 CSV output")
     ap.add_argument("--summarize-probe", nargs="+", metavar="DIR",
                     help="KT_DIR PMC_DIR...: write the profiles/ summaries for --n from rocprofv3 CSV output")
     args = ap.parse_args()
     if args.summarize_probe:
         summarize_probe(args.n, args.summarize_probe[0], args.summarize_probe[1:])
+        return 0
+    if args.summarize_bench:
+        summarize_bench(*args.summarize_bench)
+        return 0
+    if args.summarize_contract:
+        summarize_contract(args.summarize_contract[0], args.summarize_contract[1:])
         return 0
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}): this build measures the "
@@ -594,6 +809,8 @@ def main() -> int:
 
     if args.probe_traffic:
         return probe_traffic(args.n)
+    if args.probe_contract:
+        return probe_contract()
 
     import torch
     from tt_boltz_amd import ops, pairformer, synthetic
@@ -814,6 +1031,8 @@ def main() -> int:
     }
     if not args.no_stack:
         del zb, sb
+        out["contract_vs_hipblaslt"] = contract_vs_library()
+        torch.cuda.empty_cache()
         out["stack"] = stack_bench()
         torch.cuda.empty_cache()
         out["fast"] = fast_bench()
