@@ -504,12 +504,23 @@ int pf_add_fwd(const float* a, const float* b, float* out, long n, void* stream)
 int pf_attend_timing(int enable);
 int pf_attend_timing_read(double* total_ms, int* launches);
 
+/* The same for a chosen kernel kind: PF_TIMED_ATTEND (as above) or PF_TIMED_CONTRACT8 (the
+ * block-fp8 contraction inside pf_trimul_mx8_fwd and pf_trimul_mx8_contract). */
+#define PF_TIMED_ATTEND 0
+#define PF_TIMED_CONTRACT8 1
+#define PF_TIMED_KINDS 2
+int pf_kernel_timing(int kind, int enable);
+int pf_kernel_timing_read(int kind, double* total_ms, int* launches);
+
 /* MFMA issue rate under load: `workgroups` workgroups of 16 waves each issue `iters` (a
  * multiple of 4) rounds of four mutually independent 32x32x16 16-bit MFMAs (pseudo-random operands in (-1, 1) that change
  * every MFMA), i.e. pf_mfma_rate_probe_waves(workgroups) * iters * 4 * 32768 FLOP; every wave
  * writes one float of `sink` (workgroups * 16 floats). */
 long pf_mfma_rate_probe_waves(int workgroups);
 int pf_mfma_rate_probe(int workgroups, int iters, float* sink, void* stream);
+/* The same on the block-scaled fp8 MFMA (32x32x64 e4m3, unit scales): 4 * 131072 FLOP per
+ * round and wave. */
+int pf_mfma8_rate_probe(int workgroups, int iters, float* sink, void* stream);
 
 #ifdef __cplusplus
 }

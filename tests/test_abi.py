@@ -157,6 +157,20 @@ def test_workspace_sizes():
     assert lib.pf_trimul_mx8_workspace_size(1, 512, 128) == 2 * planes + 2 * planes // 32 + 2 * planes
 
 
+def test_measurement_aids_reject_bad_arguments_without_launching():
+    lib = _lib.load()
+    assert lib.pf_kernel_timing(2, 1) == -1 and "unknown kind 2" in _err()
+    assert lib.pf_kernel_timing(-1, 0) == -1 and "unknown kind" in _err()
+    ms, n = ctypes.c_double(0.0), ctypes.c_int(0)
+    assert lib.pf_kernel_timing_read(7, ctypes.byref(ms), ctypes.byref(n)) == -1 and "unknown kind 7" in _err()
+    assert lib.pf_kernel_timing_read(0, None, None) == -1 and "null output pointer" in _err()
+    assert lib.pf_mfma8_rate_probe(4, 6, 16, None) == -1 and "multiple of 4" in _err()
+    assert lib.pf_mfma_rate_probe(0, 8, 16, None) == -1 and "workgroups > 0" in _err()
+    # timing switched on and off without any launch records nothing
+    assert lib.pf_kernel_timing(1, 1) == 0 and lib.pf_kernel_timing(1, 0) == 0
+    assert lib.pf_kernel_timing_read(1, ctypes.byref(ms), ctypes.byref(n)) == 0 and n.value == 0 and ms.value == 0.0
+
+
 def test_python_check_raises_with_message():
     lib = _lib.load()
     lib.pf_trimul_fwd(None)

@@ -175,8 +175,11 @@ SIGNATURES = {
     "pf_transition_mx8_pair_bias_fwd": (c_int, [ctypes.POINTER(TransitionMx8Args), ctypes.POINTER(ApbArgs)]),
     "pf_attend_timing": (c_int, [c_int]),
     "pf_attend_timing_read": (c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_int)]),
+    "pf_kernel_timing": (c_int, [c_int, c_int]),
+    "pf_kernel_timing_read": (c_int, [c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_int)]),
     "pf_mfma_rate_probe_waves": (c_long, [c_int]),
     "pf_mfma_rate_probe": (c_int, [c_int, c_int, c_void_p, c_void_p]),
+    "pf_mfma8_rate_probe": (c_int, [c_int, c_int, c_void_p, c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -791,7 +791,9 @@ extern "C" int pf_trimul_mx8_fwd(const pf_trimul_mx8_args* a) {
   PF_CHECK_LAUNCH("tm8_proj_kernel");
   const int tpd = (N + BT - 1) / BT;
   const int total = B * C * tpd * tpd;
+  pf_kernel_mark(PF_TIMED_CONTRACT8, st, 0);
   tm8_contract_kernel<op_t><<<total, 64 * TM8C_WAVES, TM8C_LDS, st>>>(t.A8, t.B8, t.SA, t.SB, t.X, N, tpd, total, X_STORE_SCALE);
+  pf_kernel_mark(PF_TIMED_CONTRACT8, st, 1);
   PF_CHECK_LAUNCH("tm8_contract_kernel");
   const long nsteps = (long)B * N * N / 128;
   // persistent: two 4-wave workgroups per CU, each staging the weights once
@@ -817,8 +819,10 @@ extern "C" int pf_trimul_mx8_contract(const void* A8, const void* B8, const void
     return rc;
   const int tpd = (N + BT - 1) / BT;
   const int total = planes * tpd * tpd;
+  pf_kernel_mark(PF_TIMED_CONTRACT8, (hipStream_t)stream, 0);
   tm8_contract_kernel<float><<<total, 64 * TM8C_WAVES, TM8C_LDS, (hipStream_t)stream>>>(
       (const uint8_t*)A8, (const uint8_t*)B8, (const uint8_t*)SA, (const uint8_t*)SB, X, N, tpd, total, 1.f);
+  pf_kernel_mark(PF_TIMED_CONTRACT8, (hipStream_t)stream, 1);
   PF_CHECK_LAUNCH("tm8_contract_kernel");
   return PF_OK;
 }

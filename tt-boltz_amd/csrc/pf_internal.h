@@ -58,3 +58,5 @@ int pf_pair_logits(const float* z, const float* lnw, const float* lnb, const voi
 // for this host thread, the launcher records an event before (end = 0) and after (end = 1)
 // every ta_attn_kernel launch on its stream; otherwise a no-op.
 void pf_attend_mark(hipStream_t st, int end);
+// The same for any kind PF_TIMED_* (pf_kernel_timing).
+void pf_kernel_mark(int kind, hipStream_t st, int end);

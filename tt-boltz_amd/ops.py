@@ -225,12 +225,30 @@ def attend_timing_read(variant: str = DEFAULT_VARIANT):
     return ms.value, n.value
 
 
+TIMED_ATTEND, TIMED_CONTRACT8 = 0, 1   # pf_kernel_timing kinds (PF_TIMED_*)
+
+
+def kernel_timing(kind: int, enable: bool, variant: str = DEFAULT_VARIANT) -> None:
+    """``attend_timing`` for a chosen kernel kind (TIMED_ATTEND, TIMED_CONTRACT8)."""
+    _lib.check(_lib.load(variant).pf_kernel_timing(kind, 1 if enable else 0), "pf_kernel_timing", variant)
+
+
+def kernel_timing_read(kind: int, variant: str = DEFAULT_VARIANT):
+    """(summed launch ms, launches) of the kind's launches recorded since ``kernel_timing``."""
+    ms, n = ctypes.c_double(0.0), ctypes.c_int(0)
+    _lib.check(_lib.load(variant).pf_kernel_timing_read(kind, ctypes.byref(ms), ctypes.byref(n)),
+               "pf_kernel_timing_read", variant)
+    return ms.value, n.value
+
+
 def mfma_rate_probe(device: torch.device, iters: int = 20000, per_cu: int = 2, reps: int = 3,
-                    variant: str = DEFAULT_VARIANT) -> dict:
-    """Sustained 16-bit MFMA rate of the chip under load (pseudo-random operands, every SIMD
-    issuing back-to-back 32x32x16 MFMAs from ``4 * per_cu`` waves), timed with HIP events: the
-    best of ``reps`` launches after one warm-up."""
+                    variant: str = DEFAULT_VARIANT, fp8: bool = False) -> dict:
+    """Sustained MFMA rate of the chip under load (pseudo-random operands, every SIMD issuing
+    back-to-back 32x32x16 16-bit MFMAs, or with ``fp8`` block-scaled 32x32x64 e4m3 MFMAs, from
+    ``4 * per_cu`` waves), timed with HIP events: the best of ``reps`` launches after one
+    warm-up."""
     lib = _lib.load(variant)
+    probe, flop_per_mfma = (lib.pf_mfma8_rate_probe, 131072) if fp8 else (lib.pf_mfma_rate_probe, 32768)
     cus = torch.cuda.get_device_properties(device).multi_processor_count
     wgs = cus * per_cu
     waves = lib.pf_mfma_rate_probe_waves(wgs)
@@ -240,13 +258,13 @@ def mfma_rate_probe(device: torch.device, iters: int = 20000, per_cu: int = 2, r
     for r in range(reps + 1):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        _lib.check(lib.pf_mfma_rate_probe(wgs, iters, _ptr(sink), stream), "pf_mfma_rate_probe", variant)
+        _lib.check(probe(wgs, iters, _ptr(sink), stream), "pf_mfma_rate_probe", variant)
         b.record()
         torch.cuda.synchronize()
         ms = a.elapsed_time(b)
         if r and (best is None or ms < best):
             best = ms
-    flop = waves * iters * 4 * 32768
+    flop = waves * iters * 4 * flop_per_mfma
     return {"tflops": round(flop / (best * 1e-3) / 1e12, 1), "launch_ms": round(best, 3), "waves": waves,
             "mfma_per_wave": iters * 4, "finite": bool(torch.isfinite(sink).all())}
 
