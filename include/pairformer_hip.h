@@ -195,8 +195,10 @@ typedef struct pf_transition_args {
   /* With fc3_lo: 0 = multiply by fc3_16 + residual at every position; 1 = multiply by fc3_16
    * and add residual . mean(h), h = silu(fc1 LN(x)) * fc2 LN(x) averaged over up to 256 sampled
    * tiles of 32 consecutive rows (a pass over those rows before the main one): the part of the
-   * residual's error that every position shares, at a fraction of the cost.  Needs the
-   * workspace (pf_transition_workspace_size; C = 128) and hidden a multiple of 64, <= 512. */
+   * residual's error that every position shares, at a fraction of the cost.  The sample is
+   * drawn from all rows (with B > 1 the batch elements' means are pooled; the Python module
+   * uses it for one batch element).  Needs the workspace (pf_transition_workspace_size;
+   * C = 128) and hidden a multiple of 64, <= 512. */
   int fc3_mean_fix;
 } pf_transition_args;
 
