@@ -8,7 +8,9 @@
 //                    the output-aligned layout (pf_common.h): fc3 yields D[channel][pair],
 //                    so a lane owns one pair and writes 16-byte runs, and the residual is
 //                    fetched with 16-byte loads, all issued before the first store.  Weight
-//                    blocks arrive by LDS DMA (layout at the kernel).
+//                    blocks arrive by LDS DMA (layout at the kernel).  fc3's rounding
+//                    residual enters as a second MFMA or through a sampled mean
+//                    correction (TrMode below).
 //                    Replaces Transition.forward (tt_bio/boltz2.py:1227-1258) and the ttnn
 //                    Transition (tt_bio/tenstorrent.py:856-946).
 //   ln_rows_kernel   LayerNorm over rows, any C (nn.LayerNorm / tt_bio/boltz2.py:738-768).

@@ -123,10 +123,11 @@ class Options:
     1.254 vs 1.263 ms per layer with 0; 1.269 with 2, 1.308 with 4).
     ``weight_residuals``: the pair kernels whose weights fit twice in LDS (the triangle
     attention's gate and output projection, the triangle multiplication's output projection,
-    the pair transition's output projection, the recycling projection) take each 16-bit weight
-    together with its rounding residual and multiply by both (default on).  A 16-bit weight's rounding error is the same at every
-    position, so it adds up coherently through a deep stack; with the residual the weights are
-    good to ~2^-22 of their size.
+    the recycling projection; the pair transition's output projection when the mean correction
+    is off or the batch is larger than one) take each 16-bit weight together with its rounding
+    residual and multiply by both (default on).  A 16-bit weight's rounding error is the same at
+    every position, so it adds up coherently through a deep stack; with the residual the
+    weights are good to ~2^-22 of their size.
     ``mean_correction``: the weights after a LayerNorm whose LDS does not hold them twice (the
     triangle multiplication's p_in, g_in, g_out; the triangle attention's q, k, v and bias
     projections) get the exact W . beta offsets plus the mean correction
