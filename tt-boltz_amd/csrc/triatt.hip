@@ -433,7 +433,7 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   opx8 qf[2], qn[2];   // this head's Q fragments, the next head's (loaded a step ahead)
   f32x16 o;
   float mh, lsum;
-  bool mset;
+  uint64_t mset;   // lane mask: the queries (lanes) that have a reference maximum
   auto q_fetch = [&](int hd) PF_INLINE {
     const int jq = min(jq0, N - 32);
     const op_t* qptr = Q + ((((long)b * N + ip) * H + hd) * N + jq + m) * D + 8 * h;
@@ -444,7 +444,7 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
     o = zero16();
     lsum = 0.f;
     mh = 0.f;
-    mset = false;
+    mset = 0;
     set_fb(0.f);
   };
   // P = exp2(S') packed into the two P.V operands; returns the lane's row sum
@@ -497,22 +497,25 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
       __builtin_amdgcn_s_setprio(0);
       u32x4 pf[2];
       float l = exp_pack(sc, pf);
-      if (__ballot(!mset || l > LSTEP_MAX) != 0) {
+      // the lane masks come straight from v_cmp (a bool ballot would materialize and re-test
+      // each lane's predicate); every lane is active here (a live row's valid query block)
+      if ((__builtin_amdgcn_fcmpf(l, LSTEP_MAX, 2 /* ordered > */) | ~mset) != 0) {
         float mx = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[r]);
         mx = xor32_max(mx);
-        const float d = mset ? (mx > RESCALE_SLACK ? mx : 0.f) : (mx == -INFINITY ? 0.f : mx);
+        const bool ms = (mset >> lane) & 1;
+        const float d = ms ? (mx > RESCALE_SLACK ? mx : 0.f) : (mx == -INFINITY ? 0.f : mx);
         const float mnew = (float)(op_t)(mh + d);
         const float dsub = mnew - mh;
-        const float alpha = mset ? exp2_fast(-dsub) : 1.f;
+        const float alpha = ms ? exp2_fast(-dsub) : 1.f;
         lsum *= alpha;
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[r] *= alpha;
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[r] -= dsub;
         l = exp_pack(sc, pf);
-        mset = mset || mx != -INFINITY;
+        mset |= __builtin_amdgcn_fcmpf(mx, -INFINITY, 14 /* unordered or != */);
         mh = mnew;
         set_fb(mnew);
       }
