@@ -189,18 +189,22 @@ __global__ __launch_bounds__(64 * TRW, MODE == TR_HILO || MODE == TR_STATS ? 2 :
     }
   } else {
     if constexpr (MODE == TR_MEANFIX) {
-      // acc[ob] += corr on every pair, as one more MFMA: A = corr * 2^10 in column k = 0 (row m
-      // = channel 32 ob + m, as for W3), B = 2^-10 (exact).  Accumulators that started from
-      // corr instead would keep a second copy of all 64 across the loop.
+      // acc[ob] += corr on every pair, as one more MFMA: A = corr as a 16-bit hi + lo pair in
+      // columns k = 0, 1 (row m = channel 32 ob + m, as for W3), B = 1; below the 16-bit
+      // normal range the pair keeps corr to ~1e-8 absolute, far under the outputs' scale.
+      // Accumulators that started from corr instead would keep a second copy of all 64 across
+      // the loop.
       opx8 ones;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) ones[t] = (op_t)(1.f / 1024.f);
+      for (int t = 0; t < 8; ++t) ones[t] = (op_t)1.f;
 #pragma unroll
       for (int ob = 0; ob < 4; ++ob) {
         opx8 a;
 #pragma unroll
         for (int t = 0; t < 8; ++t) a[t] = (op_t)0.f;
-        a[0] = (op_t)(h == 0 ? cm[ob] * 1024.f : 0.f);
+        const op_t hi = (op_t)(h == 0 ? cm[ob] : 0.f);
+        a[0] = hi;
+        a[1] = (op_t)(h == 0 ? cm[ob] - (float)hi : 0.f);
         acc[ob] = mfma32(a, ones, acc[ob]);
       }
     }
