@@ -743,7 +743,7 @@ def fast_bench(N: int = 1024, seed: int = 4, steps: int = 5) -> dict:
     peak8 = ops.mfma_rate_probe(dev, fp8=True)
     res["mx8_contract"] = {"kernel": "tm8_contract_kernel", "launch_ms": round(c_in, 4), "tflops": round(tf_in, 1),
                            "peak_fp8_tflops": 5000.0, "frac_of_fp8_peak": round(tf_in / 5000.0, 4),
-                           "launch_ms_source": f"in-layer: mean of {c_n} launches inside the timed fp8 layers "
+                           "launch_ms_source": f"in-layer: mean of {c_n} launches inside the fp8 layers of the line (the timed steps and one warm-up step) "
                                                "(HIP events; fp16 output, as the trimul writes it)",
                            "measured_peak_fp8": {**peak8, "frac": round(tf_in / peak8["tflops"], 4),
                                                  "note": "sustained block-scaled fp8 MFMA rate under load "
