@@ -154,18 +154,27 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
       load_row_frag<CC>(z + pn * CC, h, x);
       if (MASK) maskn = mask[pn];
     }
-#pragma unroll
-    for (int cb = 0; cb < 2 * CC / 32; ++cb) {
-      __builtin_amdgcn_sched_barrier(0);
+    // software pipeline: the MFMAs of block cb + 1 are issued before block cb's epilogue
+    f32x16 apq[2], agq[2];
+    auto mm = [&](int cb, f32x16& ap, f32x16& ag) PF_INLINE {
       const op_t* wp = lp + (32 * cb + m) * LW + 8 * h;
       const op_t* wg = lg + (32 * cb + m) * LW + 8 * h;
-      const float cp = cbias[32 * cb + m], cg = cbias[2 * CC + 32 * cb + m];
-      f32x16 ap = zero16(), ag = zero16();
+      ap = zero16();
+      ag = zero16();
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         ap = mfma32(xf[s], ld_x8(wp + 16 * s), ap);   // rows = position, cols = output channel
         ag = mfma32(xf[s], ld_x8(wg + 16 * s), ag);
       }
+    };
+    mm(0, apq[0], agq[0]);
+#pragma unroll
+    for (int cb = 0; cb < 2 * CC / 32; ++cb) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (cb + 1 < 2 * CC / 32) mm(cb + 1, apq[(cb + 1) & 1], agq[(cb + 1) & 1]);
+      const float cp = cbias[32 * cb + m], cg = cbias[2 * CC + 32 * cb + m];
+      const f32x16& ap = apq[cb & 1];
+      const f32x16& ag = agq[cb & 1];
       // lane (channel m, half h) holds positions 8g + 4h + e: stage [channel][position]
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
