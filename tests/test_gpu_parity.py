@@ -421,11 +421,14 @@ def test_layer_batch2_matches_single(gpu):
     check("batch-2 layer s", s_b, s_ref)
 
 
-@pytest.mark.parametrize("P,M,Nc,K", [(3, 96, 320, 192), (2, 512, 256, 1024), (1, 288, 800, 64)])
+@pytest.mark.parametrize("P,M,Nc,K", [(3, 96, 320, 192), (2, 512, 256, 1024), (1, 288, 800, 64),
+                                     (70, 320, 512, 128)])
 def test_batched_nt_gemm(gpu, P, M, Nc, K):
     """Rectangular form of the contraction kernel (partial 256-tiles in both dimensions):
     fp32 output equals an fp32 product of the same rounded operands up to summation order;
-    the operand-type output is that result (times scale) rounded once."""
+    the operand-type output is that result (times scale) rounded once.  70 x 320 x 512 has
+    280 tiles: on 256 CUs the last 24 run as 128-row halves, one of each pair partly and one
+    wholly past M."""
     g = torch.Generator().manual_seed(M + Nc + K)
     A = torch.randn((P, M, K), generator=g).half()
     Bm = torch.randn((P, Nc, K), generator=g).half()

@@ -311,7 +311,9 @@ __global__ __launch_bounds__(256) void tm_contract_kernel(
 // lands at LDS base + 16*l), so no VGPRs are spent on staging, through a 2-deep ring of
 // [256][64] slabs per operand: every DMA request is a whole 128-byte row segment, and
 // slab kt+1 is in flight while slab kt is consumed.  Within a slab the fragment reads of
-// the next k-step are interleaved one per MFMA of the current one.
+// the next k-step are interleaved one per MFMA of the current one.  One workgroup fills a CU,
+// so when the tile count leaves a last round on half of the CUs or fewer (N = 768: 1152 tiles
+// on 256 CUs), those tiles are split in two 128-row halves and the round takes half as long.
 // ---------------------------------------------------------------------------------
 constexpr int BM2 = 256;
 constexpr int TMD_WAVES = 8;
@@ -327,27 +329,30 @@ constexpr int DK8 = 64;
 constexpr int DSLAB8 = BM2 * DK8;
 constexpr size_t TMD8_LDS_BYTES = (size_t)2 * 2 * DSLAB8 * sizeof(op_t);
 
-template <typename OutT>
-__global__ __launch_bounds__(64 * TMD_WAVES, 1) void tm_contract_dma_kernel(
-    const op_t* __restrict__ A, const op_t* __restrict__ Bop, OutT* __restrict__ X,
-    int M, int Nc, int K, int tn, int total, float out_scale, const float* __restrict__ amax_parts, int nparts) {
-  extern __shared__ __attribute__((aligned(16))) op_t smem[];
+// One output tile of 64 XN (i) x 256 (j): XN = 4 is the whole 256x256 tile; XN = 2 is half of
+// one (rows i0 .. i0 + 127), used for the tiles of a last, partial round of the chip (below).
+// A half tile's waves own 64 (i) x 64 (j) each and read 4 fragments per 4 MFMAs.
+template <int XN, typename OutT>
+PF_DEV void contract_tile(const op_t* __restrict__ A, const op_t* __restrict__ Bop, OutT* __restrict__ X, int M,
+                          int Nc, int K, long plane, int i0, int j0, float out_scale,
+                          const float* __restrict__ amax_parts, int nparts, op_t* smem) {
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wid >> 2, wn = wid & 3;
-  const int w = xcd_remap(blockIdx.x, total);
-  const int tiles = ((M + BM2 - 1) / BM2) * tn;
-  const long plane = w / tiles;
-  const int t = w - (int)plane * tiles;
-  const int i0 = (t / tn) * BM2, j0 = (t % tn) * BM2;
+  constexpr int QA = XN;   // A-slab DMA instructions per wave (64 XN rows over 8 waves)
 
-  // DMA: instruction q (0..3) of this wave covers slab rows (4*wid + q)*8 + (lane >> 3)
-  int offA[4], offB[4];
+  // DMA: instruction q of this wave covers slab rows (QA*wid + q)*8 (A; 4*wid + q for B) + (lane >> 3)
+  int offA[QA], offB[4];
+#pragma unroll
+  for (int q = 0; q < QA; ++q) {
+    const int r = (QA * wid + q) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ slab_swz8(r);
+    offA[q] = min(i0 + r, M - 1) * K + 8 * c;
+  }
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int r = (4 * wid + q) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ slab_swz8(r);
-    offA[q] = min(i0 + r, M - 1) * K + 8 * c;
     offB[q] = min(j0 + r, Nc - 1) * K + 8 * c;
   }
   const op_t* Ap = A + plane * M * K;
@@ -358,43 +363,45 @@ __global__ __launch_bounds__(64 * TMD_WAVES, 1) void tm_contract_dma_kernel(
     const int ko = kt * DK8;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      __builtin_amdgcn_global_load_lds(Ap + offA[q] + ko, sa + (4 * wid + q) * 512, 16, 0, 0);
+      if (q < QA) __builtin_amdgcn_global_load_lds(Ap + offA[q] + ko, sa + (QA * wid + q) * 512, 16, 0, 0);
       __builtin_amdgcn_global_load_lds(Bp + offB[q] + ko, sb + (4 * wid + q) * 512, 16, 0, 0);
     }
   };
   const int swz = slab_swz8(m);   // rows base + 32x + m: bits 0-3 of the row are those of m
-  const int rdA = (wm * 128 + m) * DK8, rdB = (wn * 64 + m) * DK8;
-  auto read_frags = [&](int kt, int s, opx8 (&fa)[4], opx8 (&fb)[2]) {
+  const int rdA = (wm * 32 * XN + m) * DK8, rdB = (wn * 64 + m) * DK8;
+  auto read_frags = [&](int kt, int s, opx8 (&fa)[XN], opx8 (&fb)[2]) {
     const op_t* sa = smem + (kt & 1) * 2 * DSLAB8;
     const op_t* sb = sa + DSLAB8;
     const int cs = 8 * ((2 * s + h) ^ swz);
 #pragma unroll
-    for (int x = 0; x < 4; ++x) fa[x] = ld_x8(sa + rdA + 32 * x * DK8 + cs);
+    for (int x = 0; x < XN; ++x) fa[x] = ld_x8(sa + rdA + 32 * x * DK8 + cs);
 #pragma unroll
     for (int y = 0; y < 2; ++y) fb[y] = ld_x8(sb + rdB + 32 * y * DK8 + cs);
   };
-  f32x16 acc[2][4];
+  f32x16 acc[2][XN];
 #pragma unroll
   for (int y = 0; y < 2; ++y)
 #pragma unroll
-    for (int x = 0; x < 4; ++x) acc[y][x] = zero16();
-  auto mma = [&](const opx8 (&fa)[4], const opx8 (&fb)[2]) {
+    for (int x = 0; x < XN; ++x) acc[y][x] = zero16();
+  auto mma = [&](const opx8 (&fa)[XN], const opx8 (&fb)[2]) {
 #pragma unroll
     for (int y = 0; y < 2; ++y)
 #pragma unroll
-      for (int x = 0; x < 4; ++x) acc[y][x] = mfma32(fb[y], fa[x], acc[y][x]);
+      for (int x = 0; x < XN; ++x) acc[y][x] = mfma32(fb[y], fa[x], acc[y][x]);
   };
-  // 6 fragment reads of the next k-step, one after each of the first 6 MFMAs
-#define PF_INTERLEAVE_6_READS()                                   \
-  _Pragma("unroll") for (int q_ = 0; q_ < 6; ++q_) {              \
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            \
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);            \
-  }                                                               \
-  __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  // the XN + 2 fragment reads of the next k-step, one after each of the first XN + 2 MFMAs
+  auto interleave = [&]() {
+#pragma unroll
+    for (int q = 0; q < XN + 2; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if constexpr (2 * XN > XN + 2) __builtin_amdgcn_sched_group_barrier(0x008, XN - 2, 0);
+  };
 
   const int nk = K / DK8;
   issue(0);
-  opx8 f0a[4], f0b[2], f1a[4], f1b[2];
+  opx8 f0a[XN], f0b[2], f1a[XN], f1b[2];
   for (int kt = 0; kt < nk; ++kt) {
     // slab kt landed (slab kt+1 not yet issued); the barrier also tells every wave that
     // slab kt-1's buffer is free, so slab kt+1 can go into it
@@ -408,21 +415,20 @@ __global__ __launch_bounds__(64 * TMD_WAVES, 1) void tm_contract_dma_kernel(
     __builtin_amdgcn_sched_barrier(0);
     read_frags(kt, 2, f0a, f0b);
     mma(f1a, f1b);
-    PF_INTERLEAVE_6_READS();
+    interleave();
     __builtin_amdgcn_sched_barrier(0);
     read_frags(kt, 3, f1a, f1b);
     mma(f0a, f0b);
-    PF_INTERLEAVE_6_READS();
+    interleave();
     __builtin_amdgcn_sched_barrier(0);
     mma(f1a, f1b);
     __builtin_amdgcn_sched_barrier(0);
   }
-#undef PF_INTERLEAVE_6_READS
   if (nparts > 0) out_scale = x_store_scale(planes_amax(amax_parts, nparts), K);
   OutT* Xp = X + plane * M * Nc;
 #pragma unroll
-  for (int x = 0; x < 4; ++x) {
-    const int ib = i0 + wm * 128 + 32 * x;
+  for (int x = 0; x < XN; ++x) {
+    const int ib = i0 + wm * 32 * XN + 32 * x;
 #pragma unroll
     for (int y = 0; y < 2; ++y) {
       const int jb = j0 + wn * 64 + 32 * y;
@@ -439,6 +445,34 @@ __global__ __launch_bounds__(64 * TMD_WAVES, 1) void tm_contract_dma_kernel(
         store_runs16((op_t*)(Xp + (long)(ib + m) * Nc + jb), acc[y][x], out_scale, h);   // 16-byte runs
       }
     }
+  }
+}
+
+// Workgroups 0 .. full-1 take whole tiles 0 .. full-1; the `ntiles - full` tiles after them
+// (a last round that would leave at least half of the CUs idle) go to two workgroups each, one
+// per 128-row half, so that round takes about half as long.  Both ranges are mapped XCD-aware
+// on their own, so the workgroups of one plane share an XCD's L2.
+template <typename OutT>
+__global__ __launch_bounds__(64 * TMD_WAVES, 1) void tm_contract_dma_kernel(
+    const op_t* __restrict__ A, const op_t* __restrict__ Bop, OutT* __restrict__ X,
+    int M, int Nc, int K, int tn, int ntiles, int full, float out_scale, const float* __restrict__ amax_parts,
+    int nparts) {
+  extern __shared__ __attribute__((aligned(16))) op_t smem[];
+  const int tiles = ((M + BM2 - 1) / BM2) * tn;   // per plane
+  const int bid = blockIdx.x;
+  if (bid < full) {
+    const int w = xcd_remap(bid, full);
+    const long plane = w / tiles;
+    const int t = w - (int)plane * tiles;
+    contract_tile<4, OutT>(A, Bop, X, M, Nc, K, plane, (t / tn) * BM2, (t % tn) * BM2, out_scale, amax_parts,
+                           nparts, smem);
+  } else {
+    const int hw = xcd_remap(bid - full, 2 * (ntiles - full));
+    const int w = full + (hw >> 1);
+    const long plane = w / tiles;
+    const int t = w - (int)plane * tiles;
+    contract_tile<2, OutT>(A, Bop, X, M, Nc, K, plane, (t / tn) * BM2 + (hw & 1) * (BM2 / 2), (t % tn) * BM2,
+                           out_scale, amax_parts, nparts, smem);
   }
 }
 
@@ -625,9 +659,13 @@ int launch_contract_rect(const op_t* A, const op_t* B, OutT* X, int planes, int 
     return rc;
   const int tn = (Nc + BM2 - 1) / BM2;
   const long total = (long)planes * ((M + BM2 - 1) / BM2) * tn;
-  if (total > 0x7fffffff) return pf_fail(PF_E_INVALID, "contraction: too many tiles (%ld)", total);
-  tm_contract_dma_kernel<OutT><<<(unsigned)total, 64 * TMD_WAVES, TMD8_LDS_BYTES, st>>>(
-      A, B, X, M, Nc, K, tn, (int)total, scale, amax_parts, nparts);
+  if (total > 0x3fffffff) return pf_fail(PF_E_INVALID, "contraction: too many tiles (%ld)", total);
+  // a last round of whole tiles on at most half of the CUs runs as half tiles
+  const int cus = device_cus();
+  const long rest = cus > 0 ? total % cus : 0;
+  const long full = 2 * rest <= cus && total > cus ? total - rest : total;
+  tm_contract_dma_kernel<OutT><<<(unsigned)(full + 2 * (total - full)), 64 * TMD_WAVES, TMD8_LDS_BYTES, st>>>(
+      A, B, X, M, Nc, K, tn, (int)total, (int)full, scale, amax_parts, nparts);
   PF_CHECK_LAUNCH("tm_contract_dma_kernel");
   return PF_OK;
 }
