@@ -91,6 +91,101 @@ def cpu_baseline(N: int, seed: int, reps: int = 3) -> dict:
                       f"{sec:.2f} s/layer; cpu={cpu}"}
 
 
+def cpu_configs(reps: int = 3) -> dict:
+    """The CPU oracle against this build's GPU path on the BASELINE configs, per op where the
+    config is per op: config 0 (one layer at N = 128, in full), configs 1 / 2 (each triangle
+    multiplication / attention at N = 512 with the 51-token padded tail), and a bounded sample of
+    config 4 (the block-fp8 emulator's triangle multiplication and pair transition at N = 512
+    against the fast-mode kernels at the same N; the emulator runs once, its N = 1024 case would
+    take minutes).  CPU: fp32 oracle, all host threads, median of `reps` after one warm-up (one
+    run for the emulator).  GPU: HIP events, device-resident inputs, same weights and inputs."""
+    import torch
+    from oracle import pairformer_ref as ref
+    from tt_boltz_amd import ops, pairformer, synthetic
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    dev = pairformer.get_device()
+    stream = torch.cuda.current_stream()
+
+    def cpu_s(fn, n):
+        with torch.no_grad():
+            if n > 1:
+                fn()
+            ts = []
+            for _ in range(n):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    def entry(c_s, g_ms):
+        return {"cpu_s": round(c_s, 4), "gpu_ms": round(g_ms, 4), "gpu_speedup": round(c_s * 1e3 / g_ms, 1)}
+
+    res = {"cores": cores, "torch": torch.__version__}
+    # config 0: one PairformerLayer at N = 128
+    cfg = synthetic.CONFIGS[0]
+    N = cfg["N"]
+    w = synthetic.stack_weights(1, cfg["seed"])
+    s, z, mask, pm = synthetic.pair_inputs(N, cfg["seed"])
+    lw = ref.sub(w, "layers.0")
+    c = cpu_s(lambda: ref.pairformer_layer(s, z, mask, pm, lw, ref.chunk_size_for(N)), reps)
+    pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, w)
+    ws = ops.workspace(pf.workspace_bytes(1, N), dev)
+    zd, sd = z.to(dev).contiguous(), s.to(dev).contiguous()
+    md, pmd = mask.to(dev).contiguous(), pm.to(dev).contiguous()
+    res["config0_layer_n128"] = entry(c, time_events(lambda: pf.blocks[0](sd, zd, pmd, md, ws), 20, stream))
+    del pf, ws
+    # configs 1 and 2: the four triangle ops at N = 512, padded tail
+    for k, ops_ in ((1, (("trimul_out", "tri_mul_out", "outgoing"), ("trimul_in", "tri_mul_in", "incoming"))),
+                    (2, (("triatt_start", "tri_att_start", True), ("triatt_end", "tri_att_end", False)))):
+        cfg = synthetic.CONFIGS[k]
+        N = cfg["N"]
+        w = synthetic.stack_weights(1, cfg["seed"])
+        _, z, _, pm = synthetic.pair_inputs(N, cfg["seed"], pad_tail=cfg["pad_tail"], with_s=False)
+        lw = ref.sub(w, "layers.0")
+        layer = pairformer.Pairformer(1, 32, 4, 24, 16, True, w).blocks[0]
+        ws = ops.workspace(layer.workspace_bytes(1, N), dev)
+        zd, pmd = z.to(dev).contiguous(), pm.to(dev).contiguous()
+        out = torch.empty_like(zd)
+        for name, prefix, arg in ops_:
+            if k == 1:
+                c = cpu_s(lambda: ref.triangle_multiplication(z, pm, ref.sub(lw, prefix), arg), reps)
+                mod = layer.triangle_multiplication_start if arg == "outgoing" else layer.triangle_multiplication_end
+            else:
+                c = cpu_s(lambda: ref.triangle_attention(z, pm, ref.sub(lw, prefix), arg,
+                                                         ref.chunk_size_for(N)), reps)
+                mod = layer.triangle_attention_start if arg else layer.triangle_attention_end
+            res[f"config{k}_{name}_n{N}"] = entry(c, time_events(lambda: mod(zd, pmd, out=out, ws=ws), 10, stream))
+        del layer, ws
+    # config 4 sample: the block-fp8 emulator at N = 512
+    cfg = synthetic.CONFIGS[4]
+    N = 512
+    w = synthetic.stack_weights(1, cfg["seed"])
+    _, z, _, pm = synthetic.pair_inputs(N, cfg["seed"], with_s=False)
+    lw = ref.sub(w, "layers.0")
+    pairformer.set_fast_mode(True)
+    try:
+        layer = pairformer.Pairformer(1, 32, 4, 24, 16, True, w).blocks[0]
+    finally:
+        pairformer.set_fast_mode(False)
+    ws = ops.workspace(layer.workspace_bytes(1, N), dev)
+    zd, pmd = z.to(dev).contiguous(), pm.to(dev).contiguous()
+    out = torch.empty_like(zd)
+    c = cpu_s(lambda: ref.triangle_multiplication_mx8(z, pm, ref.sub(lw, "tri_mul_out"), "outgoing"), 1)
+    res["config4_sample_trimul_out_mx8_n512"] = entry(
+        c, time_events(lambda: layer.triangle_multiplication_start(zd, pmd, out=out, ws=ws), 10, stream))
+    c = cpu_s(lambda: ref.transition_mx8(z, ref.sub(lw, "transition_z")), 1)
+    tr_ws = ws[:layer.transition_workspace_bytes(1, N)] if layer.transition_workspace_bytes(1, N) else None
+    res["config4_sample_transition_mx8_n512"] = entry(
+        c, time_events(lambda: layer.transition_z(zd, out=out, ws=tr_ws), 10, stream))
+    del layer, ws
+    res["note"] = ("CPU: fp32 oracle (oracle/pairformer_ref.py; config 4: the block-fp8 emulator, "
+                   "oracle/fp8_emu.py, one run), median of the runs after one warm-up; GPU: this build "
+                   "on device-resident inputs; config 3 is stack.cpu_extrapolated")
+    return res
+
+
 def probe_traffic(N: int) -> int:
     """The roofline kernels alone on their real operands -- the triangle-attention core and
     the trimul contraction, 5 launches each -- and a plain copy kernel of COPY_BYTES read +
@@ -512,6 +607,22 @@ def stack_bench(N: int = 768, n_layers: int = 64, recycling_steps: int = 3, seed
     finite = bool(torch.isfinite(z_out).all() and torch.isfinite(s_out).all())
     passes = recycling_steps + 1
     fl = flops_layer(N)
+    # one more pass with HIP events around every launch of the attention core and of the 16-bit
+    # contraction (on the pair stream, as in the timed passes): their in-stack launch times
+    ops.kernel_timing(ops.TIMED_ATTEND, True)
+    ops.kernel_timing(ops.TIMED_CONTRACT, True)
+    rec(s0, z0, mask, 0)
+    att_ms, att_n = ops.kernel_timing_read(ops.TIMED_ATTEND)
+    con_ms, con_n = ops.kernel_timing_read(ops.TIMED_CONTRACT)
+    ops.kernel_timing(ops.TIMED_ATTEND, False)
+    ops.kernel_timing(ops.TIMED_CONTRACT, False)
+    torch.cuda.synchronize()
+
+    def in_stack(total_ms, n, flop):
+        ms = total_ms / max(n, 1)
+        tf = flop / (ms * 1e-3) / 1e12
+        return {"launch_ms": round(ms, 4), "launches": n, "tflops": round(tf, 1),
+                "frac_of_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
     # the contraction alone at this N (128 planes, one direction per launch)
     A = torch.randn((128, N, N), device=dev).half()
     Bm = torch.randn((128, N, N), device=dev).half()
@@ -525,7 +636,12 @@ def stack_bench(N: int = 768, n_layers: int = 64, recycling_steps: int = 3, seed
             "layer_tflops_achieved": round(fl["layer"] * n_layers * passes / trunk_s / 1e12, 1),
             "finite": finite,
             "contract": {"kernel": "tm_contract_dma_kernel", "launch_ms": round(c_ms, 4),
-                         "tflops": round(c_tf, 1), "frac_of_peak": round(c_tf / MFMA_BF16_PEAK_TFLOPS, 4)},
+                         "tflops": round(c_tf, 1), "frac_of_peak": round(c_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                         "note": "alone: 20 back-to-back launches on random [128, N, N] fp16 planes"},
+            "contract_in_stack": {"kernel": "tm_contract_dma_kernel", **in_stack(con_ms, con_n, fl["trimul_contract"]),
+                                  "note": "HIP events around each launch during one extra 64-layer pass"},
+            "attention_in_stack": {"kernel": "ta_attn_kernel", **in_stack(att_ms, att_n, fl["triatt_core"]),
+                                   "note": "HIP events around each launch during one extra 64-layer pass"},
             "workload": "64-layer Boltz-2 Pairformer trunk, N=768, seed 3 weights, z~0.5 N(0,1), s~N(0,1), "
                         "masks all ones, 4 recycling passes, fp32 residual stream"}
 
@@ -1075,6 +1191,7 @@ def main() -> int:
                 "trunk_s": round(layer_s * out["stack"]["layers"] * out["stack"]["passes"], 1),
                 "layer_s": round(layer_s, 2), "cores": c3["cores"], "kind": "port",
                 "note": "extrapolated: 1 PairformerLayer at N=768 on the fp32 CPU oracle, x64 layers x4 passes"}
+            out["cpu_configs"] = cpu_configs()
     print(json.dumps(out), flush=True)
     return 0
 

@@ -506,11 +506,13 @@ int pf_add_fwd(const float* a, const float* b, float* out, long n, void* stream)
 int pf_attend_timing(int enable);
 int pf_attend_timing_read(double* total_ms, int* launches);
 
-/* The same for a chosen kernel kind: PF_TIMED_ATTEND (as above) or PF_TIMED_CONTRACT8 (the
- * block-fp8 contraction inside pf_trimul_mx8_fwd and pf_trimul_mx8_contract). */
+/* The same for a chosen kernel kind: PF_TIMED_ATTEND (as above), PF_TIMED_CONTRACT8 (the
+ * block-fp8 contraction inside pf_trimul_mx8_fwd and pf_trimul_mx8_contract) or
+ * PF_TIMED_CONTRACT (the 16-bit contraction inside pf_trimul_fwd). */
 #define PF_TIMED_ATTEND 0
 #define PF_TIMED_CONTRACT8 1
-#define PF_TIMED_KINDS 2
+#define PF_TIMED_CONTRACT 2
+#define PF_TIMED_KINDS 3
 int pf_kernel_timing(int kind, int enable);
 int pf_kernel_timing_read(int kind, double* total_ms, int* launches);
 

@@ -159,7 +159,7 @@ def test_workspace_sizes():
 
 def test_measurement_aids_reject_bad_arguments_without_launching():
     lib = _lib.load()
-    assert lib.pf_kernel_timing(2, 1) == -1 and "unknown kind 2" in _err()
+    assert lib.pf_kernel_timing(3, 1) == -1 and "unknown kind 3" in _err()
     assert lib.pf_kernel_timing(-1, 0) == -1 and "unknown kind" in _err()
     ms, n = ctypes.c_double(0.0), ctypes.c_int(0)
     assert lib.pf_kernel_timing_read(7, ctypes.byref(ms), ctypes.byref(n)) == -1 and "unknown kind 7" in _err()

@@ -34,6 +34,29 @@ def test_contract8_timing_counts_each_launch(gpu):
     ops.kernel_timing(ops.TIMED_ATTEND, False)
 
 
+def test_contract_timing_inside_trimul(gpu):
+    """PF_TIMED_CONTRACT brackets the 16-bit contraction of each pf_trimul_fwd call (and only
+    that: the standalone pf_trimul_contract is not recorded)."""
+    from tt_boltz_amd import pairformer, synthetic
+    N = 128
+    pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, synthetic.stack_weights(1, 0))
+    tm = pf.blocks[0].triangle_multiplication_start
+    _, z_cpu, _, _ = synthetic.pair_inputs(N, 0, with_s=False)
+    z = z_cpu.to(gpu).contiguous()
+    out = torch.empty_like(z)
+    ws = ops.workspace(tm.workspace_bytes(1, N), gpu)
+    A = torch.randn((128, N, N), device=gpu).half()
+    X = torch.empty_like(A)
+    ops.kernel_timing(ops.TIMED_CONTRACT, True)
+    for _ in range(2):
+        tm(z, None, out=out, ws=ws)
+    ops.launch_trimul_contract(A, A, X)
+    ms, n = ops.kernel_timing_read(ops.TIMED_CONTRACT)
+    ops.kernel_timing(ops.TIMED_CONTRACT, False)
+    print(f"[measure] contract timing inside trimul: {n} launches, {ms:.3f} ms", flush=True)
+    assert n == 2 and ms > 0
+
+
 @pytest.mark.parametrize("fp8", [False, True])
 def test_mfma_rate_probe(gpu, fp8):
     r = ops.mfma_rate_probe(gpu, iters=256, per_cu=1, reps=1, fp8=fp8)

@@ -187,9 +187,12 @@ def test_triatt_config2(gpu, ending):
     check(f"config2 triatt ending={ending} full", out, want)
 
 
-def test_tri_attention_core(gpu):
+@pytest.mark.parametrize("N", [96, 100])
+def test_tri_attention_core(gpu, N):
+    """N = 100 runs padded to 128 with n_valid = 100: the fully masked row's mean of v then
+    leaves out the padded keys, and the padded rows take the same path."""
     g = torch.Generator().manual_seed(3)
-    B, N, H, D = 1, 96, 4, 32
+    B, H, D = 1, 4, 32
     q, k, v = (torch.randn((B, N, H, N, D), generator=g) for _ in range(3))
     bias = torch.randn((B, 1, H, N, N), generator=g)
     mask = (torch.rand((B, N, 1, 1, N), generator=g) > 0.2).float()

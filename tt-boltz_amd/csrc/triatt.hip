@@ -578,35 +578,55 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   }
 
   // A dead row (every valid key masked): the reference's logits all round to -1e9, so each
-  // query's output is the plain mean of v over the n_valid keys.  The wave sums its row's V^T
-  // (keys stored at perm16 positions) for d = m, the two lane halves taking alternate keys.
-  if (!live && qvalid) {
-    const float inv_n = 1.f / (float)n_valid;
-    for (int hd2 = 0; hd2 < H; ++hd2) {
-      const op_t* vrow = Vt + ((((long)b * N + ip) * H + hd2) * D + m) * (long)N;
-      float acc = 0.f;
-      for (int p0 = 8 * h; p0 < N; p0 += 16) {   // 8 stored keys per 16-byte load
-        const opx8 v8 = ld_x8(vrow + p0);
+  // query's output is the plain mean of v over the n_valid keys, the same for every query of
+  // the row.  The row's four query-block waves split its four heads: wave qb sums head qb's
+  // V^T (keys stored at perm16 positions) for d = m, the two lane halves taking alternate
+  // 16-byte chunks (8 loads in flight, v_dot2 pair sums, keys past n_valid zeroed by
+  // selects), and the means meet in LDS.  Every wave takes part in both barriers.
+  static_assert(H == TA_WAVES / 4, "one head per query-block wave of a row");
+  __syncthreads();   // the last step's stage reads are done before the LDS is reused
+  float* smean = reinterpret_cast<float*>(alds);   // [4 rows][H][D]
+  if (!live) {
+    const int hd2 = qb;
+    const bool all_valid = n_valid >= N;   // wave-uniform
+    const op_t* vrow = Vt + ((((long)b * N + ip) * H + hd2) * D + m) * (long)N;
+    float acc = 0.f;
+    for (int p0 = 8 * h; p0 < N; p0 += 16 * 8) {   // 8 stored keys per 16-byte load
+      opx8 v8[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (perm16(p0 + e) < n_valid) acc += (float)v8[e];
-      }
-      const float mean = xor32_sum(acc) * inv_n;   // lanes m and m + 32 both hold d = m
-      const int j = jq0 + m;
+      for (int u = 0; u < 8; ++u) v8[u] = p0 + 16 * u < N ? ld_x8(vrow + p0 + 16 * u) : zero_x8();
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          opx2 pr = {v8[u][e], v8[u][e + 1]};
+          if (!all_valid) {
+            pr[0] = perm16(p0 + 16 * u + e) < n_valid ? pr[0] : (op_t)0.f;
+            pr[1] = perm16(p0 + 16 * u + e + 1) < n_valid ? pr[1] : (op_t)0.f;
+          }
+          acc = dot2_ones(pr, acc);
+        }
+    }
+    const float mean = xor32_sum(acc) / (float)n_valid;   // lanes m and m + 32 both hold d = m
+    if (h == 0) smean[(row * H + hd2) * D + m] = mean;
+  }
+  __syncthreads();
+  if (!live && qvalid) {
+    const int j = jq0 + m;
+#pragma unroll
+    for (int hd2 = 0; hd2 < H; ++hd2) {
+      const float* mrow = smean + (row * H + hd2) * D;
       if (OUT_F32) {
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          f32x4 v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = __shfl(mean, 16 * h + 4 * q4 + e);
-          *reinterpret_cast<f32x4*>(O32 + ((((long)b * N + ip) * H + hd2) * N + j) * D + 16 * h + 4 * q4) = v;
-        }
+        for (int q4 = 0; q4 < 4; ++q4)
+          *reinterpret_cast<f32x4*>(O32 + ((((long)b * N + ip) * H + hd2) * N + j) * D + 16 * h + 4 * q4) =
+              *reinterpret_cast<const f32x4*>(mrow + 16 * h + 4 * q4);
       } else {
 #pragma unroll
         for (int q8 = 0; q8 < 2; ++q8) {
           opx8 v;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = (op_t)__shfl(mean, 16 * h + 8 * q8 + e);
+          for (int e = 0; e < 8; ++e) v[e] = (op_t)mrow[16 * h + 8 * q8 + e];
           st_x8(O16 + (((long)b * N + ip) * N + j) * C + 32 * hd2 + 16 * h + 8 * q8, v);
         }
       }

@@ -717,7 +717,9 @@ int trimul_run(const pf_trimul_args* a) {
         amax_parts, B, N, a->direction, a->eps, offb, (const op_t*)a->p_in_lo, (const op_t*)a->g_in_lo, stats);
     PF_CHECK_LAUNCH("tm_proj_kernel");
   }
+  pf_kernel_mark(PF_TIMED_CONTRACT, st, 0);
   const int rc = launch_contract<op_t>(opA, opB, X, B * CC, N, X_STORE_SCALE, st, amax_parts, grid_proj);
+  pf_kernel_mark(PF_TIMED_CONTRACT, st, 1);
   if (rc != PF_OK) return rc;
   {
     const int resid = !a->accumulate ? 0 : (a->out == a->z_in ? 1 : 2);

@@ -225,11 +225,11 @@ def attend_timing_read(variant: str = DEFAULT_VARIANT):
     return ms.value, n.value
 
 
-TIMED_ATTEND, TIMED_CONTRACT8 = 0, 1   # pf_kernel_timing kinds (PF_TIMED_*)
+TIMED_ATTEND, TIMED_CONTRACT8, TIMED_CONTRACT = 0, 1, 2   # pf_kernel_timing kinds (PF_TIMED_*)
 
 
 def kernel_timing(kind: int, enable: bool, variant: str = DEFAULT_VARIANT) -> None:
-    """``attend_timing`` for a chosen kernel kind (TIMED_ATTEND, TIMED_CONTRACT8)."""
+    """``attend_timing`` for a chosen kernel kind (TIMED_ATTEND, TIMED_CONTRACT8, TIMED_CONTRACT)."""
     _lib.check(_lib.load(variant).pf_kernel_timing(kind, 1 if enable else 0), "pf_kernel_timing", variant)
 
 
