@@ -1122,6 +1122,31 @@ def main() -> int:
     plain_ms = pe0.elapsed_time(pe1) / args.steps
     del pf_plain, single_plain, zp, sp
 
+    # the same layer on padded inputs as a caller passes them: the last 51 of the N tokens are
+    # padding (token and pair masks, n_valid), the schedule as in the timed loop
+    pad_tail = 51
+    _, z_pad, mask_pad, pm_pad = synthetic.pair_inputs(N, seed, pad_tail=pad_tail, with_s=False)
+    zq, sq = z_pad.to(dev).contiguous(), s_cpu.to(dev).contiguous()
+    mq, pmq = mask_pad.to(dev).contiguous(), pm_pad.to(dev).contiguous()
+    single_pad = pf.single_track(1, N, dev)
+
+    def step_pad():
+        layer(sq, zq, pmq, mq, ws, N - pad_tail, single_pad)
+
+    for _ in range(args.warmup):
+        step_pad()
+    single_pad.join()
+    torch.cuda.synchronize()
+    qe0, qe1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    qe0.record(stream)
+    for _ in range(args.steps):
+        step_pad()
+    single_pad.join()
+    qe1.record(stream)
+    torch.cuda.synchronize()
+    pad_ms = qe0.elapsed_time(qe1) / args.steps
+    del single_pad, zq, sq, mq, pmq
+
     out = {
         "metric": "Pairformer layers/sec at N=512, fp16 MFMA operands (bf16-operand rate in operand_variants)",
         "value": round(1000.0 / ms_step, 3),
@@ -1141,6 +1166,10 @@ def main() -> int:
                                      "mantissa bits), the default because bf16 operands miss the 2e-3 "
                                      "mean-error bar; bf16_layers_per_s is the bf16-operand build"},
         "single_stream_layers_per_s": round(1000.0 / serial_ms, 3),
+        "padded_input": {"layers_per_s": round(1000.0 / pad_ms, 3), "ms_per_step": round(pad_ms, 4),
+                         "n_valid": N - pad_tail,
+                         "note": f"the same layer with the last {pad_tail} of {N} tokens padded (token and pair "
+                                 "masks given, n_valid set), as a caller's padded batch arrives"},
         "precision_paths": {"plain16_layers_per_s": round(1000.0 / plain_ms, 3),
                             "cost_pct": round(100.0 * (ms_step / plain_ms - 1.0), 2),
                             "note": "value runs the weight-precision paths (hi + lo weights in the trimul "
