@@ -301,12 +301,17 @@ __global__ __launch_bounds__(256, 2) void tm8_proj_kernel(
 // Contraction X[p][i][j] = sum_k A[p][i][k] * B[p][j][k] on MXFP8 planes.
 // 256x256 output tile per workgroup of 8 waves (two per SIMD), each 128 (i) x 64 (j), as
 // the 16-bit kernel; slabs of 128 k (128 bytes per row) move global -> LDS by DMA through a
-// 2-deep ring with the same XOR row swizzle; the scale dwords (4 blocks of the slab) are
-// prefetched into registers one slab ahead.
+// 2-deep ring with the same XOR row swizzle.  The slab's scale dwords (the 4 blocks of each
+// row) travel with it by DMA (one 4-byte-per-lane instruction per wave: waves 0-3 the A rows,
+// 4-7 the B rows), into [row][4 bytes] after the two operand slabs of the stage; loaded into
+// registers with ordinary global loads instead, they held every slab's wait back (+30 % at
+// N = 1024).
 // ---------------------------------------------------------------------------------
 constexpr int BT = 256, SK = 128, TM8C_WAVES = 8;
 constexpr int SLAB8 = BT * SK;                        // bytes per operand slab
-constexpr size_t TM8C_LDS = (size_t)2 * 2 * SLAB8;
+constexpr int SCL8 = 2 * BT * 4;                      // the slab's scale dwords, A rows then B rows
+constexpr int STAGE8 = 2 * SLAB8 + SCL8;              // bytes per ring stage
+constexpr size_t TM8C_LDS = (size_t)2 * STAGE8;
 PF_DEV int slab_swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 
 template <typename OutT>
@@ -336,15 +341,13 @@ __global__ __launch_bounds__(64 * TM8C_WAVES, 1) void tm8_contract_kernel(
   }
   const uint8_t* Ap = A + plane * NN;
   const uint8_t* Bp = Bop + plane * NN;
-  // scale rows of this lane's fragments: A rows i0 + wm*128 + 32x + m, B rows j0 + wn*64 + 32y + m
-  // (32-bit offsets from SA / SB: fewer registers than pointers)
-  int sArow[4], sBrow[2];
-#pragma unroll
-  for (int x = 0; x < 4; ++x) sArow[x] = (int)((plane * N + min(i0 + wm * 128 + 32 * x + m, N - 1)) * NB);
-#pragma unroll
-  for (int y = 0; y < 2; ++y) sBrow[y] = (int)((plane * N + min(j0 + wn * 64 + 32 * y + m, N - 1)) * NB);
+  // scale DMA: wave w < 4 moves A rows 64 w + lane, wave w >= 4 B rows 64 (w - 4) + lane (a
+  // 32-bit offset from SA / SB: fewer registers than a pointer)
+  const uint8_t* Sp = wid < 4 ? SA : SB;
+  const int srow = (wid & 3) * 64 + lane;
+  const int sOff = (int)((plane * N + min((wid < 4 ? i0 : j0) + srow, N - 1)) * NB);
   auto issue = [&](int kt) {
-    uint8_t* sa = smem8 + (kt & 1) * 2 * SLAB8;
+    uint8_t* sa = smem8 + (kt & 1) * STAGE8;
     uint8_t* sb = sa + SLAB8;
     const int ko = kt * SK;
 #pragma unroll
@@ -352,18 +355,21 @@ __global__ __launch_bounds__(64 * TM8C_WAVES, 1) void tm8_contract_kernel(
       __builtin_amdgcn_global_load_lds(Ap + offA[q] + ko, sa + (4 * wid + q) * 1024, 16, 0, 0);
       __builtin_amdgcn_global_load_lds(Bp + offB[q] + ko, sb + (4 * wid + q) * 1024, 16, 0, 0);
     }
+    __builtin_amdgcn_global_load_lds(Sp + sOff + 4 * kt, sa + 2 * SLAB8 + 256 * wid, 4, 0, 0);
   };
-  int scA[4], scB[2], nscA[4], nscB[2];
-  auto load_scales = [&](int kt, int (&a)[4], int (&b)[2]) {
+  // this lane's scale dwords of a stage: A rows wm*128 + 32x + m, B rows wn*64 + 32y + m
+  int scA[4], scB[2];
+  auto read_scales = [&](int kt) {
+    const uint8_t* ss = smem8 + (kt & 1) * STAGE8 + 2 * SLAB8;
 #pragma unroll
-    for (int x = 0; x < 4; ++x) a[x] = *reinterpret_cast<const int*>(SA + sArow[x] + 4 * kt);
+    for (int x = 0; x < 4; ++x) scA[x] = *reinterpret_cast<const int*>(ss + 4 * (wm * 128 + 32 * x + m));
 #pragma unroll
-    for (int y = 0; y < 2; ++y) b[y] = *reinterpret_cast<const int*>(SB + sBrow[y] + 4 * kt);
+    for (int y = 0; y < 2; ++y) scB[y] = *reinterpret_cast<const int*>(ss + 4 * BT + 4 * (wn * 64 + 32 * y + m));
   };
   const int swz = slab_swz8(m);
   const int rdA = (wm * 128 + m) * SK, rdB = (wn * 64 + m) * SK;
   auto read_frags = [&](int kt, int s, i32x8 (&fa)[4], i32x8 (&fb)[2]) {
-    const uint8_t* sa = smem8 + (kt & 1) * 2 * SLAB8;
+    const uint8_t* sa = smem8 + (kt & 1) * STAGE8;
     const uint8_t* sb = sa + SLAB8;
     const int c0 = 16 * ((4 * s + h) ^ swz), c1 = 16 * ((4 * s + 2 + h) ^ swz);
 #pragma unroll
@@ -383,20 +389,13 @@ __global__ __launch_bounds__(64 * TM8C_WAVES, 1) void tm8_contract_kernel(
 
   const int nk = N / SK;
   issue(0);
-  load_scales(0, nscA, nscB);
   for (int kt = 0; kt < nk; ++kt) {
     // slab kt and its scales landed; the barrier also frees slab kt-1's buffer
     __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
     __builtin_amdgcn_s_barrier();
-#pragma unroll
-    for (int x = 0; x < 4; ++x) scA[x] = nscA[x];
-#pragma unroll
-    for (int y = 0; y < 2; ++y) scB[y] = nscB[y];
-    if (kt + 1 < nk) {
-      issue(kt + 1);
-      load_scales(kt + 1, nscA, nscB);
-    }
+    if (kt + 1 < nk) issue(kt + 1);
     __builtin_amdgcn_sched_barrier(0);
+    read_scales(kt);
     // k-step 0's fragments, then step 1's reads interleaved with step 0's MFMAs (two reads
     // after each of the first six), then step 1's MFMAs
     i32x8 f0a[4], f0b[2], f1a[4], f1b[2];
