@@ -758,6 +758,26 @@ def test_layer_n768(gpu):
     check("layer N=768 s", s_got, s_ref)
 
 
+def test_layer_n2048_padded(gpu):
+    """The largest size tested: one full PairformerLayer at N = 2048 (z 2 GB fp32, the
+    triangle attention's q/k/v/o 4 GB), the last 37 tokens masked, against the fp32 oracle
+    evaluated on the device (attention in row chunks): byte offsets past 2^31 in the
+    attention's workspace, and the fully masked rows' path at this size."""
+    N, pad = 2048, 37
+    w = synthetic.stack_weights(1, 66)
+    s, z, mask, pm = synthetic.pair_inputs(N, 67, z_scale=0.5, pad_tail=pad)
+    wd = {k: v.to(gpu) for k, v in ref.sub(w, "layers.0").items()}
+    with torch.no_grad():
+        s_ref, z_ref = ref.pairformer_layer(s.to(gpu), z.to(gpu), mask.to(gpu), pm.to(gpu), wd, 64)
+    torch.cuda.empty_cache()
+    pf = pairformer.Pairformer(1, 32, 4, 24, 16, True, w)
+    s_got, z_got = pf(s.to(gpu).contiguous(), z.to(gpu).contiguous(), pm.to(gpu).contiguous(), mask.to(gpu))
+    nv = N - pad
+    check("layer N=2048 z (valid)", z_got[:, :nv, :nv], z_ref[:, :nv, :nv])
+    check("layer N=2048 z", z_got, z_ref)
+    check("layer N=2048 s", s_got, s_ref)
+
+
 def test_layer_config1_bf16_operands(gpu):
     """The bf16-operand library (the metric's dtype) on one full PairformerLayer at the
     config 1/2 shape: N = 512 with the last 51 tokens masked, against the fp32 oracle evaluated
