@@ -375,6 +375,9 @@ __global__ __launch_bounds__(64 * T64_WAVES, 1) void tr64_kernel(
 }
 
 // One wave per row.
+// One wave per row.  Rows of up to 64 * LN_REG values are read once into registers (all of a
+// lane's loads in flight together); longer rows are read three times.
+constexpr int LN_REG = 8;
 __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                       const float* __restrict__ b, float* __restrict__ out,
                                                       long rows, int C_, float eps) {
@@ -382,13 +385,36 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ 
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
   const float* xr = x + row * C_;
+  float* orow = out + row * C_;
+  if (C_ <= 64 * LN_REG) {
+    float xv[LN_REG];
+#pragma unroll
+    for (int u = 0; u < LN_REG; ++u) xv[u] = lane + 64 * u < C_ ? xr[lane + 64 * u] : 0.f;
+    float s = 0.f;
+#pragma unroll
+    for (int u = 0; u < LN_REG; ++u) s += xv[u];
+    const float mean = wave_sum(s) / C_;
+    float v = 0.f;
+#pragma unroll
+    for (int u = 0; u < LN_REG; ++u) {
+      const float d = lane + 64 * u < C_ ? xv[u] - mean : 0.f;
+      v += d * d;
+    }
+    const float rstd = rsqrtf(wave_sum(v) / C_ + eps);
+#pragma unroll
+    for (int u = 0; u < LN_REG; ++u) {
+      const int c = lane + 64 * u;
+      if (c < C_) orow[c] = (xv[u] - mean) * rstd * w[c] + b[c];
+    }
+    return;
+  }
   float s = 0.f;
   for (int c = lane; c < C_; c += 64) s += xr[c];
   const float mean = wave_sum(s) / C_;
   float v = 0.f;
   for (int c = lane; c < C_; c += 64) { const float d = xr[c] - mean; v += d * d; }
   const float rstd = rsqrtf(wave_sum(v) / C_ + eps);
-  for (int c = lane; c < C_; c += 64) out[row * C_ + c] = (xr[c] - mean) * rstd * w[c] + b[c];
+  for (int c = lane; c < C_; c += 64) orow[c] = (xr[c] - mean) * rstd * w[c] + b[c];
 }
 
 // A workgroup = one 32-row x 32-column output tile of one job; its 4 waves split the K
