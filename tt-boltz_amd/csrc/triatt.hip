@@ -335,13 +335,24 @@ template <bool OUT_F32>
 __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
     const op_t* __restrict__ Q, const op_t* __restrict__ K, const op_t* __restrict__ Vt,
     const float* __restrict__ bias32, const op_t* __restrict__ mask16, op_t* __restrict__ O16,
-    float* __restrict__ O32, int N, int n_valid, int total) {
+    float* __restrict__ O32, int N, int n_valid, int total, int full) {
   extern __shared__ __attribute__((aligned(16))) char alds[];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int row = wid & 3, qb = wid >> 2;   // frame row, 32-query block
-  const int nQP = (N + 127) >> 7, nKB = N >> 6, T = H * nKB;
-  const int w = xcd_remap(blockIdx.x, total);
+  // Workgroups 0 .. full-1 take all heads of their (rows, queries) block; the blocks after them
+  // (a last round that would leave at least half of the CUs idle) go to two workgroups each,
+  // heads 0-1 and heads 2-3, so that round takes about half as long.
+  int w, h0 = 0, nh = H;
+  if ((int)blockIdx.x < full) {
+    w = xcd_remap(blockIdx.x, full);
+  } else {
+    const int hw = xcd_remap(blockIdx.x - full, 2 * (total - full));
+    w = full + (hw >> 1);
+    h0 = (hw & 1) * (H / 2);
+    nh = H / 2;
+  }
+  const int nQP = (N + 127) >> 7, nKB = N >> 6, T = nh * nKB;
   const int per_b = (N >> 2) * nQP;
   const int b = w / per_b;
   const int rem = w - b * per_b;
@@ -408,7 +419,7 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(aV[i]));
   asm volatile("" : "+v"(aK[0]), "+v"(aK[1]), "+v"(aM));
 
-  issue(0, 0, 0);   // the first stage's DMA overlaps the scan below
+  issue(0, h0, 0);   // the first stage's DMA overlaps the scan below
   // rows whose valid keys are all masked (wave-uniform)
   bool live_l = false;
   {
@@ -546,8 +557,8 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   // the DMA of the next step into the other stage; during a head's last step the next head's
   // Q is loaded (it lands by the next loop-top wait).  The barrier also tells every wave that
   // the other stage (read in the previous step) is free.
-  int kbi = 0, hd = 0;  // step it = hd * nKB + kbi
-  if (qvalid && live) q_fetch(0);
+  int kbi = 0, hd = h0;  // step it = (hd - h0) * nKB + kbi
+  if (qvalid && live) q_fetch(h0);
   auto one_step = [&](auto stg, int it) PF_INLINE {
     constexpr int STG = decltype(stg)::value;
     __builtin_amdgcn_s_waitcnt(vmcnt_le(0));   // this wave's part of stage STG (and Q) landed ...
@@ -563,7 +574,7 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
         qf[0] = qn[0];
         qf[1] = qn[1];
       }
-      if (kbi == nKB - 1 && hd + 1 < H) q_fetch(hd + 1);   // lands by the next step's wait
+      if (kbi == nKB - 1 && hd + 1 < h0 + nh) q_fetch(hd + 1);   // lands by the next step's wait
       step2(stg);
       if (kbi == nKB - 1) finalize(hd);
     }
@@ -586,8 +597,8 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   static_assert(H == TA_WAVES / 4, "one head per query-block wave of a row");
   __syncthreads();   // the last step's stage reads are done before the LDS is reused
   float* smean = reinterpret_cast<float*>(alds);   // [4 rows][H][D]
-  if (!live) {
-    const int hd2 = qb;
+  if (!live && qb < nh) {
+    const int hd2 = h0 + qb;
     const bool all_valid = n_valid >= N;   // wave-uniform
     const op_t* vrow = Vt + ((((long)b * N + ip) * H + hd2) * D + m) * (long)N;
     float acc = 0.f;
@@ -613,8 +624,7 @@ __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
   __syncthreads();
   if (!live && qvalid) {
     const int j = jq0 + m;
-#pragma unroll
-    for (int hd2 = 0; hd2 < H; ++hd2) {
+    for (int hd2 = h0; hd2 < h0 + nh; ++hd2) {
       const float* mrow = smean + (row * H + hd2) * D;
       if (OUT_F32) {
 #pragma unroll
@@ -855,9 +865,13 @@ template <bool OUT_F32>
 int launch_attn(const TaBuffers& t, float* o32, int B, int N, int n_valid, hipStream_t st) {
   if (const int rc = pf_reserve_lds((const void*)ta_attn_kernel<OUT_F32>, TA_LDS, "ta_attn_kernel")) return rc;
   const int total = B * (N / 4) * ((N + 127) / 128);
+  // a last round of whole blocks on at most half of the CUs runs as head halves
+  const int cus = device_cus();
+  const int rest = cus > 0 ? total % cus : 0;
+  const int full = 2 * rest <= cus && total > cus ? total - rest : total;
   pf_attend_mark(st, 0);
-  ta_attn_kernel<OUT_F32><<<total, 64 * TA_WAVES, TA_LDS, st>>>(t.Q, t.K, t.Vt, t.bias32, t.mask16, t.O, o32, N,
-                                                               n_valid, total);
+  ta_attn_kernel<OUT_F32><<<full + 2 * (total - full), 64 * TA_WAVES, TA_LDS, st>>>(
+      t.Q, t.K, t.Vt, t.bias32, t.mask16, t.O, o32, N, n_valid, total, full);
   PF_CHECK_LAUNCH("ta_attn_kernel");
   pf_attend_mark(st, 1);
   return PF_OK;
