@@ -808,19 +808,43 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
 }
 
 // Layout conversion for the standalone attention core (fp32 API tensors -> kernel layout).
-__global__ void ta_prep_qkv_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                   const float* __restrict__ v, float qs, op_t* __restrict__ Q,
-                                   op_t* __restrict__ K, op_t* __restrict__ Vt, long rows, int N) {
-  // rows = B*N*H sequences of N x D; element e of sequence r: (j, d) = (e / D, e % D)
-  const long total = rows * N * D;
-  for (long e = (long)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (long)gridDim.x * blockDim.x) {
-    const long r = e / ((long)N * D);
-    const int jd = (int)(e - r * N * D);
-    const int j = jd / D, d = jd - j * D;
-    Q[e] = (op_t)(q[e] * qs);
-    K[e] = (op_t)k[e];
-    Vt[r * N * D + (long)d * N + perm16(j)] = (op_t)v[e];
+// A workgroup takes 64 keys of one (b, i, h) sequence: q / k as 8-value runs per thread
+// (coalesced 32-byte loads, 16-byte stores), v through an LDS transpose so that every V^T row
+// (d) leaves as 16-byte runs of 8 stored keys.
+constexpr int PREP_KB = 64;
+__global__ __launch_bounds__(256) void ta_prep_qkv_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                          const float* __restrict__ v, float qs,
+                                                          op_t* __restrict__ Q, op_t* __restrict__ K,
+                                                          op_t* __restrict__ Vt, int N) {
+  __shared__ op_t sV[D][PREP_KB + 8];   // [d][key within the block], rows 16 bytes longer
+  const int nb = N / PREP_KB;
+  const long r = blockIdx.x / nb;                       // sequence (b, i, h)
+  const int j0 = (int)(blockIdx.x - r * nb) * PREP_KB;
+  const int tid = threadIdx.x, jl = tid >> 2, d0 = (tid & 3) * 8;
+  const long e = (r * N + j0 + jl) * D + d0;           // element (key j0 + jl, d0) of q / k / v
+  const f32x4 q0 = *reinterpret_cast<const f32x4*>(q + e), q1 = *reinterpret_cast<const f32x4*>(q + e + 4);
+  const f32x4 k0 = *reinterpret_cast<const f32x4*>(k + e), k1 = *reinterpret_cast<const f32x4*>(k + e + 4);
+  const f32x4 v0 = *reinterpret_cast<const f32x4*>(v + e), v1 = *reinterpret_cast<const f32x4*>(v + e + 4);
+  opx8 oq, ok;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    oq[u] = (op_t)(q0[u] * qs);
+    oq[4 + u] = (op_t)(q1[u] * qs);
+    ok[u] = (op_t)k0[u];
+    ok[4 + u] = (op_t)k1[u];
+    sV[d0 + u][jl] = (op_t)v0[u];
+    sV[d0 + 4 + u][jl] = (op_t)v1[u];
   }
+  st_x8(Q + e, oq);
+  st_x8(K + e, ok);
+  __syncthreads();
+  // V^T row d = tid / 8, stored positions 8 c .. 8 c + 7 hold keys perm16(8 c + i) (perm16 is
+  // its own inverse and keeps every 16-key group in place)
+  const int d = tid >> 3, c = tid & 7;
+  opx8 ov;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ov[i] = sV[d][perm16(8 * c + i)];
+  st_x8(Vt + (r * D + d) * N + j0 + 8 * c, ov);
 }
 
 __global__ void ta_prep_bias_kernel(const float* __restrict__ bias, const float* __restrict__ mask,
@@ -1095,7 +1119,7 @@ extern "C" int pf_tri_attention(const float* q, const float* k, const float* v, 
   hipStream_t st = (hipStream_t)stream;
   TaBuffers t = ta_buffers(workspace, B, N);
   const long rows = (long)B * N * H;
-  ta_prep_qkv_kernel<<<2048, 256, 0, st>>>(q, k, v, scale * LOG2E, t.Q, t.K, t.Vt, rows, N);
+  ta_prep_qkv_kernel<<<(unsigned)(rows * (N / PREP_KB)), 256, 0, st>>>(q, k, v, scale * LOG2E, t.Q, t.K, t.Vt, N);
   PF_CHECK_LAUNCH("ta_prep_qkv_kernel");
   ta_prep_bias_kernel<<<1024, 256, 0, st>>>(bias, mask, t.bias32, t.mask16, (long)B * H * N * N, (long)B * N * N,
                                             N, n_valid);
