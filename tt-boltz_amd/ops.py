@@ -576,11 +576,12 @@ def triangle_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bias: 
         return o
 
     qp, kp, vp = padq(q), padq(k), padq(v)
-    bp = torch.zeros((B, H, n_pad, n_pad), dtype=torch.float32, device=dev)
-    bp[:, :, :N, :N] = bias.reshape(B, H, N, N)
-    if mask is None and n_pad == N:
-        mp = None
+    if n_pad == N:   # no padding: the caller's bias and mask as they are (fp32, contiguous)
+        bp = bias.reshape(B, H, N, N).to(torch.float32).contiguous()
+        mp = None if mask is None else mask.reshape(B, N, N).to(torch.float32).contiguous()
     else:
+        bp = torch.zeros((B, H, n_pad, n_pad), dtype=torch.float32, device=dev)
+        bp[:, :, :N, :N] = bias.reshape(B, H, N, N)
         mp = torch.zeros((B, n_pad, n_pad), dtype=torch.float32, device=dev)
         mp[:, :N, :N] = 1.0 if mask is None else mask.reshape(B, N, N).to(torch.float32)
     o = torch.empty((B, n_pad, H, n_pad, D), dtype=torch.float32, device=dev)
