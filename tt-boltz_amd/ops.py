@@ -536,7 +536,11 @@ def triangle_multiplicative_update(x: torch.Tensor, direction: str = "outgoing",
     B, N, _, C = x.shape
     n_pad = padded_len(N)
     zp = pad_pair(x.to(torch.float32), n_pad) if n_pad != N else x.to(torch.float32).contiguous()
-    mp = pad_pair_mask(None if mask is None else (mask.unsqueeze(0) if mask.dim() == 2 else mask), B, N, n_pad, dev)
+    m3 = None if mask is None else (mask.unsqueeze(0) if mask.dim() == 2 else mask)
+    if m3 is not None and n_pad == N and tuple(m3.shape) == (B, N, N):
+        mp = m3.to(device=dev, dtype=torch.float32).contiguous()   # read-only: no padded copy needed
+    else:
+        mp = pad_pair_mask(m3, B, N, n_pad, dev)
     w = convert_weights({"norm_in.weight": norm_in_weight, "norm_in.bias": norm_in_bias,
                          "p_in.weight": p_in_weight, "g_in.weight": g_in_weight,
                          "norm_out.weight": norm_out_weight, "norm_out.bias": norm_out_bias,
