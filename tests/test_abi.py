@@ -237,3 +237,32 @@ def test_failed_block_drops_deferred_single_track():
     fake.blocks = [good]
     pairformer.Pairformer.__call__(fake, s, z, ws=torch.zeros(1))
     assert single.joined and single.pending is not None and ran == []   # join() of the fake issues nothing
+
+
+def test_weight_conversion_cache_follows_the_source_tensor():
+    """The fused-op wrappers convert a weight once per tensor: the copy is reused while the
+    source lives unmodified, redone after an in-place change, and dropped with the source."""
+    import gc
+    import torch
+    from tt_boltz_amd import ops
+    cpu = torch.device("cpu")
+    w = torch.randn(64, 32)
+    a = ops.opw(w, cpu, "fp16")
+    assert a.dtype == torch.float16 and torch.equal(a.float(), w.half().float())
+    assert ops.opw(w, cpu, "fp16") is a                      # reused
+    assert ops.opw(w, cpu, "bf16") is not a                  # another operand type: its own copy
+    w.mul_(2.0)                                              # in place: the version counter moves
+    b = ops.opw(w, cpu, "fp16")
+    assert b is not a and torch.equal(b.float(), w.half().float())
+    n = len(ops._CONVERTED)
+    del w, a, b
+    gc.collect()
+    assert len(ops._CONVERTED) < n                           # entries die with their source
+    h = torch.randn(8, 8).half()
+    assert ops.opw(h, cpu, "fp16").data_ptr() == h.data_ptr()   # nothing to convert, nothing kept
+    assert all(e[0]() is not h for e in ops._CONVERTED.values())
+    v = torch.randn(16)
+    assert ops.f32(v, cpu).data_ptr() == v.data_ptr()
+    with torch.inference_mode():
+        t = torch.randn(4, 4)
+    assert torch.equal(ops.opw(t, cpu, "fp16").float(), t.half().float())   # no version counter: converted each time

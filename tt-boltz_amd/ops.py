@@ -18,6 +18,7 @@ stream.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from typing import Mapping, Optional
 
 import torch
@@ -58,9 +59,36 @@ def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
 
 
+#: converted copies of weight tensors: id(source) -> (weakref to the source, its version counter
+#: at conversion, device, dtype, the copy).  An entry lives as long as its source tensor and is
+#: used only while the source is unmodified (same version), so the per-call fused-op wrappers
+#: convert (or upload) a given weight once.
+_CONVERTED: dict = {}
+
+
+def _converted(w: torch.Tensor, device: torch.device, dtype: torch.dtype) -> torch.Tensor:
+    try:
+        version = w._version
+    except RuntimeError:   # inference tensors keep no version counter: convert every time
+        version = None
+    key = id(w)
+    e = _CONVERTED.get(key) if version is not None else None
+    if e is not None and e[0]() is w and e[1] == version and e[2] == torch.device(device) and e[3] == dtype:
+        return e[4]
+    out = w.detach().to(device=device, dtype=dtype).contiguous()
+    if version is None or out.data_ptr() == w.data_ptr():
+        return out   # already in place: nothing to keep (and no reference that keeps w alive)
+    try:
+        ref = weakref.ref(w, lambda _r, k=key: _CONVERTED.pop(k, None))
+    except TypeError:
+        return out
+    _CONVERTED[key] = (ref, version, torch.device(device), dtype, out)
+    return out
+
+
 def opw(w: torch.Tensor, device: torch.device, variant: str = DEFAULT_VARIANT) -> torch.Tensor:
-    """A weight matrix in the MFMA operand type of ``variant``."""
-    return w.detach().to(device=device, dtype=TORCH_DTYPE[variant]).contiguous()
+    """A weight matrix in the MFMA operand type of ``variant`` (converted once per tensor)."""
+    return _converted(w, device, TORCH_DTYPE[variant])
 
 
 def opw_lo(w: torch.Tensor, device: torch.device, variant: str = DEFAULT_VARIANT) -> torch.Tensor:
@@ -72,7 +100,7 @@ def opw_lo(w: torch.Tensor, device: torch.device, variant: str = DEFAULT_VARIANT
 
 
 def f32(t: Optional[torch.Tensor], device: torch.device) -> Optional[torch.Tensor]:
-    return None if t is None else t.detach().to(device=device, dtype=torch.float32).contiguous()
+    return None if t is None else _converted(t, device, torch.float32)
 
 
 def convert_weights(w: Mapping[str, torch.Tensor], device: torch.device, variant: str = DEFAULT_VARIANT,
