@@ -223,12 +223,14 @@ def test_transition_single(gpu):
     check("transition s", got, want)
 
 
-def test_attention_pair_bias(gpu):
+@pytest.mark.parametrize("N", [100, 128])
+def test_attention_pair_bias(gpu, N):
+    """N = 100 is padded to 128 inside the wrapper; N = 128 goes to the kernels as given."""
     w = _sub_w(6, "attention")
-    s, z, mask, _ = _inputs(100, 16, pad_tail=7)
+    s, z, mask, _ = _inputs(N, 16, pad_tail=7)
     want = ref.attention_pair_bias(s, z, mask, s, w, 16)
     got = ops.attention_pair_bias(s.to(gpu), z.to(gpu), mask.to(gpu), s.to(gpu), w, 16)
-    check("attention_pair_bias", got[:, :93], want[:, :93])
+    check(f"attention_pair_bias N={N}", got[:, :N - 7], want[:, :N - 7])
 
 
 # ------------------------------------------------------------------------------ layer / module

@@ -647,13 +647,20 @@ def attention_pair_bias(s: torch.Tensor, z: torch.Tensor, mask: Optional[torch.T
     dev = _require_gpu(s, z, k_in)
     B, N, c_s = s.shape
     n_pad = padded_len(N)
-    sp = torch.zeros((B, n_pad, c_s), dtype=torch.float32, device=dev)
-    sp[:, :N] = s
-    kp = torch.zeros((B, n_pad, c_s), dtype=torch.float32, device=dev)
-    kp[:, :N] = k_in
+
+    def pad_tokens(t):   # [B, N, c] -> [B, n_pad, c] fp32; read-only, so no copy when N needs no padding
+        if n_pad == N:
+            return t.to(torch.float32).contiguous()
+        o = torch.zeros((B, n_pad) + tuple(t.shape[2:]), dtype=torch.float32, device=dev)
+        o[:, :N] = t
+        return o
+    sp, kp = pad_tokens(s), pad_tokens(k_in)
     zp = pad_pair(z.to(torch.float32), n_pad) if n_pad != N else z.to(torch.float32).contiguous()
-    mp = torch.zeros((B, n_pad), dtype=torch.float32, device=dev)
-    mp[:, :N] = 1.0 if mask is None else mask.to(torch.float32)
+    if mask is not None and n_pad == N:
+        mp = mask.to(device=dev, dtype=torch.float32).contiguous()
+    else:
+        mp = torch.zeros((B, n_pad), dtype=torch.float32, device=dev)
+        mp[:, :N] = 1.0 if mask is None else mask.to(torch.float32)
     w = convert_weights(weights, dev, variant)
     out = torch.empty_like(sp)
     ws = workspace(apb_workspace_bytes(B, n_pad, c_s, num_heads, variant), dev)
