@@ -400,6 +400,48 @@ def summarize_bench(kt_dir: str, bench_log: str) -> None:
     open(os.path.join(ROOT, "profiles", "bench_n512_roofline_kernel_stats.txt"), "w").write("\n".join(lines) + "\n")
 
 
+def summarize_stack(kt_dir: str, stack_log: str) -> None:
+    """profiles/stack_n768_kernel_stats.txt from a --kernel-trace run of ``bench.py --stack-only``
+    and the JSON it printed: the attention core and the 16-bit contraction over every trunk pass
+    of the run (warm-up, the four timed passes and the event-timed pass; the contraction's last
+    21 dispatches, its warm-up and 20-launch loop alone on random planes, apart) against the
+    JSON's attention_in_stack / contract_in_stack and contract, and every kernel of the run."""
+    import collections
+    import csv
+    st = next(json.loads(l) for l in open(stack_log) if l.startswith('{"N"'))
+    rows = sorted(csv.DictReader(open(os.path.join(kt_dir, "run_kernel_trace.csv"))),
+                  key=lambda r: int(r["Start_Timestamp"]))
+    us = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")
+    att = [us(r) for r in rows if _kernel_short(r["Kernel_Name"]) == "ta_attn_kernel"]
+    con = [us(r) for r in rows if _kernel_short(r["Kernel_Name"]) == "tm_contract_dma_kernel"]
+    con_stack, con_alone = con[:-21], con[-20:]
+    N, peak = st["N"], 2.5e15
+    f_att, f_con = 4 * N ** 3 * 128, 2 * 128 * N ** 3
+    tf = lambda flop, t: flop / (t * 1e-6) / 1e12
+    lines = ["# Attention core and trimul contraction inside the config-3 trunk (64 layers, N = 768, MI355X, one GPU)",
+             "# command: rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- python3 bench.py --stack-only",
+             "# (this file: bench.py --summarize-stack <dir> <the run's stdout>)",
+             f"# trunk: {st['layers_per_s']} layers/s ({st['trunk_s']} s for {st['passes']} passes) in that run",
+             f"# ta_attn_kernel: {len(att)} dispatches, mean {mean(att):.1f} us = {tf(f_att, mean(att)):.0f} TF/s = "
+             f"{tf(f_att, mean(att)) * 1e12 / peak:.3f} of 2.5 PF/s   | attention_in_stack "
+             f"{st['attention_in_stack']['launch_ms'] * 1e3:.1f} us (HIP events)",
+             f"# tm_contract_dma_kernel in the trunk: {len(con_stack)} dispatches, mean {mean(con_stack):.1f} us = "
+             f"{tf(f_con, mean(con_stack)):.0f} TF/s = {tf(f_con, mean(con_stack)) * 1e12 / peak:.3f}   | "
+             f"contract_in_stack {st['contract_in_stack']['launch_ms'] * 1e3:.1f} us (HIP events)",
+             f"# tm_contract_dma_kernel alone (random planes): {len(con_alone)} dispatches, mean {mean(con_alone):.1f} us = "
+             f"{tf(f_con, mean(con_alone)):.0f} TF/s = {tf(f_con, mean(con_alone)) * 1e12 / peak:.3f}   | "
+             f"contract {st['contract']['launch_ms'] * 1e3:.1f} us",
+             "# Every kernel of the run:",
+             f"# {'kernel':40s} {'calls':>6s} {'avg_us':>9s} {'total_ms':>9s}"]
+    dur = collections.defaultdict(list)
+    for r in rows:
+        dur[_kernel_short(r["Kernel_Name"])].append(us(r))
+    for k, d in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"  {k:40s} {len(d):6d} {mean(d):9.1f} {sum(d) / 1e3:9.3f}")
+    open(os.path.join(ROOT, "profiles", "stack_n768_kernel_stats.txt"), "w").write("\n".join(lines) + "\n")
+
+
 # ----------------------------------------------------------------------------- profile summaries
 PROBE_PMC_PASSES = ("SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS "
                     "SQ_VALU_MFMA_BUSY_CYCLES SQ_WAIT_INST_ANY GRBM_GUI_ACTIVE",
@@ -923,6 +965,10 @@ def main() -> int:
                     help="write profiles/bench_n512_roofline_kernel_stats.txt from a kernel trace of the bench")
     ap.add_argument("--summarize-contract", nargs="+", metavar="DIR",
                     help="KT_DIR PMC_DIR...: write profiles/contract_vs_hipblaslt.md from rocprofv3 CSV output")
+    ap.add_argument("--stack-only", action="store_true",
+                    help="print only the config-3 trunk object (stack_bench) as JSON")
+    ap.add_argument("--summarize-stack", nargs=2, metavar=("KT_DIR", "STACK_LOG"),
+                    help="write profiles/stack_n768_kernel_stats.txt from a kernel trace of --stack-only")
     ap.add_argument("--summarize-probe", nargs="+", metavar="DIR",
                     help="KT_DIR PMC_DIR...: write the profiles/ summaries for --n from rocprofv3 CSV output")
     args = ap.parse_args()
@@ -935,6 +981,9 @@ def main() -> int:
     if args.summarize_contract:
         summarize_contract(args.summarize_contract[0], args.summarize_contract[1:])
         return 0
+    if args.summarize_stack:
+        summarize_stack(*args.summarize_stack)
+        return 0
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}): this build measures the "
               "single-GPU Pairformer path; multi-GPU sharding is a design note only.", file=sys.stderr)
@@ -944,6 +993,9 @@ def main() -> int:
         return probe_traffic(args.n)
     if args.probe_contract:
         return probe_contract()
+    if args.stack_only:
+        print(json.dumps(stack_bench()), flush=True)
+        return 0
 
     import torch
     from tt_boltz_amd import ops, pairformer, synthetic
