@@ -187,11 +187,13 @@ def test_triatt_config2(gpu, ending):
     check(f"config2 triatt ending={ending} full", out, want)
 
 
-@pytest.mark.parametrize("N", [96, 100, 128])
+@pytest.mark.parametrize("N", [64, 96, 100, 128, 192, 256])
 def test_tri_attention_core(gpu, N):
     """N = 100 runs padded to 128 with n_valid = 100: the fully masked row's mean of v then
     leaves out the padded keys, and the padded rows take the same path.  N = 128 needs no
-    padding, so the caller's bias and mask go to the kernel as they are."""
+    padding, so the caller's bias and mask go to the kernel as they are.  These launches fill
+    less than half of the chip, so their blocks run split over workgroups of 2 heads (N = 64:
+    one 64-key step per head, 192, 256) or of 1 head (96, 100, 128)."""
     g = torch.Generator().manual_seed(3)
     B, H, D = 1, 4, 32
     q, k, v = (torch.randn((B, N, H, N, D), generator=g) for _ in range(3))

@@ -335,22 +335,23 @@ template <bool OUT_F32>
 __global__ __launch_bounds__(64 * TA_WAVES, 1) void ta_attn_kernel(
     const op_t* __restrict__ Q, const op_t* __restrict__ K, const op_t* __restrict__ Vt,
     const float* __restrict__ bias32, const op_t* __restrict__ mask16, op_t* __restrict__ O16,
-    float* __restrict__ O32, int N, int n_valid, int total, int full) {
+    float* __restrict__ O32, int N, int n_valid, int total, int full, int split) {
   extern __shared__ __attribute__((aligned(16))) char alds[];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int row = wid & 3, qb = wid >> 2;   // frame row, 32-query block
   // Workgroups 0 .. full-1 take all heads of their (rows, queries) block; the blocks after them
-  // (a last round that would leave at least half of the CUs idle) go to two workgroups each,
-  // heads 0-1 and heads 2-3, so that round takes about half as long.
+  // (a last round that would leave at least half of the CUs idle, or a whole launch that small)
+  // go to `split` (2 or 4) workgroups each, H / split heads apiece, so that round takes about
+  // 1 / split as long.
   int w, h0 = 0, nh = H;
   if ((int)blockIdx.x < full) {
     w = xcd_remap(blockIdx.x, full);
   } else {
-    const int hw = xcd_remap(blockIdx.x - full, 2 * (total - full));
-    w = full + (hw >> 1);
-    h0 = (hw & 1) * (H / 2);
-    nh = H / 2;
+    const int hw = xcd_remap(blockIdx.x - full, split * (total - full));
+    w = full + hw / split;
+    nh = H / split;
+    h0 = (hw % split) * nh;
   }
   const int nQP = (N + 127) >> 7, nKB = N >> 6, T = nh * nKB;
   const int per_b = (N >> 2) * nQP;
@@ -889,13 +890,20 @@ template <bool OUT_F32>
 int launch_attn(const TaBuffers& t, float* o32, int B, int N, int n_valid, hipStream_t st) {
   if (const int rc = pf_reserve_lds((const void*)ta_attn_kernel<OUT_F32>, TA_LDS, "ta_attn_kernel")) return rc;
   const int total = B * (N / 4) * ((N + 127) / 128);
-  // a last round of whole blocks on at most half of the CUs runs as head halves
+  // the blocks of a last round (all of them when the launch is one round or less) that would fill
+  // at most half of the CUs run split over 2 or 4 workgroups, H / split heads each: the largest
+  // split whose workgroups still fit on the chip
   const int cus = device_cus();
-  const int rest = cus > 0 ? total % cus : 0;
-  const int full = 2 * rest <= cus && total > cus ? total - rest : total;
+  const int rest = cus <= 0 ? 0 : total > cus ? total % cus : total;
+  // (the kernel takes its H / split * N / 64 steps in pairs, one per ring stage: a single-head
+  // split needs an even N / 64)
+  int split = 1;
+  while (split < 4 && rest > 0 && 2 * split * rest <= cus && !(split == 2 && (N / 64) % 2)) split *= 2;
+  const int full = split > 1 ? total - rest : total;
+  static_assert(H % 4 == 0, "head splits of 2 and 4");
   pf_attend_mark(st, 0);
-  ta_attn_kernel<OUT_F32><<<full + 2 * (total - full), 64 * TA_WAVES, TA_LDS, st>>>(
-      t.Q, t.K, t.Vt, t.bias32, t.mask16, t.O, o32, N, n_valid, total, full);
+  ta_attn_kernel<OUT_F32><<<full + split * (total - full), 64 * TA_WAVES, TA_LDS, st>>>(
+      t.Q, t.K, t.Vt, t.bias32, t.mask16, t.O, o32, N, n_valid, total, full, split > 1 ? split : 2);
   PF_CHECK_LAUNCH("ta_attn_kernel");
   pf_attend_mark(st, 1);
   return PF_OK;
