@@ -53,11 +53,11 @@ def _inputs(N, seed, pad_tail=0, rand_mask=False):
 
 # ------------------------------------------------------------------------------ contraction
 @pytest.mark.parametrize("variant", ["fp16", "bf16"])
-@pytest.mark.parametrize("N", [64, 192, 256, 448, 512, 640])
+@pytest.mark.parametrize("N", [64, 192, 256, 384, 448, 512, 640])
 def test_contract_matches_fp32_matmul(gpu, N, variant):
     """The MFMA contraction on operand-type planes equals an fp32 matmul of the same
     (already rounded) values up to summation order; the scaled operand-type output is
-    that result rounded once.  N < 384 runs the 128x128-tile kernel, N >= 384 the
+    that result rounded once.  N < 448 runs the 128x128-tile kernel, N >= 448 the
     256x256-tile LDS-DMA kernel (448 and 640 end in partial edge tiles)."""
     g = torch.Generator().manual_seed(N)
     dt = ops.TORCH_DTYPE[variant]

@@ -645,8 +645,9 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
   }
 }
 
-// Contraction dispatch: 256x256 tiles from N = 384 up (enough tiles to fill the chip
-// and a long enough K loop), 128x128 tiles below.
+// Contraction dispatch: 256x256 tiles from N = 448 up (enough tiles to fill the chip
+// and a long enough K loop), 128x128 tiles below (at N = 384 the 256x256 tiles would be 44 %
+// padding: 37.3 us against 32.4 us with 128x128 tiles).
 // Rectangular form (256x256 tiles, any M, Nc multiple of 32, K multiple of 64):
 // X[p][i][j] = sum_k A[p][i][k] * B[p][j][k], A [P][M][K], B [P][Nc][K], X [P][M][Nc].
 // amax_parts / nparts: when nparts > 0 the output scale is x_store_scale of those operand
@@ -673,7 +674,7 @@ int launch_contract_rect(const op_t* A, const op_t* B, OutT* X, int planes, int 
 template <typename OutT>
 int launch_contract(const op_t* opA, const op_t* opB, OutT* X, int planes, int N, float scale, hipStream_t st,
                     const float* amax_parts = nullptr, int nparts = 0) {
-  if (N >= 384) return launch_contract_rect<OutT>(opA, opB, X, planes, N, N, N, scale, st, amax_parts, nparts);
+  if (N >= 448) return launch_contract_rect<OutT>(opA, opB, X, planes, N, N, N, scale, st, amax_parts, nparts);
   const int tpd = (N + BM - 1) / BM;
   const int total = planes * tpd * tpd;
   tm_contract_kernel<OutT><<<total, 256, 0, st>>>(opA, opB, X, N, tpd, total, scale, amax_parts, nparts);
