@@ -689,6 +689,91 @@ PF_DEV void stats_mu(const float* __restrict__ partials, float* mu, float* scrat
   }
 }
 
+// Prologue helpers of the persistent pair kernels.  Every global load of a thread's share is
+// issued before the first use, so the set-up costs about one memory round trip instead of one
+// per (partly unrolled) loop step; the arithmetic and its order are those of stats_mu,
+// corrected_offset and a plain staging loop.
+template <int NT>
+constexpr int stats_per() { return PS_WG / (NT / PS_C); }
+// this thread's partials (channel threadIdx.x % 128, groups q, q + NT / 128, ...)
+template <int NT>
+PF_DEV void stats_load(const float* __restrict__ partials, float (&v)[stats_per<NT>()]) {
+  static_assert(NT % PS_C == 0 && PS_WG % (NT / PS_C) == 0, "block size");
+  constexpr int nq = NT / PS_C;
+  const int c = threadIdx.x % PS_C, q = threadIdx.x / PS_C;
+#pragma unroll
+  for (int i = 0; i < stats_per<NT>(); ++i) v[i] = partials[(q + i * nq) * PS_C + c];
+}
+// mu (LDS, 128 floats) from the loaded partials as stats_mu forms it; `scratch`: NT floats of
+// LDS.  Synchronizes once; the caller synchronizes again before reading mu.
+template <int NT>
+PF_DEV void stats_reduce(const float (&v)[stats_per<NT>()], float* mu, float* scratch) {
+  constexpr int nq = NT / PS_C;
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < stats_per<NT>(); ++i) sum += v[i];
+  scratch[threadIdx.x] = sum;
+  __syncthreads();
+  if (threadIdx.x < PS_C) {
+    float t = 0.f;
+    for (int j = 0; j < nq; ++j) t += scratch[j * PS_C + threadIdx.x];
+    mu[threadIdx.x] = t;
+  }
+}
+// a 128-element op_t row in registers
+PF_DEV void load_row_x8(const op_t* __restrict__ row, opx8 (&v)[PS_C / 8]) {
+#pragma unroll
+  for (int c = 0; c < PS_C / 8; ++c) v[c] = ld_x8(row + 8 * c);
+}
+// corrected_offset with the residual row already in registers (has_lo false: no correction);
+// GAMMA false: no gamma factor (corrected_offset's gamma = nullptr: the product by 1 it takes is
+// exact).  The LDS reads of gamma and mu go in groups of four chunks, so they are not all hoisted
+// into registers at once.
+template <bool GAMMA>
+PF_DEV float corrected_offset_regs(float offb, const opx8 (&lo)[PS_C / 8], bool has_lo, const float* gamma,
+                                   const float* mu) {
+  float acc = offb;
+  if (has_lo) {
+#pragma unroll
+    for (int c = 0; c < PS_C / 8; ++c) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float l = (float)lo[c][e];
+        acc += (GAMMA ? l * gamma[8 * c + e] : l) * mu[8 * c + e];
+      }
+      if (c % 4 == 3) __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  return acc;
+}
+// [ROWS][COLS] op_t weights: this thread's 16-byte chunks (chunk threadIdx.x + NT i), loaded
+// all at once, then stored to LDS rows `pitch` elements apart (8-byte aligned rows: two 8-byte
+// stores per chunk)
+template <int NT, int ROWS, int COLS>
+constexpr int stage_per() { return (ROWS * (COLS / 8) + NT - 1) / NT; }
+template <int NT, int ROWS, int COLS>
+PF_DEV void stage_load(const op_t* __restrict__ src, opx8 (&v)[stage_per<NT, ROWS, COLS>()]) {
+  constexpr int CH = ROWS * (COLS / 8);
+#pragma unroll
+  for (int i = 0; i < stage_per<NT, ROWS, COLS>(); ++i) {
+    const int c = threadIdx.x + NT * i;
+    if (CH % NT == 0 || c < CH) v[i] = ld_x8(src + (c / (COLS / 8)) * COLS + (c % (COLS / 8)) * 8);
+  }
+}
+template <int NT, int ROWS, int COLS>
+PF_DEV void stage_store(op_t* dst, int pitch, const opx8 (&v)[stage_per<NT, ROWS, COLS>()]) {
+  constexpr int CH = ROWS * (COLS / 8);
+#pragma unroll
+  for (int i = 0; i < stage_per<NT, ROWS, COLS>(); ++i) {
+    const int c = threadIdx.x + NT * i;
+    if (CH % NT == 0 || c < CH) {
+      op_t* d = dst + (c / (COLS / 8)) * pitch + (c % (COLS / 8)) * 8;
+      *reinterpret_cast<opx4*>(d) = opx4{v[i][0], v[i][1], v[i][2], v[i][3]};
+      *reinterpret_cast<opx4*>(d + 4) = opx4{v[i][4], v[i][5], v[i][6], v[i][7]};
+    }
+  }
+}
+
 // Offset of one output row: offb (the fp32 W . beta) plus, with the mean correction, the row of
 // the weight residual against gamma * mu (gamma, mu: 128 floats, LDS or global; gamma = nullptr
 // when the kernel folds gamma into its weights, whose residual then already carries it).

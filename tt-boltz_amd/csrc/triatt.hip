@@ -104,37 +104,71 @@ __global__ __launch_bounds__(64 * TAP_WAVES, 1) void ta_proj_kernel(
     return row < C ? wq + row * CC : row < 2 * C ? wk + (row - C) * CC
          : row < 3 * C ? wv + (row - 2 * C) * CC : wb + (row - 3 * C) * CC;
   };
-  for (int c = tid; c < TAP_ROWS * (CC / 8); c += 64 * TAP_WAVES) {
-    const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
-    opx8 v = zero_x8();
-    if (row < 3 * C + H) {
-      const opx8 w = ld_x8(wrow(row) + col);
+  {   // every global load of the set-up first (weights, the offset row, partials), then LDS
+    constexpr int NT = 64 * TAP_WAVES, CH = TAP_ROWS * (CC / 8), SPER = (CH + NT - 1) / NT;
+    static_assert(TAP_ROWS <= NT && NT % (CC / 8) == 0, "one offset row per thread; one column per thread");
+    const int col = (tid % (CC / 8)) * 8;   // the same for every chunk of this thread
+    opx8 wv[SPER];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (op_t)((float)w[e] * lnw[col + e]);
+    for (int i = 0; i < SPER; ++i) {
+      const int c = tid + NT * i, row = c / (CC / 8);
+      wv[i] = c < CH && row < 3 * C + H ? ld_x8(wrow(row) + col) : zero_x8();
     }
-    st_x8(plds + row * LW + col, v);
-  }
-  if (!FAST && mf.offb && mf.stats) {
-    stats_mu(mf.stats, mu, mu + PS_C);
-    __syncthreads();
-  }
-  for (int row = tid; row < TAP_ROWS; row += 64 * TAP_WAVES) {   // accumulator starts W beta
-    float acc = 0.f;
-    if (row < 3 * C + H) {
-      if (!FAST && mf.offb) {
-        const op_t* lo = !mf.stats ? nullptr : mf.lo[row < 3 * C ? row / C : 3] + (row < 3 * C ? row % C : row - 3 * C) * CC;
-        if constexpr (CC == PS_C) acc = corrected_offset(mf.offb[row], lo, nullptr, mu);
-      } else {
-        const op_t* w = wrow(row);
-#pragma unroll 4
-        for (int c = 0; c < CC; c += 8) {
-          const opx8 w8 = ld_x8(w + c);
+    float gcol[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[c + e];
-        }
+    for (int e = 0; e < 8; ++e) gcol[e] = lnw[col + e];
+    const bool meanfix = !FAST && mf.offb && mf.stats;
+    const int orow = tid;   // this thread's offset row
+    const bool live_row = orow < 3 * C + H;
+    float pv[stats_per<NT>()];
+    if (meanfix) stats_load<NT>(mf.stats, pv);
+    // the row behind this thread's offset: the residual (mean correction) or the weight (W beta)
+    opx8 rv[CC / 8];
+    float offb_v = 0.f;
+    const bool use_offb = !FAST && mf.offb;
+    if (live_row) {
+      if (use_offb) {
+        offb_v = mf.offb[orow];
+        if constexpr (CC == PS_C)
+          if (mf.stats) {
+            const op_t* lo = mf.lo[orow < 3 * C ? orow / C : 3] + (orow < 3 * C ? orow % C : orow - 3 * C) * CC;
+#pragma unroll
+            for (int c = 0; c < CC / 8; ++c) rv[c] = ld_x8(lo + 8 * c);
+          }
+      } else {
+        const op_t* w = wrow(orow);
+#pragma unroll
+        for (int c = 0; c < CC / 8; ++c) rv[c] = ld_x8(w + 8 * c);
       }
     }
-    cb[row] = acc;
+#pragma unroll
+    for (int i = 0; i < SPER; ++i) {
+      const int c = tid + NT * i, row = c / (CC / 8);
+      if (c < CH) {
+        opx8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (op_t)((float)wv[i][e] * gcol[e]);
+        st_x8(plds + row * LW + col, row < 3 * C + H ? v : zero_x8());
+      }
+    }
+    if (meanfix) {
+      stats_reduce<NT>(pv, mu, mu + PS_C);
+      __syncthreads();
+    }
+    if (orow < TAP_ROWS) {   // accumulator starts W beta
+      float acc = 0.f;
+      if (live_row) {
+        if (use_offb) {
+          if constexpr (CC == PS_C) acc = corrected_offset_regs<false>(offb_v, rv, mf.stats != nullptr, nullptr, mu);
+        } else {
+#pragma unroll
+          for (int c = 0; c < CC / 8; ++c)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc += (float)rv[c][e] * lnb[8 * c + e];
+        }
+      }
+      cb[orow] = acc;
+    }
   }
   __syncthreads();
 
@@ -668,18 +702,6 @@ constexpr size_t tao_lds() {
   return (C + CC) * sizeof(float) + (HILO ? 2 : 1) * ((size_t)C * (CC + 4) + (size_t)CC * (C + 4)) * sizeof(op_t);
 }
 
-// [rows][cols] op_t weights -> LDS rows `pitch` apart (8-byte aligned: two 8-byte stores per
-// 16-byte load)
-template <int NT>
-PF_DEV void stage_rows(op_t* dst, const op_t* __restrict__ src, int rows, int cols, int pitch) {
-  for (int c = threadIdx.x; c < rows * (cols / 8); c += NT) {
-    const int row = c / (cols / 8), col = (c % (cols / 8)) * 8;
-    const opx8 v = ld_x8(src + row * cols + col);
-    *reinterpret_cast<opx4*>(&dst[row * pitch + col]) = opx4{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<opx4*>(&dst[row * pitch + col + 4]) = opx4{v[4], v[5], v[6], v[7]};
-  }
-}
-
 // resid: 0 -> out = update; 1 -> out = z_in + update (out may alias z_in); 2 -> out += update
 // HILO: W_g and W_o come with their residuals wg_lo = W_g - W_g16, wo_lo = W_o - W_o16 (rounded
 // to op_t), and both products run on hi + lo (two MFMAs per fragment): weights good to ~2^-22
@@ -700,25 +722,38 @@ __global__ __launch_bounds__(64 * TAO_WAVES, 1) void ta_out_kernel(
   op_t* sWol = sWgl + C * LWG;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  stage_rows<64 * TAO_WAVES>(sWg, wg, C, CC, LWG);
-  stage_rows<64 * TAO_WAVES>(sWo, wo, CC, C, LWO);
-  if constexpr (HILO) {
-    stage_rows<64 * TAO_WAVES>(sWgl, wg_lo, C, CC, LWG);
-    stage_rows<64 * TAO_WAVES>(sWol, wo_lo, CC, C, LWO);
+  {   // weights -> LDS: every chunk of this thread loaded before the first store
+    constexpr int NT = 64 * TAO_WAVES;
+    static_assert(CC <= NT, "gamma: one value per thread");
+    opx8 vg[stage_per<NT, C, CC>()], vo[stage_per<NT, CC, C>()];
+    stage_load<NT, C, CC>(wg, vg);
+    stage_load<NT, CC, C>(wo, vo);
+    const float gv = tid < CC ? lnw[tid] : 0.f;
+    if constexpr (HILO) {
+      opx8 vgl[stage_per<NT, C, CC>()], vol[stage_per<NT, CC, C>()];
+      stage_load<NT, C, CC>(wg_lo, vgl);
+      stage_load<NT, CC, C>(wo_lo, vol);
+      stage_store<NT, C, CC>(sWgl, LWG, vgl);
+      stage_store<NT, CC, C>(sWol, LWO, vol);
+    }
+    stage_store<NT, C, CC>(sWg, LWG, vg);
+    stage_store<NT, CC, C>(sWo, LWO, vo);
+    if (tid < CC) gam[tid] = gv;
   }
   __syncthreads();
-  for (int c = tid; c < CC; c += 64 * TAO_WAVES) gam[c] = lnw[c];
-  for (int row = tid; row < C; row += 64 * TAO_WAVES) {   // gate offsets -log2(e) W_g beta
-    const op_t* w = wg + row * CC;
-    const op_t* wl = wg_lo + row * CC;
+  for (int row = tid; row < C; row += 64 * TAO_WAVES) {   // gate offsets -log2(e) W_g beta (weights from LDS)
+    const op_t* w = sWg + row * LWG;
+    const op_t* wl = sWgl + row * LWG;
     float acc = 0.f;
-#pragma unroll 4
+#pragma unroll
     for (int c = 0; c < CC; c += 8) {
-      const opx8 w8 = ld_x8(w + c);
+      const opx4 wa = ld_x4(w + c), wb = ld_x4(w + c + 4);
+      const opx8 w8 = {wa[0], wa[1], wa[2], wa[3], wb[0], wb[1], wb[2], wb[3]};
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[c + e];
       if constexpr (HILO) {
-        const opx8 l8 = ld_x8(wl + c);
+        const opx4 la = ld_x4(wl + c), lb = ld_x4(wl + c + 4);
+        const opx8 l8 = {la[0], la[1], la[2], la[3], lb[0], lb[1], lb[2], lb[3]};
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc += (float)l8[e] * lnb[c + e];
       }

@@ -89,31 +89,49 @@ __global__ __launch_bounds__(64 * TMP_WAVES, 1) void tm_proj_kernel(
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   op_t* stg = lg + 2 * CC * LW + wid * 32 * SPITCH;
   float* wave_amax = reinterpret_cast<float*>(lg + 2 * CC * LW + TMP_WAVES * 32 * SPITCH);
-#pragma unroll 4
-  for (int c = tid; c < 2 * CC * (CC / 8); c += 64 * TMP_WAVES) {
-    const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
-    st_x8(lp + row * LW + col, ld_x8(w_p + row * CC + col));
-    st_x8(lg + row * LW + col, ld_x8(w_g + row * CC + col));
-  }
-  for (int c = tid; c < CC; c += 64 * TMP_WAVES) gam[c] = lnw[c];
   float* mu = reinterpret_cast<float*>(lg + 2 * CC * LW);   // the output stages, free until the tile loop
-  if (offb && stats) stats_mu(stats, mu, mu + PS_C);
+  constexpr int NT = 64 * TMP_WAVES;
+  static_assert(4 * CC <= NT, "one offset row per thread");
+  const int orow = tid;   // this thread's offset row (W beta): 0 .. 4 CC - 1
+  opx8 rv[CC / 8];        // the row behind it: the residual (mean correction) or the weight
+  float offb_v = 0.f;
+  // set-up in two batches of global loads (each issued whole before its first use): the weights
+  // and partials, then, while the statistics reduce, the residual rows of the mean correction
+  const bool meanfix = offb && stats;
+  {
+    opx8 vp[stage_per<NT, 2 * CC, CC>()], vg[stage_per<NT, 2 * CC, CC>()];
+    stage_load<NT, 2 * CC, CC>(w_p, vp);
+    stage_load<NT, 2 * CC, CC>(w_g, vg);
+    const float gv = tid < CC ? lnw[tid] : 0.f;
+    float pv[stats_per<NT>()];
+    if (meanfix) stats_load<NT>(stats, pv);
+    if (offb && orow < 4 * CC) offb_v = offb[orow];
+    stage_store<NT, 2 * CC, CC>(lp, LW, vp);
+    stage_store<NT, 2 * CC, CC>(lg, LW, vg);
+    if (tid < CC) gam[tid] = gv;
+    if constexpr (CC == C)
+      if (meanfix && orow < 4 * CC) {
+        const op_t* lo = orow < 2 * CC ? p_lo + orow * CC : g_lo + (orow - 2 * CC) * CC;
+#pragma unroll
+        for (int c = 0; c < CC / 8; ++c) rv[c] = ld_x8(lo + 8 * c);
+      }
+    if (meanfix) stats_reduce<NT>(pv, mu, mu + PS_C);
+  }
   __syncthreads();
-  for (int row = tid; row < 4 * CC; row += 64 * TMP_WAVES) {   // offsets W beta (one row per thread)
+  if (orow < 4 * CC) {   // offsets W beta (one row per thread)
     float acc = 0.f;
     if (offb) {
-      const op_t* lo = !stats ? nullptr : row < 2 * CC ? p_lo + row * CC : g_lo + (row - 2 * CC) * CC;
-      if constexpr (CC == C) acc = corrected_offset(offb[row], lo, gam, mu);
-    } else {
-      const op_t* w = row < 2 * CC ? w_p + row * CC : w_g + (row - 2 * CC) * CC;
-#pragma unroll 4
-      for (int c = 0; c < CC; c += 8) {
-        const opx8 w8 = ld_x8(w + c);
+      if constexpr (CC == C) acc = corrected_offset_regs<true>(offb_v, rv, stats != nullptr, gam, mu);
+    } else {   // from the staged weights (rows 16-byte aligned)
+      const op_t* w = orow < 2 * CC ? lp + orow * LW : lg + (orow - 2 * CC) * LW;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[c + e];
+      for (int c = 0; c < CC / 8; ++c) {
+        const opx8 w8 = ld_x8(w + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += (float)w8[e] * lnb[8 * c + e];
       }
     }
-    cbias[row] = row < 2 * CC ? acc : -LOG2E * acc;
+    cbias[orow] = orow < 2 * CC ? acc : -LOG2E * acc;
   }
   __syncthreads();
   const uint32_t ntiles = (uint32_t)B * N * N / 32;
@@ -526,51 +544,67 @@ __global__ __launch_bounds__(64 * TMO_WAVES, 1) void tm_out_kernel(
   XT* xs = reinterpret_cast<XT*>(sWg + (HILO ? 2 : 1) * CC * LW) + wid * XCH * XSP;   // this wave's X stage
   // weights -> LDS (rows are 8-byte aligned: two 8-byte stores per 16-byte load), gamma, and
   // the offsets W beta (one row per thread)
-  for (int c = tid; c < CC * (CC / 8); c += 64 * TMO_WAVES) {
-    const int row = c / (CC / 8), col = (c % (CC / 8)) * 8;
-    const opx8 vp = ld_x8(w_pout + row * CC + col), vg = ld_x8(w_gout + row * CC + col);
-    *reinterpret_cast<opx4*>(&sWp[row * LW + col]) = opx4{vp[0], vp[1], vp[2], vp[3]};
-    *reinterpret_cast<opx4*>(&sWp[row * LW + col + 4]) = opx4{vp[4], vp[5], vp[6], vp[7]};
-    *reinterpret_cast<opx4*>(&sWg[row * LW + col]) = opx4{vg[0], vg[1], vg[2], vg[3]};
-    *reinterpret_cast<opx4*>(&sWg[row * LW + col + 4]) = opx4{vg[4], vg[5], vg[6], vg[7]};
-    if constexpr (HILO) {
-      const opx8 vl = ld_x8(w_pout_lo + row * CC + col);
-      *reinterpret_cast<opx4*>(&sWpl[row * LW + col]) = opx4{vl[0], vl[1], vl[2], vl[3]};
-      *reinterpret_cast<opx4*>(&sWpl[row * LW + col + 4]) = opx4{vl[4], vl[5], vl[6], vl[7]};
-    }
-  }
-  for (int c = tid; c < CC; c += 64 * TMO_WAVES) {
-    gam_o[c] = lno_w[c];
-    gam_i[c] = lni_w[c];
-  }
   float* mu = reinterpret_cast<float*>(xs - wid * XCH * XSP);   // the X stages, free until the tile loop
-  if (offb_g && stats) stats_mu(stats, mu, mu + PS_C);
-  __syncthreads();
-  for (int row = tid; row < 2 * CC; row += 64 * TMO_WAVES) {
-    const bool g = row >= CC;
-    if (g && offb_g) {   // gate offsets from the exact g_out beta (+ the mean correction)
-      if constexpr (CC == C)
-        cbias[row] = -LOG2E * corrected_offset(offb_g[row - CC], stats ? gout_lo + (row - CC) * CC : nullptr,
-                                               gam_i, mu);
-      continue;
+  constexpr int NT = 64 * TMO_WAVES;
+  static_assert(2 * CC <= NT, "one offset row per thread");
+  const int orow = tid;                   // this thread's offset row: p (< CC) or g
+  const bool grow = orow >= CC, gfix = grow && offb_g != nullptr;
+  opx8 rv[CC / 8];                        // g rows with offb_g: the residual of g_out (mean correction)
+  float offb_v = 0.f;
+  // set-up in two batches of global loads (each issued whole before its first use): the weights
+  // and partials, then, while the statistics reduce, the residual rows of the mean correction
+  {
+    const bool meanfix = offb_g && stats;
+    opx8 vp[stage_per<NT, CC, CC>()], vg[stage_per<NT, CC, CC>()];
+    stage_load<NT, CC, CC>(w_pout, vp);
+    stage_load<NT, CC, CC>(w_gout, vg);
+    const float go = tid < CC ? lno_w[tid] : 0.f, gi = tid < CC ? lni_w[tid] : 0.f;
+    float pv[stats_per<NT>()];
+    if (meanfix) stats_load<NT>(stats, pv);
+    if (orow < 2 * CC && gfix) offb_v = offb_g[orow - CC];
+    if constexpr (HILO) {
+      opx8 vl[stage_per<NT, CC, CC>()];
+      stage_load<NT, CC, CC>(w_pout_lo, vl);
+      stage_store<NT, CC, CC>(sWpl, LW, vl);
     }
-    const op_t* w = g ? w_gout + (row - CC) * CC : w_pout + row * CC;
-    const float* bet = g ? lni_b : lno_b;
-    float acc = 0.f;
-#pragma unroll 4
-    for (int c = 0; c < CC; c += 8) {
-      const opx8 w8 = ld_x8(w + c);
+    stage_store<NT, CC, CC>(sWp, LW, vp);
+    stage_store<NT, CC, CC>(sWg, LW, vg);
+    if (tid < CC) {
+      gam_o[tid] = go;
+      gam_i[tid] = gi;
+    }
+    if constexpr (CC == C)
+      if (orow < 2 * CC && gfix && stats) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += (float)w8[e] * bet[c + e];
-      if constexpr (HILO) {
-        if (!g) {
-          const opx8 l8 = ld_x8(w_pout_lo + row * CC + c);
+        for (int c = 0; c < CC / 8; ++c) rv[c] = ld_x8(gout_lo + (orow - CC) * CC + 8 * c);
+      }
+    if (meanfix) stats_reduce<NT>(pv, mu, mu + PS_C);
+  }
+  __syncthreads();
+  if (orow < 2 * CC) {
+    if (gfix) {   // gate offsets from the exact g_out beta (+ the mean correction)
+      if constexpr (CC == C) cbias[orow] = -LOG2E * corrected_offset_regs<true>(offb_v, rv, stats != nullptr, gam_i, mu);
+    } else {      // W beta from the staged 16-bit weights (p_out with its residual under HILO)
+      const op_t* w = grow ? sWg + (orow - CC) * LW : sWp + orow * LW;
+      const float* bet = grow ? lni_b : lno_b;
+      float acc = 0.f;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc += (float)l8[e] * bet[c + e];
+      for (int c = 0; c < CC; c += 8) {
+        const opx4 wa = ld_x4(w + c), wb = ld_x4(w + c + 4);
+        const opx8 w8 = {wa[0], wa[1], wa[2], wa[3], wb[0], wb[1], wb[2], wb[3]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += (float)w8[e] * bet[c + e];
+        if constexpr (HILO) {
+          if (!grow) {
+            const opx4 la = ld_x4(sWpl + orow * LW + c), lb = ld_x4(sWpl + orow * LW + c + 4);
+            const opx8 l8 = {la[0], la[1], la[2], la[3], lb[0], lb[1], lb[2], lb[3]};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc += (float)l8[e] * bet[c + e];
+          }
         }
       }
+      cbias[orow] = grow ? -LOG2E * acc : acc;
     }
-    cbias[row] = g ? -LOG2E * acc : acc;
   }
   __syncthreads();
   if (nparts > 0) x_scale = 1.f / x_store_scale(planes_amax(amax_parts, nparts), N);   // a power of two
