@@ -45,6 +45,7 @@ __global__ __launch_bounds__(64 * DF_WAVES, 1) void cond_proj_kernel(
   __shared__ float sb[C];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+#pragma unroll 4
   for (int c = tid; c < 2 * C * 16; c += 64 * DF_WAVES) {   // 128 rows x 32 chunks
     const int R = c >> 5, k = c & 31;
     const opx8 wv = ld_x8(W + R * 2 * C + 8 * k);
@@ -53,6 +54,7 @@ __global__ __launch_bounds__(64 * DF_WAVES, 1) void cond_proj_kernel(
     for (int u = 0; u < 8; ++u) o[u] = (op_t)((float)wv[u] * lnw[8 * k + u]);
     st_x8(&sw[k >> 4][slot16(R, k & 15)], o);
   }
+#pragma unroll 4
   for (int R = wid; R < C; R += DF_WAVES) {   // one wave per output row, 4 channels per lane
     float v = 0.f;
 #pragma unroll
@@ -125,6 +127,7 @@ __global__ __launch_bounds__(64 * TB_WAVES, 1) void token_bias_kernel(
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, m = lane & 31;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   // stage W'[o][c] = W[o][c] * gamma_l[c] (16 chunks of 8 channels per row)
+#pragma unroll 4
   for (int c = tid; c < M * 16; c += 64 * TB_WAVES) {
     const int R = c >> 4, k = c & 15, l = R / H;
     const opx8 wv = ld_x8(W + R * C + 8 * k);
@@ -134,6 +137,7 @@ __global__ __launch_bounds__(64 * TB_WAVES, 1) void token_bias_kernel(
     st_x8(&sw[slot16(R, k)], o);
   }
   // b'[o] = sum_c W[o][c] beta_l[c]: one wave per output row, two channels per lane
+#pragma unroll 4
   for (int R = wid; R < M; R += TB_WAVES) {
     const int l = R / H;
     float v = (float)W[R * C + lane] * lnb[l * C + lane] + (float)W[R * C + 64 + lane] * lnb[l * C + 64 + lane];
